@@ -1,0 +1,237 @@
+"""Benchmark of the MI355X flash-GQA hot path.
+
+Default (the driver's contract): BASELINE config 2, GQA decode at B=60,
+S=4096, Hq=128, Hkv=8, D=128, bf16 in/out, fp32 accumulation, inputs resident
+in HBM.  One "step" = one decode over the whole batch.  Prints ONE JSON line:
+value = decode KV-read throughput in GB/s (decimal), with the roofline of the
+decode kernel against 8 TB/s HBM, the causal prefill of BASELINE config 4
+(TFLOPS against 2.5 PFLOP/s bf16 dense MFMA) beside it, and the CPU oracle
+timed on a bounded sample of the same decode workload.
+
+    python bench.py [--steps K] [--warmup W] [--split-tokens N] [--no-cpu] [--all]
+
+Only one GPU is used: --gpus N with N > 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
+BF16_PEAK_TFLOPS = 2516.6      # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/clk/CU
+SCALE = 1.0 / math.sqrt(128)
+
+DECODE_CONFIGS = {
+    1: dict(B=2, S=512, Hq=16, Hkv=2, ragged=False, sigma=1.0),
+    2: dict(B=60, S=4096, Hq=128, Hkv=8, ragged=False, sigma=1.0),
+    3: dict(B=64, S=32768, Hq=64, Hkv=8, ragged=True, sigma=1.0),
+}
+PREFILL_CONFIGS = {
+    4: dict(B=1, S=4096, Hq=16, Hkv=1, sigma=1.0),
+    5: dict(B=4, S=16384, Hq=32, Hkv=8, sigma=0.5),
+}
+
+
+def _normal(shape, seed, sigma, dev):
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    x = torch.randn(shape, generator=g, device=dev, dtype=torch.float32)
+    if sigma != 1.0:
+        x.mul_(sigma)
+    return x.to(torch.bfloat16)
+
+
+def _time_calls(fn, steps, warmup):
+    """Per-call durations (ms) from HIP events on torch's current stream, which
+    is the stream every launch of the library goes to."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record()
+    for a, b in evs:
+        a.record()
+        fn()
+        b.record()
+    t_end.record()
+    torch.cuda.synchronize()
+    per = sorted(a.elapsed_time(b) for a, b in evs)
+    return t_start.elapsed_time(t_end), per
+
+
+def _decode_setup(cfg, dev, seed=2):
+    import numpy as np
+    import torch
+    B, S, Hq, Hkv = cfg["B"], cfg["S"], cfg["Hq"], cfg["Hkv"]
+    q = _normal((B, Hq, 128), seed, cfg["sigma"], dev)
+    k = _normal((B, S, Hkv, 128), seed + 1, cfg["sigma"], dev)
+    v = _normal((B, S, Hkv, 128), seed + 2, cfg["sigma"], dev)
+    lens = None
+    if cfg["ragged"]:
+        rng = np.random.default_rng(seed)
+        lens = (1 + rng.integers(0, S, size=B)).astype(np.int32)
+    sl = None if lens is None else torch.from_numpy(lens).to(dev)
+    valid_tokens = B * S if lens is None else int(lens.sum())
+    kv_bytes = 2 * valid_tokens * Hkv * 128 * 2
+    return q, k, v, sl, lens, kv_bytes
+
+
+def bench_decode(cfg_id, steps, warmup, split_tokens, dev):
+    import torch
+
+    import cuda_llm_ops_amd as fg
+    cfg = DECODE_CONFIGS[cfg_id]
+    q, k, v, sl, lens, kv_bytes = _decode_setup(cfg, dev)
+    out = torch.empty_like(q)
+    n_ws = fg.decode_workspace_bytes(cfg["B"], cfg["S"], cfg["Hq"], cfg["Hkv"], split_tokens=split_tokens)
+    ws = torch.empty(max(n_ws, 256), dtype=torch.uint8, device=dev)
+
+    def step():
+        fg.decode_flash_gqa_bshd(q, k, v, SCALE, out=out, seqlens=sl, split_tokens=split_tokens, workspace=ws)
+
+    total_ms, per = _time_calls(step, steps, warmup)
+    ms_step = total_ms / steps
+    avg_launch_ms = sum(per) / len(per)
+    qo_bytes = 2 * cfg["B"] * cfg["Hq"] * 128 * 2
+    return dict(cfg=cfg, q=q, k=k, v=v, lens=lens, out=out, kv_bytes=kv_bytes, qo_bytes=qo_bytes,
+                ms_step=ms_step, avg_launch_ms=avg_launch_ms, median_ms=per[len(per) // 2], min_ms=per[0])
+
+
+def bench_prefill(cfg_id, steps, warmup, dev):
+    import torch
+
+    import cuda_llm_ops_amd as fg
+    cfg = PREFILL_CONFIGS[cfg_id]
+    B, S, Hq, Hkv = cfg["B"], cfg["S"], cfg["Hq"], cfg["Hkv"]
+    q = _normal((B, S, Hq, 128), 4, cfg["sigma"], dev)
+    k = _normal((B, S, Hkv, 128), 5, cfg["sigma"], dev)
+    v = _normal((B, S, Hkv, 128), 6, cfg["sigma"], dev)
+    out = torch.empty_like(q)
+    lse = torch.empty((B, Hq, S), dtype=torch.float32, device=dev)
+
+    def step():
+        fg.flash_gqa_forward_bshd(q, k, v, SCALE, out=out, lse=lse, causal=True)
+
+    total_ms, per = _time_calls(step, steps, warmup)
+    # the reference's causal-halved count (test_flash_gqa_kernel.py:282-301)
+    flops = B * Hq * 2 * S * S * (128 + 128) // 2
+    avg = sum(per) / len(per)
+    return dict(config=f"causal prefill B={B} S={S} Hq={Hq} Hkv={Hkv} D=128", us_avg=avg * 1e3,
+                us_median=per[len(per) // 2] * 1e3, us_min=per[0] * 1e3, flops=flops,
+                tflops=flops / (avg * 1e-3) / 1e12, frac=flops / (avg * 1e-3) / 1e12 / BF16_PEAK_TFLOPS)
+
+
+def cpu_baseline_decode(res, budget_s=12.0):
+    """Time the CPU oracle (OpenMP C restatement of the reference's CPU decode)
+    on whole batches of the same inputs until ~budget_s of CPU work."""
+    import numpy as np
+    import torch
+
+    import oracle
+    cfg = res["cfg"]
+
+    def host(t):
+        return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+    threads = min(os.cpu_count() or 1, 16)
+    done_bytes = 0
+    elapsed = 0.0
+    nb = 0
+    B = cfg["B"]
+    while nb < B and elapsed < budget_s:
+        qh, kh, vh = host(res["q"][nb:nb + 1]), host(res["k"][nb:nb + 1]), host(res["v"][nb:nb + 1])
+        sl = None if res["lens"] is None else res["lens"][nb:nb + 1]
+        t0 = time.perf_counter()
+        oracle.decode(qh, kh, vh, SCALE, seqlens=sl, nthreads=threads, with_lse=False)
+        elapsed += time.perf_counter() - t0
+        n_tok = cfg["S"] if sl is None else int(sl[0])
+        done_bytes += 2 * n_tok * cfg["Hkv"] * 128 * 2
+        nb += 1
+    return dict(value=round(done_bytes / elapsed / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                sample=f"{nb} of {B} sequences of the same workload (all heads, all tokens), "
+                       f"{elapsed:.1f} s on {threads} OpenMP threads")
+
+
+def load_traffic(name):
+    p = os.path.join(ROOT, "profiles", name)
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f).get("traffic_bytes")
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--split-tokens", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--all", action="store_true", help="also report configs 1, 3 and 5 (to stderr)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path (--gpus must be 1)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import cuda_llm_ops_amd  # noqa: F401  (fails loudly if libfgqa.so is missing)
+    dev = torch.device("cuda:0")
+
+    res = bench_decode(2, args.steps, args.warmup, args.split_tokens, dev)
+    gbs = res["kv_bytes"] / (res["ms_step"] * 1e-3) / 1e9
+    achieved = res["kv_bytes"] / (res["avg_launch_ms"] * 1e-3) / 1e9
+    line = {
+        "metric": "decode KV-read GB/s (% HBM peak); prefill TFLOPS (% bf16 MFMA peak)",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) bf16 (seeded torch.randn on the GPU), resident in HBM",
+        "config": {"workload": "GQA decode, BASELINE config 2", "batch": 60, "seq_len": 4096,
+                   "num_q_heads": 128, "num_kv_heads": 8, "head_dim": 128, "parallelism": "none (1 GPU)",
+                   "split_tokens": args.split_tokens or "auto"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic("decode_cfg2_traffic.json"),
+                     "kernel": "decode (split-KV pass + LSE combine)", "algorithmic_bytes": res["kv_bytes"],
+                     "avg_launch_us": round(res["avg_launch_ms"] * 1e3, 2),
+                     "median_launch_us": round(res["median_ms"] * 1e3, 2),
+                     "min_launch_us": round(res["min_ms"] * 1e3, 2)},
+        "decode_all_tensor_GBs": round((res["kv_bytes"] + res["qo_bytes"]) / (res["ms_step"] * 1e-3) / 1e9, 2),
+    }
+    if not args.no_prefill:
+        line["prefill"] = bench_prefill(4, args.steps, args.warmup, dev)
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_decode(res)
+    if args.all:
+        for cid in (1, 3):
+            r = bench_decode(cid, args.steps, args.warmup, 0, dev)
+            print(json.dumps({"config": cid, "us_avg": r["avg_launch_ms"] * 1e3,
+                              "GBs": r["kv_bytes"] / (r["avg_launch_ms"] * 1e-3) / 1e9}), file=sys.stderr)
+            del r
+        r = bench_prefill(5, max(3, args.steps // 10), 2, dev)
+        print(json.dumps({"config": 5, **r}), file=sys.stderr)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

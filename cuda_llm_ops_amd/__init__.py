@@ -1,0 +1,15 @@
+"""MI355X-native flash grouped-query attention (decode + causal prefill).
+
+The kernels live in libfgqa.so (HIP, gfx950); ``flash_gqa`` is the Python host
+interface over its C ABI (include/fgqa.h).
+"""
+from ._lib import FgqaError, LIB_PATH, lib, status_string  # noqa: F401
+from .flash_gqa import (  # noqa: F401
+    decode_flash_gqa_bshd,
+    decode_workspace_bytes,
+    flash_gqa_forward_bshd,
+    launch_decode_flash_gqa_bf16_kernel,
+    launch_flash_gqa_forward_bf16_kernel,
+)
+
+__version__ = "0.1.0"

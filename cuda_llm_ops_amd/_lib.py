@@ -1,0 +1,111 @@
+"""ctypes binding of libfgqa.so, the C ABI declared in include/fgqa.h.
+
+The library is built in-tree (``make -C cuda_llm_ops_amd/csrc`` or
+``__graft_entry__.build()``).  Loading fails loudly when it is missing: there
+is no fallback implementation of any entry point.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libfgqa.so")
+
+FGQA_OK = 0
+FGQA_ERR_INVALID_ARGUMENT = -1
+FGQA_ERR_UNSUPPORTED = -2
+FGQA_ERR_WORKSPACE = -3
+FGQA_ERR_HIP = -4
+
+_I64x2 = ctypes.c_int64 * 2
+_I64x3 = ctypes.c_int64 * 3
+
+
+class DecodeArgs(ctypes.Structure):
+    """Mirror of ``fgqa_decode_args`` (include/fgqa.h)."""
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("seqlens", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("max_seqlen", ctypes.c_int32),
+        ("num_q_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("q_stride", _I64x2),
+        ("k_stride", _I64x3),
+        ("v_stride", _I64x3),
+        ("o_stride", _I64x2),
+        ("split_tokens", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+class PrefillArgs(ctypes.Structure):
+    """Mirror of ``fgqa_prefill_args`` (include/fgqa.h)."""
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("seqlen_q", ctypes.c_int32),
+        ("seqlen_kv", ctypes.c_int32),
+        ("num_q_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("causal", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("q_stride", _I64x3),
+        ("k_stride", _I64x3),
+        ("v_stride", _I64x3),
+        ("o_stride", _I64x3),
+    ]
+
+
+class FgqaError(RuntimeError):
+    def __init__(self, status: int, where: str):
+        self.status = status
+        super().__init__(f"{where}: {status_string(status)} (status {status})")
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libfgqa.so (once).  Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `make -C cuda_llm_ops_amd/csrc` "
+                "or __graft_entry__.build(); there is no fallback path")
+        L = ctypes.CDLL(LIB_PATH)
+        L.fgqa_decode_workspace_bytes.restype = ctypes.c_int
+        L.fgqa_decode_workspace_bytes.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ctypes.c_size_t)]
+        L.fgqa_decode_bf16.restype = ctypes.c_int
+        L.fgqa_decode_bf16.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.c_void_p]
+        L.fgqa_prefill_bf16.restype = ctypes.c_int
+        L.fgqa_prefill_bf16.argtypes = [ctypes.POINTER(PrefillArgs), ctypes.c_void_p]
+        L.fgqa_status_string.restype = ctypes.c_char_p
+        L.fgqa_status_string.argtypes = [ctypes.c_int]
+        L.fgqa_version.restype = ctypes.c_int
+        L.fgqa_version.argtypes = []
+        _lib = L
+    return _lib
+
+
+def status_string(status: int) -> str:
+    return lib().fgqa_status_string(int(status)).decode()
+
+
+def check(status: int, where: str) -> None:
+    if status != FGQA_OK:
+        raise FgqaError(status, where)

@@ -1,0 +1,100 @@
+// C++ operator entry points of the FlashGQA path, implemented over the C ABI
+// (include/fgqa.h).  Host-only C++: no HIP types or calls in this file.
+#include <cstring>
+
+#include "FlashGQA/decode_flash_gqa_kernel.h"
+#include "FlashGQA/flash_gqa_forward_kernel.h"
+#include "fgqa.h"
+
+namespace {
+thread_local int g_last_status = FGQA_OK;
+
+fgqa_decode_args contiguous_decode(const bf16_t* q, const bf16_t* k, const bf16_t* v, float scale, bf16_t* o,
+                                   int batchSize, int seqLength, int numQueryHeads, int numKvHeads, int headDim) {
+    fgqa_decode_args a;
+    std::memset(&a, 0, sizeof(a));
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.o = o;
+    a.batch = batchSize;
+    a.max_seqlen = seqLength;
+    a.num_q_heads = numQueryHeads;
+    a.num_kv_heads = numKvHeads;
+    a.head_dim = headDim;
+    a.scale = scale;
+    // q, o: [B, Hq, D];  k, v: [B, S, Hkv, D]
+    a.q_stride[0] = (int64_t)numQueryHeads * headDim;
+    a.q_stride[1] = headDim;
+    a.o_stride[0] = a.q_stride[0];
+    a.o_stride[1] = a.q_stride[1];
+    a.k_stride[0] = (int64_t)seqLength * numKvHeads * headDim;
+    a.k_stride[1] = (int64_t)numKvHeads * headDim;
+    a.k_stride[2] = headDim;
+    for (int i = 0; i < 3; ++i) a.v_stride[i] = a.k_stride[i];
+    return a;
+}
+}  // namespace
+
+void LaunchFlashGqaBf16Kernel(const bf16_t* q, const bf16_t* k, const bf16_t* v, float scale, bf16_t* o,
+                              float* oIntermediate, int batchSize, int seqLength, int numQueryHeads,
+                              int numKvHeads, int headDim) {
+    (void)oIntermediate;
+    fgqa_decode_args a =
+        contiguous_decode(q, k, v, scale, o, batchSize, seqLength, numQueryHeads, numKvHeads, headDim);
+    g_last_status = fgqa_decode_bf16(&a, nullptr);
+}
+
+void LaunchFlashGqaBf16KernelVarlen(const bf16_t* q, const bf16_t* k, const bf16_t* v, float scale, bf16_t* o,
+                                    const int32_t* seqLengths, int batchSize, int maxSeqLength, int numQueryHeads,
+                                    int numKvHeads, int headDim) {
+    fgqa_decode_args a =
+        contiguous_decode(q, k, v, scale, o, batchSize, maxSeqLength, numQueryHeads, numKvHeads, headDim);
+    a.seqlens = seqLengths;
+    g_last_status = fgqa_decode_bf16(&a, nullptr);
+}
+
+void LaunchFlashGqaForwardBf16KernelStrided(const bf16_t* q, const bf16_t* k, const bf16_t* v, float scale,
+                                            bf16_t* o, float* lse, int batchSize, int seqLengthQ, int seqLengthKv,
+                                            int numQueryHeads, int numKvHeads, int headDim, bool causal,
+                                            const int64_t qStride[3], const int64_t kStride[3],
+                                            const int64_t vStride[3], const int64_t oStride[3]) {
+    if (qStride == nullptr || kStride == nullptr || vStride == nullptr || oStride == nullptr) {
+        g_last_status = FGQA_ERR_INVALID_ARGUMENT;
+        return;
+    }
+    fgqa_prefill_args a;
+    std::memset(&a, 0, sizeof(a));
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.o = o;
+    a.lse = lse;
+    a.batch = batchSize;
+    a.seqlen_q = seqLengthQ;
+    a.seqlen_kv = seqLengthKv;
+    a.num_q_heads = numQueryHeads;
+    a.num_kv_heads = numKvHeads;
+    a.head_dim = headDim;
+    a.causal = causal ? 1 : 0;
+    a.scale = scale;
+    for (int i = 0; i < 3; ++i) {
+        a.q_stride[i] = qStride[i];
+        a.k_stride[i] = kStride[i];
+        a.v_stride[i] = vStride[i];
+        a.o_stride[i] = oStride[i];
+    }
+    g_last_status = fgqa_prefill_bf16(&a, nullptr);
+}
+
+void LaunchFlashGqaForwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf16_t* v, float scale, bf16_t* o,
+                                     float* lse, int batchSize, int seqLengthQ, int seqLengthKv, int numQueryHeads,
+                                     int numKvHeads, int headDim, bool causal) {
+    // BSHD: q, o [B, Sq, Hq, D]; k, v [B, Skv, Hkv, D]
+    const int64_t qs[3] = {(int64_t)seqLengthQ * numQueryHeads * headDim, (int64_t)numQueryHeads * headDim, headDim};
+    const int64_t ks[3] = {(int64_t)seqLengthKv * numKvHeads * headDim, (int64_t)numKvHeads * headDim, headDim};
+    LaunchFlashGqaForwardBf16KernelStrided(q, k, v, scale, o, lse, batchSize, seqLengthQ, seqLengthKv,
+                                           numQueryHeads, numKvHeads, headDim, causal, qs, ks, ks, qs);
+}
+
+int FlashGqaGetLastStatus() { return g_last_status; }

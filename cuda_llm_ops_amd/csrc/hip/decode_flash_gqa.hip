@@ -1,0 +1,463 @@
+// Split-KV (flash-decoding) GQA decode for gfx950.
+//
+// Replaces the reference's decode_flash_gqa_bf16_kernel
+// (src/cplusplus/FlashGQA/decode_flash_gqa_kernel.cu:119-389), which walks the
+// whole sequence serially per (kv head, batch) workgroup.  Here:
+//   pass 1 (decode_split_kernel): one workgroup per (split of the KV sequence,
+//     kv head, batch).  Each of its 4 waves streams 32-token steps; every K/V
+//     byte is read once from HBM and serves all G query heads of the group.
+//       S^T[t][h] = K[t][:] . Q[h][:]        v_mfma_f32_16x16x32_bf16, K loaded
+//                                            straight into the A-operand layout
+//       online softmax in fp32 (exp2 with log2(e) folded into the scale), P
+//       rounded to bf16 before P.V and the rowsum kept from the fp32 P, as the
+//       reference does (decode_flash_gqa_kernel.cu:266-278)
+//       O^T[d][h] += V^T[d][t] . P^T[t][h]   v_mfma_f32_16x16x32_bf16, V staged
+//                                            through LDS for the transpose
+//     The 4 waves merge their (max, sum, O) in LDS; with one split the
+//     workgroup writes the normalised bf16 output directly, otherwise it
+//     writes an fp32 partial (O, max, sum) to the workspace.
+//   pass 2 (decode_combine_kernel): log-sum-exp merge of the partials.
+#include <math.h>
+
+#include "fgqa_device.h"
+#include "fgqa_internal.h"
+
+namespace fgqa {
+
+struct DecodeParams {
+    const __bf16* q;
+    const __bf16* k;
+    const __bf16* v;
+    __bf16* o;
+    float* lse;
+    const int32_t* seqlens;
+    float* part_o;   // [B, Hkv, nsplit, G, 128]
+    float* part_ml;  // [B, Hkv, nsplit, G, 2]  (max in log2 units, sum)
+    int64_t q_sb, q_sh;
+    int64_t k_sb, k_ss, k_sh;
+    int64_t v_sb, v_ss, v_sh;
+    int64_t o_sb, o_sh;
+    int batch, max_seqlen, hq, hkv, group;
+    int nsplit, chunk;
+    float scale_log2;
+};
+
+constexpr int kDecThreads = 256;
+constexpr int kDecWaves = kDecThreads / kWave;
+constexpr int kDecStep = 32;        // tokens per wave step (two 16-token MFMA blocks)
+constexpr int kDecVStride = 136;    // LDS row stride (elements) of a staged V row
+constexpr int kDecSmemBytes = kDecWaves * kDecStep * kDecVStride * 2;
+static_assert(kDecWaves * 16 * kHeadDim * 4 + kDecWaves * 16 * 2 * 4 <= kDecSmemBytes,
+              "wave merge buffers must fit in the V staging area");
+
+__device__ __forceinline__ int clamp_len(const DecodeParams& p, int b) {
+    int len = p.seqlens ? p.seqlens[b] : p.max_seqlen;
+    return min(max(len, 0), p.max_seqlen);
+}
+
+__global__ __launch_bounds__(kDecThreads) void decode_split_kernel(DecodeParams p) {
+    const int split = blockIdx.x;
+    const int kvh = blockIdx.y;
+    const int b = blockIdx.z;
+    const int len = clamp_len(p, b);
+    const int t_begin = split * p.chunk;
+    const int tid = threadIdx.x;
+    if (t_begin >= len) {
+        // Empty split: the combine never reads it.  Without a combine pass an
+        // empty sequence still needs its O = 0, lse = -inf written here.
+        if (p.nsplit == 1 && (tid >> 4) < p.group) {
+            const int qh = kvh * p.group + (tid >> 4);
+            bf16x8_t z;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) z[j] = (__bf16)0.f;
+            *reinterpret_cast<bf16x8_t*>(p.o + b * p.o_sb + qh * p.o_sh + (tid & 15) * 8) = z;
+            if (p.lse != nullptr && (tid & 15) == 0) p.lse[(int64_t)b * p.hq + qh] = -INFINITY;
+        }
+        return;
+    }
+    const int t_end = min(t_begin + p.chunk, len);
+
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int l16 = lane & 15;
+    const int g4 = lane >> 4;
+
+    __shared__ __attribute__((aligned(16))) unsigned char smem[kDecSmemBytes];
+    __bf16* vl = reinterpret_cast<__bf16*>(smem) + wave * kDecStep * kDecVStride;
+
+    // Q^T as the B operand: lane holds Q[h = l16][32*kk + 8*g4 .. +7]; heads >= G are zero.
+    bf16x8_t qop[4];
+    {
+        const bool hv = l16 < p.group;
+        const __bf16* qrow = p.q + b * p.q_sb + (int64_t)(kvh * p.group + (hv ? l16 : 0)) * p.q_sh;
+        const u32x4_t zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            u32x4_t t = *reinterpret_cast<const u32x4_t*>(qrow + kk * 32 + g4 * 8);
+            qop[kk] = as_bf16x8(hv ? t : zero);
+        }
+    }
+
+    // Buffer resources end at the split's last valid token: later tokens read as zero.
+    const uint32_t kss = (uint32_t)(p.k_ss * 2);
+    const uint32_t vss = (uint32_t)(p.v_ss * 2);
+    const __amdgpu_buffer_rsrc_t krs =
+        make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, (uint32_t)(t_end - 1) * kss + kHeadDim * 2);
+    const __amdgpu_buffer_rsrc_t vrs =
+        make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, (uint32_t)(t_end - 1) * vss + kHeadDim * 2);
+
+    float m_run = -INFINITY;
+    float l_run = 0.f;  // this lane's share of the rowsum of head l16
+    f32x4_t oacc[8];
+#pragma unroll
+    for (int db = 0; db < 8; ++db) oacc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    const int n_steps = (t_end - t_begin + kDecStep - 1) / kDecStep;
+    u32x4_t kreg[2][4];
+    u32x4_t vreg[8];
+
+    auto load_step = [&](int st) {
+        const uint32_t t0 = (uint32_t)(t_begin + st * kDecStep);
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+                kreg[tb][kk] = buf_load16(krs, (t0 + tb * 16 + l16) * kss + (kk * 32 + g4 * 8) * 2);
+#pragma unroll
+        for (int r = 0; r < 8; ++r) vreg[r] = buf_load16(vrs, (t0 + r * 4 + g4) * vss + l16 * 16);
+    };
+
+    int st = wave;
+    if (st < n_steps) load_step(st);
+    for (; st < n_steps; st += kDecWaves) {
+        u32x4_t kcur[2][4];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) kcur[tb][kk] = kreg[tb][kk];
+        // Stage this step's V rows (coalesced: a quarter-wave holds one 256-byte row).
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+            *reinterpret_cast<u32x4_t*>(vl + (r * 4 + g4) * kDecVStride + l16 * 8) = vreg[r];
+        if (st + kDecWaves < n_steps) load_step(st + kDecWaves);  // prefetch the next step
+
+        const int t0 = t_begin + st * kDecStep;
+        f32x4_t s[2];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            s[tb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) s[tb] = mfma16(as_bf16x8(kcur[tb][kk]), qop[kk], s[tb]);
+        }
+
+        // Online softmax for head l16 over tokens t0 + 16*tb + 4*g4 + i.
+        float x[8];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tok = t0 + tb * 16 + g4 * 4 + i;
+                const float val = (tok < t_end) ? s[tb][i] * p.scale_log2 : -INFINITY;
+                x[tb * 4 + i] = val;
+                tmax = fmaxf(tmax, val);
+            }
+        tmax = xor_max(xor_max(tmax, 16), 32);
+        const float m_new = fmaxf(m_run, tmax);  // finite: every step holds a valid token
+        const float alpha = fast_exp2(m_run - m_new);
+        float psum = 0.f;
+        bf16x8_t pop;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float pv = fast_exp2(x[j] - m_new);
+            psum += pv;
+            pop[j] = (__bf16)pv;
+        }
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) oacc[db] *= alpha;
+
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        // V^T as the A operand: lane holds V[token(slot)][16*db + l16] for the
+        // 8 slots of group g4: tokens 4*g4 + {0..3} and 16 + 4*g4 + {0..3},
+        // the same tokens whose P this lane already holds.
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+            bf16x8_t va;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int tok = (j < 4) ? (g4 * 4 + j) : (16 + g4 * 4 + (j - 4));
+                va[j] = vl[tok * kDecVStride + db * 16 + l16];
+            }
+            oacc[db] = mfma16(va, pop, oacc[db]);
+        }
+
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+
+    l_run = xor_sum(xor_sum(l_run, 16), 32);
+
+    // Merge the 4 waves in LDS (reusing the staging area).
+    __syncthreads();
+    float* ow = reinterpret_cast<float*>(smem);        // [wave][16][128]
+    float* mlw = ow + kDecWaves * 16 * kHeadDim;       // [wave][16][2]
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ow[(wave * 16 + l16) * kHeadDim + db * 16 + g4 * 4 + i] = oacc[db][i];
+    if (g4 == 0) {
+        mlw[(wave * 16 + l16) * 2 + 0] = m_run;
+        mlw[(wave * 16 + l16) * 2 + 1] = l_run;
+    }
+    __syncthreads();
+
+    const int h = tid >> 4;
+    const int d0 = (tid & 15) * 8;
+    if (h >= p.group) return;
+    float mw[kDecWaves];
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kDecWaves; ++w) {
+        mw[w] = mlw[(w * 16 + h) * 2];
+        M = fmaxf(M, mw[w]);
+    }
+    float L = 0.f;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kDecWaves; ++w) {
+        const float c = (mw[w] == -INFINITY) ? 0.f : fast_exp2(mw[w] - M);
+        L += c * mlw[(w * 16 + h) * 2 + 1];
+        const float* src = ow + (w * 16 + h) * kHeadDim + d0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] += c * src[j];
+    }
+    const int qh = kvh * p.group + h;
+    if (p.nsplit == 1) {
+        const float inv = 1.f / L;
+        bf16x8_t out;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) out[j] = (__bf16)(acc[j] * inv);
+        *reinterpret_cast<bf16x8_t*>(p.o + b * p.o_sb + qh * p.o_sh + d0) = out;
+        if (p.lse != nullptr && (tid & 15) == 0) p.lse[(int64_t)b * p.hq + qh] = M * kLn2 + logf(L);
+    } else {
+        const int64_t slot = (((int64_t)b * p.hkv + kvh) * p.nsplit + split) * p.group + h;
+        float* po = p.part_o + slot * kHeadDim + d0;
+        *reinterpret_cast<f32x4_t*>(po) = f32x4_t{acc[0], acc[1], acc[2], acc[3]};
+        *reinterpret_cast<f32x4_t*>(po + 4) = f32x4_t{acc[4], acc[5], acc[6], acc[7]};
+        if ((tid & 15) == 0) {
+            p.part_ml[slot * 2 + 0] = M;
+            p.part_ml[slot * 2 + 1] = L;
+        }
+    }
+}
+
+// Log-sum-exp merge of the per-split partials of one (kv head, batch).
+__global__ __launch_bounds__(kDecThreads) void decode_combine_kernel(DecodeParams p) {
+    const int kvh = blockIdx.x;
+    const int b = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int h = tid >> 4;
+    const int d0 = (tid & 15) * 8;
+    if (h >= p.group) return;
+    const int len = clamp_len(p, b);
+    const int nvalid = (len + p.chunk - 1) / p.chunk;
+    const int qh = kvh * p.group + h;
+    __bf16* orow = p.o + b * p.o_sb + qh * p.o_sh + d0;
+    if (nvalid == 0) {
+        bf16x8_t z;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) z[j] = (__bf16)0.f;
+        *reinterpret_cast<bf16x8_t*>(orow) = z;
+        if (p.lse != nullptr && (tid & 15) == 0) p.lse[(int64_t)b * p.hq + qh] = -INFINITY;
+        return;
+    }
+    const int64_t base = ((int64_t)b * p.hkv + kvh) * p.nsplit;
+    float M = -INFINITY;
+    for (int s = 0; s < nvalid; ++s) M = fmaxf(M, p.part_ml[((base + s) * p.group + h) * 2]);
+    float L = 0.f;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < nvalid; ++s) {
+        const int64_t slot = (base + s) * p.group + h;
+        const float ms = p.part_ml[slot * 2];
+        const float c = (ms == -INFINITY) ? 0.f : fast_exp2(ms - M);
+        L += c * p.part_ml[slot * 2 + 1];
+        const f32x4_t a = *reinterpret_cast<const f32x4_t*>(p.part_o + slot * kHeadDim + d0);
+        const f32x4_t bb = *reinterpret_cast<const f32x4_t*>(p.part_o + slot * kHeadDim + d0 + 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            acc[j] += c * a[j];
+            acc[4 + j] += c * bb[j];
+        }
+    }
+    const float inv = 1.f / L;
+    bf16x8_t out;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) out[j] = (__bf16)(acc[j] * inv);
+    *reinterpret_cast<bf16x8_t*>(orow) = out;
+    if (p.lse != nullptr && (tid & 15) == 0) p.lse[(int64_t)b * p.hq + qh] = M * kLn2 + logf(L);
+}
+
+namespace {
+
+constexpr int kStepRound = kDecWaves * kDecStep;  // 128 tokens: one pass of the 4 waves
+
+struct DecodePlan {
+    int chunk;
+    int nsplit;
+    size_t part_o_bytes;
+    size_t ws_bytes;
+};
+
+int validate_decode(const fgqa_decode_args* a) {
+    if (a == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
+    if (a->batch < 0 || a->max_seqlen < 0 || a->num_q_heads <= 0 || a->num_kv_heads <= 0 ||
+        a->head_dim <= 0)
+        return FGQA_ERR_INVALID_ARGUMENT;
+    if (a->num_q_heads % a->num_kv_heads != 0) return FGQA_ERR_INVALID_ARGUMENT;
+    if (!isfinite(a->scale)) return FGQA_ERR_INVALID_ARGUMENT;
+    if (a->split_tokens < 0) return FGQA_ERR_INVALID_ARGUMENT;
+    for (int i = 0; i < 2; ++i)
+        if (a->q_stride[i] < 0 || a->o_stride[i] < 0) return FGQA_ERR_INVALID_ARGUMENT;
+    for (int i = 0; i < 3; ++i)
+        if (a->k_stride[i] < 0 || a->v_stride[i] < 0) return FGQA_ERR_INVALID_ARGUMENT;
+    if (a->head_dim != kHeadDim) return FGQA_ERR_UNSUPPORTED;
+    if (a->num_q_heads / a->num_kv_heads > 16) return FGQA_ERR_UNSUPPORTED;
+    // 32-bit buffer offsets: the furthest byte addressed inside one sequence.
+    const int64_t lim = (int64_t)1 << 31;
+    if ((int64_t)(a->max_seqlen + 64) * a->k_stride[1] * 2 >= lim ||
+        (int64_t)(a->max_seqlen + 64) * a->v_stride[1] * 2 >= lim)
+        return FGQA_ERR_UNSUPPORTED;
+    return FGQA_OK;
+}
+
+int validate_decode_pointers(const fgqa_decode_args* a) {
+    if (a->batch == 0) return FGQA_OK;
+    if (a->q == nullptr || a->k == nullptr || a->v == nullptr || a->o == nullptr)
+        return FGQA_ERR_INVALID_ARGUMENT;
+    if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o))
+        return FGQA_ERR_UNSUPPORTED;
+    for (int i = 0; i < 2; ++i)
+        if ((a->q_stride[i] & 7) || (a->o_stride[i] & 7)) return FGQA_ERR_UNSUPPORTED;
+    for (int i = 0; i < 3; ++i)
+        if ((a->k_stride[i] & 7) || (a->v_stride[i] & 7)) return FGQA_ERR_UNSUPPORTED;
+    return FGQA_OK;
+}
+
+int plan_decode(const fgqa_decode_args* a, DecodePlan* plan) {
+    const int64_t S = a->max_seqlen > 0 ? a->max_seqlen : 1;
+    int64_t chunk;
+    if (a->split_tokens > 0) {
+        chunk = ceil_div(a->split_tokens, kStepRound) * kStepRound;
+    } else {
+        const int cus = device_cu_count();
+        if (cus <= 0) return FGQA_ERR_HIP;
+        // Enough workgroups for ~4 per CU, but never below one 128-token round.
+        const int64_t items = (int64_t)(a->batch > 0 ? a->batch : 1) * a->num_kv_heads;
+        int64_t want = ceil_div(4LL * cus, items);
+        const int64_t max_splits = ceil_div(S, kStepRound);
+        if (want > max_splits) want = max_splits;
+        if (want < 1) want = 1;
+        chunk = ceil_div(ceil_div(S, want), kStepRound) * kStepRound;
+    }
+    if (chunk < kStepRound) chunk = kStepRound;
+    if (chunk > S) chunk = ceil_div(S, kStepRound) * kStepRound;
+    plan->chunk = (int)chunk;
+    plan->nsplit = (int)ceil_div(S, chunk);
+    const int64_t slots = (int64_t)a->batch * a->num_q_heads * plan->nsplit;
+    if (plan->nsplit > 1) {
+        plan->part_o_bytes = (size_t)(ceil_div(slots * kHeadDim * 4, 256) * 256);
+        plan->ws_bytes = plan->part_o_bytes + (size_t)(slots * 2 * 4);
+    } else {
+        plan->part_o_bytes = 0;
+        plan->ws_bytes = 0;
+    }
+    return FGQA_OK;
+}
+
+}  // namespace
+}  // namespace fgqa
+
+using namespace fgqa;
+
+extern "C" int fgqa_decode_workspace_bytes(const fgqa_decode_args* a, size_t* bytes) {
+    if (bytes == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
+    int st = validate_decode(a);
+    if (st != FGQA_OK) return st;
+    DecodePlan plan;
+    st = plan_decode(a, &plan);
+    if (st != FGQA_OK) return st;
+    *bytes = plan.ws_bytes;
+    return FGQA_OK;
+}
+
+extern "C" int fgqa_decode_bf16(const fgqa_decode_args* a, void* stream) {
+    int st = validate_decode(a);
+    if (st != FGQA_OK) return st;
+    st = validate_decode_pointers(a);
+    if (st != FGQA_OK) return st;
+    if (a->batch == 0) return FGQA_OK;
+    DecodePlan plan;
+    st = plan_decode(a, &plan);
+    if (st != FGQA_OK) return st;
+
+    DecodeParams p;
+    p.q = static_cast<const __bf16*>(a->q);
+    p.k = static_cast<const __bf16*>(a->k);
+    p.v = static_cast<const __bf16*>(a->v);
+    p.o = static_cast<__bf16*>(a->o);
+    p.lse = a->lse;
+    p.seqlens = a->seqlens;
+    p.part_o = nullptr;
+    p.part_ml = nullptr;
+    p.q_sb = a->q_stride[0];
+    p.q_sh = a->q_stride[1];
+    p.k_sb = a->k_stride[0];
+    p.k_ss = a->k_stride[1];
+    p.k_sh = a->k_stride[2];
+    p.v_sb = a->v_stride[0];
+    p.v_ss = a->v_stride[1];
+    p.v_sh = a->v_stride[2];
+    p.o_sb = a->o_stride[0];
+    p.o_sh = a->o_stride[1];
+    p.batch = a->batch;
+    p.max_seqlen = a->max_seqlen;
+    p.hq = a->num_q_heads;
+    p.hkv = a->num_kv_heads;
+    p.group = a->num_q_heads / a->num_kv_heads;
+    p.nsplit = plan.nsplit;
+    p.chunk = plan.chunk;
+    p.scale_log2 = a->scale * kLog2e;
+
+    if (plan.nsplit > 1) {
+        void* ws = a->workspace;
+        if (ws == nullptr && a->workspace_bytes == 0) {
+            ws = internal_workspace(plan.ws_bytes, &st);
+            if (st != FGQA_OK) return st;
+        } else if (ws == nullptr || a->workspace_bytes < plan.ws_bytes) {
+            return FGQA_ERR_WORKSPACE;
+        } else if (!aligned16(ws)) {
+            return FGQA_ERR_UNSUPPORTED;
+        }
+        p.part_o = static_cast<float*>(ws);
+        p.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + plan.part_o_bytes);
+    }
+
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (a->max_seqlen == 0) {
+        // Every sequence is empty: the combine writes O = 0, lse = -inf.
+        p.nsplit = 1;
+        hipLaunchKernelGGL(decode_combine_kernel, dim3(p.hkv, p.batch), dim3(kDecThreads), 0, s, p);
+    } else {
+        hipLaunchKernelGGL(decode_split_kernel, dim3(p.nsplit, p.hkv, p.batch), dim3(kDecThreads), 0, s, p);
+        if (plan.nsplit > 1)
+            hipLaunchKernelGGL(decode_combine_kernel, dim3(p.hkv, p.batch), dim3(kDecThreads), 0, s, p);
+    }
+    if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
+    return FGQA_OK;
+}

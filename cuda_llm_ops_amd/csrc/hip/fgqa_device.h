@@ -1,0 +1,58 @@
+// Device-side helpers shared by the flash-GQA HIP kernels (gfx950 only).
+//
+// MFMA operand layouts used throughout (wave64, lane l, l16 = l % 16, l32 = l % 32):
+//   v_mfma_f32_16x16x32_bf16  A[m][k]: lane m + 16*(k/8) holds k%8 of 8 bf16
+//                             B[k][n]: lane n + 16*(k/8) holds k%8 of 8 bf16
+//                             C[m][n]: lane n + 16*(m/4), register m%4
+//   v_mfma_f32_32x32x16_bf16  A[m][k]: lane m + 32*(k/8), element k%8
+//                             B[k][n]: lane n + 32*(k/8), element k%8
+//                             C[m][n]: lane n + 32*((m/4)%2), register (m%4) + 4*(m/8)
+// tests/test_gpu_layout.py checks these against a CPU matmul on the device.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fgqa {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+constexpr int kHeadDim = 128;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Raw (stride 0) buffer resource over [base, base + bytes).  A load whose
+// offset is at or past `bytes` returns zeros instead of touching memory, which
+// is how the kernels read ragged tails without a branch per load.
+// Third descriptor word 0x00020000: 32-bit data format, as used for raw
+// buffers on the gfx9 family (gfx90a/gfx94x/gfx950).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4_t buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+__device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16_t mfma32(bf16x8_t a, bf16x8_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float xor_max(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, kWave)); }
+__device__ __forceinline__ float xor_sum(float v, int mask) { return v + __shfl_xor(v, mask, kWave); }
+
+}  // namespace fgqa

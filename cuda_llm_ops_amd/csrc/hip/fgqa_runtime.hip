@@ -1,0 +1,74 @@
+// Host runtime pieces of libfgqa: status strings, the cached device
+// properties and the library-owned decode workspace.
+#include <mutex>
+#include <vector>
+
+#include "fgqa_internal.h"
+
+namespace fgqa {
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_mutex;
+int g_cu_count[kMaxDevices] = {0};
+void* g_ws_ptr[kMaxDevices] = {nullptr};
+size_t g_ws_bytes[kMaxDevices] = {0};
+}  // namespace
+
+int device_cu_count() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (g_cu_count[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        g_cu_count[dev] = cus;
+    }
+    return g_cu_count[dev];
+}
+
+void* internal_workspace(size_t bytes, int* status) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        *status = FGQA_ERR_HIP;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (g_ws_bytes[dev] < bytes) {
+        // Work already queued on any stream may still read the old buffer, so
+        // drain the device before releasing it.
+        if (g_ws_ptr[dev] != nullptr) {
+            if (hipDeviceSynchronize() != hipSuccess || hipFree(g_ws_ptr[dev]) != hipSuccess) {
+                *status = FGQA_ERR_HIP;
+                return nullptr;
+            }
+            g_ws_ptr[dev] = nullptr;
+            g_ws_bytes[dev] = 0;
+        }
+        const size_t rounded = (bytes + (1u << 20) - 1) & ~static_cast<size_t>((1u << 20) - 1);
+        void* p = nullptr;
+        if (hipMalloc(&p, rounded) != hipSuccess) {
+            *status = FGQA_ERR_HIP;
+            return nullptr;
+        }
+        g_ws_ptr[dev] = p;
+        g_ws_bytes[dev] = rounded;
+    }
+    *status = FGQA_OK;
+    return g_ws_ptr[dev];
+}
+
+}  // namespace fgqa
+
+extern "C" const char* fgqa_status_string(int status) {
+    switch (status) {
+        case FGQA_OK: return "ok";
+        case FGQA_ERR_INVALID_ARGUMENT: return "invalid argument";
+        case FGQA_ERR_UNSUPPORTED: return "unsupported shape, layout or alignment";
+        case FGQA_ERR_WORKSPACE: return "workspace too small";
+        case FGQA_ERR_HIP: return "HIP runtime error";
+        default: return "unknown status";
+    }
+}
+
+extern "C" int fgqa_version(void) { return 100; }

@@ -1,0 +1,296 @@
+"""Python host interface of the flash-GQA path, over the C ABI (libfgqa.so).
+
+Two families of entry points:
+
+* Mirrors of the reference's Python launchers, same names, argument meaning and
+  ``ValueError`` behaviour, BHSD layout:
+    - ``launch_flash_gqa_forward_bf16_kernel`` <- src/python/Triton/flash_gqa_kernel.py:185-338
+    - ``launch_decode_flash_gqa_bf16_kernel``  <- src/python/Triton/decode_flash_gqa_kernel.py:137-196
+* The C++ layouts of the reference's C++ decode entry point (Q/O ``[B,Hq,D]``,
+  K/V ``[B,S,Hkv,D]``, decode_flash_gqa_kernel.cuh:28-38) and of the new C++
+  prefill entry point (BSHD):
+    - ``decode_flash_gqa_bshd``  (adds per-sequence lengths and an LSE output)
+    - ``flash_gqa_forward_bshd``
+
+PyTorch only provides device memory and the current stream; every launch goes
+through ``fgqa_decode_bf16`` / ``fgqa_prefill_bf16``.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "launch_flash_gqa_forward_bf16_kernel",
+    "launch_decode_flash_gqa_bf16_kernel",
+    "decode_flash_gqa_bshd",
+    "flash_gqa_forward_bshd",
+    "decode_workspace_bytes",
+]
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _require_cuda(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("Flash GQA tensors must live on the GPU")
+
+
+def _kernel_ready(t: torch.Tensor) -> bool:
+    """Head dim contiguous, 16-byte aligned base, strides multiple of 8 elements."""
+    if t.stride(-1) != 1 or t.data_ptr() % 16 != 0:
+        return False
+    return all(s % 8 == 0 for s in t.stride()[:-1])
+
+
+def _prep(t: torch.Tensor) -> torch.Tensor:
+    return t if _kernel_ready(t) else t.contiguous()
+
+
+# --------------------------------------------------------------------------- decode
+def _decode_args(q, k, v, o, scale, seqlens, lse, split_tokens, workspace) -> _lib.DecodeArgs:
+    B, Hq, D = q.shape
+    _, S, Hkv, _ = k.shape
+    a = _lib.DecodeArgs()
+    a.q, a.k, a.v, a.o = _ptr(q), _ptr(k), _ptr(v), _ptr(o)
+    a.lse = _ptr(lse)
+    a.seqlens = _ptr(seqlens)
+    a.batch, a.max_seqlen, a.num_q_heads, a.num_kv_heads, a.head_dim = B, S, Hq, Hkv, D
+    a.scale = float(scale)
+    a.q_stride[:] = [q.stride(0), q.stride(1)]
+    a.k_stride[:] = [k.stride(0), k.stride(1), k.stride(2)]
+    a.v_stride[:] = [v.stride(0), v.stride(1), v.stride(2)]
+    a.o_stride[:] = [o.stride(0), o.stride(1)]
+    a.split_tokens = int(split_tokens)
+    if workspace is not None:
+        a.workspace = workspace.data_ptr()
+        a.workspace_bytes = workspace.numel() * workspace.element_size()
+    return a
+
+
+def decode_workspace_bytes(batch, max_seqlen, num_q_heads, num_kv_heads, head_dim=128, split_tokens=0) -> int:
+    """Bytes of scratch ``decode_flash_gqa_bshd`` needs for a caller workspace."""
+    a = _lib.DecodeArgs()
+    a.batch, a.max_seqlen, a.num_q_heads, a.num_kv_heads, a.head_dim = (
+        batch, max_seqlen, num_q_heads, num_kv_heads, head_dim)
+    a.scale = 1.0
+    a.q_stride[:] = [num_q_heads * head_dim, head_dim]
+    a.o_stride[:] = [num_q_heads * head_dim, head_dim]
+    a.k_stride[:] = [max_seqlen * num_kv_heads * head_dim, num_kv_heads * head_dim, head_dim]
+    a.v_stride[:] = list(a.k_stride)
+    a.split_tokens = int(split_tokens)
+    n = ctypes.c_size_t(0)
+    _lib.check(_lib.lib().fgqa_decode_workspace_bytes(ctypes.byref(a), ctypes.byref(n)),
+               "fgqa_decode_workspace_bytes")
+    return int(n.value)
+
+
+def decode_flash_gqa_bshd(q, k, v, scale=None, out=None, seqlens=None, lse=None,
+                          split_tokens=0, workspace=None):
+    """Single-token GQA decode in the reference C++ layout.
+
+    q: bf16 [B, Hq, D]; k, v: bf16 [B, S_max, Hkv, D]; seqlens: optional int32
+    [B] device tensor of valid lengths; lse: optional fp32 [B, Hq] output.
+    Returns ``out`` (bf16 [B, Hq, D]).
+    """
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise ValueError("Flash GQA decoding expects bf16 inputs")
+    if q.dim() != 3 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("expected q [B,Hq,D] and k/v [B,S,Hkv,D]")
+    _require_cuda(q, k, v)
+    B, Hq, D = q.shape
+    if k.shape != v.shape or k.shape[0] != B or k.shape[3] != D:
+        raise ValueError("K and V must be [B, S, Hkv, D] matching Q")
+    if Hq % k.shape[2] != 0:
+        raise ValueError("Query heads must be divisible by KV heads")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    q, k, v = _prep(q), _prep(k), _prep(v)
+    if out is None:
+        out = torch.empty((B, Hq, D), device=q.device, dtype=torch.bfloat16)
+    elif out.shape != (B, Hq, D) or out.dtype != torch.bfloat16 or not _kernel_ready(out):
+        raise ValueError("out must be a bf16 [B, Hq, D] tensor with contiguous rows")
+    if seqlens is not None:
+        if seqlens.dtype != torch.int32 or seqlens.shape != (B,) or not seqlens.is_contiguous():
+            raise ValueError("seqlens must be a contiguous int32 [B] tensor")
+        _require_cuda(seqlens)
+    if lse is not None and (lse.dtype != torch.float32 or lse.shape != (B, Hq) or not lse.is_contiguous()):
+        raise ValueError("lse must be a contiguous fp32 [B, Hq] tensor")
+    a = _decode_args(q, k, v, out, scale, seqlens, lse, split_tokens, workspace)
+    _lib.check(_lib.lib().fgqa_decode_bf16(ctypes.byref(a), ctypes.c_void_p(_stream())), "fgqa_decode_bf16")
+    return out
+
+
+def launch_decode_flash_gqa_bf16_kernel(q, k, v, out=None):
+    """Mirror of the reference's Triton decode launcher
+    (src/python/Triton/decode_flash_gqa_kernel.py:137-196): BHSD tensors
+    q [B, Hq, Sq, D] (query row 0 of each head is decoded, as in the reference
+    kernel :76-78,111-113), k/v [B, Hkv, S, D]; contiguous inputs; scale 1/sqrt(D)."""
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise ValueError("Flash GQA decoding expects bf16 inputs")
+    if not (q.is_contiguous() and k.is_contiguous() and v.is_contiguous()):
+        raise ValueError("Flash GQA decoding kernel expects contiguous Q/K/V tensors")
+    batch, q_heads, seqlen_q, head_dim = q.shape
+    k_batch, num_kv_heads, seqlen_kv, k_head_dim = k.shape
+    v_batch, v_heads, v_seqlen, v_head_dim = v.shape
+    if batch != k_batch or batch != v_batch:
+        raise ValueError("Q, K, and V must share batch dimension")
+    if seqlen_kv != v_seqlen:
+        raise ValueError("K and V must share sequence length")
+    if k_head_dim != v_head_dim or head_dim != k_head_dim:
+        raise ValueError("Q, K, and V must share head_dim")
+    if v_heads != num_kv_heads:
+        raise ValueError("K and V must share number of KV heads")
+    if q_heads % num_kv_heads != 0:
+        raise ValueError("Query heads must be divisible by KV heads")
+    if out is None:
+        out = torch.empty_like(q)
+    if not out.is_contiguous():
+        raise ValueError("Output tensor must be contiguous")
+    _require_cuda(q, k, v, out)
+    # BHSD views in the C++ decode's index order: q/o [B, Hq, D] at row 0,
+    # k/v [B, S, Hkv, D] by permuting strides (no copy).
+    q3 = q[:, :, 0, :]
+    o3 = out[:, :, 0, :]
+    k4 = k.permute(0, 2, 1, 3)
+    v4 = v.permute(0, 2, 1, 3)
+    decode_flash_gqa_bshd(q3, k4, v4, scale=1.0 / math.sqrt(head_dim), out=o3)
+    return out
+
+
+# --------------------------------------------------------------------------- prefill
+def _prefill(q, k, v, o, lse, scale, causal, layout):
+    """q/k/v/o 4-D in `layout` ('bshd' or 'bhsd'); launches fgqa_prefill_bf16."""
+    def sbh(t):
+        if layout == "bshd":
+            return [t.stride(0), t.stride(1), t.stride(2)]
+        return [t.stride(0), t.stride(2), t.stride(1)]
+
+    if layout == "bshd":
+        B, Sq, Hq, D = q.shape
+        _, Skv, Hkv, _ = k.shape
+    else:
+        B, Hq, Sq, D = q.shape
+        _, Hkv, Skv, _ = k.shape
+    a = _lib.PrefillArgs()
+    a.q, a.k, a.v, a.o, a.lse = _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse)
+    a.batch, a.seqlen_q, a.seqlen_kv = B, Sq, Skv
+    a.num_q_heads, a.num_kv_heads, a.head_dim = Hq, Hkv, D
+    a.causal = 1 if causal else 0
+    a.scale = float(scale)
+    a.q_stride[:] = sbh(q)
+    a.k_stride[:] = sbh(k)
+    a.v_stride[:] = sbh(v)
+    a.o_stride[:] = sbh(o)
+    _lib.check(_lib.lib().fgqa_prefill_bf16(ctypes.byref(a), ctypes.c_void_p(_stream())), "fgqa_prefill_bf16")
+
+
+def flash_gqa_forward_bshd(q, k, v, scale=None, out=None, lse=None, causal=True):
+    """Prefill forward in BSHD: q [B,Sq,Hq,D], k/v [B,Skv,Hkv,D] -> (out [B,Sq,Hq,D], lse [B,Hq,Sq])."""
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise ValueError("Flash GQA forward expects bf16 inputs")
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("expected 4-D BSHD tensors")
+    _require_cuda(q, k, v)
+    B, Sq, Hq, D = q.shape
+    if k.shape != v.shape or k.shape[0] != B or k.shape[3] != D:
+        raise ValueError("K and V must be [B, Skv, Hkv, D] matching Q")
+    if Hq % k.shape[2] != 0:
+        raise ValueError("Query heads must be divisible by KV heads")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    q, k, v = _prep(q), _prep(k), _prep(v)
+    if out is None:
+        out = torch.empty((B, Sq, Hq, D), device=q.device, dtype=torch.bfloat16)
+    elif out.shape != (B, Sq, Hq, D) or out.dtype != torch.bfloat16 or not _kernel_ready(out):
+        raise ValueError("Output must be a bf16 [batch, seqlen_q, q_heads, head_dim] tensor with contiguous rows")
+    if lse is None:
+        lse = torch.empty((B, Hq, Sq), device=q.device, dtype=torch.float32)
+    elif lse.shape != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise ValueError("LSE must be a contiguous fp32 [batch, q_heads, seqlen_q] tensor")
+    _prefill(q, k, v, out, lse, scale, causal, "bshd")
+    return out, lse
+
+
+def launch_flash_gqa_forward_bf16_kernel(q, k, v, scale=None, out=None, lse=None, causal=True,
+                                         block_kv_sub=32, num_warps=8, num_stages=3):
+    """Mirror of the reference's Triton prefill launcher
+    (src/python/Triton/flash_gqa_kernel.py:185-338): BHSD q [B,Hq,Sq,D] (or 3-D
+    [Hq,Sq,D]), k/v [B,Hkv,Skv,D]; returns (out, lse [B,Hq,Sq]).
+
+    ``block_kv_sub``, ``num_warps`` and ``num_stages`` are Triton tuning knobs
+    and are accepted for signature compatibility only.  Unlike the reference,
+    which writes a non-contiguous ``out``/``lse`` into a silent copy (:280-297),
+    a provided buffer is always written in place or rejected with ValueError.
+    """
+    del block_kv_sub, num_warps, num_stages
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise ValueError("Flash GQA forward expects bf16 inputs")
+    if q.dim() not in (3, 4):
+        raise ValueError("Q must be 3D or 4D")
+    if k.dim() != q.dim() or v.dim() != q.dim():
+        raise ValueError("Q, K, and V must have matching ranks")
+    _require_cuda(q, k, v)
+    squeeze_output = q.dim() == 3
+    qb = q.unsqueeze(0) if squeeze_output else q
+    kb = k.unsqueeze(0) if squeeze_output else k
+    vb = v.unsqueeze(0) if squeeze_output else v
+    batch, q_heads, seqlen_q, head_dim_qk = qb.shape
+    _, num_kv_heads, seqlen_kv, k_head_dim = kb.shape
+    _, v_heads, v_seqlen, head_dim_v = vb.shape
+    if seqlen_kv != v_seqlen:
+        raise ValueError("K and V must share sequence length")
+    if k_head_dim != head_dim_qk:
+        raise ValueError("Q and K must share head_dim_qk")
+    if v_heads != num_kv_heads:
+        raise ValueError("K and V must share number of KV heads")
+    if q_heads % num_kv_heads != 0:
+        raise ValueError("Query heads must be divisible by KV heads")
+    if head_dim_v != head_dim_qk:
+        raise ValueError("head_dim_v must equal head_dim_qk on this path")
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim_qk)
+    qb, kb, vb = _prep(qb), _prep(kb), _prep(vb)
+    if out is None:
+        out_b = torch.empty((batch, q_heads, seqlen_q, head_dim_v), device=qb.device, dtype=torch.bfloat16)
+    else:
+        if squeeze_output:
+            if out.dim() != 3:
+                raise ValueError("Output must be 3D when Q is 3D")
+            out_b = out.unsqueeze(0)
+        else:
+            if out.dim() != 4:
+                raise ValueError("Output must be 4D when Q is 4D")
+            out_b = out
+        if out_b.dtype != torch.bfloat16 or not _kernel_ready(out_b):
+            raise ValueError("Output must be bf16 with contiguous, 16-byte aligned rows")
+    if out_b.shape != (batch, q_heads, seqlen_q, head_dim_v):
+        raise ValueError("Output must have shape [batch, q_heads, seqlen_q, head_dim_v]")
+    if lse is None:
+        lse_b = torch.empty((batch, q_heads, seqlen_q), device=qb.device, dtype=torch.float32)
+    else:
+        if squeeze_output:
+            if lse.dim() != 2:
+                raise ValueError("LSE must be 2D when Q is 3D")
+            lse_b = lse.unsqueeze(0)
+        else:
+            if lse.dim() != 3:
+                raise ValueError("LSE must be 3D when Q is 4D")
+            lse_b = lse
+        if lse_b.shape != (batch, q_heads, seqlen_q) or lse_b.dtype != torch.float32 or not lse_b.is_contiguous():
+            raise ValueError("LSE must be a contiguous fp32 [batch, q_heads, seqlen_q] tensor")
+    _prefill(qb, kb, vb, out_b, lse_b, scale, causal, "bhsd")
+    if squeeze_output:
+        return out_b.squeeze(0), lse_b.squeeze(0)
+    return out_b, lse_b

@@ -1,0 +1,67 @@
+// FlashGQA decode: C++ operator entry point (MI355X / gfx950).
+//
+// Drop-in for the reference's include/cplusplus/FlashGQA/decode_flash_gqa_kernel.cuh:28-38
+// (definition src/cplusplus/FlashGQA/decode_flash_gqa_kernel.cu:405-470): same
+// name, same 11 parameters in the same order, same tensor layouts, bf16 in/out,
+// fp32 accumulation, asynchronous launch on the default stream, void return.
+#pragma once
+
+#include "Utils/utils.h"
+
+// Hardware wavefront width on gfx950 (the reference's header exports its CUDA
+// warp width, 32, under this name).
+constexpr int WARP_SIZE = 64;
+
+/**
+ * @brief Launches the FlashGQA bf16 decoding path (split-KV pass + log-sum-exp combine).
+ * @param q Device query tensor [batchSize, numQueryHeads, headDim].
+ * @param k Device key tensor [batchSize, seqLength, numKvHeads, headDim].
+ * @param v Device value tensor [batchSize, seqLength, numKvHeads, headDim].
+ * @param scale Scaling factor applied to QK scores (the reference uses 1/sqrt(headDim)).
+ * @param o Device output tensor [batchSize, numQueryHeads, headDim].
+ * @param oIntermediate Device fp32 buffer of batchSize*numQueryHeads*headDim floats.
+ *        Accepted for signature compatibility and left untouched: the split
+ *        partials live in a library-owned per-device workspace.
+ * @param batchSize Batch size.
+ * @param seqLength Sequence length (any value >= 1; the reference required a multiple of 128).
+ * @param numQueryHeads Number of query heads.
+ * @param numKvHeads Number of KV heads (numQueryHeads / numKvHeads <= 16; the reference required 16).
+ * @param headDim Per-head embedding dimension (128).
+ *
+ * Like the reference, unsupported arguments launch nothing and report nothing
+ * through the return value; FlashGqaGetLastStatus() gives the reason.
+ */
+void LaunchFlashGqaBf16Kernel(const bf16_t* q,
+                              const bf16_t* k,
+                              const bf16_t* v,
+                              float scale,
+                              bf16_t* o,
+                              float* oIntermediate,
+                              int batchSize,
+                              int seqLength,
+                              int numQueryHeads,
+                              int numKvHeads,
+                              int headDim);
+
+/**
+ * @brief Ragged variant: per-sequence valid lengths (device int32 [batchSize],
+ *        each <= maxSeqLength) over K/V padded to maxSeqLength; positions at or
+ *        past a sequence's length are never read.  No reference counterpart.
+ */
+void LaunchFlashGqaBf16KernelVarlen(const bf16_t* q,
+                                    const bf16_t* k,
+                                    const bf16_t* v,
+                                    float scale,
+                                    bf16_t* o,
+                                    const int32_t* seqLengths,
+                                    int batchSize,
+                                    int maxSeqLength,
+                                    int numQueryHeads,
+                                    int numKvHeads,
+                                    int headDim);
+
+/**
+ * @brief Status (an fgqa_status value from fgqa.h) of the calling thread's last
+ *        Launch* call in this API: 0 when it launched.
+ */
+int FlashGqaGetLastStatus();

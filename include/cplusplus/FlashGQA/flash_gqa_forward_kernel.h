@@ -1,0 +1,64 @@
+// FlashGQA prefill forward: C++ operator entry points (MI355X / gfx950).
+//
+// The reference implements prefill only in Triton
+// (src/python/Triton/flash_gqa_kernel.py:185-338, kernel :15-138); these are
+// its C++ counterparts.  Same maths and LSE layout; the default layout is
+// BSHD, matching the reference's C++ decode K/V layout.
+#pragma once
+
+#include <cstdint>
+
+#include "Utils/utils.h"
+
+/**
+ * @brief Launches the FlashGQA bf16 prefill forward (BSHD layout).
+ * @param q Device query tensor [batchSize, seqLengthQ, numQueryHeads, headDim].
+ * @param k Device key tensor [batchSize, seqLengthKv, numKvHeads, headDim].
+ * @param v Device value tensor [batchSize, seqLengthKv, numKvHeads, headDim].
+ * @param scale Scaling factor applied to QK scores.
+ * @param o Device output tensor [batchSize, seqLengthQ, numQueryHeads, headDim].
+ * @param lse Device fp32 log-sum-exp [batchSize, numQueryHeads, seqLengthQ] (natural log), or nullptr.
+ * @param batchSize Batch size.
+ * @param seqLengthQ Query sequence length.
+ * @param seqLengthKv Key/value sequence length.
+ * @param numQueryHeads Number of query heads.
+ * @param numKvHeads Number of KV heads (must divide numQueryHeads).
+ * @param headDim Per-head embedding dimension (128).
+ * @param causal Apply the top-left aligned causal mask (query i sees keys j <= i).
+ */
+void LaunchFlashGqaForwardBf16Kernel(const bf16_t* q,
+                                     const bf16_t* k,
+                                     const bf16_t* v,
+                                     float scale,
+                                     bf16_t* o,
+                                     float* lse,
+                                     int batchSize,
+                                     int seqLengthQ,
+                                     int seqLengthKv,
+                                     int numQueryHeads,
+                                     int numKvHeads,
+                                     int headDim,
+                                     bool causal);
+
+/**
+ * @brief Strided variant: element strides {batch, sequence, head} per tensor
+ *        (head dim contiguous).  BHSD, the Triton layout, is
+ *        qStride = {Hq*Sq*D, D, Sq*D}, kStride = vStride = {Hkv*Skv*D, D, Skv*D}.
+ */
+void LaunchFlashGqaForwardBf16KernelStrided(const bf16_t* q,
+                                            const bf16_t* k,
+                                            const bf16_t* v,
+                                            float scale,
+                                            bf16_t* o,
+                                            float* lse,
+                                            int batchSize,
+                                            int seqLengthQ,
+                                            int seqLengthKv,
+                                            int numQueryHeads,
+                                            int numKvHeads,
+                                            int headDim,
+                                            bool causal,
+                                            const int64_t qStride[3],
+                                            const int64_t kStride[3],
+                                            const int64_t vStride[3],
+                                            const int64_t oStride[3]);

@@ -1,0 +1,134 @@
+/*
+ * fgqa.h -- C ABI of the MI355X (gfx950) flash grouped-query attention library
+ * (libfgqa.so).  Plain pointers, sizes and a status code; no C++ or HIP types.
+ *
+ * The C++ operator entry points in include/cplusplus/ are thin wrappers over
+ * these functions.  An FFI (ctypes, cgo, JNI, N-API) binds these directly.
+ *
+ * Conventions
+ *   - bf16 tensors are passed as `const void*` / `void*` device pointers to
+ *     bfloat16 values (2 bytes, upper half of IEEE binary32).
+ *   - Strides are in ELEMENTS; the head dimension is always contiguous.
+ *     Base pointers must be 16-byte aligned and every stride a multiple of 8.
+ *   - `stream` is a hipStream_t (NULL = the default stream).  Launches are
+ *     asynchronous; the functions never synchronise the device.
+ *   - Supported: head_dim == 128; decode needs num_q_heads / num_kv_heads <= 16.
+ *   - Every entry point returns FGQA_OK (0) or a negative fgqa_status; nothing
+ *     is launched when the status is not FGQA_OK.  No exception crosses the ABI.
+ */
+#ifndef FGQA_H
+#define FGQA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum fgqa_status {
+    FGQA_OK = 0,
+    FGQA_ERR_INVALID_ARGUMENT = -1, /* null pointer, negative size, Hq % Hkv != 0 ... */
+    FGQA_ERR_UNSUPPORTED = -2,      /* valid but not implemented: head_dim, group size, alignment */
+    FGQA_ERR_WORKSPACE = -3,        /* caller workspace smaller than fgqa_decode_workspace_bytes */
+    FGQA_ERR_HIP = -4               /* a HIP runtime call or kernel launch failed */
+};
+
+/*
+ * Single-token decode (flash-decoding: split-KV pass + log-sum-exp combine).
+ * Replaces LaunchFlashGqaBf16Kernel, reference
+ * include/cplusplus/FlashGQA/decode_flash_gqa_kernel.cuh:28-38
+ * (definition src/cplusplus/FlashGQA/decode_flash_gqa_kernel.cu:405-470).
+ *
+ *   q  [B, Hq, D]           strides q_stride  = {b, h}
+ *   k  [B, S_max, Hkv, D]   strides k_stride  = {b, s, h}   (reference layout)
+ *   v  [B, S_max, Hkv, D]   strides v_stride  = {b, s, h}
+ *   o  [B, Hq, D]           strides o_stride  = {b, h}
+ *   lse  fp32 [B, Hq] contiguous, natural log (nullable)
+ *   seqlens  device int32 [B] valid lengths, each clamped to [0, max_seqlen]
+ *            (nullable: every sequence has max_seqlen tokens).  Keys at
+ *            positions >= seqlens[b] are never read.  A zero-length sequence
+ *            yields O = 0 and lse = -inf.
+ *   scale  multiplies q.k (the reference passes 1/sqrt(D)).
+ *   split_tokens  KV tokens per split (rounded up to 128); 0 = automatic.
+ *   workspace / workspace_bytes  device scratch of at least
+ *            fgqa_decode_workspace_bytes(); pass NULL/0 to let the library use
+ *            its own per-device cached buffer (allocated on first use).
+ */
+typedef struct fgqa_decode_args {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* lse;
+    const int32_t* seqlens;
+    int32_t batch;
+    int32_t max_seqlen;
+    int32_t num_q_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    float scale;
+    int64_t q_stride[2];
+    int64_t k_stride[3];
+    int64_t v_stride[3];
+    int64_t o_stride[2];
+    int32_t split_tokens;
+    void* workspace;
+    size_t workspace_bytes;
+} fgqa_decode_args;
+
+/* Bytes of workspace fgqa_decode_bf16 needs for these arguments (pointers unused). */
+int fgqa_decode_workspace_bytes(const fgqa_decode_args* args, size_t* bytes);
+
+/* Launch the decode on `stream`. */
+int fgqa_decode_bf16(const fgqa_decode_args* args, void* stream);
+
+/*
+ * Causal (or full) prefill forward.  Replaces the Triton-only
+ * launch_flash_gqa_forward_bf16_kernel, reference
+ * src/python/Triton/flash_gqa_kernel.py:185-338 (kernel :15-138), which has no
+ * C++ counterpart in the reference.
+ *
+ *   q  [B, Sq, Hq, D]  (BSHD) or any layout expressible by q_stride = {b, s, h}
+ *   k  [B, Skv, Hkv, D]        k_stride = {b, s, h}
+ *   v  [B, Skv, Hkv, D]        v_stride = {b, s, h}
+ *   o  [B, Sq, Hq, D]          o_stride = {b, s, h}
+ *   lse  fp32 [B, Hq, Sq] contiguous, natural log (nullable) -- the Triton layout
+ *   causal  nonzero: query i sees keys j <= i (top-left aligned, as the
+ *           reference's q_idx >= kv_idx mask).  A row with no visible key
+ *           (Skv == 0) yields O = 0 and lse = -inf.
+ * BHSD (the Triton layout) is q_stride = {Hq*Sq*D, D, Sq*D} etc.
+ */
+typedef struct fgqa_prefill_args {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* lse;
+    int32_t batch;
+    int32_t seqlen_q;
+    int32_t seqlen_kv;
+    int32_t num_q_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t causal;
+    float scale;
+    int64_t q_stride[3];
+    int64_t k_stride[3];
+    int64_t v_stride[3];
+    int64_t o_stride[3];
+} fgqa_prefill_args;
+
+int fgqa_prefill_bf16(const fgqa_prefill_args* args, void* stream);
+
+/* Static, human-readable text for a status code. */
+const char* fgqa_status_string(int status);
+
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int fgqa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FGQA_H */

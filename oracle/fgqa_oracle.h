@@ -1,0 +1,99 @@
+/*
+ * fgqa_oracle.h -- CPU restatement of the reference's flash grouped-query
+ * attention (decode + causal prefill), used ONLY as a parity checker.
+ *
+ * TEST INFRASTRUCTURE.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load this library, and only as the checker (or, for
+ * cpu_baseline, as the timed CPU reference).  The product path
+ * (cuda_llm_ops_amd, include/) never links, loads or calls it.
+ *
+ * bf16 values travel as uint16_t bit patterns (upper half of IEEE binary32).
+ * All sizes are element counts; strides are element strides.
+ *
+ * Parity status of each function (how it is pinned, see tests/test_oracle.py):
+ *   fgqa_oracle_f32_to_bf16 / bf16_to_f32   exhaustive 2^16 round trip + IEEE-754
+ *                                            RNE tie cases + numpy restatement
+ *   fgqa_oracle_decode_bf16                 fp64 brute force (fgqa_oracle_attention_f64)
+ *                                            at the stated tolerance, closed forms
+ *                                            (len=1, constant V, equal K), invariants
+ *   fgqa_oracle_prefill_bf16                fp64 brute force, closed forms (row 0 = V[0],
+ *                                            LSE of equal logits = log n), invariants
+ *   fgqa_oracle_attention_f64               textbook softmax attention in double;
+ *                                            pinned by numpy float64 restatement and
+ *                                            closed forms on tiny inputs
+ */
+#ifndef FGQA_ORACLE_H
+#define FGQA_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* IEEE-754 binary32 -> bfloat16, round to nearest even; NaN stays NaN (quiet). */
+uint16_t fgqa_oracle_f32_to_bf16(float x);
+float fgqa_oracle_bf16_to_f32(uint16_t h);
+void fgqa_oracle_f32_to_bf16_array(const float* src, uint16_t* dst, size_t n);
+void fgqa_oracle_bf16_to_f32_array(const uint16_t* src, float* dst, size_t n);
+
+/*
+ * Decode (one query token per sequence), restating the reference's C++ CPU
+ * reference examples/cplusplus/test_decode_flash_gqa.cu:184-255:
+ * 128-token flash tiles (tile = 128 there), fp32 q.k dot, running max in
+ * scaled units, fp32 rowsum, P rounded to bf16 before P.V, O/rowsum -> bf16.
+ * Generalised (as the new kernel is) to any group size, a partial last tile
+ * and per-sequence lengths.
+ *
+ * Layouts (the reference's, decode_flash_gqa_kernel.cu:144-148):
+ *   q, o : [B, Hq, D]         k, v : [B, S_max, Hkv, D]
+ * seqlens: host array of B lengths (each 0..S_max) or NULL (= S_max for all).
+ * lse (nullable): fp32 [B, Hq], natural log; a length-0 row gives O = 0, lse = -inf.
+ * tile: flash tile length (the reference uses 128).  nthreads <= 0: OpenMP default.
+ * Returns 0, or -1 on invalid arguments.
+ */
+int fgqa_oracle_decode_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                            float scale, uint16_t* o, float* lse,
+                            int batch, int s_max, int hq, int hkv, int d,
+                            const int32_t* seqlens, int tile, int nthreads);
+
+/*
+ * Prefill forward, restating the reference's torch reference
+ * examples/python/Triton/test_flash_gqa_kernel.py:60-90 (fp32 scores, causal
+ * triu(diagonal=1) mask = top-left aligned, q_idx >= kv_idx as in
+ * src/python/Triton/flash_gqa_kernel.py:113-117, full softmax, fp32 P.V,
+ * lse = log(sum exp) + max) with BSHD-or-any strides.
+ *   q: (b, s, h) strides qs[3]; k: ks[3]; v: vs[3]; o: os[3]; head dim contiguous.
+ *   lse (nullable): fp32, contiguous [B, Hq, Sq].
+ * q_offset: query row i sits at absolute position i + q_offset, so a causal
+ * row sees keys j <= i + q_offset (0 for the reference's square Sq = Skv case;
+ * a nonzero offset lets a test check a slice of rows of a long sequence).
+ * A row with no visible key gives O = 0 and lse = -inf.
+ */
+int fgqa_oracle_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                             float scale, uint16_t* o, float* lse,
+                             int batch, int sq, int skv, int hq, int hkv, int d,
+                             const int64_t* q_strides, const int64_t* k_strides,
+                             const int64_t* v_strides, const int64_t* o_strides,
+                             int causal, int q_offset, int nthreads);
+
+/*
+ * Textbook softmax attention in double precision (the mathematical answer the
+ * two fp32 restatements approximate).  Query row i of sequence b sees keys
+ * j < kv_len(b) and, if causal, j <= i + causal_offset.  kv_len(b) = seqlens[b]
+ * when seqlens != NULL, else skv.  Strides as in fgqa_oracle_prefill_bf16.
+ * o: double [B, Sq, Hq, D] contiguous; lse: double [B, Hq, Sq] (nullable).
+ */
+int fgqa_oracle_attention_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                              double scale, double* o, double* lse,
+                              int batch, int sq, int skv, int hq, int hkv, int d,
+                              const int64_t* q_strides, const int64_t* k_strides,
+                              const int64_t* v_strides, const int32_t* seqlens,
+                              int causal, int causal_offset, int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FGQA_ORACLE_H */

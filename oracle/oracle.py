@@ -1,0 +1,174 @@
+"""ctypes bindings and numpy helpers around ``liboracle.so`` (fgqa_oracle.c).
+
+TEST INFRASTRUCTURE ONLY -- see ``oracle/__init__.py``.
+
+bf16 tensors are numpy ``uint16`` arrays holding bfloat16 bit patterns.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_f64p = ctypes.POINTER(ctypes.c_double)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+
+
+def build() -> str:
+    """Compile liboracle.so with the committed Makefile (gcc, OpenMP)."""
+    subprocess.run(["make", "-C", _HERE, "-B", "liboracle.so"], check=True,
+                   stdout=subprocess.DEVNULL)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.fgqa_oracle_f32_to_bf16.restype = ctypes.c_uint16
+        L.fgqa_oracle_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.fgqa_oracle_bf16_to_f32.restype = ctypes.c_float
+        L.fgqa_oracle_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        L.fgqa_oracle_f32_to_bf16_array.argtypes = [_f32p, _u16p, ctypes.c_size_t]
+        L.fgqa_oracle_bf16_to_f32_array.argtypes = [_u16p, _f32p, ctypes.c_size_t]
+        L.fgqa_oracle_decode_bf16.restype = ctypes.c_int
+        L.fgqa_oracle_decode_bf16.argtypes = [
+            _u16p, _u16p, _u16p, ctypes.c_float, _u16p, _f32p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            _i32p, ctypes.c_int, ctypes.c_int]
+        L.fgqa_oracle_prefill_bf16.restype = ctypes.c_int
+        L.fgqa_oracle_prefill_bf16.argtypes = [
+            _u16p, _u16p, _u16p, ctypes.c_float, _u16p, _f32p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            _i64p, _i64p, _i64p, _i64p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.fgqa_oracle_attention_f64.restype = ctypes.c_int
+        L.fgqa_oracle_attention_f64.argtypes = [
+            _u16p, _u16p, _u16p, ctypes.c_double, _f64p, _f64p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            _i64p, _i64p, _i64p, _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray | None, ctype):
+    if a is None:
+        return ctypes.cast(None, ctypes.POINTER(ctype))
+    return a.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+# ---------------------------------------------------------------- bf16 helpers
+def f32_to_bf16(x) -> np.ndarray:
+    """float32 -> bf16 bits, round to nearest even (numpy restatement of
+    fgqa_oracle_f32_to_bf16; the two are checked against each other exhaustively)."""
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    u = x.view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    r = np.where(nan, ((u >> 16) | 0x40) & 0xFFFF, r)
+    return r.astype(np.uint16)
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    h = np.ascontiguousarray(np.asarray(h, dtype=np.uint16))
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+def normal_bf16(seed: int, shape, sigma: float = 1.0, stream: int = 0) -> np.ndarray:
+    """Seeded N(0, sigma^2) bf16 bits (numpy PCG64; `stream` separates Q/K/V)."""
+    rng = np.random.default_rng([seed, stream])
+    x = rng.standard_normal(size=shape, dtype=np.float32) * np.float32(sigma)
+    return f32_to_bf16(x)
+
+
+# ---------------------------------------------------------------- oracles
+def decode(q, k, v, scale, seqlens=None, tile=128, nthreads=0, with_lse=True):
+    """Decode oracle. q [B,Hq,D], k/v [B,S,Hkv,D] (uint16 bf16 bits).
+    Returns (o uint16 [B,Hq,D], lse float32 [B,Hq] or None)."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    B, Hq, D = q.shape
+    _, S, Hkv, _ = k.shape
+    o = np.empty((B, Hq, D), dtype=np.uint16)
+    lse = np.empty((B, Hq), dtype=np.float32) if with_lse else None
+    sl = None if seqlens is None else np.ascontiguousarray(seqlens, dtype=np.int32)
+    rc = lib().fgqa_oracle_decode_bf16(
+        _ptr(q, ctypes.c_uint16), _ptr(k, ctypes.c_uint16), _ptr(v, ctypes.c_uint16),
+        float(scale), _ptr(o, ctypes.c_uint16), _ptr(lse, ctypes.c_float),
+        B, S, Hq, Hkv, D, _ptr(sl, ctypes.c_int32), int(tile), int(nthreads))
+    if rc != 0:
+        raise ValueError("fgqa_oracle_decode_bf16: invalid arguments")
+    return o, lse
+
+
+def _strides(a: np.ndarray, layout: str):
+    """Element strides (b, s, h) of a 4-D array in `layout` ('bshd' or 'bhsd')."""
+    st = [s // a.itemsize for s in a.strides]
+    if layout == "bshd":
+        return np.array([st[0], st[1], st[2]], dtype=np.int64)
+    if layout == "bhsd":
+        return np.array([st[0], st[2], st[1]], dtype=np.int64)
+    raise ValueError(layout)
+
+
+def _dims(a: np.ndarray, layout: str):
+    B = a.shape[0]
+    if layout == "bshd":
+        return B, a.shape[1], a.shape[2], a.shape[3]
+    return B, a.shape[2], a.shape[1], a.shape[3]
+
+
+def prefill(q, k, v, scale, causal=True, layout="bshd", q_offset=0, nthreads=0):
+    """Prefill oracle. layout 'bshd': q [B,Sq,Hq,D], k/v [B,Skv,Hkv,D];
+    'bhsd': q [B,Hq,Sq,D], k/v [B,Hkv,Skv,D].  Returns (o in q's layout, lse [B,Hq,Sq])."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    B, Sq, Hq, D = _dims(q, layout)
+    _, Skv, Hkv, _ = _dims(k, layout)
+    o = np.empty_like(q)
+    lse = np.empty((B, Hq, Sq), dtype=np.float32)
+    qs, ks, vs, os_ = (_strides(x, layout) for x in (q, k, v, o))
+    rc = lib().fgqa_oracle_prefill_bf16(
+        _ptr(q, ctypes.c_uint16), _ptr(k, ctypes.c_uint16), _ptr(v, ctypes.c_uint16),
+        float(scale), _ptr(o, ctypes.c_uint16), _ptr(lse, ctypes.c_float),
+        B, Sq, Skv, Hq, Hkv, D,
+        _ptr(qs, ctypes.c_int64), _ptr(ks, ctypes.c_int64), _ptr(vs, ctypes.c_int64),
+        _ptr(os_, ctypes.c_int64), int(bool(causal)), int(q_offset), int(nthreads))
+    if rc != 0:
+        raise ValueError("fgqa_oracle_prefill_bf16: invalid arguments")
+    return o, lse
+
+
+def attention_f64(q, k, v, scale, causal=False, causal_offset=0, seqlens=None,
+                  layout="bshd", nthreads=0):
+    """float64 softmax attention. Returns (o float64 [B,Sq,Hq,D], lse float64 [B,Hq,Sq])."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    B, Sq, Hq, D = _dims(q, layout)
+    _, Skv, Hkv, _ = _dims(k, layout)
+    o = np.empty((B, Sq, Hq, D), dtype=np.float64)
+    lse = np.empty((B, Hq, Sq), dtype=np.float64)
+    qs, ks, vs = (_strides(x, layout) for x in (q, k, v))
+    sl = None if seqlens is None else np.ascontiguousarray(seqlens, dtype=np.int32)
+    rc = lib().fgqa_oracle_attention_f64(
+        _ptr(q, ctypes.c_uint16), _ptr(k, ctypes.c_uint16), _ptr(v, ctypes.c_uint16),
+        float(scale), _ptr(o, ctypes.c_double), _ptr(lse, ctypes.c_double),
+        B, Sq, Skv, Hq, Hkv, D,
+        _ptr(qs, ctypes.c_int64), _ptr(ks, ctypes.c_int64), _ptr(vs, ctypes.c_int64),
+        _ptr(sl, ctypes.c_int32), int(bool(causal)), int(causal_offset), int(nthreads))
+    if rc != 0:
+        raise ValueError("fgqa_oracle_attention_f64: invalid arguments")
+    return o, lse

@@ -1,0 +1,58 @@
+"""Shared helpers for the parity tests (inputs, tolerances, transfers)."""
+from __future__ import annotations
+
+import numpy as np
+
+# Parity bar on bf16 outputs (stated by the task for this path).
+MAX_ABS_TOL = 2e-2
+MEAN_ABS_TOL = 2e-3
+
+
+def err_stats(out, ref):
+    """(max-abs, mean-abs) of float arrays; NaN anywhere counts as infinite error."""
+    out = np.asarray(out, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    if out.shape != ref.shape:
+        raise AssertionError(f"shape mismatch {out.shape} vs {ref.shape}")
+    if out.size == 0:
+        return 0.0, 0.0
+    if not np.all(np.isfinite(out)) or not np.all(np.isfinite(ref)):
+        return float("inf"), float("inf")
+    d = np.abs(out - ref)
+    return float(d.max()), float(d.mean())
+
+
+def within_tol(out, ref, max_abs=MAX_ABS_TOL, mean_abs=MEAN_ABS_TOL):
+    mx, mn = err_stats(out, ref)
+    return mx <= max_abs and mn <= mean_abs
+
+
+def assert_close(out, ref, what="", max_abs=MAX_ABS_TOL, mean_abs=MEAN_ABS_TOL):
+    mx, mn = err_stats(out, ref)
+    assert mx <= max_abs and mn <= mean_abs, (
+        f"{what}: max-abs {mx:.3e} (tol {max_abs:.0e}), mean-abs {mn:.3e} (tol {mean_abs:.0e})")
+    return mx, mn
+
+
+def to_torch_bf16(a_u16, device):
+    """uint16 bf16 bits (numpy) -> torch bf16 tensor on `device`."""
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(a_u16).view(np.int16))
+    return t.view(torch.bfloat16).to(device)
+
+
+def from_torch_bf16(t):
+    """torch bf16 tensor -> numpy uint16 bits (host copy)."""
+    import torch
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def gpu_normal_bf16(shape, seed, sigma, device):
+    """Seeded N(0, sigma^2) bf16 tensor generated on the GPU (for GB-sized configs)."""
+    import torch
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    x = torch.randn(shape, generator=g, device=device, dtype=torch.float32)
+    if sigma != 1.0:
+        x.mul_(sigma)
+    return x.to(torch.bfloat16)

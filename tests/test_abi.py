@@ -1,0 +1,175 @@
+"""CPU tests of the drop-in boundary: libfgqa.so loads, exports every entry
+point the headers declare, and rejects bad arguments before touching a GPU."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+import cuda_llm_ops_amd as fg
+from cuda_llm_ops_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _exported():
+    out = subprocess.run(["nm", "-D", "--defined-only", "-C", _lib.LIB_PATH], check=True,
+                         capture_output=True, text=True).stdout
+    return out
+
+
+def test_c_abi_symbols_exported():
+    hdr = open(os.path.join(ROOT, "include", "fgqa.h")).read()
+    names = set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(fgqa_\w+)\s*\(", hdr, flags=re.M))
+    assert names == {"fgqa_decode_workspace_bytes", "fgqa_decode_bf16", "fgqa_prefill_bf16",
+                     "fgqa_status_string", "fgqa_version"}
+    L = _lib.lib()
+    syms = _exported()
+    for n in names:
+        assert hasattr(L, n), n
+        assert re.search(rf"\bT {n}$", syms, flags=re.M), f"{n} not exported with C linkage"
+
+
+def test_cplusplus_entry_points_exported():
+    syms = _exported()
+    decls = []
+    for sub in ("FlashGQA/decode_flash_gqa_kernel.h", "FlashGQA/flash_gqa_forward_kernel.h"):
+        hdr = open(os.path.join(ROOT, "include", "cplusplus", sub)).read()
+        decls += re.findall(r"^(?:void|int)\s+(\w+)\(", hdr, flags=re.M)
+    assert set(decls) == {"LaunchFlashGqaBf16Kernel", "LaunchFlashGqaBf16KernelVarlen", "FlashGqaGetLastStatus",
+                          "LaunchFlashGqaForwardBf16Kernel", "LaunchFlashGqaForwardBf16KernelStrided"}
+    for d in decls:
+        assert re.search(rf"\bT {d}\(", syms), d
+    # the drop-in keeps the reference's exact parameter list
+    # (decode_flash_gqa_kernel.cuh:28-38: 3 const bf16*, float, bf16*, float*, 5 ints)
+    assert "LaunchFlashGqaBf16Kernel(bf16_t const*, bf16_t const*, bf16_t const*, float, bf16_t*, float*, " \
+           "int, int, int, int, int)" in syms
+
+
+def test_status_strings_and_version():
+    assert fg.status_string(0) == "ok"
+    for code in (-1, -2, -3, -4):
+        assert fg.status_string(code) not in ("ok", "unknown status")
+    assert fg.status_string(12345) == "unknown status"
+    assert _lib.lib().fgqa_version() >= 100
+
+
+def _decode_args(**kw):
+    a = _lib.DecodeArgs()
+    B, S, Hq, Hkv, D = kw.get("B", 2), kw.get("S", 512), kw.get("Hq", 16), kw.get("Hkv", 2), kw.get("D", 128)
+    a.batch, a.max_seqlen, a.num_q_heads, a.num_kv_heads, a.head_dim = B, S, Hq, Hkv, D
+    a.scale = kw.get("scale", D ** -0.5)
+    a.q_stride[:] = [Hq * D, D]
+    a.o_stride[:] = [Hq * D, D]
+    a.k_stride[:] = [S * Hkv * D, Hkv * D, D]
+    a.v_stride[:] = [S * Hkv * D, Hkv * D, D]
+    a.split_tokens = kw.get("split_tokens", 256)
+    for name in ("q", "k", "v", "o"):
+        setattr(a, name, kw.get(name, 4096))  # fake, aligned, never dereferenced on the host
+    return a
+
+
+def _ws(a):
+    n = ctypes.c_size_t(0)
+    st = _lib.lib().fgqa_decode_workspace_bytes(ctypes.byref(a), ctypes.byref(n))
+    return st, n.value
+
+
+def test_decode_workspace_formula():
+    # B*Hq*nsplit partials of (128 fp32 O, rounded to 256 bytes) + (max, sum)
+    for S, split in ((512, 256), (4096, 1024), (1000, 128), (100, 128)):
+        st, n = _ws(_decode_args(S=S, split_tokens=split))
+        nsplit = -(-S // split)
+        slots = 2 * 16 * nsplit
+        expect = 0 if nsplit == 1 else -(-slots * 512 // 256) * 256 + slots * 8
+        assert st == 0 and n == expect, (S, split, n, expect)
+    # split_tokens rounds up to the 128-token step of a workgroup
+    assert _ws(_decode_args(S=4096, split_tokens=1000)) == _ws(_decode_args(S=4096, split_tokens=1024))
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(Hq=15), _lib.FGQA_ERR_INVALID_ARGUMENT),      # Hq % Hkv != 0
+    (dict(B=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(S=-5), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(scale=float("nan")), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(split_tokens=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(D=64), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(Hq=64, Hkv=2), _lib.FGQA_ERR_UNSUPPORTED),     # group of 32 heads
+])
+def test_decode_rejects_before_launch(kw, code):
+    a = _decode_args(**kw)
+    assert _ws(a)[0] == code
+    assert _lib.lib().fgqa_decode_bf16(ctypes.byref(a), None) == code
+
+
+def test_decode_rejects_pointers_and_alignment():
+    L = _lib.lib()
+    a = _decode_args(q=None)
+    assert L.fgqa_decode_bf16(ctypes.byref(a), None) == _lib.FGQA_ERR_INVALID_ARGUMENT
+    a = _decode_args(k=4096 + 2)
+    assert L.fgqa_decode_bf16(ctypes.byref(a), None) == _lib.FGQA_ERR_UNSUPPORTED
+    a = _decode_args()
+    a.k_stride[1] = 2 * 128 + 4
+    assert L.fgqa_decode_bf16(ctypes.byref(a), None) == _lib.FGQA_ERR_UNSUPPORTED
+    # an explicit workspace that is too small
+    a = _decode_args(split_tokens=128)
+    a.workspace, a.workspace_bytes = 4096, 16
+    assert L.fgqa_decode_bf16(ctypes.byref(a), None) == _lib.FGQA_ERR_WORKSPACE
+    assert L.fgqa_decode_bf16(None, None) == _lib.FGQA_ERR_INVALID_ARGUMENT
+    assert L.fgqa_decode_workspace_bytes(None, None) == _lib.FGQA_ERR_INVALID_ARGUMENT
+    # batch == 0 is a valid no-op that launches nothing
+    assert L.fgqa_decode_bf16(ctypes.byref(_decode_args(B=0, q=None)), None) == 0
+
+
+def _prefill_args(**kw):
+    a = _lib.PrefillArgs()
+    B, Sq, Skv, Hq, Hkv, D = (kw.get(n, d) for n, d in
+                              (("B", 1), ("Sq", 256), ("Skv", 256), ("Hq", 16), ("Hkv", 1), ("D", 128)))
+    a.batch, a.seqlen_q, a.seqlen_kv, a.num_q_heads, a.num_kv_heads, a.head_dim = B, Sq, Skv, Hq, Hkv, D
+    a.causal = 1
+    a.scale = kw.get("scale", D ** -0.5)
+    a.q_stride[:] = [Sq * Hq * D, Hq * D, D]
+    a.o_stride[:] = [Sq * Hq * D, Hq * D, D]
+    a.k_stride[:] = [Skv * Hkv * D, Hkv * D, D]
+    a.v_stride[:] = [Skv * Hkv * D, Hkv * D, D]
+    for name in ("q", "k", "v", "o"):
+        setattr(a, name, kw.get(name, 4096))
+    return a
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(Hq=15, Hkv=2), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(Sq=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(scale=float("inf")), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(D=256), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(v=None), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(o=4096 + 8), _lib.FGQA_ERR_UNSUPPORTED),
+])
+def test_prefill_rejects_before_launch(kw, code):
+    assert _lib.lib().fgqa_prefill_bf16(ctypes.byref(_prefill_args(**kw)), None) == code
+
+
+def test_prefill_empty_is_noop():
+    L = _lib.lib()
+    assert L.fgqa_prefill_bf16(ctypes.byref(_prefill_args(Sq=0, q=None)), None) == 0
+    assert L.fgqa_prefill_bf16(ctypes.byref(_prefill_args(B=0, q=None)), None) == 0
+
+
+def test_python_mirror_validation_without_gpu():
+    import torch
+    q = torch.zeros(2, 16, 1, 128, dtype=torch.float16)
+    k = torch.zeros(2, 2, 64, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="bf16"):
+        fg.launch_decode_flash_gqa_bf16_kernel(q, k, k)
+    with pytest.raises(ValueError, match="bf16"):
+        fg.launch_flash_gqa_forward_bf16_kernel(q, k, k)
+    qb = torch.zeros(2, 16, 1, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="ranks"):
+        fg.launch_flash_gqa_forward_bf16_kernel(qb, k[0], k[0])
+    with pytest.raises(ValueError, match="contiguous"):
+        fg.launch_decode_flash_gqa_bf16_kernel(qb, k.transpose(2, 3), k)
+    with pytest.raises(ValueError, match="divisible"):
+        fg.launch_decode_flash_gqa_bf16_kernel(torch.zeros(2, 15, 1, 128, dtype=torch.bfloat16), k, k)
+    with pytest.raises(ValueError, match="GPU"):
+        fg.launch_flash_gqa_forward_bf16_kernel(qb, k, k)

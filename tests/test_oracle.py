@@ -1,0 +1,299 @@
+"""CPU tests that pin the oracle (oracle/fgqa_oracle.c) before it is trusted.
+
+The reference ships no golden vectors or fixtures for this path (its checks are
+printed, recomputed from random inputs each run), so the oracle is pinned by:
+  * the IEEE-754 definition of round-to-nearest-even for bf16 (exhaustive);
+  * a float64 brute-force softmax attention, itself checked against an
+    independent numpy float64 restatement;
+  * closed forms (one token -> V[0], constant V, zero Q -> mean of V, LSE of
+    equal logits = log n) and invariants (tile-size invariance, head
+    permutation, decode == last causal prefill row, NaN padding never read);
+  * planted mistakes (wrong scale, wrong KV-head mapping, causal off by one,
+    transposed V) that the tolerance check must reject.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from tests._helpers import assert_close, within_tol
+
+SCALE = 1.0 / math.sqrt(128)
+
+
+# ----------------------------------------------------------------- bf16
+def _rne_by_definition(x32: np.ndarray) -> np.ndarray:
+    """bf16 RNE from the definition: pick the nearer of the two bf16 neighbours
+    (exact distances in float64), ties to the even mantissa."""
+    u = x32.view(np.uint32).astype(np.uint64)
+    lo = (u >> 16) & 0xFFFF                       # truncation (toward zero)
+    hi = lo + 1                                   # next bf16 away from zero
+    flo = (lo.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    fhi = (hi.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    xv = x32.astype(np.float64)
+    dlo = np.abs(xv - flo)
+    dhi = np.abs(fhi - xv)
+    pick_hi = (dhi < dlo) | ((dhi == dlo) & ((lo & 1) == 1))
+    return np.where(pick_hi, hi, lo).astype(np.uint16)
+
+
+def test_bf16_roundtrip_exhaustive():
+    L = oracle.lib()
+    bits = np.arange(65536, dtype=np.uint16)
+    f = oracle.bf16_to_f32(bits)
+    back = oracle.f32_to_bf16(f)
+    nan = np.isnan(f)
+    assert np.array_equal(back[~nan], bits[~nan])
+    assert np.all(np.isnan(oracle.bf16_to_f32(back[nan])))
+    # C and numpy conversions agree on every bf16 value
+    c_back = np.array([L.fgqa_oracle_f32_to_bf16(float(x)) for x in f[::97]], dtype=np.uint16)
+    assert np.array_equal(c_back[~np.isnan(f[::97])], bits[::97][~np.isnan(f[::97])])
+
+
+def test_bf16_rne_ties_and_random():
+    # exact midpoints: 1 + 2^-8 lies between 0x3F80 and 0x3F81 -> even 0x3F80;
+    # 1 + 3*2^-8 lies between 0x3F81 and 0x3F82 -> even 0x3F82
+    cases = np.array([1 + 2**-8, 1 + 3 * 2**-8, -(1 + 2**-8), 1 + 2**-8 + 2**-20,
+                      3.3895313892515355e38, 3.4028234663852886e38, 0.0, -0.0,
+                      1e-45, np.inf, -np.inf], dtype=np.float32)
+    expect = np.array([0x3F80, 0x3F82, 0xBF80, 0x3F81, 0x7F7F, 0x7F80, 0, 0x8000, 0, 0x7F80, 0xFF80],
+                      dtype=np.uint16)
+    assert np.array_equal(oracle.f32_to_bf16(cases), expect)
+    L = oracle.lib()
+    assert [L.fgqa_oracle_f32_to_bf16(float(x)) for x in cases] == list(expect)
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal(1 << 20) * np.exp(rng.uniform(-30, 30, 1 << 20))).astype(np.float32)
+    finite = np.isfinite(x) & (np.abs(x) < 3.38e38)
+    x = x[finite]
+    ref = _rne_by_definition(x)
+    assert np.array_equal(oracle.f32_to_bf16(x), ref)
+    out = np.empty(x.size, dtype=np.uint16)
+    L.fgqa_oracle_f32_to_bf16_array(x.ctypes.data_as(oracle.oracle._f32p), out.ctypes.data_as(oracle.oracle._u16p),
+                                    x.size)
+    assert np.array_equal(out, ref)
+
+
+# ----------------------------------------------------------------- f64 brute force
+def _attention_numpy_f64(q, k, v, scale, causal, seqlens=None, q_offset=0):
+    """Independent float64 restatement (BSHD) used to pin the C brute force."""
+    qf = oracle.bf16_to_f32(q).astype(np.float64)
+    kf = oracle.bf16_to_f32(k).astype(np.float64)
+    vf = oracle.bf16_to_f32(v).astype(np.float64)
+    B, Sq, Hq, D = qf.shape
+    _, Skv, Hkv, _ = kf.shape
+    G = Hq // Hkv
+    o = np.zeros((B, Sq, Hq, D))
+    lse = np.full((B, Hq, Sq), -np.inf)
+    for b in range(B):
+        n = Skv if seqlens is None else int(seqlens[b])
+        for h in range(Hq):
+            s = qf[b, :, h, :] @ kf[b, :n, h // G, :].T * scale
+            if causal:
+                ii = np.arange(Sq)[:, None] + q_offset
+                jj = np.arange(n)[None, :]
+                s = np.where(jj <= ii, s, -np.inf)
+            for i in range(Sq):
+                row = s[i]
+                if n == 0 or np.all(np.isneginf(row)):
+                    continue
+                m = row.max()
+                e = np.exp(row - m)
+                o[b, i, h] = (e / e.sum()) @ vf[b, :n, h // G, :]
+                lse[b, h, i] = math.log(e.sum()) + m
+    return o, lse
+
+
+@pytest.mark.parametrize("causal,sq,skv,hq,hkv", [(True, 17, 17, 4, 2), (False, 5, 23, 6, 3), (True, 9, 30, 2, 1)])
+def test_f64_bruteforce_matches_numpy(causal, sq, skv, hq, hkv):
+    q = oracle.normal_bf16(11, (2, sq, hq, 16))
+    k = oracle.normal_bf16(11, (2, skv, hkv, 16), stream=1)
+    v = oracle.normal_bf16(11, (2, skv, hkv, 16), stream=2)
+    o, lse = oracle.attention_f64(q, k, v, 0.25, causal=causal, causal_offset=3)
+    on, ln = _attention_numpy_f64(q, k, v, 0.25, causal, q_offset=3)
+    assert np.allclose(o, on, rtol=0, atol=1e-12)
+    assert np.allclose(lse, ln, rtol=0, atol=1e-12)
+    sl = np.array([skv, 3], dtype=np.int32)
+    o, lse = oracle.attention_f64(q, k, v, 0.25, causal=False, seqlens=sl)
+    on, ln = _attention_numpy_f64(q, k, v, 0.25, False, seqlens=sl)
+    assert np.allclose(o, on, rtol=0, atol=1e-12) and np.allclose(lse, ln, rtol=0, atol=1e-12)
+
+
+def test_f64_closed_forms():
+    # one key -> output is V[0]; equal logits over n keys -> lse = log n + s
+    q = np.zeros((1, 1, 2, 8), np.uint16)
+    k = oracle.normal_bf16(1, (1, 5, 1, 8))
+    v = oracle.normal_bf16(1, (1, 5, 1, 8), stream=2)
+    o, lse = oracle.attention_f64(q, k, v, 1.0)
+    vf = oracle.bf16_to_f32(v).astype(np.float64)
+    assert np.allclose(o[0, 0, 0], vf[0, :, 0].mean(0), atol=1e-14)
+    assert np.allclose(lse, math.log(5), atol=1e-14)
+    o, _ = oracle.attention_f64(q, k[:, :1], v[:, :1], 1.0)
+    assert np.array_equal(o[0, 0, 1], vf[0, 0, 0])
+
+
+# ----------------------------------------------------------------- decode oracle
+def _assert_bf16_rounding_only(out, exact):
+    """|out - exact| within one bf16 ulp of |exact| (2^-8 relative) plus the fp32
+    accumulation and bf16-P error, which stay below 2e-3 absolute at these sizes."""
+    err = np.abs(np.asarray(out, np.float64) - exact)
+    bound = np.abs(exact) * 2.0**-8 + 2e-3
+    assert np.all(err <= bound), f"worst excess {np.max(err - bound):.3e}"
+
+
+def _decode_inputs(seed, B, Hq, Hkv, S, D=128):
+    q = oracle.normal_bf16(seed, (B, Hq, D))
+    k = oracle.normal_bf16(seed, (B, S, Hkv, D), stream=1)
+    v = oracle.normal_bf16(seed, (B, S, Hkv, D), stream=2)
+    return q, k, v
+
+
+def _decode_f64(q, k, v, scale, seqlens=None):
+    o, lse = oracle.attention_f64(q[:, None], k, v, scale, seqlens=seqlens)
+    return o[:, 0], lse[:, :, 0]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S", [(2, 16, 2, 512), (1, 16, 1, 300), (3, 4, 4, 129), (2, 8, 2, 1000)])
+def test_decode_oracle_vs_f64(B, Hq, Hkv, S):
+    q, k, v = _decode_inputs(3, B, Hq, Hkv, S)
+    o, lse = oracle.decode(q, k, v, SCALE)
+    of, lf = _decode_f64(q, k, v, SCALE)
+    assert_close(oracle.bf16_to_f32(o), of, "decode oracle vs f64")
+    _assert_bf16_rounding_only(oracle.bf16_to_f32(o), of)
+    assert np.max(np.abs(lse - lf)) < 1e-4
+
+
+def test_decode_oracle_ragged_and_nan_padding():
+    B, Hq, Hkv, S = 6, 8, 2, 300
+    q, k, v = _decode_inputs(5, B, Hq, Hkv, S)
+    sl = np.array([0, 1, 127, 128, 129, 300], dtype=np.int32)
+    o, lse = oracle.decode(q, k, v, SCALE, seqlens=sl)
+    of, lf = _decode_f64(q, k, v, SCALE, seqlens=sl)
+    assert_close(oracle.bf16_to_f32(o), of, "ragged decode oracle vs f64")
+    assert np.all(oracle.bf16_to_f32(o[0]) == 0) and np.all(np.isneginf(lse[0]))
+    # padding past each length is never read: NaN there changes nothing
+    kn, vn = k.copy(), v.copy()
+    for b, n in enumerate(sl):
+        kn[b, n:] = 0x7FC0
+        vn[b, n:] = 0x7FC0
+    o2, lse2 = oracle.decode(q, kn, vn, SCALE, seqlens=sl)
+    assert np.array_equal(o, o2) and np.array_equal(lse, lse2)
+
+
+def test_decode_oracle_known_answers():
+    B, Hq, Hkv, S = 2, 8, 2, 257
+    q, k, v = _decode_inputs(9, B, Hq, Hkv, S)
+    # one token: P = bf16(exp(0)) = 1, l = 1 -> O = V[0] bit-exactly
+    o, lse = oracle.decode(q, k[:, :1], v[:, :1], SCALE)
+    G = Hq // Hkv
+    for h in range(Hq):
+        assert np.array_equal(o[:, h], v[:, 0, h // G])
+    # Q = 0: every logit is 0 -> O = mean of V over tokens, lse = log S
+    qz = np.zeros_like(q)
+    o, lse = oracle.decode(qz, k, v, SCALE)
+    vm = oracle.bf16_to_f32(v).astype(np.float64).mean(axis=1)  # [B, Hkv, D]
+    assert_close(oracle.bf16_to_f32(o), np.repeat(vm, G, axis=1), "Q=0 -> mean(V)", max_abs=4e-3)
+    assert np.allclose(lse, math.log(S), atol=1e-5)
+    # constant V = c: O = c * sum(bf16 P) / sum(P), within bf16 rounding of P
+    c = oracle.f32_to_bf16(np.float32(0.75))
+    vc = np.full_like(v, c)
+    o, _ = oracle.decode(q, k, vc, SCALE)
+    assert np.all(np.abs(oracle.bf16_to_f32(o) - 0.75) <= 0.75 * 2**-7)
+
+
+def test_decode_oracle_invariants():
+    B, Hq, Hkv, S = 2, 16, 2, 700
+    q, k, v = _decode_inputs(13, B, Hq, Hkv, S)
+    o128, _ = oracle.decode(q, k, v, SCALE, tile=128)
+    # flash tile length changes only rounding
+    for tile in (37, 512, 4096):
+        o_t, _ = oracle.decode(q, k, v, SCALE, tile=tile)
+        assert_close(oracle.bf16_to_f32(o_t), oracle.bf16_to_f32(o128), f"tile {tile}", max_abs=8e-3)
+    # permuting query heads inside a group permutes the output exactly
+    perm = np.concatenate([np.random.default_rng(0).permutation(8), 8 + np.random.default_rng(1).permutation(8)])
+    o_p, _ = oracle.decode(q[:, perm], k, v, SCALE)
+    assert np.array_equal(o_p, o128[:, perm])
+    # decode == last row of a causal prefill over the same keys
+    qp = np.zeros((B, S, Hq, 128), np.uint16)
+    qp[:, S - 1] = q
+    op, lp = oracle.prefill(qp[:, S - 8:], k, v, SCALE, causal=True, q_offset=S - 8)
+    assert_close(oracle.bf16_to_f32(op[:, -1]), oracle.bf16_to_f32(o128), "decode vs prefill last row", max_abs=8e-3)
+
+
+# ----------------------------------------------------------------- prefill oracle
+def _prefill_inputs(seed, B, Sq, Skv, Hq, Hkv, sigma=1.0, D=128):
+    q = oracle.normal_bf16(seed, (B, Sq, Hq, D), sigma)
+    k = oracle.normal_bf16(seed, (B, Skv, Hkv, D), sigma, stream=1)
+    v = oracle.normal_bf16(seed, (B, Skv, Hkv, D), sigma, stream=2)
+    return q, k, v
+
+
+@pytest.mark.parametrize("B,Sq,Skv,Hq,Hkv,causal", [
+    (1, 256, 256, 4, 1, True), (2, 64, 64, 4, 2, False), (1, 100, 160, 2, 2, True), (1, 160, 100, 3, 1, True)])
+def test_prefill_oracle_vs_f64(B, Sq, Skv, Hq, Hkv, causal):
+    q, k, v = _prefill_inputs(21, B, Sq, Skv, Hq, Hkv)
+    o, lse = oracle.prefill(q, k, v, SCALE, causal=causal)
+    of, lf = oracle.attention_f64(q, k, v, SCALE, causal=causal)
+    assert_close(oracle.bf16_to_f32(o), of, "prefill oracle vs f64")
+    _assert_bf16_rounding_only(oracle.bf16_to_f32(o), of)
+    assert np.max(np.abs(lse - lf)) < 1e-4
+
+
+def test_prefill_oracle_layouts_rows_and_closed_forms():
+    B, S, Hq, Hkv = 2, 96, 4, 2
+    q, k, v = _prefill_inputs(23, B, S, S, Hq, Hkv)
+    o, lse = oracle.prefill(q, k, v, SCALE, causal=True)
+    # BHSD layout gives the same numbers
+    ob, lb = oracle.prefill(q.transpose(0, 2, 1, 3), k.transpose(0, 2, 1, 3), v.transpose(0, 2, 1, 3), SCALE,
+                            causal=True, layout="bhsd")
+    assert np.array_equal(ob.transpose(0, 2, 1, 3), o) and np.array_equal(lb, lse)
+    # a slice of rows with q_offset equals the same rows of the full run
+    os_, ls_ = oracle.prefill(q[:, 40:70], k, v, SCALE, causal=True, q_offset=40)
+    assert np.array_equal(os_, o[:, 40:70]) and np.array_equal(ls_, lse[:, :, 40:70])
+    # causal row 0 sees only key 0: O = V[0] exactly, lse = q0.k0*scale
+    G = Hq // Hkv
+    for h in range(Hq):
+        assert np.array_equal(o[:, 0, h], v[:, 0, h // G])
+    qk0 = (oracle.bf16_to_f32(q[:, 0]).astype(np.float64) *
+           np.repeat(oracle.bf16_to_f32(k[:, 0]).astype(np.float64), G, axis=1)).sum(-1) * SCALE
+    assert np.allclose(lse[:, :, 0], qk0, atol=1e-5)
+
+
+def test_prefill_oracle_empty_kv():
+    q, k, v = _prefill_inputs(1, 1, 4, 0, 2, 1)
+    o, lse = oracle.prefill(q, k, v, SCALE, causal=True)
+    assert np.all(o == 0) and np.all(np.isneginf(lse))
+
+
+# ----------------------------------------------------------------- planted mistakes
+def test_planted_mistakes_are_caught():
+    """Each plausible slip must fail the parity bar against the f64 answer."""
+    B, Hq, Hkv, S = 2, 16, 2, 512
+    q, k, v = _decode_inputs(31, B, Hq, Hkv, S)
+    of, _ = _decode_f64(q, k, v, SCALE)
+    good, _ = oracle.decode(q, k, v, SCALE)
+    assert within_tol(oracle.bf16_to_f32(good), of)
+    # dropped/wrong scale
+    bad, _ = oracle.decode(q, k, v, SCALE * 1.5)
+    assert not within_tol(oracle.bf16_to_f32(bad), of)
+    # query head h served by KV head h % Hkv instead of h // G: place q[h] at
+    # slot p(h) = (h % Hkv) * G + h // Hkv, whose KV head is h % Hkv
+    G = Hq // Hkv
+    p_of_h = np.array([(h % Hkv) * G + h // Hkv for h in range(Hq)])
+    qslot = np.empty_like(q)
+    qslot[:, p_of_h] = q
+    bad, _ = oracle.decode(qslot, k, v, SCALE)
+    assert not within_tol(oracle.bf16_to_f32(bad)[:, p_of_h], of)
+    # V read with tokens and head-dim transposed (first 128 tokens)
+    vt = v.copy()
+    vt[:, :128, :, :] = v[:, :128, :, :].transpose(0, 3, 2, 1)
+    bad, _ = oracle.decode(q, k, vt, SCALE)
+    assert not within_tol(oracle.bf16_to_f32(bad), of)
+    # causal mask off by one in prefill
+    qp, kp, vp = _prefill_inputs(33, 1, 64, 64, 2, 1)
+    pf, _ = oracle.attention_f64(qp, kp, vp, SCALE, causal=True)
+    bad, _ = oracle.prefill(qp, kp, vp, SCALE, causal=True, q_offset=1)
+    assert not within_tol(oracle.bf16_to_f32(bad), pf)
+    good, _ = oracle.prefill(qp, kp, vp, SCALE, causal=True)
+    assert within_tol(oracle.bf16_to_f32(good), pf)
+    _assert_bf16_rounding_only(oracle.bf16_to_f32(good), pf)
