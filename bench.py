@@ -136,7 +136,8 @@ def bench_prefill(cfg_id, steps, warmup, dev):
 
 def cpu_baseline_decode(res, budget_s=12.0):
     """Time the CPU oracle (OpenMP C restatement of the reference's CPU decode)
-    on whole batches of the same inputs until ~budget_s of CPU work."""
+    on whole sequences of the same inputs, cycling through the batch until
+    ~budget_s of CPU work (or one full pass, whichever is longer)."""
     import numpy as np
     import torch
 
@@ -151,9 +152,10 @@ def cpu_baseline_decode(res, budget_s=12.0):
     elapsed = 0.0
     nb = 0
     B = cfg["B"]
-    while nb < B and elapsed < budget_s:
-        qh, kh, vh = host(res["q"][nb:nb + 1]), host(res["k"][nb:nb + 1]), host(res["v"][nb:nb + 1])
-        sl = None if res["lens"] is None else res["lens"][nb:nb + 1]
+    while nb < B or elapsed < budget_s:
+        bi = nb % B
+        qh, kh, vh = host(res["q"][bi:bi + 1]), host(res["k"][bi:bi + 1]), host(res["v"][bi:bi + 1])
+        sl = None if res["lens"] is None else res["lens"][bi:bi + 1]
         t0 = time.perf_counter()
         oracle.decode(qh, kh, vh, SCALE, seqlens=sl, nthreads=threads, with_lse=False)
         elapsed += time.perf_counter() - t0
@@ -161,8 +163,21 @@ def cpu_baseline_decode(res, budget_s=12.0):
         done_bytes += 2 * n_tok * cfg["Hkv"] * 128 * 2
         nb += 1
     return dict(value=round(done_bytes / elapsed / 1e9, 3), unit="GB/s", cores=threads, kind="port",
-                sample=f"{nb} of {B} sequences of the same workload (all heads, all tokens), "
-                       f"{elapsed:.1f} s on {threads} OpenMP threads")
+                sample=f"{nb} sequence decodes ({nb / B:.2f} passes over the {B}-sequence workload, all heads, "
+                       f"all tokens), {elapsed:.1f} s on {threads} OpenMP threads")
+
+
+def hbm_copy(steps, warmup, dev, nbytes=1 << 30):
+    """Plain device-to-device copy of `nbytes` (torch's copy kernel): the
+    calibration point for the HBM byte counters and the practical read+write
+    bandwidth of the box."""
+    import torch
+    src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    total_ms, per = _time_calls(lambda: dst.copy_(src), steps, warmup)
+    avg = sum(per) / len(per)
+    return dict(bytes_read=nbytes, bytes_written=nbytes, us_avg=avg * 1e3,
+                read_plus_write_GBs=2 * nbytes / (avg * 1e-3) / 1e9)
 
 
 def load_traffic(name):
@@ -182,6 +197,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--all", action="store_true", help="also report configs 1, 3 and 5 (to stderr)")
+    ap.add_argument("--mode", choices=["bench", "decode", "prefill", "copy"], default="bench",
+                    help="decode/prefill/copy: run only that workload (for profiling) and print its timing")
+    ap.add_argument("--config", type=int, default=0, help="with --mode decode/prefill: BASELINE config id")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (--gpus must be 1)", file=sys.stderr)
@@ -190,6 +208,20 @@ def main():
     import torch
     import cuda_llm_ops_amd  # noqa: F401  (fails loudly if libfgqa.so is missing)
     dev = torch.device("cuda:0")
+
+    if args.mode == "copy":
+        print(json.dumps({"mode": "copy", **hbm_copy(args.steps, args.warmup, dev)}), flush=True)
+        return
+    if args.mode == "decode":
+        r = bench_decode(args.config or 2, args.steps, args.warmup, args.split_tokens, dev)
+        print(json.dumps({"mode": "decode", "config": args.config or 2, "us_avg": r["avg_launch_ms"] * 1e3,
+                          "kv_bytes": r["kv_bytes"], "GBs": r["kv_bytes"] / (r["avg_launch_ms"] * 1e-3) / 1e9}),
+              flush=True)
+        return
+    if args.mode == "prefill":
+        print(json.dumps({"mode": "prefill", **bench_prefill(args.config or 4, args.steps, args.warmup, dev)}),
+              flush=True)
+        return
 
     res = bench_decode(2, args.steps, args.warmup, args.split_tokens, dev)
     gbs = res["kv_bytes"] / (res["ms_step"] * 1e-3) / 1e9

@@ -6,13 +6,14 @@
 //   pass 1 (decode_split_kernel): one workgroup per (split of the KV sequence,
 //     kv head, batch).  Each of its 4 waves streams 32-token steps; every K/V
 //     byte is read once from HBM and serves all G query heads of the group.
-//       S^T[t][h] = K[t][:] . Q[h][:]        v_mfma_f32_16x16x32_bf16, K loaded
-//                                            straight into the A-operand layout
+//       K and V rows stream in with coalesced 16-byte non-temporal loads
+//       (a quarter-wave reads one 256-byte row) and are staged in LDS
+//       S^T[t][h] = K[t][:] . Q[h][:]        v_mfma_f32_16x16x32_bf16
 //       online softmax in fp32 (exp2 with log2(e) folded into the scale), P
 //       rounded to bf16 before P.V and the rowsum kept from the fp32 P, as the
 //       reference does (decode_flash_gqa_kernel.cu:266-278)
-//       O^T[d][h] += V^T[d][t] . P^T[t][h]   v_mfma_f32_16x16x32_bf16, V staged
-//                                            through LDS for the transpose
+//       O^T[d][h] += V^T[d][t] . P^T[t][h]   v_mfma_f32_16x16x32_bf16, V^T
+//                                            gathered from the staged rows
 //     The 4 waves merge their (max, sum, O) in LDS; with one split the
 //     workgroup writes the normalised bf16 output directly, otherwise it
 //     writes an fp32 partial (O, max, sum) to the workspace.
@@ -45,10 +46,12 @@ struct DecodeParams {
 constexpr int kDecThreads = 256;
 constexpr int kDecWaves = kDecThreads / kWave;
 constexpr int kDecStep = 32;        // tokens per wave step (two 16-token MFMA blocks)
-constexpr int kDecVStride = 136;    // LDS row stride (elements) of a staged V row
-constexpr int kDecSmemBytes = kDecWaves * kDecStep * kDecVStride * 2;
+constexpr int kDecRowStride = 136;  // LDS row stride (elements) of a staged K or V row: 272 B
+                                    // spreads 16 rows over all 64 banks for b128 reads
+constexpr int kDecTileElems = kDecStep * kDecRowStride;
+constexpr int kDecSmemBytes = kDecWaves * 2 * kDecTileElems * 2;  // per wave: K tile + V tile
 static_assert(kDecWaves * 16 * kHeadDim * 4 + kDecWaves * 16 * 2 * 4 <= kDecSmemBytes,
-              "wave merge buffers must fit in the V staging area");
+              "wave merge buffers must fit in the staging area");
 
 __device__ __forceinline__ int clamp_len(const DecodeParams& p, int b) {
     int len = p.seqlens ? p.seqlens[b] : p.max_seqlen;
@@ -83,7 +86,8 @@ __global__ __launch_bounds__(kDecThreads) void decode_split_kernel(DecodeParams 
     const int g4 = lane >> 4;
 
     __shared__ __attribute__((aligned(16))) unsigned char smem[kDecSmemBytes];
-    __bf16* vl = reinterpret_cast<__bf16*>(smem) + wave * kDecStep * kDecVStride;
+    __bf16* kl = reinterpret_cast<__bf16*>(smem) + wave * 2 * kDecTileElems;
+    __bf16* vl = kl + kDecTileElems;
 
     // Q^T as the B operand: lane holds Q[h = l16][32*kk + 8*g4 .. +7]; heads >= G are zero.
     bf16x8_t qop[4];
@@ -113,41 +117,45 @@ __global__ __launch_bounds__(kDecThreads) void decode_split_kernel(DecodeParams 
     for (int db = 0; db < 8; ++db) oacc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     const int n_steps = (t_end - t_begin + kDecStep - 1) / kDecStep;
-    u32x4_t kreg[2][4];
+    // One step = 32 token rows of K and of V.  Load r (0..7) of a lane covers
+    // row 4*r + g4, 16-byte chunk l16: each quarter-wave reads one whole
+    // 256-byte row, the coalesced pattern (K and V alike).
+    u32x4_t kreg[8];
     u32x4_t vreg[8];
-
     auto load_step = [&](int st) {
         const uint32_t t0 = (uint32_t)(t_begin + st * kDecStep);
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
+        for (int r = 0; r < 8; ++r) kreg[r] = buf_load16_nt(krs, (t0 + r * 4 + g4) * kss + l16 * 16);
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk)
-                kreg[tb][kk] = buf_load16(krs, (t0 + tb * 16 + l16) * kss + (kk * 32 + g4 * 8) * 2);
-#pragma unroll
-        for (int r = 0; r < 8; ++r) vreg[r] = buf_load16(vrs, (t0 + r * 4 + g4) * vss + l16 * 16);
+        for (int r = 0; r < 8; ++r) vreg[r] = buf_load16_nt(vrs, (t0 + r * 4 + g4) * vss + l16 * 16);
     };
 
     int st = wave;
     if (st < n_steps) load_step(st);
     for (; st < n_steps; st += kDecWaves) {
-        u32x4_t kcur[2][4];
+        // Stage this step's rows, then put the next step's loads in flight.
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk) kcur[tb][kk] = kreg[tb][kk];
-        // Stage this step's V rows (coalesced: a quarter-wave holds one 256-byte row).
-#pragma unroll
-        for (int r = 0; r < 8; ++r)
-            *reinterpret_cast<u32x4_t*>(vl + (r * 4 + g4) * kDecVStride + l16 * 8) = vreg[r];
-        if (st + kDecWaves < n_steps) load_step(st + kDecWaves);  // prefetch the next step
+        for (int r = 0; r < 8; ++r) {
+            *reinterpret_cast<u32x4_t*>(kl + (r * 4 + g4) * kDecRowStride + l16 * 8) = kreg[r];
+            *reinterpret_cast<u32x4_t*>(vl + (r * 4 + g4) * kDecRowStride + l16 * 8) = vreg[r];
+        }
+        if (st + kDecWaves < n_steps) load_step(st + kDecWaves);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+        // S^T = K Q^T; K as the A operand: lane holds K[16*tb + l16][32*kk + 8*g4 .. +7].
         const int t0 = t_begin + st * kDecStep;
         f32x4_t s[2];
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) {
             s[tb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) s[tb] = mfma16(as_bf16x8(kcur[tb][kk]), qop[kk], s[tb]);
+            for (int kk = 0; kk < 4; ++kk) {
+                const bf16x8_t ka =
+                    *reinterpret_cast<const bf16x8_t*>(kl + (tb * 16 + l16) * kDecRowStride + kk * 32 + g4 * 8);
+                s[tb] = mfma16(ka, qop[kk], s[tb]);
+            }
         }
 
         // Online softmax for head l16 over tokens t0 + 16*tb + 4*g4 + i.
@@ -178,10 +186,6 @@ __global__ __launch_bounds__(kDecThreads) void decode_split_kernel(DecodeParams 
 #pragma unroll
         for (int db = 0; db < 8; ++db) oacc[db] *= alpha;
 
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
         // V^T as the A operand: lane holds V[token(slot)][16*db + l16] for the
         // 8 slots of group g4: tokens 4*g4 + {0..3} and 16 + 4*g4 + {0..3},
         // the same tokens whose P this lane already holds.
@@ -191,7 +195,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_split_kernel(DecodeParams 
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int tok = (j < 4) ? (g4 * 4 + j) : (16 + g4 * 4 + (j - 4));
-                va[j] = vl[tok * kDecVStride + db * 16 + l16];
+                va[j] = vl[tok * kDecRowStride + db * 16 + l16];
             }
             oacc[db] = mfma16(va, pop, oacc[db]);
         }
@@ -306,6 +310,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_combine_kernel(DecodeParam
 namespace {
 
 constexpr int kStepRound = kDecWaves * kDecStep;  // 128 tokens: one pass of the 4 waves
+constexpr int kMaxAutoChunk = 4096;               // longest split the planner picks by itself
 
 struct DecodePlan {
     int chunk;
@@ -355,15 +360,19 @@ int plan_decode(const fgqa_decode_args* a, DecodePlan* plan) {
     if (a->split_tokens > 0) {
         chunk = ceil_div(a->split_tokens, kStepRound) * kStepRound;
     } else {
+        // The KV stream is HBM-bound: a split only pays when there are too
+        // few (batch, kv head) streams to occupy every CU, or when sequences
+        // are long enough that one workgroup per stream would leave a long
+        // tail.  Splits cost a partial write/read and a combine pass.
         const int cus = device_cu_count();
         if (cus <= 0) return FGQA_ERR_HIP;
-        // Enough workgroups for ~4 per CU, but never below one 128-token round.
         const int64_t items = (int64_t)(a->batch > 0 ? a->batch : 1) * a->num_kv_heads;
-        int64_t want = ceil_div(4LL * cus, items);
+        int64_t want = (items >= cus) ? 1 : ceil_div(4LL * cus, items);
         const int64_t max_splits = ceil_div(S, kStepRound);
         if (want > max_splits) want = max_splits;
         if (want < 1) want = 1;
         chunk = ceil_div(ceil_div(S, want), kStepRound) * kStepRound;
+        if (chunk > kMaxAutoChunk) chunk = kMaxAutoChunk;
     }
     if (chunk < kStepRound) chunk = kStepRound;
     if (chunk > S) chunk = ceil_div(S, kStepRound) * kStepRound;
