@@ -29,6 +29,16 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
 BF16_PEAK_TFLOPS = 2516.6      # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/clk/CU
 SCALE = 1.0 / math.sqrt(128)
 
+# HBM bytes per launch of the dominant kernel, from rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE runs of `bench.py --mode decode|prefill` (KiB per dispatch x 1024).
+# FETCH_SIZE is scaled by 2.0: on this GPU it reads 524,302 KiB for a 1 GiB
+# buffer copy whose WRITE_SIZE reads the exact 1,048,576 KiB.  The summaries
+# with the commands are profiles/*_hbm_traffic.md.  Re-measure when a kernel
+# changes.
+TRAFFIC_BYTES = {
+    "decode_cfg2": 1010662256,   # = Q+K+V+O (1,010,565,120 B) + 0.01 %
+}
+
 DECODE_CONFIGS = {
     1: dict(B=2, S=512, Hq=16, Hkv=2, ragged=False, sigma=1.0),
     2: dict(B=60, S=4096, Hq=128, Hkv=8, ragged=False, sigma=1.0),
@@ -99,8 +109,8 @@ def bench_decode(cfg_id, steps, warmup, split_tokens, dev):
     n_ws = fg.decode_workspace_bytes(cfg["B"], cfg["S"], cfg["Hq"], cfg["Hkv"], split_tokens=split_tokens)
     ws = torch.empty(max(n_ws, 256), dtype=torch.uint8, device=dev)
 
-    def step():
-        fg.decode_flash_gqa_bshd(q, k, v, SCALE, out=out, seqlens=sl, split_tokens=split_tokens, workspace=ws)
+    # validated once; each step is one call of the C ABI on torch's current stream
+    step = fg.prepare_decode(q, k, v, SCALE, out=out, seqlens=sl, split_tokens=split_tokens, workspace=ws)
 
     total_ms, per = _time_calls(step, steps, warmup)
     ms_step = total_ms / steps
@@ -122,16 +132,20 @@ def bench_prefill(cfg_id, steps, warmup, dev):
     out = torch.empty_like(q)
     lse = torch.empty((B, Hq, S), dtype=torch.float32, device=dev)
 
-    def step():
-        fg.flash_gqa_forward_bshd(q, k, v, SCALE, out=out, lse=lse, causal=True)
+    step = fg.prepare_prefill(q, k, v, SCALE, out=out, lse=lse, causal=True)
 
     total_ms, per = _time_calls(step, steps, warmup)
     # the reference's causal-halved count (test_flash_gqa_kernel.py:282-301)
     flops = B * Hq * 2 * S * S * (128 + 128) // 2
     avg = sum(per) / len(per)
-    return dict(config=f"causal prefill B={B} S={S} Hq={Hq} Hkv={Hkv} D=128", us_avg=avg * 1e3,
-                us_median=per[len(per) // 2] * 1e3, us_min=per[0] * 1e3, flops=flops,
-                tflops=flops / (avg * 1e-3) / 1e12, frac=flops / (avg * 1e-3) / 1e12 / BF16_PEAK_TFLOPS)
+    tflops = flops / (avg * 1e-3) / 1e12
+    return dict(config=f"causal prefill B={B} S={S} Hq={Hq} Hkv={Hkv} D=128 (BASELINE config {cfg_id})",
+                us_avg=round(avg * 1e3, 2), us_median=round(per[len(per) // 2] * 1e3, 2),
+                us_min=round(per[0] * 1e3, 2),
+                roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
+                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                          "traffic": TRAFFIC_BYTES.get(f"prefill_cfg{cfg_id}"), "kernel": "prefill_kernel",
+                          "algorithmic_flops": flops})
 
 
 def cpu_baseline_decode(res, budget_s=12.0):
@@ -178,14 +192,6 @@ def hbm_copy(steps, warmup, dev, nbytes=1 << 30):
     avg = sum(per) / len(per)
     return dict(bytes_read=nbytes, bytes_written=nbytes, us_avg=avg * 1e3,
                 read_plus_write_GBs=2 * nbytes / (avg * 1e-3) / 1e9)
-
-
-def load_traffic(name):
-    p = os.path.join(ROOT, "profiles", name)
-    if os.path.exists(p):
-        with open(p) as f:
-            return json.load(f).get("traffic_bytes")
-    return None
 
 
 def main():
@@ -243,7 +249,7 @@ def main():
                    "num_q_heads": 128, "num_kv_heads": 8, "head_dim": 128, "parallelism": "none (1 GPU)",
                    "split_tokens": args.split_tokens or "auto"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic("decode_cfg2_traffic.json"),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_BYTES.get("decode_cfg2"),
                      "kernel": "decode (split-KV pass + LSE combine)", "algorithmic_bytes": res["kv_bytes"],
                      "avg_launch_us": round(res["avg_launch_ms"] * 1e3, 2),
                      "median_launch_us": round(res["median_ms"] * 1e3, 2),

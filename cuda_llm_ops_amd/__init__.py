@@ -10,6 +10,9 @@ from .flash_gqa import (  # noqa: F401
     flash_gqa_forward_bshd,
     launch_decode_flash_gqa_bf16_kernel,
     launch_flash_gqa_forward_bf16_kernel,
+    prepare_decode,
+    prepare_prefill,
+    PreparedLaunch,
 )
 
 __version__ = "0.1.0"

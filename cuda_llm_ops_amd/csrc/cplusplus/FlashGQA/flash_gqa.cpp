@@ -40,6 +40,12 @@ void LaunchFlashGqaBf16Kernel(const bf16_t* q, const bf16_t* k, const bf16_t* v,
                               float* oIntermediate, int batchSize, int seqLength, int numQueryHeads,
                               int numKvHeads, int headDim) {
     (void)oIntermediate;
+    // The reference returns before launching when batchSize or seqLength is
+    // not positive (decode_flash_gqa_kernel.cu:416-418); so does the drop-in.
+    if (batchSize <= 0 || seqLength <= 0) {
+        g_last_status = (batchSize < 0 || seqLength < 0) ? FGQA_ERR_INVALID_ARGUMENT : FGQA_OK;
+        return;
+    }
     fgqa_decode_args a =
         contiguous_decode(q, k, v, scale, o, batchSize, seqLength, numQueryHeads, numKvHeads, headDim);
     g_last_status = fgqa_decode_bf16(&a, nullptr);

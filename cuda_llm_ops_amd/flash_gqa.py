@@ -30,6 +30,9 @@ __all__ = [
     "decode_flash_gqa_bshd",
     "flash_gqa_forward_bshd",
     "decode_workspace_bytes",
+    "prepare_decode",
+    "prepare_prefill",
+    "PreparedLaunch",
 ]
 
 
@@ -96,14 +99,8 @@ def decode_workspace_bytes(batch, max_seqlen, num_q_heads, num_kv_heads, head_di
     return int(n.value)
 
 
-def decode_flash_gqa_bshd(q, k, v, scale=None, out=None, seqlens=None, lse=None,
-                          split_tokens=0, workspace=None):
-    """Single-token GQA decode in the reference C++ layout.
-
-    q: bf16 [B, Hq, D]; k, v: bf16 [B, S_max, Hkv, D]; seqlens: optional int32
-    [B] device tensor of valid lengths; lse: optional fp32 [B, Hq] output.
-    Returns ``out`` (bf16 [B, Hq, D]).
-    """
+def _decode_prepare(q, k, v, scale, out, seqlens, lse, split_tokens, workspace):
+    """Validate decode arguments and build the C ABI argument block (no launch)."""
     if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
         raise ValueError("Flash GQA decoding expects bf16 inputs")
     if q.dim() != 3 or k.dim() != 4 or v.dim() != 4:
@@ -128,8 +125,48 @@ def decode_flash_gqa_bshd(q, k, v, scale=None, out=None, seqlens=None, lse=None,
     if lse is not None and (lse.dtype != torch.float32 or lse.shape != (B, Hq) or not lse.is_contiguous()):
         raise ValueError("lse must be a contiguous fp32 [B, Hq] tensor")
     a = _decode_args(q, k, v, out, scale, seqlens, lse, split_tokens, workspace)
+    # keep every tensor the argument block points at alive with it
+    return a, out, (q, k, v, out, seqlens, lse, workspace)
+
+
+def decode_flash_gqa_bshd(q, k, v, scale=None, out=None, seqlens=None, lse=None,
+                          split_tokens=0, workspace=None):
+    """Single-token GQA decode in the reference C++ layout.
+
+    q: bf16 [B, Hq, D]; k, v: bf16 [B, S_max, Hkv, D]; seqlens: optional int32
+    [B] device tensor of valid lengths; lse: optional fp32 [B, Hq] output.
+    Returns ``out`` (bf16 [B, Hq, D]).
+    """
+    a, out, _keep = _decode_prepare(q, k, v, scale, out, seqlens, lse, split_tokens, workspace)
     _lib.check(_lib.lib().fgqa_decode_bf16(ctypes.byref(a), ctypes.c_void_p(_stream())), "fgqa_decode_bf16")
     return out
+
+
+class PreparedLaunch:
+    """A launch validated once whose C ABI argument block is kept: calling it
+    re-launches the same work on torch's current stream with only the cost of
+    one C call (for serving loops and benchmarks that repeat a step on the same
+    buffers).  The tensors it was built from stay referenced by it."""
+
+    def __init__(self, fn, args, keep, out, where):
+        self._fn = fn
+        self._args = args
+        self._ref = ctypes.byref(args)
+        self._keep = keep
+        self.out = out
+        self._where = where
+
+    def __call__(self):
+        st = self._fn(self._ref, ctypes.c_void_p(_stream()))
+        if st != _lib.FGQA_OK:
+            raise _lib.FgqaError(st, self._where)
+        return self.out
+
+
+def prepare_decode(q, k, v, scale=None, out=None, seqlens=None, lse=None, split_tokens=0, workspace=None):
+    """``decode_flash_gqa_bshd`` validated once; returns a ``PreparedLaunch``."""
+    a, out, keep = _decode_prepare(q, k, v, scale, out, seqlens, lse, split_tokens, workspace)
+    return PreparedLaunch(_lib.lib().fgqa_decode_bf16, a, keep, out, "fgqa_decode_bf16")
 
 
 def launch_decode_flash_gqa_bf16_kernel(q, k, v, out=None):
@@ -170,8 +207,8 @@ def launch_decode_flash_gqa_bf16_kernel(q, k, v, out=None):
 
 
 # --------------------------------------------------------------------------- prefill
-def _prefill(q, k, v, o, lse, scale, causal, layout):
-    """q/k/v/o 4-D in `layout` ('bshd' or 'bhsd'); launches fgqa_prefill_bf16."""
+def _prefill_args(q, k, v, o, lse, scale, causal, layout) -> _lib.PrefillArgs:
+    """C ABI argument block for q/k/v/o 4-D in `layout` ('bshd' or 'bhsd')."""
     def sbh(t):
         if layout == "bshd":
             return [t.stride(0), t.stride(1), t.stride(2)]
@@ -193,11 +230,15 @@ def _prefill(q, k, v, o, lse, scale, causal, layout):
     a.k_stride[:] = sbh(k)
     a.v_stride[:] = sbh(v)
     a.o_stride[:] = sbh(o)
+    return a
+
+
+def _prefill(q, k, v, o, lse, scale, causal, layout):
+    a = _prefill_args(q, k, v, o, lse, scale, causal, layout)
     _lib.check(_lib.lib().fgqa_prefill_bf16(ctypes.byref(a), ctypes.c_void_p(_stream())), "fgqa_prefill_bf16")
 
 
-def flash_gqa_forward_bshd(q, k, v, scale=None, out=None, lse=None, causal=True):
-    """Prefill forward in BSHD: q [B,Sq,Hq,D], k/v [B,Skv,Hkv,D] -> (out [B,Sq,Hq,D], lse [B,Hq,Sq])."""
+def _prefill_bshd_prepare(q, k, v, scale, out, lse, causal):
     if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
         raise ValueError("Flash GQA forward expects bf16 inputs")
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
@@ -219,8 +260,24 @@ def flash_gqa_forward_bshd(q, k, v, scale=None, out=None, lse=None, causal=True)
         lse = torch.empty((B, Hq, Sq), device=q.device, dtype=torch.float32)
     elif lse.shape != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
         raise ValueError("LSE must be a contiguous fp32 [batch, q_heads, seqlen_q] tensor")
-    _prefill(q, k, v, out, lse, scale, causal, "bshd")
+    a = _prefill_args(q, k, v, out, lse, scale, causal, "bshd")
+    return a, out, lse, (q, k, v, out, lse)
+
+
+def flash_gqa_forward_bshd(q, k, v, scale=None, out=None, lse=None, causal=True):
+    """Prefill forward in BSHD: q [B,Sq,Hq,D], k/v [B,Skv,Hkv,D] -> (out [B,Sq,Hq,D], lse [B,Hq,Sq])."""
+    a, out, lse, _keep = _prefill_bshd_prepare(q, k, v, scale, out, lse, causal)
+    _lib.check(_lib.lib().fgqa_prefill_bf16(ctypes.byref(a), ctypes.c_void_p(_stream())), "fgqa_prefill_bf16")
     return out, lse
+
+
+def prepare_prefill(q, k, v, scale=None, out=None, lse=None, causal=True):
+    """``flash_gqa_forward_bshd`` validated once; returns a ``PreparedLaunch``
+    whose ``out`` is the output tensor (the LSE tensor is ``.lse``)."""
+    a, out, lse, keep = _prefill_bshd_prepare(q, k, v, scale, out, lse, causal)
+    pl = PreparedLaunch(_lib.lib().fgqa_prefill_bf16, a, keep, out, "fgqa_prefill_bf16")
+    pl.lse = lse
+    return pl
 
 
 def launch_flash_gqa_forward_bf16_kernel(q, k, v, scale=None, out=None, lse=None, causal=True,
