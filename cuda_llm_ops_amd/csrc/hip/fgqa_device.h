@@ -7,7 +7,7 @@
 //   v_mfma_f32_32x32x16_bf16  A[m][k]: lane m + 32*(k/8), element k%8
 //                             B[k][n]: lane n + 32*(k/8), element k%8
 //                             C[m][n]: lane n + 32*((m/4)%2), register (m%4) + 4*(m/8)
-// tests/test_gpu_layout.py checks these against a CPU matmul on the device.
+// The GPU parity tests check every kernel built on these layouts against the CPU oracle.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -59,6 +59,29 @@ __device__ __forceinline__ f32x16_t mfma32(bf16x8_t a, bf16x8_t b, f32x16_t c) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Transposed LDS read (ds_read_b64_tr_b16).  Within each group of 16 lanes,
+// lane i receives 4 b16 values: value j is element (i % 4) of the 8-byte
+// chunk addressed by lane 4*j + i/4 of the same group.  So if lane s of the
+// group points at row R(s/4), columns C + 4*(s%4) .. +3 of a row-major b16
+// matrix, lane i receives rows R(0..3) of column C + i.
+__device__ __forceinline__ bf16x4_t lds_read_tr16(const __bf16* p) {
+    typedef short s16x4_t __attribute__((ext_vector_type(4)));
+    const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4_t*)(__attribute__((address_space(3))) void*)(p));
+    return __builtin_bit_cast(bf16x4_t, v);
+}
+
+// {value of lane l % 32, value of lane 32 + l % 32} for every lane l
+// (v_permlane32_swap): combines the two halves of a wave in one VALU op.
+__device__ __forceinline__ float half_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 __device__ __forceinline__ float xor_max(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, kWave)); }
 __device__ __forceinline__ float xor_sum(float v, int mask) { return v + __shfl_xor(v, mask, kWave); }

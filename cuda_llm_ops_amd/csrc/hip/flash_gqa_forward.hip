@@ -6,19 +6,26 @@
 // P rounded to bf16 before P.V with the rowsum kept from the fp32 P (:122-129),
 // O /= rowsum and lse = max + log(rowsum) (:131-138).
 //
-// One workgroup = 4 waves = 128 query rows: HB heads of one KV group x
-// (128/HB) consecutive query positions, so the 4 waves share every K/V tile
-// staged in LDS (HB = 4 when G % 4 == 0, else 2 or 1).  Per wave, 32 rows:
-//   S^T[t][q] = K[t][:] . Q[q][:]       v_mfma_f32_32x32x16_bf16 (K from LDS,
-//                                       Q^T held in registers for the whole loop)
-//   O^T[d][q] += V^T[d][t] . P^T[t][q]  v_mfma_f32_32x32x16_bf16; P^T is the
-//                                       S^T accumulator itself, converted in
-//                                       registers, V^T staged transposed in LDS
-// K/V tiles of 64 tokens are double buffered in LDS: tile j+1 is fetched into
-// registers while tile j is multiplied.  Causal tile skipping: a workgroup
-// stops at its last query row, and heavy (late) query blocks are launched
-// first so the light ones fill the tail.
+// Work unit = 128 query rows: HB heads of one KV group x (128/HB) consecutive
+// query positions (HB = 4 when G % 4 == 0, else 2 or 1), so the 4 waves of a
+// workgroup share every K/V tile staged in LDS.  Under the causal mask a
+// workgroup runs two units, query blocks n-1-i and i, so every workgroup has
+// the same number of K/V tiles and the grid needs no tail balancing.
+//
+// Per wave (32 rows) and 64-token K/V tile j, software pipelined one tile ahead:
+//   phase A: S^T(j+1) = K(j+1) . Q^T          v_mfma_f32_32x32x16_bf16, K from LDS,
+//                                              Q^T in registers for the whole unit
+//            || exp2 / row sums / bf16 cast of S(j)
+//   phase B: O^T += V^T(j) . P^T(j)          v_mfma_f32_32x32x16_bf16; V^T read from
+//                                              the row-major V tile with ds_read_b64_tr_b16,
+//                                              P^T is the S^T accumulator converted in place
+//            || masks / row max / scale of S(j+1)
+// The running max is only moved (and O rescaled) when a row's new max exceeds
+// it by more than 2^8, so P <= 256 and O stays far inside fp32 range.
+// K/V tiles are staged in LDS through registers: while tile j is computed,
+// K(j+2) and V(j+1) are written to LDS and K(j+3), V(j+2) are fetched.
 #include <math.h>
+#include <stdlib.h>
 
 #include "fgqa_device.h"
 #include "fgqa_internal.h"
@@ -36,51 +43,47 @@ struct PrefillParams {
     int64_t v_sb, v_ss, v_sh;
     int64_t o_sb, o_ss, o_sh;
     int batch, sq, skv, hq, hkv, group, causal;
-    int hb;         // heads per workgroup
-    int n_hgroups;  // group / hb
-    int n_qblocks;  // ceil(sq / (128 / hb))
-    float scale_log2;
+    int hb;          // heads per unit
+    int n_hgroups;   // group / hb
+    int n_qblocks;   // ceil(sq / (128 / hb))
+    int n_streams;   // n_hgroups * hkv * batch
+    float scale_log2;   // |scale| * log2(e)
+    uint32_t q_sign;    // 0x80008000 when scale < 0 (Q is negated on load), else 0
+    int grid_mode;      // block -> unit mapping, see pf_blocks
 };
 
 constexpr int kPfThreads = 256;
-constexpr int kPfTile = 64;        // KV tokens per tile
-constexpr int kPfKStride = 136;    // K tile row stride in LDS (elements): conflict-free b128 reads
-constexpr int kPfVtStride = 68;    // V^T tile row stride in LDS (elements): conflict-free b64 reads
-constexpr int kPfKBytes = kPfTile * kPfKStride * 2;
-constexpr int kPfVtBytes = kHeadDim * kPfVtStride * 2;
-constexpr int kPfBufBytes = kPfKBytes + kPfVtBytes;
-constexpr int kPfSmemBytes = 2 * kPfBufBytes;
+constexpr int kPfTile = 64;                          // KV tokens per tile
+constexpr int kPfRowBytes = kHeadDim * 2;            // one K or V row
+constexpr int kPfTileBytes = kPfTile * kPfRowBytes;  // 16 KB
+constexpr int kPfSmemBytes = 4 * kPfTileBytes;       // K0, K1, V0, V1
+constexpr float kPfRescaleSlack = 8.f;               // log2 units: P <= 2^8 between rescales
 
-__global__ __launch_bounds__(kPfThreads) void prefill_kernel(PrefillParams p) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+// LDS tiles hold unpadded 256-byte rows whose 16-byte chunks are permuted
+// (XOR swizzle) so that both read patterns are free of bank conflicts:
+//   K: chunk c of row r sits in slot c ^ (r % 16)      (16 rows, one chunk each: b128 reads)
+//   V: chunk c of row r sits in slot c ^ 4*(r % 4)     (4 rows x 4 chunks: transposed b64 reads)
+// Tiles are filled by buffer_load ... lds (16 bytes per lane straight into
+// LDS): one instruction writes 1 KB = 4 rows, lane l taking slot l % 16 of
+// row l / 16, so each lane fetches the chunk that belongs in its slot.
 
-    // Block index -> (query block, head group, kv head, batch); late query
-    // blocks (most KV tiles under a causal mask) come first.
-    int idx = blockIdx.x;
-    const int per_q = p.n_hgroups * p.hkv * p.batch;
-    int qb = idx / per_q;
-    int rem = idx - qb * per_q;
-    if (p.causal) qb = p.n_qblocks - 1 - qb;
-    const int hg = rem % p.n_hgroups;
-    rem /= p.n_hgroups;
-    const int kvh = rem % p.hkv;
-    const int b = rem / p.hkv;
-
+template <bool kPipe>
+__device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* smem, int qb, int hg, int kvh,
+                                        int b) {
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
-    const int wave = tid / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);   // wave-uniform
     const int l32 = lane & 31;
+    const int l16 = lane & 15;
     const int g2 = lane >> 5;
     const int qrows = 128 / p.hb;
     const int q_wg0 = qb * qrows;
     const int h = kvh * p.group + hg * p.hb + (wave % p.hb);
     const int q0w = q_wg0 + (wave / p.hb) * 32;
+    const int qrow = q0w + l32;
 
-    // KV extent of the workgroup and of this wave.
     int kv_end = p.skv;
     if (p.causal) kv_end = min(kv_end, min(q_wg0 + qrows, p.sq));
-    int kv_end_w = p.skv;
-    if (p.causal) kv_end_w = min(kv_end_w, q0w + 32);
     const int n_tiles = (kv_end + kPfTile - 1) / kPfTile;
 
     // Q^T as the B operand: lane holds Q[q0w + l32][16*kk + 8*g2 .. +7]; rows >= sq read as 0.
@@ -89,131 +92,209 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(PrefillParams p) {
         make_rsrc(p.q + b * p.q_sb + h * p.q_sh, (uint32_t)(p.sq - 1) * qss + kHeadDim * 2);
     bf16x8_t qop[8];
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-        qop[kk] = as_bf16x8(buf_load16(qrs, (uint32_t)(q0w + l32) * qss + (kk * 16 + g2 * 8) * 2));
+    for (int kk = 0; kk < 8; ++kk) {
+        u32x4_t t = buf_load16(qrs, (uint32_t)qrow * qss + (kk * 16 + g2 * 8) * 2);
+        t ^= p.q_sign;
+        qop[kk] = as_bf16x8(t);
+    }
 
-    // Tile loader: thread (c = tid % 16, r0 = tid / 16) moves the 16-byte chunk c
-    // of token rows r0 + 16*i, i = 0..3.
-    const int c = tid & 15;
-    const int r0 = tid >> 4;
+    // Direct K/V tile loads.  Rows past the last key are clamped to it (their
+    // scores are masked, so they only need to be finite).
     const uint32_t kss = (uint32_t)(p.k_ss * 2);
     const uint32_t vss = (uint32_t)(p.v_ss * 2);
-    const uint32_t kv_last = (uint32_t)(p.skv > 0 ? p.skv - 1 : 0);
-    const __amdgpu_buffer_rsrc_t krs = make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, kv_last * kss + kHeadDim * 2);
-    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, kv_last * vss + kHeadDim * 2);
-    u32x4_t kr[4], vr[4];
-    auto load_tile = [&](int j) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t tok = (uint32_t)(j * kPfTile + r0 + 16 * i);
-            kr[i] = buf_load16(krs, tok * kss + c * 16);
-            vr[i] = buf_load16(vrs, tok * vss + c * 16);
-        }
+    const int kv_last = p.skv > 0 ? p.skv - 1 : 0;
+    const __amdgpu_buffer_rsrc_t krs =
+        make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, (uint32_t)kv_last * kss + kHeadDim * 2);
+    const __amdgpu_buffer_rsrc_t vrs =
+        make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, (uint32_t)kv_last * vss + kHeadDim * 2);
+    auto lds_at = [&](int byte_off) {
+        return (__attribute__((address_space(3))) void*)(smem + byte_off);
     };
-    auto store_tile = [&](int buf) {
-        __bf16* kl = reinterpret_cast<__bf16*>(smem + buf * kPfBufBytes);
-        __bf16* vt = reinterpret_cast<__bf16*>(smem + buf * kPfBufBytes + kPfKBytes);
+    auto issue_tile = [&](int j, int kb, int vb) {   // K(j) -> K buffer kb (or none), V(j) -> V buffer vb (or none)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int row = r0 + 16 * i;
-            *reinterpret_cast<u32x4_t*>(kl + row * kPfKStride + c * 8) = kr[i];
-            const bf16x8_t vv = as_bf16x8(vr[i]);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) vt[(c * 8 + e) * kPfVtStride + row] = vv[e];
+            const int r0 = 4 * (wave + 4 * i);          // first row written by this instruction
+            const int r = r0 + (lane >> 4);
+            const uint32_t tok = (uint32_t)min(j * kPfTile + r, kv_last);
+            if (kb >= 0)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, lds_at(kb * kPfTileBytes + r0 * kPfRowBytes), 16,
+                                                         tok * kss + ((l16 ^ (r & 15)) << 4), 0, 0, 0);
+            if (vb >= 0)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, lds_at((2 + vb) * kPfTileBytes + r0 * kPfRowBytes), 16,
+                                                         tok * vss + ((l16 ^ (4 * (r & 3))) << 4), 0, 0, 0);
         }
     };
 
-    float m_run = -INFINITY;
-    float l_run = 0.f;
+    // S^T(tile j) = K(j) . Q^T: lane holds column q = l32, tokens 32*tb + 8*(i/4) + 4*g2 + i%4.
+    // K operand of (tb, kk): row 32*tb + l32, chunk 2*kk + g2.
+    int koff[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) koff[kk] = l32 * kPfRowBytes + (((2 * kk + g2) ^ l16) << 4);
+    auto qk = [&](f32x16_t (&s)[2], int buf) {
+        const unsigned char* kl = smem + buf * kPfTileBytes;
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[tb][i] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) {
+                const bf16x8_t ka = *reinterpret_cast<const bf16x8_t*>(kl + tb * 32 * kPfRowBytes + koff[kk]);
+                s[tb] = mfma32(ka, qop[kk], s[tb]);
+            }
+    };
+
+    const float c = p.scale_log2;
+    // this lane's row sees keys [0, row_lim)
+    const int row_lim = p.causal ? min(p.skv, qrow + 1) : p.skv;
+    float m_run = -INFINITY;   // running max (log2 units) of this lane's row
+    float m_use = 0.f;         // m_run, or 0 while m_run is -inf
+    float l_run = 0.f;         // this lane's share of the row sum
     f32x16_t oacc[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int i = 0; i < 16; ++i) oacc[db][i] = 0.f;
 
-    if (n_tiles > 0) {
-        load_tile(0);
-        store_tile(0);
-    }
-    const int qrow = q0w + l32;
-    for (int j = 0; j < n_tiles; ++j) {
-        __syncthreads();
-        const int buf = j & 1;
-        if (j + 1 < n_tiles) load_tile(j + 1);
+    // Masks, row max and the scaled/shifted exponent argument of S(j), in place.
+    auto alu0 = [&](f32x16_t (&s)[2], int j) {
         const int kv0 = j * kPfTile;
-        if (kv0 < kv_end_w) {
-            const __bf16* kl = reinterpret_cast<const __bf16*>(smem + buf * kPfBufBytes);
-            const __bf16* vt = reinterpret_cast<const __bf16*>(smem + buf * kPfBufBytes + kPfKBytes);
-            f32x16_t s[2];
-#pragma unroll
-            for (int tb = 0; tb < 2; ++tb) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) s[tb][i] = 0.f;
-#pragma unroll
-                for (int kk = 0; kk < 8; ++kk) {
-                    const bf16x8_t ka =
-                        *reinterpret_cast<const bf16x8_t*>(kl + (tb * 32 + l32) * kPfKStride + kk * 16 + g2 * 8);
-                    s[tb] = mfma32(ka, qop[kk], s[tb]);
-                }
-            }
-            // Online softmax for query row qrow over tokens kv0 + 32*tb + 8*(i/4) + 4*g2 + i%4.
-            const bool need_mask = (kv0 + kPfTile > p.skv) || (p.causal && kv0 + kPfTile - 1 > q0w);
-            float tmax = -INFINITY;
+        const bool need_mask = (kv0 + kPfTile > p.skv) || (p.causal && kv0 + kPfTile - 1 > q0w);
+        if (need_mask) {
+            // tokens at or past `lim` (relative to this lane's first token) are masked
+            const int lim = row_lim - (kv0 + g2 * 4);
 #pragma unroll
             for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    float val = s[tb][i] * p.scale_log2;
-                    if (need_mask) {
-                        const int tok = kv0 + tb * 32 + (i >> 2) * 8 + g2 * 4 + (i & 3);
-                        if (tok >= p.skv || (p.causal && tok > qrow)) val = -INFINITY;
-                    }
-                    s[tb][i] = val;
-                    tmax = fmaxf(tmax, val);
-                }
-            tmax = xor_max(tmax, 32);
+                for (int i = 0; i < 16; ++i)
+                    if (tb * 32 + (i >> 2) * 8 + (i & 3) >= lim) s[tb][i] = -INFINITY;
+        }
+        float tmax = s[0][0];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (tb != 0 || i != 0) tmax = fmaxf(tmax, s[tb][i]);
+        tmax = half_max(tmax) * c;
+        if (__builtin_amdgcn_ballot_w64(tmax > m_run + kPfRescaleSlack) != 0) {
             const float m_new = fmaxf(m_run, tmax);
-            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-            const float alpha = fast_exp2(m_run - m_use);
-            float psum = 0.f;
-#pragma unroll
-            for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const float pv = fast_exp2(s[tb][i] - m_use);
-                    s[tb][i] = pv;
-                    psum += pv;
-                }
-            l_run = l_run * alpha + psum;
-            m_run = m_new;
+            const float m_new_use = (m_new == -INFINITY) ? 0.f : m_new;
+            const float alpha = fast_exp2(m_use - m_new_use);   // 0 on the first tile
+            l_run *= alpha;
 #pragma unroll
             for (int db = 0; db < 4; ++db) oacc[db] *= alpha;
-
-            // P.V over four 16-token k-blocks: slots 8*g2 + e map to tokens
-            // tA + e (e < 4) and tA + 8 + (e - 4), tA = 32*tb + 16*kh + 4*g2,
-            // exactly the S^T registers 8*kh .. 8*kh + 7 of this lane.
-#pragma unroll
-            for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-                for (int kh = 0; kh < 2; ++kh) {
-                    bf16x8_t pb;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) pb[e] = (__bf16)s[tb][kh * 8 + e];
-                    const int tA = tb * 32 + kh * 16 + g2 * 4;
-#pragma unroll
-                    for (int db = 0; db < 4; ++db) {
-                        const __bf16* vrow = vt + (db * 32 + l32) * kPfVtStride;
-                        const bf16x4_t lo = *reinterpret_cast<const bf16x4_t*>(vrow + tA);
-                        const bf16x4_t hi = *reinterpret_cast<const bf16x4_t*>(vrow + tA + 8);
-                        const bf16x8_t va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                        oacc[db] = mfma32(va, pb, oacc[db]);
-                    }
-                }
+            m_run = m_new;
+            m_use = m_new_use;
         }
-        if (j + 1 < n_tiles) store_tile(buf ^ 1);
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[tb][i] = __builtin_fmaf(s[tb][i], c, -m_use);
+    };
+
+    // exp2, row sums and the bf16 P^T operands of S(j).
+    bf16x8_t pop[4];
+    auto alu1 = [&](f32x16_t (&s)[2]) {
+        float psum = 0.f;
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float pv = fast_exp2(s[tb][kh * 8 + e]);
+                    psum += pv;
+                    pop[tb * 2 + kh][e] = (__bf16)pv;
+                }
+        l_run += psum;
+    };
+
+    // O^T += V^T(j) . P^T(j) over four 16-token k-blocks.  Slots 0..3 of lane
+    // (l32, g2) hold tokens 16*kb + 4*g2 + 0..3, slots 4..7 tokens 16*kb + 8 + 4*g2 + 0..3:
+    // the S^T registers 8*(kb%2) .. +7 of block kb/2, and the two transposed
+    // V reads below.  Lane i of a 16-lane group supplies row 16*kb + 4*g2 + i/4
+    // (+8), columns 32*db + 16*((lane/16)%2) + 4*(i%4) .. +3, which is chunk
+    // 4*db + 2*((lane/16)%2) + (i%4)/2, half i%2 of the swizzled row.
+    int voff[4];
+    {
+        const int q4 = l16 >> 2;
+        const int dh = (lane >> 4) & 1;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+            voff[db] = (4 * g2 + q4) * kPfRowBytes + ((4 * (db ^ q4) + 2 * dh + ((l16 >> 1) & 1)) << 4) + 8 * (l16 & 1);
+    }
+    auto pv = [&](int buf) {
+        const unsigned char* vl = smem + (2 + buf) * kPfTileBytes;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const unsigned char* base = vl + 16 * kb * kPfRowBytes + voff[db];
+                const bf16x4_t lo = lds_read_tr16(reinterpret_cast<const __bf16*>(base));
+                const bf16x4_t hi = lds_read_tr16(reinterpret_cast<const __bf16*>(base + 8 * kPfRowBytes));
+                const bf16x8_t va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                oacc[db] = mfma32(va, pop[kb], oacc[db]);
+            }
+    };
+
+    // this wave's direct LDS loads have landed (then a barrier publishes them)
+    auto wait_vmem = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
+
+    __syncthreads();  // the previous unit may still read the buffers
+    if constexpr (kPipe) {
+        // K runs one tile ahead of V: iteration j reads K(j+1) and V(j) while
+        // K(j+2) and V(j+1) land in the buffers freed by iteration j-1.
+        if (n_tiles > 0) issue_tile(0, 0, 0);
+        if (n_tiles > 1) issue_tile(1, 1, -1);
+        wait_vmem();
+        __syncthreads();
+
+        // One pipelined step: S(j+1) into sn while S(j) (in sc) finishes.
+        auto step = [&](f32x16_t (&sc)[2], f32x16_t (&sn)[2], int j) {
+            const bool more = j + 1 < n_tiles;   // block-uniform
+            if (j + 2 < n_tiles) issue_tile(j + 2, j & 1, -1);
+            if (more) issue_tile(j + 1, -1, (j + 1) & 1);
+            // phase A: S(j+1) on the MFMA pipe, exp2 of S(j) on the VALU
+            if (more) qk(sn, (j + 1) & 1);
+            alu1(sc);
+            // phase B: P(j).V(j) on the MFMA pipe, max/scale of S(j+1) on the VALU
+            pv(j & 1);
+            if (more) alu0(sn, j + 1);
+            wait_vmem();
+            __syncthreads();
+        };
+        f32x16_t sa[2], sb[2];
+        if (n_tiles > 0) {
+            qk(sa, 0);
+            alu0(sa, 0);
+        }
+        for (int j = 0; j < n_tiles; j += 2) {
+            step(sa, sb, j);
+            if (j + 1 < n_tiles) step(sb, sa, j + 1);
+        }
+    } else {
+        // Tile j+1 lands in the other buffer while tile j is computed.
+        // Overlap of MFMA and VALU work comes from the other wave on the SIMD.
+        if (n_tiles > 0) issue_tile(0, 0, 0);
+        wait_vmem();
+        __syncthreads();
+        f32x16_t s[2];
+        for (int j = 0; j < n_tiles; ++j) {
+            if (j + 1 < n_tiles) issue_tile(j + 1, (j + 1) & 1, (j + 1) & 1);
+            // Tiles past this wave's causal limit are fully masked and add
+            // nothing; they are computed anyway so that the accumulators never
+            // pass through a branch (which costs register copies).
+            qk(s, j & 1);
+            alu0(s, j);
+            alu1(s);
+            pv(j & 1);
+            wait_vmem();
+            __syncthreads();
+        }
     }
 
-    l_run = xor_sum(l_run, 32);
+    l_run = half_sum(l_run);
     if (qrow < p.sq) {
         const float inv = (l_run > 0.f) ? 1.f / l_run : 0.f;
         __bf16* orow = p.o + b * p.o_sb + (int64_t)qrow * p.o_ss + h * p.o_sh;
@@ -229,6 +310,50 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(PrefillParams p) {
         if (p.lse != nullptr && g2 == 0)
             p.lse[((int64_t)b * p.hq + h) * p.sq + qrow] = (l_run > 0.f) ? m_run * kLn2 + logf(l_run) : -INFINITY;
     }
+}
+
+// Block -> work unit(s).  grid_mode 0: each block runs the pair of query
+// blocks (n-1-slot, slot) of one stream (causal), or one block (non-causal).
+// grid_mode 1: one unit per block, heaviest first, blocks k and k + N/2 taking
+// complementary units.  grid_mode 2: one unit per block, heaviest first.
+// Streams (head group, kv head, batch) are the fastest index, so with a
+// multiple of 8 streams each stream's blocks share one XCD.
+template <bool kPipe>
+__device__ __forceinline__ void pf_blocks(const PrefillParams& p, unsigned char* smem) {
+    const int k = blockIdx.x;
+    int stream, qa, qb2 = -1;
+    if (p.grid_mode == 0) {
+        stream = k % p.n_streams;
+        const int slot = k / p.n_streams;
+        qa = p.causal ? p.n_qblocks - 1 - slot : slot;
+        if (p.causal && slot < qa) qb2 = slot;
+    } else {
+        const int total = p.n_qblocks * p.n_streams;
+        int r = k;
+        if (p.grid_mode == 1) {
+            const int half = (total + 1) / 2;
+            r = (k < half) ? k : total - 1 - (k - half);
+        }
+        stream = r % p.n_streams;
+        const int rank_q = r / p.n_streams;
+        qa = p.causal ? p.n_qblocks - 1 - rank_q : rank_q;
+    }
+    const int hg = stream % p.n_hgroups;
+    const int kvh = (stream / p.n_hgroups) % p.hkv;
+    const int b = stream / (p.n_hgroups * p.hkv);
+    const int nunits = qb2 >= 0 ? 2 : 1;
+    for (int u = 0; u < nunits; ++u) pf_unit<kPipe>(p, smem, u == 0 ? qa : qb2, hg, kvh, b);
+}
+
+__global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillParams p) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    pf_blocks<true>(p, smem);
+}
+
+// Two waves per SIMD: 256 registers per wave at most.
+__global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel_2w(PrefillParams p) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    pf_blocks<false>(p, smem);
 }
 
 namespace {
@@ -298,20 +423,40 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
     p.hb = (p.group % 4 == 0) ? 4 : (p.group % 2 == 0) ? 2 : 1;
     p.n_hgroups = p.group / p.hb;
     p.n_qblocks = (int)ceil_div(p.sq, 128 / p.hb);
-    p.scale_log2 = a->scale * kLog2e;
+    p.n_streams = p.n_hgroups * p.hkv * p.batch;
+    p.scale_log2 = fabsf(a->scale) * kLog2e;
+    p.q_sign = (a->scale < 0.f) ? 0x80008000u : 0u;
 
-    const int64_t nblocks = (int64_t)p.n_qblocks * p.n_hgroups * p.hkv * p.batch;
+    const int64_t units = (int64_t)p.n_qblocks * p.n_streams;
+    // Causal work per unit grows with its query block.  When every unit gets
+    // a slot at once (two workgroups per CU), blocks k and k + units/2 take
+    // complementary units; otherwise blocks go heaviest first.
+    const int cus = device_cu_count();
+    p.grid_mode = (p.causal && cus > 0 && units <= 2 * (int64_t)cus) ? 1 : 2;
+    bool two_waves = false;
+    if (const char* e = getenv("FGQA_PF_VARIANT")) {   // tuning override: kernel*10 + grid_mode
+        const int variant = atoi(e);
+        two_waves = variant / 10 == 1;
+        p.grid_mode = variant % 10;
+    }
+    if (!p.causal && p.grid_mode == 1) p.grid_mode = 2;
+    const int64_t nblocks = (p.grid_mode == 0 && p.causal) ? ceil_div(p.n_qblocks, 2) * p.n_streams : units;
     if (nblocks >= ((int64_t)1 << 31)) return FGQA_ERR_UNSUPPORTED;
 
-    static bool smem_set = false;
-    if (!smem_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, kPfSmemBytes) != hipSuccess)
+    const void* fn = two_waves ? reinterpret_cast<const void*>(prefill_kernel_2w)
+                               : reinterpret_cast<const void*>(prefill_kernel);
+    static bool smem_set[2] = {false, false};
+    if (!smem_set[two_waves]) {
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kPfSmemBytes) != hipSuccess)
             return FGQA_ERR_HIP;
-        smem_set = true;
+        smem_set[two_waves] = true;
     }
-    hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)nblocks), dim3(kPfThreads), kPfSmemBytes,
-                       static_cast<hipStream_t>(stream), p);
+    if (two_waves)
+        hipLaunchKernelGGL(prefill_kernel_2w, dim3((unsigned)nblocks), dim3(kPfThreads), kPfSmemBytes,
+                           static_cast<hipStream_t>(stream), p);
+    else
+        hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)nblocks), dim3(kPfThreads), kPfSmemBytes,
+                           static_cast<hipStream_t>(stream), p);
     if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
     return FGQA_OK;
 }
