@@ -7,10 +7,15 @@
 // O /= rowsum and lse = max + log(rowsum) (:131-138).
 //
 // Work unit = 128 query rows: HB heads of one KV group x (128/HB) consecutive
-// query positions (HB = 4 when G % 4 == 0, else 2 or 1), so the 4 waves of a
-// workgroup share every K/V tile staged in LDS.  Under the causal mask a
-// workgroup runs two units, query blocks n-1-i and i, so every workgroup has
-// the same number of K/V tiles and the grid needs no tail balancing.
+// query positions (HB = 4 when G % 4 == 0, else 2 or 1), one wave per 32 rows,
+// so the waves of a unit share every K/V tile staged in LDS.  Two shapes:
+//   prefill_kernel        4 waves run a unit over its whole KV range; two
+//                         workgroups share a CU (2 waves per SIMD).
+//   prefill_split_kernel  8 waves: two groups of 4 run the two halves of the
+//                         unit's KV range side by side (2 waves per SIMD) and
+//                         merge their partial (max, sum, O) through LDS.  Used
+//                         when there are too few units to keep every CU busy
+//                         with two workgroups until the end.
 //
 // Per wave (32 rows) and 64-token K/V tile j, software pipelined one tile ahead:
 //   phase A: S^T(j+1) = K(j+1) . Q^T          v_mfma_f32_32x32x16_bf16, K from LDS,
@@ -20,11 +25,12 @@
 //                                              the row-major V tile with ds_read_b64_tr_b16,
 //                                              P^T is the S^T accumulator converted in place
 //            || masks / row max / scale of S(j+1)
-// The running max is only moved (and O rescaled) when a row's new max exceeds
+// The running max only moves (and O is rescaled) when a row's new max exceeds
 // it by more than 2^8, so P <= 256 and O stays far inside fp32 range.
-// K/V tiles are staged in LDS through registers: while tile j is computed,
-// K(j+2) and V(j+1) are written to LDS and K(j+3), V(j+2) are fetched.
+// K(j+2) and V(j+1) stream straight into LDS (buffer_load ... lds) while tile
+// j is computed.
 #include <math.h>
+#include <stdint.h>
 #include <stdlib.h>
 
 #include "fgqa_device.h"
@@ -49,15 +55,18 @@ struct PrefillParams {
     int n_streams;   // n_hgroups * hkv * batch
     float scale_log2;   // |scale| * log2(e)
     uint32_t q_sign;    // 0x80008000 when scale < 0 (Q is negated on load), else 0
-    int grid_mode;      // block -> unit mapping, see pf_blocks
 };
 
-constexpr int kPfThreads = 256;
+constexpr int kPfWaves = 4;                          // waves per group (one unit's rows)
+constexpr int kPfThreads = kPfWaves * kWave;
 constexpr int kPfTile = 64;                          // KV tokens per tile
 constexpr int kPfRowBytes = kHeadDim * 2;            // one K or V row
 constexpr int kPfTileBytes = kPfTile * kPfRowBytes;  // 16 KB
-constexpr int kPfSmemBytes = 4 * kPfTileBytes;       // K0, K1, V0, V1
+constexpr int kPfGroupBytes = 4 * kPfTileBytes;      // K0, K1, V0, V1 of one group
 constexpr float kPfRescaleSlack = 8.f;               // log2 units: P <= 2^8 between rescales
+// merge area of the split kernel: per wave, 64 O values + max + sum per lane
+constexpr int kPfMergeFloats = 66;
+static_assert(kPfWaves * kPfMergeFloats * kWave * 4 <= 2 * kPfGroupBytes, "merge area must fit in the tile buffers");
 
 // LDS tiles hold unpadded 256-byte rows whose 16-byte chunks are permuted
 // (XOR swizzle) so that both read patterns are free of bank conflicts:
@@ -67,12 +76,18 @@ constexpr float kPfRescaleSlack = 8.f;               // log2 units: P <= 2^8 bet
 // LDS): one instruction writes 1 KB = 4 rows, lane l taking slot l % 16 of
 // row l / 16, so each lane fetches the chunk that belongs in its slot.
 
-template <bool kPipe>
-__device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* smem, int qb, int hg, int kvh,
+// One unit (query block qb of head group hg, kv head kvh, batch b).  With
+// kGroups == 2, group `grp` covers tiles [grp*half, grp*half + half) of the
+// unit's KV range; tiles past the range are fully masked and add nothing.
+template <int kGroups>
+__device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* smem_all, int qb, int hg, int kvh,
                                         int b) {
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
-    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);   // wave-uniform
+    const int wave_wg = __builtin_amdgcn_readfirstlane(tid / kWave);   // wave-uniform
+    const int grp = wave_wg / kPfWaves;
+    const int wave = wave_wg % kPfWaves;
+    unsigned char* smem = smem_all + grp * kPfGroupBytes;
     const int l32 = lane & 31;
     const int l16 = lane & 15;
     const int g2 = lane >> 5;
@@ -84,7 +99,11 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
 
     int kv_end = p.skv;
     if (p.causal) kv_end = min(kv_end, min(q_wg0 + qrows, p.sq));
-    const int n_tiles = (kv_end + kPfTile - 1) / kPfTile;
+    const int unit_tiles = (kv_end + kPfTile - 1) / kPfTile;
+    const int n_tiles = kGroups == 1 ? unit_tiles : (unit_tiles + 1) / 2;   // loop trips, same for both groups
+    const int t_first = grp * n_tiles;                                        // first tile of this group
+    // keys this group may use: the unit's range, cut at the group's last tile
+    const int kv_hi = min(kv_end, (t_first + n_tiles) * kPfTile);
 
     // Q^T as the B operand: lane holds Q[q0w + l32][16*kk + 8*g2 .. +7]; rows >= sq read as 0.
     const uint32_t qss = (uint32_t)(p.q_ss * 2);
@@ -107,21 +126,28 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, (uint32_t)kv_last * kss + kHeadDim * 2);
     const __amdgpu_buffer_rsrc_t vrs =
         make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, (uint32_t)kv_last * vss + kHeadDim * 2);
-    auto lds_at = [&](int byte_off) {
-        return (__attribute__((address_space(3))) void*)(smem + byte_off);
+    // K(t_first + j) -> K buffer kb (skipped when kb < 0), V(t_first + j) -> V buffer vb.
+    // Written as inline asm so that the compiler does not treat every later
+    // LDS read as dependent on these writes (it would wait for them to land
+    // before reading the other buffer); their completion is awaited
+    // explicitly (wait_vmem) before the barrier that publishes the tile.
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)smem;
+    auto dma16 = [](uint32_t lds_addr, uint32_t voffset, __amdgpu_buffer_rsrc_t rsrc) {
+        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                     :: "s"(lds_addr), "v"(voffset), "s"(rsrc) : "memory");
     };
-    auto issue_tile = [&](int j, int kb, int vb) {   // K(j) -> K buffer kb (or none), V(j) -> V buffer vb (or none)
+    auto issue_tile = [&](int j, int kb, int vb) {
+        const int t = t_first + j;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r0 = 4 * (wave + 4 * i);          // first row written by this instruction
             const int r = r0 + (lane >> 4);
-            const uint32_t tok = (uint32_t)min(j * kPfTile + r, kv_last);
+            const uint32_t tok = (uint32_t)min(t * kPfTile + r, kv_last);
             if (kb >= 0)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, lds_at(kb * kPfTileBytes + r0 * kPfRowBytes), 16,
-                                                         tok * kss + ((l16 ^ (r & 15)) << 4), 0, 0, 0);
+                dma16(lds_base + kb * kPfTileBytes + r0 * kPfRowBytes, tok * kss + ((l16 ^ (r & 15)) << 4), krs);
             if (vb >= 0)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, lds_at((2 + vb) * kPfTileBytes + r0 * kPfRowBytes), 16,
-                                                         tok * vss + ((l16 ^ (4 * (r & 3))) << 4), 0, 0, 0);
+                dma16(lds_base + (2 + vb) * kPfTileBytes + r0 * kPfRowBytes, tok * vss + ((l16 ^ (4 * (r & 3))) << 4),
+                      vrs);
         }
     };
 
@@ -157,26 +183,33 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
 #pragma unroll
         for (int i = 0; i < 16; ++i) oacc[db][i] = 0.f;
 
-    // Masks, row max and the scaled/shifted exponent argument of S(j), in place.
-    auto alu0 = [&](f32x16_t (&s)[2], int j) {
-        const int kv0 = j * kPfTile;
-        const bool need_mask = (kv0 + kPfTile > p.skv) || (p.causal && kv0 + kPfTile - 1 > q0w);
+    // Causal / tail mask of S(j), in place (only tiles that cross a boundary).
+    auto mask = [&](f32x16_t (&s)[2], int j) {
+        const int kv0 = (t_first + j) * kPfTile;
+        const bool need_mask = (kv0 + kPfTile > kv_hi) || (p.causal && kv0 + kPfTile - 1 > q0w);
         if (need_mask) {
             // tokens at or past `lim` (relative to this lane's first token) are masked
-            const int lim = row_lim - (kv0 + g2 * 4);
+            const int lim = min(row_lim, kv_hi) - (kv0 + g2 * 4);
 #pragma unroll
             for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
                 for (int i = 0; i < 16; ++i)
                     if (tb * 32 + (i >> 2) * 8 + (i & 3) >= lim) s[tb][i] = -INFINITY;
         }
+    };
+    // Row max of S(j) (log2 units) across both wave halves.
+    auto rowmax = [&](f32x16_t (&s)[2]) {
         float tmax = s[0][0];
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
             for (int i = 0; i < 16; ++i)
                 if (tb != 0 || i != 0) tmax = fmaxf(tmax, s[tb][i]);
-        tmax = half_max(tmax) * c;
+        return half_max(tmax) * c;
+    };
+    // Move the running max when some row's tile max exceeds it by more than
+    // the slack (rare after the first tiles): rescale O and the row sum.
+    auto update_max = [&](float tmax) {
         if (__builtin_amdgcn_ballot_w64(tmax > m_run + kPfRescaleSlack) != 0) {
             const float m_new = fmaxf(m_run, tmax);
             const float m_new_use = (m_new == -INFINITY) ? 0.f : m_new;
@@ -187,15 +220,11 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
             m_run = m_new;
             m_use = m_new_use;
         }
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) s[tb][i] = __builtin_fmaf(s[tb][i], c, -m_use);
     };
 
-    // exp2, row sums and the bf16 P^T operands of S(j).
+    // exp2(S*scale - max), row sums and the bf16 P^T operands of S(j).
     bf16x8_t pop[4];
-    auto alu1 = [&](f32x16_t (&s)[2]) {
+    auto softmax_p = [&](f32x16_t (&s)[2]) {
         float psum = 0.f;
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
@@ -203,7 +232,7 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
             for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float pv = fast_exp2(s[tb][kh * 8 + e]);
+                    const float pv = fast_exp2(__builtin_fmaf(s[tb][kh * 8 + e], c, -m_use));
                     psum += pv;
                     pop[tb * 2 + kh][e] = (__bf16)pv;
                 }
@@ -241,57 +270,94 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     // this wave's direct LDS loads have landed (then a barrier publishes them)
     auto wait_vmem = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
 
+    // K runs one tile ahead of V: iteration j reads K(j+1) and V(j) while
+    // K(j+2) and V(j+1) land in the buffers freed by iteration j-1.  No
+    // branch touches the accumulators (a branch costs register copies), and
+    // S(j+1) is computed even on the last step (its tile is fully masked).
     __syncthreads();  // the previous unit may still read the buffers
-    if constexpr (kPipe) {
-        // K runs one tile ahead of V: iteration j reads K(j+1) and V(j) while
-        // K(j+2) and V(j+1) land in the buffers freed by iteration j-1.
-        if (n_tiles > 0) issue_tile(0, 0, 0);
-        if (n_tiles > 1) issue_tile(1, 1, -1);
-        wait_vmem();
-        __syncthreads();
+    if (n_tiles > 0) issue_tile(0, 0, 0);
+    if (n_tiles > 1) issue_tile(1, 1, -1);
+    wait_vmem();
+    __syncthreads();
 
-        // One pipelined step: S(j+1) into sn while S(j) (in sc) finishes.
-        auto step = [&](f32x16_t (&sc)[2], f32x16_t (&sn)[2], int j) {
-            const bool more = j + 1 < n_tiles;   // block-uniform
-            if (j + 2 < n_tiles) issue_tile(j + 2, j & 1, -1);
-            if (more) issue_tile(j + 1, -1, (j + 1) & 1);
-            // phase A: S(j+1) on the MFMA pipe, exp2 of S(j) on the VALU
-            if (more) qk(sn, (j + 1) & 1);
-            alu1(sc);
-            // phase B: P(j).V(j) on the MFMA pipe, max/scale of S(j+1) on the VALU
-            pv(j & 1);
-            if (more) alu0(sn, j + 1);
-            wait_vmem();
-            __syncthreads();
-        };
-        f32x16_t sa[2], sb[2];
-        if (n_tiles > 0) {
-            qk(sa, 0);
-            alu0(sa, 0);
+    // One pipelined step.  On entry sc holds the masked S(j) and the running
+    // max covers it; on exit sn holds the masked S(j+1), likewise.
+    auto step = [&](f32x16_t (&sc)[2], f32x16_t (&sn)[2], int j) {
+        if (j + 2 < n_tiles) issue_tile(j + 2, j & 1, -1);
+        if (j + 1 < n_tiles) issue_tile(j + 1, -1, (j + 1) & 1);
+        // phase A: S(j+1) on the MFMA pipe while exp2 / sums / bf16 P of S(j)
+        // run on the VALU: each MFMA is followed by its K read for a later
+        // MFMA and a slice of the softmax.
+        qk(sn, (j + 1) & 1);
+        softmax_p(sc);
+        // keep P here: otherwise the compiler sinks the softmax to its use in phase B
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) asm volatile("" : "+v"(pop[kb]));
+        asm volatile("" : "+v"(l_run));
+        // K reads run 4 MFMAs ahead of their use
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);       // DS read
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // VALU
+            if (i < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
         }
-        for (int j = 0; j < n_tiles; j += 2) {
-            step(sa, sb, j);
-            if (j + 1 < n_tiles) step(sb, sa, j + 1);
+        mask(sn, j + 1);
+        // phase B: P(j).V(j) on the MFMA pipe while the row max of S(j+1)
+        // runs on the VALU.
+        pv(j & 1);
+        const float tmax = rowmax(sn);
+        // V reads run 3 MFMAs ahead of their use
+        __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);       // DS reads
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);   // VALU
+            if (i < 13) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // DS reads
         }
-    } else {
-        // Tile j+1 lands in the other buffer while tile j is computed.
-        // Overlap of MFMA and VALU work comes from the other wave on the SIMD.
-        if (n_tiles > 0) issue_tile(0, 0, 0);
+        update_max(tmax);
         wait_vmem();
         __syncthreads();
-        f32x16_t s[2];
-        for (int j = 0; j < n_tiles; ++j) {
-            if (j + 1 < n_tiles) issue_tile(j + 1, (j + 1) & 1, (j + 1) & 1);
-            // Tiles past this wave's causal limit are fully masked and add
-            // nothing; they are computed anyway so that the accumulators never
-            // pass through a branch (which costs register copies).
-            qk(s, j & 1);
-            alu0(s, j);
-            alu1(s);
-            pv(j & 1);
-            wait_vmem();
-            __syncthreads();
+    };
+    f32x16_t sa[2], sb[2];
+    if (n_tiles > 0) {
+        qk(sa, 0);
+        mask(sa, 0);
+        update_max(rowmax(sa));
+    }
+    __syncthreads();   // every wave has read K(0) before step 0 refills its buffer
+    for (int j = 0; j < n_tiles; j += 2) {
+        step(sa, sb, j);
+        if (j + 1 < n_tiles) step(sb, sa, j + 1);
+    }
+
+    if constexpr (kGroups == 2) {
+        // Group 1 hands its partial state to group 0 (same wave slot, same lane)
+        // through the tile buffers, idle since the loop's last barrier:
+        // [wave][value][lane] floats.
+        float* mg = reinterpret_cast<float*>(smem_all) + wave * kPfMergeFloats * kWave + lane;
+        if (grp == 1) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) mg[(db * 16 + i) * kWave] = oacc[db][i];
+            mg[64 * kWave] = m_run;
+            mg[65 * kWave] = l_run;
         }
+        __syncthreads();
+        if (grp == 1) return;
+        const float m1 = mg[64 * kWave];
+        const float l1 = mg[65 * kWave];
+        const float m = fmaxf(m_run, m1);
+        const float mu = (m == -INFINITY) ? 0.f : m;
+        const float a0 = fast_exp2(m_run - mu);   // 0 when a group saw no key
+        const float a1 = fast_exp2(m1 - mu);
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) oacc[db][i] = oacc[db][i] * a0 + mg[(db * 16 + i) * kWave] * a1;
+        l_run = l_run * a0 + l1 * a1;
+        m_run = m;
     }
 
     l_run = half_sum(l_run);
@@ -312,48 +378,33 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     }
 }
 
-// Block -> work unit(s).  grid_mode 0: each block runs the pair of query
-// blocks (n-1-slot, slot) of one stream (causal), or one block (non-causal).
-// grid_mode 1: one unit per block, heaviest first, blocks k and k + N/2 taking
-// complementary units.  grid_mode 2: one unit per block, heaviest first.
-// Streams (head group, kv head, batch) are the fastest index, so with a
-// multiple of 8 streams each stream's blocks share one XCD.
-template <bool kPipe>
-__device__ __forceinline__ void pf_blocks(const PrefillParams& p, unsigned char* smem) {
-    const int k = blockIdx.x;
-    int stream, qa, qb2 = -1;
-    if (p.grid_mode == 0) {
-        stream = k % p.n_streams;
-        const int slot = k / p.n_streams;
-        qa = p.causal ? p.n_qblocks - 1 - slot : slot;
-        if (p.causal && slot < qa) qb2 = slot;
-    } else {
-        const int total = p.n_qblocks * p.n_streams;
-        int r = k;
-        if (p.grid_mode == 1) {
-            const int half = (total + 1) / 2;
-            r = (k < half) ? k : total - 1 - (k - half);
-        }
-        stream = r % p.n_streams;
-        const int rank_q = r / p.n_streams;
-        qa = p.causal ? p.n_qblocks - 1 - rank_q : rank_q;
-    }
-    const int hg = stream % p.n_hgroups;
-    const int kvh = (stream / p.n_hgroups) % p.hkv;
-    const int b = stream / (p.n_hgroups * p.hkv);
-    const int nunits = qb2 >= 0 ? 2 : 1;
-    for (int u = 0; u < nunits; ++u) pf_unit<kPipe>(p, smem, u == 0 ? qa : qb2, hg, kvh, b);
+// Block -> unit.  Units are ranked heaviest first (the causal KV range grows
+// with the query block), so the dispatcher hands long units out before short
+// ones.  The stream (head group, kv head, batch) is the fastest index: with a
+// multiple of 8 streams each stream's blocks share one XCD and its L2 (blocks
+// go round-robin over the 8 XCDs).
+__device__ __forceinline__ void pf_block_unit(const PrefillParams& p, int* qb, int* hg, int* kvh, int* b) {
+    const int r = blockIdx.x;
+    const int stream = r % p.n_streams;
+    const int rank_q = r / p.n_streams;
+    *qb = p.causal ? p.n_qblocks - 1 - rank_q : rank_q;
+    *hg = stream % p.n_hgroups;
+    *kvh = (stream / p.n_hgroups) % p.hkv;
+    *b = stream / (p.n_hgroups * p.hkv);
 }
 
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    pf_blocks<true>(p, smem);
+    int qb, hg, kvh, b;
+    pf_block_unit(p, &qb, &hg, &kvh, &b);
+    pf_unit<1>(p, smem, qb, hg, kvh, b);
 }
 
-// Two waves per SIMD: 256 registers per wave at most.
-__global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel_2w(PrefillParams p) {
+__global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_split_kernel(PrefillParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    pf_blocks<false>(p, smem);
+    int qb, hg, kvh, b;
+    pf_block_unit(p, &qb, &hg, &kvh, &b);
+    pf_unit<2>(p, smem, qb, hg, kvh, b);
 }
 
 namespace {
@@ -428,34 +479,30 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
     p.q_sign = (a->scale < 0.f) ? 0x80008000u : 0u;
 
     const int64_t units = (int64_t)p.n_qblocks * p.n_streams;
-    // Causal work per unit grows with its query block.  When every unit gets
-    // a slot at once (two workgroups per CU), blocks k and k + units/2 take
-    // complementary units; otherwise blocks go heaviest first.
+    if (units >= ((int64_t)1 << 31)) return FGQA_ERR_UNSUPPORTED;
     const int cus = device_cu_count();
-    p.grid_mode = (p.causal && cus > 0 && units <= 2 * (int64_t)cus) ? 1 : 2;
-    bool two_waves = false;
-    if (const char* e = getenv("FGQA_PF_VARIANT")) {   // tuning override: kernel*10 + grid_mode
-        const int variant = atoi(e);
-        two_waves = variant / 10 == 1;
-        p.grid_mode = variant % 10;
-    }
-    if (!p.causal && p.grid_mode == 1) p.grid_mode = 2;
-    const int64_t nblocks = (p.grid_mode == 0 && p.causal) ? ceil_div(p.n_qblocks, 2) * p.n_streams : units;
-    if (nblocks >= ((int64_t)1 << 31)) return FGQA_ERR_UNSUPPORTED;
+    if (cus <= 0) return FGQA_ERR_HIP;
+    // Few units (fewer than 4 per CU): split each unit's KV range over two
+    // wave groups so a CU never runs a long unit with one wave per SIMD, and
+    // let the dispatcher hand heaviest-first units to free CUs.
+    bool split = units < 4 * (int64_t)cus;
+    // FGQA_PREFILL_SPLIT=0/1 forces the choice (tuning and tests).
+    if (const char* e = getenv("FGQA_PREFILL_SPLIT")) split = e[0] == '1';
 
-    const void* fn = two_waves ? reinterpret_cast<const void*>(prefill_kernel_2w)
-                               : reinterpret_cast<const void*>(prefill_kernel);
+    const int smem_bytes = (split ? 2 : 1) * kPfGroupBytes;
+    const void* fn = split ? reinterpret_cast<const void*>(prefill_split_kernel)
+                           : reinterpret_cast<const void*>(prefill_kernel);
     static bool smem_set[2] = {false, false};
-    if (!smem_set[two_waves]) {
-        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kPfSmemBytes) != hipSuccess)
+    if (!smem_set[split]) {
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, smem_bytes) != hipSuccess)
             return FGQA_ERR_HIP;
-        smem_set[two_waves] = true;
+        smem_set[split] = true;
     }
-    if (two_waves)
-        hipLaunchKernelGGL(prefill_kernel_2w, dim3((unsigned)nblocks), dim3(kPfThreads), kPfSmemBytes,
+    if (split)
+        hipLaunchKernelGGL(prefill_split_kernel, dim3((unsigned)units), dim3(2 * kPfThreads), smem_bytes,
                            static_cast<hipStream_t>(stream), p);
     else
-        hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)nblocks), dim3(kPfThreads), kPfSmemBytes,
+        hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)units), dim3(kPfThreads), smem_bytes,
                            static_cast<hipStream_t>(stream), p);
     if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
     return FGQA_OK;

@@ -233,6 +233,26 @@ def test_prefill_shapes(cuda, B, Sq, Skv, Hq, Hkv, causal):
     _check_prefill(o, lse, o_ref, lse_ref, f"prefill B{B} Sq{Sq} Skv{Skv} Hq{Hq} Hkv{Hkv} causal{causal}")
 
 
+@pytest.mark.parametrize("split", ["0", "1"])
+@pytest.mark.parametrize("B,Sq,Skv,Hq,Hkv,causal", [
+    (1, 256, 256, 16, 1, True),
+    (2, 300, 300, 8, 2, True),      # odd tile counts per unit
+    (1, 130, 130, 3, 3, True),
+    (1, 97, 161, 4, 2, False),
+    (1, 161, 97, 4, 1, True),
+    (2, 64, 640, 16, 4, True),
+    (1, 1111, 1111, 16, 2, True),   # up to 18 tiles per unit
+    (1, 700, 900, 4, 4, False),
+])
+def test_prefill_whole_and_split_kernels(cuda, monkeypatch, split, B, Sq, Skv, Hq, Hkv, causal):
+    """Both prefill kernels: one workgroup per unit over its whole KV range,
+    and the split kernel (two wave groups on the halves of the range, merged)."""
+    monkeypatch.setenv("FGQA_PREFILL_SPLIT", split)
+    o, lse, o_ref, lse_ref = _prefill_case(cuda, 650 + Sq, B, Sq, Skv, Hq, Hkv, causal)
+    _check_prefill(o, lse, o_ref, lse_ref,
+                   f"split={split} B{B} Sq{Sq} Skv{Skv} Hq{Hq} Hkv{Hkv} causal{causal}")
+
+
 def test_prefill_row0_and_triton_layout(cuda):
     import torch
     fg = _fg()
