@@ -37,6 +37,7 @@ SCALE = 1.0 / math.sqrt(128)
 # changes.
 TRAFFIC_BYTES = {
     "decode_cfg2": 1010662256,   # = Q+K+V+O (1,010,565,120 B) + 0.01 %
+    "prefill_cfg4": 51649536,    # Q+O+LSE 32.25 MiB + K/V 2 MiB fetched once per XCD
 }
 
 DECODE_CONFIGS = {
@@ -144,7 +145,8 @@ def bench_prefill(cfg_id, steps, warmup, dev):
                 us_min=round(per[0] * 1e3, 2),
                 roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
                           "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-                          "traffic": TRAFFIC_BYTES.get(f"prefill_cfg{cfg_id}"), "kernel": "prefill_kernel",
+                          "traffic": TRAFFIC_BYTES.get(f"prefill_cfg{cfg_id}"),
+                          "kernel": "prefill_split_kernel" if cfg_id == 4 else "prefill_kernel",
                           "algorithmic_flops": flops})
 
 
