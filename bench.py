@@ -107,7 +107,8 @@ def bench_decode(cfg_id, steps, warmup, split_tokens, dev):
     cfg = DECODE_CONFIGS[cfg_id]
     q, k, v, sl, lens, kv_bytes = _decode_setup(cfg, dev)
     out = torch.empty_like(q)
-    n_ws = fg.decode_workspace_bytes(cfg["B"], cfg["S"], cfg["Hq"], cfg["Hkv"], split_tokens=split_tokens)
+    n_ws = fg.decode_workspace_bytes(cfg["B"], cfg["S"], cfg["Hq"], cfg["Hkv"], split_tokens=split_tokens,
+                                     ragged=cfg["ragged"])
     ws = torch.empty(max(n_ws, 256), dtype=torch.uint8, device=dev)
 
     # validated once; each step is one call of the C ABI on torch's current stream

@@ -38,6 +38,7 @@ struct DecodeParams {
     int64_t k_sb, k_ss, k_sh;
     int64_t v_sb, v_ss, v_sh;
     int64_t o_sb, o_sh;
+    const int32_t* work;   // ragged work list: [0] = entries, then (b << 16 | split) per entry
     int batch, max_seqlen, hq, hkv, group;
     int nsplit, chunk;
     float scale_log2;
@@ -58,10 +59,8 @@ __device__ __forceinline__ int clamp_len(const DecodeParams& p, int b) {
     return min(max(len, 0), p.max_seqlen);
 }
 
-__global__ __launch_bounds__(kDecThreads) void decode_split_kernel(DecodeParams p) {
-    const int split = blockIdx.x;
-    const int kvh = blockIdx.y;
-    const int b = blockIdx.z;
+// One (split, kv head, batch) item of pass 1.
+__device__ __forceinline__ void dec_item(const DecodeParams& p, unsigned char* smem, int split, int kvh, int b) {
     const int len = clamp_len(p, b);
     const int t_begin = split * p.chunk;
     const int tid = threadIdx.x;
@@ -85,7 +84,6 @@ __global__ __launch_bounds__(kDecThreads) void decode_split_kernel(DecodeParams 
     const int l16 = lane & 15;
     const int g4 = lane >> 4;
 
-    __shared__ __attribute__((aligned(16))) unsigned char smem[kDecSmemBytes];
     __bf16* kl = reinterpret_cast<__bf16*>(smem) + wave * 2 * kDecTileElems;
     __bf16* vl = kl + kDecTileElems;
 
@@ -261,6 +259,107 @@ __global__ __launch_bounds__(kDecThreads) void decode_split_kernel(DecodeParams 
     }
 }
 
+// Pass 1 over the full (split, kv head, batch) grid.
+__global__ __launch_bounds__(kDecThreads) void decode_split_kernel(DecodeParams p) {
+    __shared__ __attribute__((aligned(16))) unsigned char smem[kDecSmemBytes];
+    dec_item(p, smem, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+// Ragged batches: build the work list of non-empty splits, full-length splits
+// first and the partial last split of each sequence after them, longest first
+// (batch order beyond kPlanSortMax sequences), so that equal work fills the
+// GPU and the short items form the tail.  One workgroup; entry =
+// (b << 16) | split, so batch < 2^15 and splits < 2^16 (checked on the host).
+constexpr int kPlanThreads = 256;
+constexpr int kPlanSortMax = 1024;   // remainders kept in LDS and length-sorted up to this batch size
+
+// Exclusive prefix sum of one int per thread over the workgroup (256 threads).
+__device__ __forceinline__ int block_exclusive_scan(int v, int* s_wave, int* total) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    int incl = v;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int t = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += t;
+    }
+    if (lane == kWave - 1) s_wave[wave] = incl;
+    __syncthreads();
+    int base = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kPlanThreads / kWave; ++w) {
+        base += (w < wave) ? s_wave[w] : 0;
+        all += s_wave[w];
+    }
+    __syncthreads();   // s_wave is reused by the next scan
+    *total = all;
+    return base + incl - v;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(DecodeParams p, int32_t* work) {
+    __shared__ int s_wave[kPlanThreads / kWave];
+    __shared__ int s_rem[kPlanSortMax];   // len % chunk per sequence (batch <= kPlanSortMax)
+    const int tid = threadIdx.x;
+    const bool sort = p.batch <= kPlanSortMax;
+    // sequences b = tid, tid + 256, ... belong to this thread
+    int nf = 0, np = 0;
+    for (int b = tid; b < p.batch; b += kPlanThreads) {
+        const int len = clamp_len(p, b);
+        nf += len / p.chunk;
+        np += (len % p.chunk) != 0;
+        if (sort) s_rem[b] = len % p.chunk;
+    }
+    int n_full, n_part;
+    int pos_f = block_exclusive_scan(nf, s_wave, &n_full);
+    int pos_p = block_exclusive_scan(np, s_wave, &n_part);   // also publishes s_rem (barriers inside)
+    if (tid == 0) work[0] = n_full + n_part;
+    for (int b = tid; b < p.batch; b += kPlanThreads) {
+        const int len = clamp_len(p, b);
+        const int full = len / p.chunk;
+        for (int sp = 0; sp < full; ++sp) work[1 + pos_f + sp] = (b << 16) | sp;
+        pos_f += full;
+        const int rem = len % p.chunk;
+        if (rem == 0) continue;
+        int rank = pos_p;   // batch order
+        if (sort) {
+            rank = 0;       // longest remainder first, ties by batch
+            for (int o = 0; o < p.batch; ++o) {
+                const int ro = s_rem[o];
+                rank += (ro > rem) || (ro == rem && o < b);
+            }
+        }
+        work[1 + n_full + rank] = (b << 16) | full;
+        ++pos_p;
+    }
+    // Without a combine pass, empty sequences (no list entry) still need
+    // O = 0 and lse = -inf.
+    if (p.nsplit == 1) {
+        for (int b = 0; b < p.batch; ++b) {
+            if (clamp_len(p, b) != 0) continue;
+            for (int i = tid; i < p.hq * 16; i += kPlanThreads) {
+                const int qh = i >> 4;
+                bf16x8_t z;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) z[j] = (__bf16)0.f;
+                *reinterpret_cast<bf16x8_t*>(p.o + b * p.o_sb + qh * p.o_sh + (i & 15) * 8) = z;
+                if (p.lse != nullptr && (i & 15) == 0) p.lse[(int64_t)b * p.hq + qh] = -INFINITY;
+            }
+        }
+    }
+}
+
+// Pass 1 over the ragged work list: a fixed grid walks the entries, each
+// entry once per kv head (kv head fastest, so heads of one split run together).
+__global__ __launch_bounds__(kDecThreads) void decode_list_kernel(DecodeParams p) {
+    __shared__ __attribute__((aligned(16))) unsigned char smem[kDecSmemBytes];
+    const int total = p.work[0] * p.hkv;
+    for (int item = blockIdx.x; item < total; item += gridDim.x) {
+        const int e = p.work[1 + item / p.hkv];
+        __syncthreads();   // the previous item's merge buffers alias the staging area
+        dec_item(p, smem, e & 0xffff, item % p.hkv, e >> 16);
+    }
+}
+
 // Log-sum-exp merge of the per-split partials of one (kv head, batch).
 __global__ __launch_bounds__(kDecThreads) void decode_combine_kernel(DecodeParams p) {
     const int kvh = blockIdx.x;
@@ -315,9 +414,13 @@ constexpr int kMaxAutoChunk = 4096;               // longest split the planner p
 struct DecodePlan {
     int chunk;
     int nsplit;
+    bool list;            // ragged batch: work list of non-empty splits
     size_t part_o_bytes;
+    size_t part_ml_bytes;
     size_t ws_bytes;
 };
+
+constexpr int kRaggedChunk = 4096;   // split length for ragged batches (work-list mode)
 
 int validate_decode(const fgqa_decode_args* a) {
     if (a == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
@@ -356,9 +459,14 @@ int validate_decode_pointers(const fgqa_decode_args* a) {
 
 int plan_decode(const fgqa_decode_args* a, DecodePlan* plan) {
     const int64_t S = a->max_seqlen > 0 ? a->max_seqlen : 1;
+    // Ragged batches get a work list of their non-empty splits (built on the
+    // device from the lengths), so no workgroup is spent on padding.
+    plan->list = a->seqlens != nullptr && a->batch < (1 << 15);
     int64_t chunk;
     if (a->split_tokens > 0) {
         chunk = ceil_div(a->split_tokens, kStepRound) * kStepRound;
+    } else if (plan->list) {
+        chunk = kRaggedChunk;
     } else {
         // The KV stream is HBM-bound: a split only pays when there are too
         // few (batch, kv head) streams to occupy every CU, or when sequences
@@ -378,14 +486,16 @@ int plan_decode(const fgqa_decode_args* a, DecodePlan* plan) {
     if (chunk > S) chunk = ceil_div(S, kStepRound) * kStepRound;
     plan->chunk = (int)chunk;
     plan->nsplit = (int)ceil_div(S, chunk);
+    if (plan->nsplit >= (1 << 16)) plan->list = false;
     const int64_t slots = (int64_t)a->batch * a->num_q_heads * plan->nsplit;
+    plan->part_o_bytes = 0;
+    plan->part_ml_bytes = 0;
     if (plan->nsplit > 1) {
         plan->part_o_bytes = (size_t)(ceil_div(slots * kHeadDim * 4, 256) * 256);
-        plan->ws_bytes = plan->part_o_bytes + (size_t)(slots * 2 * 4);
-    } else {
-        plan->part_o_bytes = 0;
-        plan->ws_bytes = 0;
+        plan->part_ml_bytes = (size_t)(ceil_div(slots * 2 * 4, 256) * 256);
     }
+    plan->ws_bytes = plan->part_o_bytes + plan->part_ml_bytes;
+    if (plan->list) plan->ws_bytes += (size_t)(1 + (int64_t)a->batch * plan->nsplit) * 4;
     return FGQA_OK;
 }
 
@@ -443,7 +553,8 @@ extern "C" int fgqa_decode_bf16(const fgqa_decode_args* a, void* stream) {
     p.chunk = plan.chunk;
     p.scale_log2 = a->scale * kLog2e;
 
-    if (plan.nsplit > 1) {
+    int32_t* work = nullptr;
+    if (plan.ws_bytes > 0) {
         void* ws = a->workspace;
         if (ws == nullptr && a->workspace_bytes == 0) {
             ws = internal_workspace(plan.ws_bytes, &st);
@@ -453,15 +564,29 @@ extern "C" int fgqa_decode_bf16(const fgqa_decode_args* a, void* stream) {
         } else if (!aligned16(ws)) {
             return FGQA_ERR_UNSUPPORTED;
         }
-        p.part_o = static_cast<float*>(ws);
-        p.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + plan.part_o_bytes);
+        char* w = static_cast<char*>(ws);
+        if (plan.nsplit > 1) {
+            p.part_o = reinterpret_cast<float*>(w);
+            p.part_ml = reinterpret_cast<float*>(w + plan.part_o_bytes);
+        }
+        if (plan.list) work = reinterpret_cast<int32_t*>(w + plan.part_o_bytes + plan.part_ml_bytes);
     }
+    p.work = work;
 
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (a->max_seqlen == 0) {
         // Every sequence is empty: the combine writes O = 0, lse = -inf.
         p.nsplit = 1;
         hipLaunchKernelGGL(decode_combine_kernel, dim3(p.hkv, p.batch), dim3(kDecThreads), 0, s, p);
+    } else if (plan.list) {
+        const int cus = device_cu_count();
+        if (cus <= 0) return FGQA_ERR_HIP;
+        const int64_t max_items = (int64_t)p.batch * plan.nsplit * p.hkv;
+        const int grid = (int)(max_items < 2LL * cus ? max_items : 2LL * cus);   // two per CU, persistent
+        hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p, work);
+        hipLaunchKernelGGL(decode_list_kernel, dim3(grid), dim3(kDecThreads), 0, s, p);
+        if (plan.nsplit > 1)
+            hipLaunchKernelGGL(decode_combine_kernel, dim3(p.hkv, p.batch), dim3(kDecThreads), 0, s, p);
     } else {
         hipLaunchKernelGGL(decode_split_kernel, dim3(p.nsplit, p.hkv, p.batch), dim3(kDecThreads), 0, s, p);
         if (plan.nsplit > 1)

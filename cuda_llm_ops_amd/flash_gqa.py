@@ -82,9 +82,13 @@ def _decode_args(q, k, v, o, scale, seqlens, lse, split_tokens, workspace) -> _l
     return a
 
 
-def decode_workspace_bytes(batch, max_seqlen, num_q_heads, num_kv_heads, head_dim=128, split_tokens=0) -> int:
-    """Bytes of scratch ``decode_flash_gqa_bshd`` needs for a caller workspace."""
+def decode_workspace_bytes(batch, max_seqlen, num_q_heads, num_kv_heads, head_dim=128, split_tokens=0,
+                           ragged=False) -> int:
+    """Bytes of scratch ``decode_flash_gqa_bshd`` needs for a caller workspace.
+    ``ragged``: the call will pass per-sequence lengths (``seqlens``)."""
     a = _lib.DecodeArgs()
+    if ragged:
+        a.seqlens = 16   # only tested for NULL by the size query, never read
     a.batch, a.max_seqlen, a.num_q_heads, a.num_kv_heads, a.head_dim = (
         batch, max_seqlen, num_q_heads, num_kv_heads, head_dim)
     a.scale = 1.0

@@ -77,12 +77,21 @@ def _ws(a):
 
 
 def test_decode_workspace_formula():
-    # B*Hq*nsplit partials of (128 fp32 O, rounded to 256 bytes) + (max, sum)
+    # B*Hq*nsplit partials of 128 fp32 O and of (max, sum), each array rounded to 256 bytes
     for S, split in ((512, 256), (4096, 1024), (1000, 128), (100, 128)):
         st, n = _ws(_decode_args(S=S, split_tokens=split))
         nsplit = -(-S // split)
         slots = 2 * 16 * nsplit
-        expect = 0 if nsplit == 1 else -(-slots * 512 // 256) * 256 + slots * 8
+        expect = 0 if nsplit == 1 else -(-slots * 512 // 256) * 256 + -(-slots * 8 // 256) * 256
+        assert st == 0 and n == expect, (S, split, n, expect)
+    # ragged batches (seqlens given) add the work list: 1 + B*nsplit int32
+    for S, split in ((2048, 256), (4096, 1024), (1000, 128)):
+        a = _decode_args(S=S, split_tokens=split)
+        a.seqlens = 64
+        st, n = _ws(a)
+        nsplit = -(-S // split)
+        slots = 2 * 16 * nsplit
+        expect = -(-slots * 512 // 256) * 256 + -(-slots * 8 // 256) * 256 + (1 + 2 * nsplit) * 4
         assert st == 0 and n == expect, (S, split, n, expect)
     # split_tokens rounds up to the 128-token step of a workgroup
     assert _ws(_decode_args(S=4096, split_tokens=1000)) == _ws(_decode_args(S=4096, split_tokens=1024))

@@ -46,7 +46,7 @@ def _decode_case(cuda, seed, B, Hq, Hkv, S, seqlens=None, split_tokens=0, nan_pa
     lse = torch.empty((B, Hq), dtype=torch.float32, device=cuda)
     ws = None
     if workspace:
-        n = _fg().decode_workspace_bytes(B, S, Hq, Hkv, split_tokens=split_tokens)
+        n = _fg().decode_workspace_bytes(B, S, Hq, Hkv, split_tokens=split_tokens, ragged=seqlens is not None)
         ws = torch.empty(max(n, 16), dtype=torch.uint8, device=cuda)
     out = _fg().decode_flash_gqa_bshd(qd, kd, vd, SCALE, seqlens=sl, lse=lse, split_tokens=split_tokens,
                                       workspace=ws)
@@ -94,6 +94,12 @@ def test_decode_ragged_nan_padding(cuda):
     o, lse, o_ref, lse_ref = _decode_case(cuda, 401, len(sl), 16, 2, 2048, seqlens=sl, nan_pad=True,
                                           split_tokens=4096)
     _check_decode(o, lse, o_ref, lse_ref, "ragged, one split")
+    # caller workspace, several split lengths of the ragged work list
+    for split in (128, 384, 1024):
+        o, lse, o_ref, lse_ref = _decode_case(cuda, 402 + split, len(sl), 16, 2, 2048, seqlens=sl, nan_pad=True,
+                                              split_tokens=split, workspace=True)
+        _check_decode(o, lse, o_ref, lse_ref, f"ragged, split {split}, caller workspace")
+        assert np.all(oracle.bf16_to_f32(o[0]) == 0) and np.all(np.isneginf(lse[0]))
 
 
 def test_decode_known_answers(cuda):
