@@ -62,7 +62,9 @@ static void set_threads(int nthreads) {
  *   :193-201  qk = sum_d q[d]*k[t][d]            (fp32, d ascending)
  *   :202-208  m_new = max(m, qk*scale)
  *   :209-215  l_tile = sum_t expf(qk*scale - m_new)
- *   :216-223  P = bf16(expf(qk*scale - m_new))
+ *   :216-223  P = bf16(expf(qk*scale - m_new))   (p_bf16 = 1; with p_bf16 = 0
+ *             P stays fp32, which is the torch tiled decode reference
+ *             examples/python/Triton/test_decode_flash_gqa_kernel.py:56-73)
  *   :225-233  o_tile[d] = sum_t P*V[t][d]         (fp32, t ascending)
  *   :234-241  O = (first tile) ? o_tile : O*expf(m - m_new) + o_tile
  *   :243-244  l = l*expf(m - m_new) + l_tile; m = m_new
@@ -73,7 +75,7 @@ static void set_threads(int nthreads) {
 int fgqa_oracle_decode_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                             float scale, uint16_t* o, float* lse,
                             int batch, int s_max, int hq, int hkv, int d,
-                            const int32_t* seqlens, int tile, int nthreads) {
+                            const int32_t* seqlens, int tile, int p_bf16, int nthreads) {
     if (!q || !k || !v || !o) return -1;
     if (batch < 0 || s_max < 0 || hq <= 0 || hkv <= 0 || d <= 0 || d > ORACLE_MAX_D) return -1;
     if (hq % hkv != 0 || tile <= 0) return -1;
@@ -87,7 +89,7 @@ int fgqa_oracle_decode_bf16(const uint16_t* q, const uint16_t* k, const uint16_t
 #pragma omp parallel
     {
         float* s = (float*)malloc(sizeof(float) * (size_t)tile);
-        uint16_t* p = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)tile);
+        float* p = (float*)malloc(sizeof(float) * (size_t)tile);
         float acc[ORACLE_MAX_D];
         float otile[ORACLE_MAX_D];
 #pragma omp for collapse(2) schedule(dynamic)
@@ -111,13 +113,16 @@ int fgqa_oracle_decode_bf16(const uint16_t* q, const uint16_t* k, const uint16_t
                     for (int j = 0; j < n; ++j) m_new = fmaxf(m_new, s[j] * scale);
                     float l_tile = 0.f;
                     for (int j = 0; j < n; ++j) l_tile += expf(s[j] * scale - m_new);
-                    for (int j = 0; j < n; ++j) p[j] = fgqa_oracle_f32_to_bf16(expf(s[j] * scale - m_new));
+                    for (int j = 0; j < n; ++j) {
+                        const float e = expf(s[j] * scale - m_new);
+                        p[j] = p_bf16 ? bf(fgqa_oracle_f32_to_bf16(e)) : e;
+                    }
                     /* o_tile[x] accumulates over t ascending for each x (same order as
                      * the reference's inner token loop). */
                     for (int x = 0; x < d; ++x) otile[x] = 0.f;
                     for (int j = 0; j < n; ++j) {
                         const uint16_t* vrow = v + (((size_t)b * s_max + (t0 + j)) * hkv + kvh) * d;
-                        const float pj = bf(p[j]);
+                        const float pj = p[j];
                         for (int x = 0; x < d; ++x) otile[x] += pj * bf(vrow[x]);
                     }
                     const float corr = expf(m - m_new);

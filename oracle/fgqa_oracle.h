@@ -15,7 +15,9 @@
  *                                            RNE tie cases + numpy restatement
  *   fgqa_oracle_decode_bf16                 fp64 brute force (fgqa_oracle_attention_f64)
  *                                            at the stated tolerance, closed forms
- *                                            (len=1, constant V, equal K), invariants
+ *                                            (len=1, constant V, equal K), invariants;
+ *                                            the fp32-P variant (p_bf16 = 0) sits closer
+ *                                            to the fp64 answer than the bf16-P one
  *   fgqa_oracle_prefill_bf16                fp64 brute force, closed forms (row 0 = V[0],
  *                                            LSE of equal logits = log n), invariants
  *   fgqa_oracle_attention_f64               textbook softmax attention in double;
@@ -50,13 +52,17 @@ void fgqa_oracle_bf16_to_f32_array(const uint16_t* src, float* dst, size_t n);
  *   q, o : [B, Hq, D]         k, v : [B, S_max, Hkv, D]
  * seqlens: host array of B lengths (each 0..S_max) or NULL (= S_max for all).
  * lse (nullable): fp32 [B, Hq], natural log; a length-0 row gives O = 0, lse = -inf.
- * tile: flash tile length (the reference uses 128).  nthreads <= 0: OpenMP default.
+ * tile: flash tile length (the reference uses 128).
+ * p_bf16: 1 rounds P to bf16 before P.V, as the C++ reference does; 0 keeps P
+ * in fp32, which restates the torch tiled decode reference
+ * examples/python/Triton/test_decode_flash_gqa_kernel.py:26-79 (tile 128,
+ * online softmax, fp32 throughout).  nthreads <= 0: OpenMP default.
  * Returns 0, or -1 on invalid arguments.
  */
 int fgqa_oracle_decode_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                             float scale, uint16_t* o, float* lse,
                             int batch, int s_max, int hq, int hkv, int d,
-                            const int32_t* seqlens, int tile, int nthreads);
+                            const int32_t* seqlens, int tile, int p_bf16, int nthreads);
 
 /*
  * Prefill forward, restating the reference's torch reference

@@ -46,7 +46,7 @@ def lib() -> ctypes.CDLL:
         L.fgqa_oracle_decode_bf16.argtypes = [
             _u16p, _u16p, _u16p, ctypes.c_float, _u16p, _f32p,
             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-            _i32p, ctypes.c_int, ctypes.c_int]
+            _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         L.fgqa_oracle_prefill_bf16.restype = ctypes.c_int
         L.fgqa_oracle_prefill_bf16.argtypes = [
             _u16p, _u16p, _u16p, ctypes.c_float, _u16p, _f32p,
@@ -92,8 +92,10 @@ def normal_bf16(seed: int, shape, sigma: float = 1.0, stream: int = 0) -> np.nda
 
 
 # ---------------------------------------------------------------- oracles
-def decode(q, k, v, scale, seqlens=None, tile=128, nthreads=0, with_lse=True):
+def decode(q, k, v, scale, seqlens=None, tile=128, nthreads=0, with_lse=True, p_bf16=True):
     """Decode oracle. q [B,Hq,D], k/v [B,S,Hkv,D] (uint16 bf16 bits).
+    p_bf16=True rounds P to bf16 before P.V (the C++ reference); False keeps
+    fp32 P (the torch tiled reference).
     Returns (o uint16 [B,Hq,D], lse float32 [B,Hq] or None)."""
     q = np.ascontiguousarray(q, dtype=np.uint16)
     k = np.ascontiguousarray(k, dtype=np.uint16)
@@ -106,7 +108,7 @@ def decode(q, k, v, scale, seqlens=None, tile=128, nthreads=0, with_lse=True):
     rc = lib().fgqa_oracle_decode_bf16(
         _ptr(q, ctypes.c_uint16), _ptr(k, ctypes.c_uint16), _ptr(v, ctypes.c_uint16),
         float(scale), _ptr(o, ctypes.c_uint16), _ptr(lse, ctypes.c_float),
-        B, S, Hq, Hkv, D, _ptr(sl, ctypes.c_int32), int(tile), int(nthreads))
+        B, S, Hq, Hkv, D, _ptr(sl, ctypes.c_int32), int(tile), int(bool(p_bf16)), int(nthreads))
     if rc != 0:
         raise ValueError("fgqa_oracle_decode_bf16: invalid arguments")
     return o, lse

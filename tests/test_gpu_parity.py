@@ -259,6 +259,29 @@ def test_prefill_whole_and_split_kernels(cuda, monkeypatch, split, B, Sq, Skv, H
                    f"split={split} B{B} Sq{Sq} Skv{Skv} Hq{Hq} Hkv{Hkv} causal{causal}")
 
 
+@pytest.mark.parametrize("scale", [0.2, -0.05])
+def test_scale_values(cuda, scale):
+    """Non-default and negative softmax scales (the prefill kernel folds the
+    sign into Q, the decode kernel into the exponent argument)."""
+    import torch
+    fg = _fg()
+    B, S, Hq, Hkv = 2, 300, 8, 2
+    q = oracle.normal_bf16(910, (B, S, Hq, 128))
+    k = oracle.normal_bf16(910, (B, S, Hkv, 128), stream=1)
+    v = oracle.normal_bf16(910, (B, S, Hkv, 128), stream=2)
+    o_ref, lse_ref = oracle.prefill(q, k, v, scale, causal=True)
+    qd, kd, vd = (to_torch_bf16(x, cuda) for x in (q, k, v))
+    out, lse = fg.flash_gqa_forward_bshd(qd, kd, vd, scale, causal=True)
+    _sync()
+    _check_prefill(from_torch_bf16(out), lse.cpu().numpy(), o_ref, lse_ref, f"prefill scale {scale}")
+    qdec = q[:, -1].copy()
+    od_ref, ld_ref = oracle.decode(qdec, k, v, scale)
+    ld = torch.empty((B, Hq), dtype=torch.float32, device=cuda)
+    od = fg.decode_flash_gqa_bshd(to_torch_bf16(qdec, cuda), kd, vd, scale, lse=ld)
+    _sync()
+    _check_decode(from_torch_bf16(od), ld.cpu().numpy(), od_ref, ld_ref, f"decode scale {scale}")
+
+
 def test_prefill_row0_and_triton_layout(cuda):
     import torch
     fg = _fg()

@@ -201,6 +201,26 @@ def test_decode_oracle_known_answers():
     assert np.all(np.abs(oracle.bf16_to_f32(o) - 0.75) <= 0.75 * 2**-7)
 
 
+def test_decode_oracle_fp32_p_variant():
+    """p_bf16=False restates the torch tiled decode reference
+    (test_decode_flash_gqa_kernel.py:26-79): the same online softmax with P
+    kept in fp32.  It sits closer to the float64 answer than the bf16-P path,
+    and with constant V it returns that constant to output rounding."""
+    B, Hq, Hkv, S = 2, 16, 2, 1000
+    q, k, v = _decode_inputs(17, B, Hq, Hkv, S)
+    of, lf = _decode_f64(q, k, v, SCALE)
+    o32, l32 = oracle.decode(q, k, v, SCALE, p_bf16=False)
+    o16, _ = oracle.decode(q, k, v, SCALE, p_bf16=True)
+    e32 = np.abs(oracle.bf16_to_f32(o32) - of)
+    e16 = np.abs(oracle.bf16_to_f32(o16) - of)
+    _assert_bf16_rounding_only(oracle.bf16_to_f32(o32), of)
+    assert e32.mean() < 0.75 * e16.mean(), (e32.mean(), e16.mean())
+    assert np.max(np.abs(l32 - lf)) < 1e-4
+    c = oracle.f32_to_bf16(np.float32(0.75))
+    o, _ = oracle.decode(q, k, np.full_like(v, c), SCALE, p_bf16=False)
+    assert np.all(np.abs(oracle.bf16_to_f32(o) - 0.75) <= 0.75 * 2**-9)
+
+
 def test_decode_oracle_invariants():
     B, Hq, Hkv, S = 2, 16, 2, 700
     q, k, v = _decode_inputs(13, B, Hq, Hkv, S)
