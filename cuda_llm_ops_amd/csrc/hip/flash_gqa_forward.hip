@@ -132,22 +132,44 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     // before reading the other buffer); their completion is awaited
     // explicitly (wait_vmem) before the barrier that publishes the tile.
     const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)smem;
-    auto dma16 = [](uint32_t lds_addr, uint32_t voffset, __amdgpu_buffer_rsrc_t rsrc) {
-        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                     :: "s"(lds_addr), "v"(voffset), "s"(rsrc) : "memory");
+    auto dma16 = [](uint32_t lds_addr, uint32_t voffset, uint32_t soffset, __amdgpu_buffer_rsrc_t rsrc) {
+        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                     :: "s"(lds_addr), "v"(voffset), "s"(rsrc), "s"(soffset) : "memory");
     };
-    auto issue_tile = [&](int j, int kb, int vb) {
-        const int t = t_first + j;
+    // Per-lane byte offsets of the 4 rows this lane fetches within a tile
+    // (tile rows r = 4*(wave + 4*i) + lane/16, swizzled chunk); the tile's
+    // start goes in the scalar offset.
+    uint32_t koff_dma[4], voff_dma[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r0 = 4 * (wave + 4 * i);          // first row written by this instruction
-            const int r = r0 + (lane >> 4);
-            const uint32_t tok = (uint32_t)min(t * kPfTile + r, kv_last);
-            if (kb >= 0)
-                dma16(lds_base + kb * kPfTileBytes + r0 * kPfRowBytes, tok * kss + ((l16 ^ (r & 15)) << 4), krs);
-            if (vb >= 0)
-                dma16(lds_base + (2 + vb) * kPfTileBytes + r0 * kPfRowBytes, tok * vss + ((l16 ^ (4 * (r & 3))) << 4),
-                      vrs);
+    for (int i = 0; i < 4; ++i) {
+        const int r = 4 * (wave + 4 * i) + (lane >> 4);
+        koff_dma[i] = (uint32_t)r * kss + ((l16 ^ (r & 15)) << 4);
+        voff_dma[i] = (uint32_t)r * vss + ((l16 ^ (4 * (r & 3))) << 4);
+    }
+    auto issue_tile = [&](int j, int kb, int vb) {
+        const int t0 = (t_first + j) * kPfTile;
+        if (t0 + kPfTile - 1 <= kv_last) {   // whole tile in range
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t r0 = 4 * (wave + 4 * i);   // first row written by this instruction
+                if (kb >= 0)
+                    dma16(lds_base + kb * kPfTileBytes + r0 * kPfRowBytes, koff_dma[i], (uint32_t)t0 * kss, krs);
+                if (vb >= 0)
+                    dma16(lds_base + (2 + vb) * kPfTileBytes + r0 * kPfRowBytes, voff_dma[i], (uint32_t)t0 * vss, vrs);
+            }
+        } else {   // last tile: rows past the last key are clamped to it
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r0 = 4 * (wave + 4 * i);
+                const int r = r0 + (lane >> 4);
+                const uint32_t tok = (uint32_t)min(t0 + r, kv_last);
+                if (kb >= 0)
+                    dma16(lds_base + kb * kPfTileBytes + r0 * kPfRowBytes, tok * kss + ((l16 ^ (r & 15)) << 4), 0u,
+                          krs);
+                if (vb >= 0)
+                    dma16(lds_base + (2 + vb) * kPfTileBytes + r0 * kPfRowBytes,
+                          tok * vss + ((l16 ^ (4 * (r & 3))) << 4), 0u, vrs);
+            }
         }
     };
 
