@@ -1,15 +1,19 @@
-"""MI355X-native flash grouped-query attention (decode + causal prefill).
+"""MI355X-native flash grouped-query attention (decode, causal prefill and its backward).
 
 The kernels live in libfgqa.so (HIP, gfx950); ``flash_gqa`` is the Python host
 interface over its C ABI (include/fgqa.h).
 """
 from ._lib import FgqaError, LIB_PATH, lib, status_string  # noqa: F401
 from .flash_gqa import (  # noqa: F401
+    backward_workspace_bytes,
     decode_flash_gqa_bshd,
     decode_workspace_bytes,
+    flash_gqa_backward_bshd,
     flash_gqa_forward_bshd,
     launch_decode_flash_gqa_bf16_kernel,
+    launch_flash_gqa_backward_bf16_kernel,
     launch_flash_gqa_forward_bf16_kernel,
+    prepare_backward,
     prepare_decode,
     prepare_prefill,
     PreparedLaunch,

@@ -70,6 +70,39 @@ class PrefillArgs(ctypes.Structure):
     ]
 
 
+class BackwardArgs(ctypes.Structure):
+    """Mirror of ``fgqa_prefill_backward_args`` (include/fgqa.h)."""
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("grad_o", ctypes.c_void_p),
+        ("grad_q", ctypes.c_void_p),
+        ("grad_k", ctypes.c_void_p),
+        ("grad_v", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("seqlen_q", ctypes.c_int32),
+        ("seqlen_kv", ctypes.c_int32),
+        ("num_q_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("causal", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("q_stride", _I64x3),
+        ("k_stride", _I64x3),
+        ("v_stride", _I64x3),
+        ("o_stride", _I64x3),
+        ("grad_o_stride", _I64x3),
+        ("grad_q_stride", _I64x3),
+        ("grad_k_stride", _I64x3),
+        ("grad_v_stride", _I64x3),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 class FgqaError(RuntimeError):
     def __init__(self, status: int, where: str):
         self.status = status
@@ -94,6 +127,11 @@ def lib() -> ctypes.CDLL:
         L.fgqa_decode_bf16.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.c_void_p]
         L.fgqa_prefill_bf16.restype = ctypes.c_int
         L.fgqa_prefill_bf16.argtypes = [ctypes.POINTER(PrefillArgs), ctypes.c_void_p]
+        L.fgqa_prefill_backward_workspace_bytes.restype = ctypes.c_int
+        L.fgqa_prefill_backward_workspace_bytes.argtypes = [ctypes.POINTER(BackwardArgs),
+                                                            ctypes.POINTER(ctypes.c_size_t)]
+        L.fgqa_prefill_backward_bf16.restype = ctypes.c_int
+        L.fgqa_prefill_backward_bf16.argtypes = [ctypes.POINTER(BackwardArgs), ctypes.c_void_p]
         L.fgqa_status_string.restype = ctypes.c_char_p
         L.fgqa_status_string.argtypes = [ctypes.c_int]
         L.fgqa_version.restype = ctypes.c_int

@@ -3,6 +3,7 @@
 #include <cstring>
 
 #include "FlashGQA/decode_flash_gqa_kernel.h"
+#include "FlashGQA/flash_gqa_backward_kernel.h"
 #include "FlashGQA/flash_gqa_forward_kernel.h"
 #include "fgqa.h"
 
@@ -101,6 +102,39 @@ void LaunchFlashGqaForwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf1
     const int64_t ks[3] = {(int64_t)seqLengthKv * numKvHeads * headDim, (int64_t)numKvHeads * headDim, headDim};
     LaunchFlashGqaForwardBf16KernelStrided(q, k, v, scale, o, lse, batchSize, seqLengthQ, seqLengthKv,
                                            numQueryHeads, numKvHeads, headDim, causal, qs, ks, ks, qs);
+}
+
+void LaunchFlashGqaBackwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* o,
+                                      const float* lse, const bf16_t* gradO, float scale, bf16_t* gradQ,
+                                      bf16_t* gradK, bf16_t* gradV, int batchSize, int seqLengthQ, int seqLengthKv,
+                                      int numQueryHeads, int numKvHeads, int headDim, bool causal) {
+    fgqa_prefill_backward_args a;
+    std::memset(&a, 0, sizeof(a));
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.o = o;
+    a.lse = lse;
+    a.grad_o = gradO;
+    a.grad_q = gradQ;
+    a.grad_k = gradK;
+    a.grad_v = gradV;
+    a.batch = batchSize;
+    a.seqlen_q = seqLengthQ;
+    a.seqlen_kv = seqLengthKv;
+    a.num_q_heads = numQueryHeads;
+    a.num_kv_heads = numKvHeads;
+    a.head_dim = headDim;
+    a.causal = causal ? 1 : 0;
+    a.scale = scale;
+    // BSHD: q, o, gradO, gradQ [B, Sq, Hq, D]; k, v, gradK, gradV [B, Skv, Hkv, D]
+    const int64_t qs[3] = {(int64_t)seqLengthQ * numQueryHeads * headDim, (int64_t)numQueryHeads * headDim, headDim};
+    const int64_t ks[3] = {(int64_t)seqLengthKv * numKvHeads * headDim, (int64_t)numKvHeads * headDim, headDim};
+    for (int i = 0; i < 3; ++i) {
+        a.q_stride[i] = a.o_stride[i] = a.grad_o_stride[i] = a.grad_q_stride[i] = qs[i];
+        a.k_stride[i] = a.v_stride[i] = a.grad_k_stride[i] = a.grad_v_stride[i] = ks[i];
+    }
+    g_last_status = fgqa_prefill_backward_bf16(&a, nullptr);
 }
 
 int FlashGqaGetLastStatus() { return g_last_status; }

@@ -6,14 +6,16 @@ Two families of entry points:
   ``ValueError`` behaviour, BHSD layout:
     - ``launch_flash_gqa_forward_bf16_kernel`` <- src/python/Triton/flash_gqa_kernel.py:185-338
     - ``launch_decode_flash_gqa_bf16_kernel``  <- src/python/Triton/decode_flash_gqa_kernel.py:137-196
+    - ``launch_flash_gqa_backward_bf16_kernel`` <- src/python/Triton/flash_gqa_backward_kernel.py:312-478
 * The C++ layouts of the reference's C++ decode entry point (Q/O ``[B,Hq,D]``,
   K/V ``[B,S,Hkv,D]``, decode_flash_gqa_kernel.cuh:28-38) and of the new C++
   prefill entry point (BSHD):
     - ``decode_flash_gqa_bshd``  (adds per-sequence lengths and an LSE output)
     - ``flash_gqa_forward_bshd``
+    - ``flash_gqa_backward_bshd``
 
 PyTorch only provides device memory and the current stream; every launch goes
-through ``fgqa_decode_bf16`` / ``fgqa_prefill_bf16``.
+through ``fgqa_decode_bf16`` / ``fgqa_prefill_bf16`` / ``fgqa_prefill_backward_bf16``.
 """
 from __future__ import annotations
 
@@ -27,11 +29,15 @@ from . import _lib
 __all__ = [
     "launch_flash_gqa_forward_bf16_kernel",
     "launch_decode_flash_gqa_bf16_kernel",
+    "launch_flash_gqa_backward_bf16_kernel",
     "decode_flash_gqa_bshd",
     "flash_gqa_forward_bshd",
+    "flash_gqa_backward_bshd",
     "decode_workspace_bytes",
+    "backward_workspace_bytes",
     "prepare_decode",
     "prepare_prefill",
+    "prepare_backward",
     "PreparedLaunch",
 ]
 
@@ -355,3 +361,186 @@ def launch_flash_gqa_forward_bf16_kernel(q, k, v, scale=None, out=None, lse=None
     if squeeze_output:
         return out_b.squeeze(0), lse_b.squeeze(0)
     return out_b, lse_b
+
+
+# --------------------------------------------------------------------------- backward
+def _backward_args(q, k, v, o, lse, grad_o, dq, dk, dv, scale, causal, layout, workspace) -> _lib.BackwardArgs:
+    """C ABI argument block; 4-D tensors in `layout` ('bshd' or 'bhsd')."""
+    def sbh(t):
+        if layout == "bshd":
+            return [t.stride(0), t.stride(1), t.stride(2)]
+        return [t.stride(0), t.stride(2), t.stride(1)]
+
+    if layout == "bshd":
+        B, Sq, Hq, D = q.shape
+        _, Skv, Hkv, _ = k.shape
+    else:
+        B, Hq, Sq, D = q.shape
+        _, Hkv, Skv, _ = k.shape
+    a = _lib.BackwardArgs()
+    a.q, a.k, a.v, a.o, a.lse, a.grad_o = (_ptr(x) for x in (q, k, v, o, lse, grad_o))
+    a.grad_q, a.grad_k, a.grad_v = _ptr(dq), _ptr(dk), _ptr(dv)
+    a.batch, a.seqlen_q, a.seqlen_kv = B, Sq, Skv
+    a.num_q_heads, a.num_kv_heads, a.head_dim = Hq, Hkv, D
+    a.causal = 1 if causal else 0
+    a.scale = float(scale)
+    a.q_stride[:] = sbh(q)
+    a.k_stride[:] = sbh(k)
+    a.v_stride[:] = sbh(v)
+    a.o_stride[:] = sbh(o)
+    a.grad_o_stride[:] = sbh(grad_o)
+    a.grad_q_stride[:] = sbh(dq)
+    a.grad_k_stride[:] = sbh(dk)
+    a.grad_v_stride[:] = sbh(dv)
+    if workspace is not None:
+        a.workspace = workspace.data_ptr()
+        a.workspace_bytes = workspace.numel() * workspace.element_size()
+    return a
+
+
+def backward_workspace_bytes(batch, seqlen_q, seqlen_kv, num_q_heads, num_kv_heads, head_dim=128) -> int:
+    """Bytes of scratch ``flash_gqa_backward_bshd`` needs for a caller workspace
+    (256-byte aligned; depends on the current device's CU count)."""
+    a = _lib.BackwardArgs()
+    a.batch, a.seqlen_q, a.seqlen_kv = batch, seqlen_q, seqlen_kv
+    a.num_q_heads, a.num_kv_heads, a.head_dim = num_q_heads, num_kv_heads, head_dim
+    a.scale = 1.0
+    qs = [seqlen_q * num_q_heads * head_dim, num_q_heads * head_dim, head_dim]
+    ks = [seqlen_kv * num_kv_heads * head_dim, num_kv_heads * head_dim, head_dim]
+    for name in ("q_stride", "o_stride", "grad_o_stride", "grad_q_stride"):
+        getattr(a, name)[:] = qs
+    for name in ("k_stride", "v_stride", "grad_k_stride", "grad_v_stride"):
+        getattr(a, name)[:] = ks
+    n = ctypes.c_size_t(0)
+    _lib.check(_lib.lib().fgqa_prefill_backward_workspace_bytes(ctypes.byref(a), ctypes.byref(n)),
+               "fgqa_prefill_backward_workspace_bytes")
+    return int(n.value)
+
+
+def _grad_out(t, shape, ref, name):
+    if t is None:
+        return torch.empty(shape, device=ref.device, dtype=torch.bfloat16)
+    if tuple(t.shape) != tuple(shape) or t.dtype != torch.bfloat16 or not _kernel_ready(t):
+        raise ValueError(f"{name} must be a bf16 tensor of shape {list(shape)} with contiguous, aligned rows")
+    return t
+
+
+def _backward_bshd_prepare(q, k, v, o, lse, grad_o, scale, causal, grad_q, grad_k, grad_v, workspace):
+    for t in (q, k, v, o, grad_o):
+        if t.dtype != torch.bfloat16:
+            raise ValueError("Flash GQA backward expects bf16 inputs and grad_o")
+    if lse.dtype != torch.float32:
+        raise ValueError("Flash GQA backward expects lse to be float32")
+    if any(t.dim() != 4 for t in (q, k, v, o, grad_o)):
+        raise ValueError("expected 4-D BSHD tensors")
+    _require_cuda(q, k, v, o, lse, grad_o)
+    B, Sq, Hq, D = q.shape
+    if k.shape != v.shape or k.shape[0] != B or k.shape[3] != D:
+        raise ValueError("K and V must be [B, Skv, Hkv, D] matching Q")
+    if o.shape != q.shape or grad_o.shape != q.shape:
+        raise ValueError("O and grad_o must have Q's shape [B, Sq, Hq, D]")
+    if Hq % k.shape[2] != 0:
+        raise ValueError("Query heads must be divisible by KV heads")
+    if lse.shape != (B, Hq, Sq) or not lse.is_contiguous():
+        raise ValueError("LSE must be a contiguous fp32 [batch, q_heads, seqlen_q] tensor")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    q, k, v, o, grad_o = (_prep(t) for t in (q, k, v, o, grad_o))
+    grad_q = _grad_out(grad_q, q.shape, q, "grad_q")
+    grad_k = _grad_out(grad_k, k.shape, q, "grad_k")
+    grad_v = _grad_out(grad_v, v.shape, q, "grad_v")
+    a = _backward_args(q, k, v, o, lse, grad_o, grad_q, grad_k, grad_v, scale, causal, "bshd", workspace)
+    return a, (grad_q, grad_k, grad_v), (q, k, v, o, lse, grad_o, grad_q, grad_k, grad_v, workspace)
+
+
+def flash_gqa_backward_bshd(q, k, v, o, lse, grad_o, scale=None, causal=True,
+                            grad_q=None, grad_k=None, grad_v=None, workspace=None):
+    """Prefill backward in BSHD: q/o/grad_o [B,Sq,Hq,D], k/v [B,Skv,Hkv,D], lse
+    [B,Hq,Sq] from the forward -> (grad_q, grad_k, grad_v) bf16 in q/k/v's shapes."""
+    a, grads, _keep = _backward_bshd_prepare(q, k, v, o, lse, grad_o, scale, causal,
+                                             grad_q, grad_k, grad_v, workspace)
+    _lib.check(_lib.lib().fgqa_prefill_backward_bf16(ctypes.byref(a), ctypes.c_void_p(_stream())),
+               "fgqa_prefill_backward_bf16")
+    return grads
+
+
+def prepare_backward(q, k, v, o, lse, grad_o, scale=None, causal=True,
+                     grad_q=None, grad_k=None, grad_v=None, workspace=None):
+    """``flash_gqa_backward_bshd`` validated once; returns a ``PreparedLaunch``
+    whose ``out`` is the (grad_q, grad_k, grad_v) tuple."""
+    a, grads, keep = _backward_bshd_prepare(q, k, v, o, lse, grad_o, scale, causal,
+                                            grad_q, grad_k, grad_v, workspace)
+    return PreparedLaunch(_lib.lib().fgqa_prefill_backward_bf16, a, keep, grads, "fgqa_prefill_backward_bf16")
+
+
+def launch_flash_gqa_backward_bf16_kernel(q, k, v, o, lse, grad_o, scale=None, causal=True,
+                                          block_kv=64, num_warps=4, num_stages=3):
+    """Mirror of the reference's Triton backward launcher
+    (src/python/Triton/flash_gqa_backward_kernel.py:312-478): BHSD q/o/grad_o
+    [B,Hq,Sq,D] (or 3-D [Hq,Sq,D]), k/v [B,Hkv,Skv,D], lse [B,Hq,Sq] (or
+    [Hq,Sq]); returns bf16 (grad_q, grad_k, grad_v) shaped like q, k, v.
+
+    Same checks and ValueError messages as the reference (:356-405).
+    ``block_kv``, ``num_warps`` and ``num_stages`` are Triton tuning knobs,
+    accepted for signature compatibility only.  Beyond the reference, inputs
+    must share the batch dimension and head_dim_v must equal head_dim_qk (128).
+    """
+    del block_kv, num_warps, num_stages
+    if (q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16
+            or o.dtype != torch.bfloat16 or grad_o.dtype != torch.bfloat16):
+        raise ValueError("Flash GQA backward expects bf16 inputs and grad_o")
+    if lse.dtype != torch.float32:
+        raise ValueError("Flash GQA backward expects lse to be float32")
+    if q.dim() not in (3, 4):
+        raise ValueError("Q must be 3D or 4D")
+    if k.dim() != q.dim() or v.dim() != q.dim() or o.dim() != q.dim() or grad_o.dim() != q.dim():
+        raise ValueError("Q, K, V, O, and grad_o must have matching ranks")
+    squeeze_output = q.dim() == 3
+    qb, kb, vb, ob, gb = (t.unsqueeze(0) if squeeze_output else t for t in (q, k, v, o, grad_o))
+    batch, q_heads, seqlen_q, head_dim_qk = qb.shape
+    _, num_kv_heads, seqlen_kv, k_head_dim = kb.shape
+    _, v_heads, v_seqlen, head_dim_v = vb.shape
+    _, o_heads, o_seqlen, o_head_dim = ob.shape
+    _, grad_o_heads, grad_o_seqlen, grad_o_head_dim = gb.shape
+    if seqlen_kv != v_seqlen:
+        raise ValueError("K and V must share sequence length")
+    if seqlen_q != o_seqlen or seqlen_q != grad_o_seqlen:
+        raise ValueError("Q, O, and grad_o must share sequence length")
+    if k_head_dim != head_dim_qk:
+        raise ValueError("Q and K must share head_dim_qk")
+    if o_head_dim != head_dim_v or grad_o_head_dim != head_dim_v:
+        raise ValueError("O and grad_o must share head_dim_v with V")
+    if v_heads != num_kv_heads:
+        raise ValueError("K and V must share number of KV heads")
+    if o_heads != q_heads or grad_o_heads != q_heads:
+        raise ValueError("Q, O, and grad_o must share number of query heads")
+    if q_heads % num_kv_heads != 0:
+        raise ValueError("Query heads must be divisible by KV heads")
+    if squeeze_output:
+        if lse.dim() != 2:
+            raise ValueError("LSE must be 2D when Q is 3D")
+        lse_b = lse.unsqueeze(0)
+    else:
+        if lse.dim() != 3:
+            raise ValueError("LSE must be 3D when Q is 4D")
+        lse_b = lse
+    if tuple(lse_b.shape) != (batch, q_heads, seqlen_q):
+        raise ValueError("LSE must have shape [batch, q_heads, seqlen_q]")
+    if any(t.shape[0] != batch for t in (kb, vb, ob, gb)):
+        raise ValueError("Q, K, V, O, and grad_o must share batch dimension")
+    if head_dim_v != head_dim_qk:
+        raise ValueError("head_dim_v must equal head_dim_qk on this path")
+    _require_cuda(qb, kb, vb, ob, lse_b, gb)
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim_qk)
+    qb, kb, vb, ob, gb = (_prep(t) for t in (qb, kb, vb, ob, gb))
+    lse_b = lse_b.contiguous()
+    dq = torch.empty((batch, q_heads, seqlen_q, head_dim_qk), device=qb.device, dtype=torch.bfloat16)
+    dk = torch.empty((batch, num_kv_heads, seqlen_kv, head_dim_qk), device=qb.device, dtype=torch.bfloat16)
+    dv = torch.empty((batch, num_kv_heads, seqlen_kv, head_dim_v), device=qb.device, dtype=torch.bfloat16)
+    a = _backward_args(qb, kb, vb, ob, lse_b, gb, dq, dk, dv, scale, causal, "bhsd", None)
+    _lib.check(_lib.lib().fgqa_prefill_backward_bf16(ctypes.byref(a), ctypes.c_void_p(_stream())),
+               "fgqa_prefill_backward_bf16")
+    if squeeze_output:
+        return dq.squeeze(0), dk.squeeze(0), dv.squeeze(0)
+    return dq, dk, dv

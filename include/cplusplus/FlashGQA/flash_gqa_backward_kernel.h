@@ -1,0 +1,52 @@
+// FlashGQA prefill backward: C++ operator entry point (MI355X / gfx950).
+//
+// The reference implements the backward only in Triton
+// (src/python/Triton/flash_gqa_backward_kernel.py:312-478, kernels :16-50 and
+// :159-310); this is its C++ counterpart, in the BSHD layout of
+// LaunchFlashGqaForwardBf16Kernel and consuming that call's O and LSE.
+#pragma once
+
+#include <cstdint>
+
+#include "Utils/utils.h"
+
+/**
+ * @brief Launches the FlashGQA bf16 prefill backward (BSHD layout).
+ * @param q Device query tensor [batchSize, seqLengthQ, numQueryHeads, headDim].
+ * @param k Device key tensor [batchSize, seqLengthKv, numKvHeads, headDim].
+ * @param v Device value tensor [batchSize, seqLengthKv, numKvHeads, headDim].
+ * @param o Forward output [batchSize, seqLengthQ, numQueryHeads, headDim].
+ * @param lse Forward fp32 log-sum-exp [batchSize, numQueryHeads, seqLengthQ] (natural log).
+ * @param gradO Gradient of the output, layout of o.
+ * @param scale Scaling factor the forward applied to QK scores.
+ * @param gradQ Output: gradient of q, layout of q.
+ * @param gradK Output: gradient of k, layout of k.
+ * @param gradV Output: gradient of v, layout of v.
+ * @param batchSize Batch size.
+ * @param seqLengthQ Query sequence length.
+ * @param seqLengthKv Key/value sequence length.
+ * @param numQueryHeads Number of query heads.
+ * @param numKvHeads Number of KV heads (must divide numQueryHeads).
+ * @param headDim Per-head embedding dimension (128).
+ * @param causal The forward's top-left aligned causal mask (query i sees keys j <= i).
+ *
+ * Uses the library's per-device cached workspace on the default stream; the
+ * status of the call is returned by FlashGqaGetLastStatus().
+ */
+void LaunchFlashGqaBackwardBf16Kernel(const bf16_t* q,
+                                      const bf16_t* k,
+                                      const bf16_t* v,
+                                      const bf16_t* o,
+                                      const float* lse,
+                                      const bf16_t* gradO,
+                                      float scale,
+                                      bf16_t* gradQ,
+                                      bf16_t* gradK,
+                                      bf16_t* gradV,
+                                      int batchSize,
+                                      int seqLengthQ,
+                                      int seqLengthKv,
+                                      int numQueryHeads,
+                                      int numKvHeads,
+                                      int headDim,
+                                      bool causal);

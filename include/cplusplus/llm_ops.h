@@ -4,5 +4,6 @@
 #pragma once
 
 #include "FlashGQA/decode_flash_gqa_kernel.h"
+#include "FlashGQA/flash_gqa_backward_kernel.h"
 #include "FlashGQA/flash_gqa_forward_kernel.h"
 #include "Utils/utils.h"

@@ -13,6 +13,7 @@
  *   - `stream` is a hipStream_t (NULL = the default stream).  Launches are
  *     asynchronous; the functions never synchronise the device.
  *   - Supported: head_dim == 128; decode needs num_q_heads / num_kv_heads <= 16.
+ *     Sequence strides should be at least head_dim (rows do not overlap).
  *   - Every entry point returns FGQA_OK (0) or a negative fgqa_status; nothing
  *     is launched when the status is not FGQA_OK.  No exception crosses the ABI.
  */
@@ -120,6 +121,59 @@ typedef struct fgqa_prefill_args {
 } fgqa_prefill_args;
 
 int fgqa_prefill_bf16(const fgqa_prefill_args* args, void* stream);
+
+/*
+ * Prefill backward: dQ, dK, dV of the causal (or full) forward above.
+ * Replaces the Triton-only launch_flash_gqa_backward_bf16_kernel, reference
+ * src/python/Triton/flash_gqa_backward_kernel.py:312-478 (kernels :16-50 and
+ * :159-310), which has no C++ counterpart in the reference.
+ *
+ *   q, o, grad_o, grad_q  [B, Sq, Hq, D]   strides {b, s, h} each
+ *   k, v, grad_k, grad_v  [B, Skv, Hkv, D] strides {b, s, h} each
+ *   lse  fp32 [B, Hq, Sq] contiguous, natural log, as fgqa_prefill_bf16
+ *        writes it
+ *   causal, scale  as in the forward call that produced o and lse.
+ * grad_* are written (not accumulated); a key that no query row sees gets
+ * zero gradients.  Gradients are accumulated in fp32 in the workspace and
+ * rounded to bf16 once.
+ * workspace / workspace_bytes  device scratch of at least
+ *   fgqa_prefill_backward_workspace_bytes() bytes, 256-byte aligned; NULL/0
+ *   uses the library's per-device cached buffer.
+ */
+typedef struct fgqa_prefill_backward_args {
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* o;
+    const float* lse;
+    const void* grad_o;
+    void* grad_q;
+    void* grad_k;
+    void* grad_v;
+    int32_t batch;
+    int32_t seqlen_q;
+    int32_t seqlen_kv;
+    int32_t num_q_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t causal;
+    float scale;
+    int64_t q_stride[3];
+    int64_t k_stride[3];
+    int64_t v_stride[3];
+    int64_t o_stride[3];
+    int64_t grad_o_stride[3];
+    int64_t grad_q_stride[3];
+    int64_t grad_k_stride[3];
+    int64_t grad_v_stride[3];
+    void* workspace;
+    size_t workspace_bytes;
+} fgqa_prefill_backward_args;
+
+/* Bytes of workspace fgqa_prefill_backward_bf16 needs (pointers unused). */
+int fgqa_prefill_backward_workspace_bytes(const fgqa_prefill_backward_args* args, size_t* bytes);
+
+int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* args, void* stream);
 
 /* Static, human-readable text for a status code. */
 const char* fgqa_status_string(int status);

@@ -5,6 +5,7 @@ may import this package, and only as the checker (or the timed CPU baseline).
 The product (``cuda_llm_ops_amd``) never imports it.
 """
 from .oracle import (  # noqa: F401
+    attention_backward_f64,
     attention_f64,
     bf16_to_f32,
     decode,
@@ -12,4 +13,5 @@ from .oracle import (  # noqa: F401
     lib,
     normal_bf16,
     prefill,
+    prefill_backward,
 )

@@ -282,3 +282,197 @@ int fgqa_oracle_attention_f64(const uint16_t* q, const uint16_t* k, const uint16
     }
     return 0;
 }
+
+/*
+ * Prefill backward (reference src/python/Triton/flash_gqa_backward_kernel.py).
+ * p and dS of a (row, key) pair are recomputed by bwd_pair() with the same
+ * operation order wherever they are needed, so the dQ pass (parallel over
+ * rows) and the dK/dV pass (parallel over keys) see identical values.
+ */
+typedef struct {
+    const uint16_t *q, *k, *v, *grad_o;
+    const float *lse, *delta;
+    const int64_t *qs, *ks, *vs, *dos;
+    float scale;
+    int sq, hq, d, group;
+} bwd_ctx;
+
+/* :253-285 for query row i of head h and key j of batch b: returns p (fp32)
+ * and stores dS (rounded to bf16, as a float) in *ds. */
+static float bwd_pair(const bwd_ctx* c, int b, int h, int i, int j, float* ds) {
+    const int kvh = h / c->group;
+    const uint16_t* qrow = c->q + b * c->qs[0] + (int64_t)i * c->qs[1] + h * c->qs[2];
+    const uint16_t* krow = c->k + b * c->ks[0] + (int64_t)j * c->ks[1] + kvh * c->ks[2];
+    const uint16_t* vrow = c->v + b * c->vs[0] + (int64_t)j * c->vs[1] + kvh * c->vs[2];
+    const uint16_t* dorow = c->grad_o + b * c->dos[0] + (int64_t)i * c->dos[1] + h * c->dos[2];
+    float s = 0.f, dp = 0.f;
+    for (int x = 0; x < c->d; ++x) s += bf(qrow[x]) * bf(krow[x]);
+    for (int x = 0; x < c->d; ++x) dp += bf(dorow[x]) * bf(vrow[x]);
+    const size_t r = ((size_t)b * c->hq + h) * c->sq + i;
+    const float p = expf(s * c->scale - c->lse[r]);
+    *ds = bf(fgqa_oracle_f32_to_bf16(p * (dp - c->delta[r]) * c->scale));
+    return p;
+}
+
+int fgqa_oracle_prefill_backward_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                      const uint16_t* o, const float* lse, const uint16_t* grad_o,
+                                      float scale, float* dq, float* dk, float* dv,
+                                      int batch, int sq, int skv, int hq, int hkv, int d,
+                                      const int64_t* qs, const int64_t* ks,
+                                      const int64_t* vs, const int64_t* os,
+                                      const int64_t* dos, int causal,
+                                      const int* rows, const int* keys, int nthreads) {
+    if (!q || !k || !v || !o || !lse || !grad_o || !qs || !ks || !vs || !os || !dos) return -1;
+    if (batch < 0 || sq < 0 || skv < 0 || hq <= 0 || hkv <= 0 || d <= 0 || d > ORACLE_MAX_D) return -1;
+    if (hq % hkv != 0) return -1;
+    const int group = hq / hkv;
+    const int r0 = rows ? rows[0] : 0, r1 = rows ? rows[1] : sq;
+    const int k0 = keys ? keys[0] : 0, k1 = keys ? keys[1] : skv;
+    if (r0 < 0 || r1 > sq || k0 < 0 || k1 > skv) return -1;
+    set_threads(nthreads);
+
+    /* :16-50 delta for every row (the dK/dV pass needs all of them) */
+    const size_t nrows = (size_t)batch * hq * sq;
+    float* delta = (float*)malloc(sizeof(float) * (nrows > 0 ? nrows : 1));
+    if (!delta) return -1;
+#pragma omp parallel for collapse(3) schedule(static)
+    for (int b = 0; b < batch; ++b)
+        for (int h = 0; h < hq; ++h)
+            for (int i = 0; i < sq; ++i) {
+                const uint16_t* orow = o + b * os[0] + (int64_t)i * os[1] + h * os[2];
+                const uint16_t* dorow = grad_o + b * dos[0] + (int64_t)i * dos[1] + h * dos[2];
+                float acc = 0.f;
+                for (int x = 0; x < d; ++x) acc += bf(orow[x]) * bf(dorow[x]);
+                delta[((size_t)b * hq + h) * sq + i] = acc;
+            }
+
+    bwd_ctx c = {q, k, v, grad_o, lse, delta, qs, ks, vs, dos, scale, sq, hq, d, group};
+
+    /* :292-293 dQ_i = sum_j dS_ij k_j over the keys row i sees */
+    if (dq) {
+#pragma omp parallel for collapse(3) schedule(dynamic, 4)
+        for (int b = 0; b < batch; ++b)
+            for (int h = 0; h < hq; ++h)
+                for (int i = r0; i < r1; ++i) {
+                    const int kvh = h / group;
+                    float acc[ORACLE_MAX_D];
+                    for (int x = 0; x < d; ++x) acc[x] = 0.f;
+                    const int jend = causal ? (i + 1 < skv ? i + 1 : skv) : skv;
+                    for (int j = 0; j < jend; ++j) {
+                        float ds;
+                        (void)bwd_pair(&c, b, h, i, j, &ds);
+                        const uint16_t* krow = k + b * ks[0] + (int64_t)j * ks[1] + kvh * ks[2];
+                        for (int x = 0; x < d; ++x) acc[x] += ds * bf(krow[x]);
+                    }
+                    float* out = dq + (((size_t)b * sq + i) * hq + h) * d;
+                    for (int x = 0; x < d; ++x) out[x] = acc[x];
+                }
+    }
+
+    /* :271-272, :287 dV_j = sum p_bf16 dO_i, dK_j = sum dS_ij q_i over the
+     * G heads of kv head kvh and the rows that see key j */
+    if (dk || dv) {
+#pragma omp parallel for collapse(3) schedule(dynamic, 4)
+        for (int b = 0; b < batch; ++b)
+            for (int kvh = 0; kvh < hkv; ++kvh)
+                for (int j = k0; j < k1; ++j) {
+                    float ak[ORACLE_MAX_D], av[ORACLE_MAX_D];
+                    for (int x = 0; x < d; ++x) ak[x] = av[x] = 0.f;
+                    const int ibeg = causal ? j : 0;
+                    for (int h = kvh * group; h < (kvh + 1) * group; ++h)
+                        for (int i = ibeg; i < sq; ++i) {
+                            float ds;
+                            const float pb = bf(fgqa_oracle_f32_to_bf16(bwd_pair(&c, b, h, i, j, &ds)));
+                            const uint16_t* qrow = q + b * qs[0] + (int64_t)i * qs[1] + h * qs[2];
+                            const uint16_t* dorow = grad_o + b * dos[0] + (int64_t)i * dos[1] + h * dos[2];
+                            for (int x = 0; x < d; ++x) {
+                                ak[x] += ds * bf(qrow[x]);
+                                av[x] += pb * bf(dorow[x]);
+                            }
+                        }
+                    const size_t base = (((size_t)b * skv + j) * hkv + kvh) * d;
+                    if (dk)
+                        for (int x = 0; x < d; ++x) dk[base + x] = ak[x];
+                    if (dv)
+                        for (int x = 0; x < d; ++x) dv[base + x] = av[x];
+                }
+    }
+    free(delta);
+    return 0;
+}
+
+/* Exact gradient of softmax attention in double (see the header). */
+int fgqa_oracle_attention_backward_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                       const uint16_t* o, const uint16_t* grad_o, double scale,
+                                       double* dq, double* dk, double* dv,
+                                       int batch, int sq, int skv, int hq, int hkv, int d,
+                                       const int64_t* qs, const int64_t* ks,
+                                       const int64_t* vs, const int64_t* os,
+                                       const int64_t* dos, int causal, int nthreads) {
+    if (!q || !k || !v || !grad_o || !dq || !dk || !dv || !qs || !ks || !vs || !dos) return -1;
+    if (o && !os) return -1;
+    if (batch < 0 || sq < 0 || skv < 0 || hq <= 0 || hkv <= 0 || d <= 0) return -1;
+    if (hq % hkv != 0) return -1;
+    const int group = hq / hkv;
+    set_threads(nthreads);
+    memset(dq, 0, sizeof(double) * (size_t)batch * sq * hq * d);
+    memset(dk, 0, sizeof(double) * (size_t)batch * skv * hkv * d);
+    memset(dv, 0, sizeof(double) * (size_t)batch * skv * hkv * d);
+
+    /* One (batch, kv head) per task: its dK/dV rows are private to it. */
+#pragma omp parallel for collapse(2) schedule(dynamic, 1)
+    for (int b = 0; b < batch; ++b)
+        for (int kvh = 0; kvh < hkv; ++kvh) {
+            double* p = (double*)malloc(sizeof(double) * (size_t)(skv > 0 ? skv : 1));
+            double* dp = (double*)malloc(sizeof(double) * (size_t)(skv > 0 ? skv : 1));
+            for (int h = kvh * group; h < (kvh + 1) * group; ++h)
+                for (int i = 0; i < sq; ++i) {
+                    const uint16_t* qrow = q + b * qs[0] + (int64_t)i * qs[1] + h * qs[2];
+                    const uint16_t* dorow = grad_o + b * dos[0] + (int64_t)i * dos[1] + h * dos[2];
+                    const int nvis = causal ? (i + 1 < skv ? i + 1 : skv) : skv;
+                    if (nvis == 0) continue;
+                    double rmax = -INFINITY;
+                    for (int j = 0; j < nvis; ++j) {
+                        const uint16_t* krow = k + b * ks[0] + (int64_t)j * ks[1] + kvh * ks[2];
+                        double acc = 0.0;
+                        for (int x = 0; x < d; ++x) acc += (double)bf(qrow[x]) * (double)bf(krow[x]);
+                        p[j] = acc * scale;
+                        if (p[j] > rmax) rmax = p[j];
+                    }
+                    double sum = 0.0;
+                    for (int j = 0; j < nvis; ++j) {
+                        p[j] = exp(p[j] - rmax);
+                        sum += p[j];
+                    }
+                    double delta = 0.0;
+                    for (int j = 0; j < nvis; ++j) {
+                        p[j] /= sum;
+                        const uint16_t* vrow = v + b * vs[0] + (int64_t)j * vs[1] + kvh * vs[2];
+                        double acc = 0.0;
+                        for (int x = 0; x < d; ++x) acc += (double)bf(dorow[x]) * (double)bf(vrow[x]);
+                        dp[j] = acc;
+                        delta += p[j] * acc;
+                    }
+                    if (o) {
+                        const uint16_t* orow = o + b * os[0] + (int64_t)i * os[1] + h * os[2];
+                        delta = 0.0;
+                        for (int x = 0; x < d; ++x) delta += (double)bf(orow[x]) * (double)bf(dorow[x]);
+                    }
+                    double* dqrow = dq + (((size_t)b * sq + i) * hq + h) * d;
+                    for (int j = 0; j < nvis; ++j) {
+                        const double ds = p[j] * (dp[j] - delta) * scale;
+                        const uint16_t* krow = k + b * ks[0] + (int64_t)j * ks[1] + kvh * ks[2];
+                        double* dkrow = dk + (((size_t)b * skv + j) * hkv + kvh) * d;
+                        double* dvrow = dv + (((size_t)b * skv + j) * hkv + kvh) * d;
+                        for (int x = 0; x < d; ++x) {
+                            dqrow[x] += ds * (double)bf(krow[x]);
+                            dkrow[x] += ds * (double)bf(qrow[x]);
+                            dvrow[x] += p[j] * (double)bf(dorow[x]);
+                        }
+                    }
+                }
+            free(p);
+            free(dp);
+        }
+    return 0;
+}

@@ -20,6 +20,12 @@
  *                                            to the fp64 answer than the bf16-P one
  *   fgqa_oracle_prefill_bf16                fp64 brute force, closed forms (row 0 = V[0],
  *                                            LSE of equal logits = log n), invariants
+ *   fgqa_oracle_prefill_backward_bf16       fp64 backward (fgqa_oracle_attention_backward_f64,
+ *                                            the torch-reference form) at the stated tolerance,
+ *                                            closed forms (one key: dQ = dK = 0, dV = sum dO),
+ *                                            invariants (sum_j dK_j = 0, sum_j dV_j = sum dO)
+ *   fgqa_oracle_attention_backward_f64      central finite differences of a float64
+ *                                            numpy forward on tiny inputs
  *   fgqa_oracle_attention_f64               textbook softmax attention in double;
  *                                            pinned by numpy float64 restatement and
  *                                            closed forms on tiny inputs
@@ -83,6 +89,53 @@ int fgqa_oracle_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_
                              const int64_t* q_strides, const int64_t* k_strides,
                              const int64_t* v_strides, const int64_t* o_strides,
                              int causal, int q_offset, int nthreads);
+
+/*
+ * Prefill backward, restating the reference's Triton backward
+ * src/python/Triton/flash_gqa_backward_kernel.py for one query row i and key j
+ * of query head h (kv head h / G):
+ *   :16-50   delta_i = sum_x O_i[x] dO_i[x]                         (fp32)
+ *   :253-262 p = exp(q_i.k_j * scale - lse_i); 0 where j > i (causal,
+ *            top-left) or j >= Skv                                   (fp32)
+ *   :263     p_bf16 = bf16(p)
+ *   :271-272 dV_j += p_bf16 * dO_i
+ *   :274-275 dP = dO_i . v_j                                         (fp32)
+ *   :283-285 dS = bf16(p * (dP - delta_i) * scale)
+ *   :287     dK_j += dS * q_i          :292-293  dQ_i += dS * k_j
+ * summed over the G query heads of the kv head for dK/dV.  Outputs are the
+ * fp32 accumulators (the reference casts them to bf16 at :470-472):
+ *   dq: float [B, Sq, Hq, D]; dk, dv: float [B, Skv, Hkv, D], contiguous.
+ * Strides as fgqa_oracle_prefill_bf16 (o: os, grad_o: dos); lse fp32
+ * contiguous [B, Hq, Sq] (natural log, as the forward writes it).
+ * rows (nullable) = {first, end}: dq is computed only for query rows in
+ * [first, end) (other rows left untouched); keys (nullable) likewise limits
+ * the dk/dv rows computed.  dq/dk/dv may each be NULL to skip that output.
+ */
+int fgqa_oracle_prefill_backward_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                      const uint16_t* o, const float* lse, const uint16_t* grad_o,
+                                      float scale, float* dq, float* dk, float* dv,
+                                      int batch, int sq, int skv, int hq, int hkv, int d,
+                                      const int64_t* q_strides, const int64_t* k_strides,
+                                      const int64_t* v_strides, const int64_t* o_strides,
+                                      const int64_t* grad_o_strides, int causal,
+                                      const int* rows, const int* keys, int nthreads);
+
+/*
+ * Gradient of textbook softmax attention in double precision: P recomputed
+ * from scratch (no LSE input), dV = P^T dO, dP = dO V^T,
+ * dS = P (dP - delta), dQ = scale dS K, dK = scale dS^T Q.  delta_i is
+ * sum_j P_ij dP_ij (the exact gradient) when o == NULL, else
+ * sum_x O_i[x] dO_i[x] from the given bf16 O, which restates the reference's
+ * torch backward reference examples/python/Triton/test_flash_gqa_kernel.py:97-173.
+ * Outputs double, contiguous: dq [B, Sq, Hq, D]; dk, dv [B, Skv, Hkv, D].
+ */
+int fgqa_oracle_attention_backward_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                       const uint16_t* o, const uint16_t* grad_o, double scale,
+                                       double* dq, double* dk, double* dv,
+                                       int batch, int sq, int skv, int hq, int hkv, int d,
+                                       const int64_t* q_strides, const int64_t* k_strides,
+                                       const int64_t* v_strides, const int64_t* o_strides,
+                                       const int64_t* grad_o_strides, int causal, int nthreads);
 
 /*
  * Textbook softmax attention in double precision (the mathematical answer the

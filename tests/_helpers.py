@@ -34,6 +34,39 @@ def assert_close(out, ref, what="", max_abs=MAX_ABS_TOL, mean_abs=MEAN_ABS_TOL):
     return mx, mn
 
 
+# Parity bar on bf16 gradients (backward): the same 2e-2 / 2e-3 figures taken
+# relative to max(1, |ref|), because gradients reach |g| >> 1 where a single
+# bf16 ulp already exceeds 2e-2 absolute.
+GRAD_REL_TOL = 2e-2
+GRAD_MEAN_TOL = 2e-3
+
+
+def grad_err_stats(out, ref):
+    """(max of |out-ref| / max(1,|ref|), mean|out-ref| / max(1, mean|ref|)); NaN -> inf."""
+    out = np.asarray(out, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    if out.shape != ref.shape:
+        raise AssertionError(f"shape mismatch {out.shape} vs {ref.shape}")
+    if out.size == 0:
+        return 0.0, 0.0
+    if not np.all(np.isfinite(out)) or not np.all(np.isfinite(ref)):
+        return float("inf"), float("inf")
+    d = np.abs(out - ref)
+    return float((d / np.maximum(1.0, np.abs(ref))).max()), float(d.mean() / max(1.0, float(np.abs(ref).mean())))
+
+
+def grad_within_tol(out, ref, rel=GRAD_REL_TOL, mean=GRAD_MEAN_TOL):
+    r, m = grad_err_stats(out, ref)
+    return r <= rel and m <= mean
+
+
+def assert_grad_close(out, ref, what="", rel=GRAD_REL_TOL, mean=GRAD_MEAN_TOL):
+    r, m = grad_err_stats(out, ref)
+    assert r <= rel and m <= mean, (
+        f"{what}: max rel-err {r:.3e} (tol {rel:.0e}), mean rel-err {m:.3e} (tol {mean:.0e})")
+    return r, m
+
+
 def to_torch_bf16(a_u16, device):
     """uint16 bf16 bits (numpy) -> torch bf16 tensor on `device`."""
     import torch

@@ -23,6 +23,7 @@ def test_c_abi_symbols_exported():
     hdr = open(os.path.join(ROOT, "include", "fgqa.h")).read()
     names = set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(fgqa_\w+)\s*\(", hdr, flags=re.M))
     assert names == {"fgqa_decode_workspace_bytes", "fgqa_decode_bf16", "fgqa_prefill_bf16",
+                     "fgqa_prefill_backward_workspace_bytes", "fgqa_prefill_backward_bf16",
                      "fgqa_status_string", "fgqa_version"}
     L = _lib.lib()
     syms = _exported()
@@ -34,11 +35,13 @@ def test_c_abi_symbols_exported():
 def test_cplusplus_entry_points_exported():
     syms = _exported()
     decls = []
-    for sub in ("FlashGQA/decode_flash_gqa_kernel.h", "FlashGQA/flash_gqa_forward_kernel.h"):
+    for sub in ("FlashGQA/decode_flash_gqa_kernel.h", "FlashGQA/flash_gqa_forward_kernel.h",
+                "FlashGQA/flash_gqa_backward_kernel.h"):
         hdr = open(os.path.join(ROOT, "include", "cplusplus", sub)).read()
         decls += re.findall(r"^(?:void|int)\s+(\w+)\(", hdr, flags=re.M)
     assert set(decls) == {"LaunchFlashGqaBf16Kernel", "LaunchFlashGqaBf16KernelVarlen", "FlashGqaGetLastStatus",
-                          "LaunchFlashGqaForwardBf16Kernel", "LaunchFlashGqaForwardBf16KernelStrided"}
+                          "LaunchFlashGqaForwardBf16Kernel", "LaunchFlashGqaForwardBf16KernelStrided",
+                          "LaunchFlashGqaBackwardBf16Kernel"}
     for d in decls:
         assert re.search(rf"\bT {d}\(", syms), d
     # the drop-in keeps the reference's exact parameter list
@@ -182,3 +185,80 @@ def test_python_mirror_validation_without_gpu():
         fg.launch_decode_flash_gqa_bf16_kernel(torch.zeros(2, 15, 1, 128, dtype=torch.bfloat16), k, k)
     with pytest.raises(ValueError, match="GPU"):
         fg.launch_flash_gqa_forward_bf16_kernel(qb, k, k)
+
+
+def _backward_args(**kw):
+    a = _lib.BackwardArgs()
+    B, Sq, Skv, Hq, Hkv, D = (kw.get(n, d) for n, d in
+                              (("B", 1), ("Sq", 256), ("Skv", 256), ("Hq", 16), ("Hkv", 1), ("D", 128)))
+    a.batch, a.seqlen_q, a.seqlen_kv, a.num_q_heads, a.num_kv_heads, a.head_dim = B, Sq, Skv, Hq, Hkv, D
+    a.causal = 1
+    a.scale = kw.get("scale", D ** -0.5)
+    for name in ("q_stride", "o_stride", "grad_o_stride", "grad_q_stride"):
+        getattr(a, name)[:] = [Sq * Hq * D, Hq * D, D]
+    for name in ("k_stride", "v_stride", "grad_k_stride", "grad_v_stride"):
+        getattr(a, name)[:] = [Skv * Hkv * D, Hkv * D, D]
+    for name in ("q", "k", "v", "o", "lse", "grad_o", "grad_q", "grad_k", "grad_v"):
+        setattr(a, name, kw.get(name, 4096))
+    return a
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(Hq=15, Hkv=2), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(Sq=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(scale=float("nan")), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(D=64), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(lse=None), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(grad_k=None), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(grad_v=4096 + 4), _lib.FGQA_ERR_UNSUPPORTED),
+])
+def test_backward_rejects_before_launch(kw, code):
+    assert _lib.lib().fgqa_prefill_backward_bf16(ctypes.byref(_backward_args(**kw)), None) == code
+
+
+def test_backward_empty_is_noop():
+    L = _lib.lib()
+    assert L.fgqa_prefill_backward_bf16(ctypes.byref(_backward_args(B=0, q=None)), None) == 0
+    assert L.fgqa_prefill_backward_bf16(ctypes.byref(_backward_args(Sq=0, Skv=0, q=None)), None) == 0
+    assert L.fgqa_prefill_backward_bf16(None, None) == _lib.FGQA_ERR_INVALID_ARGUMENT
+    n = ctypes.c_size_t(0)
+    assert L.fgqa_prefill_backward_workspace_bytes(None, ctypes.byref(n)) == _lib.FGQA_ERR_INVALID_ARGUMENT
+    assert L.fgqa_prefill_backward_workspace_bytes(ctypes.byref(_backward_args()), None) == \
+        _lib.FGQA_ERR_INVALID_ARGUMENT
+
+
+def test_backward_mirror_validation_without_gpu():
+    """The mirror of the reference launcher raises the reference's ValueErrors
+    (flash_gqa_backward_kernel.py:356-405) before touching a GPU."""
+    import torch
+    bf = torch.bfloat16
+    q = torch.zeros(2, 4, 64, 128, dtype=bf)
+    k = torch.zeros(2, 2, 64, 128, dtype=bf)
+    lse = torch.zeros(2, 4, 64, dtype=torch.float32)
+    f = fg.launch_flash_gqa_backward_bf16_kernel
+    with pytest.raises(ValueError, match="expects bf16 inputs and grad_o"):
+        f(q, k, k, q, lse, q.half())
+    with pytest.raises(ValueError, match="lse to be float32"):
+        f(q, k, k, q, lse.double(), q)
+    with pytest.raises(ValueError, match="3D or 4D"):
+        f(q[0, 0], k[0, 0], k[0, 0], q[0, 0], lse[0], q[0, 0])
+    with pytest.raises(ValueError, match="matching ranks"):
+        f(q, k[0], k, q, lse, q)
+    with pytest.raises(ValueError, match="K and V must share sequence length"):
+        f(q, k, k[:, :, :32], q, lse, q)
+    with pytest.raises(ValueError, match="Q, O, and grad_o must share sequence length"):
+        f(q, k, k, q[:, :, :32], lse, q)
+    with pytest.raises(ValueError, match="share number of KV heads"):
+        f(q, k, k[:, :1], q, lse, q)
+    with pytest.raises(ValueError, match="share number of query heads"):
+        f(q, k, k, q[:, :2], lse, q)
+    with pytest.raises(ValueError, match="divisible"):
+        f(q[:, :3], k, k, q[:, :3], lse[:, :3], q[:, :3])
+    with pytest.raises(ValueError, match="LSE must be 3D"):
+        f(q, k, k, q, lse[0], q)
+    with pytest.raises(ValueError, match="LSE must be 2D"):
+        f(q[0], k[0], k[0], q[0], lse, q[0])
+    with pytest.raises(ValueError, match="LSE must have shape"):
+        f(q, k, k, q, lse[:, :, :32], q)
+    with pytest.raises(ValueError, match="GPU"):
+        f(q, k, k, q, lse, q)
