@@ -12,32 +12,33 @@
 //   dK_j   += dS_ij q_i          dQ_i += dS_ij k_j               (:287-293)
 // fp32 accumulation, bf16 results (:470-472).
 //
-// Three launches on the caller's stream:
-//   bwd_prep_kernel     per query row: -lse*log2(e) and -delta*scale into the
-//                       workspace; zeroes the row's fp32 dQ accumulator (and,
-//                       when heads are split over workgroups, the fp32 dK/dV
-//                       accumulators).
-//   bwd_kv_kernel       one workgroup = one 128-key block of one KV head and a
-//                       subset of its query heads.  Wave w owns keys 32w..32w+31
-//                       of the block: their K and V rows stay in registers as
-//                       MFMA operands and their dK, dV (fp32, 32 x 128 each) are
-//                       accumulated in registers over the whole loop over
-//                       (head, 32-row query block).  Per query block:
-//                         S  = Q K^T,  dP = dO V^T     (C[q][key], Q/dO rows from LDS)
-//                         P, dS on the VALU            (P -> bf16 in place as the
-//                                                       A operand of the next two)
-//                         dV += P^T dO, dK += dS^T Q   (dO/Q read transposed, ds_read_b64_tr_b16)
-//                         dS^T -> LDS
-//                       and one step later, once every wave's dS^T is in LDS,
-//                         dQ = dS K over the 128 keys (each wave 32 of the 128
-//                         columns of D), added to the fp32 dQ accumulator with
-//                         global float atomics.
-//                       Q, dO, -lse*log2e and -delta*scale of the next block
-//                       stream into LDS (buffer_load ... lds) during the current one.
-//   bwd_convert_kernel  fp32 accumulators -> bf16 outputs (any strides).
+// The reference adds dQ (and dK, dV) with fp32 atomics.  On MI355X a float
+// atomic add sustains ~1.3 TB/s against ~10 TB/s for plain stores, and the
+// dQ updates alone are ~0.55 GB at the 4096-token, 16-head shape, so here no
+// gradient goes through an atomic: each is owned by exactly one workgroup and
+// P, dP are recomputed where needed.  Results are deterministic.
+//
+// Launches on the caller's stream:
+//   bwd_prep_kernel    per query row: -lse*log2(e) and -delta*scale.
+//   bwd_dkdv_kernel    key-major: a workgroup owns a 128-key block of one KV
+//                      head (wave w: keys 32w..32w+31, K/V rows in registers)
+//                      and loops over (query head of its subset, 32-row query
+//                      block):  S = Q K^T, dP = dO V^T (Q/dO rows from LDS),
+//                      P and dS on the VALU (in place as bf16 A operands),
+//                      dV += P^T dO, dK += dS^T Q (dO/Q read transposed,
+//                      ds_read_b64_tr_b16).  dK/dV stay in registers (fp32).
+//   bwd_dq_kernel      query-major, the forward kernel's work unit (128 query
+//                      rows: heads x positions of one KV group, one wave per
+//                      32 rows): per 64-key tile S^T = K Q^T, dP^T = V dO^T
+//                      (Q^T, dO^T in registers, K/V tiles in LDS), dS^T on the
+//                      VALU, dQ^T += K^T dS^T (K read transposed).
+//   bwd_dkdv_reduce_kernel  only when a KV head's query heads are split over
+//                      several workgroups: sums their fp32 partial dK/dV.
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
+
+#include <type_traits>
 
 #include "fgqa_device.h"
 #include "fgqa_internal.h"
@@ -64,51 +65,52 @@ struct BwdParams {
     int64_t dv_sb, dv_ss, dv_sh;
     // workspace
     float* rowstat;   // [2][B*Hq*Sq]: -lse*log2(e), then -delta*scale
-    float* dq_acc;    // [B, Hq, Sq, D] fp32
-    float* dk_acc;    // [B, Hkv, Skv, D] fp32 (heads split), else null
-    float* dv_acc;
+    float* dk_part;   // [n_hsplit][B, Hkv, Skv, D] fp32 partial sums (heads split), else null
+    float* dv_part;
     int batch, sq, skv, hq, hkv, group, causal;
+    // key-major (dK/dV) grid
     int hs;           // query heads per workgroup
     int n_hsplit;     // group / hs
     int n_kvblocks;   // ceil(skv / 128)
-    int n_streams;    // n_hsplit * hkv * batch
-    int n_qblocks;    // ceil(sq / 32)
+    int kv_streams;   // n_hsplit * hkv * batch
+    int n_qblocks32;  // ceil(sq / 32)
+    // query-major (dQ) grid, as the forward's
+    int hb;           // heads per 128-row unit
+    int n_hgroups;    // group / hb
+    int n_qunits;     // ceil(sq / (128 / hb))
+    int q_streams;    // n_hgroups * hkv * batch
     float scale;
     float scale_log2;   // scale * log2(e)
 };
 
 constexpr int kBwWaves = 4;
 constexpr int kBwThreads = kBwWaves * kWave;
-constexpr int kBwKeys = 128;                          // keys per workgroup
-constexpr int kBwRows = 32;                           // query rows per step
-constexpr int kBwRowBytes = kHeadDim * 2;             // one Q / dO / K row
-constexpr int kBwTileBytes = kBwRows * kBwRowBytes;   // 8 KB: Q or dO of one step
-constexpr int kBwDsRowBytes = kBwRows * 2;            // one dS^T row (a key, 32 query rows)
-constexpr int kBwDsBytes = kBwKeys * kBwDsRowBytes;   // 8 KB
-constexpr int kBwStatBytes = 2 * kBwRows * 4;         // -lse*log2e and -delta*scale of 32 rows
-// LDS map (bytes): Q[2] | dO[2] | dS^T[2] | stats[2].  The prologue stages
-// the workgroup's K block (128 rows, 32 KB) over Q[2] and dO[2].
-constexpr int kBwQOff = 0;
-constexpr int kBwDoOff = 2 * kBwTileBytes;
-constexpr int kBwDsOff = 4 * kBwTileBytes;
-constexpr int kBwStatOff = kBwDsOff + 2 * kBwDsBytes;
-constexpr int kBwSmemBytes = kBwStatOff + 2 * kBwStatBytes;
-static_assert(kBwKeys * kBwRowBytes <= kBwDsOff, "K staging must fit below the dS buffers");
+constexpr int kBwRowBytes = kHeadDim * 2;             // one Q / dO / K / V row
 
-// Q, dO and K rows (256 B) sit in LDS with their 16-byte chunks permuted:
+// ---- key-major kernel
+constexpr int kKvKeys = 128;                          // keys per workgroup
+constexpr int kKvRows = 32;                           // query rows per step
+constexpr int kKvTileBytes = kKvRows * kBwRowBytes;   // 8 KB: Q or dO of one step
+constexpr int kKvStatBytes = 2 * kKvRows * 4;         // -lse*log2e and -delta*scale of 32 rows
+// LDS: Q[3] | dO[3] | stats[3]
+constexpr int kKvQOff = 0;
+constexpr int kKvDoOff = 3 * kKvTileBytes;
+constexpr int kKvStatOff = 6 * kKvTileBytes;
+constexpr int kKvSmemBytes = kKvStatOff + 3 * kKvStatBytes;
+
+// ---- query-major kernel
+constexpr int kDqTile = 64;                           // keys per tile
+constexpr int kDqTileBytes = kDqTile * kBwRowBytes;   // 16 KB
+// LDS: K[2] | V[2]
+constexpr int kDqSmemBytes = 4 * kDqTileBytes;
+
+// Q, dO, K and V rows (256 B) sit in LDS with their 16-byte chunks permuted:
 // chunk c of row r goes to slot c ^ bw_swz(r).  bw_swz is a bijection on
 // r % 16 (16 consecutive rows read at the same chunk hit 16 different slots:
 // conflict-free b128 row reads) whose top two bits are r % 4 (4 consecutive
 // rows read over 4 consecutive chunks hit 4 disjoint slot groups:
 // conflict-free transposed reads).
 __device__ __forceinline__ int bw_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
-
-// dS^T rows are 64 bytes (32 query rows); chunk c (16 B) of key row r goes to
-// slot c ^ ((r >> 2) & 3) and its 8-byte halves are exchanged when r & 16,
-// which keeps both the b64 writes and the transposed reads conflict-free.
-__device__ __forceinline__ int bw_ds_addr(int r, int chunk, int half) {
-    return r * kBwDsRowBytes + ((chunk ^ ((r >> 2) & 3)) << 4) + 8 * (half ^ ((r >> 4) & 1));
-}
 
 __device__ __forceinline__ void bw_dma16(uint32_t lds_addr, uint32_t voffset, __amdgpu_buffer_rsrc_t rsrc) {
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
@@ -120,8 +122,23 @@ __device__ __forceinline__ void bw_dma4(uint32_t lds_addr, uint32_t voffset, __a
 }
 __device__ __forceinline__ void bw_wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-__device__ __forceinline__ void atomic_add_f32(float* p, float v) {
-    __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Byte offset, within a block of 16 swizzled 256-byte rows, that lane supplies
+// to a transposed read (ds_read_b64_tr_b16) so that the wave receives the
+// 32x32x16 MFMA operand  X[k = row][n = 32*cb + l32]  with the k order used
+// throughout: slots 0..3 of lane (l32, half g2) = rows 4*g2 + 0..3 (h8 = 0),
+// slots 4..7 = rows 8 + 4*g2 + 0..3 (h8 = 1).  Source lane (g2, gq, l16)
+// points at row 4*g2 + l16/4 + 8*h8, columns 32*cb + 16*gq + 4*(l16%4) .. +3.
+__device__ __forceinline__ int bw_tr_off(int lane, int cb, int h8) {
+    const int l16 = lane & 15, gq = (lane >> 4) & 1, g2 = lane >> 5;
+    const int r = 4 * g2 + (l16 >> 2) + 8 * h8;
+    const int c = 4 * cb + 2 * gq + ((l16 >> 1) & 1);
+    return r * kBwRowBytes + ((c ^ bw_swz(r)) << 4) + 8 * (l16 & 1);
+}
+
+__device__ __forceinline__ bf16x8_t tr_pair(const unsigned char* base, int off0, int off1) {
+    const bf16x4_t lo = lds_read_tr16(reinterpret_cast<const __bf16*>(base + off0));
+    const bf16x4_t hi = lds_read_tr16(reinterpret_cast<const __bf16*>(base + off1));
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
 // ---------------------------------------------------------------- prep
@@ -129,99 +146,56 @@ __device__ __forceinline__ void atomic_add_f32(float* p, float v) {
 // the LSE layout [B, Hq, Sq].
 __global__ __launch_bounds__(256) void bwd_prep_kernel(BwdParams p) {
     const int64_t rows_q = (int64_t)p.batch * p.hq * p.sq;
-    const int64_t rows_kv = (int64_t)p.batch * p.hkv * p.skv;
     const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
     const int part = threadIdx.x & 15;
-    if (row < rows_q) {
-        const int i = (int)(row % p.sq);
-        const int64_t bh = row / p.sq;
-        const int h = (int)(bh % p.hq);
-        const int b = (int)(bh / p.hq);
-        const u32x4_t ov = *reinterpret_cast<const u32x4_t*>(p.o + b * p.o_sb + i * p.o_ss + h * p.o_sh + part * 8);
-        const u32x4_t dv = *reinterpret_cast<const u32x4_t*>(p.dout + b * p.do_sb + i * p.do_ss + h * p.do_sh + part * 8);
-        const bf16x8_t o8 = as_bf16x8(ov), d8 = as_bf16x8(dv);
-        float acc = 0.f;
+    if (row >= rows_q) return;
+    const int i = (int)(row % p.sq);
+    const int64_t bh = row / p.sq;
+    const int h = (int)(bh % p.hq);
+    const int b = (int)(bh / p.hq);
+    const u32x4_t ov = *reinterpret_cast<const u32x4_t*>(p.o + b * p.o_sb + i * p.o_ss + h * p.o_sh + part * 8);
+    const u32x4_t dv = *reinterpret_cast<const u32x4_t*>(p.dout + b * p.do_sb + i * p.do_ss + h * p.do_sh + part * 8);
+    const bf16x8_t o8 = as_bf16x8(ov), d8 = as_bf16x8(dv);
+    float acc = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc += (float)o8[e] * (float)d8[e];
-        acc = xor_sum(acc, 1);
-        acc = xor_sum(acc, 2);
-        acc = xor_sum(acc, 4);
-        acc = xor_sum(acc, 8);
-        if (part == 0) {
-            p.rowstat[row] = -p.lse[row] * kLog2e;
-            p.rowstat[rows_q + row] = -acc * p.scale;
-        }
-        f32x4_t* z = reinterpret_cast<f32x4_t*>(p.dq_acc + row * kHeadDim + part * 8);
-        z[0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        z[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    }
-    if (p.dk_acc != nullptr && row < rows_kv) {
-        f32x4_t* zk = reinterpret_cast<f32x4_t*>(p.dk_acc + row * kHeadDim + part * 8);
-        f32x4_t* zv = reinterpret_cast<f32x4_t*>(p.dv_acc + row * kHeadDim + part * 8);
-        zk[0] = zk[1] = zv[0] = zv[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int e = 0; e < 8; ++e) acc += (float)o8[e] * (float)d8[e];
+    acc = xor_sum(acc, 1);
+    acc = xor_sum(acc, 2);
+    acc = xor_sum(acc, 4);
+    acc = xor_sum(acc, 8);
+    if (part == 0) {
+        p.rowstat[row] = -p.lse[row] * kLog2e;
+        p.rowstat[rows_q + row] = -acc * p.scale;
     }
 }
 
-// ---------------------------------------------------------------- convert
-__device__ __forceinline__ void bw_store_row(__bf16* dst, const float* src) {
-    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(src);
-    const f32x4_t c = *reinterpret_cast<const f32x4_t*>(src + 4);
-    bf16x8_t w;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        w[e] = (__bf16)a[e];
-        w[4 + e] = (__bf16)c[e];
-    }
-    *reinterpret_cast<bf16x8_t*>(dst) = w;
-}
-
-__global__ __launch_bounds__(256) void bwd_convert_kernel(BwdParams p) {
-    const int64_t rows_q = (int64_t)p.batch * p.hq * p.sq;
-    const int64_t rows_kv = (int64_t)p.batch * p.hkv * p.skv;
-    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-    const int part = threadIdx.x & 15;
-    if (row < rows_q) {
-        const int i = (int)(row % p.sq);
-        const int64_t bh = row / p.sq;
-        const int h = (int)(bh % p.hq);
-        const int b = (int)(bh / p.hq);
-        bw_store_row(p.dq + b * p.dq_sb + i * p.dq_ss + h * p.dq_sh + part * 8, p.dq_acc + row * kHeadDim + part * 8);
-    }
-    if (p.dk_acc != nullptr && row < rows_kv) {
-        const int j = (int)(row % p.skv);
-        const int64_t bh = row / p.skv;
-        const int kvh = (int)(bh % p.hkv);
-        const int b = (int)(bh / p.hkv);
-        bw_store_row(p.dk + b * p.dk_sb + j * p.dk_ss + kvh * p.dk_sh + part * 8, p.dk_acc + row * kHeadDim + part * 8);
-        bw_store_row(p.dv + b * p.dv_sb + j * p.dv_ss + kvh * p.dv_sh + part * 8, p.dv_acc + row * kHeadDim + part * 8);
-    }
-}
-
-// ---------------------------------------------------------------- main
-__global__ __launch_bounds__(kBwThreads, 1) void bwd_kv_kernel(BwdParams p) {
+// ---------------------------------------------------------------- dK / dV
+// Software pipelined one step ahead: step t runs
+//   phase A: S(t+1), dP(t+1) on the MFMA pipe  ||  P(t), dS(t) on the VALU
+//   phase B: dV += P(t)^T dO(t), dK += dS(t)^T Q(t) on the MFMA pipe
+// with Q/dO(t+2) streaming into the third LDS buffer meanwhile.
+__global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int l32 = lane & 31;
     const int l16 = lane & 15;
-    const int g2 = lane >> 5;          // half of the wave
-    const int gq = (lane >> 4) & 1;    // 16-lane group within the half
-    const int s4 = l16 >> 2;           // source row (within 4) of a transposed read
+    const int g2 = lane >> 5;
     const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)smem;
 
     // Block -> (key block, head subset, kv head, batch).  Key blocks in
     // ascending order: under the causal mask block 0 sees every query block,
     // so the heaviest workgroups are dispatched first.
-    const int stream = blockIdx.x % p.n_streams;
-    const int kb = blockIdx.x / p.n_streams;
+    const int stream = blockIdx.x % p.kv_streams;
+    const int kb = blockIdx.x / p.kv_streams;
     const int hsp = stream % p.n_hsplit;
     const int kvh = (stream / p.n_hsplit) % p.hkv;
     const int b = stream / (p.n_hsplit * p.hkv);
-    const int kv0 = kb * kBwKeys;
+    const int kv0 = kb * kKvKeys;
     const int h0 = kvh * p.group + hsp * p.hs;
 
-    // ---- K, V rows of this wave's keys as B operands of S = Q K^T, dP = dO V^T:
+    // K, V rows of this wave's keys as B operands of S = Q K^T, dP = dO V^T:
     // lane (key l32, half g2), k-step ks holds elements 16ks + 8g2 .. +7.
     // Keys >= skv read as zero.
     const uint32_t kss = (uint32_t)(p.k_ss * 2);
@@ -230,8 +204,7 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_kv_kernel(BwdParams p) {
         make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, (uint32_t)(p.skv - 1) * kss + kBwRowBytes);
     const __amdgpu_buffer_rsrc_t vrs =
         make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, (uint32_t)(p.skv - 1) * vss + kBwRowBytes);
-    const int key_l = 32 * wave + l32;   // this lane's key within the block
-    const int key = kv0 + key_l;
+    const int key = kv0 + 32 * wave + l32;   // this lane's key (column of S)
     bf16x8_t kop[8], vop[8];
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
@@ -239,52 +212,20 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_kv_kernel(BwdParams p) {
         vop[ks] = as_bf16x8(buf_load16(vrs, (uint32_t)key * vss + (16 * ks + 8 * g2) * 2));
     }
 
-    // ---- K block staged in LDS (rows swizzled), then read transposed as the B
-    // operand of dQ = dS K: lane (column 32*wave + l32 of D, half g2), k-step ks
-    // holds keys 16ks + 4g2 + 0..3 and 16ks + 8 + 4g2 + 0..3 (the same key order
-    // as the dS operand below).
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int r0 = 4 * (wave + 4 * i);
-        const int r = r0 + (lane >> 4);
-        bw_dma16(lds_base + r0 * kBwRowBytes, (uint32_t)(kv0 + r) * kss + ((l16 ^ bw_swz(r)) << 4), krs);
-    }
-    bw_wait_vmem();
-    __syncthreads();
-    // transposed-read offsets for 256-byte swizzled rows: source lane supplies
-    // row 4g2 + s4 (+8), chunk 4*cb + 2gq + (l16>>1 & 1), half l16 & 1
-    auto tr_off = [&](int cb, int h8) {
-        const int r = 4 * g2 + s4 + 8 * h8;
-        const int c = 4 * cb + 2 * gq + ((l16 >> 1) & 1);
-        return r * kBwRowBytes + ((c ^ bw_swz(r)) << 4) + 8 * (l16 & 1);
-    };
-    bf16x8_t ktr[8];
-    {
-        const int o0 = tr_off(wave, 0), o1 = tr_off(wave, 1);
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-            const unsigned char* base = smem + ks * 16 * kBwRowBytes;
-            const bf16x4_t lo = lds_read_tr16(reinterpret_cast<const __bf16*>(base + o0));
-            const bf16x4_t hi = lds_read_tr16(reinterpret_cast<const __bf16*>(base + o1));
-            ktr[ks] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        }
-    }
-    __syncthreads();   // K staging area is reused for Q / dO below
-
-    // ---- iteration space: head hh = h0 + t / per_head, query block qb0 + t % per_head
-    const int qb0 = p.causal ? min(kv0 / kBwRows, p.n_qblocks) : 0;
-    const int per_head = p.n_qblocks - qb0;
-    const int n_iter = (p.skv > 0) ? p.hs * per_head : 0;
+    // step t: head h0 + t / per_head, query block qb0 + t % per_head
+    const int qb0 = p.causal ? min(kv0 / kKvRows, p.n_qblocks32) : 0;
+    const int per_head = p.n_qblocks32 - qb0;
+    const int n_iter = p.hs * per_head;
 
     const uint32_t qss = (uint32_t)(p.q_ss * 2);
     const uint32_t dss = (uint32_t)(p.do_ss * 2);
     const int64_t rows_q = (int64_t)p.batch * p.hq * p.sq;
     const __amdgpu_buffer_rsrc_t srs = make_rsrc(p.rowstat, (uint32_t)(2 * rows_q * 4));
-    // Q, dO rows of step t (32 rows, wave w fetches rows 8w..8w+7 of each)
-    // and their statistics (wave 0) into buffer bi.
+    // Q, dO rows of step t (wave w fetches rows 8w..8w+7 of each) and their
+    // statistics (wave 0) into buffer bi.  Rows >= sq read as zero.
     auto issue = [&](int t, int bi) {
         const int hh = h0 + t / per_head;
-        const int q0 = (qb0 + t % per_head) * kBwRows;
+        const int q0 = (qb0 + t % per_head) * kKvRows;
         const __amdgpu_buffer_rsrc_t qrs =
             make_rsrc(p.q + b * p.q_sb + hh * p.q_sh, (uint32_t)(p.sq - 1) * qss + kBwRowBytes);
         const __amdgpu_buffer_rsrc_t drs =
@@ -294,14 +235,14 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_kv_kernel(BwdParams p) {
             const int r0 = 8 * wave + 4 * j;
             const int r = r0 + (lane >> 4);
             const int slot = (l16 ^ bw_swz(r)) << 4;
-            bw_dma16(lds_base + kBwQOff + bi * kBwTileBytes + r0 * kBwRowBytes, (uint32_t)(q0 + r) * qss + slot, qrs);
-            bw_dma16(lds_base + kBwDoOff + bi * kBwTileBytes + r0 * kBwRowBytes, (uint32_t)(q0 + r) * dss + slot, drs);
+            bw_dma16(lds_base + kKvQOff + bi * kKvTileBytes + r0 * kBwRowBytes, (uint32_t)(q0 + r) * qss + slot, qrs);
+            bw_dma16(lds_base + kKvDoOff + bi * kKvTileBytes + r0 * kBwRowBytes, (uint32_t)(q0 + r) * dss + slot, drs);
         }
         if (wave == 0) {
             const int r = q0 + l32;
             const int64_t idx = ((int64_t)b * p.hq + hh) * p.sq + r + (g2 ? rows_q : 0);
             const uint32_t off = (r < p.sq) ? (uint32_t)(idx * 4) : 0xFFFFFFF0u;   // out of range -> 0
-            bw_dma4(lds_base + kBwStatOff + bi * kBwStatBytes, off, srs);
+            bw_dma4(lds_base + kKvStatOff + bi * kKvStatBytes, off, srs);
         }
     };
 
@@ -311,151 +252,136 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_kv_kernel(BwdParams p) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) dk_acc[db][i] = dv_acc[db][i] = 0.f;
 
-    // transposed-read offsets into the Q / dO tiles (same row pattern as ktr)
+    // transposed-read offsets into the Q / dO tiles
     int trq[4][2];
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-        trq[db][0] = tr_off(db, 0);
-        trq[db][1] = tr_off(db, 1);
+        trq[db][0] = bw_tr_off(lane, db, 0);
+        trq[db][1] = bw_tr_off(lane, db, 1);
     }
-    // dS^T transposed reads for dQ: rows 4g2 + s4 (+8) of each 16-key step,
-    // query chunk 2gq + (l16>>1 & 1), half l16 & 1 (the half swap of bw_ds_addr
-    // depends on bit 4 of the key, i.e. on the parity of the step)
-    int trs[2][2];
-#pragma unroll
-    for (int par = 0; par < 2; ++par)
-#pragma unroll
-        for (int h8 = 0; h8 < 2; ++h8)
-            trs[par][h8] = bw_ds_addr(16 * par + 4 * g2 + s4 + 8 * h8, 2 * gq + ((l16 >> 1) & 1), l16 & 1) -
-                           16 * par * kBwDsRowBytes;
+    // b128 row-read offsets of the A operands of S and dP (row l32, chunk 2ks + g2)
+    int roff[8];
     const int fl = bw_swz(l32);
-
-    // dQ of the step held in dS^T buffer bi, for rows q0.. of head hh: wave w
-    // computes columns 32w..32w+31 of D over all 128 keys and adds them to the
-    // fp32 accumulator.
-    auto dq_step = [&](int bi, int hh, int q0) {
-        const unsigned char* dsl = smem + kBwDsOff + bi * kBwDsBytes;
-        f32x16_t acc;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-            const unsigned char* base = dsl + ks * 16 * kBwDsRowBytes;
-            const bf16x4_t lo = lds_read_tr16(reinterpret_cast<const __bf16*>(base + trs[ks & 1][0]));
-            const bf16x4_t hi = lds_read_tr16(reinterpret_cast<const __bf16*>(base + trs[ks & 1][1]));
-            acc = mfma32(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), ktr[ks], acc);
-        }
-        // C[q][d]: lane (d = 32w + l32, half g2), register 4i + r -> row 8i + 4g2 + r
-        float* dst = p.dq_acc + (((int64_t)b * p.hq + hh) * p.sq + q0) * kHeadDim + 32 * wave + l32;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int q = 8 * i + 4 * g2 + r;
-                if (q0 + q < p.sq) atomic_add_f32(dst + q * kHeadDim, acc[4 * i + r]);
-            }
-    };
-
+    for (int ks = 0; ks < 8; ++ks) roff[ks] = l32 * kBwRowBytes + (((2 * ks + g2) ^ fl) << 4);
     const float c2 = p.scale_log2;
     const float scale = p.scale;
-    // this lane's key is seen by query rows [lo_row, sq)
-    const int lo_row = (key >= p.skv) ? 0x7fffffff : (p.causal ? key : 0);
-
-    if (n_iter > 0) issue(0, 0);
-    bw_wait_vmem();
-    __syncthreads();
-
-    int prev_h = 0, prev_q0 = 0;
-    for (int t = 0; t < n_iter; ++t) {
-        const int bi = t & 1;
-        const int hh = h0 + t / per_head;
-        const int q0 = (qb0 + t % per_head) * kBwRows;
-        if (t + 1 < n_iter) issue(t + 1, bi ^ 1);
-        if (t > 0) dq_step(bi ^ 1, prev_h, prev_q0);
-
-        // S = Q K^T and dP = dO V^T: C[q][key], lane (key l32, half g2),
-        // register 4i + r <-> query row 8i + 4g2 + r
-        const unsigned char* ql = smem + kBwQOff + bi * kBwTileBytes;
-        const unsigned char* dl = smem + kBwDoOff + bi * kBwTileBytes;
-        f32x16_t s, dp;
+    // S = Q K^T and dP = dO V^T of the step in buffer bi: C[q][key], lane
+    // (key l32, half g2), register 4i + r <-> query row 8i + 4g2 + r
+    auto sdp = [&](f32x16_t& s, f32x16_t& dp, auto bi_c) {
+        constexpr int bi = decltype(bi_c)::value;
+        const unsigned char* ql = smem + kKvQOff + bi * kKvTileBytes;
+        const unsigned char* dl = smem + kKvDoOff + bi * kKvTileBytes;
 #pragma unroll
         for (int i = 0; i < 16; ++i) s[i] = dp[i] = 0.f;
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
-            const int off = l32 * kBwRowBytes + (((2 * ks + g2) ^ fl) << 4);
-            s = mfma32(*reinterpret_cast<const bf16x8_t*>(ql + off), kop[ks], s);
-            dp = mfma32(*reinterpret_cast<const bf16x8_t*>(dl + off), vop[ks], dp);
+            s = mfma32(*reinterpret_cast<const bf16x8_t*>(ql + roff[ks]), kop[ks], s);
+            dp = mfma32(*reinterpret_cast<const bf16x8_t*>(dl + roff[ks]), vop[ks], dp);
         }
-
-        // P = exp2(S*scale*log2e - lse*log2e) (0 where masked), dS = P (dP - delta) scale
-        const float* st = reinterpret_cast<const float*>(smem + kBwStatOff + bi * kBwStatBytes);
-        bf16x8_t pop[2], dsop[2];
-        float dsv[16];
+    };
+    // P = exp2(S*scale*log2e - lse*log2e), dS = P (dP - delta) scale, both as
+    // bf16 A operands (k-step ks = registers 8ks .. 8ks+7).  Element (i, r) is
+    // query row q0 + 8i + 4g2 + r; it is masked (P = 0) when 8i + r < m, with
+    // m = key - q0 - 4g2 under the causal mask.  Rows >= sq need no mask: their
+    // dO rows and -delta*scale read as zero, so P.dO and dS vanish; keys >= skv
+    // only reach their own dK/dV rows, which are never stored.
+    bf16x8_t pop[2], dsop[2];
+    auto softmax = [&](const f32x16_t& s, const f32x16_t& dp, auto bi_c, int m) {
+        constexpr int bi = decltype(bi_c)::value;
+        const float* st = reinterpret_cast<const float*>(smem + kKvStatOff + bi * kKvStatBytes);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const f32x4_t nl = *reinterpret_cast<const f32x4_t*>(st + 8 * i + 4 * g2);
-            const f32x4_t nd = *reinterpret_cast<const f32x4_t*>(st + kBwRows + 8 * i + 4 * g2);
+            const f32x4_t nd = *reinterpret_cast<const f32x4_t*>(st + kKvRows + 8 * i + 4 * g2);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int q = q0 + 8 * i + 4 * g2 + r;
-                const bool valid = (q >= lo_row) && (q < p.sq);
                 float pv = fast_exp2(__builtin_fmaf(s[4 * i + r], c2, nl[r]));
-                pv = valid ? pv : 0.f;
+                pv = (8 * i + r >= m) ? pv : 0.f;
                 const float ds = pv * __builtin_fmaf(dp[4 * i + r], scale, nd[r]);
                 pop[i >> 1][(i & 1) * 4 + r] = (__bf16)pv;
                 dsop[i >> 1][(i & 1) * 4 + r] = (__bf16)ds;
-                dsv[4 * i + r] = ds;
             }
         }
-
-        // dV += P^T dO, dK += dS^T Q: C[key][d], 4 column tiles of D; the
-        // k-step ks takes query rows 16ks + 4g2 + 0..3 and 16ks + 8 + 4g2 + 0..3
-        // (registers 8ks .. 8ks+7 of S / dP), read transposed from the tiles.
+    };
+    // dV += P^T dO, dK += dS^T Q: C[key][d], 4 column tiles of D; k-step ks
+    // takes query rows 16ks + 4g2 + 0..3 and 16ks + 8 + 4g2 + 0..3, read
+    // transposed from the tiles.
+    auto dkdv = [&](auto bi_c) {
+        constexpr int bi = decltype(bi_c)::value;
+        const unsigned char* ql = smem + kKvQOff + bi * kKvTileBytes;
+        const unsigned char* dl = smem + kKvDoOff + bi * kKvTileBytes;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
                 const int rb = ks * 16 * kBwRowBytes;
-                const bf16x4_t dlo = lds_read_tr16(reinterpret_cast<const __bf16*>(dl + rb + trq[db][0]));
-                const bf16x4_t dhi = lds_read_tr16(reinterpret_cast<const __bf16*>(dl + rb + trq[db][1]));
-                dv_acc[db] = mfma32(pop[ks], __builtin_shufflevector(dlo, dhi, 0, 1, 2, 3, 4, 5, 6, 7), dv_acc[db]);
-                const bf16x4_t qlo = lds_read_tr16(reinterpret_cast<const __bf16*>(ql + rb + trq[db][0]));
-                const bf16x4_t qhi = lds_read_tr16(reinterpret_cast<const __bf16*>(ql + rb + trq[db][1]));
-                dk_acc[db] = mfma32(dsop[ks], __builtin_shufflevector(qlo, qhi, 0, 1, 2, 3, 4, 5, 6, 7), dk_acc[db]);
+                dv_acc[db] = mfma32(pop[ks], tr_pair(dl + rb, trq[db][0], trq[db][1]), dv_acc[db]);
+                dk_acc[db] = mfma32(dsop[ks], tr_pair(ql + rb, trq[db][0], trq[db][1]), dk_acc[db]);
             }
+    };
 
-        // dS^T rows of this wave's keys: query rows 8i + 4g2 .. +3 = chunk i, half g2
-        unsigned char* dsl = smem + kBwDsOff + bi * kBwDsBytes;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            bf16x4_t w;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) w[r] = (__bf16)dsv[4 * i + r];
-            *reinterpret_cast<bf16x4_t*>(dsl + bw_ds_addr(key_l, i, g2)) = w;
-        }
+    // Triple-buffered Q/dO: step t reads buffers t%3 (dV/dK) and (t+1)%3
+    // (S/dP of the next step) while step t+2 lands in (t+2)%3, which step t-1
+    // finished with before the barrier that ended it.  The loop runs a
+    // multiple of 3 steps so that every buffer offset is a constant; steps
+    // past n_iter are fully masked (m = 64) and read buffers that hold zeros
+    // or an earlier step's rows, so they add exact zeros.  No branch touches
+    // the accumulators.
+    {
+        // zero the buffers first: a padded step may read one never loaded
+        const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+        for (int off = tid * 16; off < kKvSmemBytes; off += kBwThreads * 16)
+            *reinterpret_cast<f32x4_t*>(smem + off) = z;
+    }
+    __syncthreads();
+    if (n_iter > 0) issue(0, 0);
+    if (n_iter > 1) issue(1, 1);
+    bw_wait_vmem();
+    __syncthreads();
 
-        prev_h = hh;
-        prev_q0 = q0;
+    using C0 = std::integral_constant<int, 0>;
+    using C1 = std::integral_constant<int, 1>;
+    using C2 = std::integral_constant<int, 2>;
+    // step t: sc/dpc hold S/dP(t), sn/dpn receive S/dP(t+1); buffers BC = t%3,
+    // BN = (t+1)%3, BF = (t+2)%3
+    auto step = [&](f32x16_t& sc, f32x16_t& dpc, f32x16_t& sn, f32x16_t& dpn, int t, auto bc, auto bn, auto bf) {
+        if (t + 2 < n_iter) issue(t + 2, decltype(bf)::value);
+        const int q0 = (qb0 + t % per_head) * kKvRows;
+        const int m = (t < n_iter) ? (p.causal ? key - q0 - 4 * g2 : -64) : 64;
+        // phase A: S/dP(t+1) on the MFMA pipe while P/dS(t) run on the VALU
+        sdp(sn, dpn, bn);
+        softmax(sc, dpc, bc, m);
+        // phase B: dV/dK(t)
+        dkdv(bc);
         bw_wait_vmem();
         __syncthreads();
+    };
+    f32x16_t sa, dpa, sb, dpb, sx, dpx;
+    sdp(sa, dpa, C0{});
+    for (int t = 0; t < n_iter; t += 3) {
+        step(sa, dpa, sb, dpb, t, C0{}, C1{}, C2{});
+        step(sb, dpb, sx, dpx, t + 1, C1{}, C2{}, C0{});
+        step(sx, dpx, sa, dpa, t + 2, C2{}, C0{}, C1{});
     }
-    if (n_iter > 0) dq_step((n_iter - 1) & 1, prev_h, prev_q0);
 
-    // ---- dK, dV of this wave's keys: C[key][d], lane (d = 32db + l32, half g2),
-    // register 4i + r <-> key 32w + 8i + 4g2 + r
+    // dK, dV of this wave's keys: C[key][d], lane (d = 32db + l32, half g2),
+    // register 4i + r <-> key 32w + 8i + 4g2 + r.  One workgroup per (key
+    // block, head subset): bf16 straight out, or an fp32 partial per subset.
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int j = kv0 + 32 * wave + 8 * i + 4 * g2 + r;
             if (j >= p.skv) continue;
-            if (p.dk_acc != nullptr) {
-                float* dkr = p.dk_acc + (((int64_t)b * p.hkv + kvh) * p.skv + j) * kHeadDim + l32;
-                float* dvr = p.dv_acc + (((int64_t)b * p.hkv + kvh) * p.skv + j) * kHeadDim + l32;
+            if (p.dk_part != nullptr) {
+                const int64_t row = (((int64_t)hsp * p.batch + b) * p.hkv + kvh) * p.skv + j;
+                float* dkr = p.dk_part + row * kHeadDim + l32;
+                float* dvr = p.dv_part + row * kHeadDim + l32;
 #pragma unroll
                 for (int db = 0; db < 4; ++db) {
-                    atomic_add_f32(dkr + 32 * db, dk_acc[db][4 * i + r]);
-                    atomic_add_f32(dvr + 32 * db, dv_acc[db][4 * i + r]);
+                    dkr[32 * db] = dk_acc[db][4 * i + r];
+                    dvr[32 * db] = dv_acc[db][4 * i + r];
                 }
             } else {
                 __bf16* dkr = p.dk + b * p.dk_sb + (int64_t)j * p.dk_ss + kvh * p.dk_sh + l32;
@@ -469,11 +395,198 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_kv_kernel(BwdParams p) {
         }
 }
 
+// Sum of the n_hsplit fp32 partials -> bf16 dK, dV.  16 lanes per key row.
+__global__ __launch_bounds__(256) void bwd_dkdv_reduce_kernel(BwdParams p) {
+    const int64_t rows_kv = (int64_t)p.batch * p.hkv * p.skv;
+    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int part = threadIdx.x & 15;
+    if (row >= rows_kv) return;
+    f32x4_t k0 = {0.f, 0.f, 0.f, 0.f}, k1 = k0, v0 = k0, v1 = k0;
+    for (int s = 0; s < p.n_hsplit; ++s) {
+        const int64_t off = (s * rows_kv + row) * kHeadDim + part * 8;
+        const f32x4_t* pk = reinterpret_cast<const f32x4_t*>(p.dk_part + off);
+        const f32x4_t* pv = reinterpret_cast<const f32x4_t*>(p.dv_part + off);
+        k0 += pk[0];
+        k1 += pk[1];
+        v0 += pv[0];
+        v1 += pv[1];
+    }
+    const int j = (int)(row % p.skv);
+    const int64_t bh = row / p.skv;
+    const int kvh = (int)(bh % p.hkv);
+    const int b = (int)(bh / p.hkv);
+    bf16x8_t wk, wv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        wk[e] = (__bf16)k0[e];
+        wk[4 + e] = (__bf16)k1[e];
+        wv[e] = (__bf16)v0[e];
+        wv[4 + e] = (__bf16)v1[e];
+    }
+    *reinterpret_cast<bf16x8_t*>(p.dk + b * p.dk_sb + j * p.dk_ss + kvh * p.dk_sh + part * 8) = wk;
+    *reinterpret_cast<bf16x8_t*>(p.dv + b * p.dv_sb + j * p.dv_ss + kvh * p.dv_sh + part * 8) = wv;
+}
+
+// ---------------------------------------------------------------- dQ
+// Unit = 128 query rows: hb heads of one KV group x (128 / hb) positions,
+// wave w -> head (w % hb), positions 32 * (w / hb) .. +31 of the unit, as the
+// forward kernel.  Units are ranked heaviest first under the causal mask.
+__global__ __launch_bounds__(kBwThreads, 2) void bwd_dq_kernel(BwdParams p) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int l32 = lane & 31;
+    const int l16 = lane & 15;
+    const int g2 = lane >> 5;
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)smem;
+
+    const int stream = blockIdx.x % p.q_streams;
+    const int rank = blockIdx.x / p.q_streams;
+    const int qb = p.causal ? p.n_qunits - 1 - rank : rank;
+    const int hg = stream % p.n_hgroups;
+    const int kvh = (stream / p.n_hgroups) % p.hkv;
+    const int b = stream / (p.n_hgroups * p.hkv);
+    const int qrows = 128 / p.hb;
+    const int q_wg0 = qb * qrows;
+    const int h = kvh * p.group + hg * p.hb + (wave % p.hb);
+    const int q0w = q_wg0 + (wave / p.hb) * 32;
+    const int qrow = q0w + l32;
+
+    // Q^T and dO^T as B operands: lane holds row qrow, elements 16kk + 8g2 .. +7;
+    // rows >= sq read as zero.
+    const uint32_t qss = (uint32_t)(p.q_ss * 2);
+    const uint32_t dss = (uint32_t)(p.do_ss * 2);
+    const __amdgpu_buffer_rsrc_t qrs =
+        make_rsrc(p.q + b * p.q_sb + h * p.q_sh, (uint32_t)(p.sq - 1) * qss + kBwRowBytes);
+    const __amdgpu_buffer_rsrc_t drs =
+        make_rsrc(p.dout + b * p.do_sb + h * p.do_sh, (uint32_t)(p.sq - 1) * dss + kBwRowBytes);
+    bf16x8_t qop[8], doop[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+        qop[kk] = as_bf16x8(buf_load16(qrs, (uint32_t)qrow * qss + (16 * kk + 8 * g2) * 2));
+        doop[kk] = as_bf16x8(buf_load16(drs, (uint32_t)qrow * dss + (16 * kk + 8 * g2) * 2));
+    }
+    const int64_t rows_q = (int64_t)p.batch * p.hq * p.sq;
+    const int64_t ridx = ((int64_t)b * p.hq + h) * p.sq + qrow;
+    const float nl = (qrow < p.sq) ? p.rowstat[ridx] : 0.f;
+    const float nd = (qrow < p.sq) ? p.rowstat[rows_q + ridx] : 0.f;
+
+    int kv_end = p.skv;
+    if (p.causal) kv_end = min(kv_end, min(q_wg0 + qrows, p.sq));
+    const int n_tiles = (kv_end + kDqTile - 1) / kDqTile;
+    // this lane's row sees keys [0, row_lim)
+    const int row_lim = (qrow >= p.sq) ? 0 : (p.causal ? min(p.skv, qrow + 1) : p.skv);
+
+    const uint32_t kss = (uint32_t)(p.k_ss * 2);
+    const uint32_t vss = (uint32_t)(p.v_ss * 2);
+    const __amdgpu_buffer_rsrc_t krs =
+        make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, (uint32_t)(p.skv - 1) * kss + kBwRowBytes);
+    const __amdgpu_buffer_rsrc_t vrs =
+        make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, (uint32_t)(p.skv - 1) * vss + kBwRowBytes);
+    // K, V tile j into buffer bi: rows r = 4*(wave + 4i) + lane/16; keys >= skv read as zero
+    auto issue = [&](int j, int bi) {
+        const int t0 = j * kDqTile;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r0 = 4 * (wave + 4 * i);
+            const int r = r0 + (lane >> 4);
+            const int slot = (l16 ^ bw_swz(r)) << 4;
+            bw_dma16(lds_base + bi * kDqTileBytes + r0 * kBwRowBytes, (uint32_t)(t0 + r) * kss + slot, krs);
+            bw_dma16(lds_base + (2 + bi) * kDqTileBytes + r0 * kBwRowBytes, (uint32_t)(t0 + r) * vss + slot, vrs);
+        }
+    };
+
+    f32x16_t dq_acc[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dq_acc[db][i] = 0.f;
+    int trk[4][2];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+        trk[db][0] = bw_tr_off(lane, db, 0);
+        trk[db][1] = bw_tr_off(lane, db, 1);
+    }
+    const int fl = bw_swz(l32);
+    const float c2 = p.scale_log2;
+    const float scale = p.scale;
+
+    if (n_tiles > 0) issue(0, 0);
+    bw_wait_vmem();
+    __syncthreads();
+
+    for (int j = 0; j < n_tiles; ++j) {
+        const int bi = j & 1;
+        if (j + 1 < n_tiles) issue(j + 1, bi ^ 1);
+        const unsigned char* kl = smem + bi * kDqTileBytes;
+        const unsigned char* vl = smem + (2 + bi) * kDqTileBytes;
+
+        // S^T = K Q^T, dP^T = V dO^T: C[key][q], lane (q = l32, half g2),
+        // block tb register i <-> key 32tb + 8(i/4) + 4g2 + i%4 of the tile
+        f32x16_t s[2], dp[2];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[tb][i] = dp[tb][i] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) {
+                const int off = (32 * tb + l32) * kBwRowBytes + (((2 * kk + g2) ^ fl) << 4);
+                s[tb] = mfma32(*reinterpret_cast<const bf16x8_t*>(kl + off), qop[kk], s[tb]);
+                dp[tb] = mfma32(*reinterpret_cast<const bf16x8_t*>(vl + off), doop[kk], dp[tb]);
+            }
+
+        // dS^T = P^T (dP^T - delta) scale as the B operand of dQ^T += K^T dS^T:
+        // block kb = 2tb + kh holds registers 8kh .. 8kh+7 of S^T block tb,
+        // i.e. keys 16kb + 4g2 + 0..3 and 16kb + 8 + 4g2 + 0..3.
+        bf16x8_t dsop[4];
+        const int key0 = j * kDqTile;
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int i = kh * 8 + e;
+                    const int key = key0 + 32 * tb + 8 * (i >> 2) + 4 * g2 + (i & 3);
+                    float pv = fast_exp2(__builtin_fmaf(s[tb][i], c2, nl));
+                    pv = (key < row_lim) ? pv : 0.f;
+                    dsop[tb * 2 + kh][e] = (__bf16)(pv * __builtin_fmaf(dp[tb][i], scale, nd));
+                }
+
+        // dQ^T[d][q] += sum over keys of K^T[d][key] dS^T[key][q], 4 column tiles of D
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+                dq_acc[db] = mfma32(tr_pair(kl + 16 * kb * kBwRowBytes, trk[db][0], trk[db][1]), dsop[kb], dq_acc[db]);
+
+        bw_wait_vmem();
+        __syncthreads();
+    }
+
+    // dQ^T: lane (q = l32, half g2), block db register i <-> d = 32db + 8(i/4) + 4g2 + i%4
+    if (qrow < p.sq) {
+        __bf16* dst = p.dq + b * p.dq_sb + (int64_t)qrow * p.dq_ss + h * p.dq_sh;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                bf16x4_t w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w[e] = (__bf16)dq_acc[db][i4 * 4 + e];
+                *reinterpret_cast<bf16x4_t*>(dst + db * 32 + i4 * 8 + g2 * 4) = w;
+            }
+    }
+}
+
 namespace {
 
 struct BwdPlan {
     int n_hsplit;
-    size_t stat_bytes, dq_bytes, dkv_bytes, ws_bytes;
+    size_t stat_bytes, part_bytes, ws_bytes;
 };
 
 size_t round256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -491,6 +604,8 @@ int validate_backward(const fgqa_prefill_backward_args* a) {
         for (int i = 0; i < 3; ++i)
             if (s[i] < 0) return FGQA_ERR_INVALID_ARGUMENT;
     if (a->head_dim != kHeadDim) return FGQA_ERR_UNSUPPORTED;
+    // query rows past sq must read as zero (rows may not overlap)
+    if (a->q_stride[1] < kHeadDim || a->grad_o_stride[1] < kHeadDim) return FGQA_ERR_UNSUPPORTED;
     const int64_t lim = (int64_t)1 << 31;
     if ((int64_t)(a->seqlen_q + 128) * a->q_stride[1] * 2 >= lim ||
         (int64_t)(a->seqlen_q + 128) * a->grad_o_stride[1] * 2 >= lim ||
@@ -517,14 +632,15 @@ int validate_backward_pointers(const fgqa_prefill_backward_args* a) {
     return FGQA_OK;
 }
 
-// Heads per workgroup: all G query heads of a KV head (dK/dV written once,
-// straight from registers) unless that leaves fewer than 2 workgroups per CU,
-// in which case the heads are split over workgroups and dK/dV go through fp32
-// accumulators.  FGQA_BWD_HSPLIT=<n> forces n (a divisor of G) for tests.
+// Query heads per dK/dV workgroup: all G query heads of a KV head (dK/dV
+// written once, straight from registers) unless that leaves fewer than 2
+// workgroups per CU; then the heads are split over workgroups, each writing
+// an fp32 partial that bwd_dkdv_reduce_kernel sums.  FGQA_BWD_HSPLIT=<n>
+// forces n (a divisor of G) for tests.
 BwdPlan plan_backward(const fgqa_prefill_backward_args* a, int cus) {
     BwdPlan pl;
     const int group = a->num_q_heads / a->num_kv_heads;
-    const int64_t base = ceil_div(a->seqlen_kv, kBwKeys) * (int64_t)a->num_kv_heads * a->batch;
+    const int64_t base = ceil_div(a->seqlen_kv, kKvKeys) * (int64_t)a->num_kv_heads * a->batch;
     pl.n_hsplit = group;
     for (int d = 1; d <= group; ++d)
         if (group % d == 0 && base * d >= 2 * (int64_t)cus) {
@@ -538,10 +654,18 @@ BwdPlan plan_backward(const fgqa_prefill_backward_args* a, int cus) {
     const size_t rows_q = (size_t)a->batch * a->num_q_heads * a->seqlen_q;
     const size_t rows_kv = (size_t)a->batch * a->num_kv_heads * a->seqlen_kv;
     pl.stat_bytes = round256(2 * rows_q * sizeof(float));
-    pl.dq_bytes = round256(rows_q * kHeadDim * sizeof(float));
-    pl.dkv_bytes = pl.n_hsplit > 1 ? round256(rows_kv * kHeadDim * sizeof(float)) : 0;
-    pl.ws_bytes = pl.stat_bytes + pl.dq_bytes + 2 * pl.dkv_bytes;
+    pl.part_bytes = pl.n_hsplit > 1 ? round256((size_t)pl.n_hsplit * rows_kv * kHeadDim * sizeof(float)) : 0;
+    pl.ws_bytes = pl.stat_bytes + 2 * pl.part_bytes;
     return pl;
+}
+
+int set_smem(const void* fn, int bytes, bool* done) {
+    if (!*done) {
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess)
+            return FGQA_ERR_HIP;
+        *done = true;
+    }
+    return FGQA_OK;
 }
 
 }  // namespace
@@ -598,9 +722,8 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     p.dk_sb = a->grad_k_stride[0]; p.dk_ss = a->grad_k_stride[1]; p.dk_sh = a->grad_k_stride[2];
     p.dv_sb = a->grad_v_stride[0]; p.dv_ss = a->grad_v_stride[1]; p.dv_sh = a->grad_v_stride[2];
     p.rowstat = reinterpret_cast<float*>(ws);
-    p.dq_acc = reinterpret_cast<float*>(ws + pl.stat_bytes);
-    p.dk_acc = pl.n_hsplit > 1 ? reinterpret_cast<float*>(ws + pl.stat_bytes + pl.dq_bytes) : nullptr;
-    p.dv_acc = pl.n_hsplit > 1 ? reinterpret_cast<float*>(ws + pl.stat_bytes + pl.dq_bytes + pl.dkv_bytes) : nullptr;
+    p.dk_part = pl.n_hsplit > 1 ? reinterpret_cast<float*>(ws + pl.stat_bytes) : nullptr;
+    p.dv_part = pl.n_hsplit > 1 ? reinterpret_cast<float*>(ws + pl.stat_bytes + pl.part_bytes) : nullptr;
     p.batch = a->batch;
     p.sq = a->seqlen_q;
     p.skv = a->seqlen_kv;
@@ -610,31 +733,36 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     p.causal = a->causal ? 1 : 0;
     p.n_hsplit = pl.n_hsplit;
     p.hs = p.group / pl.n_hsplit;
-    p.n_kvblocks = (int)ceil_div(p.skv, kBwKeys);
-    p.n_streams = pl.n_hsplit * p.hkv * p.batch;
-    p.n_qblocks = (int)ceil_div(p.sq, kBwRows);
+    p.n_kvblocks = (int)ceil_div(p.skv, kKvKeys);
+    p.kv_streams = pl.n_hsplit * p.hkv * p.batch;
+    p.n_qblocks32 = (int)ceil_div(p.sq, kKvRows);
+    p.hb = (p.group % 4 == 0) ? 4 : (p.group % 2 == 0) ? 2 : 1;
+    p.n_hgroups = p.group / p.hb;
+    p.n_qunits = (int)ceil_div(p.sq, 128 / p.hb);
+    p.q_streams = p.n_hgroups * p.hkv * p.batch;
     p.scale = a->scale;
     p.scale_log2 = a->scale * kLog2e;
 
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const int64_t rows_q = (int64_t)p.batch * p.hq * p.sq;
     const int64_t rows_kv = (int64_t)p.batch * p.hkv * p.skv;
-    const int64_t rows = (pl.n_hsplit > 1 && rows_kv > rows_q) ? rows_kv : rows_q;
-    const int64_t units = (int64_t)p.n_kvblocks * p.n_streams;
-    if (ceil_div(rows, 16) >= ((int64_t)1 << 31) || units >= ((int64_t)1 << 31)) return FGQA_ERR_UNSUPPORTED;
+    const int64_t kv_units = (int64_t)p.n_kvblocks * p.kv_streams;
+    const int64_t q_units = (int64_t)p.n_qunits * p.q_streams;
+    if (ceil_div(rows_q, 16) >= ((int64_t)1 << 31) || ceil_div(rows_kv, 16) >= ((int64_t)1 << 31) ||
+        kv_units >= ((int64_t)1 << 31) || q_units >= ((int64_t)1 << 31))
+        return FGQA_ERR_UNSUPPORTED;
 
-    if (rows > 0) hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)ceil_div(rows, 16)), dim3(256), 0, s, p);
-    if (units > 0) {
-        static bool smem_set = false;
-        if (!smem_set) {
-            if (hipFuncSetAttribute(reinterpret_cast<const void*>(bwd_kv_kernel),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, kBwSmemBytes) != hipSuccess)
-                return FGQA_ERR_HIP;
-            smem_set = true;
-        }
-        hipLaunchKernelGGL(bwd_kv_kernel, dim3((unsigned)units), dim3(kBwThreads), kBwSmemBytes, s, p);
-    }
-    if (rows > 0) hipLaunchKernelGGL(bwd_convert_kernel, dim3((unsigned)ceil_div(rows, 16)), dim3(256), 0, s, p);
+    static bool smem_kv = false, smem_q = false;
+    if ((st = set_smem(reinterpret_cast<const void*>(bwd_dkdv_kernel), kKvSmemBytes, &smem_kv)) != FGQA_OK) return st;
+    if ((st = set_smem(reinterpret_cast<const void*>(bwd_dq_kernel), kDqSmemBytes, &smem_q)) != FGQA_OK) return st;
+
+    if (rows_q > 0) hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)ceil_div(rows_q, 16)), dim3(256), 0, s, p);
+    if (kv_units > 0)
+        hipLaunchKernelGGL(bwd_dkdv_kernel, dim3((unsigned)kv_units), dim3(kBwThreads), kKvSmemBytes, s, p);
+    if (q_units > 0)
+        hipLaunchKernelGGL(bwd_dq_kernel, dim3((unsigned)q_units), dim3(kBwThreads), kDqSmemBytes, s, p);
+    if (pl.n_hsplit > 1 && rows_kv > 0)
+        hipLaunchKernelGGL(bwd_dkdv_reduce_kernel, dim3((unsigned)ceil_div(rows_kv, 16)), dim3(256), 0, s, p);
     if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
     return FGQA_OK;
 }
