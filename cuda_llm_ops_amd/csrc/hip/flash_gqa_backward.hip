@@ -430,23 +430,23 @@ __global__ __launch_bounds__(256) void bwd_dkdv_reduce_kernel(BwdParams p) {
 // ---------------------------------------------------------------- dQ
 // Unit = 128 query rows: hb heads of one KV group x (128 / hb) positions,
 // wave w -> head (w % hb), positions 32 * (w / hb) .. +31 of the unit, as the
-// forward kernel.  Units are ranked heaviest first under the causal mask.
-__global__ __launch_bounds__(kBwThreads, 2) void bwd_dq_kernel(BwdParams p) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+// forward kernel.  With kGroups == 2 two groups of 4 waves take the two halves
+// of the unit's key range and add their dQ through LDS at the end (dQ is a
+// plain sum over keys: P comes from the final LSE).
+template <int kGroups>
+__device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem_all, int qb, int hg, int kvh,
+                                        int b) {
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
-    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int wave_wg = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int grp = wave_wg / kBwWaves;
+    const int wave = wave_wg % kBwWaves;
+    unsigned char* smem = smem_all + grp * kDqSmemBytes;
     const int l32 = lane & 31;
     const int l16 = lane & 15;
     const int g2 = lane >> 5;
     const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)smem;
 
-    const int stream = blockIdx.x % p.q_streams;
-    const int rank = blockIdx.x / p.q_streams;
-    const int qb = p.causal ? p.n_qunits - 1 - rank : rank;
-    const int hg = stream % p.n_hgroups;
-    const int kvh = (stream / p.n_hgroups) % p.hkv;
-    const int b = stream / (p.n_hgroups * p.hkv);
     const int qrows = 128 / p.hb;
     const int q_wg0 = qb * qrows;
     const int h = kvh * p.group + hg * p.hb + (wave % p.hb);
@@ -474,9 +474,13 @@ __global__ __launch_bounds__(kBwThreads, 2) void bwd_dq_kernel(BwdParams p) {
 
     int kv_end = p.skv;
     if (p.causal) kv_end = min(kv_end, min(q_wg0 + qrows, p.sq));
-    const int n_tiles = (kv_end + kDqTile - 1) / kDqTile;
-    // this lane's row sees keys [0, row_lim)
-    const int row_lim = (qrow >= p.sq) ? 0 : (p.causal ? min(p.skv, qrow + 1) : p.skv);
+    const int unit_tiles = (kv_end + kDqTile - 1) / kDqTile;
+    const int n_tiles = kGroups == 1 ? unit_tiles : (unit_tiles + 1) / 2;   // same for both groups
+    const int t_first = grp * n_tiles;
+    // keys this lane's row may use: below kv_hi (end of the group's range) and,
+    // under the causal mask, at most qrow
+    const int kv_hi = min(kv_end, (t_first + n_tiles) * kDqTile);
+    const int row_lim = (qrow >= p.sq) ? 0 : min(kv_hi, p.causal ? qrow + 1 : p.skv);
 
     const uint32_t kss = (uint32_t)(p.k_ss * 2);
     const uint32_t vss = (uint32_t)(p.v_ss * 2);
@@ -484,9 +488,10 @@ __global__ __launch_bounds__(kBwThreads, 2) void bwd_dq_kernel(BwdParams p) {
         make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, (uint32_t)(p.skv - 1) * kss + kBwRowBytes);
     const __amdgpu_buffer_rsrc_t vrs =
         make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, (uint32_t)(p.skv - 1) * vss + kBwRowBytes);
-    // K, V tile j into buffer bi: rows r = 4*(wave + 4i) + lane/16; keys >= skv read as zero
+    // K, V tile j (of the group) into buffer bi: rows r = 4*(wave + 4i) + lane/16;
+    // keys >= skv read as zero
     auto issue = [&](int j, int bi) {
-        const int t0 = j * kDqTile;
+        const int t0 = (t_first + j) * kDqTile;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r0 = 4 * (wave + 4 * i);
@@ -508,22 +513,21 @@ __global__ __launch_bounds__(kBwThreads, 2) void bwd_dq_kernel(BwdParams p) {
         trk[db][0] = bw_tr_off(lane, db, 0);
         trk[db][1] = bw_tr_off(lane, db, 1);
     }
+    int roff[8];
     const int fl = bw_swz(l32);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) roff[kk] = l32 * kBwRowBytes + (((2 * kk + g2) ^ fl) << 4);
     const float c2 = p.scale_log2;
     const float scale = p.scale;
 
-    if (n_tiles > 0) issue(0, 0);
-    bw_wait_vmem();
-    __syncthreads();
-
-    for (int j = 0; j < n_tiles; ++j) {
-        const int bi = j & 1;
-        if (j + 1 < n_tiles) issue(j + 1, bi ^ 1);
+    // One tile from buffer BI.  Element (tb, i) of S^T/dP^T is key
+    // 32tb + 8(i/4) + 4g2 + i%4 of the tile; it is used when 32tb + 8(i/4) + i%4 < m,
+    // m = row_lim - (tile start) - 4g2 (m <= 0 masks the whole tile).
+    auto tile = [&](auto bi_c, int m) {
+        constexpr int bi = decltype(bi_c)::value;
         const unsigned char* kl = smem + bi * kDqTileBytes;
         const unsigned char* vl = smem + (2 + bi) * kDqTileBytes;
-
-        // S^T = K Q^T, dP^T = V dO^T: C[key][q], lane (q = l32, half g2),
-        // block tb register i <-> key 32tb + 8(i/4) + 4g2 + i%4 of the tile
+        // S^T = K Q^T, dP^T = V dO^T: C[key][q], lane (q = l32, half g2)
         f32x16_t s[2], dp[2];
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
@@ -533,16 +537,14 @@ __global__ __launch_bounds__(kBwThreads, 2) void bwd_dq_kernel(BwdParams p) {
         for (int kk = 0; kk < 8; ++kk)
 #pragma unroll
             for (int tb = 0; tb < 2; ++tb) {
-                const int off = (32 * tb + l32) * kBwRowBytes + (((2 * kk + g2) ^ fl) << 4);
+                const int off = tb * 32 * kBwRowBytes + roff[kk];
                 s[tb] = mfma32(*reinterpret_cast<const bf16x8_t*>(kl + off), qop[kk], s[tb]);
                 dp[tb] = mfma32(*reinterpret_cast<const bf16x8_t*>(vl + off), doop[kk], dp[tb]);
             }
-
         // dS^T = P^T (dP^T - delta) scale as the B operand of dQ^T += K^T dS^T:
         // block kb = 2tb + kh holds registers 8kh .. 8kh+7 of S^T block tb,
         // i.e. keys 16kb + 4g2 + 0..3 and 16kb + 8 + 4g2 + 0..3.
         bf16x8_t dsop[4];
-        const int key0 = j * kDqTile;
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
@@ -550,21 +552,59 @@ __global__ __launch_bounds__(kBwThreads, 2) void bwd_dq_kernel(BwdParams p) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int i = kh * 8 + e;
-                    const int key = key0 + 32 * tb + 8 * (i >> 2) + 4 * g2 + (i & 3);
                     float pv = fast_exp2(__builtin_fmaf(s[tb][i], c2, nl));
-                    pv = (key < row_lim) ? pv : 0.f;
+                    pv = (32 * tb + 8 * (i >> 2) + (i & 3) < m) ? pv : 0.f;
                     dsop[tb * 2 + kh][e] = (__bf16)(pv * __builtin_fmaf(dp[tb][i], scale, nd));
                 }
-
         // dQ^T[d][q] += sum over keys of K^T[d][key] dS^T[key][q], 4 column tiles of D
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
             for (int db = 0; db < 4; ++db)
                 dq_acc[db] = mfma32(tr_pair(kl + 16 * kb * kBwRowBytes, trk[db][0], trk[db][1]), dsop[kb], dq_acc[db]);
+    };
 
+    // Double-buffered K/V, two tiles per trip so that buffer offsets are
+    // constants; a trip's second tile past n_tiles is fully masked (m <= 0)
+    // and reads a buffer that holds zeros or the previous tile.
+    {
+        const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+        for (int off = (tid % kBwThreads) * 16; off < kDqSmemBytes; off += kBwThreads * 16)
+            *reinterpret_cast<f32x4_t*>(smem + off) = z;
+    }
+    __syncthreads();
+    if (n_tiles > 0) issue(0, 0);
+    bw_wait_vmem();
+    __syncthreads();
+    using C0 = std::integral_constant<int, 0>;
+    using C1 = std::integral_constant<int, 1>;
+    for (int j = 0; j < n_tiles; j += 2) {
+        if (j + 1 < n_tiles) issue(j + 1, 1);
+        tile(C0{}, row_lim - (t_first + j) * kDqTile - 4 * g2);
         bw_wait_vmem();
         __syncthreads();
+        if (j + 2 < n_tiles) issue(j + 2, 0);
+        tile(C1{}, (j + 1 < n_tiles) ? row_lim - (t_first + j + 1) * kDqTile - 4 * g2 : 0);
+        bw_wait_vmem();
+        __syncthreads();
+    }
+
+    if constexpr (kGroups == 2) {
+        // group 1 hands its dQ^T to group 0 through the (idle) tile buffers:
+        // [wave][value][lane] floats
+        float* mg = reinterpret_cast<float*>(smem_all) + wave * 64 * kWave + lane;
+        if (grp == 1) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) mg[(db * 16 + i) * kWave] = dq_acc[db][i];
+        }
+        __syncthreads();
+        if (grp == 1) return;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) dq_acc[db][i] += mg[(db * 16 + i) * kWave];
     }
 
     // dQ^T: lane (q = l32, half g2), block db register i <-> d = 32db + 8(i/4) + 4g2 + i%4
@@ -580,6 +620,32 @@ __global__ __launch_bounds__(kBwThreads, 2) void bwd_dq_kernel(BwdParams p) {
                 *reinterpret_cast<bf16x4_t*>(dst + db * 32 + i4 * 8 + g2 * 4) = w;
             }
     }
+}
+
+// Block -> unit, ranked heaviest first under the causal mask (the key range
+// grows with the query block); the stream (head group, kv head, batch) is the
+// fastest index.
+__device__ __forceinline__ void dq_block_unit(const BwdParams& p, int* qb, int* hg, int* kvh, int* b) {
+    const int stream = blockIdx.x % p.q_streams;
+    const int rank = blockIdx.x / p.q_streams;
+    *qb = p.causal ? p.n_qunits - 1 - rank : rank;
+    *hg = stream % p.n_hgroups;
+    *kvh = (stream / p.n_hgroups) % p.hkv;
+    *b = stream / (p.n_hgroups * p.hkv);
+}
+
+__global__ __launch_bounds__(kBwThreads, 2) void bwd_dq_kernel(BwdParams p) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    int qb, hg, kvh, b;
+    dq_block_unit(p, &qb, &hg, &kvh, &b);
+    dq_unit<1>(p, smem, qb, hg, kvh, b);
+}
+
+__global__ __launch_bounds__(2 * kBwThreads, 1) void bwd_dq_split_kernel(BwdParams p) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    int qb, hg, kvh, b;
+    dq_block_unit(p, &qb, &hg, &kvh, &b);
+    dq_unit<2>(p, smem, qb, hg, kvh, b);
 }
 
 namespace {
@@ -752,14 +818,22 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
         kv_units >= ((int64_t)1 << 31) || q_units >= ((int64_t)1 << 31))
         return FGQA_ERR_UNSUPPORTED;
 
-    static bool smem_kv = false, smem_q = false;
+    // Few dQ units (fewer than 4 per CU): split each unit's key range over two
+    // wave groups, as the forward does.  FGQA_BWD_DQ_SPLIT=0/1 forces the choice.
+    bool dq_split = q_units < 4 * (int64_t)cus;
+    if (const char* e = getenv("FGQA_BWD_DQ_SPLIT")) dq_split = e[0] == '1';
+    static bool smem_kv = false, smem_q = false, smem_q2 = false;
     if ((st = set_smem(reinterpret_cast<const void*>(bwd_dkdv_kernel), kKvSmemBytes, &smem_kv)) != FGQA_OK) return st;
     if ((st = set_smem(reinterpret_cast<const void*>(bwd_dq_kernel), kDqSmemBytes, &smem_q)) != FGQA_OK) return st;
+    if ((st = set_smem(reinterpret_cast<const void*>(bwd_dq_split_kernel), 2 * kDqSmemBytes, &smem_q2)) != FGQA_OK)
+        return st;
 
     if (rows_q > 0) hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)ceil_div(rows_q, 16)), dim3(256), 0, s, p);
     if (kv_units > 0)
         hipLaunchKernelGGL(bwd_dkdv_kernel, dim3((unsigned)kv_units), dim3(kBwThreads), kKvSmemBytes, s, p);
-    if (q_units > 0)
+    if (q_units > 0 && dq_split)
+        hipLaunchKernelGGL(bwd_dq_split_kernel, dim3((unsigned)q_units), dim3(2 * kBwThreads), 2 * kDqSmemBytes, s, p);
+    else if (q_units > 0)
         hipLaunchKernelGGL(bwd_dq_kernel, dim3((unsigned)q_units), dim3(kBwThreads), kDqSmemBytes, s, p);
     if (pl.n_hsplit > 1 && rows_kv > 0)
         hipLaunchKernelGGL(bwd_dkdv_reduce_kernel, dim3((unsigned)ceil_div(rows_kv, 16)), dim3(256), 0, s, p);

@@ -92,6 +92,20 @@ def test_backward_head_split_modes(cuda, monkeypatch, hsplit):
     _check(_gpu_backward(cuda, q, k, v, o, lse, do), refs, f"hsplit={hsplit}")
 
 
+@pytest.mark.parametrize("split", ["0", "1"])
+@pytest.mark.parametrize("B,Sq,Skv,Hq,Hkv,causal", [
+    (1, 320, 320, 16, 1, True), (2, 200, 200, 4, 2, True), (1, 130, 250, 2, 1, False), (1, 64, 64, 3, 1, True)])
+def test_backward_dq_whole_and_split_kernels(cuda, monkeypatch, split, B, Sq, Skv, Hq, Hkv, causal):
+    """The dQ kernel over a unit's whole key range, or split over two wave
+    groups whose dQ is summed through LDS."""
+    monkeypatch.setenv("FGQA_BWD_DQ_SPLIT", split)
+    what = f"dq split={split} B{B} Sq{Sq} Skv{Skv} Hq{Hq} Hkv{Hkv} causal{causal}"
+    print(what, flush=True)
+    q, k, v, o, lse, do = _inputs(860 + Sq, B, Sq, Skv, Hq, Hkv, causal=causal)
+    refs = oracle.prefill_backward(q, k, v, o, lse, do, SCALE, causal=causal)
+    _check(_gpu_backward(cuda, q, k, v, o, lse, do, causal=causal), refs, what)
+
+
 @pytest.mark.parametrize("scale", [0.2, -0.05])
 def test_backward_scale_values(cuda, scale):
     print(f"backward scale={scale}", flush=True)
