@@ -5,8 +5,8 @@ S=4096, Hq=128, Hkv=8, D=128, bf16 in/out, fp32 accumulation, inputs resident
 in HBM.  One "step" = one decode over the whole batch.  Prints ONE JSON line:
 value = decode KV-read throughput in GB/s (decimal), with the roofline of the
 decode kernel against 8 TB/s HBM, the causal prefill of BASELINE config 4
-(TFLOPS against 2.5 PFLOP/s bf16 dense MFMA) beside it, and the CPU oracle
-timed on a bounded sample of the same decode workload.
+and its backward (TFLOPS against 2.5 PFLOP/s bf16 dense MFMA) beside it, and
+the CPU oracle timed on a bounded sample of the same decode workload.
 
     python bench.py [--steps K] [--warmup W] [--split-tokens N] [--no-cpu] [--all]
 
@@ -197,6 +197,39 @@ def hbm_copy(steps, warmup, dev, nbytes=1 << 30):
                 read_plus_write_GBs=2 * nbytes / (avg * 1e-3) / 1e9)
 
 
+def bench_backward(cfg_id, steps, warmup, dev):
+    """Prefill backward (dQ, dK, dV) of a causal forward at a BASELINE prefill
+    shape; one step = every launch of fgqa_prefill_backward_bf16."""
+    import torch
+
+    import cuda_llm_ops_amd as fg
+    cfg = PREFILL_CONFIGS[cfg_id]
+    B, S, Hq, Hkv = cfg["B"], cfg["S"], cfg["Hq"], cfg["Hkv"]
+    q = _normal((B, S, Hq, 128), 4, cfg["sigma"], dev)
+    k = _normal((B, S, Hkv, 128), 5, cfg["sigma"], dev)
+    v = _normal((B, S, Hkv, 128), 6, cfg["sigma"], dev)
+    do = _normal((B, S, Hq, 128), 7, 1.0, dev)
+    out, lse = fg.flash_gqa_forward_bshd(q, k, v, SCALE, causal=True)
+    n_ws = fg.backward_workspace_bytes(B, S, S, Hq, Hkv)
+    ws = torch.empty(max(n_ws, 256), dtype=torch.uint8, device=dev)
+    step = fg.prepare_backward(q, k, v, out, lse, do, SCALE, causal=True, workspace=ws)
+
+    total_ms, per = _time_calls(step, steps, warmup)
+    # the reference's count, QK + dP + dQ + dK + dV causal-halved
+    # (test_flash_gqa_kernel.py:344-363); the kernels execute 7 such GEMMs
+    # (S and dP are recomputed by the dQ pass), 7/5 of it
+    flops = B * Hq * 2 * S * S * (3 * 128 + 2 * 128) // 2
+    avg = sum(per) / len(per)
+    tflops = flops / (avg * 1e-3) / 1e12
+    return dict(config=f"causal prefill backward B={B} S={S} Hq={Hq} Hkv={Hkv} D=128 (BASELINE config {cfg_id} shape)",
+                us_avg=round(avg * 1e3, 2), us_median=round(per[len(per) // 2] * 1e3, 2),
+                us_min=round(per[0] * 1e3, 2),
+                roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
+                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                          "kernel": "bwd_prep + bwd_dkdv + bwd_dq(_split) + bwd_dkdv_reduce (whole step)",
+                          "algorithmic_flops": flops, "executed_mfma_flops": flops * 7 // 5})
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -205,10 +238,12 @@ def main():
     ap.add_argument("--split-tokens", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-backward", action="store_true")
     ap.add_argument("--all", action="store_true", help="also report configs 1, 3 and 5 (to stderr)")
-    ap.add_argument("--mode", choices=["bench", "decode", "prefill", "copy"], default="bench",
+    ap.add_argument("--mode", choices=["bench", "decode", "prefill", "backward", "copy"], default="bench",
                     help="decode/prefill/copy: run only that workload (for profiling) and print its timing")
-    ap.add_argument("--config", type=int, default=0, help="with --mode decode/prefill: BASELINE config id")
+    ap.add_argument("--config", type=int, default=0,
+                    help="with --mode decode/prefill/backward: BASELINE config id")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (--gpus must be 1)", file=sys.stderr)
@@ -229,6 +264,10 @@ def main():
         return
     if args.mode == "prefill":
         print(json.dumps({"mode": "prefill", **bench_prefill(args.config or 4, args.steps, args.warmup, dev)}),
+              flush=True)
+        return
+    if args.mode == "backward":
+        print(json.dumps({"mode": "backward", **bench_backward(args.config or 4, args.steps, args.warmup, dev)}),
               flush=True)
         return
 
@@ -261,6 +300,8 @@ def main():
     }
     if not args.no_prefill:
         line["prefill"] = bench_prefill(4, args.steps, args.warmup, dev)
+    if not args.no_backward:
+        line["backward"] = bench_backward(4, max(5, args.steps // 2), max(2, args.warmup // 2), dev)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_decode(res)
     if args.all:
