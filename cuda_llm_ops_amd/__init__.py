@@ -1,4 +1,4 @@
-"""MI355X-native flash grouped-query attention (decode, causal prefill and its backward).
+"""MI355X-native flash grouped-query attention (decode incl. paged/fp8 KV caches, causal prefill and its backward).
 
 The kernels live in libfgqa.so (HIP, gfx950); ``flash_gqa`` is the Python host
 interface over its C ABI (include/fgqa.h).
@@ -7,14 +7,17 @@ from ._lib import FgqaError, LIB_PATH, lib, status_string  # noqa: F401
 from .flash_gqa import (  # noqa: F401
     backward_workspace_bytes,
     decode_flash_gqa_bshd,
+    decode_flash_gqa_paged,
     decode_workspace_bytes,
     flash_gqa_backward_bshd,
     flash_gqa_forward_bshd,
     launch_decode_flash_gqa_bf16_kernel,
     launch_flash_gqa_backward_bf16_kernel,
     launch_flash_gqa_forward_bf16_kernel,
+    paged_decode_workspace_bytes,
     prepare_backward,
     prepare_decode,
+    prepare_decode_paged,
     prepare_prefill,
     PreparedLaunch,
 )

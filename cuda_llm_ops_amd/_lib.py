@@ -70,6 +70,42 @@ class PrefillArgs(ctypes.Structure):
     ]
 
 
+FGQA_KV_BF16 = 0
+FGQA_KV_FP8_E4M3 = 1
+
+
+class PagedDecodeArgs(ctypes.Structure):
+    """Mirror of ``fgqa_decode_paged_args`` (include/fgqa.h)."""
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k_cache", ctypes.c_void_p),
+        ("v_cache", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("block_table", ctypes.c_void_p),
+        ("seqlens", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("max_seqlen", ctypes.c_int32),
+        ("num_q_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+        ("num_pages", ctypes.c_int32),
+        ("kv_dtype", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("k_scale", ctypes.c_float),
+        ("v_scale", ctypes.c_float),
+        ("q_stride", _I64x2),
+        ("o_stride", _I64x2),
+        ("k_stride", _I64x3),
+        ("v_stride", _I64x3),
+        ("block_table_stride", ctypes.c_int64),
+        ("split_tokens", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 class BackwardArgs(ctypes.Structure):
     """Mirror of ``fgqa_prefill_backward_args`` (include/fgqa.h)."""
     _fields_ = [
@@ -127,6 +163,11 @@ def lib() -> ctypes.CDLL:
         L.fgqa_decode_bf16.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.c_void_p]
         L.fgqa_prefill_bf16.restype = ctypes.c_int
         L.fgqa_prefill_bf16.argtypes = [ctypes.POINTER(PrefillArgs), ctypes.c_void_p]
+        L.fgqa_decode_paged_workspace_bytes.restype = ctypes.c_int
+        L.fgqa_decode_paged_workspace_bytes.argtypes = [ctypes.POINTER(PagedDecodeArgs),
+                                                        ctypes.POINTER(ctypes.c_size_t)]
+        L.fgqa_decode_paged.restype = ctypes.c_int
+        L.fgqa_decode_paged.argtypes = [ctypes.POINTER(PagedDecodeArgs), ctypes.c_void_p]
         L.fgqa_prefill_backward_workspace_bytes.restype = ctypes.c_int
         L.fgqa_prefill_backward_workspace_bytes.argtypes = [ctypes.POINTER(BackwardArgs),
                                                             ctypes.POINTER(ctypes.c_size_t)]

@@ -18,6 +18,13 @@
 //     workgroup writes the normalised bf16 output directly, otherwise it
 //     writes an fp32 partial (O, max, sum) to the workspace.
 //   pass 2 (decode_combine_kernel): log-sum-exp merge of the partials.
+//
+// Paged KV cache (fgqa_decode_paged): the same kernels read K/V rows through a
+// block table (token t of sequence b lives in page block_table[b][t / page],
+// slot t % page), in bf16 or in OCP fp8 e4m3 with per-tensor scales.  fp8 rows
+// are widened to bf16 exactly (v_cvt_scalef32_pk_bf16_fp8, scale 1) as they are
+// staged in LDS; the K scale is folded into the softmax scale and the V scale
+// into the output, so the arithmetic after staging is the bf16 path's.
 #include <math.h>
 
 #include "fgqa_device.h"
@@ -42,7 +49,29 @@ struct DecodeParams {
     int batch, max_seqlen, hq, hkv, group;
     int nsplit, chunk;
     float scale_log2;
+    // paged KV: k/v are the page caches, strides {page, slot, head} in elements
+    // of the cache type; page of token t = block_table[b * bt_stride + (t >> page_shift)]
+    const int32_t* block_table;
+    int64_t bt_stride;
+    int page_shift;
+    int num_pages;      // page indices are clamped to [0, num_pages)
+    float v_scale;      // multiplies O (the fp8 V scale; 1 otherwise)
 };
+
+// Cache layouts the decode items read.
+enum DecKv { kKvContig = 0, kKvPagedBf16 = 1, kKvPagedFp8 = 2 };
+
+// 16 OCP fp8 e4m3 values -> 16 bf16 (exact: every e4m3 value is a bf16 value).
+__device__ __forceinline__ void fp8x16_to_bf16(u32x4_t in, u32x4_t* lo, u32x4_t* hi) {
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        w[2 * i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(in[i], 1.0f, false));
+        w[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(in[i], 1.0f, true));
+    }
+    *lo = u32x4_t{w[0], w[1], w[2], w[3]};
+    *hi = u32x4_t{w[4], w[5], w[6], w[7]};
+}
 
 constexpr int kDecThreads = 256;
 constexpr int kDecWaves = kDecThreads / kWave;
@@ -60,6 +89,7 @@ __device__ __forceinline__ int clamp_len(const DecodeParams& p, int b) {
 }
 
 // One (split, kv head, batch) item of pass 1.
+template <int kKv>
 __device__ __forceinline__ void dec_item(const DecodeParams& p, unsigned char* smem, int split, int kvh, int b) {
     const int len = clamp_len(p, b);
     const int t_begin = split * p.chunk;
@@ -100,14 +130,6 @@ __device__ __forceinline__ void dec_item(const DecodeParams& p, unsigned char* s
         }
     }
 
-    // Buffer resources end at the split's last valid token: later tokens read as zero.
-    const uint32_t kss = (uint32_t)(p.k_ss * 2);
-    const uint32_t vss = (uint32_t)(p.v_ss * 2);
-    const __amdgpu_buffer_rsrc_t krs =
-        make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, (uint32_t)(t_end - 1) * kss + kHeadDim * 2);
-    const __amdgpu_buffer_rsrc_t vrs =
-        make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, (uint32_t)(t_end - 1) * vss + kHeadDim * 2);
-
     float m_run = -INFINITY;
     float l_run = 0.f;  // this lane's share of the rowsum of head l16
     f32x4_t oacc[8];
@@ -115,29 +137,95 @@ __device__ __forceinline__ void dec_item(const DecodeParams& p, unsigned char* s
     for (int db = 0; db < 8; ++db) oacc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     const int n_steps = (t_end - t_begin + kDecStep - 1) / kDecStep;
-    // One step = 32 token rows of K and of V.  Load r (0..7) of a lane covers
-    // row 4*r + g4, 16-byte chunk l16: each quarter-wave reads one whole
-    // 256-byte row, the coalesced pattern (K and V alike).
-    u32x4_t kreg[8];
-    u32x4_t vreg[8];
-    auto load_step = [&](int st) {
-        const uint32_t t0 = (uint32_t)(t_begin + st * kDecStep);
+    // One step = 32 token rows of K and of V.  bf16: load r (0..7) of a lane
+    // covers row 4*r + g4, 16-byte chunk l16, so each quarter-wave reads one
+    // whole 256-byte row (the coalesced pattern).  fp8: rows are 128 bytes;
+    // load r (0..3) covers row 8*r + lane/8, chunk lane%8.
+    constexpr int kRows = (kKv == kKvPagedFp8) ? 4 : 8;
+    const int fp8_row = lane >> 3;
+    const int fp8_chunk = lane & 7;
+    auto row_of = [&](int r) { return (kKv == kKvPagedFp8) ? 8 * r + fp8_row : 4 * r + g4; };
+    u32x4_t kreg[kRows];
+    u32x4_t vreg[kRows];
+
+    // Contiguous cache: buffer resources end at the split's last valid token,
+    // so later tokens read as zero.
+    const uint32_t kss = (uint32_t)(p.k_ss * 2);
+    const uint32_t vss = (uint32_t)(p.v_ss * 2);
+    __amdgpu_buffer_rsrc_t krs, vrs;
+    if constexpr (kKv == kKvContig) {
+        krs = make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, (uint32_t)(t_end - 1) * kss + kHeadDim * 2);
+        vrs = make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, (uint32_t)(t_end - 1) * vss + kHeadDim * 2);
+    }
+    // Paged cache: each row's page comes from the block table one step ahead
+    // of its load.  Tokens past the split's end reuse its last token (their
+    // scores are masked; the row only has to be finite).
+    constexpr int kElemBytes = (kKv == kKvPagedFp8) ? 1 : 2;
+    const unsigned char* kbase = reinterpret_cast<const unsigned char*>(p.k) + kvh * p.k_sh * kElemBytes;
+    const unsigned char* vbase = reinterpret_cast<const unsigned char*>(p.v) + kvh * p.v_sh * kElemBytes;
+    const int32_t* bt = p.block_table + (int64_t)b * p.bt_stride;
+    const int pmask = (1 << p.page_shift) - 1;
+    int pg[kRows];
+    auto fetch_pages = [&](int s) {
+        if constexpr (kKv != kKvContig) {
 #pragma unroll
-        for (int r = 0; r < 8; ++r) kreg[r] = buf_load16_nt(krs, (t0 + r * 4 + g4) * kss + l16 * 16);
+            for (int r = 0; r < kRows; ++r) {
+                const int tok = min(t_begin + s * kDecStep + row_of(r), t_end - 1);
+                pg[r] = min(max(bt[tok >> p.page_shift], 0), p.num_pages - 1);
+            }
+        }
+    };
+    auto load_step = [&](int s) {
+        const int t0 = t_begin + s * kDecStep;
+        if constexpr (kKv == kKvContig) {
 #pragma unroll
-        for (int r = 0; r < 8; ++r) vreg[r] = buf_load16_nt(vrs, (t0 + r * 4 + g4) * vss + l16 * 16);
+            for (int r = 0; r < 8; ++r) kreg[r] = buf_load16_nt(krs, (uint32_t)(t0 + r * 4 + g4) * kss + l16 * 16);
+#pragma unroll
+            for (int r = 0; r < 8; ++r) vreg[r] = buf_load16_nt(vrs, (uint32_t)(t0 + r * 4 + g4) * vss + l16 * 16);
+        } else {
+            const int cb = (kKv == kKvPagedFp8) ? fp8_chunk * 16 : l16 * 16;
+#pragma unroll
+            for (int r = 0; r < kRows; ++r) {
+                const int slot = min(t0 + row_of(r), t_end - 1) & pmask;
+                const int64_t ko = ((int64_t)pg[r] * p.k_sb + (int64_t)slot * p.k_ss) * kElemBytes + cb;
+                const int64_t vo = ((int64_t)pg[r] * p.v_sb + (int64_t)slot * p.v_ss) * kElemBytes + cb;
+                kreg[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(kbase + ko));
+                vreg[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(vbase + vo));
+            }
+        }
     };
 
     int st = wave;
-    if (st < n_steps) load_step(st);
+    if (st < n_steps) {
+        fetch_pages(st);
+        load_step(st);
+    }
+    if (st + kDecWaves < n_steps) fetch_pages(st + kDecWaves);
     for (; st < n_steps; st += kDecWaves) {
-        // Stage this step's rows, then put the next step's loads in flight.
+        // Stage this step's rows (fp8 widened to bf16), then put the next
+        // step's loads and the page lookups of the step after in flight.
+        if constexpr (kKv == kKvPagedFp8) {
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            *reinterpret_cast<u32x4_t*>(kl + (r * 4 + g4) * kDecRowStride + l16 * 8) = kreg[r];
-            *reinterpret_cast<u32x4_t*>(vl + (r * 4 + g4) * kDecRowStride + l16 * 8) = vreg[r];
+            for (int r = 0; r < kRows; ++r) {
+                u32x4_t lo, hi;
+                __bf16* kd = kl + row_of(r) * kDecRowStride + fp8_chunk * 16;
+                __bf16* vd = vl + row_of(r) * kDecRowStride + fp8_chunk * 16;
+                fp8x16_to_bf16(kreg[r], &lo, &hi);
+                *reinterpret_cast<u32x4_t*>(kd) = lo;
+                *reinterpret_cast<u32x4_t*>(kd + 8) = hi;
+                fp8x16_to_bf16(vreg[r], &lo, &hi);
+                *reinterpret_cast<u32x4_t*>(vd) = lo;
+                *reinterpret_cast<u32x4_t*>(vd + 8) = hi;
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                *reinterpret_cast<u32x4_t*>(kl + (r * 4 + g4) * kDecRowStride + l16 * 8) = kreg[r];
+                *reinterpret_cast<u32x4_t*>(vl + (r * 4 + g4) * kDecRowStride + l16 * 8) = vreg[r];
+            }
         }
         if (st + kDecWaves < n_steps) load_step(st + kDecWaves);
+        if (st + 2 * kDecWaves < n_steps) fetch_pages(st + 2 * kDecWaves);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -241,7 +329,7 @@ __device__ __forceinline__ void dec_item(const DecodeParams& p, unsigned char* s
     }
     const int qh = kvh * p.group + h;
     if (p.nsplit == 1) {
-        const float inv = 1.f / L;
+        const float inv = p.v_scale / L;
         bf16x8_t out;
 #pragma unroll
         for (int j = 0; j < 8; ++j) out[j] = (__bf16)(acc[j] * inv);
@@ -250,8 +338,9 @@ __device__ __forceinline__ void dec_item(const DecodeParams& p, unsigned char* s
     } else {
         const int64_t slot = (((int64_t)b * p.hkv + kvh) * p.nsplit + split) * p.group + h;
         float* po = p.part_o + slot * kHeadDim + d0;
-        *reinterpret_cast<f32x4_t*>(po) = f32x4_t{acc[0], acc[1], acc[2], acc[3]};
-        *reinterpret_cast<f32x4_t*>(po + 4) = f32x4_t{acc[4], acc[5], acc[6], acc[7]};
+        const float vs = p.v_scale;
+        *reinterpret_cast<f32x4_t*>(po) = f32x4_t{acc[0] * vs, acc[1] * vs, acc[2] * vs, acc[3] * vs};
+        *reinterpret_cast<f32x4_t*>(po + 4) = f32x4_t{acc[4] * vs, acc[5] * vs, acc[6] * vs, acc[7] * vs};
         if ((tid & 15) == 0) {
             p.part_ml[slot * 2 + 0] = M;
             p.part_ml[slot * 2 + 1] = L;
@@ -262,7 +351,7 @@ __device__ __forceinline__ void dec_item(const DecodeParams& p, unsigned char* s
 // Pass 1 over the full (split, kv head, batch) grid.
 __global__ __launch_bounds__(kDecThreads) void decode_split_kernel(DecodeParams p) {
     __shared__ __attribute__((aligned(16))) unsigned char smem[kDecSmemBytes];
-    dec_item(p, smem, blockIdx.x, blockIdx.y, blockIdx.z);
+    dec_item<kKvContig>(p, smem, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // Ragged batches: build the work list of non-empty splits, full-length splits
@@ -350,13 +439,14 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(DecodeParams 
 
 // Pass 1 over the ragged work list: a fixed grid walks the entries, each
 // entry once per kv head (kv head fastest, so heads of one split run together).
+template <int kKv>
 __global__ __launch_bounds__(kDecThreads) void decode_list_kernel(DecodeParams p) {
     __shared__ __attribute__((aligned(16))) unsigned char smem[kDecSmemBytes];
     const int total = p.work[0] * p.hkv;
     for (int item = blockIdx.x; item < total; item += gridDim.x) {
         const int e = p.work[1 + item / p.hkv];
         __syncthreads();   // the previous item's merge buffers alias the staging area
-        dec_item(p, smem, e & 0xffff, item % p.hkv, e >> 16);
+        dec_item<kKv>(p, smem, e & 0xffff, item % p.hkv, e >> 16);
     }
 }
 
@@ -457,11 +547,17 @@ int validate_decode_pointers(const fgqa_decode_args* a) {
     return FGQA_OK;
 }
 
-int plan_decode(const fgqa_decode_args* a, DecodePlan* plan) {
+// Split plan from the sizes alone (shared by the contiguous and paged entries).
+struct DecodeShape {
+    int batch, max_seqlen, num_q_heads, num_kv_heads, split_tokens;
+    bool ragged;   // per-sequence lengths are given
+};
+
+int plan_decode(const DecodeShape* a, DecodePlan* plan) {
     const int64_t S = a->max_seqlen > 0 ? a->max_seqlen : 1;
     // Ragged batches get a work list of their non-empty splits (built on the
     // device from the lengths), so no workgroup is spent on padding.
-    plan->list = a->seqlens != nullptr && a->batch < (1 << 15);
+    plan->list = a->ragged && a->batch < (1 << 15);
     int64_t chunk;
     if (a->split_tokens > 0) {
         chunk = ceil_div(a->split_tokens, kStepRound) * kStepRound;
@@ -504,12 +600,20 @@ int plan_decode(const fgqa_decode_args* a, DecodePlan* plan) {
 
 using namespace fgqa;
 
+namespace {
+DecodeShape shape_of(const fgqa_decode_args* a) {
+    return DecodeShape{a->batch, a->max_seqlen, a->num_q_heads, a->num_kv_heads, a->split_tokens,
+                       a->seqlens != nullptr};
+}
+}  // namespace
+
 extern "C" int fgqa_decode_workspace_bytes(const fgqa_decode_args* a, size_t* bytes) {
     if (bytes == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
     int st = validate_decode(a);
     if (st != FGQA_OK) return st;
     DecodePlan plan;
-    st = plan_decode(a, &plan);
+    const DecodeShape shape = shape_of(a);
+    st = plan_decode(&shape, &plan);
     if (st != FGQA_OK) return st;
     *bytes = plan.ws_bytes;
     return FGQA_OK;
@@ -522,10 +626,16 @@ extern "C" int fgqa_decode_bf16(const fgqa_decode_args* a, void* stream) {
     if (st != FGQA_OK) return st;
     if (a->batch == 0) return FGQA_OK;
     DecodePlan plan;
-    st = plan_decode(a, &plan);
+    const DecodeShape shape = shape_of(a);
+    st = plan_decode(&shape, &plan);
     if (st != FGQA_OK) return st;
 
     DecodeParams p;
+    p.block_table = nullptr;
+    p.bt_stride = 0;
+    p.page_shift = 0;
+    p.num_pages = 0;
+    p.v_scale = 1.f;
     p.q = static_cast<const __bf16*>(a->q);
     p.k = static_cast<const __bf16*>(a->k);
     p.v = static_cast<const __bf16*>(a->v);
@@ -584,11 +694,160 @@ extern "C" int fgqa_decode_bf16(const fgqa_decode_args* a, void* stream) {
         const int64_t max_items = (int64_t)p.batch * plan.nsplit * p.hkv;
         const int grid = (int)(max_items < 2LL * cus ? max_items : 2LL * cus);   // two per CU, persistent
         hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p, work);
-        hipLaunchKernelGGL(decode_list_kernel, dim3(grid), dim3(kDecThreads), 0, s, p);
+        hipLaunchKernelGGL(decode_list_kernel<kKvContig>, dim3(grid), dim3(kDecThreads), 0, s, p);
         if (plan.nsplit > 1)
             hipLaunchKernelGGL(decode_combine_kernel, dim3(p.hkv, p.batch), dim3(kDecThreads), 0, s, p);
     } else {
         hipLaunchKernelGGL(decode_split_kernel, dim3(p.nsplit, p.hkv, p.batch), dim3(kDecThreads), 0, s, p);
+        if (plan.nsplit > 1)
+            hipLaunchKernelGGL(decode_combine_kernel, dim3(p.hkv, p.batch), dim3(kDecThreads), 0, s, p);
+    }
+    if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
+    return FGQA_OK;
+}
+
+// ---------------------------------------------------------------- paged KV cache
+namespace fgqa {
+namespace {
+
+int validate_paged(const fgqa_decode_paged_args* a) {
+    if (a == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
+    if (a->batch < 0 || a->max_seqlen < 0 || a->num_q_heads <= 0 || a->num_kv_heads <= 0 || a->head_dim <= 0 ||
+        a->page_size <= 0 || a->num_pages < 0 || a->block_table_stride < 0)
+        return FGQA_ERR_INVALID_ARGUMENT;
+    if (a->num_q_heads % a->num_kv_heads != 0) return FGQA_ERR_INVALID_ARGUMENT;
+    if (!isfinite(a->scale) || !isfinite(a->k_scale) || !isfinite(a->v_scale)) return FGQA_ERR_INVALID_ARGUMENT;
+    if (a->split_tokens < 0) return FGQA_ERR_INVALID_ARGUMENT;
+    if (a->kv_dtype != FGQA_KV_BF16 && a->kv_dtype != FGQA_KV_FP8_E4M3) return FGQA_ERR_INVALID_ARGUMENT;
+    if ((a->page_size & (a->page_size - 1)) != 0 || a->page_size > (1 << 20)) return FGQA_ERR_UNSUPPORTED;
+    // the block table row covers max_seqlen tokens
+    if ((int64_t)a->max_seqlen > a->block_table_stride * (int64_t)a->page_size) return FGQA_ERR_INVALID_ARGUMENT;
+    for (int i = 0; i < 2; ++i)
+        if (a->q_stride[i] < 0 || a->o_stride[i] < 0) return FGQA_ERR_INVALID_ARGUMENT;
+    for (int i = 0; i < 3; ++i)
+        if (a->k_stride[i] < 0 || a->v_stride[i] < 0) return FGQA_ERR_INVALID_ARGUMENT;
+    if (a->head_dim != kHeadDim) return FGQA_ERR_UNSUPPORTED;
+    if (a->num_q_heads / a->num_kv_heads > 16) return FGQA_ERR_UNSUPPORTED;
+    return FGQA_OK;
+}
+
+int validate_paged_pointers(const fgqa_decode_paged_args* a) {
+    if (a->batch == 0) return FGQA_OK;
+    if (a->q == nullptr || a->o == nullptr || a->seqlens == nullptr || a->block_table == nullptr)
+        return FGQA_ERR_INVALID_ARGUMENT;
+    if (a->max_seqlen > 0 && (a->k_cache == nullptr || a->v_cache == nullptr || a->num_pages == 0))
+        return FGQA_ERR_INVALID_ARGUMENT;
+    if (!aligned16(a->q) || !aligned16(a->o) || !aligned16(a->k_cache) || !aligned16(a->v_cache))
+        return FGQA_ERR_UNSUPPORTED;
+    for (int i = 0; i < 2; ++i)
+        if ((a->q_stride[i] & 7) || (a->o_stride[i] & 7)) return FGQA_ERR_UNSUPPORTED;
+    // 16-byte aligned rows: strides in elements of the cache type
+    const int64_t m = (a->kv_dtype == FGQA_KV_FP8_E4M3) ? 15 : 7;
+    for (int i = 0; i < 3; ++i)
+        if ((a->k_stride[i] & m) || (a->v_stride[i] & m)) return FGQA_ERR_UNSUPPORTED;
+    return FGQA_OK;
+}
+
+DecodeShape shape_of_paged(const fgqa_decode_paged_args* a) {
+    return DecodeShape{a->batch, a->max_seqlen, a->num_q_heads, a->num_kv_heads, a->split_tokens, true};
+}
+
+}  // namespace
+}  // namespace fgqa
+
+extern "C" int fgqa_decode_paged_workspace_bytes(const fgqa_decode_paged_args* a, size_t* bytes) {
+    if (bytes == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
+    int st = validate_paged(a);
+    if (st != FGQA_OK) return st;
+    DecodePlan plan;
+    const DecodeShape shape = shape_of_paged(a);
+    st = plan_decode(&shape, &plan);
+    if (st != FGQA_OK) return st;
+    *bytes = plan.ws_bytes;
+    return FGQA_OK;
+}
+
+extern "C" int fgqa_decode_paged(const fgqa_decode_paged_args* a, void* stream) {
+    int st = validate_paged(a);
+    if (st != FGQA_OK) return st;
+    st = validate_paged_pointers(a);
+    if (st != FGQA_OK) return st;
+    if (a->batch == 0) return FGQA_OK;
+    DecodePlan plan;
+    const DecodeShape shape = shape_of_paged(a);
+    st = plan_decode(&shape, &plan);
+    if (st != FGQA_OK) return st;
+
+    DecodeParams p;
+    p.q = static_cast<const __bf16*>(a->q);
+    p.k = static_cast<const __bf16*>(a->k_cache);
+    p.v = static_cast<const __bf16*>(a->v_cache);
+    p.o = static_cast<__bf16*>(a->o);
+    p.lse = a->lse;
+    p.seqlens = a->seqlens;
+    p.part_o = nullptr;
+    p.part_ml = nullptr;
+    p.q_sb = a->q_stride[0];
+    p.q_sh = a->q_stride[1];
+    p.k_sb = a->k_stride[0];
+    p.k_ss = a->k_stride[1];
+    p.k_sh = a->k_stride[2];
+    p.v_sb = a->v_stride[0];
+    p.v_ss = a->v_stride[1];
+    p.v_sh = a->v_stride[2];
+    p.o_sb = a->o_stride[0];
+    p.o_sh = a->o_stride[1];
+    p.batch = a->batch;
+    p.max_seqlen = a->max_seqlen;
+    p.hq = a->num_q_heads;
+    p.hkv = a->num_kv_heads;
+    p.group = a->num_q_heads / a->num_kv_heads;
+    p.nsplit = plan.nsplit;
+    p.chunk = plan.chunk;
+    p.scale_log2 = a->scale * a->k_scale * kLog2e;
+    p.block_table = a->block_table;
+    p.bt_stride = a->block_table_stride;
+    int shift = 0;
+    while ((1 << shift) < a->page_size) ++shift;
+    p.page_shift = shift;
+    p.num_pages = a->num_pages;
+    p.v_scale = a->v_scale;
+
+    int32_t* work = nullptr;
+    if (plan.ws_bytes > 0) {
+        void* ws = a->workspace;
+        if (ws == nullptr && a->workspace_bytes == 0) {
+            ws = internal_workspace(plan.ws_bytes, &st);
+            if (st != FGQA_OK) return st;
+        } else if (ws == nullptr || a->workspace_bytes < plan.ws_bytes) {
+            return FGQA_ERR_WORKSPACE;
+        } else if (!aligned16(ws)) {
+            return FGQA_ERR_UNSUPPORTED;
+        }
+        char* w = static_cast<char*>(ws);
+        if (plan.nsplit > 1) {
+            p.part_o = reinterpret_cast<float*>(w);
+            p.part_ml = reinterpret_cast<float*>(w + plan.part_o_bytes);
+        }
+        if (plan.list) work = reinterpret_cast<int32_t*>(w + plan.part_o_bytes + plan.part_ml_bytes);
+    }
+    p.work = work;
+    if (!plan.list) return FGQA_ERR_UNSUPPORTED;   // batch >= 2^15 or >= 2^16 splits
+
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (a->max_seqlen == 0) {
+        p.nsplit = 1;
+        hipLaunchKernelGGL(decode_combine_kernel, dim3(p.hkv, p.batch), dim3(kDecThreads), 0, s, p);
+    } else {
+        const int cus = device_cu_count();
+        if (cus <= 0) return FGQA_ERR_HIP;
+        const int64_t max_items = (int64_t)p.batch * plan.nsplit * p.hkv;
+        const int grid = (int)(max_items < 2LL * cus ? max_items : 2LL * cus);
+        hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p, work);
+        if (a->kv_dtype == FGQA_KV_FP8_E4M3)
+            hipLaunchKernelGGL(decode_list_kernel<kKvPagedFp8>, dim3(grid), dim3(kDecThreads), 0, s, p);
+        else
+            hipLaunchKernelGGL(decode_list_kernel<kKvPagedBf16>, dim3(grid), dim3(kDecThreads), 0, s, p);
         if (plan.nsplit > 1)
             hipLaunchKernelGGL(decode_combine_kernel, dim3(p.hkv, p.batch), dim3(kDecThreads), 0, s, p);
     }

@@ -11,6 +11,7 @@ Two families of entry points:
   K/V ``[B,S,Hkv,D]``, decode_flash_gqa_kernel.cuh:28-38) and of the new C++
   prefill entry point (BSHD):
     - ``decode_flash_gqa_bshd``  (adds per-sequence lengths and an LSE output)
+    - ``decode_flash_gqa_paged`` (paged KV cache with a block table, bf16 or fp8 e4m3)
     - ``flash_gqa_forward_bshd``
     - ``flash_gqa_backward_bshd``
 
@@ -31,6 +32,9 @@ __all__ = [
     "launch_decode_flash_gqa_bf16_kernel",
     "launch_flash_gqa_backward_bf16_kernel",
     "decode_flash_gqa_bshd",
+    "decode_flash_gqa_paged",
+    "paged_decode_workspace_bytes",
+    "prepare_decode_paged",
     "flash_gqa_forward_bshd",
     "flash_gqa_backward_bshd",
     "decode_workspace_bytes",
@@ -177,6 +181,113 @@ def prepare_decode(q, k, v, scale=None, out=None, seqlens=None, lse=None, split_
     """``decode_flash_gqa_bshd`` validated once; returns a ``PreparedLaunch``."""
     a, out, keep = _decode_prepare(q, k, v, scale, out, seqlens, lse, split_tokens, workspace)
     return PreparedLaunch(_lib.lib().fgqa_decode_bf16, a, keep, out, "fgqa_decode_bf16")
+
+
+# --------------------------------------------------------------------------- paged decode
+_PAGED_DTYPES = {torch.bfloat16: _lib.FGQA_KV_BF16}
+if hasattr(torch, "float8_e4m3fn"):
+    _PAGED_DTYPES[torch.float8_e4m3fn] = _lib.FGQA_KV_FP8_E4M3
+
+
+def _paged_args(q, kc, vc, block_table, seqlens, o, lse, scale, k_scale, v_scale, max_seqlen,
+                split_tokens, workspace):
+    B, Hq, D = q.shape
+    num_pages, page_size, Hkv, _ = kc.shape
+    a = _lib.PagedDecodeArgs()
+    a.q, a.k_cache, a.v_cache, a.o, a.lse = _ptr(q), _ptr(kc), _ptr(vc), _ptr(o), _ptr(lse)
+    a.block_table, a.seqlens = _ptr(block_table), _ptr(seqlens)
+    a.batch, a.max_seqlen, a.num_q_heads, a.num_kv_heads, a.head_dim = B, max_seqlen, Hq, Hkv, D
+    a.page_size, a.num_pages = page_size, num_pages
+    a.kv_dtype = _PAGED_DTYPES[kc.dtype]
+    a.scale, a.k_scale, a.v_scale = float(scale), float(k_scale), float(v_scale)
+    a.q_stride[:] = [q.stride(0), q.stride(1)]
+    a.o_stride[:] = [o.stride(0), o.stride(1)]
+    a.k_stride[:] = [kc.stride(0), kc.stride(1), kc.stride(2)]
+    a.v_stride[:] = [vc.stride(0), vc.stride(1), vc.stride(2)]
+    a.block_table_stride = block_table.stride(0) if block_table.dim() == 2 else 0
+    a.split_tokens = int(split_tokens)
+    if workspace is not None:
+        a.workspace = workspace.data_ptr()
+        a.workspace_bytes = workspace.numel() * workspace.element_size()
+    return a
+
+
+def paged_decode_workspace_bytes(batch, max_seqlen, num_q_heads, num_kv_heads, page_size, head_dim=128,
+                                 split_tokens=0) -> int:
+    """Bytes of scratch ``decode_flash_gqa_paged`` needs for a caller workspace."""
+    a = _lib.PagedDecodeArgs()
+    a.batch, a.max_seqlen, a.num_q_heads, a.num_kv_heads, a.head_dim = (
+        batch, max_seqlen, num_q_heads, num_kv_heads, head_dim)
+    a.page_size, a.num_pages, a.kv_dtype = page_size, 1, _lib.FGQA_KV_BF16
+    a.scale = a.k_scale = a.v_scale = 1.0
+    a.block_table_stride = -(-max_seqlen // page_size) if max_seqlen > 0 else 0
+    a.split_tokens = int(split_tokens)
+    n = ctypes.c_size_t(0)
+    _lib.check(_lib.lib().fgqa_decode_paged_workspace_bytes(ctypes.byref(a), ctypes.byref(n)),
+               "fgqa_decode_paged_workspace_bytes")
+    return int(n.value)
+
+
+def _paged_prepare(q, k_cache, v_cache, block_table, seqlens, scale, k_scale, v_scale, out, lse, max_seqlen,
+                   split_tokens, workspace):
+    if q.dtype != torch.bfloat16:
+        raise ValueError("paged decode expects a bf16 query")
+    if k_cache.dtype != v_cache.dtype or k_cache.dtype not in _PAGED_DTYPES:
+        raise ValueError("k_cache and v_cache must both be bf16 or float8_e4m3fn")
+    if q.dim() != 3 or k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError("expected q [B,Hq,D] and k_cache/v_cache [num_pages, page_size, Hkv, D]")
+    _require_cuda(q, k_cache, v_cache, block_table, seqlens)
+    B, Hq, D = q.shape
+    if k_cache.shape[3] != D:
+        raise ValueError("the caches' head_dim must match Q")
+    if Hq % k_cache.shape[2] != 0:
+        raise ValueError("Query heads must be divisible by KV heads")
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != B \
+            or block_table.stride(1) != 1:
+        raise ValueError("block_table must be an int32 [B, max_pages] tensor with contiguous rows")
+    if seqlens.dtype != torch.int32 or seqlens.shape != (B,) or not seqlens.is_contiguous():
+        raise ValueError("seqlens must be a contiguous int32 [B] tensor")
+    if k_cache.stride(3) != 1 or v_cache.stride(3) != 1:
+        raise ValueError("the caches' head_dim must be contiguous")
+    page_size = k_cache.shape[1]
+    if max_seqlen is None:
+        max_seqlen = block_table.shape[1] * page_size
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    q = _prep(q)
+    if out is None:
+        out = torch.empty((B, Hq, D), device=q.device, dtype=torch.bfloat16)
+    elif out.shape != (B, Hq, D) or out.dtype != torch.bfloat16 or not _kernel_ready(out):
+        raise ValueError("out must be a bf16 [B, Hq, D] tensor with contiguous rows")
+    if lse is not None and (lse.dtype != torch.float32 or lse.shape != (B, Hq) or not lse.is_contiguous()):
+        raise ValueError("lse must be a contiguous fp32 [B, Hq] tensor")
+    a = _paged_args(q, k_cache, v_cache, block_table, seqlens, out, lse, scale, k_scale, v_scale,
+                    int(max_seqlen), split_tokens, workspace)
+    return a, out, (q, k_cache, v_cache, block_table, seqlens, out, lse, workspace)
+
+
+def decode_flash_gqa_paged(q, k_cache, v_cache, block_table, seqlens, scale=None, k_scale=1.0, v_scale=1.0,
+                           out=None, lse=None, max_seqlen=None, split_tokens=0, workspace=None):
+    """Single-token GQA decode over a paged KV cache.
+
+    q: bf16 [B, Hq, D]; k_cache, v_cache: [num_pages, page_size, Hkv, D] in
+    bf16 or torch.float8_e4m3fn (holding K / k_scale and V / v_scale);
+    block_table: int32 [B, max_pages] (token t of sequence b is slot
+    t % page_size of page block_table[b, t // page_size]); seqlens: int32 [B].
+    page_size must be a power of two.  Returns ``out`` (bf16 [B, Hq, D]).
+    """
+    a, out, _keep = _paged_prepare(q, k_cache, v_cache, block_table, seqlens, scale, k_scale, v_scale, out,
+                                   lse, max_seqlen, split_tokens, workspace)
+    _lib.check(_lib.lib().fgqa_decode_paged(ctypes.byref(a), ctypes.c_void_p(_stream())), "fgqa_decode_paged")
+    return out
+
+
+def prepare_decode_paged(q, k_cache, v_cache, block_table, seqlens, scale=None, k_scale=1.0, v_scale=1.0,
+                         out=None, lse=None, max_seqlen=None, split_tokens=0, workspace=None):
+    """``decode_flash_gqa_paged`` validated once; returns a ``PreparedLaunch``."""
+    a, out, keep = _paged_prepare(q, k_cache, v_cache, block_table, seqlens, scale, k_scale, v_scale, out, lse,
+                                  max_seqlen, split_tokens, workspace)
+    return PreparedLaunch(_lib.lib().fgqa_decode_paged, a, keep, out, "fgqa_decode_paged")
 
 
 def launch_decode_flash_gqa_bf16_kernel(q, k, v, out=None):

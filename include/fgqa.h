@@ -85,6 +85,61 @@ int fgqa_decode_workspace_bytes(const fgqa_decode_args* args, size_t* bytes);
 int fgqa_decode_bf16(const fgqa_decode_args* args, void* stream);
 
 /*
+ * Decode over a paged KV cache (block table), in bf16 or fp8.  No counterpart
+ * in the reference: it extends the decode above (and its per-sequence
+ * lengths) to the paged layout serving engines keep their KV cache in.
+ *
+ *   q, o       bf16 [B, Hq, D], strides {b, h} (as fgqa_decode_bf16)
+ *   k_cache    [num_pages, page_size, Hkv, D] of kv_dtype, strides
+ *   v_cache      {page, slot, head} in elements of kv_dtype
+ *   block_table  device int32 [B, block_table_stride]: token t of sequence b
+ *              is slot t % page_size of page block_table[b][t / page_size].
+ *              Entries are clamped to [0, num_pages) on the device.
+ *   seqlens    device int32 [B] (required), each clamped to [0, max_seqlen];
+ *              max_seqlen <= block_table_stride * page_size.
+ *   page_size  a power of two.
+ *   kv_dtype   FGQA_KV_BF16 or FGQA_KV_FP8_E4M3 (OCP e4m3, as torch.float8_e4m3fn);
+ *              the cache holds K/k_scale and V/v_scale: scores use
+ *              q.k * k_scale * scale and O is multiplied by v_scale.
+ *   lse        nullable fp32 [B, Hq], natural log.
+ * Alignment: q, o, caches 16-byte aligned; cache strides multiples of 16 bytes.
+ */
+enum fgqa_kv_dtype { FGQA_KV_BF16 = 0, FGQA_KV_FP8_E4M3 = 1 };
+
+typedef struct fgqa_decode_paged_args {
+    const void* q;
+    const void* k_cache;
+    const void* v_cache;
+    void* o;
+    float* lse;
+    const int32_t* block_table;
+    const int32_t* seqlens;
+    int32_t batch;
+    int32_t max_seqlen;
+    int32_t num_q_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t page_size;
+    int32_t num_pages;
+    int32_t kv_dtype;
+    float scale;
+    float k_scale;
+    float v_scale;
+    int64_t q_stride[2];
+    int64_t o_stride[2];
+    int64_t k_stride[3];
+    int64_t v_stride[3];
+    int64_t block_table_stride;
+    int32_t split_tokens;
+    void* workspace;
+    size_t workspace_bytes;
+} fgqa_decode_paged_args;
+
+int fgqa_decode_paged_workspace_bytes(const fgqa_decode_paged_args* args, size_t* bytes);
+
+int fgqa_decode_paged(const fgqa_decode_paged_args* args, void* stream);
+
+/*
  * Causal (or full) prefill forward.  Replaces the Triton-only
  * launch_flash_gqa_forward_bf16_kernel, reference
  * src/python/Triton/flash_gqa_kernel.py:185-338 (kernel :15-138), which has no

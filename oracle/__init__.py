@@ -9,7 +9,9 @@ from .oracle import (  # noqa: F401
     attention_f64,
     bf16_to_f32,
     decode,
+    decode_paged,
     f32_to_bf16,
+    fp8e4m3_to_f32,
     lib,
     normal_bf16,
     prefill,

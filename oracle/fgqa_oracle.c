@@ -150,6 +150,102 @@ int fgqa_oracle_decode_bf16(const uint16_t* q, const uint16_t* k, const uint16_t
     return 0;
 }
 
+float fgqa_oracle_fp8e4m3_to_f32(uint8_t c) {
+    const int sgn = (c >> 7) & 1, e = (c >> 3) & 15, m = c & 7;
+    if (e == 15 && m == 7) return NAN;
+    const float v = (e == 0) ? ldexpf((float)m, -9) : ldexpf(1.0f + (float)m / 8.0f, e - 7);
+    return sgn ? -v : v;
+}
+
+/* Row `t` of sequence b, kv head kvh, decoded to float. */
+static void paged_row(const void* cache, int kv_fp8, const int32_t* bt, int64_t bt_stride, int page_size,
+                      const int64_t* st, int b, int t, int kvh, int d, float* out) {
+    const int64_t page = bt[(int64_t)b * bt_stride + t / page_size];
+    const int64_t off = page * st[0] + (int64_t)(t % page_size) * st[1] + (int64_t)kvh * st[2];
+    if (kv_fp8) {
+        const uint8_t* r = (const uint8_t*)cache + off;
+        for (int x = 0; x < d; ++x) out[x] = fgqa_oracle_fp8e4m3_to_f32(r[x]);
+    } else {
+        const uint16_t* r = (const uint16_t*)cache + off;
+        for (int x = 0; x < d; ++x) out[x] = bf(r[x]);
+    }
+}
+
+int fgqa_oracle_decode_paged(const uint16_t* q, const void* k_cache, const void* v_cache, int kv_fp8,
+                             const int32_t* block_table, int64_t bt_stride, int page_size,
+                             const int64_t* ks, const int64_t* vs,
+                             float scale, float k_scale, float v_scale, uint16_t* o, float* lse,
+                             int batch, int hq, int hkv, int d, const int32_t* seqlens, int tile,
+                             int nthreads) {
+    if (!q || !k_cache || !v_cache || !block_table || !ks || !vs || !o || !seqlens) return -1;
+    if (batch < 0 || hq <= 0 || hkv <= 0 || d <= 0 || d > ORACLE_MAX_D || page_size <= 0) return -1;
+    if (hq % hkv != 0 || tile <= 0) return -1;
+    for (int b = 0; b < batch; ++b)
+        if (seqlens[b] < 0 || (int64_t)seqlens[b] > bt_stride * page_size) return -1;
+    const int group = hq / hkv;
+    const float sc = scale * k_scale;
+    set_threads(nthreads);
+
+#pragma omp parallel
+    {
+        float* s = (float*)malloc(sizeof(float) * (size_t)tile);
+        float* p = (float*)malloc(sizeof(float) * (size_t)tile);
+        float acc[ORACLE_MAX_D];
+        float otile[ORACLE_MAX_D];
+        float row[ORACLE_MAX_D];
+#pragma omp for collapse(2) schedule(dynamic)
+        for (int b = 0; b < batch; ++b) {
+            for (int h = 0; h < hq; ++h) {
+                const int len = seqlens[b];
+                const int kvh = h / group;
+                const uint16_t* qrow = q + ((size_t)b * hq + h) * d;
+                float m = -INFINITY;
+                float l = 0.f;
+                for (int x = 0; x < d; ++x) acc[x] = 0.f;
+                for (int t0 = 0; t0 < len; t0 += tile) {
+                    const int n = (len - t0 < tile) ? (len - t0) : tile;
+                    for (int j = 0; j < n; ++j) {
+                        paged_row(k_cache, kv_fp8, block_table, bt_stride, page_size, ks, b, t0 + j, kvh, d, row);
+                        float qk = 0.f;
+                        for (int x = 0; x < d; ++x) qk += bf(qrow[x]) * row[x];
+                        s[j] = qk;
+                    }
+                    float m_new = m;
+                    for (int j = 0; j < n; ++j) m_new = fmaxf(m_new, s[j] * sc);
+                    float l_tile = 0.f;
+                    for (int j = 0; j < n; ++j) l_tile += expf(s[j] * sc - m_new);
+                    for (int j = 0; j < n; ++j) p[j] = bf(fgqa_oracle_f32_to_bf16(expf(s[j] * sc - m_new)));
+                    for (int x = 0; x < d; ++x) otile[x] = 0.f;
+                    for (int j = 0; j < n; ++j) {
+                        paged_row(v_cache, kv_fp8, block_table, bt_stride, page_size, vs, b, t0 + j, kvh, d, row);
+                        const float pj = p[j];
+                        for (int x = 0; x < d; ++x) otile[x] += pj * row[x];
+                    }
+                    const float corr = expf(m - m_new);
+                    if (t0 == 0) {
+                        for (int x = 0; x < d; ++x) acc[x] = otile[x];
+                    } else {
+                        for (int x = 0; x < d; ++x) acc[x] = acc[x] * corr + otile[x];
+                    }
+                    l = l * corr + l_tile;
+                    m = m_new;
+                }
+                uint16_t* orow = o + ((size_t)b * hq + h) * d;
+                if (len == 0) {
+                    for (int x = 0; x < d; ++x) orow[x] = 0;
+                    if (lse) lse[(size_t)b * hq + h] = -INFINITY;
+                } else {
+                    for (int x = 0; x < d; ++x) orow[x] = fgqa_oracle_f32_to_bf16((acc[x] / l) * v_scale);
+                    if (lse) lse[(size_t)b * hq + h] = m + logf(l);
+                }
+            }
+        }
+        free(s);
+        free(p);
+    }
+    return 0;
+}
+
 /*
  * Prefill.  Per (batch, query head, query row) this follows the torch
  * reference examples/python/Triton/test_flash_gqa_kernel.py:60-90:

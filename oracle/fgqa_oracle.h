@@ -26,6 +26,11 @@
  *                                            invariants (sum_j dK_j = 0, sum_j dV_j = sum dO)
  *   fgqa_oracle_attention_backward_f64      central finite differences of a float64
  *                                            numpy forward on tiny inputs
+ *   fgqa_oracle_fp8e4m3_to_f32              all 256 codes against torch.float8_e4m3fn
+ *   fgqa_oracle_decode_paged                bit-identical to fgqa_oracle_decode_bf16 on a
+ *                                            contiguous bf16 cache; page-permutation
+ *                                            invariance; fp8 path vs the fp64 brute force
+ *                                            on the decoded values
  *   fgqa_oracle_attention_f64               textbook softmax attention in double;
  *                                            pinned by numpy float64 restatement and
  *                                            closed forms on tiny inputs
@@ -69,6 +74,31 @@ int fgqa_oracle_decode_bf16(const uint16_t* q, const uint16_t* k, const uint16_t
                             float scale, uint16_t* o, float* lse,
                             int batch, int s_max, int hq, int hkv, int d,
                             const int32_t* seqlens, int tile, int p_bf16, int nthreads);
+
+/*
+ * OCP FP8 E4M3 (torch.float8_e4m3fn) -> float, from the format definition:
+ * bias 7, 3 mantissa bits, subnormals m/8 * 2^-6, S.1111.111 = NaN, no inf.
+ */
+float fgqa_oracle_fp8e4m3_to_f32(uint8_t c);
+
+/*
+ * Decode over a paged KV cache (no counterpart in the reference): the loop of
+ * fgqa_oracle_decode_bf16 (p_bf16 = 1) with each K/V row fetched through the
+ * block table and, for kv_fp8, decoded from e4m3.  Scores use
+ * q.k * (scale * k_scale); the output is bf16((O / l) * v_scale).  With bf16
+ * caches holding a contiguous sequence, k_scale = v_scale = 1, the results
+ * are bit-identical to fgqa_oracle_decode_bf16.
+ *   q, o: [B, Hq, D] contiguous; k_cache / v_cache: uint16 bf16 bits or uint8
+ *   e4m3 codes, element strides {page, slot, head}; token t of sequence b is
+ *   slot t % page_size of page block_table[b * bt_stride + t / page_size].
+ *   seqlens: host int32 [B] (required).
+ */
+int fgqa_oracle_decode_paged(const uint16_t* q, const void* k_cache, const void* v_cache, int kv_fp8,
+                             const int32_t* block_table, int64_t bt_stride, int page_size,
+                             const int64_t* k_strides, const int64_t* v_strides,
+                             float scale, float k_scale, float v_scale, uint16_t* o, float* lse,
+                             int batch, int hq, int hkv, int d, const int32_t* seqlens, int tile,
+                             int nthreads);
 
 /*
  * Prefill forward, restating the reference's torch reference

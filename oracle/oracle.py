@@ -67,6 +67,13 @@ def lib() -> ctypes.CDLL:
             _u16p, _u16p, _u16p, _u16p, _u16p, ctypes.c_double, _f64p, _f64p, _f64p,
             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
             _i64p, _i64p, _i64p, _i64p, _i64p, ctypes.c_int, ctypes.c_int]
+        L.fgqa_oracle_fp8e4m3_to_f32.restype = ctypes.c_float
+        L.fgqa_oracle_fp8e4m3_to_f32.argtypes = [ctypes.c_uint8]
+        L.fgqa_oracle_decode_paged.restype = ctypes.c_int
+        L.fgqa_oracle_decode_paged.argtypes = [
+            _u16p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, _i32p, ctypes.c_int64, ctypes.c_int,
+            _i64p, _i64p, ctypes.c_float, ctypes.c_float, ctypes.c_float, _u16p, _f32p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _i32p, ctypes.c_int, ctypes.c_int]
         _lib = L
     return _lib
 
@@ -242,3 +249,41 @@ def attention_backward_f64(q, k, v, grad_o, scale, causal=True, o=None, layout="
     if rc != 0:
         raise ValueError("fgqa_oracle_attention_backward_f64: invalid arguments")
     return dq, dk, dv
+
+
+def fp8e4m3_to_f32(codes) -> np.ndarray:
+    """uint8 OCP e4m3 codes -> float32 (via fgqa_oracle_fp8e4m3_to_f32)."""
+    codes = np.asarray(codes, dtype=np.uint8)
+    table = np.array([lib().fgqa_oracle_fp8e4m3_to_f32(c) for c in range(256)], dtype=np.float32)
+    return table[codes]
+
+
+def decode_paged(q, k_cache, v_cache, block_table, seqlens, scale, k_scale=1.0, v_scale=1.0,
+                 tile=128, nthreads=0, with_lse=True):
+    """Paged decode oracle.  q [B,Hq,D] uint16 bf16 bits; k/v caches
+    [num_pages, page_size, Hkv, D] as uint16 (bf16) or uint8 (fp8 e4m3) arrays;
+    block_table int32 [B, max_pages]; seqlens int32 [B].
+    Returns (o uint16 [B,Hq,D], lse float32 [B,Hq] or None)."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    if k_cache.dtype != v_cache.dtype or k_cache.dtype not in (np.uint16, np.uint8):
+        raise ValueError("k_cache / v_cache must both be uint16 (bf16) or uint8 (fp8)")
+    kv_fp8 = int(k_cache.dtype == np.uint8)
+    k_cache = np.ascontiguousarray(k_cache)
+    v_cache = np.ascontiguousarray(v_cache)
+    bt = np.ascontiguousarray(block_table, dtype=np.int32)
+    sl = np.ascontiguousarray(seqlens, dtype=np.int32)
+    B, Hq, D = q.shape
+    _, page_size, Hkv, _ = k_cache.shape
+    ks = np.array([s // k_cache.itemsize for s in k_cache.strides[:3]], dtype=np.int64)
+    vs = np.array([s // v_cache.itemsize for s in v_cache.strides[:3]], dtype=np.int64)
+    o = np.empty((B, Hq, D), dtype=np.uint16)
+    lse = np.empty((B, Hq), dtype=np.float32) if with_lse else None
+    rc = lib().fgqa_oracle_decode_paged(
+        _ptr(q, ctypes.c_uint16), k_cache.ctypes.data_as(ctypes.c_void_p), v_cache.ctypes.data_as(ctypes.c_void_p),
+        kv_fp8, _ptr(bt, ctypes.c_int32), int(bt.shape[1]), int(page_size),
+        _ptr(ks, ctypes.c_int64), _ptr(vs, ctypes.c_int64), float(scale), float(k_scale), float(v_scale),
+        _ptr(o, ctypes.c_uint16), _ptr(lse, ctypes.c_float), B, Hq, Hkv, D, _ptr(sl, ctypes.c_int32),
+        int(tile), int(nthreads))
+    if rc != 0:
+        raise ValueError("fgqa_oracle_decode_paged: invalid arguments")
+    return o, lse

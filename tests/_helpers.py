@@ -89,3 +89,35 @@ def gpu_normal_bf16(shape, seed, sigma, device):
     if sigma != 1.0:
         x.mul_(sigma)
     return x.to(torch.bfloat16)
+
+
+def fp8_quantize(x, scale):
+    """float array / scale -> OCP e4m3 codes (uint8), round to nearest even (torch's cast)."""
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32) / np.float32(scale))
+    # the cast turns values beyond the e4m3 range (448) into NaN
+    return t.clamp_(-448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
+def make_paged(k, v, lens, page_size, rng, extra_pages=3):
+    """Scatter contiguous caches k/v [B, S, Hkv, D] (any dtype) into randomly
+    ordered pages [num_pages, page_size, Hkv, D] (unused pages hold garbage)
+    and return (k_cache, v_cache, block_table int32 [B, max_pages])."""
+    B, S, Hkv, D = k.shape
+    max_pages = max(1, -(-S // page_size))
+    need = [-(-int(n) // page_size) for n in lens]
+    num_pages = sum(need) + extra_pages
+    perm = rng.permutation(num_pages)
+    kc = rng.integers(0, 256, size=(num_pages, page_size, Hkv, D)).astype(k.dtype)
+    vc = rng.integers(0, 256, size=(num_pages, page_size, Hkv, D)).astype(v.dtype)
+    table = np.zeros((B, max_pages), dtype=np.int32)
+    nxt = 0
+    for b in range(B):
+        for j in range(need[b]):
+            pg = int(perm[nxt])
+            nxt += 1
+            table[b, j] = pg
+            t0, t1 = j * page_size, min((j + 1) * page_size, S)
+            kc[pg, : t1 - t0] = k[b, t0:t1]
+            vc[pg, : t1 - t0] = v[b, t0:t1]
+    return kc, vc, table

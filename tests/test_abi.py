@@ -24,6 +24,7 @@ def test_c_abi_symbols_exported():
     names = set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(fgqa_\w+)\s*\(", hdr, flags=re.M))
     assert names == {"fgqa_decode_workspace_bytes", "fgqa_decode_bf16", "fgqa_prefill_bf16",
                      "fgqa_prefill_backward_workspace_bytes", "fgqa_prefill_backward_bf16",
+                     "fgqa_decode_paged_workspace_bytes", "fgqa_decode_paged",
                      "fgqa_status_string", "fgqa_version"}
     L = _lib.lib()
     syms = _exported()
@@ -262,3 +263,43 @@ def test_backward_mirror_validation_without_gpu():
         f(q, k, k, q, lse[:, :, :32], q)
     with pytest.raises(ValueError, match="GPU"):
         f(q, k, k, q, lse, q)
+
+
+def _paged_args(**kw):
+    a = _lib.PagedDecodeArgs()
+    B, Hq, Hkv, D, ps = kw.get("B", 2), kw.get("Hq", 16), kw.get("Hkv", 2), kw.get("D", 128), kw.get("ps", 16)
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.page_size = B, Hq, Hkv, D, ps
+    a.max_seqlen = kw.get("S", 256)
+    a.num_pages = kw.get("pages", 64)
+    a.kv_dtype = kw.get("dtype", _lib.FGQA_KV_BF16)
+    a.scale, a.k_scale, a.v_scale = D ** -0.5, kw.get("ks", 1.0), 1.0
+    a.q_stride[:] = [Hq * D, D]
+    a.o_stride[:] = [Hq * D, D]
+    st = kw.get("kstride", [ps * Hkv * D, Hkv * D, D])
+    a.k_stride[:] = st
+    a.v_stride[:] = st
+    a.block_table_stride = kw.get("bts", 16)
+    for name in ("q", "k_cache", "v_cache", "o", "block_table", "seqlens"):
+        setattr(a, name, kw.get(name, 4096))
+    return a
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(ps=24), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(S=257), _lib.FGQA_ERR_INVALID_ARGUMENT),          # table covers 16 pages x 16 = 256 tokens
+    (dict(dtype=7), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(seqlens=None), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(block_table=None), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(ks=float("inf")), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(Hq=34, Hkv=2), _lib.FGQA_ERR_UNSUPPORTED),        # G = 17
+    (dict(dtype=_lib.FGQA_KV_FP8_E4M3, kstride=[16 * 2 * 128, 2 * 128 + 8, 128]), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(D=64), _lib.FGQA_ERR_UNSUPPORTED),
+])
+def test_paged_decode_rejects_before_launch(kw, code):
+    assert _lib.lib().fgqa_decode_paged(ctypes.byref(_paged_args(**kw)), None) == code
+
+
+def test_paged_decode_empty_batch_is_noop():
+    L = _lib.lib()
+    assert L.fgqa_decode_paged(ctypes.byref(_paged_args(B=0, q=None)), None) == 0
+    assert L.fgqa_decode_paged(None, None) == _lib.FGQA_ERR_INVALID_ARGUMENT

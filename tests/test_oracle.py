@@ -475,3 +475,72 @@ def test_backward_planted_mistakes_are_caught():
     ls[:, perm] = lse
     gq, gk, gv = oracle.prefill_backward(qs, k, v, os_, ls, ds, SCALE, causal=True)
     assert not ok((gq[:, :, perm], gk, gv))
+
+
+
+# ----------------------------------------------------------------- paged / fp8 decode oracle
+from tests._helpers import fp8_quantize, make_paged  # noqa: E402
+
+
+def test_fp8_e4m3_decoding_matches_torch():
+    """fgqa_oracle_fp8e4m3_to_f32 on all 256 codes equals torch.float8_e4m3fn."""
+    import torch
+    codes = np.arange(256, dtype=np.uint8)
+    ours = oracle.fp8e4m3_to_f32(codes)
+    theirs = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    nan = np.isnan(theirs)
+    assert np.array_equal(np.isnan(ours), nan)
+    assert np.array_equal(ours[~nan], theirs[~nan])
+    assert np.array_equal(np.signbit(ours[~nan]), np.signbit(theirs[~nan]))
+    assert ours[0x7E] == 448.0 and ours[0x01] == 2.0 ** -9
+
+
+@pytest.mark.parametrize("page_size", [1, 16, 64])
+def test_paged_oracle_bit_identical_to_contiguous(page_size):
+    """bf16 pages in random order, scales 1: the same bits as the contiguous decode oracle."""
+    rng = np.random.default_rng(page_size)
+    B, Hq, Hkv, S = 3, 8, 2, 300
+    q, k, v = _decode_inputs(61, B, Hq, Hkv, S)
+    lens = np.array([300, 1, 137], dtype=np.int32)
+    o_ref, l_ref = oracle.decode(q, k, v, SCALE, seqlens=lens)
+    kc, vc, bt = make_paged(k, v, lens, page_size, rng)
+    o, lse = oracle.decode_paged(q, kc, vc, bt, lens, SCALE)
+    assert np.array_equal(o, o_ref) and np.array_equal(lse, l_ref)
+    # a second, different page assignment gives the same bits again
+    kc2, vc2, bt2 = make_paged(k, v, lens, page_size, np.random.default_rng(page_size + 100))
+    o2, _ = oracle.decode_paged(q, kc2, vc2, bt2, lens, SCALE)
+    assert np.array_equal(o2, o_ref)
+
+
+def test_paged_oracle_fp8_against_f64():
+    """fp8 caches: the oracle equals the fp64 attention over the decoded values
+    (scores scaled by k_scale, output by v_scale) at the parity bar; wrong
+    scales or a wrong page are caught."""
+    rng = np.random.default_rng(7)
+    B, Hq, Hkv, S = 2, 16, 2, 400
+    q = oracle.normal_bf16(63, (B, Hq, 128))
+    kf = rng.standard_normal((B, S, Hkv, 128)).astype(np.float32)
+    vf = rng.standard_normal((B, S, Hkv, 128)).astype(np.float32)
+    ks, vs = float(np.abs(kf).max() / 448), float(np.abs(vf).max() / 448)
+    k8, v8 = fp8_quantize(kf, ks), fp8_quantize(vf, vs)
+    lens = np.array([400, 233], dtype=np.int32)
+    kc, vc, bt = make_paged(k8, v8, lens, 16, rng)
+    o, lse = oracle.decode_paged(q, kc, vc, bt, lens, SCALE, k_scale=ks, v_scale=vs)
+    # fp64 reference on the decoded values (exact in bf16: e4m3 is a subset)
+    kb = oracle.f32_to_bf16(oracle.fp8e4m3_to_f32(k8))
+    vb = oracle.f32_to_bf16(oracle.fp8e4m3_to_f32(v8))
+    of, lf = oracle.attention_f64(q[:, None], kb, vb, SCALE * ks, seqlens=lens)
+    ref = of[:, 0] * vs
+    assert_close(oracle.bf16_to_f32(o), ref, "paged fp8 oracle vs f64")
+    assert np.max(np.abs(lse - lf[:, :, 0])) < 1e-4
+    bad, _ = oracle.decode_paged(q, kc, vc, bt, lens, SCALE, k_scale=ks, v_scale=vs * 1.1)
+    assert not within_tol(oracle.bf16_to_f32(bad), ref)
+    bad, _ = oracle.decode_paged(q, kc, vc, bt, lens, SCALE, k_scale=ks * 3, v_scale=vs)
+    assert not within_tol(oracle.bf16_to_f32(bad), ref)
+    # (key order does not matter to decode, so a swapped pair of pages is no
+    # mistake; a page pointing at unused cache memory is)
+    bt_bad = bt.copy()
+    used = set(bt[0, :25].tolist()) | set(bt[1, :15].tolist())
+    bt_bad[0, 3] = next(pg for pg in range(kc.shape[0]) if pg not in used)
+    bad, _ = oracle.decode_paged(q, kc, vc, bt_bad, lens, SCALE, k_scale=ks, v_scale=vs)
+    assert not within_tol(oracle.bf16_to_f32(bad)[0], ref[0])
