@@ -4,9 +4,10 @@ Default (the driver's contract): BASELINE config 2, GQA decode at B=60,
 S=4096, Hq=128, Hkv=8, D=128, bf16 in/out, fp32 accumulation, inputs resident
 in HBM.  One "step" = one decode over the whole batch.  Prints ONE JSON line:
 value = decode KV-read throughput in GB/s (decimal), with the roofline of the
-decode kernel against 8 TB/s HBM, the causal prefill of BASELINE config 4
-and its backward (TFLOPS against 2.5 PFLOP/s bf16 dense MFMA) beside it, and
-the CPU oracle timed on a bounded sample of the same decode workload.
+decode kernel against 8 TB/s HBM, the paged-KV decode (bf16 and fp8 caches)
+at config 3's lengths, the causal prefill of BASELINE config 4 and its
+backward (TFLOPS against 2.5 PFLOP/s bf16 dense MFMA) beside it, and the CPU
+oracle timed on a bounded sample of the same decode workload.
 
     python bench.py [--steps K] [--warmup W] [--split-tokens N] [--no-cpu] [--all]
 
@@ -197,6 +198,50 @@ def hbm_copy(steps, warmup, dev, nbytes=1 << 30):
                 read_plus_write_GBs=2 * nbytes / (avg * 1e-3) / 1e9)
 
 
+def bench_paged(cfg_id, steps, warmup, dev, page_size=16, kv="bf16"):
+    """Decode over a paged KV cache (block table, pages in random order) with
+    the lengths of a BASELINE decode config; KV bytes count the valid tokens
+    in the cache's own dtype (fp8: 1 byte per element)."""
+    import numpy as np
+    import torch
+
+    import cuda_llm_ops_amd as fg
+    cfg = DECODE_CONFIGS[cfg_id]
+    B, S, Hq, Hkv = cfg["B"], cfg["S"], cfg["Hq"], cfg["Hkv"]
+    q, k, v, sl, lens, _ = _decode_setup(cfg, dev)
+    if sl is None:
+        sl = torch.full((B,), S, dtype=torch.int32, device=dev)
+        lens = np.full(B, S, dtype=np.int32)
+    max_pages = S // page_size
+    n = B * max_pages
+    perm = torch.from_numpy(np.random.default_rng(11).permutation(n).astype(np.int64)).to(dev)
+    table = perm.view(B, max_pages).to(torch.int32)
+    k_scale = v_scale = 1.0
+    if kv == "fp8":
+        k_scale, v_scale = 6.0 / 448, 6.0 / 448
+        k = (k.float() / k_scale).clamp_(-448, 448).to(torch.float8_e4m3fn)
+        v = (v.float() / v_scale).clamp_(-448, 448).to(torch.float8_e4m3fn)
+    kc = torch.empty((n, page_size, Hkv, 128), dtype=k.dtype, device=dev)
+    vc = torch.empty_like(kc)
+    kc[perm] = k.reshape(n, page_size, Hkv, 128)
+    vc[perm] = v.reshape(n, page_size, Hkv, 128)
+    del k, v
+    out = torch.empty_like(q)
+    n_ws = fg.paged_decode_workspace_bytes(B, S, Hq, Hkv, page_size)
+    ws = torch.empty(max(n_ws, 256), dtype=torch.uint8, device=dev)
+    step = fg.prepare_decode_paged(q, kc, vc, table, sl, SCALE, k_scale=k_scale, v_scale=v_scale, out=out,
+                                   workspace=ws)
+    total_ms, per = _time_calls(step, steps, warmup)
+    elem = 1 if kv == "fp8" else 2
+    kv_bytes = 2 * int(lens.sum()) * Hkv * 128 * elem
+    avg = sum(per) / len(per)
+    gbs = kv_bytes / (avg * 1e-3) / 1e9
+    return dict(config=f"paged decode, BASELINE config {cfg_id} lengths, page {page_size}, {kv} KV",
+                us_avg=round(avg * 1e3, 2), kv_bytes=kv_bytes, GBs=round(gbs, 1),
+                frac_hbm=round(gbs / HBM_PEAK_GBS, 4),
+                tokens_per_s=round(float(lens.sum()) / (avg * 1e-3), 0))
+
+
 def bench_backward(cfg_id, steps, warmup, dev):
     """Prefill backward (dQ, dK, dV) of a causal forward at a BASELINE prefill
     shape; one step = every launch of fgqa_prefill_backward_bf16."""
@@ -239,8 +284,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-backward", action="store_true")
+    ap.add_argument("--no-paged", action="store_true")
+    ap.add_argument("--page-size", type=int, default=16, help="with --mode paged")
+    ap.add_argument("--kv", choices=["bf16", "fp8"], default="bf16", help="with --mode paged")
     ap.add_argument("--all", action="store_true", help="also report configs 1, 3 and 5 (to stderr)")
-    ap.add_argument("--mode", choices=["bench", "decode", "prefill", "backward", "copy"], default="bench",
+    ap.add_argument("--mode", choices=["bench", "decode", "paged", "prefill", "backward", "copy"], default="bench",
                     help="decode/prefill/copy: run only that workload (for profiling) and print its timing")
     ap.add_argument("--config", type=int, default=0,
                     help="with --mode decode/prefill/backward: BASELINE config id")
@@ -265,6 +313,10 @@ def main():
     if args.mode == "prefill":
         print(json.dumps({"mode": "prefill", **bench_prefill(args.config or 4, args.steps, args.warmup, dev)}),
               flush=True)
+        return
+    if args.mode == "paged":
+        print(json.dumps({"mode": "paged", **bench_paged(args.config or 3, args.steps, args.warmup, dev,
+                                                          args.page_size, args.kv)}), flush=True)
         return
     if args.mode == "backward":
         print(json.dumps({"mode": "backward", **bench_backward(args.config or 4, args.steps, args.warmup, dev)}),
@@ -300,6 +352,9 @@ def main():
     }
     if not args.no_prefill:
         line["prefill"] = bench_prefill(4, args.steps, args.warmup, dev)
+    if not args.no_paged:
+        line["decode_paged"] = [bench_paged(3, max(5, args.steps // 5), 2, dev, 16, kv)
+                                for kv in ("bf16", "fp8")]
     if not args.no_backward:
         line["backward"] = bench_backward(4, max(5, args.steps // 2), max(2, args.warmup // 2), dev)
     if not args.no_cpu:

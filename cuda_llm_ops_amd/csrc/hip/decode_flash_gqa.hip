@@ -13,7 +13,8 @@
 //       rounded to bf16 before P.V and the rowsum kept from the fp32 P, as the
 //       reference does (decode_flash_gqa_kernel.cu:266-278)
 //       O^T[d][h] += V^T[d][t] . P^T[t][h]   v_mfma_f32_16x16x32_bf16, V^T
-//                                            gathered from the staged rows
+//                                            read transposed from the staged
+//                                            rows (ds_read_b64_tr_b16)
 //     The 4 waves merge their (max, sum, O) in LDS; with one split the
 //     workgroup writes the normalised bf16 output directly, otherwise it
 //     writes an fp32 partial (O, max, sum) to the workspace.
@@ -274,16 +275,15 @@ __device__ __forceinline__ void dec_item(const DecodeParams& p, unsigned char* s
 
         // V^T as the A operand: lane holds V[token(slot)][16*db + l16] for the
         // 8 slots of group g4: tokens 4*g4 + {0..3} and 16 + 4*g4 + {0..3},
-        // the same tokens whose P this lane already holds.
+        // the same tokens whose P this lane already holds.  Two transposed
+        // reads (ds_read_b64_tr_b16) per column block: source lane l16 of the
+        // group points at row 4*g4 + l16/4 (+16), columns 16*db + 4*(l16%4) .. +3.
+        const __bf16* vsrc = vl + (4 * g4 + (l16 >> 2)) * kDecRowStride + 4 * (l16 & 3);
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
-            bf16x8_t va;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int tok = (j < 4) ? (g4 * 4 + j) : (16 + g4 * 4 + (j - 4));
-                va[j] = vl[tok * kDecRowStride + db * 16 + l16];
-            }
-            oacc[db] = mfma16(va, pop, oacc[db]);
+            const bf16x4_t lo = lds_read_tr16(vsrc + db * 16);
+            const bf16x4_t hi = lds_read_tr16(vsrc + 16 * kDecRowStride + db * 16);
+            oacc[db] = mfma16(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), pop, oacc[db]);
         }
 
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
