@@ -61,6 +61,42 @@ void LaunchFlashGqaBf16KernelVarlen(const bf16_t* q, const bf16_t* k, const bf16
     g_last_status = fgqa_decode_bf16(&a, nullptr);
 }
 
+void LaunchFlashGqaBf16KernelPaged(const bf16_t* q, const void* kCache, const void* vCache, bool kvFp8, float scale,
+                                   float kScale, float vScale, bf16_t* o, const int32_t* blockTable,
+                                   const int32_t* seqLengths, int batchSize, int maxPagesPerSeq, int pageSize,
+                                   int numPages, int numQueryHeads, int numKvHeads, int headDim) {
+    fgqa_decode_paged_args a;
+    std::memset(&a, 0, sizeof(a));
+    a.q = q;
+    a.k_cache = kCache;
+    a.v_cache = vCache;
+    a.o = o;
+    a.block_table = blockTable;
+    a.seqlens = seqLengths;
+    a.batch = batchSize;
+    a.max_seqlen = (maxPagesPerSeq > 0 && pageSize > 0) ? maxPagesPerSeq * pageSize : 0;
+    a.num_q_heads = numQueryHeads;
+    a.num_kv_heads = numKvHeads;
+    a.head_dim = headDim;
+    a.page_size = pageSize;
+    a.num_pages = numPages;
+    a.kv_dtype = kvFp8 ? FGQA_KV_FP8_E4M3 : FGQA_KV_BF16;
+    a.scale = scale;
+    a.k_scale = kScale;
+    a.v_scale = vScale;
+    // q, o: [B, Hq, D];  caches: [numPages, pageSize, Hkv, D]
+    a.q_stride[0] = (int64_t)numQueryHeads * headDim;
+    a.q_stride[1] = headDim;
+    a.o_stride[0] = a.q_stride[0];
+    a.o_stride[1] = a.q_stride[1];
+    a.k_stride[0] = (int64_t)pageSize * numKvHeads * headDim;
+    a.k_stride[1] = (int64_t)numKvHeads * headDim;
+    a.k_stride[2] = headDim;
+    for (int i = 0; i < 3; ++i) a.v_stride[i] = a.k_stride[i];
+    a.block_table_stride = maxPagesPerSeq;
+    g_last_status = fgqa_decode_paged(&a, nullptr);
+}
+
 void LaunchFlashGqaForwardBf16KernelStrided(const bf16_t* q, const bf16_t* k, const bf16_t* v, float scale,
                                             bf16_t* o, float* lse, int batchSize, int seqLengthQ, int seqLengthKv,
                                             int numQueryHeads, int numKvHeads, int headDim, bool causal,

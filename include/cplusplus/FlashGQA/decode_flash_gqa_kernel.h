@@ -61,6 +61,32 @@ void LaunchFlashGqaBf16KernelVarlen(const bf16_t* q,
                                     int headDim);
 
 /**
+ * @brief Paged variant: K/V live in a page cache [numPages, pageSize, numKvHeads, headDim]
+ *        (bf16, or OCP fp8 e4m3 bytes when kvFp8 is true, holding K/kScale and
+ *        V/vScale); token t of sequence b is slot t % pageSize of page
+ *        blockTable[b * maxPagesPerSeq + t / pageSize].  pageSize is a power of
+ *        two; seqLengths (device int32 [batchSize]) are each <= maxPagesPerSeq * pageSize.
+ *        No reference counterpart: the serving-engine layout of the decode above.
+ */
+void LaunchFlashGqaBf16KernelPaged(const bf16_t* q,
+                                   const void* kCache,
+                                   const void* vCache,
+                                   bool kvFp8,
+                                   float scale,
+                                   float kScale,
+                                   float vScale,
+                                   bf16_t* o,
+                                   const int32_t* blockTable,
+                                   const int32_t* seqLengths,
+                                   int batchSize,
+                                   int maxPagesPerSeq,
+                                   int pageSize,
+                                   int numPages,
+                                   int numQueryHeads,
+                                   int numKvHeads,
+                                   int headDim);
+
+/**
  * @brief Status (an fgqa_status value from fgqa.h) of the calling thread's last
  *        Launch* call in this API: 0 when it launched.
  */

@@ -41,6 +41,7 @@ def test_cplusplus_entry_points_exported():
         hdr = open(os.path.join(ROOT, "include", "cplusplus", sub)).read()
         decls += re.findall(r"^(?:void|int)\s+(\w+)\(", hdr, flags=re.M)
     assert set(decls) == {"LaunchFlashGqaBf16Kernel", "LaunchFlashGqaBf16KernelVarlen", "FlashGqaGetLastStatus",
+                          "LaunchFlashGqaBf16KernelPaged",
                           "LaunchFlashGqaForwardBf16Kernel", "LaunchFlashGqaForwardBf16KernelStrided",
                           "LaunchFlashGqaBackwardBf16Kernel"}
     for d in decls:

@@ -176,3 +176,45 @@ def test_paged_rejections(cuda):
         fg.decode_flash_gqa_paged(q, kc, kc, bt, sl, max_seqlen=65)
     with pytest.raises(ValueError):
         fg.decode_flash_gqa_paged(q, kc, kc.float(), bt, sl)
+
+
+def test_paged_cplusplus_entry(cuda):
+    """LaunchFlashGqaBf16KernelPaged (default stream), bf16 and fp8 caches."""
+    import ctypes
+
+    import torch
+    fg = _fg()
+    L = fg.lib()
+    fn = getattr(L, "_Z29LaunchFlashGqaBf16KernelPagedPK6bf16_tPKvS3_bfffPS_PKiS6_iiiiiii")
+    fn.restype = None
+    st = getattr(L, "_Z21FlashGqaGetLastStatusv")
+    st.restype = ctypes.c_int
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    for fp8 in (False, True):
+        print(f"paged C++ entry fp8={fp8}", flush=True)
+        rng = np.random.default_rng(5)
+        B, Hq, Hkv, S, ps = 2, 16, 2, 256, 32
+        q = oracle.normal_bf16(970, (B, Hq, 128))
+        if fp8:
+            k = fp8_quantize(rng.standard_normal((B, S, Hkv, 128)), 0.02)
+            v = fp8_quantize(rng.standard_normal((B, S, Hkv, 128)), 0.02)
+            ks = vs = 0.02
+        else:
+            k = oracle.normal_bf16(970, (B, S, Hkv, 128), stream=1)
+            v = oracle.normal_bf16(970, (B, S, Hkv, 128), stream=2)
+            ks = vs = 1.0
+        lens = np.array([256, 77], dtype=np.int32)
+        kc, vc, bt = make_paged(k, v, lens, ps, rng)
+        o_ref, _ = oracle.decode_paged(q, kc, vc, bt, lens, SCALE, k_scale=ks, v_scale=vs)
+        kd = torch.from_numpy(kc).to(cuda)
+        vd = torch.from_numpy(vc).to(cuda)
+        qd = to_torch_bf16(q, cuda)
+        btd = torch.from_numpy(bt).to(cuda)
+        sld = torch.from_numpy(lens).to(cuda)
+        od = torch.zeros_like(qd)
+        torch.cuda.synchronize()
+        fn(p(qd), p(kd), p(vd), ctypes.c_bool(fp8), ctypes.c_float(SCALE), ctypes.c_float(ks), ctypes.c_float(vs),
+           p(od), p(btd), p(sld), B, bt.shape[1], ps, kc.shape[0], Hq, Hkv, 128)
+        assert st() == 0
+        torch.cuda.synchronize()
+        assert_close(oracle.bf16_to_f32(from_torch_bf16(od)), oracle.bf16_to_f32(o_ref), f"C++ paged fp8={fp8}")
