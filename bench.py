@@ -242,6 +242,32 @@ def bench_paged(cfg_id, steps, warmup, dev, page_size=16, kv="bf16"):
                 tokens_per_s=round(float(lens.sum()) / (avg * 1e-3), 0))
 
 
+def bench_swa(steps, warmup, dev, window=512):
+    """Sliding-window (+ sink) prefill at the reference's SWA benchmark shape
+    (README: B=1, S=4096, Hq=16, Hkv=1, D=128, window 512)."""
+    import torch
+
+    import cuda_llm_ops_amd as fg
+    B, S, Hq, Hkv = 1, 4096, 16, 1
+    q = _normal((B, S, Hq, 128), 8, 1.0, dev)
+    k = _normal((B, S, Hkv, 128), 9, 1.0, dev)
+    v = _normal((B, S, Hkv, 128), 10, 1.0, dev)
+    sink = torch.rand(Hq, generator=torch.Generator().manual_seed(11)).to(dev) + 1e-6
+    out = torch.empty_like(q)
+    lse = torch.empty((B, Hq, S), dtype=torch.float32, device=dev)
+    step = fg.prepare_prefill(q, k, v, SCALE, out=out, lse=lse, causal=True, window_size=window, sink=sink)
+    total_ms, per = _time_calls(step, steps, warmup)
+    # the reference's count (test_flash_swa_kernel.py:318-337)
+    flops = B * Hq * 2 * S * window * (128 + 128)
+    avg = sum(per) / len(per)
+    tflops = flops / (avg * 1e-3) / 1e12
+    return dict(config=f"sliding-window prefill with sink, B={B} S={S} Hq={Hq} Hkv={Hkv} D=128 window={window}",
+                us_avg=round(avg * 1e3, 2), us_min=round(per[0] * 1e3, 2),
+                roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
+                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                          "algorithmic_flops": flops})
+
+
 def bench_backward(cfg_id, steps, warmup, dev):
     """Prefill backward (dQ, dK, dV) of a causal forward at a BASELINE prefill
     shape; one step = every launch of fgqa_prefill_backward_bf16."""
@@ -285,10 +311,12 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-backward", action="store_true")
     ap.add_argument("--no-paged", action="store_true")
+    ap.add_argument("--no-swa", action="store_true")
     ap.add_argument("--page-size", type=int, default=16, help="with --mode paged")
     ap.add_argument("--kv", choices=["bf16", "fp8"], default="bf16", help="with --mode paged")
     ap.add_argument("--all", action="store_true", help="also report configs 1, 3 and 5 (to stderr)")
-    ap.add_argument("--mode", choices=["bench", "decode", "paged", "prefill", "backward", "copy"], default="bench",
+    ap.add_argument("--mode", choices=["bench", "decode", "paged", "prefill", "swa", "backward", "copy"],
+                    default="bench",
                     help="decode/prefill/copy: run only that workload (for profiling) and print its timing")
     ap.add_argument("--config", type=int, default=0,
                     help="with --mode decode/prefill/backward: BASELINE config id")
@@ -317,6 +345,9 @@ def main():
     if args.mode == "paged":
         print(json.dumps({"mode": "paged", **bench_paged(args.config or 3, args.steps, args.warmup, dev,
                                                           args.page_size, args.kv)}), flush=True)
+        return
+    if args.mode == "swa":
+        print(json.dumps({"mode": "swa", **bench_swa(args.steps, args.warmup, dev)}), flush=True)
         return
     if args.mode == "backward":
         print(json.dumps({"mode": "backward", **bench_backward(args.config or 4, args.steps, args.warmup, dev)}),
@@ -355,6 +386,8 @@ def main():
     if not args.no_paged:
         line["decode_paged"] = [bench_paged(3, max(5, args.steps // 5), 2, dev, 16, kv)
                                 for kv in ("bf16", "fp8")]
+    if not args.no_swa:
+        line["swa"] = bench_swa(max(5, args.steps // 2), max(2, args.warmup // 2), dev)
     if not args.no_backward:
         line["backward"] = bench_backward(4, max(5, args.steps // 2), max(2, args.warmup // 2), dev)
     if not args.no_cpu:

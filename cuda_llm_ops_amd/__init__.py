@@ -14,6 +14,7 @@ from .flash_gqa import (  # noqa: F401
     launch_decode_flash_gqa_bf16_kernel,
     launch_flash_gqa_backward_bf16_kernel,
     launch_flash_gqa_forward_bf16_kernel,
+    launch_flash_swa_forward_bf16_kernel,
     paged_decode_workspace_bytes,
     prepare_backward,
     prepare_decode,

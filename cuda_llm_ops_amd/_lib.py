@@ -67,6 +67,8 @@ class PrefillArgs(ctypes.Structure):
         ("k_stride", _I64x3),
         ("v_stride", _I64x3),
         ("o_stride", _I64x3),
+        ("window_size", ctypes.c_int32),
+        ("sink", ctypes.c_void_p),
     ]
 
 

@@ -55,6 +55,8 @@ struct PrefillParams {
     int n_streams;   // n_hgroups * hkv * batch
     float scale_log2;   // |scale| * log2(e)
     uint32_t q_sign;    // 0x80008000 when scale < 0 (Q is negated on load), else 0
+    int window;         // > 0: sliding window, row i sees keys [i - window + 1, i] (causal)
+    const float* sink;  // nullable [Hq]: added to the softmax denominator as sink * exp(-max)
 };
 
 constexpr int kPfWaves = 4;                          // waves per group (one unit's rows)
@@ -79,7 +81,9 @@ static_assert(kPfWaves * kPfMergeFloats * kWave * 4 <= 2 * kPfGroupBytes, "merge
 // One unit (query block qb of head group hg, kv head kvh, batch b).  With
 // kGroups == 2, group `grp` covers tiles [grp*half, grp*half + half) of the
 // unit's KV range; tiles past the range are fully masked and add nothing.
-template <int kGroups>
+// kSwa: sliding window and/or sink (a separate instantiation, so the plain
+// causal kernels carry none of its work).
+template <int kGroups, bool kSwa>
 __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* smem_all, int qb, int hg, int kvh,
                                         int b) {
     const int tid = threadIdx.x;
@@ -99,9 +103,11 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
 
     int kv_end = p.skv;
     if (p.causal) kv_end = min(kv_end, min(q_wg0 + qrows, p.sq));
-    const int unit_tiles = (kv_end + kPfTile - 1) / kPfTile;
+    // a sliding window starts the unit at the tile holding its first row's first key
+    const int t_lo = (kSwa && p.window > 0) ? max(0, q_wg0 - p.window + 1) / kPfTile : 0;
+    const int unit_tiles = max(0, (kv_end + kPfTile - 1) / kPfTile - t_lo);
     const int n_tiles = kGroups == 1 ? unit_tiles : (unit_tiles + 1) / 2;   // loop trips, same for both groups
-    const int t_first = grp * n_tiles;                                        // first tile of this group
+    const int t_first = t_lo + grp * n_tiles;                                 // first tile of this group
     // keys this group may use: the unit's range, cut at the group's last tile
     const int kv_hi = min(kv_end, (t_first + n_tiles) * kPfTile);
 
@@ -205,18 +211,23 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
 #pragma unroll
         for (int i = 0; i < 16; ++i) oacc[db][i] = 0.f;
 
-    // Causal / tail mask of S(j), in place (only tiles that cross a boundary).
+    // Causal / window / tail mask of S(j), in place (only tiles that cross a boundary).
     auto mask = [&](f32x16_t (&s)[2], int j) {
         const int kv0 = (t_first + j) * kPfTile;
-        const bool need_mask = (kv0 + kPfTile > kv_hi) || (p.causal && kv0 + kPfTile - 1 > q0w);
+        bool need_mask = (kv0 + kPfTile > kv_hi) || (p.causal && kv0 + kPfTile - 1 > q0w);
+        if constexpr (kSwa) need_mask = need_mask || (p.window > 0 && kv0 < q0w + 32 - p.window);
         if (need_mask) {
-            // tokens at or past `lim` (relative to this lane's first token) are masked
+            // tokens at or past `lim`, or (window) before `lo`, relative to
+            // this lane's first token, are masked
             const int lim = min(row_lim, kv_hi) - (kv0 + g2 * 4);
+            const int lo = (kSwa && p.window > 0) ? qrow - p.window + 1 - (kv0 + g2 * 4) : -kPfTile;
 #pragma unroll
             for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    if (tb * 32 + (i >> 2) * 8 + (i & 3) >= lim) s[tb][i] = -INFINITY;
+                for (int i = 0; i < 16; ++i) {
+                    const int idx = tb * 32 + (i >> 2) * 8 + (i & 3);
+                    if (idx >= lim || (kSwa && idx < lo)) s[tb][i] = -INFINITY;
+                }
         }
     };
     // Row max of S(j) (log2 units) across both wave halves.
@@ -380,11 +391,17 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
             for (int i = 0; i < 16; ++i) oacc[db][i] = oacc[db][i] * a0 + mg[(db * 16 + i) * kWave] * a1;
         l_run = l_run * a0 + l1 * a1;
         m_run = m;
+        m_use = mu;   // O and the sum are now relative to mu (the sink term uses it)
     }
 
     l_run = half_sum(l_run);
+    // the sink joins the denominator relative to the same reference max:
+    // sum exp(x - m) + sink * exp(-m)  (flash_swa_kernel.py:142-147)
+    const bool has_sink = kSwa && p.sink != nullptr;
+    const float sink = has_sink ? p.sink[h] : 0.f;
+    const float denom = (l_run > 0.f && has_sink) ? l_run + sink * fast_exp2(-m_use) : l_run;
     if (qrow < p.sq) {
-        const float inv = (l_run > 0.f) ? 1.f / l_run : 0.f;
+        const float inv = (l_run > 0.f) ? 1.f / denom : 0.f;
         __bf16* orow = p.o + b * p.o_sb + (int64_t)qrow * p.o_ss + h * p.o_sh;
 #pragma unroll
         for (int db = 0; db < 4; ++db)
@@ -396,7 +413,9 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
                 *reinterpret_cast<bf16x4_t*>(orow + db * 32 + i4 * 8 + g2 * 4) = w;
             }
         if (p.lse != nullptr && g2 == 0)
-            p.lse[((int64_t)b * p.hq + h) * p.sq + qrow] = (l_run > 0.f) ? m_run * kLn2 + logf(l_run) : -INFINITY;
+            p.lse[((int64_t)b * p.hq + h) * p.sq + qrow] =
+                (l_run > 0.f) ? m_run * kLn2 + logf(denom)
+                              : (has_sink ? logf(fmaxf(sink, 1.0e-9f)) : -INFINITY);
     }
 }
 
@@ -415,18 +434,19 @@ __device__ __forceinline__ void pf_block_unit(const PrefillParams& p, int* qb, i
     *b = stream / (p.n_hgroups * p.hkv);
 }
 
+template <bool kSwa>
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     int qb, hg, kvh, b;
     pf_block_unit(p, &qb, &hg, &kvh, &b);
-    pf_unit<1>(p, smem, qb, hg, kvh, b);
+    pf_unit<1, kSwa>(p, smem, qb, hg, kvh, b);
 }
 
 __global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_split_kernel(PrefillParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     int qb, hg, kvh, b;
     pf_block_unit(p, &qb, &hg, &kvh, &b);
-    pf_unit<2>(p, smem, qb, hg, kvh, b);
+    pf_unit<2, false>(p, smem, qb, hg, kvh, b);
 }
 
 namespace {
@@ -438,6 +458,8 @@ int validate_prefill(const fgqa_prefill_args* a) {
         return FGQA_ERR_INVALID_ARGUMENT;
     if (a->num_q_heads % a->num_kv_heads != 0) return FGQA_ERR_INVALID_ARGUMENT;
     if (!isfinite(a->scale)) return FGQA_ERR_INVALID_ARGUMENT;
+    // a sliding window is a causal window (flash_swa_kernel.py: kv <= q)
+    if (a->window_size < 0 || (a->window_size > 0 && !a->causal)) return FGQA_ERR_INVALID_ARGUMENT;
     for (int i = 0; i < 3; ++i)
         if (a->q_stride[i] < 0 || a->k_stride[i] < 0 || a->v_stride[i] < 0 || a->o_stride[i] < 0)
             return FGQA_ERR_INVALID_ARGUMENT;
@@ -499,6 +521,8 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
     p.n_streams = p.n_hgroups * p.hkv * p.batch;
     p.scale_log2 = fabsf(a->scale) * kLog2e;
     p.q_sign = (a->scale < 0.f) ? 0x80008000u : 0u;
+    p.window = a->window_size;
+    p.sink = a->sink;
 
     const int64_t units = (int64_t)p.n_qblocks * p.n_streams;
     if (units >= ((int64_t)1 << 31)) return FGQA_ERR_UNSUPPORTED;
@@ -507,25 +531,32 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
     // Few units (fewer than 4 per CU): split each unit's KV range over two
     // wave groups so a CU never runs a long unit with one wave per SIMD, and
     // let the dispatcher hand heaviest-first units to free CUs.
-    bool split = units < 4 * (int64_t)cus;
-    // FGQA_PREFILL_SPLIT=0/1 forces the choice (tuning and tests).
-    if (const char* e = getenv("FGQA_PREFILL_SPLIT")) split = e[0] == '1';
+    // (A sliding window gives every unit about the same number of tiles:
+    // nothing to balance, so the whole-range kernel is used.)
+    const bool swa = p.window > 0 || p.sink != nullptr;
+    bool split = units < 4 * (int64_t)cus && !swa;
+    // FGQA_PREFILL_SPLIT=0/1 forces the choice (tuning and tests; the window /
+    // sink variant has no split form).
+    if (const char* e = getenv("FGQA_PREFILL_SPLIT")) split = e[0] == '1' && !swa;
 
     const int smem_bytes = (split ? 2 : 1) * kPfGroupBytes;
-    const void* fn = split ? reinterpret_cast<const void*>(prefill_split_kernel)
-                           : reinterpret_cast<const void*>(prefill_kernel);
-    static bool smem_set[2] = {false, false};
-    if (!smem_set[split]) {
-        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, smem_bytes) != hipSuccess)
+    const int which = split ? 2 : (swa ? 1 : 0);
+    const void* fns[3] = {reinterpret_cast<const void*>(prefill_kernel<false>),
+                          reinterpret_cast<const void*>(prefill_kernel<true>),
+                          reinterpret_cast<const void*>(prefill_split_kernel)};
+    static bool smem_set[3] = {false, false, false};
+    if (!smem_set[which]) {
+        if (hipFuncSetAttribute(fns[which], hipFuncAttributeMaxDynamicSharedMemorySize, smem_bytes) != hipSuccess)
             return FGQA_ERR_HIP;
-        smem_set[split] = true;
+        smem_set[which] = true;
     }
+    const hipStream_t s = static_cast<hipStream_t>(stream);
     if (split)
-        hipLaunchKernelGGL(prefill_split_kernel, dim3((unsigned)units), dim3(2 * kPfThreads), smem_bytes,
-                           static_cast<hipStream_t>(stream), p);
+        hipLaunchKernelGGL(prefill_split_kernel, dim3((unsigned)units), dim3(2 * kPfThreads), smem_bytes, s, p);
+    else if (swa)
+        hipLaunchKernelGGL(prefill_kernel<true>, dim3((unsigned)units), dim3(kPfThreads), smem_bytes, s, p);
     else
-        hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)units), dim3(kPfThreads), smem_bytes,
-                           static_cast<hipStream_t>(stream), p);
+        hipLaunchKernelGGL(prefill_kernel<false>, dim3((unsigned)units), dim3(kPfThreads), smem_bytes, s, p);
     if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
     return FGQA_OK;
 }

@@ -7,6 +7,7 @@ Two families of entry points:
     - ``launch_flash_gqa_forward_bf16_kernel`` <- src/python/Triton/flash_gqa_kernel.py:185-338
     - ``launch_decode_flash_gqa_bf16_kernel``  <- src/python/Triton/decode_flash_gqa_kernel.py:137-196
     - ``launch_flash_gqa_backward_bf16_kernel`` <- src/python/Triton/flash_gqa_backward_kernel.py:312-478
+    - ``launch_flash_swa_forward_bf16_kernel``  <- src/python/Triton/SWA/flash_swa_kernel.py:185-366
 * The C++ layouts of the reference's C++ decode entry point (Q/O ``[B,Hq,D]``,
   K/V ``[B,S,Hkv,D]``, decode_flash_gqa_kernel.cuh:28-38) and of the new C++
   prefill entry point (BSHD):
@@ -31,6 +32,7 @@ __all__ = [
     "launch_flash_gqa_forward_bf16_kernel",
     "launch_decode_flash_gqa_bf16_kernel",
     "launch_flash_gqa_backward_bf16_kernel",
+    "launch_flash_swa_forward_bf16_kernel",
     "decode_flash_gqa_bshd",
     "decode_flash_gqa_paged",
     "paged_decode_workspace_bytes",
@@ -328,7 +330,7 @@ def launch_decode_flash_gqa_bf16_kernel(q, k, v, out=None):
 
 
 # --------------------------------------------------------------------------- prefill
-def _prefill_args(q, k, v, o, lse, scale, causal, layout) -> _lib.PrefillArgs:
+def _prefill_args(q, k, v, o, lse, scale, causal, layout, window_size=0, sink=None) -> _lib.PrefillArgs:
     """C ABI argument block for q/k/v/o 4-D in `layout` ('bshd' or 'bhsd')."""
     def sbh(t):
         if layout == "bshd":
@@ -351,15 +353,27 @@ def _prefill_args(q, k, v, o, lse, scale, causal, layout) -> _lib.PrefillArgs:
     a.k_stride[:] = sbh(k)
     a.v_stride[:] = sbh(v)
     a.o_stride[:] = sbh(o)
+    a.window_size = int(window_size)
+    a.sink = _ptr(sink)
     return a
 
 
-def _prefill(q, k, v, o, lse, scale, causal, layout):
-    a = _prefill_args(q, k, v, o, lse, scale, causal, layout)
+def _prefill(q, k, v, o, lse, scale, causal, layout, window_size=0, sink=None):
+    a = _prefill_args(q, k, v, o, lse, scale, causal, layout, window_size, sink)
     _lib.check(_lib.lib().fgqa_prefill_bf16(ctypes.byref(a), ctypes.c_void_p(_stream())), "fgqa_prefill_bf16")
 
 
-def _prefill_bshd_prepare(q, k, v, scale, out, lse, causal):
+def _check_sink(sink, hq, dev):
+    if sink is None:
+        return None
+    if not isinstance(sink, torch.Tensor) or sink.dim() != 1 or sink.numel() != hq:
+        raise ValueError(f"sink must be a 1D tensor with {hq} elements")
+    if sink.device != dev:
+        raise ValueError("sink must be on the same device as Q")
+    return sink.to(torch.float32).contiguous()
+
+
+def _prefill_bshd_prepare(q, k, v, scale, out, lse, causal, window_size=0, sink=None):
     if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
         raise ValueError("Flash GQA forward expects bf16 inputs")
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
@@ -381,21 +395,24 @@ def _prefill_bshd_prepare(q, k, v, scale, out, lse, causal):
         lse = torch.empty((B, Hq, Sq), device=q.device, dtype=torch.float32)
     elif lse.shape != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
         raise ValueError("LSE must be a contiguous fp32 [batch, q_heads, seqlen_q] tensor")
-    a = _prefill_args(q, k, v, out, lse, scale, causal, "bshd")
-    return a, out, lse, (q, k, v, out, lse)
+    sink = _check_sink(sink, Hq, q.device)
+    a = _prefill_args(q, k, v, out, lse, scale, causal, "bshd", window_size, sink)
+    return a, out, lse, (q, k, v, out, lse, sink)
 
 
-def flash_gqa_forward_bshd(q, k, v, scale=None, out=None, lse=None, causal=True):
-    """Prefill forward in BSHD: q [B,Sq,Hq,D], k/v [B,Skv,Hkv,D] -> (out [B,Sq,Hq,D], lse [B,Hq,Sq])."""
-    a, out, lse, _keep = _prefill_bshd_prepare(q, k, v, scale, out, lse, causal)
+def flash_gqa_forward_bshd(q, k, v, scale=None, out=None, lse=None, causal=True, window_size=0, sink=None):
+    """Prefill forward in BSHD: q [B,Sq,Hq,D], k/v [B,Skv,Hkv,D] -> (out [B,Sq,Hq,D], lse [B,Hq,Sq]).
+    window_size > 0 (causal only): row i sees keys [i - window_size + 1, i]; sink: optional
+    fp32 [Hq] added to the softmax denominator as sink * exp(-max) (the reference's SWA kernel)."""
+    a, out, lse, _keep = _prefill_bshd_prepare(q, k, v, scale, out, lse, causal, window_size, sink)
     _lib.check(_lib.lib().fgqa_prefill_bf16(ctypes.byref(a), ctypes.c_void_p(_stream())), "fgqa_prefill_bf16")
     return out, lse
 
 
-def prepare_prefill(q, k, v, scale=None, out=None, lse=None, causal=True):
+def prepare_prefill(q, k, v, scale=None, out=None, lse=None, causal=True, window_size=0, sink=None):
     """``flash_gqa_forward_bshd`` validated once; returns a ``PreparedLaunch``
     whose ``out`` is the output tensor (the LSE tensor is ``.lse``)."""
-    a, out, lse, keep = _prefill_bshd_prepare(q, k, v, scale, out, lse, causal)
+    a, out, lse, keep = _prefill_bshd_prepare(q, k, v, scale, out, lse, causal, window_size, sink)
     pl = PreparedLaunch(_lib.lib().fgqa_prefill_bf16, a, keep, out, "fgqa_prefill_bf16")
     pl.lse = lse
     return pl
@@ -655,3 +672,97 @@ def launch_flash_gqa_backward_bf16_kernel(q, k, v, o, lse, grad_o, scale=None, c
     if squeeze_output:
         return dq.squeeze(0), dk.squeeze(0), dv.squeeze(0)
     return dq, dk, dv
+
+
+# --------------------------------------------------------------------------- sliding window + sink
+def launch_flash_swa_forward_bf16_kernel(q, k, v, scale=None, out=None, lse=None, window_size=None,
+                                         sink_value=None, block_kv_sub=16, num_warps=4, num_stages=3):
+    """Mirror of the reference's Triton SWA launcher
+    (src/python/Triton/SWA/flash_swa_kernel.py:185-366): causal sliding-window
+    attention (row i sees keys [i - window_size + 1, i]) with a per-head sink
+    in the softmax denominator; BHSD q [B,Hq,Sq,D] (or 3-D), k/v [B,Hkv,Skv,D];
+    returns (out, lse [B,Hq,Sq]).
+
+    Same checks and ValueError messages as the reference.  ``block_kv_sub``,
+    ``num_warps`` and ``num_stages`` are Triton tuning knobs, accepted for
+    signature compatibility only.  Beyond the reference, window_size must be
+    positive (the reference masks every key for 0) and head_dim_v must equal
+    head_dim_qk (128).
+    """
+    del block_kv_sub, num_warps, num_stages
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise ValueError("Flash SWA forward expects bf16 inputs")
+    if q.dim() not in (3, 4):
+        raise ValueError("Q must be 3D or 4D")
+    if k.dim() != q.dim() or v.dim() != q.dim():
+        raise ValueError("Q, K, and V must have matching ranks")
+    squeeze_output = q.dim() == 3
+    qb = q.unsqueeze(0) if squeeze_output else q
+    kb = k.unsqueeze(0) if squeeze_output else k
+    vb = v.unsqueeze(0) if squeeze_output else v
+    batch, q_heads, seqlen_q, head_dim_qk = qb.shape
+    _, num_kv_heads, seqlen_kv, k_head_dim = kb.shape
+    _, v_heads, v_seqlen, head_dim_v = vb.shape
+    if seqlen_kv != v_seqlen:
+        raise ValueError("K and V must share sequence length")
+    if k_head_dim != head_dim_qk:
+        raise ValueError("Q and K must share head_dim_qk")
+    if v_heads != num_kv_heads:
+        raise ValueError("K and V must share number of KV heads")
+    if q_heads % num_kv_heads != 0:
+        raise ValueError("Query heads must be divisible by KV heads")
+    if window_size is None:
+        raise ValueError("window_size must be provided")
+    if sink_value is None:
+        raise ValueError("sink_value must be provided")
+    if int(window_size) <= 0:
+        raise ValueError("window_size must be positive")
+    if head_dim_v != head_dim_qk:
+        raise ValueError("head_dim_v must equal head_dim_qk on this path")
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim_qk)
+    if out is None:
+        out_b = torch.empty((batch, q_heads, seqlen_q, head_dim_v), device=qb.device, dtype=torch.bfloat16)
+    else:
+        if squeeze_output:
+            if out.dim() != 3:
+                raise ValueError("Output must be 3D when Q is 3D")
+            out_b = out.unsqueeze(0)
+        else:
+            if out.dim() != 4:
+                raise ValueError("Output must be 4D when Q is 4D")
+            out_b = out
+        if out_b.dtype != torch.bfloat16 or not _kernel_ready(out_b):
+            raise ValueError("Output must be bf16 with contiguous, 16-byte aligned rows")
+    if out_b.shape != (batch, q_heads, seqlen_q, head_dim_v):
+        raise ValueError("Output must have shape [batch, q_heads, seqlen_q, head_dim_v]")
+    if lse is None:
+        lse_b = torch.empty((batch, q_heads, seqlen_q), device=qb.device, dtype=torch.float32)
+    else:
+        if squeeze_output:
+            if lse.dim() != 2:
+                raise ValueError("LSE must be 2D when Q is 3D")
+            lse_b = lse.unsqueeze(0)
+        else:
+            if lse.dim() != 3:
+                raise ValueError("LSE must be 3D when Q is 4D")
+            lse_b = lse
+        if lse_b.dtype != torch.float32 or not lse_b.is_contiguous():
+            raise ValueError("LSE must be a contiguous fp32 tensor")
+    if lse_b.shape != (batch, q_heads, seqlen_q):
+        raise ValueError("LSE must have shape [batch, q_heads, seqlen_q]")
+    if not isinstance(sink_value, torch.Tensor):
+        raise ValueError("sink_value must be a torch.Tensor")
+    if sink_value.dim() != 1:
+        raise ValueError("sink_value must be a 1D tensor with shape [q_heads]")
+    if sink_value.numel() != q_heads:
+        raise ValueError(f"sink_value must have {q_heads} elements")
+    if sink_value.device != qb.device:
+        raise ValueError("sink_value must be on the same device as Q")
+    _require_cuda(qb, kb, vb)
+    sink = sink_value.to(torch.float32).contiguous()
+    qb, kb, vb = _prep(qb), _prep(kb), _prep(vb)
+    _prefill(qb, kb, vb, out_b, lse_b, scale, True, "bhsd", int(window_size), sink)
+    if squeeze_output:
+        return out_b.squeeze(0), lse_b.squeeze(0)
+    return out_b, lse_b

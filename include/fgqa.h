@@ -154,6 +154,13 @@ int fgqa_decode_paged(const fgqa_decode_paged_args* args, void* stream);
  *           reference's q_idx >= kv_idx mask).  A row with no visible key
  *           (Skv == 0) yields O = 0 and lse = -inf.
  * BHSD (the Triton layout) is q_stride = {Hq*Sq*D, D, Sq*D} etc.
+ *   window_size  0: none.  > 0 (causal only): sliding window, row i sees keys
+ *           [i - window_size + 1, i], as the reference's
+ *           src/python/Triton/SWA/flash_swa_kernel.py:15-160.
+ *   sink    nullable device fp32 [Hq]: per-head sink added to the softmax
+ *           denominator, sum_j exp(s_j - m) + sink * exp(-m); lse includes it.
+ *           A row with no visible key then gives O = 0, lse = log(max(sink, 1e-9)).
+ *   Callers that zero the struct get neither.
  */
 typedef struct fgqa_prefill_args {
     const void* q;
@@ -173,6 +180,8 @@ typedef struct fgqa_prefill_args {
     int64_t k_stride[3];
     int64_t v_stride[3];
     int64_t o_stride[3];
+    int32_t window_size;
+    const float* sink;
 } fgqa_prefill_args;
 
 int fgqa_prefill_bf16(const fgqa_prefill_args* args, void* stream);

@@ -16,4 +16,5 @@ from .oracle import (  # noqa: F401
     normal_bf16,
     prefill,
     prefill_backward,
+    prefill_swa,
 )

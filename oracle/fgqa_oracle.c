@@ -317,6 +317,69 @@ int fgqa_oracle_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_
     return 0;
 }
 
+/* Sliding-window + sink prefill (see the header for the reference lines). */
+int fgqa_oracle_prefill_swa_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                 float scale, uint16_t* o, float* lse,
+                                 int batch, int sq, int skv, int hq, int hkv, int d,
+                                 const int64_t* qs, const int64_t* ks,
+                                 const int64_t* vs, const int64_t* os,
+                                 int window, const float* sink, int q_offset, int nthreads) {
+    if (!q || !k || !v || !o || !qs || !ks || !vs || !os) return -1;
+    if (batch < 0 || sq < 0 || skv < 0 || hq <= 0 || hkv <= 0 || d <= 0 || d > ORACLE_MAX_D) return -1;
+    if (hq % hkv != 0 || window <= 0) return -1;
+    const int group = hq / hkv;
+    set_threads(nthreads);
+
+#pragma omp parallel
+    {
+        float* sc = (float*)malloc(sizeof(float) * (size_t)(skv > 0 ? skv : 1));
+        float out[ORACLE_MAX_D];
+#pragma omp for collapse(3) schedule(dynamic, 4)
+        for (int b = 0; b < batch; ++b) {
+            for (int h = 0; h < hq; ++h) {
+                for (int i = 0; i < sq; ++i) {
+                    const int kvh = h / group;
+                    const uint16_t* qrow = q + b * qs[0] + (int64_t)i * qs[1] + h * qs[2];
+                    uint16_t* orow = o + b * os[0] + (int64_t)i * os[1] + h * os[2];
+                    const long pos = (long)i + q_offset;        /* keys j <= pos, j > pos - window */
+                    const int j1 = (pos + 1 < skv) ? (int)(pos + 1) : skv;
+                    const int j0 = (pos - window + 1 > 0) ? (int)(pos - window + 1) : 0;
+                    const float sk = sink ? sink[h] : 0.f;
+                    if (j0 >= j1) {
+                        for (int x = 0; x < d; ++x) orow[x] = 0;
+                        if (lse) lse[((size_t)b * hq + h) * sq + i] = sink ? logf(fmaxf(sk, 1.0e-9f)) : -INFINITY;
+                        continue;
+                    }
+                    float rmax = -INFINITY;
+                    for (int j = j0; j < j1; ++j) {
+                        const uint16_t* krow = k + b * ks[0] + (int64_t)j * ks[1] + kvh * ks[2];
+                        float acc = 0.f;
+                        for (int x = 0; x < d; ++x) acc += bf(qrow[x]) * bf(krow[x]);
+                        sc[j] = acc * scale;
+                        rmax = fmaxf(rmax, sc[j]);
+                    }
+                    float sum = 0.f;
+                    for (int j = j0; j < j1; ++j) {
+                        sc[j] = expf(sc[j] - rmax);
+                        sum += sc[j];
+                    }
+                    if (sink) sum = sum + sk * expf(-rmax);
+                    for (int x = 0; x < d; ++x) out[x] = 0.f;
+                    for (int j = j0; j < j1; ++j) {
+                        const uint16_t* vrow = v + b * vs[0] + (int64_t)j * vs[1] + kvh * vs[2];
+                        const float pj = sc[j] / sum;
+                        for (int x = 0; x < d; ++x) out[x] += pj * bf(vrow[x]);
+                    }
+                    for (int x = 0; x < d; ++x) orow[x] = fgqa_oracle_f32_to_bf16(out[x]);
+                    if (lse) lse[((size_t)b * hq + h) * sq + i] = logf(sum) + rmax;
+                }
+            }
+        }
+        free(sc);
+    }
+    return 0;
+}
+
 /* Softmax attention in double: the exact answer both fp32 paths approximate. */
 int fgqa_oracle_attention_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                               double scale, double* o, double* lse,

@@ -31,6 +31,10 @@
  *                                            contiguous bf16 cache; page-permutation
  *                                            invariance; fp8 path vs the fp64 brute force
  *                                            on the decoded values
+ *   fgqa_oracle_prefill_swa_bf16            bit-identical to fgqa_oracle_prefill_bf16 for a
+ *                                            window >= Sq and no sink; a float64 numpy
+ *                                            restatement with the window and sink; closed
+ *                                            forms (window 1: O = V[i] / (1 + sink e^-s_ii))
  *   fgqa_oracle_attention_f64               textbook softmax attention in double;
  *                                            pinned by numpy float64 restatement and
  *                                            closed forms on tiny inputs
@@ -166,6 +170,25 @@ int fgqa_oracle_attention_backward_f64(const uint16_t* q, const uint16_t* k, con
                                        const int64_t* q_strides, const int64_t* k_strides,
                                        const int64_t* v_strides, const int64_t* o_strides,
                                        const int64_t* grad_o_strides, int causal, int nthreads);
+
+/*
+ * Causal sliding-window prefill with a per-head sink, restating the reference's
+ * torch reference examples/python/Triton/test_flash_swa_kernel.py:97-116:
+ *   scores = (q . k) * scale (fp32), masked to keys [i - window + 1, i];
+ *   row_max; e = exp(scores - row_max);
+ *   denom = sum(e) + sink[h] * exp(-row_max); probs = e / denom;
+ *   lse = log(denom) + row_max;  out = probs . v (fp32) -> bf16.
+ * sink: host fp32 [Hq] or NULL (no sink).  Layouts and strides as
+ * fgqa_oracle_prefill_bf16; query row i sits at position i + q_offset.  A row with no visible key gives O = 0 and
+ * lse = log(max(sink, 1e-9)) (the reference kernel's convention,
+ * src/python/Triton/SWA/flash_swa_kernel.py:150-155), or -inf without a sink.
+ */
+int fgqa_oracle_prefill_swa_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                 float scale, uint16_t* o, float* lse,
+                                 int batch, int sq, int skv, int hq, int hkv, int d,
+                                 const int64_t* q_strides, const int64_t* k_strides,
+                                 const int64_t* v_strides, const int64_t* o_strides,
+                                 int window, const float* sink, int q_offset, int nthreads);
 
 /*
  * Textbook softmax attention in double precision (the mathematical answer the

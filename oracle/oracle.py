@@ -74,6 +74,11 @@ def lib() -> ctypes.CDLL:
             _u16p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, _i32p, ctypes.c_int64, ctypes.c_int,
             _i64p, _i64p, ctypes.c_float, ctypes.c_float, ctypes.c_float, _u16p, _f32p,
             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _i32p, ctypes.c_int, ctypes.c_int]
+        L.fgqa_oracle_prefill_swa_bf16.restype = ctypes.c_int
+        L.fgqa_oracle_prefill_swa_bf16.argtypes = [
+            _u16p, _u16p, _u16p, ctypes.c_float, _u16p, _f32p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            _i64p, _i64p, _i64p, _i64p, ctypes.c_int, _f32p, ctypes.c_int, ctypes.c_int]
         _lib = L
     return _lib
 
@@ -286,4 +291,27 @@ def decode_paged(q, k_cache, v_cache, block_table, seqlens, scale, k_scale=1.0, 
         int(tile), int(nthreads))
     if rc != 0:
         raise ValueError("fgqa_oracle_decode_paged: invalid arguments")
+    return o, lse
+
+
+def prefill_swa(q, k, v, scale, window, sink=None, layout="bshd", q_offset=0, nthreads=0):
+    """Sliding-window (+ sink) prefill oracle.  sink: float32 [Hq] or None.
+    Returns (o in q's layout, lse [B,Hq,Sq])."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    B, Sq, Hq, D = _dims(q, layout)
+    _, Skv, Hkv, _ = _dims(k, layout)
+    o = np.empty_like(q)
+    lse = np.empty((B, Hq, Sq), dtype=np.float32)
+    sk = None if sink is None else np.ascontiguousarray(sink, dtype=np.float32)
+    qs, ks, vs, os_ = (_strides(x, layout) for x in (q, k, v, o))
+    rc = lib().fgqa_oracle_prefill_swa_bf16(
+        _ptr(q, ctypes.c_uint16), _ptr(k, ctypes.c_uint16), _ptr(v, ctypes.c_uint16),
+        float(scale), _ptr(o, ctypes.c_uint16), _ptr(lse, ctypes.c_float),
+        B, Sq, Skv, Hq, Hkv, D,
+        _ptr(qs, ctypes.c_int64), _ptr(ks, ctypes.c_int64), _ptr(vs, ctypes.c_int64),
+        _ptr(os_, ctypes.c_int64), int(window), _ptr(sk, ctypes.c_float), int(q_offset), int(nthreads))
+    if rc != 0:
+        raise ValueError("fgqa_oracle_prefill_swa_bf16: invalid arguments")
     return o, lse

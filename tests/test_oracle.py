@@ -544,3 +544,65 @@ def test_paged_oracle_fp8_against_f64():
     bt_bad[0, 3] = next(pg for pg in range(kc.shape[0]) if pg not in used)
     bad, _ = oracle.decode_paged(q, kc, vc, bt_bad, lens, SCALE, k_scale=ks, v_scale=vs)
     assert not within_tol(oracle.bf16_to_f32(bad)[0], ref[0])
+
+
+# ----------------------------------------------------------------- sliding window + sink oracle
+def _swa_numpy_f64(q, k, v, scale, window, sink):
+    """float64 restatement of test_flash_swa_kernel.py:97-116 (BSHD)."""
+    qf, kf, vf = (oracle.bf16_to_f32(x).astype(np.float64) for x in (q, k, v))
+    B, Sq, Hq, D = qf.shape
+    Skv, Hkv = kf.shape[1], kf.shape[2]
+    G = Hq // Hkv
+    o = np.zeros((B, Sq, Hq, D))
+    lse = np.zeros((B, Hq, Sq))
+    for b in range(B):
+        for h in range(Hq):
+            s = qf[b, :, h] @ kf[b, :, h // G].T * scale
+            ii, jj = np.meshgrid(np.arange(Sq), np.arange(Skv), indexing="ij")
+            s = np.where((jj <= ii) & (jj >= ii - (window - 1)), s, -np.inf)
+            for i in range(Sq):
+                if np.all(np.isneginf(s[i])):
+                    lse[b, h, i] = math.log(max(sink[h], 1e-9))
+                    continue
+                m = s[i].max()
+                e = np.exp(s[i] - m)
+                den = e.sum() + sink[h] * math.exp(-m)
+                o[b, i, h] = (e / den) @ vf[b, :, h // G]
+                lse[b, h, i] = math.log(den) + m
+    return o, lse
+
+
+def test_swa_oracle_reduces_to_causal_prefill():
+    """A window covering the whole sequence and no sink: the causal prefill oracle, bit for bit."""
+    q, k, v = _prefill_inputs(71, 2, 150, 150, 4, 2)
+    o, lse = oracle.prefill(q, k, v, SCALE, causal=True)
+    ow, lw = oracle.prefill_swa(q, k, v, SCALE, window=150)
+    assert np.array_equal(o, ow) and np.array_equal(lse, lw)
+
+
+@pytest.mark.parametrize("window,sq,skv", [(1, 40, 40), (7, 60, 60), (32, 90, 90), (16, 50, 30)])
+def test_swa_oracle_vs_numpy_f64(window, sq, skv):
+    q, k, v = _prefill_inputs(73 + window, 1, sq, skv, 4, 2, D=32)
+    sink = np.array([0.5, 2.0, 1e-6, 30.0], dtype=np.float32)
+    o, lse = oracle.prefill_swa(q, k, v, 0.2, window=window, sink=sink)
+    of, lf = _swa_numpy_f64(q, k, v, 0.2, window, sink)
+    assert_close(oracle.bf16_to_f32(o), of, f"swa window={window}")
+    assert np.max(np.abs(lse - lf)) < 1e-4
+    if window == 1:
+        # closed form: row i sees only key i: O = V[i] / (1 + sink exp(-s_ii))
+        qf, kf, vf = (oracle.bf16_to_f32(x).astype(np.float64) for x in (q, k, v))
+        s = np.einsum("bihd,bihd->bih", qf, np.repeat(kf, 2, axis=2)) * 0.2
+        ref = vf.repeat(2, axis=2) / (1 + sink[None, None, :, None] * np.exp(-s)[..., None])
+        assert_close(oracle.bf16_to_f32(o), ref, "swa window=1 closed form")
+    # planted mistakes: window off by one, sink dropped, sink taken as a logit
+    bad, _ = oracle.prefill_swa(q, k, v, 0.2, window=window + 1, sink=sink)
+    if window < sq:
+        assert not within_tol(oracle.bf16_to_f32(bad), of)
+    bad, _ = oracle.prefill_swa(q, k, v, 0.2, window=window, sink=None)
+    assert not within_tol(oracle.bf16_to_f32(bad), of)
+    bad, _ = oracle.prefill_swa(q, k, v, 0.2, window=window, sink=np.exp(sink))
+    assert not within_tol(oracle.bf16_to_f32(bad), of)
+    if sq > skv + window - 1:   # rows past every window: O = 0, lse = log(max(sink, 1e-9))
+        r = skv + window - 1
+        assert np.all(o[:, r:] == 0)
+        assert np.allclose(lse[:, :, r:], np.log(np.maximum(sink, 1e-9))[None, :, None])
