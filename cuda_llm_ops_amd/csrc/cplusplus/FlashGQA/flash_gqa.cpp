@@ -173,4 +173,38 @@ void LaunchFlashGqaBackwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf
     g_last_status = fgqa_prefill_backward_bf16(&a, nullptr);
 }
 
+void LaunchFlashSwaForwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf16_t* v, float scale, bf16_t* o,
+                                     float* lse, int batchSize, int seqLengthQ, int seqLengthKv, int numQueryHeads,
+                                     int numKvHeads, int headDim, int windowSize, const float* sink) {
+    fgqa_prefill_args a;
+    std::memset(&a, 0, sizeof(a));
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.o = o;
+    a.lse = lse;
+    a.batch = batchSize;
+    a.seqlen_q = seqLengthQ;
+    a.seqlen_kv = seqLengthKv;
+    a.num_q_heads = numQueryHeads;
+    a.num_kv_heads = numKvHeads;
+    a.head_dim = headDim;
+    a.causal = 1;
+    a.scale = scale;
+    const int64_t qs[3] = {(int64_t)seqLengthQ * numQueryHeads * headDim, (int64_t)numQueryHeads * headDim, headDim};
+    const int64_t ks[3] = {(int64_t)seqLengthKv * numKvHeads * headDim, (int64_t)numKvHeads * headDim, headDim};
+    for (int i = 0; i < 3; ++i) {
+        a.q_stride[i] = a.o_stride[i] = qs[i];
+        a.k_stride[i] = a.v_stride[i] = ks[i];
+    }
+    // the window must be positive here (0 means "no window" in the C ABI)
+    if (windowSize <= 0) {
+        g_last_status = FGQA_ERR_INVALID_ARGUMENT;
+        return;
+    }
+    a.window_size = windowSize;
+    a.sink = sink;
+    g_last_status = fgqa_prefill_bf16(&a, nullptr);
+}
+
 int FlashGqaGetLastStatus() { return g_last_status; }

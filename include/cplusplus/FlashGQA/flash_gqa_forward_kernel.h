@@ -62,3 +62,25 @@ void LaunchFlashGqaForwardBf16KernelStrided(const bf16_t* q,
                                             const int64_t kStride[3],
                                             const int64_t vStride[3],
                                             const int64_t oStride[3]);
+
+/**
+ * @brief Sliding-window prefill with a per-head sink (BSHD), the C++
+ *        counterpart of the reference's Triton-only SWA launcher
+ *        (src/python/Triton/SWA/flash_swa_kernel.py:185-366): causal, row i
+ *        sees keys [i - windowSize + 1, i]; sink (nullable device fp32
+ *        [numQueryHeads]) joins the softmax denominator as sink * exp(-max).
+ */
+void LaunchFlashSwaForwardBf16Kernel(const bf16_t* q,
+                                     const bf16_t* k,
+                                     const bf16_t* v,
+                                     float scale,
+                                     bf16_t* o,
+                                     float* lse,
+                                     int batchSize,
+                                     int seqLengthQ,
+                                     int seqLengthKv,
+                                     int numQueryHeads,
+                                     int numKvHeads,
+                                     int headDim,
+                                     int windowSize,
+                                     const float* sink);

@@ -43,7 +43,7 @@ def test_cplusplus_entry_points_exported():
     assert set(decls) == {"LaunchFlashGqaBf16Kernel", "LaunchFlashGqaBf16KernelVarlen", "FlashGqaGetLastStatus",
                           "LaunchFlashGqaBf16KernelPaged",
                           "LaunchFlashGqaForwardBf16Kernel", "LaunchFlashGqaForwardBf16KernelStrided",
-                          "LaunchFlashGqaBackwardBf16Kernel"}
+                          "LaunchFlashGqaBackwardBf16Kernel", "LaunchFlashSwaForwardBf16Kernel"}
     for d in decls:
         assert re.search(rf"\bT {d}\(", syms), d
     # the drop-in keeps the reference's exact parameter list
@@ -149,6 +149,8 @@ def _prefill_args(**kw):
     a.v_stride[:] = [Skv * Hkv * D, Hkv * D, D]
     for name in ("q", "k", "v", "o"):
         setattr(a, name, kw.get(name, 4096))
+    a.window_size = kw.get("window", 0)
+    a.causal = kw.get("causal", 1)
     return a
 
 
@@ -159,6 +161,8 @@ def _prefill_args(**kw):
     (dict(D=256), _lib.FGQA_ERR_UNSUPPORTED),
     (dict(v=None), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(o=4096 + 8), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(window=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(window=64, causal=0), _lib.FGQA_ERR_INVALID_ARGUMENT),   # a window is causal
 ])
 def test_prefill_rejects_before_launch(kw, code):
     assert _lib.lib().fgqa_prefill_bf16(ctypes.byref(_prefill_args(**kw)), None) == code

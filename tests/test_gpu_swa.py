@@ -114,3 +114,35 @@ def test_swa_reference_shape_full_size(cuda):
                                           from_torch_bf16(v[:, k0:r1]), SCALE, W, sk, q_offset=r0 - k0)
         _check(from_torch_bf16(out[:, r0:r1]), lse[:, :, r0:r1].cpu().numpy(), o_ref, l_ref,
                f"swa full size rows {r0}:{r1}")
+
+
+def test_swa_cplusplus_entry(cuda):
+    """LaunchFlashSwaForwardBf16Kernel (BSHD, default stream)."""
+    import ctypes
+
+    import torch
+    fg = _fg()
+    L = fg.lib()
+    print("swa C++ entry", flush=True)
+    B, S, Hq, Hkv, W = 1, 320, 8, 1, 40
+    q = oracle.normal_bf16(1300, (B, S, Hq, 128))
+    k = oracle.normal_bf16(1300, (B, S, Hkv, 128), stream=1)
+    v = oracle.normal_bf16(1300, (B, S, Hkv, 128), stream=2)
+    sink = np.linspace(0.5, 2.0, Hq).astype(np.float32)
+    o_ref, l_ref = oracle.prefill_swa(q, k, v, SCALE, W, sink)
+    qd, kd, vd = (to_torch_bf16(x, cuda) for x in (q, k, v))
+    sd = torch.from_numpy(sink).to(cuda)
+    od = torch.zeros_like(qd)
+    ld = torch.zeros((B, Hq, S), dtype=torch.float32, device=cuda)
+    fn = getattr(L, "_Z31LaunchFlashSwaForwardBf16KernelPK6bf16_tS1_S1_fPS_PfiiiiiiiPKf")
+    fn.restype = None
+    st = getattr(L, "_Z21FlashGqaGetLastStatusv")
+    st.restype = ctypes.c_int
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    torch.cuda.synchronize()
+    fn(p(qd), p(kd), p(vd), ctypes.c_float(SCALE), p(od), p(ld), B, S, S, Hq, Hkv, 128, W, p(sd))
+    assert st() == 0
+    torch.cuda.synchronize()
+    _check(from_torch_bf16(od), ld.cpu().numpy(), o_ref, l_ref, "C++ SWA")
+    fn(p(qd), p(kd), p(vd), ctypes.c_float(SCALE), p(od), p(ld), B, S, S, Hq, Hkv, 128, 0, p(sd))
+    assert st() == -1
