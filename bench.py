@@ -268,6 +268,34 @@ def bench_swa(steps, warmup, dev, window=512):
                           "algorithmic_flops": flops})
 
 
+def bench_mla(steps, warmup, dev):
+    """MLA prefill (Q/K head dim 192, V/O 128, causal) at the reference's MLA
+    benchmark shape (README: B=1, S=4096, Hq=Hkv=16)."""
+    import math
+
+    import torch
+
+    import cuda_llm_ops_amd as fg
+    B, S, Hq, Hkv, Dqk, Dv = 1, 4096, 16, 16, 192, 128
+    q = _normal((B, S, Hq, Dqk), 12, 1.0, dev)
+    k = _normal((B, S, Hkv, Dqk), 13, 1.0, dev)
+    v = _normal((B, S, Hkv, Dv), 14, 1.0, dev)
+    out = torch.empty((B, S, Hq, Dv), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((B, Hq, S), dtype=torch.float32, device=dev)
+    step = fg.prepare_prefill(q, k, v, 1.0 / math.sqrt(Dqk), out=out, lse=lse, causal=True)
+    total_ms, per = _time_calls(step, steps, warmup)
+    # the reference's causal-halved count (test_flash_mla_kernel.py:282-301)
+    flops = B * Hq * 2 * S * S * (Dqk + Dv) // 2
+    avg = sum(per) / len(per)
+    tflops = flops / (avg * 1e-3) / 1e12
+    return dict(config=f"MLA causal prefill B={B} S={S} Hq={Hq} Hkv={Hkv} Dqk={Dqk} Dv={Dv}",
+                us_avg=round(avg * 1e3, 2), us_median=round(per[len(per) // 2] * 1e3, 2),
+                us_min=round(per[0] * 1e3, 2),
+                roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
+                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                          "algorithmic_flops": flops})
+
+
 def bench_backward(cfg_id, steps, warmup, dev):
     """Prefill backward (dQ, dK, dV) of a causal forward at a BASELINE prefill
     shape; one step = every launch of fgqa_prefill_backward_bf16."""
@@ -312,10 +340,11 @@ def main():
     ap.add_argument("--no-backward", action="store_true")
     ap.add_argument("--no-paged", action="store_true")
     ap.add_argument("--no-swa", action="store_true")
+    ap.add_argument("--no-mla", action="store_true")
     ap.add_argument("--page-size", type=int, default=16, help="with --mode paged")
     ap.add_argument("--kv", choices=["bf16", "fp8"], default="bf16", help="with --mode paged")
     ap.add_argument("--all", action="store_true", help="also report configs 1, 3 and 5 (to stderr)")
-    ap.add_argument("--mode", choices=["bench", "decode", "paged", "prefill", "swa", "backward", "copy"],
+    ap.add_argument("--mode", choices=["bench", "decode", "paged", "prefill", "swa", "mla", "backward", "copy"],
                     default="bench",
                     help="decode/prefill/copy: run only that workload (for profiling) and print its timing")
     ap.add_argument("--config", type=int, default=0,
@@ -345,6 +374,9 @@ def main():
     if args.mode == "paged":
         print(json.dumps({"mode": "paged", **bench_paged(args.config or 3, args.steps, args.warmup, dev,
                                                           args.page_size, args.kv)}), flush=True)
+        return
+    if args.mode == "mla":
+        print(json.dumps({"mode": "mla", **bench_mla(args.steps, args.warmup, dev)}), flush=True)
         return
     if args.mode == "swa":
         print(json.dumps({"mode": "swa", **bench_swa(args.steps, args.warmup, dev)}), flush=True)
@@ -388,6 +420,8 @@ def main():
                                 for kv in ("bf16", "fp8")]
     if not args.no_swa:
         line["swa"] = bench_swa(max(5, args.steps // 2), max(2, args.warmup // 2), dev)
+    if not args.no_mla:
+        line["mla"] = bench_mla(max(5, args.steps // 2), max(2, args.warmup // 2), dev)
     if not args.no_backward:
         line["backward"] = bench_backward(4, max(5, args.steps // 2), max(2, args.warmup // 2), dev)
     if not args.no_cpu:

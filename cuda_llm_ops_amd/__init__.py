@@ -1,4 +1,4 @@
-"""MI355X-native flash grouped-query attention (decode incl. paged/fp8 KV caches, causal prefill and its backward).
+"""MI355X-native flash grouped-query attention (decode incl. paged/fp8 KV caches, causal, sliding-window and MLA prefill, and the prefill backward).
 
 The kernels live in libfgqa.so (HIP, gfx950); ``flash_gqa`` is the Python host
 interface over its C ABI (include/fgqa.h).
@@ -15,6 +15,8 @@ from .flash_gqa import (  # noqa: F401
     launch_flash_gqa_backward_bf16_kernel,
     launch_flash_gqa_forward_bf16_kernel,
     launch_flash_swa_forward_bf16_kernel,
+    launch_flash_mla_forward_bf16_kernel,
+    PREFILL_HEAD_DIMS,
     paged_decode_workspace_bytes,
     prepare_backward,
     prepare_decode,

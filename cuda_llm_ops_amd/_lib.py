@@ -69,6 +69,7 @@ class PrefillArgs(ctypes.Structure):
         ("o_stride", _I64x3),
         ("window_size", ctypes.c_int32),
         ("sink", ctypes.c_void_p),
+        ("head_dim_v", ctypes.c_int32),
     ]
 
 

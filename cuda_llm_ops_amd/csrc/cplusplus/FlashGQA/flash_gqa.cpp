@@ -207,4 +207,42 @@ void LaunchFlashSwaForwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf1
     g_last_status = fgqa_prefill_bf16(&a, nullptr);
 }
 
+void LaunchFlashMlaForwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf16_t* v, float scale, bf16_t* o,
+                                     float* lse, int batchSize, int seqLengthQ, int seqLengthKv, int numQueryHeads,
+                                     int numKvHeads, int headDimQk, int headDimV, bool causal) {
+    fgqa_prefill_args a;
+    std::memset(&a, 0, sizeof(a));
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.o = o;
+    a.lse = lse;
+    a.batch = batchSize;
+    a.seqlen_q = seqLengthQ;
+    a.seqlen_kv = seqLengthKv;
+    a.num_q_heads = numQueryHeads;
+    a.num_kv_heads = numKvHeads;
+    a.head_dim = headDimQk;
+    a.head_dim_v = headDimV;
+    a.causal = causal ? 1 : 0;
+    a.scale = scale;
+    if (headDimV <= 0) {   // 0 would mean "same as headDimQk" in the C ABI
+        g_last_status = FGQA_ERR_INVALID_ARGUMENT;
+        return;
+    }
+    a.q_stride[0] = (int64_t)seqLengthQ * numQueryHeads * headDimQk;
+    a.q_stride[1] = (int64_t)numQueryHeads * headDimQk;
+    a.q_stride[2] = headDimQk;
+    a.k_stride[0] = (int64_t)seqLengthKv * numKvHeads * headDimQk;
+    a.k_stride[1] = (int64_t)numKvHeads * headDimQk;
+    a.k_stride[2] = headDimQk;
+    a.v_stride[0] = (int64_t)seqLengthKv * numKvHeads * headDimV;
+    a.v_stride[1] = (int64_t)numKvHeads * headDimV;
+    a.v_stride[2] = headDimV;
+    a.o_stride[0] = (int64_t)seqLengthQ * numQueryHeads * headDimV;
+    a.o_stride[1] = (int64_t)numQueryHeads * headDimV;
+    a.o_stride[2] = headDimV;
+    g_last_status = fgqa_prefill_bf16(&a, nullptr);
+}
+
 int FlashGqaGetLastStatus() { return g_last_status; }

@@ -29,6 +29,12 @@
 // it by more than 2^8, so P <= 256 and O stays far inside fp32 range.
 // K(j+2) and V(j+1) stream straight into LDS (buffer_load ... lds) while tile
 // j is computed.
+//
+// The MLA prefill (src/python/Triton/flash_mla_kernel.py:16-270: Q/K head dim
+// 192, V/O head dim 128, same maths) is the same kernel instantiated with
+// kDk = 192: Q^T holds 12 k-steps in registers, K rows are 384 bytes, phase A
+// issues 24 MFMAs per tile instead of 16, and a group's LDS grows from 64 KB
+// to 80 KB (two workgroups still share a CU's 160 KB).
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -59,39 +65,58 @@ struct PrefillParams {
     const float* sink;  // nullable [Hq]: added to the softmax denominator as sink * exp(-max)
 };
 
-constexpr int kPfWaves = 4;                          // waves per group (one unit's rows)
+constexpr int kPfWaves = 4;                            // waves per group (one unit's rows)
 constexpr int kPfThreads = kPfWaves * kWave;
-constexpr int kPfTile = 64;                          // KV tokens per tile
-constexpr int kPfRowBytes = kHeadDim * 2;            // one K or V row
-constexpr int kPfTileBytes = kPfTile * kPfRowBytes;  // 16 KB
-constexpr int kPfGroupBytes = 4 * kPfTileBytes;      // K0, K1, V0, V1 of one group
-constexpr float kPfRescaleSlack = 8.f;               // log2 units: P <= 2^8 between rescales
+constexpr int kPfTile = 64;                            // KV tokens per tile
+constexpr int kPfVRowBytes = kHeadDim * 2;             // one V row (V/O head dim 128)
+constexpr int kPfVTileBytes = kPfTile * kPfVRowBytes;  // 16 KB
+constexpr float kPfRescaleSlack = 8.f;                 // log2 units: P <= 2^8 between rescales
 // merge area of the split kernel: per wave, 64 O values + max + sum per lane
 constexpr int kPfMergeFloats = 66;
-static_assert(kPfWaves * kPfMergeFloats * kWave * 4 <= 2 * kPfGroupBytes, "merge area must fit in the tile buffers");
 
-// LDS tiles hold unpadded 256-byte rows whose 16-byte chunks are permuted
-// (XOR swizzle) so that both read patterns are free of bank conflicts:
-//   K: chunk c of row r sits in slot c ^ (r % 16)      (16 rows, one chunk each: b128 reads)
+// Sizes that depend on the Q/K head dim kDk (128, or 192 for MLA).
+template <int kDk>
+struct PfDims {
+    static_assert(kDk == 128 || kDk == 192, "Q/K head dim");
+    static constexpr int kRowBytes = kDk * 2;                         // one K row
+    static constexpr int kChunks = kDk / 8;                           // 16-byte chunks per K row
+    static constexpr int kKTileBytes = kPfTile * kRowBytes;           // 16 or 24 KB
+    static constexpr int kGroupBytes = 2 * kKTileBytes + 2 * kPfVTileBytes;   // K0, K1, V0, V1
+    static constexpr int kSteps = kDk / 16;                           // MFMA k-steps over the head dim
+    static constexpr int kDmaK = kDk / 32;                            // K-tile DMA instructions per wave
+    static constexpr int kKoffRegs = kDk == 128 ? 8 : 4;              // per-lane K read offsets
+    // K swizzle: chunk c of row r sits in slot c ^ kswz(r).  16 consecutive
+    // rows read at one chunk hit 16 distinct 16-byte bank groups: 256-byte
+    // rows all start at bank 0 (XOR with r % 16); 384-byte rows start at bank
+    // 0 or 32 by row parity, so an XOR with (r / 2) % 8 (which keeps c inside
+    // its aligned block of 8) spreads each parity class over 8 groups.
+    static __device__ __forceinline__ int kswz(int r) { return kDk == 128 ? (r & 15) : ((r >> 1) & 7); }
+    static_assert(kPfWaves * kPfMergeFloats * kWave * 4 <= 2 * kGroupBytes, "merge area must fit in the tile buffers");
+};
+
+// LDS tiles hold unpadded rows whose 16-byte chunks are permuted (XOR
+// swizzle) so that both read patterns are free of bank conflicts:
+//   K: chunk c of row r sits in slot c ^ kswz(r)       (16 rows, one chunk each: b128 reads)
 //   V: chunk c of row r sits in slot c ^ 4*(r % 4)     (4 rows x 4 chunks: transposed b64 reads)
 // Tiles are filled by buffer_load ... lds (16 bytes per lane straight into
-// LDS): one instruction writes 1 KB = 4 rows, lane l taking slot l % 16 of
-// row l / 16, so each lane fetches the chunk that belongs in its slot.
+// LDS): one instruction writes 1 KB, lane l taking the l-th 16-byte slot of
+// it, so each lane fetches the chunk that belongs in its slot.
 
 // One unit (query block qb of head group hg, kv head kvh, batch b).  With
 // kGroups == 2, group `grp` covers tiles [grp*half, grp*half + half) of the
 // unit's KV range; tiles past the range are fully masked and add nothing.
 // kSwa: sliding window and/or sink (a separate instantiation, so the plain
 // causal kernels carry none of its work).
-template <int kGroups, bool kSwa>
+template <int kGroups, bool kSwa, int kDk>
 __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* smem_all, int qb, int hg, int kvh,
                                         int b) {
+    using D = PfDims<kDk>;
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave_wg = __builtin_amdgcn_readfirstlane(tid / kWave);   // wave-uniform
     const int grp = wave_wg / kPfWaves;
     const int wave = wave_wg % kPfWaves;
-    unsigned char* smem = smem_all + grp * kPfGroupBytes;
+    unsigned char* smem = smem_all + grp * D::kGroupBytes;
     const int l32 = lane & 31;
     const int l16 = lane & 15;
     const int g2 = lane >> 5;
@@ -114,10 +139,10 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     // Q^T as the B operand: lane holds Q[q0w + l32][16*kk + 8*g2 .. +7]; rows >= sq read as 0.
     const uint32_t qss = (uint32_t)(p.q_ss * 2);
     const __amdgpu_buffer_rsrc_t qrs =
-        make_rsrc(p.q + b * p.q_sb + h * p.q_sh, (uint32_t)(p.sq - 1) * qss + kHeadDim * 2);
-    bf16x8_t qop[8];
+        make_rsrc(p.q + b * p.q_sb + h * p.q_sh, (uint32_t)(p.sq - 1) * qss + D::kRowBytes);
+    bf16x8_t qop[D::kSteps];
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
+    for (int kk = 0; kk < D::kSteps; ++kk) {
         u32x4_t t = buf_load16(qrs, (uint32_t)qrow * qss + (kk * 16 + g2 * 8) * 2);
         t ^= p.q_sign;
         qop[kk] = as_bf16x8(t);
@@ -129,7 +154,7 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     const uint32_t vss = (uint32_t)(p.v_ss * 2);
     const int kv_last = p.skv > 0 ? p.skv - 1 : 0;
     const __amdgpu_buffer_rsrc_t krs =
-        make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, (uint32_t)kv_last * kss + kHeadDim * 2);
+        make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, (uint32_t)kv_last * kss + D::kRowBytes);
     const __amdgpu_buffer_rsrc_t vrs =
         make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, (uint32_t)kv_last * vss + kHeadDim * 2);
     // K(t_first + j) -> K buffer kb (skipped when kb < 0), V(t_first + j) -> V buffer vb.
@@ -142,59 +167,74 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                      :: "s"(lds_addr), "v"(voffset), "s"(rsrc), "s"(soffset) : "memory");
     };
-    // Per-lane byte offsets of the 4 rows this lane fetches within a tile
-    // (tile rows r = 4*(wave + 4*i) + lane/16, swizzled chunk); the tile's
-    // start goes in the scalar offset.
-    uint32_t koff_dma[4], voff_dma[4];
+    // Instruction i of this wave fills the 1 KB at slot 64*(wave + 4*i) of a
+    // tile; lane l writes slot 64*(wave + 4*i) + l, i.e. row r = slot / chunks,
+    // swizzled position slot % chunks, which holds chunk (slot % chunks) ^ swz(r).
+    // Per-lane byte offsets of those chunks within a tile; the tile's start
+    // goes in the scalar offset.
+    int krow_dma[D::kDmaK];
+    uint32_t kcol_dma[D::kDmaK], koff_dma[D::kDmaK], voff_dma[4];
+#pragma unroll
+    for (int i = 0; i < D::kDmaK; ++i) {
+        const int slot = 64 * (wave + 4 * i) + lane;
+        const int r = slot / D::kChunks;
+        krow_dma[i] = r;
+        kcol_dma[i] = (uint32_t)(((slot % D::kChunks) ^ D::kswz(r)) << 4);
+        koff_dma[i] = (uint32_t)r * kss + kcol_dma[i];
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int r = 4 * (wave + 4 * i) + (lane >> 4);
-        koff_dma[i] = (uint32_t)r * kss + ((l16 ^ (r & 15)) << 4);
         voff_dma[i] = (uint32_t)r * vss + ((l16 ^ (4 * (r & 3))) << 4);
     }
     auto issue_tile = [&](int j, int kb, int vb) {
         const int t0 = (t_first + j) * kPfTile;
+        const uint32_t kdst = lds_base + kb * D::kKTileBytes;
+        const uint32_t vdst = lds_base + 2 * D::kKTileBytes + vb * kPfVTileBytes;
+        // K and V instructions interleaved, K first
         if (t0 + kPfTile - 1 <= kv_last) {   // whole tile in range
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t r0 = 4 * (wave + 4 * i);   // first row written by this instruction
-                if (kb >= 0)
-                    dma16(lds_base + kb * kPfTileBytes + r0 * kPfRowBytes, koff_dma[i], (uint32_t)t0 * kss, krs);
-                if (vb >= 0)
-                    dma16(lds_base + (2 + vb) * kPfTileBytes + r0 * kPfRowBytes, voff_dma[i], (uint32_t)t0 * vss, vrs);
+            for (int i = 0; i < D::kDmaK; ++i) {
+                if (kb >= 0) dma16(kdst + 1024 * (wave + 4 * i), koff_dma[i], (uint32_t)t0 * kss, krs);
+                if (i < 4 && vb >= 0) dma16(vdst + 1024 * (wave + 4 * i), voff_dma[i], (uint32_t)t0 * vss, vrs);
             }
         } else {   // last tile: rows past the last key are clamped to it
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r0 = 4 * (wave + 4 * i);
-                const int r = r0 + (lane >> 4);
-                const uint32_t tok = (uint32_t)min(t0 + r, kv_last);
-                if (kb >= 0)
-                    dma16(lds_base + kb * kPfTileBytes + r0 * kPfRowBytes, tok * kss + ((l16 ^ (r & 15)) << 4), 0u,
-                          krs);
-                if (vb >= 0)
-                    dma16(lds_base + (2 + vb) * kPfTileBytes + r0 * kPfRowBytes,
-                          tok * vss + ((l16 ^ (4 * (r & 3))) << 4), 0u, vrs);
+            for (int i = 0; i < D::kDmaK; ++i) {
+                if (kb >= 0) {
+                    const uint32_t tok = (uint32_t)min(t0 + krow_dma[i], kv_last);
+                    dma16(kdst + 1024 * (wave + 4 * i), tok * kss + kcol_dma[i], 0u, krs);
+                }
+                if (i < 4 && vb >= 0) {
+                    const int r = 4 * (wave + 4 * i) + (lane >> 4);
+                    const uint32_t tok = (uint32_t)min(t0 + r, kv_last);
+                    dma16(vdst + 1024 * (wave + 4 * i), tok * vss + ((l16 ^ (4 * (r & 3))) << 4), 0u, vrs);
+                }
             }
         }
     };
 
     // S^T(tile j) = K(j) . Q^T: lane holds column q = l32, tokens 32*tb + 8*(i/4) + 4*g2 + i%4.
-    // K operand of (tb, kk): row 32*tb + l32, chunk 2*kk + g2.
-    int koff[8];
+    // K operand of (tb, kk): row 32*tb + l32, chunk 2*kk + g2.  The swizzle of
+    // rows 32*tb + l32 does not depend on tb; with 384-byte rows it only
+    // permutes within aligned blocks of 8 chunks, so k-steps kk and kk + 4 sit
+    // 128 bytes apart and share one offset register.
+    int koff[D::kKoffRegs];
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) koff[kk] = l32 * kPfRowBytes + (((2 * kk + g2) ^ l16) << 4);
+    for (int kk = 0; kk < D::kKoffRegs; ++kk)
+        koff[kk] = l32 * D::kRowBytes + (((2 * kk + g2) ^ D::kswz(l32)) << 4);
     auto qk = [&](f32x16_t (&s)[2], int buf) {
-        const unsigned char* kl = smem + buf * kPfTileBytes;
+        const unsigned char* kl = smem + buf * D::kKTileBytes;
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
             for (int i = 0; i < 16; ++i) s[tb][i] = 0.f;
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk)
+        for (int kk = 0; kk < D::kSteps; ++kk)
 #pragma unroll
             for (int tb = 0; tb < 2; ++tb) {
-                const bf16x8_t ka = *reinterpret_cast<const bf16x8_t*>(kl + tb * 32 * kPfRowBytes + koff[kk]);
+                const int off = tb * 32 * D::kRowBytes + koff[kk % D::kKoffRegs] + (kk / D::kKoffRegs) * 128;
+                const bf16x8_t ka = *reinterpret_cast<const bf16x8_t*>(kl + off);
                 s[tb] = mfma32(ka, qop[kk], s[tb]);
             }
     };
@@ -284,17 +324,17 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         const int dh = (lane >> 4) & 1;
 #pragma unroll
         for (int db = 0; db < 4; ++db)
-            voff[db] = (4 * g2 + q4) * kPfRowBytes + ((4 * (db ^ q4) + 2 * dh + ((l16 >> 1) & 1)) << 4) + 8 * (l16 & 1);
+            voff[db] = (4 * g2 + q4) * kPfVRowBytes + ((4 * (db ^ q4) + 2 * dh + ((l16 >> 1) & 1)) << 4) + 8 * (l16 & 1);
     }
     auto pv = [&](int buf) {
-        const unsigned char* vl = smem + (2 + buf) * kPfTileBytes;
+        const unsigned char* vl = smem + 2 * D::kKTileBytes + buf * kPfVTileBytes;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
-                const unsigned char* base = vl + 16 * kb * kPfRowBytes + voff[db];
+                const unsigned char* base = vl + 16 * kb * kPfVRowBytes + voff[db];
                 const bf16x4_t lo = lds_read_tr16(reinterpret_cast<const __bf16*>(base));
-                const bf16x4_t hi = lds_read_tr16(reinterpret_cast<const __bf16*>(base + 8 * kPfRowBytes));
+                const bf16x4_t hi = lds_read_tr16(reinterpret_cast<const __bf16*>(base + 8 * kPfVRowBytes));
                 const bf16x8_t va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
                 oacc[db] = mfma32(va, pop[kb], oacc[db]);
             }
@@ -327,13 +367,15 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) asm volatile("" : "+v"(pop[kb]));
         asm volatile("" : "+v"(l_run));
-        // K reads run 4 MFMAs ahead of their use
+        // K reads run 4 MFMAs ahead of their use; the softmax's ~96 VALU ops
+        // spread over the phase's 16 (or 24) MFMAs
+        constexpr int kA = 2 * D::kSteps;
         __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);       // DS read
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+        for (int i = 0; i < kA; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // VALU
-            if (i < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+            __builtin_amdgcn_sched_group_barrier(0x002, 96 / kA, 0);   // VALU
+            if (i < kA - 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
         }
         mask(sn, j + 1);
         // phase B: P(j).V(j) on the MFMA pipe while the row max of S(j+1)
@@ -434,19 +476,20 @@ __device__ __forceinline__ void pf_block_unit(const PrefillParams& p, int* qb, i
     *b = stream / (p.n_hgroups * p.hkv);
 }
 
-template <bool kSwa>
+template <bool kSwa, int kDk>
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     int qb, hg, kvh, b;
     pf_block_unit(p, &qb, &hg, &kvh, &b);
-    pf_unit<1, kSwa>(p, smem, qb, hg, kvh, b);
+    pf_unit<1, kSwa, kDk>(p, smem, qb, hg, kvh, b);
 }
 
+template <int kDk>
 __global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_split_kernel(PrefillParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     int qb, hg, kvh, b;
     pf_block_unit(p, &qb, &hg, &kvh, &b);
-    pf_unit<2, false>(p, smem, qb, hg, kvh, b);
+    pf_unit<2, false, kDk>(p, smem, qb, hg, kvh, b);
 }
 
 namespace {
@@ -463,7 +506,11 @@ int validate_prefill(const fgqa_prefill_args* a) {
     for (int i = 0; i < 3; ++i)
         if (a->q_stride[i] < 0 || a->k_stride[i] < 0 || a->v_stride[i] < 0 || a->o_stride[i] < 0)
             return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->head_dim != kHeadDim) return FGQA_ERR_UNSUPPORTED;
+    if (a->head_dim_v < 0) return FGQA_ERR_INVALID_ARGUMENT;
+    const int dv = a->head_dim_v == 0 ? a->head_dim : a->head_dim_v;
+    // (128, 128) and the MLA shape (192, 128); MLA has no window / sink form
+    if (dv != kHeadDim || (a->head_dim != kHeadDim && a->head_dim != 192)) return FGQA_ERR_UNSUPPORTED;
+    if (a->head_dim == 192 && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
     const int64_t lim = (int64_t)1 << 31;
     if ((int64_t)(a->seqlen_q + 128) * a->q_stride[1] * 2 >= lim ||
         (int64_t)(a->seqlen_kv + 128) * a->k_stride[1] * 2 >= lim ||
@@ -539,24 +586,36 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
     // sink variant has no split form).
     if (const char* e = getenv("FGQA_PREFILL_SPLIT")) split = e[0] == '1' && !swa;
 
-    const int smem_bytes = (split ? 2 : 1) * kPfGroupBytes;
-    const int which = split ? 2 : (swa ? 1 : 0);
-    const void* fns[3] = {reinterpret_cast<const void*>(prefill_kernel<false>),
-                          reinterpret_cast<const void*>(prefill_kernel<true>),
-                          reinterpret_cast<const void*>(prefill_split_kernel)};
-    static bool smem_set[3] = {false, false, false};
-    if (!smem_set[which]) {
+    const bool mla = a->head_dim == 192;
+    const int group_bytes = mla ? PfDims<192>::kGroupBytes : PfDims<128>::kGroupBytes;
+    const int smem_bytes = (split ? 2 : 1) * group_bytes;
+    // kernel table: plain, window / sink, split, MLA, MLA split
+    const int which = mla ? (split ? 4 : 3) : (split ? 2 : (swa ? 1 : 0));
+    const void* fns[5] = {reinterpret_cast<const void*>(prefill_kernel<false, 128>),
+                          reinterpret_cast<const void*>(prefill_kernel<true, 128>),
+                          reinterpret_cast<const void*>(prefill_split_kernel<128>),
+                          reinterpret_cast<const void*>(prefill_kernel<false, 192>),
+                          reinterpret_cast<const void*>(prefill_split_kernel<192>)};
+    // The attribute is per kernel and per device: set it once per device.
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return FGQA_ERR_HIP;
+    constexpr int kMaxDev = 64;
+    static bool smem_set[kMaxDev][5] = {};
+    if (dev < 0 || dev >= kMaxDev) return FGQA_ERR_UNSUPPORTED;
+    if (!smem_set[dev][which]) {
         if (hipFuncSetAttribute(fns[which], hipFuncAttributeMaxDynamicSharedMemorySize, smem_bytes) != hipSuccess)
             return FGQA_ERR_HIP;
-        smem_set[which] = true;
+        smem_set[dev][which] = true;
     }
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (split)
-        hipLaunchKernelGGL(prefill_split_kernel, dim3((unsigned)units), dim3(2 * kPfThreads), smem_bytes, s, p);
-    else if (swa)
-        hipLaunchKernelGGL(prefill_kernel<true>, dim3((unsigned)units), dim3(kPfThreads), smem_bytes, s, p);
-    else
-        hipLaunchKernelGGL(prefill_kernel<false>, dim3((unsigned)units), dim3(kPfThreads), smem_bytes, s, p);
+    const dim3 grid((unsigned)units);
+    switch (which) {
+        case 0: hipLaunchKernelGGL((prefill_kernel<false, 128>), grid, dim3(kPfThreads), smem_bytes, s, p); break;
+        case 1: hipLaunchKernelGGL((prefill_kernel<true, 128>), grid, dim3(kPfThreads), smem_bytes, s, p); break;
+        case 2: hipLaunchKernelGGL(prefill_split_kernel<128>, grid, dim3(2 * kPfThreads), smem_bytes, s, p); break;
+        case 3: hipLaunchKernelGGL((prefill_kernel<false, 192>), grid, dim3(kPfThreads), smem_bytes, s, p); break;
+        default: hipLaunchKernelGGL(prefill_split_kernel<192>, grid, dim3(2 * kPfThreads), smem_bytes, s, p); break;
+    }
     if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
     return FGQA_OK;
 }

@@ -7,7 +7,8 @@ Two families of entry points:
     - ``launch_flash_gqa_forward_bf16_kernel`` <- src/python/Triton/flash_gqa_kernel.py:185-338
     - ``launch_decode_flash_gqa_bf16_kernel``  <- src/python/Triton/decode_flash_gqa_kernel.py:137-196
     - ``launch_flash_gqa_backward_bf16_kernel`` <- src/python/Triton/flash_gqa_backward_kernel.py:312-478
-    - ``launch_flash_swa_forward_bf16_kernel``  <- src/python/Triton/SWA/flash_swa_kernel.py:185-366
+    - ``launch_flash_swa_forward_bf16_kernel``  <- src/python/Triton/SWA/flash_swa_kernel.py:188-370
+    - ``launch_flash_mla_forward_bf16_kernel``  <- src/python/Triton/flash_mla_kernel.py:315-508
 * The C++ layouts of the reference's C++ decode entry point (Q/O ``[B,Hq,D]``,
   K/V ``[B,S,Hkv,D]``, decode_flash_gqa_kernel.cuh:28-38) and of the new C++
   prefill entry point (BSHD):
@@ -33,6 +34,8 @@ __all__ = [
     "launch_decode_flash_gqa_bf16_kernel",
     "launch_flash_gqa_backward_bf16_kernel",
     "launch_flash_swa_forward_bf16_kernel",
+    "launch_flash_mla_forward_bf16_kernel",
+    "PREFILL_HEAD_DIMS",
     "decode_flash_gqa_bshd",
     "decode_flash_gqa_paged",
     "paged_decode_workspace_bytes",
@@ -347,6 +350,7 @@ def _prefill_args(q, k, v, o, lse, scale, causal, layout, window_size=0, sink=No
     a.q, a.k, a.v, a.o, a.lse = _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse)
     a.batch, a.seqlen_q, a.seqlen_kv = B, Sq, Skv
     a.num_q_heads, a.num_kv_heads, a.head_dim = Hq, Hkv, D
+    a.head_dim_v = v.shape[3]
     a.causal = 1 if causal else 0
     a.scale = float(scale)
     a.q_stride[:] = sbh(q)
@@ -356,6 +360,19 @@ def _prefill_args(q, k, v, o, lse, scale, causal, layout, window_size=0, sink=No
     a.window_size = int(window_size)
     a.sink = _ptr(sink)
     return a
+
+
+# (Q/K head dim, V/O head dim) pairs the prefill kernels are built for:
+# GQA, and MLA (src/python/Triton/flash_mla_kernel.py's 192 / 128).
+PREFILL_HEAD_DIMS = ((128, 128), (192, 128))
+
+
+def _check_head_dims(dqk, dv, window_size=0, sink=None):
+    if (dqk, dv) not in PREFILL_HEAD_DIMS:
+        raise ValueError(f"(head_dim_qk, head_dim_v) = ({dqk}, {dv}) is not supported; "
+                         f"supported: {PREFILL_HEAD_DIMS}")
+    if dqk != dv and (int(window_size) != 0 or sink is not None):
+        raise ValueError("a sliding window or sink needs head_dim_qk == head_dim_v == 128")
 
 
 def _prefill(q, k, v, o, lse, scale, causal, layout, window_size=0, sink=None):
@@ -380,17 +397,19 @@ def _prefill_bshd_prepare(q, k, v, scale, out, lse, causal, window_size=0, sink=
         raise ValueError("expected 4-D BSHD tensors")
     _require_cuda(q, k, v)
     B, Sq, Hq, D = q.shape
-    if k.shape != v.shape or k.shape[0] != B or k.shape[3] != D:
-        raise ValueError("K and V must be [B, Skv, Hkv, D] matching Q")
+    Dv = v.shape[3]
+    if k.shape[:3] != v.shape[:3] or k.shape[0] != B or k.shape[3] != D:
+        raise ValueError("K must be [B, Skv, Hkv, D] matching Q and V [B, Skv, Hkv, Dv]")
     if Hq % k.shape[2] != 0:
         raise ValueError("Query heads must be divisible by KV heads")
+    _check_head_dims(D, Dv, window_size, sink)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     q, k, v = _prep(q), _prep(k), _prep(v)
     if out is None:
-        out = torch.empty((B, Sq, Hq, D), device=q.device, dtype=torch.bfloat16)
-    elif out.shape != (B, Sq, Hq, D) or out.dtype != torch.bfloat16 or not _kernel_ready(out):
-        raise ValueError("Output must be a bf16 [batch, seqlen_q, q_heads, head_dim] tensor with contiguous rows")
+        out = torch.empty((B, Sq, Hq, Dv), device=q.device, dtype=torch.bfloat16)
+    elif out.shape != (B, Sq, Hq, Dv) or out.dtype != torch.bfloat16 or not _kernel_ready(out):
+        raise ValueError("Output must be a bf16 [batch, seqlen_q, q_heads, head_dim_v] tensor with contiguous rows")
     if lse is None:
         lse = torch.empty((B, Hq, Sq), device=q.device, dtype=torch.float32)
     elif lse.shape != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
@@ -401,9 +420,11 @@ def _prefill_bshd_prepare(q, k, v, scale, out, lse, causal, window_size=0, sink=
 
 
 def flash_gqa_forward_bshd(q, k, v, scale=None, out=None, lse=None, causal=True, window_size=0, sink=None):
-    """Prefill forward in BSHD: q [B,Sq,Hq,D], k/v [B,Skv,Hkv,D] -> (out [B,Sq,Hq,D], lse [B,Hq,Sq]).
-    window_size > 0 (causal only): row i sees keys [i - window_size + 1, i]; sink: optional
-    fp32 [Hq] added to the softmax denominator as sink * exp(-max) (the reference's SWA kernel)."""
+    """Prefill forward in BSHD: q [B,Sq,Hq,D], k [B,Skv,Hkv,D], v [B,Skv,Hkv,Dv]
+    -> (out [B,Sq,Hq,Dv], lse [B,Hq,Sq]).  (D, Dv) is (128, 128), or (192, 128)
+    for MLA.  window_size > 0 (causal only): row i sees keys [i - window_size + 1, i];
+    sink: optional fp32 [Hq] added to the softmax denominator as sink * exp(-max)
+    (the reference's SWA kernel); both need D == Dv == 128."""
     a, out, lse, _keep = _prefill_bshd_prepare(q, k, v, scale, out, lse, causal, window_size, sink)
     _lib.check(_lib.lib().fgqa_prefill_bf16(ctypes.byref(a), ctypes.c_void_p(_stream())), "fgqa_prefill_bf16")
     return out, lse
@@ -430,8 +451,31 @@ def launch_flash_gqa_forward_bf16_kernel(q, k, v, scale=None, out=None, lse=None
     a provided buffer is always written in place or rejected with ValueError.
     """
     del block_kv_sub, num_warps, num_stages
+    return _launch_bhsd_prefill("GQA", q, k, v, scale, out, lse, causal)
+
+
+def launch_flash_mla_forward_bf16_kernel(q, k, v, scale=None, out=None, lse=None, causal=True,
+                                         block_kv_sub=64, num_warps=8, num_stages=3):
+    """Mirror of the reference's Triton MLA prefill launcher
+    (src/python/Triton/flash_mla_kernel.py:315-508): BHSD q [B,Hq,Sq,Dqk] (or
+    3-D [Hq,Sq,Dqk]), k [B,Hkv,Skv,Dqk], v [B,Hkv,Skv,Dv]; returns
+    (out [B,Hq,Sq,Dv], lse [B,Hq,Sq]).  The default scale is 1/sqrt(Dqk).
+
+    Same checks and ValueError messages as the reference (:356-436).  The
+    kernels are built for (Dqk, Dv) = (192, 128), the reference's MLA shape,
+    and (128, 128); other pairs raise ValueError.  ``block_kv_sub``,
+    ``num_warps`` and ``num_stages`` are Triton tuning knobs, accepted for
+    signature compatibility only.  A provided ``out``/``lse`` is written in
+    place or rejected (the reference writes a non-contiguous one into a copy).
+    """
+    del block_kv_sub, num_warps, num_stages
+    return _launch_bhsd_prefill("MLA", q, k, v, scale, out, lse, causal)
+
+
+def _launch_bhsd_prefill(kind, q, k, v, scale, out, lse, causal):
+    """Shared body of the GQA and MLA Triton-launcher mirrors (BHSD, 3-D or 4-D)."""
     if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
-        raise ValueError("Flash GQA forward expects bf16 inputs")
+        raise ValueError(f"Flash {kind} forward expects bf16 inputs")
     if q.dim() not in (3, 4):
         raise ValueError("Q must be 3D or 4D")
     if k.dim() != q.dim() or v.dim() != q.dim():
@@ -452,8 +496,9 @@ def launch_flash_gqa_forward_bf16_kernel(q, k, v, scale=None, out=None, lse=None
         raise ValueError("K and V must share number of KV heads")
     if q_heads % num_kv_heads != 0:
         raise ValueError("Query heads must be divisible by KV heads")
-    if head_dim_v != head_dim_qk:
+    if kind == "GQA" and head_dim_v != head_dim_qk:
         raise ValueError("head_dim_v must equal head_dim_qk on this path")
+    _check_head_dims(head_dim_qk, head_dim_v)
     if scale is None:
         scale = 1.0 / math.sqrt(head_dim_qk)
     qb, kb, vb = _prep(qb), _prep(kb), _prep(vb)
@@ -489,6 +534,8 @@ def launch_flash_gqa_forward_bf16_kernel(q, k, v, scale=None, out=None, lse=None
     if squeeze_output:
         return out_b.squeeze(0), lse_b.squeeze(0)
     return out_b, lse_b
+
+
 
 
 # --------------------------------------------------------------------------- backward
@@ -678,7 +725,7 @@ def launch_flash_gqa_backward_bf16_kernel(q, k, v, o, lse, grad_o, scale=None, c
 def launch_flash_swa_forward_bf16_kernel(q, k, v, scale=None, out=None, lse=None, window_size=None,
                                          sink_value=None, block_kv_sub=16, num_warps=4, num_stages=3):
     """Mirror of the reference's Triton SWA launcher
-    (src/python/Triton/SWA/flash_swa_kernel.py:185-366): causal sliding-window
+    (src/python/Triton/SWA/flash_swa_kernel.py:188-370): causal sliding-window
     attention (row i sees keys [i - window_size + 1, i]) with a per-head sink
     in the softmax denominator; BHSD q [B,Hq,Sq,D] (or 3-D), k/v [B,Hkv,Skv,D];
     returns (out, lse [B,Hq,Sq]).

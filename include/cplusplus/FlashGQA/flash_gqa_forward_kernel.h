@@ -66,7 +66,7 @@ void LaunchFlashGqaForwardBf16KernelStrided(const bf16_t* q,
 /**
  * @brief Sliding-window prefill with a per-head sink (BSHD), the C++
  *        counterpart of the reference's Triton-only SWA launcher
- *        (src/python/Triton/SWA/flash_swa_kernel.py:185-366): causal, row i
+ *        (src/python/Triton/SWA/flash_swa_kernel.py:188-370): causal, row i
  *        sees keys [i - windowSize + 1, i]; sink (nullable device fp32
  *        [numQueryHeads]) joins the softmax denominator as sink * exp(-max).
  */
@@ -84,3 +84,29 @@ void LaunchFlashSwaForwardBf16Kernel(const bf16_t* q,
                                      int headDim,
                                      int windowSize,
                                      const float* sink);
+
+/**
+ * @brief MLA prefill forward (BSHD): Q/K head dim headDimQk, V/O head dim
+ *        headDimV, the C++ counterpart of the reference's Triton-only MLA
+ *        launcher (src/python/Triton/flash_mla_kernel.py:315-508, kernel
+ *        :16-270).  Supported: (headDimQk, headDimV) = (192, 128) or (128, 128).
+ * @param q Device query tensor [batchSize, seqLengthQ, numQueryHeads, headDimQk].
+ * @param k Device key tensor [batchSize, seqLengthKv, numKvHeads, headDimQk].
+ * @param v Device value tensor [batchSize, seqLengthKv, numKvHeads, headDimV].
+ * @param o Device output tensor [batchSize, seqLengthQ, numQueryHeads, headDimV].
+ * @param lse Device fp32 log-sum-exp [batchSize, numQueryHeads, seqLengthQ] (natural log), or nullptr.
+ */
+void LaunchFlashMlaForwardBf16Kernel(const bf16_t* q,
+                                     const bf16_t* k,
+                                     const bf16_t* v,
+                                     float scale,
+                                     bf16_t* o,
+                                     float* lse,
+                                     int batchSize,
+                                     int seqLengthQ,
+                                     int seqLengthKv,
+                                     int numQueryHeads,
+                                     int numKvHeads,
+                                     int headDimQk,
+                                     int headDimV,
+                                     bool causal);

@@ -161,6 +161,12 @@ int fgqa_decode_paged(const fgqa_decode_paged_args* args, void* stream);
  *           denominator, sum_j exp(s_j - m) + sink * exp(-m); lse includes it.
  *           A row with no visible key then gives O = 0, lse = log(max(sink, 1e-9)).
  *   Callers that zero the struct get neither.
+ *   head_dim_v  V/O head dim; 0 means head_dim.  head_dim = 192 with
+ *           head_dim_v = 128 is the MLA prefill, replacing the Triton-only
+ *           launch_flash_mla_forward_bf16_kernel, reference
+ *           src/python/Triton/flash_mla_kernel.py:315-508 (kernel :16-270):
+ *           q/k rows hold head_dim elements, v/o rows head_dim_v.  Supported:
+ *           (128, 128), and (192, 128) without window or sink.
  */
 typedef struct fgqa_prefill_args {
     const void* q;
@@ -182,6 +188,7 @@ typedef struct fgqa_prefill_args {
     int64_t o_stride[3];
     int32_t window_size;
     const float* sink;
+    int32_t head_dim_v;
 } fgqa_prefill_args;
 
 int fgqa_prefill_bf16(const fgqa_prefill_args* args, void* stream);

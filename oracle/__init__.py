@@ -16,5 +16,6 @@ from .oracle import (  # noqa: F401
     normal_bf16,
     prefill,
     prefill_backward,
+    prefill_mla,
     prefill_swa,
 )

@@ -255,14 +255,15 @@ int fgqa_oracle_decode_paged(const uint16_t* q, const void* k_cache, const void*
  *           lse = log(sum(e)) + row_max
  *   :88     out = probs . v (fp32), then cast to bf16 (:93)
  */
-int fgqa_oracle_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                             float scale, uint16_t* o, float* lse,
-                             int batch, int sq, int skv, int hq, int hkv, int d,
-                             const int64_t* qs, const int64_t* ks,
-                             const int64_t* vs, const int64_t* os,
-                             int causal, int q_offset, int nthreads) {
+static int prefill_core(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                        float scale, uint16_t* o, float* lse,
+                        int batch, int sq, int skv, int hq, int hkv, int d, int dv,
+                        const int64_t* qs, const int64_t* ks,
+                        const int64_t* vs, const int64_t* os,
+                        int causal, int q_offset, int nthreads) {
     if (!q || !k || !v || !o || !qs || !ks || !vs || !os) return -1;
     if (batch < 0 || sq < 0 || skv < 0 || hq <= 0 || hkv <= 0 || d <= 0 || d > ORACLE_MAX_D) return -1;
+    if (dv <= 0 || dv > ORACLE_MAX_D) return -1;
     if (hq % hkv != 0) return -1;
     const int group = hq / hkv;
     set_threads(nthreads);
@@ -292,7 +293,7 @@ int fgqa_oracle_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_
                         rmax = fmaxf(rmax, sc[j]);
                     }
                     if (nvis == 0) {
-                        for (int x = 0; x < d; ++x) orow[x] = 0;
+                        for (int x = 0; x < dv; ++x) orow[x] = 0;
                         if (lse) lse[((size_t)b * hq + h) * sq + i] = -INFINITY;
                         continue;
                     }
@@ -301,13 +302,13 @@ int fgqa_oracle_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_
                         sc[j] = expf(sc[j] - rmax);
                         sum += sc[j];
                     }
-                    for (int x = 0; x < d; ++x) out[x] = 0.f;
+                    for (int x = 0; x < dv; ++x) out[x] = 0.f;
                     for (int j = 0; j < nvis; ++j) {
                         const uint16_t* vrow = v + b * vs[0] + (int64_t)j * vs[1] + kvh * vs[2];
                         const float pj = sc[j] / sum;
-                        for (int x = 0; x < d; ++x) out[x] += pj * bf(vrow[x]);
+                        for (int x = 0; x < dv; ++x) out[x] += pj * bf(vrow[x]);
                     }
-                    for (int x = 0; x < d; ++x) orow[x] = fgqa_oracle_f32_to_bf16(out[x]);
+                    for (int x = 0; x < dv; ++x) orow[x] = fgqa_oracle_f32_to_bf16(out[x]);
                     if (lse) lse[((size_t)b * hq + h) * sq + i] = logf(sum) + rmax;
                 }
             }
@@ -315,6 +316,32 @@ int fgqa_oracle_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_
         free(sc);
     }
     return 0;
+}
+
+int fgqa_oracle_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                             float scale, uint16_t* o, float* lse,
+                             int batch, int sq, int skv, int hq, int hkv, int d,
+                             const int64_t* qs, const int64_t* ks,
+                             const int64_t* vs, const int64_t* os,
+                             int causal, int q_offset, int nthreads) {
+    return prefill_core(q, k, v, scale, o, lse, batch, sq, skv, hq, hkv, d, d, qs, ks, vs, os,
+                        causal, q_offset, nthreads);
+}
+
+/*
+ * MLA prefill: the same loop with separate Q/K and V/O head dims.  It restates
+ * examples/python/Triton/test_flash_mla_kernel.py:27-95 (fp32 scores over
+ * head_dim_qk, triu(diagonal=1) causal mask at :69-72, full softmax and
+ * lse at :82-86, fp32 probs . v over head_dim_v at :88, cast to bf16 at :93).
+ */
+int fgqa_oracle_prefill_mla_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                 float scale, uint16_t* o, float* lse,
+                                 int batch, int sq, int skv, int hq, int hkv, int dqk, int dv,
+                                 const int64_t* qs, const int64_t* ks,
+                                 const int64_t* vs, const int64_t* os,
+                                 int causal, int q_offset, int nthreads) {
+    return prefill_core(q, k, v, scale, o, lse, batch, sq, skv, hq, hkv, dqk, dv, qs, ks, vs, os,
+                        causal, q_offset, nthreads);
 }
 
 /* Sliding-window + sink prefill (see the header for the reference lines). */

@@ -20,6 +20,10 @@
  *                                            to the fp64 answer than the bf16-P one
  *   fgqa_oracle_prefill_bf16                fp64 brute force, closed forms (row 0 = V[0],
  *                                            LSE of equal logits = log n), invariants
+ *   fgqa_oracle_prefill_mla_bf16            bit-identical to fgqa_oracle_prefill_bf16 when
+ *                                            dqk = dv; a float64 numpy restatement with
+ *                                            dqk = 192, dv = 128; closed forms (causal row 0
+ *                                            = V[0]; Q = 0 gives the running mean of V)
  *   fgqa_oracle_prefill_backward_bf16       fp64 backward (fgqa_oracle_attention_backward_f64,
  *                                            the torch-reference form) at the stated tolerance,
  *                                            closed forms (one key: dQ = dK = 0, dV = sum dO),
@@ -123,6 +127,19 @@ int fgqa_oracle_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_
                              const int64_t* q_strides, const int64_t* k_strides,
                              const int64_t* v_strides, const int64_t* o_strides,
                              int causal, int q_offset, int nthreads);
+
+/*
+ * MLA prefill (separate head dims: Q/K rows of dqk, V/O rows of dv), restating
+ * the reference's torch reference examples/python/Triton/test_flash_mla_kernel.py:27-95
+ * with the same steps as fgqa_oracle_prefill_bf16 (scores over dqk, P.V over dv).
+ * o has dv-element rows at strides o_strides; everything else as fgqa_oracle_prefill_bf16.
+ */
+int fgqa_oracle_prefill_mla_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                 float scale, uint16_t* o, float* lse,
+                                 int batch, int sq, int skv, int hq, int hkv, int dqk, int dv,
+                                 const int64_t* q_strides, const int64_t* k_strides,
+                                 const int64_t* v_strides, const int64_t* o_strides,
+                                 int causal, int q_offset, int nthreads);
 
 /*
  * Prefill backward, restating the reference's Triton backward

@@ -52,6 +52,11 @@ def lib() -> ctypes.CDLL:
             _u16p, _u16p, _u16p, ctypes.c_float, _u16p, _f32p,
             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
             _i64p, _i64p, _i64p, _i64p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.fgqa_oracle_prefill_mla_bf16.restype = ctypes.c_int
+        L.fgqa_oracle_prefill_mla_bf16.argtypes = [
+            _u16p, _u16p, _u16p, ctypes.c_float, _u16p, _f32p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            _i64p, _i64p, _i64p, _i64p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         L.fgqa_oracle_attention_f64.restype = ctypes.c_int
         L.fgqa_oracle_attention_f64.argtypes = [
             _u16p, _u16p, _u16p, ctypes.c_double, _f64p, _f64p,
@@ -172,6 +177,32 @@ def prefill(q, k, v, scale, causal=True, layout="bshd", q_offset=0, nthreads=0):
         _ptr(os_, ctypes.c_int64), int(bool(causal)), int(q_offset), int(nthreads))
     if rc != 0:
         raise ValueError("fgqa_oracle_prefill_bf16: invalid arguments")
+    return o, lse
+
+
+def prefill_mla(q, k, v, scale, causal=True, layout="bshd", q_offset=0, nthreads=0):
+    """MLA prefill oracle: q/k rows of Dqk elements, v rows of Dv (may differ).
+    layout 'bshd': q [B,Sq,Hq,Dqk], k [B,Skv,Hkv,Dqk], v [B,Skv,Hkv,Dv];
+    'bhsd': heads before sequence.  Returns (o [.., Dv] in q's layout, lse [B,Hq,Sq])."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    B, Sq, Hq, Dqk = _dims(q, layout)
+    _, Skv, Hkv, Dk = _dims(k, layout)
+    Dv = v.shape[3]
+    if Dk != Dqk:
+        raise ValueError("prefill_mla: q and k head dims differ")
+    o = np.empty(q.shape[:3] + (Dv,), dtype=np.uint16)
+    lse = np.empty((B, Hq, Sq), dtype=np.float32)
+    qs, ks, vs, os_ = (_strides(x, layout) for x in (q, k, v, o))
+    rc = lib().fgqa_oracle_prefill_mla_bf16(
+        _ptr(q, ctypes.c_uint16), _ptr(k, ctypes.c_uint16), _ptr(v, ctypes.c_uint16),
+        float(scale), _ptr(o, ctypes.c_uint16), _ptr(lse, ctypes.c_float),
+        B, Sq, Skv, Hq, Hkv, Dqk, Dv,
+        _ptr(qs, ctypes.c_int64), _ptr(ks, ctypes.c_int64), _ptr(vs, ctypes.c_int64),
+        _ptr(os_, ctypes.c_int64), int(bool(causal)), int(q_offset), int(nthreads))
+    if rc != 0:
+        raise ValueError("fgqa_oracle_prefill_mla_bf16: invalid arguments")
     return o, lse
 
 

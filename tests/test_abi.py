@@ -43,7 +43,8 @@ def test_cplusplus_entry_points_exported():
     assert set(decls) == {"LaunchFlashGqaBf16Kernel", "LaunchFlashGqaBf16KernelVarlen", "FlashGqaGetLastStatus",
                           "LaunchFlashGqaBf16KernelPaged",
                           "LaunchFlashGqaForwardBf16Kernel", "LaunchFlashGqaForwardBf16KernelStrided",
-                          "LaunchFlashGqaBackwardBf16Kernel", "LaunchFlashSwaForwardBf16Kernel"}
+                          "LaunchFlashGqaBackwardBf16Kernel", "LaunchFlashSwaForwardBf16Kernel",
+                          "LaunchFlashMlaForwardBf16Kernel"}
     for d in decls:
         assert re.search(rf"\bT {d}\(", syms), d
     # the drop-in keeps the reference's exact parameter list
@@ -150,7 +151,9 @@ def _prefill_args(**kw):
     for name in ("q", "k", "v", "o"):
         setattr(a, name, kw.get(name, 4096))
     a.window_size = kw.get("window", 0)
+    a.sink = kw.get("sink", None)
     a.causal = kw.get("causal", 1)
+    a.head_dim_v = kw.get("Dv", 0)
     return a
 
 
@@ -163,9 +166,38 @@ def _prefill_args(**kw):
     (dict(o=4096 + 8), _lib.FGQA_ERR_UNSUPPORTED),
     (dict(window=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(window=64, causal=0), _lib.FGQA_ERR_INVALID_ARGUMENT),   # a window is causal
+    (dict(Dv=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(D=192), _lib.FGQA_ERR_UNSUPPORTED),             # head_dim_v 0 means 192: not built
+    (dict(D=192, Dv=64), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(D=128, Dv=192), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(D=192, Dv=128, window=64), _lib.FGQA_ERR_UNSUPPORTED),   # MLA has no window form
+    (dict(D=192, Dv=128, sink=4096), _lib.FGQA_ERR_UNSUPPORTED),
 ])
 def test_prefill_rejects_before_launch(kw, code):
     assert _lib.lib().fgqa_prefill_bf16(ctypes.byref(_prefill_args(**kw)), None) == code
+
+
+def test_ctypes_structs_match_the_header(tmp_path):
+    """Every ctypes mirror in _lib has the C struct's size and field offsets
+    (a small C program compiled against include/fgqa.h prints them)."""
+    mirrors = {"fgqa_decode_args": _lib.DecodeArgs, "fgqa_decode_paged_args": _lib.PagedDecodeArgs,
+               "fgqa_prefill_args": _lib.PrefillArgs, "fgqa_prefill_backward_args": _lib.BackwardArgs}
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "fgqa.h"', "int main(void) {"]
+    for cname, py in mirrors.items():
+        lines.append(f'    printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in py._fields_:
+            lines.append(f'    printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines += ["    return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = {tuple(ln.split()[:2]): int(ln.split()[2]) for ln in out if ln.strip()}
+    for cname, py in mirrors.items():
+        assert got[(cname, "size")] == ctypes.sizeof(py), cname
+        for fname, _ in py._fields_:
+            assert got[(cname, fname)] == getattr(py, fname).offset, f"{cname}.{fname}"
 
 
 def test_prefill_empty_is_noop():
@@ -191,6 +223,18 @@ def test_python_mirror_validation_without_gpu():
         fg.launch_decode_flash_gqa_bf16_kernel(torch.zeros(2, 15, 1, 128, dtype=torch.bfloat16), k, k)
     with pytest.raises(ValueError, match="GPU"):
         fg.launch_flash_gqa_forward_bf16_kernel(qb, k, k)
+    # the MLA mirror (flash_mla_kernel.py:356-361) and the BSHD head-dim check
+    q192 = torch.zeros(2, 16, 64, 192, dtype=torch.bfloat16)
+    k192 = torch.zeros(2, 2, 64, 192, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="Flash MLA forward expects bf16 inputs"):
+        fg.launch_flash_mla_forward_bf16_kernel(q192.half(), k192, k)
+    with pytest.raises(ValueError, match="Q must be 3D or 4D"):
+        fg.launch_flash_mla_forward_bf16_kernel(q192[0, 0], k192[0, 0], k[0, 0])
+    with pytest.raises(ValueError, match="ranks"):
+        fg.launch_flash_mla_forward_bf16_kernel(q192, k192[0], k)
+    with pytest.raises(ValueError, match="GPU"):
+        fg.launch_flash_mla_forward_bf16_kernel(q192, k192, k)
+    assert (192, 128) in fg.PREFILL_HEAD_DIMS and (128, 128) in fg.PREFILL_HEAD_DIMS
 
 
 def _backward_args(**kw):

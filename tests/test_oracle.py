@@ -606,3 +606,92 @@ def test_swa_oracle_vs_numpy_f64(window, sq, skv):
         r = skv + window - 1
         assert np.all(o[:, r:] == 0)
         assert np.allclose(lse[:, :, r:], np.log(np.maximum(sink, 1e-9))[None, :, None])
+
+
+# ----------------------------------------------------------------- MLA prefill oracle (Dqk != Dv)
+def _mla_inputs(seed, B, Sq, Skv, Hq, Hkv, Dqk, Dv, uniform=False):
+    if uniform:   # the reference test's inputs: torch.rand, U[0, 1)
+        rng = np.random.default_rng(seed)
+        mk = lambda shape: oracle.f32_to_bf16(rng.random(shape, dtype=np.float32))  # noqa: E731
+        return mk((B, Sq, Hq, Dqk)), mk((B, Skv, Hkv, Dqk)), mk((B, Skv, Hkv, Dv))
+    q = oracle.normal_bf16(seed, (B, Sq, Hq, Dqk))
+    k = oracle.normal_bf16(seed, (B, Skv, Hkv, Dqk), stream=1)
+    v = oracle.normal_bf16(seed, (B, Skv, Hkv, Dv), stream=2)
+    return q, k, v
+
+
+def _mla_numpy_f64(q, k, v, scale, causal):
+    """float64 restatement of test_flash_mla_kernel.py:27-95 (BSHD, top-left causal)."""
+    qf, kf, vf = (oracle.bf16_to_f32(x).astype(np.float64) for x in (q, k, v))
+    B, Sq, Hq, _ = qf.shape
+    Skv, Hkv, Dv = kf.shape[1], kf.shape[2], vf.shape[3]
+    G = Hq // Hkv
+    o = np.zeros((B, Sq, Hq, Dv))
+    lse = np.zeros((B, Hq, Sq))
+    ii, jj = np.meshgrid(np.arange(Sq), np.arange(Skv), indexing="ij")
+    for b in range(B):
+        for h in range(Hq):
+            s = qf[b, :, h] @ kf[b, :, h // G].T * scale
+            if causal:
+                s = np.where(jj <= ii, s, -np.inf)
+            m = s.max(axis=1, keepdims=True)
+            e = np.exp(s - m)
+            den = e.sum(axis=1, keepdims=True)
+            o[b, :, h] = (e / den) @ vf[b, :, h // G]
+            lse[b, h] = np.log(den[:, 0]) + m[:, 0]
+    return o, lse
+
+
+def test_mla_oracle_equals_gqa_oracle_when_dims_match():
+    """Dqk = Dv = 128: the MLA entry is the prefill oracle, bit for bit (both layouts)."""
+    q, k, v = _prefill_inputs(81, 2, 70, 90, 4, 2)
+    for causal in (True, False):
+        o, lse = oracle.prefill(q, k, v, SCALE, causal=causal)
+        om, lm = oracle.prefill_mla(q, k, v, SCALE, causal=causal)
+        assert np.array_equal(o, om) and np.array_equal(lse, lm)
+    t = lambda x: np.ascontiguousarray(x.transpose(0, 2, 1, 3))  # noqa: E731
+    ob, lb = oracle.prefill_mla(t(q), t(k), t(v), SCALE, causal=True, layout="bhsd")
+    o, lse = oracle.prefill(q, k, v, SCALE, causal=True)
+    assert np.array_equal(t(ob), o) and np.array_equal(lb, lse)
+
+
+@pytest.mark.parametrize("B,Sq,Skv,Hq,Hkv,causal,uniform", [
+    (1, 96, 96, 2, 2, True, False), (1, 64, 80, 4, 2, False, False),
+    (2, 70, 50, 2, 1, True, False), (1, 128, 128, 2, 2, True, True)])
+def test_mla_oracle_vs_numpy_f64(B, Sq, Skv, Hq, Hkv, causal, uniform):
+    Dqk, Dv = 192, 128
+    scale = 1.0 / math.sqrt(Dqk)   # the reference launcher's default (flash_mla_kernel.py)
+    q, k, v = _mla_inputs(83 + Sq, B, Sq, Skv, Hq, Hkv, Dqk, Dv, uniform)
+    o, lse = oracle.prefill_mla(q, k, v, scale, causal=causal)
+    assert o.shape == (B, Sq, Hq, Dv)
+    of, lf = _mla_numpy_f64(q, k, v, scale, causal)
+    assert_close(oracle.bf16_to_f32(o), of, "mla vs f64")
+    assert np.max(np.abs(lse - lf)) < 1e-4
+    if uniform:
+        return   # U[0, 1) inputs give near-uniform softmax rows: the mistakes below barely move O
+    # planted mistakes: scores over the first 128 dims only; the 1/sqrt(Dv) scale;
+    # V read as the first Dv columns of a Dqk-wide row (K in place of V)
+    bad, _ = oracle.prefill_mla(q[..., :128], k[..., :128], v, scale, causal=causal)
+    assert not within_tol(oracle.bf16_to_f32(bad), of)
+    bad, _ = oracle.prefill_mla(q, k, v, 1.0 / math.sqrt(Dv), causal=causal)
+    assert not within_tol(oracle.bf16_to_f32(bad), of)
+    bad, _ = oracle.prefill_mla(q, k, np.ascontiguousarray(k[..., :Dv]), scale, causal=causal)
+    assert not within_tol(oracle.bf16_to_f32(bad), of)
+    if causal and Sq <= Skv:
+        bad, _ = oracle.prefill_mla(q, k, v, scale, causal=True, q_offset=1)   # causal off by one
+        assert not within_tol(oracle.bf16_to_f32(bad), of)
+
+
+def test_mla_oracle_closed_forms():
+    """Causal row 0 = V[0]; Q = 0 gives O_i = mean(V[0..i]) and lse_i = ln(i + 1)."""
+    B, S, Hq, Hkv, Dqk, Dv = 1, 60, 2, 1, 192, 128
+    q, k, v = _mla_inputs(85, B, S, S, Hq, Hkv, Dqk, Dv)
+    o, _ = oracle.prefill_mla(q, k, v, 0.3, causal=True)
+    assert np.array_equal(o[:, 0, 0], v[:, 0, 0]) and np.array_equal(o[:, 0, 1], v[:, 0, 0])
+    qz = np.zeros_like(q)
+    o, lse = oracle.prefill_mla(qz, k, v, 0.3, causal=True)
+    vf = oracle.bf16_to_f32(v).astype(np.float64)[0, :, 0]
+    ref = np.cumsum(vf, axis=0) / np.arange(1, S + 1)[:, None]
+    for h in range(Hq):
+        assert_close(oracle.bf16_to_f32(o)[0, :, h], ref, "mla Q = 0")
+        assert np.allclose(lse[0, h], np.log(np.arange(1, S + 1)), atol=1e-5)
