@@ -296,6 +296,57 @@ def bench_mla(steps, warmup, dev):
                           "algorithmic_flops": flops})
 
 
+def _sparse_indices(B, Hkv, S, nsparse, seed, dev, recent=16):
+    """Index lists shaped like the reference test's
+    (examples/python/Triton/test_flash_sgqa_kernel.py:30-94): row i has
+    min(nsparse, i + 1) entries, its `recent` latest causal keys, then keys drawn
+    from the older causal range (here with replacement), then -1 padding."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    pos = torch.arange(S, device=dev, dtype=torch.int64)[:, None]
+    slot = torch.arange(nsparse, device=dev, dtype=torch.int64)[None, :]
+    n_valid = torch.clamp(pos + 1, max=nsparse)
+    n_recent = torch.clamp(n_valid, max=recent)
+    start = pos - n_recent + 1
+    rnd = (torch.rand((B, Hkv, S, nsparse), generator=g, device=dev) * start.clamp(min=1)).long()
+    idx = torch.where(slot < n_recent, start + slot, rnd)
+    idx = torch.where(slot < n_valid, idx, torch.full_like(idx, -1))
+    return idx.to(torch.int32).contiguous()
+
+
+def bench_sparse(steps, warmup, dev):
+    """Sparse-index prefill at the reference's sparse-GQA benchmark shape
+    (README: B=1, S=32768, Hq=16, Hkv=1, D=128, 512 entries per row, causal),
+    with index lists shaped like the reference test's (recent 16 + random)."""
+    import torch
+
+    import cuda_llm_ops_amd as fg
+    B, S, Hq, Hkv, n = 1, 32768, 16, 1, 512
+    q = _normal((B, S, Hq, 128), 15, 1.0, dev)
+    k = _normal((B, S, Hkv, 128), 16, 1.0, dev)
+    v = _normal((B, S, Hkv, 128), 17, 1.0, dev)
+    idx = _sparse_indices(B, Hkv, S, n, 18, dev)
+    out = torch.empty_like(q)
+    lse = torch.empty((B, Hq, S), dtype=torch.float32, device=dev)
+    step = fg.prepare_sparse_prefill(q, k, v, idx, SCALE, out=out, lse=lse, causal=True)
+    total_ms, per = _time_calls(step, steps, warmup)
+    # the reference's count (test_flash_sgqa_kernel.py:488-506)
+    flops = 2 * B * Hq * S * n * (128 + 128)
+    # K and V rows gathered per launch (one 256-byte K row and V row per list entry,
+    # shared by the 16 query heads); served mostly from L2 / MALL
+    gathered = B * Hkv * S * n * 2 * 256
+    avg = sum(per) / len(per)
+    tflops = flops / (avg * 1e-3) / 1e12
+    return dict(config=f"sparse-index prefill B={B} S={S} Hq={Hq} Hkv={Hkv} D=128 entries={n} causal",
+                us_avg=round(avg * 1e3, 2), us_median=round(per[len(per) // 2] * 1e3, 2),
+                us_min=round(per[0] * 1e3, 2),
+                gathered_bytes=gathered, gather_GBs=round(gathered / (avg * 1e-3) / 1e9, 1),
+                roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
+                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                          "algorithmic_flops": flops})
+
+
 def bench_backward(cfg_id, steps, warmup, dev):
     """Prefill backward (dQ, dK, dV) of a causal forward at a BASELINE prefill
     shape; one step = every launch of fgqa_prefill_backward_bf16."""
@@ -341,10 +392,11 @@ def main():
     ap.add_argument("--no-paged", action="store_true")
     ap.add_argument("--no-swa", action="store_true")
     ap.add_argument("--no-mla", action="store_true")
+    ap.add_argument("--no-sparse", action="store_true")
     ap.add_argument("--page-size", type=int, default=16, help="with --mode paged")
     ap.add_argument("--kv", choices=["bf16", "fp8"], default="bf16", help="with --mode paged")
     ap.add_argument("--all", action="store_true", help="also report configs 1, 3 and 5 (to stderr)")
-    ap.add_argument("--mode", choices=["bench", "decode", "paged", "prefill", "swa", "mla", "backward", "copy"],
+    ap.add_argument("--mode", choices=["bench", "decode", "paged", "prefill", "swa", "mla", "sparse", "backward", "copy"],
                     default="bench",
                     help="decode/prefill/copy: run only that workload (for profiling) and print its timing")
     ap.add_argument("--config", type=int, default=0,
@@ -374,6 +426,9 @@ def main():
     if args.mode == "paged":
         print(json.dumps({"mode": "paged", **bench_paged(args.config or 3, args.steps, args.warmup, dev,
                                                           args.page_size, args.kv)}), flush=True)
+        return
+    if args.mode == "sparse":
+        print(json.dumps({"mode": "sparse", **bench_sparse(args.steps, args.warmup, dev)}), flush=True)
         return
     if args.mode == "mla":
         print(json.dumps({"mode": "mla", **bench_mla(args.steps, args.warmup, dev)}), flush=True)
@@ -422,6 +477,8 @@ def main():
         line["swa"] = bench_swa(max(5, args.steps // 2), max(2, args.warmup // 2), dev)
     if not args.no_mla:
         line["mla"] = bench_mla(max(5, args.steps // 2), max(2, args.warmup // 2), dev)
+    if not args.no_sparse:
+        line["sparse"] = bench_sparse(max(5, args.steps // 5), 2, dev)
     if not args.no_backward:
         line["backward"] = bench_backward(4, max(5, args.steps // 2), max(2, args.warmup // 2), dev)
     if not args.no_cpu:

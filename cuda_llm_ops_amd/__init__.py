@@ -1,4 +1,4 @@
-"""MI355X-native flash grouped-query attention (decode incl. paged/fp8 KV caches, causal, sliding-window and MLA prefill, and the prefill backward).
+"""MI355X-native flash grouped-query attention (decode incl. paged/fp8 KV caches, causal, sliding-window, MLA and sparse-index prefill, and the prefill backward).
 
 The kernels live in libfgqa.so (HIP, gfx950); ``flash_gqa`` is the Python host
 interface over its C ABI (include/fgqa.h).
@@ -16,6 +16,9 @@ from .flash_gqa import (  # noqa: F401
     launch_flash_gqa_forward_bf16_kernel,
     launch_flash_swa_forward_bf16_kernel,
     launch_flash_mla_forward_bf16_kernel,
+    launch_flash_sgqa_forward_bf16_kernel,
+    flash_sgqa_forward_bshd,
+    prepare_sparse_prefill,
     PREFILL_HEAD_DIMS,
     paged_decode_workspace_bytes,
     prepare_backward,

@@ -142,6 +142,32 @@ class BackwardArgs(ctypes.Structure):
     ]
 
 
+class SparsePrefillArgs(ctypes.Structure):
+    """Mirror of ``fgqa_sparse_prefill_args`` (include/fgqa.h)."""
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("kv_indices", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("seqlen_q", ctypes.c_int32),
+        ("seqlen_kv", ctypes.c_int32),
+        ("num_q_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("num_sparse_kv", ctypes.c_int32),
+        ("causal", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("q_stride", _I64x3),
+        ("k_stride", _I64x3),
+        ("v_stride", _I64x3),
+        ("o_stride", _I64x3),
+        ("idx_stride", _I64x3),
+    ]
+
+
 class FgqaError(RuntimeError):
     def __init__(self, status: int, where: str):
         self.status = status
@@ -176,6 +202,8 @@ def lib() -> ctypes.CDLL:
                                                             ctypes.POINTER(ctypes.c_size_t)]
         L.fgqa_prefill_backward_bf16.restype = ctypes.c_int
         L.fgqa_prefill_backward_bf16.argtypes = [ctypes.POINTER(BackwardArgs), ctypes.c_void_p]
+        L.fgqa_sparse_prefill_bf16.restype = ctypes.c_int
+        L.fgqa_sparse_prefill_bf16.argtypes = [ctypes.POINTER(SparsePrefillArgs), ctypes.c_void_p]
         L.fgqa_status_string.restype = ctypes.c_char_p
         L.fgqa_status_string.argtypes = [ctypes.c_int]
         L.fgqa_version.restype = ctypes.c_int

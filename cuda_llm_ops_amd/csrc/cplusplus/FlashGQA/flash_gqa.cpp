@@ -245,4 +245,37 @@ void LaunchFlashMlaForwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf1
     g_last_status = fgqa_prefill_bf16(&a, nullptr);
 }
 
+void LaunchFlashSgqaForwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf16_t* v, const int32_t* kvIndices,
+                                      int numSparseKv, float scale, bf16_t* o, float* lse, int batchSize,
+                                      int seqLengthQ, int seqLengthKv, int numQueryHeads, int numKvHeads, int headDim,
+                                      bool causal) {
+    fgqa_sparse_prefill_args a;
+    std::memset(&a, 0, sizeof(a));
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.o = o;
+    a.lse = lse;
+    a.kv_indices = kvIndices;
+    a.batch = batchSize;
+    a.seqlen_q = seqLengthQ;
+    a.seqlen_kv = seqLengthKv;
+    a.num_q_heads = numQueryHeads;
+    a.num_kv_heads = numKvHeads;
+    a.head_dim = headDim;
+    a.num_sparse_kv = numSparseKv;
+    a.causal = causal ? 1 : 0;
+    a.scale = scale;
+    const int64_t qs[3] = {(int64_t)seqLengthQ * numQueryHeads * headDim, (int64_t)numQueryHeads * headDim, headDim};
+    const int64_t ks[3] = {(int64_t)seqLengthKv * numKvHeads * headDim, (int64_t)numKvHeads * headDim, headDim};
+    for (int i = 0; i < 3; ++i) {
+        a.q_stride[i] = a.o_stride[i] = qs[i];
+        a.k_stride[i] = a.v_stride[i] = ks[i];
+    }
+    a.idx_stride[0] = (int64_t)numKvHeads * seqLengthQ * numSparseKv;
+    a.idx_stride[1] = (int64_t)seqLengthQ * numSparseKv;
+    a.idx_stride[2] = numSparseKv;
+    g_last_status = fgqa_sparse_prefill_bf16(&a, nullptr);
+}
+
 int FlashGqaGetLastStatus() { return g_last_status; }

@@ -9,6 +9,7 @@ Two families of entry points:
     - ``launch_flash_gqa_backward_bf16_kernel`` <- src/python/Triton/flash_gqa_backward_kernel.py:312-478
     - ``launch_flash_swa_forward_bf16_kernel``  <- src/python/Triton/SWA/flash_swa_kernel.py:188-370
     - ``launch_flash_mla_forward_bf16_kernel``  <- src/python/Triton/flash_mla_kernel.py:315-508
+    - ``launch_flash_sgqa_forward_bf16_kernel`` <- src/python/Triton/SparseGQA/flash_sgqa_kernel.py:202-396
 * The C++ layouts of the reference's C++ decode entry point (Q/O ``[B,Hq,D]``,
   K/V ``[B,S,Hkv,D]``, decode_flash_gqa_kernel.cuh:28-38) and of the new C++
   prefill entry point (BSHD):
@@ -35,6 +36,9 @@ __all__ = [
     "launch_flash_gqa_backward_bf16_kernel",
     "launch_flash_swa_forward_bf16_kernel",
     "launch_flash_mla_forward_bf16_kernel",
+    "launch_flash_sgqa_forward_bf16_kernel",
+    "flash_sgqa_forward_bshd",
+    "prepare_sparse_prefill",
     "PREFILL_HEAD_DIMS",
     "decode_flash_gqa_bshd",
     "decode_flash_gqa_paged",
@@ -810,6 +814,199 @@ def launch_flash_swa_forward_bf16_kernel(q, k, v, scale=None, out=None, lse=None
     sink = sink_value.to(torch.float32).contiguous()
     qb, kb, vb = _prep(qb), _prep(kb), _prep(vb)
     _prefill(qb, kb, vb, out_b, lse_b, scale, True, "bhsd", int(window_size), sink)
+    if squeeze_output:
+        return out_b.squeeze(0), lse_b.squeeze(0)
+    return out_b, lse_b
+
+
+# --------------------------------------------------------------------------- sparse-index prefill
+def _sparse_args(q, k, v, o, lse, idx, scale, causal, layout) -> _lib.SparsePrefillArgs:
+    """C ABI argument block; q/k/v/o 4-D in `layout` ('bshd' or 'bhsd'), idx [B, Hkv, Sq, n]."""
+    def sbh(t):
+        if layout == "bshd":
+            return [t.stride(0), t.stride(1), t.stride(2)]
+        return [t.stride(0), t.stride(2), t.stride(1)]
+
+    if layout == "bshd":
+        B, Sq, Hq, D = q.shape
+        _, Skv, Hkv, _ = k.shape
+    else:
+        B, Hq, Sq, D = q.shape
+        _, Hkv, Skv, _ = k.shape
+    a = _lib.SparsePrefillArgs()
+    a.q, a.k, a.v, a.o, a.lse, a.kv_indices = (_ptr(x) for x in (q, k, v, o, lse, idx))
+    a.batch, a.seqlen_q, a.seqlen_kv = B, Sq, Skv
+    a.num_q_heads, a.num_kv_heads, a.head_dim = Hq, Hkv, D
+    a.num_sparse_kv = idx.shape[3]
+    a.causal = 1 if causal else 0
+    a.scale = float(scale)
+    a.q_stride[:] = sbh(q)
+    a.k_stride[:] = sbh(k)
+    a.v_stride[:] = sbh(v)
+    a.o_stride[:] = sbh(o)
+    a.idx_stride[:] = [idx.stride(0), idx.stride(1), idx.stride(2)]
+    return a
+
+
+def _check_indices(idx, B, Hkv, Sq):
+    if not isinstance(idx, torch.Tensor) or idx.dtype != torch.int32:
+        raise ValueError("kv_indices must be an int32 tensor")
+    if idx.dim() != 4 or idx.shape[:3] != (B, Hkv, Sq) or idx.shape[3] < 1:
+        raise ValueError("kv_indices must be [batch, num_kv_heads, seqlen_q, num_sparse_kv]")
+    if idx.stride(3) != 1:
+        idx = idx.contiguous()
+    return idx
+
+
+def _sparse_bshd_prepare(q, k, v, kv_indices, scale, out, lse, causal):
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise ValueError("Flash SGQA forward expects bf16 inputs")
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("expected 4-D BSHD tensors")
+    _require_cuda(q, k, v, kv_indices)
+    B, Sq, Hq, D = q.shape
+    if k.shape != v.shape or k.shape[0] != B or k.shape[3] != D:
+        raise ValueError("K and V must be [B, Skv, Hkv, D] matching Q")
+    if Hq % k.shape[2] != 0:
+        raise ValueError("Query heads must be divisible by KV heads")
+    if D != 128:
+        raise ValueError("head_dim must be 128 on this path")
+    idx = _check_indices(kv_indices, B, k.shape[2], Sq)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    q, k, v = _prep(q), _prep(k), _prep(v)
+    if out is None:
+        out = torch.empty((B, Sq, Hq, D), device=q.device, dtype=torch.bfloat16)
+    elif out.shape != (B, Sq, Hq, D) or out.dtype != torch.bfloat16 or not _kernel_ready(out):
+        raise ValueError("Output must be a bf16 [batch, seqlen_q, q_heads, head_dim] tensor with contiguous rows")
+    if lse is None:
+        lse = torch.empty((B, Hq, Sq), device=q.device, dtype=torch.float32)
+    elif lse.shape != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise ValueError("LSE must be a contiguous fp32 [batch, q_heads, seqlen_q] tensor")
+    a = _sparse_args(q, k, v, out, lse, idx, scale, causal, "bshd")
+    return a, out, lse, (q, k, v, out, lse, idx)
+
+
+def flash_sgqa_forward_bshd(q, k, v, kv_indices, scale=None, out=None, lse=None, causal=True):
+    """Sparse-index prefill in BSHD: q [B,Sq,Hq,D], k/v [B,Skv,Hkv,D], kv_indices
+    int32 [B,Hkv,Sq,n] (key lists shared by a KV head's query heads; entries
+    < 0, >= Skv or, if causal, > the row are skipped) -> (out [B,Sq,Hq,D], lse [B,Hq,Sq])."""
+    a, out, lse, _keep = _sparse_bshd_prepare(q, k, v, kv_indices, scale, out, lse, causal)
+    _lib.check(_lib.lib().fgqa_sparse_prefill_bf16(ctypes.byref(a), ctypes.c_void_p(_stream())),
+               "fgqa_sparse_prefill_bf16")
+    return out, lse
+
+
+def prepare_sparse_prefill(q, k, v, kv_indices, scale=None, out=None, lse=None, causal=True):
+    """``flash_sgqa_forward_bshd`` validated once; returns a ``PreparedLaunch``
+    (the LSE tensor is ``.lse``)."""
+    a, out, lse, keep = _sparse_bshd_prepare(q, k, v, kv_indices, scale, out, lse, causal)
+    pl = PreparedLaunch(_lib.lib().fgqa_sparse_prefill_bf16, a, keep, out, "fgqa_sparse_prefill_bf16")
+    pl.lse = lse
+    return pl
+
+
+def launch_flash_sgqa_forward_bf16_kernel(q, k, v, sparse_kv_indices, num_sparse_kv, scale=None, out=None,
+                                          lse=None, causal=True, block_sparse_sub=None, num_warps=None,
+                                          num_stages=None):
+    """Mirror of the reference's Triton sparse-GQA launcher
+    (src/python/Triton/SparseGQA/flash_sgqa_kernel.py:202-396): BHSD q [B,Hq,Sq,D] (or
+    3-D [Hq,Sq,D]), k/v [B,Hkv,Skv,D], sparse_kv_indices int32
+    [B,Hkv,Sq,num_sparse_kv]; returns (out, lse [B,Hq,Sq]).
+
+    Same checks and ValueError messages as the reference (:247-361), including
+    its rule that a provided out/lse must be contiguous.  ``block_sparse_sub``,
+    ``num_warps`` and ``num_stages`` are validated as the reference does and
+    otherwise unused (Triton tuning knobs).  Beyond the reference, head_dim and
+    head_dim_v must be 128.
+    """
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise ValueError("Flash SGQA forward expects bf16 inputs")
+    if sparse_kv_indices.dtype != torch.int32:
+        raise ValueError("sparse_kv_indices must be int32")
+    if sparse_kv_indices.dim() != 4:
+        raise ValueError("sparse_kv_indices must be 4D [batch, num_kv_heads, seqlen_q, num_sparse_kv]")
+    if not isinstance(num_sparse_kv, int):
+        raise ValueError("num_sparse_kv must be an int")
+    if num_sparse_kv < 1:
+        raise ValueError("num_sparse_kv must be >= 1")
+    if block_sparse_sub is not None and (not isinstance(block_sparse_sub, int) or block_sparse_sub < 1):
+        raise ValueError("block_sparse_sub must be None or an int >= 1")
+    if num_warps is not None and (not isinstance(num_warps, int) or num_warps < 1):
+        raise ValueError("num_warps must be None or an int >= 1")
+    if num_stages is not None and (not isinstance(num_stages, int) or num_stages < 1):
+        raise ValueError("num_stages must be None or an int >= 1")
+    if q.dim() not in (3, 4):
+        raise ValueError("Q must be 3D or 4D")
+    if k.dim() != q.dim() or v.dim() != q.dim():
+        raise ValueError("Q, K, and V must have matching ranks")
+    _require_cuda(q, k, v, sparse_kv_indices)
+    squeeze_output = q.dim() == 3
+    qb = q.unsqueeze(0) if squeeze_output else q
+    kb = k.unsqueeze(0) if squeeze_output else k
+    vb = v.unsqueeze(0) if squeeze_output else v
+    batch, q_heads, seqlen_q, head_dim_qk = qb.shape
+    _, num_kv_heads, seqlen_kv, k_head_dim = kb.shape
+    _, v_heads, v_seqlen, head_dim_v = vb.shape
+    if seqlen_kv != v_seqlen:
+        raise ValueError("K and V must share sequence length")
+    if k_head_dim != head_dim_qk:
+        raise ValueError("Q and K must share head_dim_qk")
+    if v_heads != num_kv_heads:
+        raise ValueError("K and V must share number of KV heads")
+    if q_heads % num_kv_heads != 0:
+        raise ValueError("Query heads must be divisible by KV heads")
+    if sparse_kv_indices.shape != (batch, num_kv_heads, seqlen_q, num_sparse_kv):
+        raise ValueError("sparse_kv_indices must have shape "
+                         f"[batch, num_kv_heads, seqlen_q, {num_sparse_kv}]")
+    if head_dim_qk != 128 or head_dim_v != 128:
+        raise ValueError("head_dim_qk and head_dim_v must be 128 on this path")
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim_qk)
+    if out is None:
+        out_b = torch.empty((batch, q_heads, seqlen_q, head_dim_v), device=qb.device, dtype=torch.bfloat16)
+    else:
+        if squeeze_output:
+            if out.dim() != 3:
+                raise ValueError("Output must be 3D when Q is 3D")
+            if not out.is_contiguous():
+                raise ValueError("Output must be contiguous when provided")
+            out_b = out.unsqueeze(0)
+        else:
+            if out.dim() != 4:
+                raise ValueError("Output must be 4D when Q is 4D")
+            if not out.is_contiguous():
+                raise ValueError("Output must be contiguous when provided")
+            out_b = out
+        if out_b.dtype != torch.bfloat16:
+            raise ValueError("Output must be bf16")
+    if out_b.shape != (batch, q_heads, seqlen_q, head_dim_v):
+        raise ValueError("Output must have shape [batch, q_heads, seqlen_q, head_dim_v]")
+    if lse is None:
+        lse_b = torch.empty((batch, q_heads, seqlen_q), device=qb.device, dtype=torch.float32)
+    else:
+        if squeeze_output:
+            if lse.dim() != 2:
+                raise ValueError("LSE must be 2D when Q is 3D")
+            if not lse.is_contiguous():
+                raise ValueError("LSE must be contiguous when provided")
+            lse_b = lse.unsqueeze(0)
+        else:
+            if lse.dim() != 3:
+                raise ValueError("LSE must be 3D when Q is 4D")
+            if not lse.is_contiguous():
+                raise ValueError("LSE must be contiguous when provided")
+            lse_b = lse
+        if lse_b.dtype != torch.float32:
+            raise ValueError("LSE must be fp32")
+    if lse_b.shape != (batch, q_heads, seqlen_q):
+        raise ValueError("LSE must have shape [batch, q_heads, seqlen_q]")
+    if seqlen_q > 0:
+        qb, kb, vb = _prep(qb), _prep(kb), _prep(vb)
+        idx = sparse_kv_indices if sparse_kv_indices.stride(3) == 1 else sparse_kv_indices.contiguous()
+        a = _sparse_args(qb, kb, vb, out_b, lse_b, idx, scale, causal, "bhsd")
+        _lib.check(_lib.lib().fgqa_sparse_prefill_bf16(ctypes.byref(a), ctypes.c_void_p(_stream())),
+                   "fgqa_sparse_prefill_bf16")
     if squeeze_output:
         return out_b.squeeze(0), lse_b.squeeze(0)
     return out_b, lse_b

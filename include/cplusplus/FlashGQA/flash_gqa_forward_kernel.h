@@ -110,3 +110,29 @@ void LaunchFlashMlaForwardBf16Kernel(const bf16_t* q,
                                      int headDimQk,
                                      int headDimV,
                                      bool causal);
+
+/**
+ * @brief Sparse-index GQA prefill forward (BSHD), the C++ counterpart of the
+ *        reference's Triton-only sparse-GQA launcher
+ *        (src/python/Triton/SparseGQA/flash_sgqa_kernel.py:202-396, kernel
+ *        :15-137).  Query row i of every query head of KV head h attends the
+ *        keys listed in kvIndices[b][h][i][0 .. numSparseKv); entries < 0,
+ *        >= seqLengthKv or (causal) > i are skipped, duplicates count twice.
+ * @param kvIndices Device int32 [batchSize, numKvHeads, seqLengthQ, numSparseKv], contiguous.
+ * @param lse Device fp32 [batchSize, numQueryHeads, seqLengthQ] (natural log), or nullptr.
+ */
+void LaunchFlashSgqaForwardBf16Kernel(const bf16_t* q,
+                                      const bf16_t* k,
+                                      const bf16_t* v,
+                                      const int32_t* kvIndices,
+                                      int numSparseKv,
+                                      float scale,
+                                      bf16_t* o,
+                                      float* lse,
+                                      int batchSize,
+                                      int seqLengthQ,
+                                      int seqLengthKv,
+                                      int numQueryHeads,
+                                      int numKvHeads,
+                                      int headDim,
+                                      bool causal);

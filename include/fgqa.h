@@ -246,6 +246,47 @@ int fgqa_prefill_backward_workspace_bytes(const fgqa_prefill_backward_args* args
 
 int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* args, void* stream);
 
+/*
+ * Sparse-index GQA prefill forward.  Replaces the Triton-only
+ * launch_flash_sgqa_forward_bf16_kernel, reference
+ * src/python/Triton/SparseGQA/flash_sgqa_kernel.py:202-396 (kernel :15-137).
+ *
+ *   q  [B, Sq, Hq, D], k/v [B, Skv, Hkv, D], o [B, Sq, Hq, D]: strides
+ *      {batch, sequence, head} as in fgqa_prefill_args; D = 128.
+ *   kv_indices  int32, entry e of query row i of kv head h at
+ *      kv_indices + b*idx_stride[0] + h*idx_stride[1] + i*idx_stride[2] + e,
+ *      e < num_sparse_kv (the reference's [B, Hkv, Sq, num_sparse_kv]).
+ *      Query row i of every query head of kv head h attends the listed keys:
+ *      an entry j is used when 0 <= j < seqlen_kv and, if causal, j <= i
+ *      (others, e.g. -1 padding, are skipped); a key listed twice counts twice.
+ *   lse  fp32 [B, Hq, Sq] contiguous, natural log (nullable).  A row with no
+ *      usable entry gives O = 0 and lse = -inf.
+ */
+typedef struct fgqa_sparse_prefill_args {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* lse;
+    const int32_t* kv_indices;
+    int32_t batch;
+    int32_t seqlen_q;
+    int32_t seqlen_kv;
+    int32_t num_q_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t num_sparse_kv;
+    int32_t causal;
+    float scale;
+    int64_t q_stride[3];
+    int64_t k_stride[3];
+    int64_t v_stride[3];
+    int64_t o_stride[3];
+    int64_t idx_stride[3];
+} fgqa_sparse_prefill_args;
+
+int fgqa_sparse_prefill_bf16(const fgqa_sparse_prefill_args* args, void* stream);
+
 /* Static, human-readable text for a status code. */
 const char* fgqa_status_string(int status);
 

@@ -18,4 +18,5 @@ from .oracle import (  # noqa: F401
     prefill_backward,
     prefill_mla,
     prefill_swa,
+    sparse_prefill,
 )

@@ -662,3 +662,82 @@ int fgqa_oracle_attention_backward_f64(const uint16_t* q, const uint16_t* k, con
         }
     return 0;
 }
+
+/*
+ * Sparse-index prefill.  Per (batch, query head h, query row i) this follows
+ * the torch reference examples/python/Triton/test_flash_sgqa_kernel.py:97-222:
+ *   :185-188  slot s of row i holds key index j = idx[b][h / G][i][s]; it is
+ *             valid when 0 <= j < Skv and, if causal, j <= the row's position
+ *   :194-195  scores = (q . k_j) * scale over every slot (fp32), -inf if invalid
+ *   :197-201  row_max; e = exp(scores - row_max), 0 where invalid; denom = sum(e);
+ *             probs = e / denom (0 when denom == 0)
+ *   :203-208  out = probs . v_j (fp32), lse = log(denom) + row_max, or -inf when
+ *             denom == 0; out cast to bf16 (:212)
+ * Slots are visited in order, so a key listed twice counts twice.
+ */
+int fgqa_oracle_sparse_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                    float scale, uint16_t* o, float* lse,
+                                    int batch, int sq, int skv, int hq, int hkv, int d,
+                                    const int64_t* qs, const int64_t* ks,
+                                    const int64_t* vs, const int64_t* os,
+                                    const int32_t* idx, const int64_t* is, int nsparse,
+                                    int causal, int q_offset, int nthreads) {
+    if (!q || !k || !v || !o || !qs || !ks || !vs || !os || !idx || !is) return -1;
+    if (batch < 0 || sq < 0 || skv < 0 || hq <= 0 || hkv <= 0 || d <= 0 || d > ORACLE_MAX_D) return -1;
+    if (hq % hkv != 0 || nsparse < 1) return -1;
+    const int group = hq / hkv;
+    set_threads(nthreads);
+
+#pragma omp parallel
+    {
+        float* sc = (float*)malloc(sizeof(float) * (size_t)nsparse);
+        int* kj = (int*)malloc(sizeof(int) * (size_t)nsparse);
+        float out[ORACLE_MAX_D];
+#pragma omp for collapse(3) schedule(dynamic, 4)
+        for (int b = 0; b < batch; ++b) {
+            for (int h = 0; h < hq; ++h) {
+                for (int i = 0; i < sq; ++i) {
+                    const int kvh = h / group;
+                    const uint16_t* qrow = q + b * qs[0] + (int64_t)i * qs[1] + h * qs[2];
+                    uint16_t* orow = o + b * os[0] + (int64_t)i * os[1] + h * os[2];
+                    const int32_t* list = idx + b * is[0] + kvh * is[1] + (int64_t)i * is[2];
+                    const long pos = (long)i + q_offset;
+                    int nvis = 0;
+                    float rmax = -INFINITY;
+                    for (int s = 0; s < nsparse; ++s) {
+                        const int j = list[s];
+                        if (j < 0 || j >= skv || (causal && j > pos)) continue;
+                        const uint16_t* krow = k + b * ks[0] + (int64_t)j * ks[1] + kvh * ks[2];
+                        float acc = 0.f;
+                        for (int x = 0; x < d; ++x) acc += bf(qrow[x]) * bf(krow[x]);
+                        kj[nvis] = j;
+                        sc[nvis] = acc * scale;
+                        rmax = fmaxf(rmax, sc[nvis]);
+                        ++nvis;
+                    }
+                    if (nvis == 0) {
+                        for (int x = 0; x < d; ++x) orow[x] = 0;
+                        if (lse) lse[((size_t)b * hq + h) * sq + i] = -INFINITY;
+                        continue;
+                    }
+                    float sum = 0.f;
+                    for (int t = 0; t < nvis; ++t) {
+                        sc[t] = expf(sc[t] - rmax);
+                        sum += sc[t];
+                    }
+                    for (int x = 0; x < d; ++x) out[x] = 0.f;
+                    for (int t = 0; t < nvis; ++t) {
+                        const uint16_t* vrow = v + b * vs[0] + (int64_t)kj[t] * vs[1] + kvh * vs[2];
+                        const float pj = sc[t] / sum;
+                        for (int x = 0; x < d; ++x) out[x] += pj * bf(vrow[x]);
+                    }
+                    for (int x = 0; x < d; ++x) orow[x] = fgqa_oracle_f32_to_bf16(out[x]);
+                    if (lse) lse[((size_t)b * hq + h) * sq + i] = logf(sum) + rmax;
+                }
+            }
+        }
+        free(kj);
+        free(sc);
+    }
+    return 0;
+}

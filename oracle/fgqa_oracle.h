@@ -39,6 +39,11 @@
  *                                            window >= Sq and no sink; a float64 numpy
  *                                            restatement with the window and sink; closed
  *                                            forms (window 1: O = V[i] / (1 + sink e^-s_ii))
+ *   fgqa_oracle_sparse_prefill_bf16         bit-identical to fgqa_oracle_prefill_bf16 when
+ *                                            every row lists keys 0..Skv-1 in order; a
+ *                                            float64 numpy restatement; closed forms (one
+ *                                            valid entry: O = V[j]; none: O = 0, lse = -inf;
+ *                                            a key listed twice = its score + ln 2)
  *   fgqa_oracle_attention_f64               textbook softmax attention in double;
  *                                            pinned by numpy float64 restatement and
  *                                            closed forms on tiny inputs
@@ -206,6 +211,24 @@ int fgqa_oracle_prefill_swa_bf16(const uint16_t* q, const uint16_t* k, const uin
                                  const int64_t* q_strides, const int64_t* k_strides,
                                  const int64_t* v_strides, const int64_t* o_strides,
                                  int window, const float* sink, int q_offset, int nthreads);
+
+/*
+ * Sparse-index prefill, restating the reference's torch reference
+ * examples/python/Triton/test_flash_sgqa_kernel.py:97-222: query row i of head
+ * h attends the keys listed in idx[b][h / G][i][0 .. nsparse), skipping
+ * entries < 0, >= skv or (causal) > i + q_offset; a key listed twice counts
+ * twice.  fp32 scores, full softmax, fp32 P.V, bf16 O; a row with no valid
+ * entry gives O = 0 and lse = -inf.
+ *   idx: int32, idx_strides = {batch, kv head, query row} in elements, the
+ *        entry dim contiguous.  Other layouts as fgqa_oracle_prefill_bf16.
+ */
+int fgqa_oracle_sparse_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                    float scale, uint16_t* o, float* lse,
+                                    int batch, int sq, int skv, int hq, int hkv, int d,
+                                    const int64_t* q_strides, const int64_t* k_strides,
+                                    const int64_t* v_strides, const int64_t* o_strides,
+                                    const int32_t* idx, const int64_t* idx_strides, int nsparse,
+                                    int causal, int q_offset, int nthreads);
 
 /*
  * Textbook softmax attention in double precision (the mathematical answer the

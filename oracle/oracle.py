@@ -57,6 +57,12 @@ def lib() -> ctypes.CDLL:
             _u16p, _u16p, _u16p, ctypes.c_float, _u16p, _f32p,
             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
             _i64p, _i64p, _i64p, _i64p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.fgqa_oracle_sparse_prefill_bf16.restype = ctypes.c_int
+        L.fgqa_oracle_sparse_prefill_bf16.argtypes = [
+            _u16p, _u16p, _u16p, ctypes.c_float, _u16p, _f32p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            _i64p, _i64p, _i64p, _i64p, _i32p, _i64p, ctypes.c_int,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int]
         L.fgqa_oracle_attention_f64.restype = ctypes.c_int
         L.fgqa_oracle_attention_f64.argtypes = [
             _u16p, _u16p, _u16p, ctypes.c_double, _f64p, _f64p,
@@ -203,6 +209,34 @@ def prefill_mla(q, k, v, scale, causal=True, layout="bshd", q_offset=0, nthreads
         _ptr(os_, ctypes.c_int64), int(bool(causal)), int(q_offset), int(nthreads))
     if rc != 0:
         raise ValueError("fgqa_oracle_prefill_mla_bf16: invalid arguments")
+    return o, lse
+
+
+def sparse_prefill(q, k, v, idx, scale, causal=True, layout="bshd", q_offset=0, nthreads=0):
+    """Sparse-index prefill oracle.  idx: int32 [B, Hkv, Sq, nsparse] (key index
+    lists, -1 = empty slot).  Layouts of q/k/v as `prefill`.  Returns (o in q's
+    layout, lse [B,Hq,Sq])."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    idx = np.ascontiguousarray(idx, dtype=np.int32)
+    B, Sq, Hq, D = _dims(q, layout)
+    _, Skv, Hkv, _ = _dims(k, layout)
+    if idx.ndim != 4 or idx.shape[:3] != (B, Hkv, Sq):
+        raise ValueError("sparse_prefill: idx must be [B, Hkv, Sq, nsparse]")
+    o = np.empty_like(q)
+    lse = np.empty((B, Hq, Sq), dtype=np.float32)
+    qs, ks, vs, os_ = (_strides(x, layout) for x in (q, k, v, o))
+    ist = np.array([idx.strides[0] // 4, idx.strides[1] // 4, idx.strides[2] // 4], dtype=np.int64)
+    rc = lib().fgqa_oracle_sparse_prefill_bf16(
+        _ptr(q, ctypes.c_uint16), _ptr(k, ctypes.c_uint16), _ptr(v, ctypes.c_uint16),
+        float(scale), _ptr(o, ctypes.c_uint16), _ptr(lse, ctypes.c_float),
+        B, Sq, Skv, Hq, Hkv, D,
+        _ptr(qs, ctypes.c_int64), _ptr(ks, ctypes.c_int64), _ptr(vs, ctypes.c_int64),
+        _ptr(os_, ctypes.c_int64), _ptr(idx, ctypes.c_int32), _ptr(ist, ctypes.c_int64),
+        idx.shape[3], int(bool(causal)), int(q_offset), int(nthreads))
+    if rc != 0:
+        raise ValueError("fgqa_oracle_sparse_prefill_bf16: invalid arguments")
     return o, lse
 
 

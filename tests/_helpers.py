@@ -121,3 +121,45 @@ def make_paged(k, v, lens, page_size, rng, extra_pages=3):
             kc[pg, : t1 - t0] = k[b, t0:t1]
             vc[pg, : t1 - t0] = v[b, t0:t1]
     return kc, vc, table
+
+
+def build_sparse_indices(seed, B, Hkv, Sq, Skv, nsparse, recent=16):
+    """Key index lists shaped like the reference test's
+    (examples/python/Triton/test_flash_sgqa_kernel.py:30-94): row i lists its
+    `recent` latest causal keys first, then distinct keys sampled without
+    replacement from the older causal range, then -1 padding.  int32
+    [B, Hkv, Sq, nsparse]; numpy's generator replaces torch's."""
+    rng = np.random.default_rng(seed)
+    idx = np.full((B, Hkv, Sq, nsparse), -1, dtype=np.int32)
+    for i in range(Sq):
+        upper = min(i, Skv - 1)
+        n_valid = min(nsparse, upper + 1)
+        n_recent = min(recent, n_valid)
+        start = upper - n_recent + 1
+        if n_recent > 0:
+            idx[:, :, i, :n_recent] = np.arange(start, upper + 1, dtype=np.int32)
+        rest = n_valid - n_recent
+        if rest > 0:
+            for b in range(B):
+                for h in range(Hkv):
+                    idx[b, h, i, n_recent:n_recent + rest] = rng.permutation(start)[:rest]
+    return idx
+
+
+def gpu_sparse_indices(B, Hkv, S, nsparse, seed, device, recent=16):
+    """Index lists of the reference test's shape, built on the GPU for long
+    sequences: row i has min(nsparse, i + 1) usable entries, its `recent`
+    latest causal keys first, then keys drawn uniformly (with replacement)
+    from the older causal range, then -1 padding.  int32 [B, Hkv, S, nsparse]."""
+    import torch
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    pos = torch.arange(S, device=device, dtype=torch.int64)[:, None]
+    slot = torch.arange(nsparse, device=device, dtype=torch.int64)[None, :]
+    n_valid = torch.clamp(pos + 1, max=nsparse)
+    n_recent = torch.clamp(n_valid, max=recent)
+    start = pos - n_recent + 1                      # first recent key
+    rnd = (torch.rand((B, Hkv, S, nsparse), generator=g, device=device) * start.clamp(min=1)).long()
+    idx = torch.where(slot < n_recent, start + slot, rnd)
+    idx = torch.where(slot < n_valid, idx, torch.full_like(idx, -1))
+    return idx.to(torch.int32).contiguous()

@@ -24,7 +24,7 @@ def test_c_abi_symbols_exported():
     names = set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(fgqa_\w+)\s*\(", hdr, flags=re.M))
     assert names == {"fgqa_decode_workspace_bytes", "fgqa_decode_bf16", "fgqa_prefill_bf16",
                      "fgqa_prefill_backward_workspace_bytes", "fgqa_prefill_backward_bf16",
-                     "fgqa_decode_paged_workspace_bytes", "fgqa_decode_paged",
+                     "fgqa_decode_paged_workspace_bytes", "fgqa_decode_paged", "fgqa_sparse_prefill_bf16",
                      "fgqa_status_string", "fgqa_version"}
     L = _lib.lib()
     syms = _exported()
@@ -44,7 +44,7 @@ def test_cplusplus_entry_points_exported():
                           "LaunchFlashGqaBf16KernelPaged",
                           "LaunchFlashGqaForwardBf16Kernel", "LaunchFlashGqaForwardBf16KernelStrided",
                           "LaunchFlashGqaBackwardBf16Kernel", "LaunchFlashSwaForwardBf16Kernel",
-                          "LaunchFlashMlaForwardBf16Kernel"}
+                          "LaunchFlashMlaForwardBf16Kernel", "LaunchFlashSgqaForwardBf16Kernel"}
     for d in decls:
         assert re.search(rf"\bT {d}\(", syms), d
     # the drop-in keeps the reference's exact parameter list
@@ -181,7 +181,8 @@ def test_ctypes_structs_match_the_header(tmp_path):
     """Every ctypes mirror in _lib has the C struct's size and field offsets
     (a small C program compiled against include/fgqa.h prints them)."""
     mirrors = {"fgqa_decode_args": _lib.DecodeArgs, "fgqa_decode_paged_args": _lib.PagedDecodeArgs,
-               "fgqa_prefill_args": _lib.PrefillArgs, "fgqa_prefill_backward_args": _lib.BackwardArgs}
+               "fgqa_prefill_args": _lib.PrefillArgs, "fgqa_prefill_backward_args": _lib.BackwardArgs,
+               "fgqa_sparse_prefill_args": _lib.SparsePrefillArgs}
     lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "fgqa.h"', "int main(void) {"]
     for cname, py in mirrors.items():
         lines.append(f'    printf("{cname} size %zu\\n", sizeof({cname}));')
@@ -198,6 +199,77 @@ def test_ctypes_structs_match_the_header(tmp_path):
         assert got[(cname, "size")] == ctypes.sizeof(py), cname
         for fname, _ in py._fields_:
             assert got[(cname, fname)] == getattr(py, fname).offset, f"{cname}.{fname}"
+
+
+def _sparse_args(**kw):
+    a = _lib.SparsePrefillArgs()
+    B, Sq, Skv, Hq, Hkv, D, n = (kw.get(nm, d) for nm, d in (("B", 1), ("Sq", 256), ("Skv", 256), ("Hq", 16),
+                                                               ("Hkv", 1), ("D", 128), ("n", 64)))
+    a.batch, a.seqlen_q, a.seqlen_kv, a.num_q_heads, a.num_kv_heads, a.head_dim = B, Sq, Skv, Hq, Hkv, D
+    a.num_sparse_kv = n
+    a.causal = 1
+    a.scale = kw.get("scale", D ** -0.5)
+    a.q_stride[:] = [Sq * Hq * D, Hq * D, D]
+    a.o_stride[:] = [Sq * Hq * D, Hq * D, D]
+    a.k_stride[:] = [Skv * Hkv * D, Hkv * D, D]
+    a.v_stride[:] = [Skv * Hkv * D, Hkv * D, D]
+    a.idx_stride[:] = [Hkv * Sq * n, Sq * n, n]
+    for name in ("q", "k", "v", "o", "kv_indices"):
+        setattr(a, name, kw.get(name, 4096))
+    return a
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(Hq=15, Hkv=2), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(n=0), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(Skv=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(scale=float("nan")), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(D=64), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(kv_indices=None), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(kv_indices=4098), _lib.FGQA_ERR_UNSUPPORTED),   # int32 entries need 4-byte alignment
+    (dict(q=4096 + 8), _lib.FGQA_ERR_UNSUPPORTED),
+])
+def test_sparse_prefill_rejects_before_launch(kw, code):
+    assert _lib.lib().fgqa_sparse_prefill_bf16(ctypes.byref(_sparse_args(**kw)), None) == code
+
+
+def test_sparse_prefill_empty_is_noop():
+    L = _lib.lib()
+    assert L.fgqa_sparse_prefill_bf16(ctypes.byref(_sparse_args(Sq=0, q=None)), None) == 0
+    assert L.fgqa_sparse_prefill_bf16(ctypes.byref(_sparse_args(B=0, kv_indices=None)), None) == 0
+
+
+def test_sparse_mirror_validation_without_gpu():
+    """The mirror raises the reference's ValueErrors
+    (SparseGQA/flash_sgqa_kernel.py:247-266) before touching a GPU."""
+    import torch
+    bf = torch.bfloat16
+    q = torch.zeros(1, 4, 8, 128, dtype=bf)
+    k = torch.zeros(1, 1, 8, 128, dtype=bf)
+    idx = torch.zeros(1, 1, 8, 4, dtype=torch.int32)
+    f = fg.launch_flash_sgqa_forward_bf16_kernel
+    with pytest.raises(ValueError, match="Flash SGQA forward expects bf16 inputs"):
+        f(q.half(), k, k, idx, 4)
+    with pytest.raises(ValueError, match="sparse_kv_indices must be int32"):
+        f(q, k, k, idx.long(), 4)
+    with pytest.raises(ValueError, match="sparse_kv_indices must be 4D"):
+        f(q, k, k, idx[0], 4)
+    with pytest.raises(ValueError, match="num_sparse_kv must be an int"):
+        f(q, k, k, idx, 4.0)
+    with pytest.raises(ValueError, match="num_sparse_kv must be >= 1"):
+        f(q, k, k, idx, 0)
+    with pytest.raises(ValueError, match="block_sparse_sub must be None or an int >= 1"):
+        f(q, k, k, idx, 4, block_sparse_sub=0)
+    with pytest.raises(ValueError, match="num_warps must be None"):
+        f(q, k, k, idx, 4, num_warps="8")
+    with pytest.raises(ValueError, match="num_stages must be None"):
+        f(q, k, k, idx, 4, num_stages=-1)
+    with pytest.raises(ValueError, match="Q must be 3D or 4D"):
+        f(q[0, 0], k[0, 0], k[0, 0], idx, 4)
+    with pytest.raises(ValueError, match="matching ranks"):
+        f(q, k[0], k, idx, 4)
+    with pytest.raises(ValueError, match="GPU"):
+        f(q, k, k, idx, 4)
 
 
 def test_prefill_empty_is_noop():

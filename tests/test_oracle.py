@@ -695,3 +695,111 @@ def test_mla_oracle_closed_forms():
     for h in range(Hq):
         assert_close(oracle.bf16_to_f32(o)[0, :, h], ref, "mla Q = 0")
         assert np.allclose(lse[0, h], np.log(np.arange(1, S + 1)), atol=1e-5)
+
+
+# ----------------------------------------------------------------- sparse-index prefill oracle
+def _sparse_numpy_f64(q, k, v, idx, scale, causal):
+    """float64 restatement of test_flash_sgqa_kernel.py:168-222 (BSHD)."""
+    qf, kf, vf = (oracle.bf16_to_f32(x).astype(np.float64) for x in (q, k, v))
+    B, Sq, Hq, D = qf.shape
+    Skv, Hkv = kf.shape[1], kf.shape[2]
+    G = Hq // Hkv
+    o = np.zeros((B, Sq, Hq, D))
+    lse = np.full((B, Hq, Sq), -np.inf)
+    for b in range(B):
+        for h in range(Hq):
+            for i in range(Sq):
+                j = idx[b, h // G, i].astype(np.int64)
+                ok = (j >= 0) & (j < Skv)
+                if causal:
+                    ok &= j <= i
+                if not ok.any():
+                    continue
+                jj = j[ok]
+                s = kf[b, jj, h // G] @ qf[b, i, h] * scale
+                m = s.max()
+                e = np.exp(s - m)
+                o[b, i, h] = (e / e.sum()) @ vf[b, jj, h // G]
+                lse[b, h, i] = math.log(e.sum()) + m
+    return o, lse
+
+
+def test_sparse_oracle_dense_lists_equal_the_prefill_oracle():
+    """Every row listing keys 0..Skv-1 in order: the causal (and full) prefill oracle, bit for bit."""
+    B, S, Hq, Hkv = 1, 80, 4, 2
+    q, k, v = _prefill_inputs(91, B, S, S, Hq, Hkv)
+    idx = np.broadcast_to(np.arange(S, dtype=np.int32), (B, Hkv, S, S)).copy()
+    for causal in (True, False):
+        o, lse = oracle.prefill(q, k, v, SCALE, causal=causal)
+        os_, ls = oracle.sparse_prefill(q, k, v, idx, SCALE, causal=causal)
+        assert np.array_equal(o, os_) and np.array_equal(lse, ls)
+
+
+@pytest.mark.parametrize("B,S,Hq,Hkv,nsparse,causal", [
+    (1, 96, 4, 1, 40, True), (2, 64, 4, 2, 24, True), (1, 70, 2, 2, 33, False)])
+def test_sparse_oracle_vs_numpy_f64(B, S, Hq, Hkv, nsparse, causal):
+    from tests._helpers import build_sparse_indices
+    q, k, v = _prefill_inputs(93 + S, B, S, S, Hq, Hkv, D=64)
+    idx = build_sparse_indices(95 + S, B, Hkv, S, S, nsparse, recent=8)
+    # edge entries the kernels must skip or keep: out of range, a future key,
+    # a key listed twice
+    rng = np.random.default_rng(S)
+    idx[..., -1] = rng.integers(S, 2 * S, size=idx.shape[:3])
+    idx[..., -2] = np.minimum(np.arange(S)[None, None, :] + 3, S - 1)
+    idx[..., -3] = idx[..., 0]
+    o, lse = oracle.sparse_prefill(q, k, v, idx, 0.15, causal=causal)
+    of, lf = _sparse_numpy_f64(q, k, v, idx, 0.15, causal)
+    assert_close(oracle.bf16_to_f32(o), of, "sparse vs f64")
+    fin = np.isfinite(lf)
+    assert np.array_equal(np.isfinite(lse), fin)
+    assert np.max(np.abs(lse[fin] - lf[fin])) < 1e-4
+    # planted mistakes: causal off by one (future key 3 ahead allowed through a
+    # shifted row position); empty (-1) slots gathered as key 0 without being
+    # masked; the index list of the query head instead of its kv head;
+    # out-of-range entries wrapped into range
+    if causal:
+        bad, _ = oracle.sparse_prefill(q, k, v, idx, 0.15, causal=True, q_offset=3)
+        assert not within_tol(oracle.bf16_to_f32(bad), of)
+    wrapped = np.where(idx < 0, 0, idx).astype(np.int32)
+    bad, _ = oracle.sparse_prefill(q, k, v, wrapped, 0.15, causal=causal)
+    assert not within_tol(oracle.bf16_to_f32(bad), of)
+    if Hkv > 1:
+        bad, _ = oracle.sparse_prefill(q, k, v, idx[:, ::-1], 0.15, causal=causal)
+        assert not within_tol(oracle.bf16_to_f32(bad), of)
+    wrapped = np.where(idx >= S, idx - S, idx).astype(np.int32)
+    bad, _ = oracle.sparse_prefill(q, k, v, wrapped, 0.15, causal=causal)
+    assert not within_tol(oracle.bf16_to_f32(bad), of)
+
+
+def test_sparse_oracle_closed_forms():
+    """One valid entry: O = V[j] exactly, lse = score; no valid entry: O = 0,
+    lse = -inf; a key listed twice weighs as its score + ln 2."""
+    B, S, Hq, Hkv, n = 1, 40, 2, 1, 8
+    q, k, v = _prefill_inputs(97, B, S, S, Hq, Hkv)
+    idx = np.full((B, Hkv, S, n), -1, dtype=np.int32)
+    idx[0, 0, :, 3] = np.arange(S) // 2          # one causal key per row
+    idx[0, 0, 5, :] = -1                          # row 5: nothing valid
+    idx[0, 0, 6, 0] = 7                           # row 6: only a future key
+    idx[0, 0, 6, 3] = -1
+    o, lse = oracle.sparse_prefill(q, k, v, idx, SCALE, causal=True)
+    for i in range(S):
+        if i in (5, 6):
+            assert np.all(o[0, i] == 0) and np.all(np.isneginf(lse[0, :, i]))
+        else:
+            assert np.array_equal(o[0, i, 0], v[0, i // 2, 0]) and np.array_equal(o[0, i, 1], v[0, i // 2, 0])
+    # duplicates: listing key a twice next to key b equals softmax over {a: s_a + ln 2, b: s_b}
+    idx2 = np.full((B, Hkv, S, 3), -1, dtype=np.int32)
+    idx2[0, 0, :, 0] = 0
+    idx2[0, 0, :, 1] = 0
+    idx2[0, 0, :, 2] = np.arange(S)
+    o2, lse2 = oracle.sparse_prefill(q, k, v, idx2, SCALE, causal=True)
+    qf, kf, vf = (oracle.bf16_to_f32(x).astype(np.float64) for x in (q, k, v))
+    for i in range(1, S):
+        for h in range(Hq):
+            sa = qf[0, i, h] @ kf[0, 0, 0] * SCALE + math.log(2.0)
+            sb = qf[0, i, h] @ kf[0, i, 0] * SCALE
+            m = max(sa, sb)
+            wa, wb = math.exp(sa - m), math.exp(sb - m)
+            ref = (wa * vf[0, 0, 0] + wb * vf[0, i, 0]) / (wa + wb)
+            assert np.max(np.abs(oracle.bf16_to_f32(o2[0, i, h]) - ref)) < 1e-2
+            assert abs(lse2[0, h, i] - (m + math.log(wa + wb))) < 1e-4
