@@ -12,12 +12,11 @@
 // One wave owns one work item: a query position, a KV head and up to 16 of
 // its query heads, which share the position's index list.  The heads are the
 // N dimension of v_mfma_f32_16x16x32_bf16; per 32-entry step:
-//   S^T (32 keys x 16 heads) = K_gathered . Q^T     8 MFMAs; K rows are gathered
-//                                                    straight into A operands
-//   O^T (128 x 16)          += V^T . P^T            8 MFMAs; V rows are gathered
-//                                                    into registers, written to
-//                                                    the wave's LDS tile and read
-//                                                    transposed (ds_read_b64_tr_b16)
+//   S^T (32 keys x 16 heads) = K_gathered . Q^T     8 MFMAs, K from the wave's
+//                                                    LDS tile (b128 reads)
+//   O^T (128 x 16)          += V^T . P^T            8 MFMAs, V read transposed
+//                                                    from its LDS tile
+//                                                    (ds_read_b64_tr_b16)
 // The next step's K and V rows are in flight while a step is computed.  Each
 // step reads 16 KB of K/V rows; the MFMA work per step is small, so the kernel
 // is bound by how fast the gathers are served (mostly from L2 and the MALL:
@@ -52,31 +51,46 @@ struct SparseParams {
 
 constexpr int kSpWaves = 4;                  // waves (= work items) per workgroup
 constexpr int kSpStep = 32;                  // index entries per step
-constexpr int kSpTileBytes = kSpStep * 256;  // one step's V rows in LDS (8 KB per wave)
+constexpr int kSpKRow = 288;                 // K row stride in LDS (256 + 32 bytes)
+constexpr int kSpVRow = 288;                 // V row stride in LDS
+constexpr int kSpKBytes = kSpStep * kSpKRow;
+constexpr int kSpVBytes = kSpStep * kSpVRow;
+constexpr int kSpIdxBytes = kSpStep * 4;
+constexpr int kSpWaveBytes = kSpKBytes + kSpVBytes + kSpIdxBytes;   // 17.9 KB of LDS per wave
 constexpr float kSpRescaleSlack = 8.f;       // log2 units: P <= 2^8 between rescales
 
-// V tile layout in LDS: 16-byte chunk c (dims 8c .. 8c+7) of row r sits at
-// c * 512 + (r ^ 8*(c % 2)) * 16.  A row's chunks are 512 bytes apart; the
-// XOR keeps the transposed reads (4 rows x 2 chunks x 2 halves per 16 lanes,
-// 8 rows per 32 lanes) and the b128 writes free of bank conflicts.
+// Gathers are row-contiguous: load instruction i of a step fetches entries
+// 4i .. 4i+3, 16 lanes per 256-byte row, so every 16 lanes read two whole
+// 128-byte lines (a lane-per-row gather makes the L1 handle one access per
+// lane and is several times slower).  The rows then go through the wave's LDS
+// tiles to reach the MFMA operand layouts.  A 288-byte row stride (256 + 32)
+// keeps every LDS pattern here free of bank conflicts (SQ_LDS_BANK_CONFLICT
+// reads 0 for the b128 writes of one row's 16 chunks, the b128 A-operand reads
+// of 16 rows at one chunk, and the transposed reads of rows 0..7 x chunks
+// {2dt, 2dt + 1} per 32 lanes; a 272-byte stride costs the b128 reads 4
+// conflict cycles each).
 
-// Block -> first work item.  Blocks go round-robin over the 8 XCDs; this map
-// hands each XCD one contiguous range of items (positions), so the rows its
-// L2 holds are the causal prefix of nearby positions.
+// Block -> first work item: the last positions first.  Blocks go round-robin
+// over the 8 XCDs, so every XCD works through the same positions at the same
+// time: each L2 holds rows of the same causal prefix and the XCDs finish
+// together.  (Handing each XCD one contiguous range of positions gives the
+// XCDs with early positions a prefix that fits their L2 and the others one that
+// does not; at S = 32768 the late XCDs then ran 30 % longer per item and the
+// launch took 16 % longer.)  Early positions have the fewest usable entries, so
+// running them last shortens the tail.
 __device__ __forceinline__ int64_t sp_block_first_item(int64_t nblocks) {
-    const int64_t bid = blockIdx.x;
-    const int64_t q = nblocks / 8, r = nblocks % 8;
-    const int64_t x = bid % 8, j = bid / 8;
-    return (x * q + (x < r ? x : r) + j) * kSpWaves;
+    return (nblocks - 1 - (int64_t)blockIdx.x) * kSpWaves;
 }
 
 __global__ __launch_bounds__(kSpWaves * kWave, 2) void sparse_prefill_kernel(SparseParams p) {
-    __shared__ __attribute__((aligned(16))) unsigned char smem[kSpWaves * kSpTileBytes];
+    __shared__ __attribute__((aligned(16))) unsigned char smem[kSpWaves * kSpWaveBytes];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int64_t item = sp_block_first_item(gridDim.x) + wave;
     if (item >= p.n_items) return;   // the kernel has no barrier: a finished wave may leave
-    unsigned char* vl = smem + wave * kSpTileBytes;
+    unsigned char* kl = smem + wave * kSpWaveBytes;
+    unsigned char* vl = kl + kSpKBytes;
+    int* il = reinterpret_cast<int*>(vl + kSpVBytes);
 
     // (the divisions run on the VALU: readfirstlane tells the compiler the
     // results are wave-uniform, so buffer descriptors stay in SGPRs)
@@ -113,60 +127,63 @@ __global__ __launch_bounds__(kSpWaves * kWave, 2) void sparse_prefill_kernel(Spa
     const __amdgpu_buffer_rsrc_t irs =
         make_rsrc(p.idx + b * p.i_sb + kvh * p.i_sh + (int64_t)pos * p.i_ss, (uint32_t)p.nsparse * 4);
     // K/V rows of this (batch, kv head); rows are addressed by 32-bit offsets.
-    const uint32_t kss = (uint32_t)(p.k_ss * 2);
-    const uint32_t vss = (uint32_t)(p.v_ss * 2);
     // (Skv = 0: empty ranges, every load returns 0 and every entry is masked.
     // The select would otherwise put the descriptors in VGPRs.)
+    const uint32_t kss = (uint32_t)(p.k_ss * 2);
+    const uint32_t vss = (uint32_t)(p.v_ss * 2);
     const uint32_t kv_rows = (uint32_t)p.skv;
     const uint32_t k_bytes = __builtin_amdgcn_readfirstlane(kv_rows ? (kv_rows - 1) * kss + 256 : 0u);
     const uint32_t v_bytes = __builtin_amdgcn_readfirstlane(kv_rows ? (kv_rows - 1) * vss + 256 : 0u);
     const __amdgpu_buffer_rsrc_t krs = make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, k_bytes);
     const __amdgpu_buffer_rsrc_t vrs = make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, v_bytes);
 
-    // Entry e of step t: lane l loads entry 32t + l % 32 (lanes 32..63 repeat
-    // 0..31).  usable -> its key row, else row 0 (read, then masked).
-    auto load_idx = [&](int t) -> int { return (int)__builtin_amdgcn_raw_buffer_load_b32(irs, (uint32_t)(t * kSpStep + l32) * 4, 0, 0); };
-    struct StepIdx {
-        uint32_t row;    // this lane's entry's key row (0 when unusable)
-        uint32_t mask;   // bit e: entry 32t + e is usable
+    // Index lists of steps t and t + 1 (t even): lane l loads entry 32t + l.
+    auto load_pair = [&](int t) -> int {
+        return (int)__builtin_amdgcn_raw_buffer_load_b32(irs, (uint32_t)(t * kSpStep + lane) * 4, 0, 0);
     };
-    auto decode_idx = [&](int t, int j) -> StepIdx {
-        const bool ok = (t * kSpStep + l32 < p.nsparse) && j >= 0 && j < p.skv && (!p.causal || j <= pos);
-        const uint64_t bal = __builtin_amdgcn_ballot_w64(ok);
-        return StepIdx{ok ? (uint32_t)j : 0u, (uint32_t)bal};
+    // Usable-entry masks of the pair: bit e of the low (high) word = entry
+    // 32t + e (32t + 32 + e).  Usable -> its key row, else row 0 (read, then masked).
+    auto pair_mask = [&](int t, int j) -> uint64_t {
+        const bool ok = (t * kSpStep + lane < p.nsparse) && j >= 0 && j < p.skv && (!p.causal || j <= pos);
+        return __builtin_amdgcn_ballot_w64(ok);
+    };
+    // Leaves the key rows of step t (half = 0) or t + 1 (half = 1) in the index
+    // area, stored so that lane l finds the rows of entries 4i + l/16 (i = 0..7)
+    // in 8 consecutive words.
+    auto post_rows = [&](int j, uint64_t mask, int half) {
+        if ((lane >> 5) == half) il[(l32 & 3) * 8 + (l32 >> 2)] = ((mask >> lane) & 1u) ? j : 0;
     };
 
-    // K A operands of one step: tile t (entries 16t .. 16t+15), lane (key l16,
-    // group g) holds dims 32*ks + 8g .. +7 of entry 16t + l16's row.
-    // V: lane l gathers chunks 2i + l/32 (i = 0..7) of entry l % 32's row.
-    bf16x8_t ka[2][4], kb[2][4];
-    u32x4_t vreg[8];
-    auto issue = [&](const StepIdx& si, bf16x8_t (&kd)[2][4]) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const uint32_t row = (uint32_t)__shfl((int)si.row, 16 * t + l16, kWave);
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) kd[t][ks] = as_bf16x8(buf_load16(krs, row * kss + ks * 64 + g * 16));
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) vreg[i] = buf_load16(vrs, si.row * vss + (2 * i + (lane >> 5)) * 16);
+    // Row gathers of one step: instruction i, lane l -> entry 4i + l/16,
+    // 16-byte chunk l % 16, into one of two register sets (two steps in flight).
+    struct Rows {
+        u32x4_t k[8], v[8];
     };
-    auto write_v = [&] {
+    Rows ra, rb;
+    auto issue = [&](Rows& r) {
+        const u32x4_t r0 = *reinterpret_cast<const u32x4_t*>(il + (lane >> 4) * 8);
+        const u32x4_t r1 = *reinterpret_cast<const u32x4_t*>(il + (lane >> 4) * 8 + 4);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int c = 2 * i + (lane >> 5);
-            *reinterpret_cast<u32x4_t*>(vl + c * 512 + ((l32 ^ (8 * (lane >> 5))) << 4)) = vreg[i];
+            const uint32_t row = i < 4 ? r0[i] : r1[i - 4];
+            r.k[i] = buf_load16(krs, row * kss + l16 * 16);
+            r.v[i] = buf_load16(vrs, row * vss + l16 * 16);
         }
     };
-    // Transposed V reads: lane (l16, g) of half kh supplies row 16*kh + 4g + l16/4,
-    // dims 16*dt + 4*(l16 % 4) .. +3, i.e. chunk 2dt + (l16/2) % 2, half l16 % 2.
-    uint32_t vrd[2];
+    const int wrow = lane >> 4;   // row within each group of 4 entries
+    auto stage = [&](const Rows& r) {
 #pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-        const int c1 = (l16 >> 1) & 1;
-        const int r = 16 * kh + 4 * g + (l16 >> 2);
-        vrd[kh] = c1 * 512 + ((r ^ (8 * c1)) << 4) + 8 * (l16 & 1);
-    }
+        for (int i = 0; i < 8; ++i) {
+            *reinterpret_cast<u32x4_t*>(kl + (4 * i + wrow) * kSpKRow + l16 * 16) = r.k[i];
+            *reinterpret_cast<u32x4_t*>(vl + (4 * i + wrow) * kSpVRow + l16 * 16) = r.v[i];
+        }
+    };
+    // A operand (K) of tile tt, k-step ks: lane (key l16, group g) reads dims
+    // 32*ks + 8g .. +7 of entry 16tt + l16.
+    const unsigned char* krd = kl + l16 * kSpKRow + g * 16;
+    // Transposed V reads: lane (l16, g) of half kh supplies entry 16kh + 4g + l16/4,
+    // dims 16dt + 4*(l16 % 4) .. +3, i.e. chunk 2dt + (l16/2) % 2, half l16 % 2.
+    const unsigned char* vrd = vl + (4 * g + (l16 >> 2)) * kSpVRow + ((l16 >> 1) & 1) * 16 + (l16 & 1) * 8;
 
     const float c = p.scale_log2;
     float m_run = -INFINITY;   // running max (log2 units) of head l16
@@ -176,15 +193,18 @@ __global__ __launch_bounds__(kSpWaves * kWave, 2) void sparse_prefill_kernel(Spa
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) oacc[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    // One step on entries 32t .. 32t+31, K operands in kc.  S^T C layout: lane
-    // (head l16, group g) register r of tile tt = entry 16tt + 4g + r.
-    auto compute = [&](const bf16x8_t (&kc)[2][4], uint32_t mask) {
+    // One step on the staged entries.  S^T C layout: lane (head l16, group g)
+    // register r of tile tt = entry 16tt + 4g + r.
+    auto compute = [&](uint32_t mask) {
         f32x4_t s[2];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             s[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) s[tt] = mfma16(kc[tt][ks], qop[ks], s[tt]);
+            for (int ks = 0; ks < 4; ++ks) {
+                const bf16x8_t ka = *reinterpret_cast<const bf16x8_t*>(krd + tt * 16 * kSpKRow + ks * 64);
+                s[tt] = mfma16(ka, qop[ks], s[tt]);
+            }
         }
         float tmax = -INFINITY;
 #pragma unroll
@@ -219,33 +239,41 @@ __global__ __launch_bounds__(kSpWaves * kWave, 2) void sparse_prefill_kernel(Spa
         l_run += psum;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
-            const bf16x4_t lo = lds_read_tr16(reinterpret_cast<const __bf16*>(vl + dt * 1024 + vrd[0]));
-            const bf16x4_t hi = lds_read_tr16(reinterpret_cast<const __bf16*>(vl + dt * 1024 + vrd[1]));
+            const bf16x4_t lo = lds_read_tr16(reinterpret_cast<const __bf16*>(vrd + dt * 32));
+            const bf16x4_t hi = lds_read_tr16(reinterpret_cast<const __bf16*>(vrd + 16 * kSpVRow + dt * 32));
             oacc[dt] = mfma16(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), pop, oacc[dt]);
         }
     };
 
-    // Step t's rows are issued during step t - 1; index lists run two steps
-    // ahead.  n_steps is even, so the loop alternates the two K register sets
-    // without copies; steps past nsparse are fully masked.
-    // Each index list is loaded before the rows of the step in front of it, so
-    // that waiting for it never waits for those rows.
-    StepIdx sc = decode_idx(0, load_idx(0));
-    int jn = load_idx(1);
-    issue(sc, ka);
+    // Step t: its rows (gathered two steps earlier) are staged into LDS, then
+    // step t + 2's rows are gathered into the freed register set while step t
+    // is computed.  Index lists are loaded a step before their rows are
+    // gathered and before the rows in front of them, so waiting for a list never
+    // waits for rows.  Steps past nsparse are fully masked (their gathers read
+    // row 0 and are never used); n_steps is even, so the two register sets
+    // alternate without copies.
+    // One index load per loop trip, issued before the rows behind it.
+    int j = load_pair(0);
+    uint64_t mcur = pair_mask(0, j);
+    post_rows(j, mcur, 0);
+    issue(ra);
+    int jn = load_pair(2);
+    post_rows(j, mcur, 1);
+    issue(rb);
     for (int t = 0; t < p.n_steps; t += 2) {
-        write_v();
-        const StepIdx s1 = decode_idx(t + 1, jn);
-        jn = load_idx(t + 2);
-        issue(s1, kb);
-        compute(ka, sc.mask);
+        stage(ra);
+        const uint64_t mnext = pair_mask(t + 2, jn);
+        post_rows(jn, mnext, 0);
+        issue(ra);
+        compute((uint32_t)mcur);
 
-        write_v();
-        const StepIdx s2 = decode_idx(t + 2, jn);
-        jn = load_idx(t + 3);
-        issue(s2, ka);   // past the end on the last trip: masked rows 0, never used
-        compute(kb, s1.mask);
-        sc = s2;
+        stage(rb);
+        j = jn;
+        jn = load_pair(t + 4);
+        post_rows(j, mnext, 1);
+        issue(rb);
+        compute((uint32_t)(mcur >> 32));
+        mcur = mnext;
     }
 
     // Row sums over the four lane groups; then O and the LSE of head l16.
