@@ -39,6 +39,8 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "fgqa_device.h"
 #include "fgqa_internal.h"
 
@@ -64,6 +66,16 @@ struct PrefillParams {
     int window;         // > 0: sliding window, row i sees keys [i - window + 1, i] (causal)
     const float* sink;  // nullable [Hq]: added to the softmax denominator as sink * exp(-max)
 };
+
+// f(integral_constant<int, 0>), ..., f(integral_constant<int, N-1>): an
+// unrolled loop whose index is a constant expression in the body.
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, I + 1>(f);
+    }
+}
 
 constexpr int kPfWaves = 4;                            // waves per group (one unit's rows)
 constexpr int kPfThreads = kPfWaves * kWave;
@@ -163,9 +175,14 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     // before reading the other buffer); their completion is awaited
     // explicitly (wait_vmem) before the barrier that publishes the tile.
     const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)smem;
-    auto dma16 = [](uint32_t lds_addr, uint32_t voffset, uint32_t soffset, __amdgpu_buffer_rsrc_t rsrc) {
-        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                     :: "s"(lds_addr), "v"(voffset), "s"(rsrc), "s"(soffset) : "memory");
+    // Instruction i writes 4096*i bytes past the wave's first KB of the tile.
+    // The destination goes to M0 as base + literal inside the asm, so only
+    // one SGPR per tile buffer stays live (one SGPR per instruction made the
+    // compiler spill them and reload each with v_readlane in the loop).
+    auto dma16 = [](auto ic, uint32_t base, uint32_t voffset, uint32_t soffset, __amdgpu_buffer_rsrc_t rsrc) {
+        constexpr int kOff = decltype(ic)::value * 4096;
+        asm volatile("s_add_u32 m0, %0, %4\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                     :: "s"(base), "v"(voffset), "s"(rsrc), "s"(soffset), "i"(kOff) : "memory", "scc");
     };
     // Instruction i of this wave fills the 1 KB at slot 64*(wave + 4*i) of a
     // tile; lane l writes slot 64*(wave + 4*i) + l, i.e. row r = slot / chunks,
@@ -189,28 +206,28 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     }
     auto issue_tile = [&](int j, int kb, int vb) {
         const int t0 = (t_first + j) * kPfTile;
-        const uint32_t kdst = lds_base + kb * D::kKTileBytes;
-        const uint32_t vdst = lds_base + 2 * D::kKTileBytes + vb * kPfVTileBytes;
+        const uint32_t kdst = lds_base + kb * D::kKTileBytes + 1024 * wave;
+        const uint32_t vdst = lds_base + 2 * D::kKTileBytes + vb * kPfVTileBytes + 1024 * wave;
         // K and V instructions interleaved, K first
         if (t0 + kPfTile - 1 <= kv_last) {   // whole tile in range
-#pragma unroll
-            for (int i = 0; i < D::kDmaK; ++i) {
-                if (kb >= 0) dma16(kdst + 1024 * (wave + 4 * i), koff_dma[i], (uint32_t)t0 * kss, krs);
-                if (i < 4 && vb >= 0) dma16(vdst + 1024 * (wave + 4 * i), voff_dma[i], (uint32_t)t0 * vss, vrs);
-            }
+            static_for<D::kDmaK>([&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                if (kb >= 0) dma16(ic, kdst, koff_dma[i], (uint32_t)t0 * kss, krs);
+                if (i < 4 && vb >= 0) dma16(ic, vdst, voff_dma[i], (uint32_t)t0 * vss, vrs);
+            });
         } else {   // last tile: rows past the last key are clamped to it
-#pragma unroll
-            for (int i = 0; i < D::kDmaK; ++i) {
+            static_for<D::kDmaK>([&](auto ic) {
+                constexpr int i = decltype(ic)::value;
                 if (kb >= 0) {
                     const uint32_t tok = (uint32_t)min(t0 + krow_dma[i], kv_last);
-                    dma16(kdst + 1024 * (wave + 4 * i), tok * kss + kcol_dma[i], 0u, krs);
+                    dma16(ic, kdst, tok * kss + kcol_dma[i], 0u, krs);
                 }
                 if (i < 4 && vb >= 0) {
                     const int r = 4 * (wave + 4 * i) + (lane >> 4);
                     const uint32_t tok = (uint32_t)min(t0 + r, kv_last);
-                    dma16(vdst + 1024 * (wave + 4 * i), tok * vss + ((l16 ^ (4 * (r & 3))) << 4), 0u, vrs);
+                    dma16(ic, vdst, tok * vss + ((l16 ^ (4 * (r & 3))) << 4), 0u, vrs);
                 }
-            }
+            });
         }
     };
 
