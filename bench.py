@@ -380,6 +380,39 @@ def bench_backward(cfg_id, steps, warmup, dev):
                           "algorithmic_flops": flops, "executed_mfma_flops": flops * 7 // 5})
 
 
+def bench_swa_backward(steps, warmup, dev, window=512):
+    """Sliding-window (+ sink) prefill backward at the reference's SWA benchmark
+    shape (README: B=1, S=4096, Hq=16, Hkv=1, D=128, window 512), fed the GPU
+    forward's O and sink-adjusted LSE; one step = every launch of
+    fgqa_prefill_backward_bf16."""
+    import torch
+
+    import cuda_llm_ops_amd as fg
+    B, S, Hq, Hkv = 1, 4096, 16, 1
+    q = _normal((B, S, Hq, 128), 15, 1.0, dev)
+    k = _normal((B, S, Hkv, 128), 16, 1.0, dev)
+    v = _normal((B, S, Hkv, 128), 17, 1.0, dev)
+    do = _normal((B, S, Hq, 128), 18, 1.0, dev)
+    sink = torch.rand(Hq, generator=torch.Generator().manual_seed(19)).to(dev) + 1e-6
+    out, lse = fg.flash_gqa_forward_bshd(q, k, v, SCALE, causal=True, window_size=window, sink=sink)
+    n_ws = fg.backward_workspace_bytes(B, S, S, Hq, Hkv)
+    ws = torch.empty(max(n_ws, 256), dtype=torch.uint8, device=dev)
+    step = fg.prepare_backward(q, k, v, out, lse, do, SCALE, causal=True, workspace=ws, window_size=window)
+    total_ms, per = _time_calls(step, steps, warmup)
+    # the reference's count, QK + dP + dQ + dK + dV over the window
+    # (test_flash_swa_kernel.py:400-420); the kernels execute 7 such GEMMs
+    flops = B * Hq * 2 * S * window * (3 * 128 + 2 * 128)
+    avg = sum(per) / len(per)
+    tflops = flops / (avg * 1e-3) / 1e12
+    return dict(config=f"sliding-window prefill backward, B={B} S={S} Hq={Hq} Hkv={Hkv} D=128 window={window}",
+                us_avg=round(avg * 1e3, 2), us_median=round(per[len(per) // 2] * 1e3, 2),
+                us_min=round(per[0] * 1e3, 2),
+                roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
+                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                          "kernel": "bwd_prep + bwd_dkdv + bwd_dq(_split) + bwd_dkdv_reduce (whole step)",
+                          "algorithmic_flops": flops, "executed_mfma_flops": flops * 7 // 5})
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -391,12 +424,14 @@ def main():
     ap.add_argument("--no-backward", action="store_true")
     ap.add_argument("--no-paged", action="store_true")
     ap.add_argument("--no-swa", action="store_true")
+    ap.add_argument("--no-swa-backward", action="store_true")
     ap.add_argument("--no-mla", action="store_true")
     ap.add_argument("--no-sparse", action="store_true")
     ap.add_argument("--page-size", type=int, default=16, help="with --mode paged")
     ap.add_argument("--kv", choices=["bf16", "fp8"], default="bf16", help="with --mode paged")
     ap.add_argument("--all", action="store_true", help="also report configs 1, 3 and 5 (to stderr)")
-    ap.add_argument("--mode", choices=["bench", "decode", "paged", "prefill", "swa", "mla", "sparse", "backward", "copy"],
+    ap.add_argument("--mode", choices=["bench", "decode", "paged", "prefill", "swa", "mla", "sparse", "backward",
+                                       "swa_backward", "copy"],
                     default="bench",
                     help="decode/prefill/copy: run only that workload (for profiling) and print its timing")
     ap.add_argument("--config", type=int, default=0,
@@ -440,6 +475,9 @@ def main():
         print(json.dumps({"mode": "backward", **bench_backward(args.config or 4, args.steps, args.warmup, dev)}),
               flush=True)
         return
+    if args.mode == "swa_backward":
+        print(json.dumps({"mode": "swa_backward", **bench_swa_backward(args.steps, args.warmup, dev)}), flush=True)
+        return
 
     res = bench_decode(2, args.steps, args.warmup, args.split_tokens, dev)
     gbs = res["kv_bytes"] / (res["ms_step"] * 1e-3) / 1e9
@@ -481,6 +519,8 @@ def main():
         line["sparse"] = bench_sparse(max(5, args.steps // 5), 2, dev)
     if not args.no_backward:
         line["backward"] = bench_backward(4, max(5, args.steps // 2), max(2, args.warmup // 2), dev)
+    if not args.no_swa_backward:
+        line["swa_backward"] = bench_swa_backward(max(5, args.steps // 2), max(2, args.warmup // 2), dev)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_decode(res)
     if args.all:

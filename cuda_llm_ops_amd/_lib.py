@@ -139,6 +139,7 @@ class BackwardArgs(ctypes.Structure):
         ("grad_v_stride", _I64x3),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
+        ("window_size", ctypes.c_int32),
     ]
 
 

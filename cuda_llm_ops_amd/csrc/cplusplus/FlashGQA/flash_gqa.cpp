@@ -140,10 +140,10 @@ void LaunchFlashGqaForwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf1
                                            numQueryHeads, numKvHeads, headDim, causal, qs, ks, ks, qs);
 }
 
-void LaunchFlashGqaBackwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* o,
-                                      const float* lse, const bf16_t* gradO, float scale, bf16_t* gradQ,
-                                      bf16_t* gradK, bf16_t* gradV, int batchSize, int seqLengthQ, int seqLengthKv,
-                                      int numQueryHeads, int numKvHeads, int headDim, bool causal) {
+static void backward_bshd(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* o, const float* lse,
+                          const bf16_t* gradO, float scale, bf16_t* gradQ, bf16_t* gradK, bf16_t* gradV,
+                          int batchSize, int seqLengthQ, int seqLengthKv, int numQueryHeads, int numKvHeads,
+                          int headDim, bool causal, int windowSize) {
     fgqa_prefill_backward_args a;
     std::memset(&a, 0, sizeof(a));
     a.q = q;
@@ -163,6 +163,7 @@ void LaunchFlashGqaBackwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf
     a.head_dim = headDim;
     a.causal = causal ? 1 : 0;
     a.scale = scale;
+    a.window_size = windowSize;
     // BSHD: q, o, gradO, gradQ [B, Sq, Hq, D]; k, v, gradK, gradV [B, Skv, Hkv, D]
     const int64_t qs[3] = {(int64_t)seqLengthQ * numQueryHeads * headDim, (int64_t)numQueryHeads * headDim, headDim};
     const int64_t ks[3] = {(int64_t)seqLengthKv * numKvHeads * headDim, (int64_t)numKvHeads * headDim, headDim};
@@ -171,6 +172,22 @@ void LaunchFlashGqaBackwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf
         a.k_stride[i] = a.v_stride[i] = a.grad_k_stride[i] = a.grad_v_stride[i] = ks[i];
     }
     g_last_status = fgqa_prefill_backward_bf16(&a, nullptr);
+}
+
+void LaunchFlashGqaBackwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* o,
+                                      const float* lse, const bf16_t* gradO, float scale, bf16_t* gradQ,
+                                      bf16_t* gradK, bf16_t* gradV, int batchSize, int seqLengthQ, int seqLengthKv,
+                                      int numQueryHeads, int numKvHeads, int headDim, bool causal) {
+    backward_bshd(q, k, v, o, lse, gradO, scale, gradQ, gradK, gradV, batchSize, seqLengthQ, seqLengthKv,
+                  numQueryHeads, numKvHeads, headDim, causal, 0);
+}
+
+void LaunchFlashSwaBackwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* o,
+                                      const float* lse, const bf16_t* gradO, float scale, bf16_t* gradQ,
+                                      bf16_t* gradK, bf16_t* gradV, int batchSize, int seqLengthQ, int seqLengthKv,
+                                      int numQueryHeads, int numKvHeads, int headDim, int windowSize) {
+    backward_bshd(q, k, v, o, lse, gradO, scale, gradQ, gradK, gradV, batchSize, seqLengthQ, seqLengthKv,
+                  numQueryHeads, numKvHeads, headDim, true, windowSize);
 }
 
 void LaunchFlashSwaForwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf16_t* v, float scale, bf16_t* o,

@@ -71,4 +71,4 @@ extern "C" const char* fgqa_status_string(int status) {
     }
 }
 
-extern "C" int fgqa_version(void) { return 103; }
+extern "C" int fgqa_version(void) { return 104; }

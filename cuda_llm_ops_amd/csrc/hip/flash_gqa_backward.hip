@@ -68,6 +68,7 @@ struct BwdParams {
     float* dk_part;   // [n_hsplit][B, Hkv, Skv, D] fp32 partial sums (heads split), else null
     float* dv_part;
     int batch, sq, skv, hq, hkv, group, causal;
+    int window;       // > 0: sliding window (causal), row i uses keys (i - window, i]
     // key-major (dK/dV) grid
     int hs;           // query heads per workgroup
     int n_hsplit;     // group / hs
@@ -174,6 +175,9 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(BwdParams p) {
 //   phase A: S(t+1), dP(t+1) on the MFMA pipe  ||  P(t), dS(t) on the VALU
 //   phase B: dV += P(t)^T dO(t), dK += dS(t)^T Q(t) on the MFMA pipe
 // with Q/dO(t+2) streaming into the third LDS buffer meanwhile.
+// kSwa: sliding window (a separate instantiation, so the causal kernels carry
+// none of its work).
+template <bool kSwa>
 __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int tid = threadIdx.x;
@@ -214,7 +218,9 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
 
     // step t: head h0 + t / per_head, query block qb0 + t % per_head
     const int qb0 = p.causal ? min(kv0 / kKvRows, p.n_qblocks32) : 0;
-    const int per_head = p.n_qblocks32 - qb0;
+    // a window ends the key block's rows at its last key + window - 1
+    const int qb_end = kSwa ? min(p.n_qblocks32, (kv0 + kKvKeys + p.window - 2) / kKvRows + 1) : p.n_qblocks32;
+    const int per_head = max(0, qb_end - qb0);
     const int n_iter = p.hs * per_head;
 
     const uint32_t qss = (uint32_t)(p.q_ss * 2);
@@ -283,11 +289,12 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
     // P = exp2(S*scale*log2e - lse*log2e), dS = P (dP - delta) scale, both as
     // bf16 A operands (k-step ks = registers 8ks .. 8ks+7).  Element (i, r) is
     // query row q0 + 8i + 4g2 + r; it is masked (P = 0) when 8i + r < m, with
-    // m = key - q0 - 4g2 under the causal mask.  Rows >= sq need no mask: their
+    // m = key - q0 - 4g2 under the causal mask, and (window) when 8i + r > mx,
+    // mx = key + window - 1 - q0 - 4g2.  Rows >= sq need no mask: their
     // dO rows and -delta*scale read as zero, so P.dO and dS vanish; keys >= skv
     // only reach their own dK/dV rows, which are never stored.
     bf16x8_t pop[2], dsop[2];
-    auto softmax = [&](const f32x16_t& s, const f32x16_t& dp, auto bi_c, int m) {
+    auto softmax = [&](const f32x16_t& s, const f32x16_t& dp, auto bi_c, int m, int mx) {
         constexpr int bi = decltype(bi_c)::value;
         const float* st = reinterpret_cast<const float*>(smem + kKvStatOff + bi * kKvStatBytes);
 #pragma unroll
@@ -297,7 +304,10 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 float pv = fast_exp2(__builtin_fmaf(s[4 * i + r], c2, nl[r]));
-                pv = (8 * i + r >= m) ? pv : 0.f;
+                if constexpr (kSwa)
+                    pv = (8 * i + r >= m && 8 * i + r <= mx) ? pv : 0.f;
+                else
+                    pv = (8 * i + r >= m) ? pv : 0.f;
                 const float ds = pv * __builtin_fmaf(dp[4 * i + r], scale, nd[r]);
                 pop[i >> 1][(i & 1) * 4 + r] = (__bf16)pv;
                 dsop[i >> 1][(i & 1) * 4 + r] = (__bf16)ds;
@@ -349,9 +359,10 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
         if (t + 2 < n_iter) issue(t + 2, decltype(bf)::value);
         const int q0 = (qb0 + t % per_head) * kKvRows;
         const int m = (t < n_iter) ? (p.causal ? key - q0 - 4 * g2 : -64) : 64;
+        const int mx = key + p.window - 1 - q0 - 4 * g2;
         // phase A: S/dP(t+1) on the MFMA pipe while P/dS(t) run on the VALU
         sdp(sn, dpn, bn);
-        softmax(sc, dpc, bc, m);
+        softmax(sc, dpc, bc, m, mx);
         // phase B: dV/dK(t)
         dkdv(bc);
         bw_wait_vmem();
@@ -433,7 +444,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_reduce_kernel(BwdParams p) {
 // forward kernel.  With kGroups == 2 two groups of 4 waves take the two halves
 // of the unit's key range and add their dQ through LDS at the end (dQ is a
 // plain sum over keys: P comes from the final LSE).
-template <int kGroups>
+template <int kGroups, bool kSwa>
 __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem_all, int qb, int hg, int kvh,
                                         int b) {
     const int tid = threadIdx.x;
@@ -474,9 +485,11 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem_
 
     int kv_end = p.skv;
     if (p.causal) kv_end = min(kv_end, min(q_wg0 + qrows, p.sq));
-    const int unit_tiles = (kv_end + kDqTile - 1) / kDqTile;
+    // a window starts the unit at the tile holding its first row's first key
+    const int t_lo = kSwa ? max(0, q_wg0 - p.window + 1) / kDqTile : 0;
+    const int unit_tiles = max(0, (kv_end + kDqTile - 1) / kDqTile - t_lo);
     const int n_tiles = kGroups == 1 ? unit_tiles : (unit_tiles + 1) / 2;   // same for both groups
-    const int t_first = grp * n_tiles;
+    const int t_first = t_lo + grp * n_tiles;
     // keys this lane's row may use: below kv_hi (end of the group's range) and,
     // under the causal mask, at most qrow
     const int kv_hi = min(kv_end, (t_first + n_tiles) * kDqTile);
@@ -522,8 +535,9 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem_
 
     // One tile from buffer BI.  Element (tb, i) of S^T/dP^T is key
     // 32tb + 8(i/4) + 4g2 + i%4 of the tile; it is used when 32tb + 8(i/4) + i%4 < m,
-    // m = row_lim - (tile start) - 4g2 (m <= 0 masks the whole tile).
-    auto tile = [&](auto bi_c, int m) {
+    // m = row_lim - (tile start) - 4g2 (m <= 0 masks the whole tile), and
+    // (window) when it is >= lo, lo = qrow - window + 1 - (tile start) - 4g2.
+    auto tile = [&](auto bi_c, int m, int lo) {
         constexpr int bi = decltype(bi_c)::value;
         const unsigned char* kl = smem + bi * kDqTileBytes;
         const unsigned char* vl = smem + (2 + bi) * kDqTileBytes;
@@ -553,7 +567,11 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem_
                 for (int e = 0; e < 8; ++e) {
                     const int i = kh * 8 + e;
                     float pv = fast_exp2(__builtin_fmaf(s[tb][i], c2, nl));
-                    pv = (32 * tb + 8 * (i >> 2) + (i & 3) < m) ? pv : 0.f;
+                    const int idx = 32 * tb + 8 * (i >> 2) + (i & 3);
+                    if constexpr (kSwa)
+                        pv = (idx < m && idx >= lo) ? pv : 0.f;
+                    else
+                        pv = (idx < m) ? pv : 0.f;
                     dsop[tb * 2 + kh][e] = (__bf16)(pv * __builtin_fmaf(dp[tb][i], scale, nd));
                 }
         // dQ^T[d][q] += sum over keys of K^T[d][key] dS^T[key][q], 4 column tiles of D
@@ -580,11 +598,12 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem_
     using C1 = std::integral_constant<int, 1>;
     for (int j = 0; j < n_tiles; j += 2) {
         if (j + 1 < n_tiles) issue(j + 1, 1);
-        tile(C0{}, row_lim - (t_first + j) * kDqTile - 4 * g2);
+        tile(C0{}, row_lim - (t_first + j) * kDqTile - 4 * g2, qrow - p.window + 1 - (t_first + j) * kDqTile - 4 * g2);
         bw_wait_vmem();
         __syncthreads();
         if (j + 2 < n_tiles) issue(j + 2, 0);
-        tile(C1{}, (j + 1 < n_tiles) ? row_lim - (t_first + j + 1) * kDqTile - 4 * g2 : 0);
+        tile(C1{}, (j + 1 < n_tiles) ? row_lim - (t_first + j + 1) * kDqTile - 4 * g2 : 0,
+             qrow - p.window + 1 - (t_first + j + 1) * kDqTile - 4 * g2);
         bw_wait_vmem();
         __syncthreads();
     }
@@ -634,18 +653,20 @@ __device__ __forceinline__ void dq_block_unit(const BwdParams& p, int* qb, int* 
     *b = stream / (p.n_hgroups * p.hkv);
 }
 
+template <bool kSwa>
 __global__ __launch_bounds__(kBwThreads, 2) void bwd_dq_kernel(BwdParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     int qb, hg, kvh, b;
     dq_block_unit(p, &qb, &hg, &kvh, &b);
-    dq_unit<1>(p, smem, qb, hg, kvh, b);
+    dq_unit<1, kSwa>(p, smem, qb, hg, kvh, b);
 }
 
+template <bool kSwa>
 __global__ __launch_bounds__(2 * kBwThreads, 1) void bwd_dq_split_kernel(BwdParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     int qb, hg, kvh, b;
     dq_block_unit(p, &qb, &hg, &kvh, &b);
-    dq_unit<2>(p, smem, qb, hg, kvh, b);
+    dq_unit<2, kSwa>(p, smem, qb, hg, kvh, b);
 }
 
 namespace {
@@ -664,6 +685,8 @@ int validate_backward(const fgqa_prefill_backward_args* a) {
         return FGQA_ERR_INVALID_ARGUMENT;
     if (a->num_q_heads % a->num_kv_heads != 0) return FGQA_ERR_INVALID_ARGUMENT;
     if (!isfinite(a->scale)) return FGQA_ERR_INVALID_ARGUMENT;
+    // a sliding window is a causal window (flash_swa_backward_kernel.py:278-282)
+    if (a->window_size < 0 || (a->window_size > 0 && !a->causal)) return FGQA_ERR_INVALID_ARGUMENT;
     const int64_t* strides[8] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride,
                                  a->grad_o_stride, a->grad_q_stride, a->grad_k_stride, a->grad_v_stride};
     for (const int64_t* s : strides)
@@ -797,6 +820,7 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     p.hkv = a->num_kv_heads;
     p.group = a->num_q_heads / a->num_kv_heads;
     p.causal = a->causal ? 1 : 0;
+    p.window = a->window_size;
     p.n_hsplit = pl.n_hsplit;
     p.hs = p.group / pl.n_hsplit;
     p.n_kvblocks = (int)ceil_div(p.skv, kKvKeys);
@@ -822,19 +846,39 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     // wave groups, as the forward does.  FGQA_BWD_DQ_SPLIT=0/1 forces the choice.
     bool dq_split = q_units < 4 * (int64_t)cus;
     if (const char* e = getenv("FGQA_BWD_DQ_SPLIT")) dq_split = e[0] == '1';
-    static bool smem_kv = false, smem_q = false, smem_q2 = false;
-    if ((st = set_smem(reinterpret_cast<const void*>(bwd_dkdv_kernel), kKvSmemBytes, &smem_kv)) != FGQA_OK) return st;
-    if ((st = set_smem(reinterpret_cast<const void*>(bwd_dq_kernel), kDqSmemBytes, &smem_q)) != FGQA_OK) return st;
-    if ((st = set_smem(reinterpret_cast<const void*>(bwd_dq_split_kernel), 2 * kDqSmemBytes, &smem_q2)) != FGQA_OK)
-        return st;
+    const bool swa = p.window > 0;
+    // kernel table: [swa] of dK/dV, dQ, split dQ
+    const void* kv_fn[2] = {reinterpret_cast<const void*>(bwd_dkdv_kernel<false>),
+                            reinterpret_cast<const void*>(bwd_dkdv_kernel<true>)};
+    const void* q_fn[2] = {reinterpret_cast<const void*>(bwd_dq_kernel<false>),
+                           reinterpret_cast<const void*>(bwd_dq_kernel<true>)};
+    const void* q2_fn[2] = {reinterpret_cast<const void*>(bwd_dq_split_kernel<false>),
+                            reinterpret_cast<const void*>(bwd_dq_split_kernel<true>)};
+    static bool smem_kv[2] = {}, smem_q[2] = {}, smem_q2[2] = {};
+    if ((st = set_smem(kv_fn[swa], kKvSmemBytes, &smem_kv[swa])) != FGQA_OK) return st;
+    if ((st = set_smem(q_fn[swa], kDqSmemBytes, &smem_q[swa])) != FGQA_OK) return st;
+    if ((st = set_smem(q2_fn[swa], 2 * kDqSmemBytes, &smem_q2[swa])) != FGQA_OK) return st;
 
     if (rows_q > 0) hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)ceil_div(rows_q, 16)), dim3(256), 0, s, p);
-    if (kv_units > 0)
-        hipLaunchKernelGGL(bwd_dkdv_kernel, dim3((unsigned)kv_units), dim3(kBwThreads), kKvSmemBytes, s, p);
-    if (q_units > 0 && dq_split)
-        hipLaunchKernelGGL(bwd_dq_split_kernel, dim3((unsigned)q_units), dim3(2 * kBwThreads), 2 * kDqSmemBytes, s, p);
-    else if (q_units > 0)
-        hipLaunchKernelGGL(bwd_dq_kernel, dim3((unsigned)q_units), dim3(kBwThreads), kDqSmemBytes, s, p);
+    if (kv_units > 0) {
+        if (swa)
+            hipLaunchKernelGGL(bwd_dkdv_kernel<true>, dim3((unsigned)kv_units), dim3(kBwThreads), kKvSmemBytes, s, p);
+        else
+            hipLaunchKernelGGL(bwd_dkdv_kernel<false>, dim3((unsigned)kv_units), dim3(kBwThreads), kKvSmemBytes, s, p);
+    }
+    if (q_units > 0 && dq_split) {
+        if (swa)
+            hipLaunchKernelGGL(bwd_dq_split_kernel<true>, dim3((unsigned)q_units), dim3(2 * kBwThreads),
+                               2 * kDqSmemBytes, s, p);
+        else
+            hipLaunchKernelGGL(bwd_dq_split_kernel<false>, dim3((unsigned)q_units), dim3(2 * kBwThreads),
+                               2 * kDqSmemBytes, s, p);
+    } else if (q_units > 0) {
+        if (swa)
+            hipLaunchKernelGGL(bwd_dq_kernel<true>, dim3((unsigned)q_units), dim3(kBwThreads), kDqSmemBytes, s, p);
+        else
+            hipLaunchKernelGGL(bwd_dq_kernel<false>, dim3((unsigned)q_units), dim3(kBwThreads), kDqSmemBytes, s, p);
+    }
     if (pl.n_hsplit > 1 && rows_kv > 0)
         hipLaunchKernelGGL(bwd_dkdv_reduce_kernel, dim3((unsigned)ceil_div(rows_kv, 16)), dim3(256), 0, s, p);
     if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;

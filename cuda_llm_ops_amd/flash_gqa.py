@@ -543,7 +543,8 @@ def _launch_bhsd_prefill(kind, q, k, v, scale, out, lse, causal):
 
 
 # --------------------------------------------------------------------------- backward
-def _backward_args(q, k, v, o, lse, grad_o, dq, dk, dv, scale, causal, layout, workspace) -> _lib.BackwardArgs:
+def _backward_args(q, k, v, o, lse, grad_o, dq, dk, dv, scale, causal, layout, workspace,
+                   window_size=0) -> _lib.BackwardArgs:
     """C ABI argument block; 4-D tensors in `layout` ('bshd' or 'bhsd')."""
     def sbh(t):
         if layout == "bshd":
@@ -563,6 +564,7 @@ def _backward_args(q, k, v, o, lse, grad_o, dq, dk, dv, scale, causal, layout, w
     a.num_q_heads, a.num_kv_heads, a.head_dim = Hq, Hkv, D
     a.causal = 1 if causal else 0
     a.scale = float(scale)
+    a.window_size = int(window_size)
     a.q_stride[:] = sbh(q)
     a.k_stride[:] = sbh(k)
     a.v_stride[:] = sbh(v)
@@ -604,7 +606,8 @@ def _grad_out(t, shape, ref, name):
     return t
 
 
-def _backward_bshd_prepare(q, k, v, o, lse, grad_o, scale, causal, grad_q, grad_k, grad_v, workspace):
+def _backward_bshd_prepare(q, k, v, o, lse, grad_o, scale, causal, grad_q, grad_k, grad_v, workspace,
+                           window_size=0):
     for t in (q, k, v, o, grad_o):
         if t.dtype != torch.bfloat16:
             raise ValueError("Flash GQA backward expects bf16 inputs and grad_o")
@@ -628,48 +631,44 @@ def _backward_bshd_prepare(q, k, v, o, lse, grad_o, scale, causal, grad_q, grad_
     grad_q = _grad_out(grad_q, q.shape, q, "grad_q")
     grad_k = _grad_out(grad_k, k.shape, q, "grad_k")
     grad_v = _grad_out(grad_v, v.shape, q, "grad_v")
-    a = _backward_args(q, k, v, o, lse, grad_o, grad_q, grad_k, grad_v, scale, causal, "bshd", workspace)
+    a = _backward_args(q, k, v, o, lse, grad_o, grad_q, grad_k, grad_v, scale, causal, "bshd", workspace,
+                       window_size)
     return a, (grad_q, grad_k, grad_v), (q, k, v, o, lse, grad_o, grad_q, grad_k, grad_v, workspace)
 
 
 def flash_gqa_backward_bshd(q, k, v, o, lse, grad_o, scale=None, causal=True,
-                            grad_q=None, grad_k=None, grad_v=None, workspace=None):
+                            grad_q=None, grad_k=None, grad_v=None, workspace=None, window_size=0):
     """Prefill backward in BSHD: q/o/grad_o [B,Sq,Hq,D], k/v [B,Skv,Hkv,D], lse
-    [B,Hq,Sq] from the forward -> (grad_q, grad_k, grad_v) bf16 in q/k/v's shapes."""
+    [B,Hq,Sq] from the forward -> (grad_q, grad_k, grad_v) bf16 in q/k/v's shapes.
+
+    ``window_size`` > 0 (causal only) restricts row i to keys
+    [i - window_size + 1, i], the sliding-window backward; pass the forward's
+    LSE (with the sink term when the forward had one) and the gradients follow
+    the sink-adjusted softmax."""
     a, grads, _keep = _backward_bshd_prepare(q, k, v, o, lse, grad_o, scale, causal,
-                                             grad_q, grad_k, grad_v, workspace)
+                                             grad_q, grad_k, grad_v, workspace, window_size)
     _lib.check(_lib.lib().fgqa_prefill_backward_bf16(ctypes.byref(a), ctypes.c_void_p(_stream())),
                "fgqa_prefill_backward_bf16")
     return grads
 
 
 def prepare_backward(q, k, v, o, lse, grad_o, scale=None, causal=True,
-                     grad_q=None, grad_k=None, grad_v=None, workspace=None):
+                     grad_q=None, grad_k=None, grad_v=None, workspace=None, window_size=0):
     """``flash_gqa_backward_bshd`` validated once; returns a ``PreparedLaunch``
     whose ``out`` is the (grad_q, grad_k, grad_v) tuple."""
     a, grads, keep = _backward_bshd_prepare(q, k, v, o, lse, grad_o, scale, causal,
-                                            grad_q, grad_k, grad_v, workspace)
+                                            grad_q, grad_k, grad_v, workspace, window_size)
     return PreparedLaunch(_lib.lib().fgqa_prefill_backward_bf16, a, keep, grads, "fgqa_prefill_backward_bf16")
 
 
-def launch_flash_gqa_backward_bf16_kernel(q, k, v, o, lse, grad_o, scale=None, causal=True,
-                                          block_kv=64, num_warps=4, num_stages=3):
-    """Mirror of the reference's Triton backward launcher
-    (src/python/Triton/flash_gqa_backward_kernel.py:312-478): BHSD q/o/grad_o
-    [B,Hq,Sq,D] (or 3-D [Hq,Sq,D]), k/v [B,Hkv,Skv,D], lse [B,Hq,Sq] (or
-    [Hq,Sq]); returns bf16 (grad_q, grad_k, grad_v) shaped like q, k, v.
-
-    Same checks and ValueError messages as the reference (:356-405).
-    ``block_kv``, ``num_warps`` and ``num_stages`` are Triton tuning knobs,
-    accepted for signature compatibility only.  Beyond the reference, inputs
-    must share the batch dimension and head_dim_v must equal head_dim_qk (128).
-    """
-    del block_kv, num_warps, num_stages
+def _launch_bhsd_backward(kind, q, k, v, o, lse, grad_o, scale, causal, window_size):
+    """Shared body of the GQA and SWA backward mirrors: the reference's checks
+    and messages (``kind`` is "GQA" or "SWA"), then one C ABI call."""
     if (q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16
             or o.dtype != torch.bfloat16 or grad_o.dtype != torch.bfloat16):
-        raise ValueError("Flash GQA backward expects bf16 inputs and grad_o")
+        raise ValueError(f"Flash {kind} backward expects bf16 inputs and grad_o")
     if lse.dtype != torch.float32:
-        raise ValueError("Flash GQA backward expects lse to be float32")
+        raise ValueError(f"Flash {kind} backward expects lse to be float32")
     if q.dim() not in (3, 4):
         raise ValueError("Q must be 3D or 4D")
     if k.dim() != q.dim() or v.dim() != q.dim() or o.dim() != q.dim() or grad_o.dim() != q.dim():
@@ -705,6 +704,11 @@ def launch_flash_gqa_backward_bf16_kernel(q, k, v, o, lse, grad_o, scale=None, c
         lse_b = lse
     if tuple(lse_b.shape) != (batch, q_heads, seqlen_q):
         raise ValueError("LSE must have shape [batch, q_heads, seqlen_q]")
+    if kind == "SWA":
+        if window_size is None:
+            raise ValueError("window_size must be provided")
+        if int(window_size) <= 0:
+            raise ValueError("window_size must be positive")
     if any(t.shape[0] != batch for t in (kb, vb, ob, gb)):
         raise ValueError("Q, K, V, O, and grad_o must share batch dimension")
     if head_dim_v != head_dim_qk:
@@ -717,12 +721,49 @@ def launch_flash_gqa_backward_bf16_kernel(q, k, v, o, lse, grad_o, scale=None, c
     dq = torch.empty((batch, q_heads, seqlen_q, head_dim_qk), device=qb.device, dtype=torch.bfloat16)
     dk = torch.empty((batch, num_kv_heads, seqlen_kv, head_dim_qk), device=qb.device, dtype=torch.bfloat16)
     dv = torch.empty((batch, num_kv_heads, seqlen_kv, head_dim_v), device=qb.device, dtype=torch.bfloat16)
-    a = _backward_args(qb, kb, vb, ob, lse_b, gb, dq, dk, dv, scale, causal, "bhsd", None)
+    a = _backward_args(qb, kb, vb, ob, lse_b, gb, dq, dk, dv, scale, causal, "bhsd", None,
+                       int(window_size or 0))
     _lib.check(_lib.lib().fgqa_prefill_backward_bf16(ctypes.byref(a), ctypes.c_void_p(_stream())),
                "fgqa_prefill_backward_bf16")
     if squeeze_output:
         return dq.squeeze(0), dk.squeeze(0), dv.squeeze(0)
     return dq, dk, dv
+
+
+def launch_flash_gqa_backward_bf16_kernel(q, k, v, o, lse, grad_o, scale=None, causal=True,
+                                          block_kv=64, num_warps=4, num_stages=3):
+    """Mirror of the reference's Triton backward launcher
+    (src/python/Triton/flash_gqa_backward_kernel.py:312-478): BHSD q/o/grad_o
+    [B,Hq,Sq,D] (or 3-D [Hq,Sq,D]), k/v [B,Hkv,Skv,D], lse [B,Hq,Sq] (or
+    [Hq,Sq]); returns bf16 (grad_q, grad_k, grad_v) shaped like q, k, v.
+
+    Same checks and ValueError messages as the reference (:356-405).
+    ``block_kv``, ``num_warps`` and ``num_stages`` are Triton tuning knobs,
+    accepted for signature compatibility only.  Beyond the reference, inputs
+    must share the batch dimension and head_dim_v must equal head_dim_qk (128).
+    """
+    del block_kv, num_warps, num_stages
+    return _launch_bhsd_backward("GQA", q, k, v, o, lse, grad_o, scale, causal, 0)
+
+
+def launch_flash_swa_backward_bf16_kernel(q, k, v, o, lse, grad_o, scale=None, window_size=None,
+                                          block_kv=64, num_warps=8, num_stages=3):
+    """Mirror of the reference's Triton SWA backward launcher
+    (src/python/Triton/SWA/flash_swa_backward_kernel.py:323-489): gradients of
+    causal sliding-window attention (row i sees keys [i - window_size + 1, i]).
+    ``lse`` is the forward's, computed with the sink term; the sink has no
+    value row, so the gradients are the windowed softmax's with that LSE.
+    BHSD q/o/grad_o [B,Hq,Sq,D] (or 3-D), k/v [B,Hkv,Skv,D], lse [B,Hq,Sq];
+    returns bf16 (grad_q, grad_k, grad_v) shaped like q, k, v.
+
+    Same checks and ValueError messages as the reference (:370-420).
+    ``block_kv``, ``num_warps`` and ``num_stages`` are Triton tuning knobs,
+    accepted for signature compatibility only.  Beyond the reference,
+    window_size must be positive, inputs must share the batch dimension and
+    head_dim_v must equal head_dim_qk (128).
+    """
+    del block_kv, num_warps, num_stages
+    return _launch_bhsd_backward("SWA", q, k, v, o, lse, grad_o, scale, True, window_size)
 
 
 # --------------------------------------------------------------------------- sliding window + sink

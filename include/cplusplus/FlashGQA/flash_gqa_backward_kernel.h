@@ -50,3 +50,32 @@ void LaunchFlashGqaBackwardBf16Kernel(const bf16_t* q,
                                       int numKvHeads,
                                       int headDim,
                                       bool causal);
+
+/**
+ * @brief Launches the sliding-window (SWA) bf16 prefill backward (BSHD layout).
+ *
+ * Counterpart of the reference's Triton SWA backward launcher
+ * (src/python/Triton/SWA/flash_swa_backward_kernel.py:323-489, kernel
+ * :157-321): query i's gradients cover keys [i - windowSize + 1, i].  lse is
+ * LaunchFlashSwaForwardBf16Kernel's, computed with the sink term; the sink
+ * has no value row, so no sink gradient is produced (as in the reference).
+ * Parameters as LaunchFlashGqaBackwardBf16Kernel, with
+ * @param windowSize Sliding-window size (> 0).
+ */
+void LaunchFlashSwaBackwardBf16Kernel(const bf16_t* q,
+                                      const bf16_t* k,
+                                      const bf16_t* v,
+                                      const bf16_t* o,
+                                      const float* lse,
+                                      const bf16_t* gradO,
+                                      float scale,
+                                      bf16_t* gradQ,
+                                      bf16_t* gradK,
+                                      bf16_t* gradV,
+                                      int batchSize,
+                                      int seqLengthQ,
+                                      int seqLengthKv,
+                                      int numQueryHeads,
+                                      int numKvHeads,
+                                      int headDim,
+                                      int windowSize);

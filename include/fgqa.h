@@ -210,6 +210,12 @@ int fgqa_prefill_bf16(const fgqa_prefill_args* args, void* stream);
  * workspace / workspace_bytes  device scratch of at least
  *   fgqa_prefill_backward_workspace_bytes() bytes, 256-byte aligned; NULL/0
  *   uses the library's per-device cached buffer.
+ * window_size  0: none.  > 0 (causal only): the sliding-window backward,
+ *   replacing the Triton-only launch_flash_swa_backward_bf16_kernel,
+ *   reference src/python/Triton/SWA/flash_swa_backward_kernel.py:323-489
+ *   (kernel :157-321): row i uses keys [i - window_size + 1, i].  A sink
+ *   needs nothing here: it is in the lse the forward wrote (the reference
+ *   computes no sink gradient).
  */
 typedef struct fgqa_prefill_backward_args {
     const void* q;
@@ -239,6 +245,7 @@ typedef struct fgqa_prefill_backward_args {
     int64_t grad_v_stride[3];
     void* workspace;
     size_t workspace_bytes;
+    int32_t window_size;
 } fgqa_prefill_backward_args;
 
 /* Bytes of workspace fgqa_prefill_backward_bf16 needs (pointers unused). */

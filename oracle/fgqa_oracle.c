@@ -500,17 +500,17 @@ static float bwd_pair(const bwd_ctx* c, int b, int h, int i, int j, float* ds) {
     return p;
 }
 
-int fgqa_oracle_prefill_backward_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                                      const uint16_t* o, const float* lse, const uint16_t* grad_o,
-                                      float scale, float* dq, float* dk, float* dv,
-                                      int batch, int sq, int skv, int hq, int hkv, int d,
-                                      const int64_t* qs, const int64_t* ks,
-                                      const int64_t* vs, const int64_t* os,
-                                      const int64_t* dos, int causal,
-                                      const int* rows, const int* keys, int nthreads) {
+static int backward_core(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                         const uint16_t* o, const float* lse, const uint16_t* grad_o,
+                         float scale, float* dq, float* dk, float* dv,
+                         int batch, int sq, int skv, int hq, int hkv, int d,
+                         const int64_t* qs, const int64_t* ks,
+                         const int64_t* vs, const int64_t* os,
+                         const int64_t* dos, int causal, int window,
+                         const int* rows, const int* keys, int nthreads) {
     if (!q || !k || !v || !o || !lse || !grad_o || !qs || !ks || !vs || !os || !dos) return -1;
     if (batch < 0 || sq < 0 || skv < 0 || hq <= 0 || hkv <= 0 || d <= 0 || d > ORACLE_MAX_D) return -1;
-    if (hq % hkv != 0) return -1;
+    if (hq % hkv != 0 || window < 0 || (window > 0 && !causal)) return -1;
     const int group = hq / hkv;
     const int r0 = rows ? rows[0] : 0, r1 = rows ? rows[1] : sq;
     const int k0 = keys ? keys[0] : 0, k1 = keys ? keys[1] : skv;
@@ -544,7 +544,8 @@ int fgqa_oracle_prefill_backward_bf16(const uint16_t* q, const uint16_t* k, cons
                     float acc[ORACLE_MAX_D];
                     for (int x = 0; x < d; ++x) acc[x] = 0.f;
                     const int jend = causal ? (i + 1 < skv ? i + 1 : skv) : skv;
-                    for (int j = 0; j < jend; ++j) {
+                    const int jbeg = (window > 0 && i - window + 1 > 0) ? i - window + 1 : 0;
+                    for (int j = jbeg; j < jend; ++j) {
                         float ds;
                         (void)bwd_pair(&c, b, h, i, j, &ds);
                         const uint16_t* krow = k + b * ks[0] + (int64_t)j * ks[1] + kvh * ks[2];
@@ -565,8 +566,9 @@ int fgqa_oracle_prefill_backward_bf16(const uint16_t* q, const uint16_t* k, cons
                     float ak[ORACLE_MAX_D], av[ORACLE_MAX_D];
                     for (int x = 0; x < d; ++x) ak[x] = av[x] = 0.f;
                     const int ibeg = causal ? j : 0;
+                    const int iend = (window > 0 && j + window < sq) ? j + window : sq;
                     for (int h = kvh * group; h < (kvh + 1) * group; ++h)
-                        for (int i = ibeg; i < sq; ++i) {
+                        for (int i = ibeg; i < iend; ++i) {
                             float ds;
                             const float pb = bf(fgqa_oracle_f32_to_bf16(bwd_pair(&c, b, h, i, j, &ds)));
                             const uint16_t* qrow = q + b * qs[0] + (int64_t)i * qs[1] + h * qs[2];
@@ -587,18 +589,52 @@ int fgqa_oracle_prefill_backward_bf16(const uint16_t* q, const uint16_t* k, cons
     return 0;
 }
 
-/* Exact gradient of softmax attention in double (see the header). */
-int fgqa_oracle_attention_backward_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+int fgqa_oracle_prefill_backward_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                      const uint16_t* o, const float* lse, const uint16_t* grad_o,
+                                      float scale, float* dq, float* dk, float* dv,
+                                      int batch, int sq, int skv, int hq, int hkv, int d,
+                                      const int64_t* qs, const int64_t* ks,
+                                      const int64_t* vs, const int64_t* os,
+                                      const int64_t* dos, int causal,
+                                      const int* rows, const int* keys, int nthreads) {
+    return backward_core(q, k, v, o, lse, grad_o, scale, dq, dk, dv, batch, sq, skv, hq, hkv, d, qs, ks, vs, os,
+                         dos, causal, 0, rows, keys, nthreads);
+}
+
+/*
+ * Sliding-window backward: the same steps with the window mask of
+ * src/python/Triton/SWA/flash_swa_backward_kernel.py:278-282 (key j used by
+ * row i when i - window < j <= i).  The sink enters only through the given
+ * LSE, which the forward computed with it (:252-253 of the same file).
+ */
+int fgqa_oracle_prefill_swa_backward_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                          const uint16_t* o, const float* lse, const uint16_t* grad_o,
+                                          float scale, float* dq, float* dk, float* dv,
+                                          int batch, int sq, int skv, int hq, int hkv, int d,
+                                          const int64_t* qs, const int64_t* ks,
+                                          const int64_t* vs, const int64_t* os,
+                                          const int64_t* dos, int window,
+                                          const int* rows, const int* keys, int nthreads) {
+    if (window <= 0) return -1;
+    return backward_core(q, k, v, o, lse, grad_o, scale, dq, dk, dv, batch, sq, skv, hq, hkv, d, qs, ks, vs, os,
+                         dos, 1, window, rows, keys, nthreads);
+}
+
+/* Exact gradient of softmax attention in double (see the header); window > 0
+ * limits row i to keys (i - window, i], sink (nullable, per query head) adds
+ * sink[h] to the softmax denominator. */
+static int attention_backward_f64_core(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                        const uint16_t* o, const uint16_t* grad_o, double scale,
                                        double* dq, double* dk, double* dv,
                                        int batch, int sq, int skv, int hq, int hkv, int d,
                                        const int64_t* qs, const int64_t* ks,
                                        const int64_t* vs, const int64_t* os,
-                                       const int64_t* dos, int causal, int nthreads) {
+                                       const int64_t* dos, int causal, int window, const float* sink,
+                                       int nthreads) {
     if (!q || !k || !v || !grad_o || !dq || !dk || !dv || !qs || !ks || !vs || !dos) return -1;
     if (o && !os) return -1;
     if (batch < 0 || sq < 0 || skv < 0 || hq <= 0 || hkv <= 0 || d <= 0) return -1;
-    if (hq % hkv != 0) return -1;
+    if (hq % hkv != 0 || window < 0 || (window > 0 && !causal)) return -1;
     const int group = hq / hkv;
     set_threads(nthreads);
     memset(dq, 0, sizeof(double) * (size_t)batch * sq * hq * d);
@@ -616,9 +652,10 @@ int fgqa_oracle_attention_backward_f64(const uint16_t* q, const uint16_t* k, con
                     const uint16_t* qrow = q + b * qs[0] + (int64_t)i * qs[1] + h * qs[2];
                     const uint16_t* dorow = grad_o + b * dos[0] + (int64_t)i * dos[1] + h * dos[2];
                     const int nvis = causal ? (i + 1 < skv ? i + 1 : skv) : skv;
-                    if (nvis == 0) continue;
+                    const int j0 = (window > 0 && i - window + 1 > 0) ? i - window + 1 : 0;
+                    if (nvis <= j0) continue;
                     double rmax = -INFINITY;
-                    for (int j = 0; j < nvis; ++j) {
+                    for (int j = j0; j < nvis; ++j) {
                         const uint16_t* krow = k + b * ks[0] + (int64_t)j * ks[1] + kvh * ks[2];
                         double acc = 0.0;
                         for (int x = 0; x < d; ++x) acc += (double)bf(qrow[x]) * (double)bf(krow[x]);
@@ -626,12 +663,13 @@ int fgqa_oracle_attention_backward_f64(const uint16_t* q, const uint16_t* k, con
                         if (p[j] > rmax) rmax = p[j];
                     }
                     double sum = 0.0;
-                    for (int j = 0; j < nvis; ++j) {
+                    for (int j = j0; j < nvis; ++j) {
                         p[j] = exp(p[j] - rmax);
                         sum += p[j];
                     }
+                    if (sink) sum += (double)sink[h] * exp(-rmax);
                     double delta = 0.0;
-                    for (int j = 0; j < nvis; ++j) {
+                    for (int j = j0; j < nvis; ++j) {
                         p[j] /= sum;
                         const uint16_t* vrow = v + b * vs[0] + (int64_t)j * vs[1] + kvh * vs[2];
                         double acc = 0.0;
@@ -645,7 +683,7 @@ int fgqa_oracle_attention_backward_f64(const uint16_t* q, const uint16_t* k, con
                         for (int x = 0; x < d; ++x) delta += (double)bf(orow[x]) * (double)bf(dorow[x]);
                     }
                     double* dqrow = dq + (((size_t)b * sq + i) * hq + h) * d;
-                    for (int j = 0; j < nvis; ++j) {
+                    for (int j = j0; j < nvis; ++j) {
                         const double ds = p[j] * (dp[j] - delta) * scale;
                         const uint16_t* krow = k + b * ks[0] + (int64_t)j * ks[1] + kvh * ks[2];
                         double* dkrow = dk + (((size_t)b * skv + j) * hkv + kvh) * d;
@@ -661,6 +699,29 @@ int fgqa_oracle_attention_backward_f64(const uint16_t* q, const uint16_t* k, con
             free(dp);
         }
     return 0;
+}
+
+int fgqa_oracle_attention_backward_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                       const uint16_t* o, const uint16_t* grad_o, double scale,
+                                       double* dq, double* dk, double* dv,
+                                       int batch, int sq, int skv, int hq, int hkv, int d,
+                                       const int64_t* qs, const int64_t* ks,
+                                       const int64_t* vs, const int64_t* os,
+                                       const int64_t* dos, int causal, int nthreads) {
+    return attention_backward_f64_core(q, k, v, o, grad_o, scale, dq, dk, dv, batch, sq, skv, hq, hkv, d, qs, ks,
+                                       vs, os, dos, causal, 0, NULL, nthreads);
+}
+
+int fgqa_oracle_attention_swa_backward_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                           const uint16_t* o, const uint16_t* grad_o, double scale,
+                                           double* dq, double* dk, double* dv,
+                                           int batch, int sq, int skv, int hq, int hkv, int d,
+                                           const int64_t* qs, const int64_t* ks,
+                                           const int64_t* vs, const int64_t* os,
+                                           const int64_t* dos, int window, const float* sink, int nthreads) {
+    if (window <= 0) return -1;
+    return attention_backward_f64_core(q, k, v, o, grad_o, scale, dq, dk, dv, batch, sq, skv, hq, hkv, d, qs, ks,
+                                       vs, os, dos, 1, window, sink, nthreads);
 }
 
 /*

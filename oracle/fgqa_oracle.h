@@ -35,6 +35,11 @@
  *                                            contiguous bf16 cache; page-permutation
  *                                            invariance; fp8 path vs the fp64 brute force
  *                                            on the decoded values
+ *   fgqa_oracle_prefill_swa_backward_bf16   bit-identical to fgqa_oracle_prefill_backward_bf16
+ *                                            for a window >= Sq; the float64 SWA gradient
+ *                                            below at the stated tolerance
+ *   fgqa_oracle_attention_swa_backward_f64  central finite differences of a float64 numpy
+ *                                            forward with window and sink
  *   fgqa_oracle_prefill_swa_bf16            bit-identical to fgqa_oracle_prefill_bf16 for a
  *                                            window >= Sq and no sink; a float64 numpy
  *                                            restatement with the window and sink; closed
@@ -192,6 +197,37 @@ int fgqa_oracle_attention_backward_f64(const uint16_t* q, const uint16_t* k, con
                                        const int64_t* q_strides, const int64_t* k_strides,
                                        const int64_t* v_strides, const int64_t* o_strides,
                                        const int64_t* grad_o_strides, int causal, int nthreads);
+
+/*
+ * Sliding-window backward, restating the reference's Triton SWA backward
+ * src/python/Triton/SWA/flash_swa_backward_kernel.py:157-321: the steps of
+ * fgqa_oracle_prefill_backward_bf16 with its causal + window mask (:278-282,
+ * row i uses keys (i - window, i]).  The LSE is the forward's, sink included;
+ * the reference computes no sink gradient.  window > 0.
+ */
+int fgqa_oracle_prefill_swa_backward_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                          const uint16_t* o, const float* lse, const uint16_t* grad_o,
+                                          float scale, float* dq, float* dk, float* dv,
+                                          int batch, int sq, int skv, int hq, int hkv, int d,
+                                          const int64_t* q_strides, const int64_t* k_strides,
+                                          const int64_t* v_strides, const int64_t* o_strides,
+                                          const int64_t* grad_o_strides, int window,
+                                          const int* rows, const int* keys, int nthreads);
+
+/*
+ * Exact gradient (double) of causal sliding-window attention with a per-head
+ * sink in the denominator: p_j = e^{s_j} / (sum_k e^{s_k} + sink[h]) over the
+ * window's keys; the sink acts as a key with zero value, so the gradient keeps
+ * the form of fgqa_oracle_attention_backward_f64.  sink nullable.  window > 0.
+ */
+int fgqa_oracle_attention_swa_backward_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                           const uint16_t* o, const uint16_t* grad_o, double scale,
+                                           double* dq, double* dk, double* dv,
+                                           int batch, int sq, int skv, int hq, int hkv, int d,
+                                           const int64_t* q_strides, const int64_t* k_strides,
+                                           const int64_t* v_strides, const int64_t* o_strides,
+                                           const int64_t* grad_o_strides, int window, const float* sink,
+                                           int nthreads);
 
 /*
  * Causal sliding-window prefill with a per-head sink, restating the reference's

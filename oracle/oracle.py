@@ -73,6 +73,16 @@ def lib() -> ctypes.CDLL:
             _u16p, _u16p, _u16p, _u16p, _f32p, _u16p, ctypes.c_float, _f32p, _f32p, _f32p,
             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
             _i64p, _i64p, _i64p, _i64p, _i64p, ctypes.c_int, _i32p, _i32p, ctypes.c_int]
+        L.fgqa_oracle_prefill_swa_backward_bf16.restype = ctypes.c_int
+        L.fgqa_oracle_prefill_swa_backward_bf16.argtypes = [
+            _u16p, _u16p, _u16p, _u16p, _f32p, _u16p, ctypes.c_float, _f32p, _f32p, _f32p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            _i64p, _i64p, _i64p, _i64p, _i64p, ctypes.c_int, _i32p, _i32p, ctypes.c_int]
+        L.fgqa_oracle_attention_swa_backward_f64.restype = ctypes.c_int
+        L.fgqa_oracle_attention_swa_backward_f64.argtypes = [
+            _u16p, _u16p, _u16p, _u16p, _u16p, ctypes.c_double, _f64p, _f64p, _f64p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            _i64p, _i64p, _i64p, _i64p, _i64p, ctypes.c_int, _f32p, ctypes.c_int]
         L.fgqa_oracle_attention_backward_f64.restype = ctypes.c_int
         L.fgqa_oracle_attention_backward_f64.argtypes = [
             _u16p, _u16p, _u16p, _u16p, _u16p, ctypes.c_double, _f64p, _f64p, _f64p,
@@ -264,13 +274,15 @@ def attention_f64(q, k, v, scale, causal=False, causal_offset=0, seqlens=None,
 
 
 def prefill_backward(q, k, v, o, lse, grad_o, scale, causal=True, layout="bshd",
-                     rows=None, keys=None, want=("dq", "dk", "dv"), nthreads=0):
+                     rows=None, keys=None, want=("dq", "dk", "dv"), nthreads=0, window=0):
     """Backward oracle (restates src/python/Triton/flash_gqa_backward_kernel.py).
     q/o/grad_o and k/v in `layout`; lse float32 [B,Hq,Sq].  Returns the fp32
     accumulators (dq [B,Sq,Hq,D], dk, dv [B,Skv,Hkv,D], BSHD) -- round with
     f32_to_bf16 for the reference's bf16 outputs.  rows/keys = (first, end)
     limit which dq rows / dk,dv rows are computed (the others are NaN); an
-    output not named in `want` is returned as None."""
+    output not named in `want` is returned as None.  window > 0 (causal):
+    the sliding-window backward (SWA/flash_swa_backward_kernel.py), with the
+    forward's sink-adjusted lse."""
     q, k, v, o, grad_o = (np.ascontiguousarray(x, dtype=np.uint16) for x in (q, k, v, o, grad_o))
     lse = np.ascontiguousarray(lse, dtype=np.float32)
     B, Sq, Hq, D = _dims(q, layout)
@@ -281,23 +293,31 @@ def prefill_backward(q, k, v, o, lse, grad_o, scale, causal=True, layout="bshd",
     qs, ks, vs, os_, dos = (_strides(x, layout) for x in (q, k, v, o, grad_o))
     rr = None if rows is None else np.array(rows, dtype=np.int32)
     kk = None if keys is None else np.array(keys, dtype=np.int32)
-    rc = lib().fgqa_oracle_prefill_backward_bf16(
-        _ptr(q, ctypes.c_uint16), _ptr(k, ctypes.c_uint16), _ptr(v, ctypes.c_uint16),
-        _ptr(o, ctypes.c_uint16), _ptr(lse, ctypes.c_float), _ptr(grad_o, ctypes.c_uint16),
-        float(scale), _ptr(dq, ctypes.c_float), _ptr(dk, ctypes.c_float), _ptr(dv, ctypes.c_float),
-        B, Sq, Skv, Hq, Hkv, D,
-        _ptr(qs, ctypes.c_int64), _ptr(ks, ctypes.c_int64), _ptr(vs, ctypes.c_int64),
-        _ptr(os_, ctypes.c_int64), _ptr(dos, ctypes.c_int64), int(bool(causal)),
-        _ptr(rr, ctypes.c_int32), _ptr(kk, ctypes.c_int32), int(nthreads))
+    args = (_ptr(q, ctypes.c_uint16), _ptr(k, ctypes.c_uint16), _ptr(v, ctypes.c_uint16),
+            _ptr(o, ctypes.c_uint16), _ptr(lse, ctypes.c_float), _ptr(grad_o, ctypes.c_uint16),
+            float(scale), _ptr(dq, ctypes.c_float), _ptr(dk, ctypes.c_float), _ptr(dv, ctypes.c_float),
+            B, Sq, Skv, Hq, Hkv, D,
+            _ptr(qs, ctypes.c_int64), _ptr(ks, ctypes.c_int64), _ptr(vs, ctypes.c_int64),
+            _ptr(os_, ctypes.c_int64), _ptr(dos, ctypes.c_int64))
+    tail = (_ptr(rr, ctypes.c_int32), _ptr(kk, ctypes.c_int32), int(nthreads))
+    if window > 0:
+        if not causal:
+            raise ValueError("prefill_backward: a window needs causal=True")
+        rc = lib().fgqa_oracle_prefill_swa_backward_bf16(*args, int(window), *tail)
+    else:
+        rc = lib().fgqa_oracle_prefill_backward_bf16(*args, int(bool(causal)), *tail)
     if rc != 0:
         raise ValueError("fgqa_oracle_prefill_backward_bf16: invalid arguments")
     return dq, dk, dv
 
 
-def attention_backward_f64(q, k, v, grad_o, scale, causal=True, o=None, layout="bshd", nthreads=0):
+def attention_backward_f64(q, k, v, grad_o, scale, causal=True, o=None, layout="bshd", nthreads=0,
+                           window=0, sink=None):
     """Exact gradient of softmax attention in float64.  o=None: delta from P
     (the true gradient); o given (bf16 bits): delta = sum O*dO as the torch
-    reference does.  Returns (dq [B,Sq,Hq,D], dk, dv [B,Skv,Hkv,D]) float64."""
+    reference does.  window > 0 and/or sink (float32 [Hq]): causal
+    sliding-window attention with the sink in the denominator.  Returns
+    (dq [B,Sq,Hq,D], dk, dv [B,Skv,Hkv,D]) float64."""
     q, k, v, grad_o = (np.ascontiguousarray(x, dtype=np.uint16) for x in (q, k, v, grad_o))
     B, Sq, Hq, D = _dims(q, layout)
     _, Skv, Hkv, _ = _dims(k, layout)
@@ -309,13 +329,20 @@ def attention_backward_f64(q, k, v, grad_o, scale, causal=True, o=None, layout="
     if o is not None:
         o = np.ascontiguousarray(o, dtype=np.uint16)
         os_ = _strides(o, layout)
-    rc = lib().fgqa_oracle_attention_backward_f64(
-        _ptr(q, ctypes.c_uint16), _ptr(k, ctypes.c_uint16), _ptr(v, ctypes.c_uint16),
-        _ptr(o, ctypes.c_uint16), _ptr(grad_o, ctypes.c_uint16), float(scale),
-        _ptr(dq, ctypes.c_double), _ptr(dk, ctypes.c_double), _ptr(dv, ctypes.c_double),
-        B, Sq, Skv, Hq, Hkv, D,
-        _ptr(qs, ctypes.c_int64), _ptr(ks, ctypes.c_int64), _ptr(vs, ctypes.c_int64),
-        _ptr(os_, ctypes.c_int64), _ptr(dos, ctypes.c_int64), int(bool(causal)), int(nthreads))
+    args = (_ptr(q, ctypes.c_uint16), _ptr(k, ctypes.c_uint16), _ptr(v, ctypes.c_uint16),
+            _ptr(o, ctypes.c_uint16), _ptr(grad_o, ctypes.c_uint16), float(scale),
+            _ptr(dq, ctypes.c_double), _ptr(dk, ctypes.c_double), _ptr(dv, ctypes.c_double),
+            B, Sq, Skv, Hq, Hkv, D,
+            _ptr(qs, ctypes.c_int64), _ptr(ks, ctypes.c_int64), _ptr(vs, ctypes.c_int64),
+            _ptr(os_, ctypes.c_int64), _ptr(dos, ctypes.c_int64))
+    if window > 0 or sink is not None:
+        if not causal:
+            raise ValueError("attention_backward_f64: a window or sink needs causal=True")
+        w = int(window) if window > 0 else max(Sq, Skv) + 1
+        sk = None if sink is None else np.ascontiguousarray(sink, dtype=np.float32)
+        rc = lib().fgqa_oracle_attention_swa_backward_f64(*args, w, _ptr(sk, ctypes.c_float), int(nthreads))
+    else:
+        rc = lib().fgqa_oracle_attention_backward_f64(*args, int(bool(causal)), int(nthreads))
     if rc != 0:
         raise ValueError("fgqa_oracle_attention_backward_f64: invalid arguments")
     return dq, dk, dv

@@ -44,6 +44,7 @@ def test_cplusplus_entry_points_exported():
                           "LaunchFlashGqaBf16KernelPaged",
                           "LaunchFlashGqaForwardBf16Kernel", "LaunchFlashGqaForwardBf16KernelStrided",
                           "LaunchFlashGqaBackwardBf16Kernel", "LaunchFlashSwaForwardBf16Kernel",
+                          "LaunchFlashSwaBackwardBf16Kernel",
                           "LaunchFlashMlaForwardBf16Kernel", "LaunchFlashSgqaForwardBf16Kernel"}
     for d in decls:
         assert re.search(rf"\bT {d}\(", syms), d
@@ -314,7 +315,8 @@ def _backward_args(**kw):
     B, Sq, Skv, Hq, Hkv, D = (kw.get(n, d) for n, d in
                               (("B", 1), ("Sq", 256), ("Skv", 256), ("Hq", 16), ("Hkv", 1), ("D", 128)))
     a.batch, a.seqlen_q, a.seqlen_kv, a.num_q_heads, a.num_kv_heads, a.head_dim = B, Sq, Skv, Hq, Hkv, D
-    a.causal = 1
+    a.causal = kw.get("causal", 1)
+    a.window_size = kw.get("window", 0)
     a.scale = kw.get("scale", D ** -0.5)
     for name in ("q_stride", "o_stride", "grad_o_stride", "grad_q_stride"):
         getattr(a, name)[:] = [Sq * Hq * D, Hq * D, D]
@@ -333,6 +335,8 @@ def _backward_args(**kw):
     (dict(lse=None), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(grad_k=None), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(grad_v=4096 + 4), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(window=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(window=64, causal=0), _lib.FGQA_ERR_INVALID_ARGUMENT),   # the window is causal only
 ])
 def test_backward_rejects_before_launch(kw, code):
     assert _lib.lib().fgqa_prefill_backward_bf16(ctypes.byref(_backward_args(**kw)), None) == code
@@ -384,6 +388,31 @@ def test_backward_mirror_validation_without_gpu():
         f(q, k, k, q, lse[:, :, :32], q)
     with pytest.raises(ValueError, match="GPU"):
         f(q, k, k, q, lse, q)
+
+
+def test_swa_backward_mirror_validation_without_gpu():
+    """The SWA backward mirror raises the reference's ValueErrors
+    (SWA/flash_swa_backward_kernel.py:370-420) before touching a GPU."""
+    import torch
+    bf = torch.bfloat16
+    q = torch.zeros(2, 4, 64, 128, dtype=bf)
+    k = torch.zeros(2, 2, 64, 128, dtype=bf)
+    lse = torch.zeros(2, 4, 64, dtype=torch.float32)
+    f = fg.launch_flash_swa_backward_bf16_kernel
+    with pytest.raises(ValueError, match="Flash SWA backward expects bf16 inputs and grad_o"):
+        f(q, k, k, q, lse, q.half(), window_size=16)
+    with pytest.raises(ValueError, match="Flash SWA backward expects lse to be float32"):
+        f(q, k, k, q, lse.double(), q, window_size=16)
+    with pytest.raises(ValueError, match="matching ranks"):
+        f(q, k[0], k, q, lse, q, window_size=16)
+    with pytest.raises(ValueError, match="LSE must have shape"):
+        f(q, k, k, q, lse[:, :, :32], q, window_size=16)
+    with pytest.raises(ValueError, match="window_size must be provided"):
+        f(q, k, k, q, lse, q)
+    with pytest.raises(ValueError, match="window_size must be positive"):
+        f(q, k, k, q, lse, q, window_size=0)
+    with pytest.raises(ValueError, match="GPU"):
+        f(q, k, k, q, lse, q, window_size=16)
 
 
 def _paged_args(**kw):

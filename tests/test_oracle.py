@@ -803,3 +803,79 @@ def test_sparse_oracle_closed_forms():
             ref = (wa * vf[0, 0, 0] + wb * vf[0, i, 0]) / (wa + wb)
             assert np.max(np.abs(oracle.bf16_to_f32(o2[0, i, h]) - ref)) < 1e-2
             assert abs(lse2[0, h, i] - (m + math.log(wa + wb))) < 1e-4
+
+
+# ----------------------------------------------------------------- sliding-window backward oracle
+def _loss_swa_numpy_f64(qf, kf, vf, wf, scale, window, sink):
+    """sum(O * W) for float64 causal sliding-window attention with a per-head
+    sink in the denominator (numpy only, BSHD)."""
+    B, Sq, Hq, D = qf.shape
+    Skv, Hkv = kf.shape[1], kf.shape[2]
+    G = Hq // Hkv
+    ii, jj = np.meshgrid(np.arange(Sq), np.arange(Skv), indexing="ij")
+    vis = (jj <= ii) & (jj > ii - window)
+    tot = 0.0
+    for b in range(B):
+        for h in range(Hq):
+            s = np.where(vis, qf[b, :, h] @ kf[b, :, h // G].T * scale, -np.inf)
+            for i in range(Sq):
+                if not vis[i].any():
+                    continue
+                m = s[i].max()
+                e = np.exp(s[i] - m)
+                den = e.sum() + (0.0 if sink is None else float(sink[h]) * math.exp(-m))
+                tot += float(((e / den) @ vf[b, :, h // G]) @ wf[b, i, h])
+    return tot
+
+
+@pytest.mark.parametrize("window,with_sink", [(3, True), (2, False), (10, True)])
+def test_swa_backward_f64_matches_finite_differences(window, with_sink):
+    B, S, Hq, Hkv, D = 1, 6, 4, 2, 8
+    q, k, v, do = _bwd_inputs(61 + window, B, S, S, Hq, Hkv, D=D)
+    sink = np.array([0.5, 2.0, 0.1, 4.0], dtype=np.float32) if with_sink else None
+    dq, dk, dv = oracle.attention_backward_f64(q, k, v, do, 0.3, causal=True, window=window, sink=sink)
+    f = [oracle.bf16_to_f32(x).astype(np.float64) for x in (q, k, v, do)]
+    eps = 1e-5
+    for which, grad in ((0, dq), (1, dk), (2, dv)):
+        base = f[which]
+        num = np.zeros_like(base)
+        for idx in np.ndindex(base.shape):
+            old = base[idx]
+            base[idx] = old + eps
+            lp = _loss_swa_numpy_f64(f[0], f[1], f[2], f[3], 0.3, window, sink)
+            base[idx] = old - eps
+            lm = _loss_swa_numpy_f64(f[0], f[1], f[2], f[3], 0.3, window, sink)
+            base[idx] = old
+            num[idx] = (lp - lm) / (2 * eps)
+        assert np.allclose(grad, num, rtol=1e-6, atol=1e-7), (which, np.abs(grad - num).max())
+
+
+def test_swa_backward_oracle_reduces_to_causal_backward():
+    """A window covering the sequence: the causal backward oracle, bit for bit."""
+    q, k, v, do = _bwd_inputs(63, 1, 90, 90, 4, 2)
+    o, lse = oracle.prefill(q, k, v, SCALE, causal=True)
+    ref = oracle.prefill_backward(q, k, v, o, lse, do, SCALE, causal=True)
+    got = oracle.prefill_backward(q, k, v, o, lse, do, SCALE, causal=True, window=90)
+    for a, b in zip(ref, got):
+        assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("window,with_sink", [(16, True), (1, True), (40, False)])
+def test_swa_backward_oracle_vs_f64(window, with_sink):
+    B, S, Hq, Hkv = 1, 120, 8, 2
+    q, k, v, do = _bwd_inputs(65 + window, B, S, S, Hq, Hkv)
+    sink = (np.linspace(0.2, 3.0, Hq).astype(np.float32)) if with_sink else None
+    o, lse = oracle.prefill_swa(q, k, v, SCALE, window, sink)
+    dq, dk, dv = oracle.prefill_backward(q, k, v, o, lse, do, SCALE, causal=True, window=window)
+    eq, ek, ev = oracle.attention_backward_f64(q, k, v, do, SCALE, causal=True, o=o, window=window, sink=sink)
+    for name, got, ref in (("dq", dq, eq), ("dk", dk, ek), ("dv", dv, ev)):
+        rounded = oracle.bf16_to_f32(oracle.f32_to_bf16(got))
+        assert_grad_close(rounded, ref, f"swa backward oracle {name} vs f64", ORACLE_GRAD_REL, ORACLE_GRAD_MEAN)
+    # planted mistakes: window off by one; the LSE of the forward without its sink
+    if window > 1:
+        bq, bk, bv = oracle.prefill_backward(q, k, v, o, lse, do, SCALE, causal=True, window=window + 1)
+        assert not grad_within_tol(oracle.bf16_to_f32(oracle.f32_to_bf16(bk)), ek, ORACLE_GRAD_REL, ORACLE_GRAD_MEAN)
+    if with_sink:
+        _, lse_nosink = oracle.prefill_swa(q, k, v, SCALE, window, None)
+        bq, bk, bv = oracle.prefill_backward(q, k, v, o, lse_nosink, do, SCALE, causal=True, window=window)
+        assert not grad_within_tol(oracle.bf16_to_f32(oracle.f32_to_bf16(bv)), ev, ORACLE_GRAD_REL, ORACLE_GRAD_MEAN)
