@@ -395,7 +395,7 @@ def bench_swa_backward(steps, warmup, dev, window=512):
     do = _normal((B, S, Hq, 128), 18, 1.0, dev)
     sink = torch.rand(Hq, generator=torch.Generator().manual_seed(19)).to(dev) + 1e-6
     out, lse = fg.flash_gqa_forward_bshd(q, k, v, SCALE, causal=True, window_size=window, sink=sink)
-    n_ws = fg.backward_workspace_bytes(B, S, S, Hq, Hkv)
+    n_ws = fg.backward_workspace_bytes(B, S, S, Hq, Hkv, window_size=window)
     ws = torch.empty(max(n_ws, 256), dtype=torch.uint8, device=dev)
     step = fg.prepare_backward(q, k, v, out, lse, do, SCALE, causal=True, workspace=ws, window_size=window)
     total_ms, per = _time_calls(step, steps, warmup)

@@ -724,15 +724,18 @@ int validate_backward_pointers(const fgqa_prefill_backward_args* a) {
 // Query heads per dK/dV workgroup: all G query heads of a KV head (dK/dV
 // written once, straight from registers) unless that leaves fewer than 2
 // workgroups per CU; then the heads are split over workgroups, each writing
-// an fp32 partial that bwd_dkdv_reduce_kernel sums.  FGQA_BWD_HSPLIT=<n>
+// an fp32 partial that bwd_dkdv_reduce_kernel sums.  Under a sliding window
+// every key block carries the same work, so one workgroup per CU (the
+// kernel's occupancy) is enough and halves the partials.  FGQA_BWD_HSPLIT=<n>
 // forces n (a divisor of G) for tests.
 BwdPlan plan_backward(const fgqa_prefill_backward_args* a, int cus) {
     BwdPlan pl;
     const int group = a->num_q_heads / a->num_kv_heads;
     const int64_t base = ceil_div(a->seqlen_kv, kKvKeys) * (int64_t)a->num_kv_heads * a->batch;
+    const int64_t want = (a->window_size > 0 ? 1 : 2) * (int64_t)cus;
     pl.n_hsplit = group;
     for (int d = 1; d <= group; ++d)
-        if (group % d == 0 && base * d >= 2 * (int64_t)cus) {
+        if (group % d == 0 && base * d >= want) {
             pl.n_hsplit = d;
             break;
         }
@@ -843,10 +846,12 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
         return FGQA_ERR_UNSUPPORTED;
 
     // Few dQ units (fewer than 4 per CU): split each unit's key range over two
-    // wave groups, as the forward does.  FGQA_BWD_DQ_SPLIT=0/1 forces the choice.
-    bool dq_split = q_units < 4 * (int64_t)cus;
-    if (const char* e = getenv("FGQA_BWD_DQ_SPLIT")) dq_split = e[0] == '1';
+    // wave groups, as the forward does.  Under a sliding window the units
+    // carry about the same number of tiles, so there is nothing to balance and
+    // the whole-range kernel is faster.  FGQA_BWD_DQ_SPLIT=0/1 forces the choice.
     const bool swa = p.window > 0;
+    bool dq_split = q_units < 4 * (int64_t)cus && !swa;
+    if (const char* e = getenv("FGQA_BWD_DQ_SPLIT")) dq_split = e[0] == '1';
     // kernel table: [swa] of dK/dV, dQ, split dQ
     const void* kv_fn[2] = {reinterpret_cast<const void*>(bwd_dkdv_kernel<false>),
                             reinterpret_cast<const void*>(bwd_dkdv_kernel<true>)};

@@ -579,12 +579,16 @@ def _backward_args(q, k, v, o, lse, grad_o, dq, dk, dv, scale, causal, layout, w
     return a
 
 
-def backward_workspace_bytes(batch, seqlen_q, seqlen_kv, num_q_heads, num_kv_heads, head_dim=128) -> int:
+def backward_workspace_bytes(batch, seqlen_q, seqlen_kv, num_q_heads, num_kv_heads, head_dim=128,
+                             window_size=0) -> int:
     """Bytes of scratch ``flash_gqa_backward_bshd`` needs for a caller workspace
-    (256-byte aligned; depends on the current device's CU count)."""
+    (256-byte aligned; depends on the current device's CU count and on the
+    window: a sliding-window backward needs at most the causal one's)."""
     a = _lib.BackwardArgs()
     a.batch, a.seqlen_q, a.seqlen_kv = batch, seqlen_q, seqlen_kv
     a.num_q_heads, a.num_kv_heads, a.head_dim = num_q_heads, num_kv_heads, head_dim
+    a.causal = 1
+    a.window_size = int(window_size)
     a.scale = 1.0
     qs = [seqlen_q * num_q_heads * head_dim, num_q_heads * head_dim, head_dim]
     ks = [seqlen_kv * num_kv_heads * head_dim, num_kv_heads * head_dim, head_dim]

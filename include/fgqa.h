@@ -248,7 +248,8 @@ typedef struct fgqa_prefill_backward_args {
     int32_t window_size;
 } fgqa_prefill_backward_args;
 
-/* Bytes of workspace fgqa_prefill_backward_bf16 needs (pointers unused). */
+/* Bytes of workspace fgqa_prefill_backward_bf16 needs (pointers unused; the
+ * sizes, causal and window_size decide it). */
 int fgqa_prefill_backward_workspace_bytes(const fgqa_prefill_backward_args* args, size_t* bytes);
 
 int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* args, void* stream);

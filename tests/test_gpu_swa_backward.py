@@ -122,8 +122,11 @@ def test_swa_backward_dq_whole_and_split_kernels(cuda, monkeypatch, split, B, S,
     _check(_gpu_backward(cuda, q, k, v, o, lse, do, window), refs, what)
 
 
-def test_swa_backward_window_past_sequence_equals_causal_without_sink(cuda):
-    """A window at least the sequence length and no sink is the causal backward."""
+def test_swa_backward_window_past_sequence_equals_causal_without_sink(cuda, monkeypatch):
+    """A window at least the sequence length and no sink is the causal backward
+    (bit for bit, with the same work split: the plans differ by default)."""
+    monkeypatch.setenv("FGQA_BWD_HSPLIT", "2")
+    monkeypatch.setenv("FGQA_BWD_DQ_SPLIT", "1")
     print("swa backward == causal backward", flush=True)
     q, k, v, o, lse, do = _inputs(1600, 1, 256, 256, 8, 2, 256, with_sink=False)
     g_w = _gpu_backward(cuda, q, k, v, o, lse, do, 256)
@@ -211,6 +214,29 @@ def test_swa_backward_reference_shape_full_size(cuda):
     dk_expect = SCALE * ((p * delta)[..., None] * qd).sum(dim=(1, 2))
     dk_sum = dk.double().sum(1)[:, 0]
     assert float((dk_sum - dk_expect).abs().max()) < 5e-3 * float(dk.double().abs().sum(1).mean())
+
+
+def test_swa_backward_caller_workspace(cuda):
+    """A caller workspace sized for the window (at most the causal size; one
+    byte short is rejected), and the gradients it gives."""
+    import torch
+    fg = _fg()
+    print("swa backward caller workspace", flush=True)
+    B, S, Hq, Hkv, W = 1, 384, 16, 1, 96
+    q, k, v, o, lse, do = _inputs(1660, B, S, S, Hq, Hkv, W)
+    refs = oracle.prefill_backward(q, k, v, o, lse, do, SCALE, causal=True, window=W)
+    n_w = fg.backward_workspace_bytes(B, S, S, Hq, Hkv, window_size=W)
+    n_c = fg.backward_workspace_bytes(B, S, S, Hq, Hkv)
+    assert 0 < n_w <= n_c
+    qd, kd, vd, od, dod = (to_torch_bf16(x, cuda) for x in (q, k, v, o, do))
+    lsed = torch.from_numpy(lse).to(cuda)
+    small = torch.empty(n_w - 1, dtype=torch.uint8, device=cuda)
+    with pytest.raises(fg.FgqaError):
+        fg.flash_gqa_backward_bshd(qd, kd, vd, od, lsed, dod, SCALE, workspace=small, window_size=W)
+    ws = torch.empty(n_w, dtype=torch.uint8, device=cuda)
+    g = fg.flash_gqa_backward_bshd(qd, kd, vd, od, lsed, dod, SCALE, workspace=ws, window_size=W)
+    _sync()
+    _check(tuple(from_torch_bf16(x) for x in g), refs, "swa caller workspace")
 
 
 def test_swa_backward_cplusplus_dropin(cuda):
