@@ -453,3 +453,25 @@ def test_paged_decode_empty_batch_is_noop():
     L = _lib.lib()
     assert L.fgqa_decode_paged(ctypes.byref(_paged_args(B=0, q=None)), None) == 0
     assert L.fgqa_decode_paged(None, None) == _lib.FGQA_ERR_INVALID_ARGUMENT
+
+
+def test_cmake_build_matches_make(tmp_path):
+    """The CMake build (gfx950 only) gives a library with the same exported
+    entry points as the Makefile's, and refuses any other GPU target."""
+    import shutil
+    if shutil.which("cmake") is None or shutil.which("ninja") is None:
+        pytest.skip("cmake / ninja not installed")
+    bad = subprocess.run(["cmake", "-S", ROOT, "-B", str(tmp_path / "bad"), "-G", "Ninja",
+                          "-DCMAKE_HIP_ARCHITECTURES=gfx942"], capture_output=True, text=True)
+    assert bad.returncode != 0 and "gfx950" in (bad.stdout + bad.stderr)
+    b = tmp_path / "build"
+    subprocess.run(["cmake", "-S", ROOT, "-B", str(b), "-G", "Ninja"], check=True, capture_output=True)
+    subprocess.run(["cmake", "--build", str(b), "-j", "8"], check=True, capture_output=True)
+
+    def exports(path):
+        out = subprocess.run(["nm", "-D", "--defined-only", path], check=True, capture_output=True,
+                             text=True).stdout
+        return {line.split()[-1] for line in out.splitlines()
+                if " T " in line and ("fgqa_" in line or "Launch" in line or "FlashGqa" in line)}
+
+    assert exports(str(b / "libfgqa.so")) == exports(_lib.LIB_PATH)
