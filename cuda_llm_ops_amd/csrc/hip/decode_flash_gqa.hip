@@ -664,9 +664,11 @@ extern "C" int fgqa_decode_bf16(const fgqa_decode_args* a, void* stream) {
     p.scale_log2 = a->scale * kLog2e;
 
     int32_t* work = nullptr;
+    std::unique_lock<std::mutex> ws_lock;   // held through the launches when the library's buffer is used
     if (plan.ws_bytes > 0) {
         void* ws = a->workspace;
         if (ws == nullptr && a->workspace_bytes == 0) {
+            ws_lock = workspace_lock();
             ws = internal_workspace(plan.ws_bytes, &st);
             if (st != FGQA_OK) return st;
         } else if (ws == nullptr || a->workspace_bytes < plan.ws_bytes) {
@@ -814,9 +816,11 @@ extern "C" int fgqa_decode_paged(const fgqa_decode_paged_args* a, void* stream) 
     p.v_scale = a->v_scale;
 
     int32_t* work = nullptr;
+    std::unique_lock<std::mutex> ws_lock;   // held through the launches when the library's buffer is used
     if (plan.ws_bytes > 0) {
         void* ws = a->workspace;
         if (ws == nullptr && a->workspace_bytes == 0) {
+            ws_lock = workspace_lock();
             ws = internal_workspace(plan.ws_bytes, &st);
             if (st != FGQA_OK) return st;
         } else if (ws == nullptr || a->workspace_bytes < plan.ws_bytes) {

@@ -1,6 +1,8 @@
 // Host-side internals shared by the flash-GQA translation units.
 #pragma once
 
+#include <mutex>
+
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -14,10 +16,16 @@ namespace fgqa {
 int device_cu_count();
 
 // Library-owned, per-device, grow-only scratch buffer used when a caller
-// passes no workspace.  Allocation happens on first use (or growth) under a
-// mutex; the returned pointer stays valid until the next growth.  Returns
-// nullptr and sets *status on failure.
+// passes no workspace.  The caller holds workspace_lock() from this call until
+// its kernels are launched: growth frees the old buffer (after draining the
+// device), so another thread must not grow it in between.  Returns nullptr
+// and sets *status on failure.
+std::unique_lock<std::mutex> workspace_lock();
 void* internal_workspace(size_t bytes, int* status);
+
+// Sets a kernel's dynamic-LDS limit once per device (the attribute is per
+// kernel and per device).  slot: a distinct small index per kernel.
+int set_kernel_smem_once(int slot, const void* fn, int bytes);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

@@ -9,8 +9,11 @@ namespace fgqa {
 
 namespace {
 constexpr int kMaxDevices = 64;
-std::mutex g_mutex;
+std::mutex g_mutex;      // device properties and kernel attributes
+std::mutex g_ws_mutex;   // the library-owned workspaces
 int g_cu_count[kMaxDevices] = {0};
+constexpr int kMaxKernelSlots = 32;
+bool g_smem_set[kMaxDevices][kMaxKernelSlots] = {};
 void* g_ws_ptr[kMaxDevices] = {nullptr};
 size_t g_ws_bytes[kMaxDevices] = {0};
 }  // namespace
@@ -27,13 +30,27 @@ int device_cu_count() {
     return g_cu_count[dev];
 }
 
+int set_kernel_smem_once(int slot, const void* fn, int bytes) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return FGQA_ERR_HIP;
+    if (dev < 0 || dev >= kMaxDevices || slot < 0 || slot >= kMaxKernelSlots) return FGQA_ERR_UNSUPPORTED;
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (!g_smem_set[dev][slot]) {
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess)
+            return FGQA_ERR_HIP;
+        g_smem_set[dev][slot] = true;
+    }
+    return FGQA_OK;
+}
+
+std::unique_lock<std::mutex> workspace_lock() { return std::unique_lock<std::mutex>(g_ws_mutex); }
+
 void* internal_workspace(size_t bytes, int* status) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
         *status = FGQA_ERR_HIP;
         return nullptr;
     }
-    std::lock_guard<std::mutex> lock(g_mutex);
     if (g_ws_bytes[dev] < bytes) {
         // Work already queued on any stream may still read the old buffer, so
         // drain the device before releasing it.

@@ -751,15 +751,6 @@ BwdPlan plan_backward(const fgqa_prefill_backward_args* a, int cus) {
     return pl;
 }
 
-int set_smem(const void* fn, int bytes, bool* done) {
-    if (!*done) {
-        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess)
-            return FGQA_ERR_HIP;
-        *done = true;
-    }
-    return FGQA_OK;
-}
-
 }  // namespace
 }  // namespace fgqa
 
@@ -786,7 +777,9 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     const BwdPlan pl = plan_backward(a, cus);
 
     unsigned char* ws = static_cast<unsigned char*>(a->workspace);
+    std::unique_lock<std::mutex> ws_lock;   // held through the launches when the library's buffer is used
     if (ws == nullptr) {
+        ws_lock = workspace_lock();
         ws = static_cast<unsigned char*>(internal_workspace(pl.ws_bytes, &st));
         if (ws == nullptr) return st;
     } else if (a->workspace_bytes < pl.ws_bytes) {
@@ -859,10 +852,10 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
                            reinterpret_cast<const void*>(bwd_dq_kernel<true>)};
     const void* q2_fn[2] = {reinterpret_cast<const void*>(bwd_dq_split_kernel<false>),
                             reinterpret_cast<const void*>(bwd_dq_split_kernel<true>)};
-    static bool smem_kv[2] = {}, smem_q[2] = {}, smem_q2[2] = {};
-    if ((st = set_smem(kv_fn[swa], kKvSmemBytes, &smem_kv[swa])) != FGQA_OK) return st;
-    if ((st = set_smem(q_fn[swa], kDqSmemBytes, &smem_q[swa])) != FGQA_OK) return st;
-    if ((st = set_smem(q2_fn[swa], 2 * kDqSmemBytes, &smem_q2[swa])) != FGQA_OK) return st;
+    // attribute slots 10..15: the backward kernels
+    if ((st = set_kernel_smem_once(10 + swa, kv_fn[swa], kKvSmemBytes)) != FGQA_OK) return st;
+    if ((st = set_kernel_smem_once(12 + swa, q_fn[swa], kDqSmemBytes)) != FGQA_OK) return st;
+    if ((st = set_kernel_smem_once(14 + swa, q2_fn[swa], 2 * kDqSmemBytes)) != FGQA_OK) return st;
 
     if (rows_q > 0) hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)ceil_div(rows_q, 16)), dim3(256), 0, s, p);
     if (kv_units > 0) {

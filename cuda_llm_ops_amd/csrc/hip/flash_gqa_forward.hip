@@ -613,17 +613,8 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
                           reinterpret_cast<const void*>(prefill_split_kernel<128>),
                           reinterpret_cast<const void*>(prefill_kernel<false, 192>),
                           reinterpret_cast<const void*>(prefill_split_kernel<192>)};
-    // The attribute is per kernel and per device: set it once per device.
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return FGQA_ERR_HIP;
-    constexpr int kMaxDev = 64;
-    static bool smem_set[kMaxDev][5] = {};
-    if (dev < 0 || dev >= kMaxDev) return FGQA_ERR_UNSUPPORTED;
-    if (!smem_set[dev][which]) {
-        if (hipFuncSetAttribute(fns[which], hipFuncAttributeMaxDynamicSharedMemorySize, smem_bytes) != hipSuccess)
-            return FGQA_ERR_HIP;
-        smem_set[dev][which] = true;
-    }
+    // attribute slots 0..4: the prefill kernels
+    if (const int e = set_kernel_smem_once(which, fns[which], smem_bytes); e != FGQA_OK) return e;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const dim3 grid((unsigned)units);
     switch (which) {

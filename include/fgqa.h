@@ -54,7 +54,10 @@ enum fgqa_status {
  *   split_tokens  KV tokens per split (rounded up to 128); 0 = automatic.
  *   workspace / workspace_bytes  device scratch of at least
  *            fgqa_decode_workspace_bytes(); pass NULL/0 to let the library use
- *            its own per-device cached buffer (allocated on first use).
+ *            its own per-device cached buffer (allocated on first use).  Calls
+ *            that share that buffer must not run at the same time on the GPU:
+ *            concurrent calls on different streams of one device each pass
+ *            their own workspace.  (Host threads may call concurrently.)
  */
 typedef struct fgqa_decode_args {
     const void* q;
@@ -209,7 +212,8 @@ int fgqa_prefill_bf16(const fgqa_prefill_args* args, void* stream);
  * rounded to bf16 once.
  * workspace / workspace_bytes  device scratch of at least
  *   fgqa_prefill_backward_workspace_bytes() bytes, 256-byte aligned; NULL/0
- *   uses the library's per-device cached buffer.
+ *   uses the library's per-device cached buffer (same rule as for decode:
+ *   concurrent calls on different streams each pass their own workspace).
  * window_size  0: none.  > 0 (causal only): the sliding-window backward,
  *   replacing the Triton-only launch_flash_swa_backward_bf16_kernel,
  *   reference src/python/Triton/SWA/flash_swa_backward_kernel.py:323-489
