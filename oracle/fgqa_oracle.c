@@ -480,7 +480,7 @@ typedef struct {
     const float *lse, *delta;
     const int64_t *qs, *ks, *vs, *dos;
     float scale;
-    int sq, hq, d, group;
+    int sq, hq, d, dv, group;   /* d: Q/K row length, dv: V/O row length */
 } bwd_ctx;
 
 /* :253-285 for query row i of head h and key j of batch b: returns p (fp32)
@@ -493,23 +493,27 @@ static float bwd_pair(const bwd_ctx* c, int b, int h, int i, int j, float* ds) {
     const uint16_t* dorow = c->grad_o + b * c->dos[0] + (int64_t)i * c->dos[1] + h * c->dos[2];
     float s = 0.f, dp = 0.f;
     for (int x = 0; x < c->d; ++x) s += bf(qrow[x]) * bf(krow[x]);
-    for (int x = 0; x < c->d; ++x) dp += bf(dorow[x]) * bf(vrow[x]);
+    for (int x = 0; x < c->dv; ++x) dp += bf(dorow[x]) * bf(vrow[x]);
     const size_t r = ((size_t)b * c->hq + h) * c->sq + i;
     const float p = expf(s * c->scale - c->lse[r]);
     *ds = bf(fgqa_oracle_f32_to_bf16(p * (dp - c->delta[r]) * c->scale));
     return p;
 }
 
+/* d: Q/K row length; dvd: V/O/dO row length (the MLA backward has d = 192,
+ * dvd = 128; the GQA backward d = dvd).  dq, dk have d-element rows, dv
+ * dvd-element rows. */
 static int backward_core(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                          const uint16_t* o, const float* lse, const uint16_t* grad_o,
                          float scale, float* dq, float* dk, float* dv,
-                         int batch, int sq, int skv, int hq, int hkv, int d,
+                         int batch, int sq, int skv, int hq, int hkv, int d, int dvd,
                          const int64_t* qs, const int64_t* ks,
                          const int64_t* vs, const int64_t* os,
                          const int64_t* dos, int causal, int window,
                          const int* rows, const int* keys, int nthreads) {
     if (!q || !k || !v || !o || !lse || !grad_o || !qs || !ks || !vs || !os || !dos) return -1;
     if (batch < 0 || sq < 0 || skv < 0 || hq <= 0 || hkv <= 0 || d <= 0 || d > ORACLE_MAX_D) return -1;
+    if (dvd <= 0 || dvd > ORACLE_MAX_D) return -1;
     if (hq % hkv != 0 || window < 0 || (window > 0 && !causal)) return -1;
     const int group = hq / hkv;
     const int r0 = rows ? rows[0] : 0, r1 = rows ? rows[1] : sq;
@@ -528,11 +532,11 @@ static int backward_core(const uint16_t* q, const uint16_t* k, const uint16_t* v
                 const uint16_t* orow = o + b * os[0] + (int64_t)i * os[1] + h * os[2];
                 const uint16_t* dorow = grad_o + b * dos[0] + (int64_t)i * dos[1] + h * dos[2];
                 float acc = 0.f;
-                for (int x = 0; x < d; ++x) acc += bf(orow[x]) * bf(dorow[x]);
+                for (int x = 0; x < dvd; ++x) acc += bf(orow[x]) * bf(dorow[x]);
                 delta[((size_t)b * hq + h) * sq + i] = acc;
             }
 
-    bwd_ctx c = {q, k, v, grad_o, lse, delta, qs, ks, vs, dos, scale, sq, hq, d, group};
+    bwd_ctx c = {q, k, v, grad_o, lse, delta, qs, ks, vs, dos, scale, sq, hq, d, dvd, group};
 
     /* :292-293 dQ_i = sum_j dS_ij k_j over the keys row i sees */
     if (dq) {
@@ -564,7 +568,8 @@ static int backward_core(const uint16_t* q, const uint16_t* k, const uint16_t* v
             for (int kvh = 0; kvh < hkv; ++kvh)
                 for (int j = k0; j < k1; ++j) {
                     float ak[ORACLE_MAX_D], av[ORACLE_MAX_D];
-                    for (int x = 0; x < d; ++x) ak[x] = av[x] = 0.f;
+                    for (int x = 0; x < d; ++x) ak[x] = 0.f;
+                    for (int x = 0; x < dvd; ++x) av[x] = 0.f;
                     const int ibeg = causal ? j : 0;
                     const int iend = (window > 0 && j + window < sq) ? j + window : sq;
                     for (int h = kvh * group; h < (kvh + 1) * group; ++h)
@@ -573,16 +578,14 @@ static int backward_core(const uint16_t* q, const uint16_t* k, const uint16_t* v
                             const float pb = bf(fgqa_oracle_f32_to_bf16(bwd_pair(&c, b, h, i, j, &ds)));
                             const uint16_t* qrow = q + b * qs[0] + (int64_t)i * qs[1] + h * qs[2];
                             const uint16_t* dorow = grad_o + b * dos[0] + (int64_t)i * dos[1] + h * dos[2];
-                            for (int x = 0; x < d; ++x) {
-                                ak[x] += ds * bf(qrow[x]);
-                                av[x] += pb * bf(dorow[x]);
-                            }
+                            for (int x = 0; x < d; ++x) ak[x] += ds * bf(qrow[x]);
+                            for (int x = 0; x < dvd; ++x) av[x] += pb * bf(dorow[x]);
                         }
-                    const size_t base = (((size_t)b * skv + j) * hkv + kvh) * d;
+                    const size_t row = ((size_t)b * skv + j) * hkv + kvh;
                     if (dk)
-                        for (int x = 0; x < d; ++x) dk[base + x] = ak[x];
+                        for (int x = 0; x < d; ++x) dk[row * d + x] = ak[x];
                     if (dv)
-                        for (int x = 0; x < d; ++x) dv[base + x] = av[x];
+                        for (int x = 0; x < dvd; ++x) dv[row * dvd + x] = av[x];
                 }
     }
     free(delta);
@@ -597,8 +600,26 @@ int fgqa_oracle_prefill_backward_bf16(const uint16_t* q, const uint16_t* k, cons
                                       const int64_t* vs, const int64_t* os,
                                       const int64_t* dos, int causal,
                                       const int* rows, const int* keys, int nthreads) {
-    return backward_core(q, k, v, o, lse, grad_o, scale, dq, dk, dv, batch, sq, skv, hq, hkv, d, qs, ks, vs, os,
+    return backward_core(q, k, v, o, lse, grad_o, scale, dq, dk, dv, batch, sq, skv, hq, hkv, d, d, qs, ks, vs, os,
                          dos, causal, 0, rows, keys, nthreads);
+}
+
+/*
+ * MLA backward (Q/K rows of dqk, V/O/dO rows of dv), restating
+ * src/python/Triton/flash_mla_backward_kernel.py: the steps of the GQA
+ * backward above with the scores over dqk (:366-372) and dP, delta over dv
+ * (:388, :16-50).  dq, dk: dqk-element rows; dv: dv-element rows.
+ */
+int fgqa_oracle_prefill_mla_backward_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                          const uint16_t* o, const float* lse, const uint16_t* grad_o,
+                                          float scale, float* dq, float* dk, float* dv,
+                                          int batch, int sq, int skv, int hq, int hkv, int dqk, int dvd,
+                                          const int64_t* qs, const int64_t* ks,
+                                          const int64_t* vs, const int64_t* os,
+                                          const int64_t* dos, int causal,
+                                          const int* rows, const int* keys, int nthreads) {
+    return backward_core(q, k, v, o, lse, grad_o, scale, dq, dk, dv, batch, sq, skv, hq, hkv, dqk, dvd, qs, ks, vs,
+                         os, dos, causal, 0, rows, keys, nthreads);
 }
 
 /*
@@ -616,7 +637,7 @@ int fgqa_oracle_prefill_swa_backward_bf16(const uint16_t* q, const uint16_t* k, 
                                           const int64_t* dos, int window,
                                           const int* rows, const int* keys, int nthreads) {
     if (window <= 0) return -1;
-    return backward_core(q, k, v, o, lse, grad_o, scale, dq, dk, dv, batch, sq, skv, hq, hkv, d, qs, ks, vs, os,
+    return backward_core(q, k, v, o, lse, grad_o, scale, dq, dk, dv, batch, sq, skv, hq, hkv, d, d, qs, ks, vs, os,
                          dos, 1, window, rows, keys, nthreads);
 }
 
@@ -626,20 +647,20 @@ int fgqa_oracle_prefill_swa_backward_bf16(const uint16_t* q, const uint16_t* k, 
 static int attention_backward_f64_core(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                        const uint16_t* o, const uint16_t* grad_o, double scale,
                                        double* dq, double* dk, double* dv,
-                                       int batch, int sq, int skv, int hq, int hkv, int d,
+                                       int batch, int sq, int skv, int hq, int hkv, int d, int dvd,
                                        const int64_t* qs, const int64_t* ks,
                                        const int64_t* vs, const int64_t* os,
                                        const int64_t* dos, int causal, int window, const float* sink,
                                        int nthreads) {
     if (!q || !k || !v || !grad_o || !dq || !dk || !dv || !qs || !ks || !vs || !dos) return -1;
     if (o && !os) return -1;
-    if (batch < 0 || sq < 0 || skv < 0 || hq <= 0 || hkv <= 0 || d <= 0) return -1;
+    if (batch < 0 || sq < 0 || skv < 0 || hq <= 0 || hkv <= 0 || d <= 0 || dvd <= 0) return -1;
     if (hq % hkv != 0 || window < 0 || (window > 0 && !causal)) return -1;
     const int group = hq / hkv;
     set_threads(nthreads);
     memset(dq, 0, sizeof(double) * (size_t)batch * sq * hq * d);
     memset(dk, 0, sizeof(double) * (size_t)batch * skv * hkv * d);
-    memset(dv, 0, sizeof(double) * (size_t)batch * skv * hkv * d);
+    memset(dv, 0, sizeof(double) * (size_t)batch * skv * hkv * dvd);
 
     /* One (batch, kv head) per task: its dK/dV rows are private to it. */
 #pragma omp parallel for collapse(2) schedule(dynamic, 1)
@@ -673,26 +694,26 @@ static int attention_backward_f64_core(const uint16_t* q, const uint16_t* k, con
                         p[j] /= sum;
                         const uint16_t* vrow = v + b * vs[0] + (int64_t)j * vs[1] + kvh * vs[2];
                         double acc = 0.0;
-                        for (int x = 0; x < d; ++x) acc += (double)bf(dorow[x]) * (double)bf(vrow[x]);
+                        for (int x = 0; x < dvd; ++x) acc += (double)bf(dorow[x]) * (double)bf(vrow[x]);
                         dp[j] = acc;
                         delta += p[j] * acc;
                     }
                     if (o) {
                         const uint16_t* orow = o + b * os[0] + (int64_t)i * os[1] + h * os[2];
                         delta = 0.0;
-                        for (int x = 0; x < d; ++x) delta += (double)bf(orow[x]) * (double)bf(dorow[x]);
+                        for (int x = 0; x < dvd; ++x) delta += (double)bf(orow[x]) * (double)bf(dorow[x]);
                     }
                     double* dqrow = dq + (((size_t)b * sq + i) * hq + h) * d;
                     for (int j = j0; j < nvis; ++j) {
                         const double ds = p[j] * (dp[j] - delta) * scale;
                         const uint16_t* krow = k + b * ks[0] + (int64_t)j * ks[1] + kvh * ks[2];
                         double* dkrow = dk + (((size_t)b * skv + j) * hkv + kvh) * d;
-                        double* dvrow = dv + (((size_t)b * skv + j) * hkv + kvh) * d;
+                        double* dvrow = dv + (((size_t)b * skv + j) * hkv + kvh) * dvd;
                         for (int x = 0; x < d; ++x) {
                             dqrow[x] += ds * (double)bf(krow[x]);
                             dkrow[x] += ds * (double)bf(qrow[x]);
-                            dvrow[x] += p[j] * (double)bf(dorow[x]);
                         }
+                        for (int x = 0; x < dvd; ++x) dvrow[x] += p[j] * (double)bf(dorow[x]);
                     }
                 }
             free(p);
@@ -708,8 +729,19 @@ int fgqa_oracle_attention_backward_f64(const uint16_t* q, const uint16_t* k, con
                                        const int64_t* qs, const int64_t* ks,
                                        const int64_t* vs, const int64_t* os,
                                        const int64_t* dos, int causal, int nthreads) {
-    return attention_backward_f64_core(q, k, v, o, grad_o, scale, dq, dk, dv, batch, sq, skv, hq, hkv, d, qs, ks,
+    return attention_backward_f64_core(q, k, v, o, grad_o, scale, dq, dk, dv, batch, sq, skv, hq, hkv, d, d, qs, ks,
                                        vs, os, dos, causal, 0, NULL, nthreads);
+}
+
+int fgqa_oracle_attention_mla_backward_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                           const uint16_t* o, const uint16_t* grad_o, double scale,
+                                           double* dq, double* dk, double* dv,
+                                           int batch, int sq, int skv, int hq, int hkv, int dqk, int dvd,
+                                           const int64_t* qs, const int64_t* ks,
+                                           const int64_t* vs, const int64_t* os,
+                                           const int64_t* dos, int causal, int nthreads) {
+    return attention_backward_f64_core(q, k, v, o, grad_o, scale, dq, dk, dv, batch, sq, skv, hq, hkv, dqk, dvd, qs,
+                                       ks, vs, os, dos, causal, 0, NULL, nthreads);
 }
 
 int fgqa_oracle_attention_swa_backward_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v,
@@ -720,7 +752,7 @@ int fgqa_oracle_attention_swa_backward_f64(const uint16_t* q, const uint16_t* k,
                                            const int64_t* vs, const int64_t* os,
                                            const int64_t* dos, int window, const float* sink, int nthreads) {
     if (window <= 0) return -1;
-    return attention_backward_f64_core(q, k, v, o, grad_o, scale, dq, dk, dv, batch, sq, skv, hq, hkv, d, qs, ks,
+    return attention_backward_f64_core(q, k, v, o, grad_o, scale, dq, dk, dv, batch, sq, skv, hq, hkv, d, d, qs, ks,
                                        vs, os, dos, 1, window, sink, nthreads);
 }
 

@@ -30,6 +30,11 @@
  *                                            invariants (sum_j dK_j = 0, sum_j dV_j = sum dO)
  *   fgqa_oracle_attention_backward_f64      central finite differences of a float64
  *                                            numpy forward on tiny inputs
+ *   fgqa_oracle_prefill_mla_backward_bf16   bit-identical to fgqa_oracle_prefill_backward_bf16
+ *                                            when dqk = dvd; the float64 MLA gradient below
+ *                                            at the stated tolerance; planted mistakes
+ *   fgqa_oracle_attention_mla_backward_f64  central finite differences of a float64 numpy
+ *                                            forward with dqk != dvd
  *   fgqa_oracle_fp8e4m3_to_f32              all 256 codes against torch.float8_e4m3fn
  *   fgqa_oracle_decode_paged                bit-identical to fgqa_oracle_decode_bf16 on a
  *                                            contiguous bf16 cache; page-permutation
@@ -197,6 +202,32 @@ int fgqa_oracle_attention_backward_f64(const uint16_t* q, const uint16_t* k, con
                                        const int64_t* q_strides, const int64_t* k_strides,
                                        const int64_t* v_strides, const int64_t* o_strides,
                                        const int64_t* grad_o_strides, int causal, int nthreads);
+
+/*
+ * MLA backward, following
+ * src/python/Triton/flash_mla_backward_kernel.py: the steps of
+ * fgqa_oracle_prefill_backward_bf16 with Q/K rows of dqk and V/O/dO rows of
+ * dvd (scores over dqk, dP and delta over dvd).  dq, dk: fp32, dqk-element
+ * rows; dv: fp32, dvd-element rows (BSHD, as fgqa_oracle_prefill_backward_bf16).
+ */
+int fgqa_oracle_prefill_mla_backward_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                          const uint16_t* o, const float* lse, const uint16_t* grad_o,
+                                          float scale, float* dq, float* dk, float* dv,
+                                          int batch, int sq, int skv, int hq, int hkv, int dqk, int dvd,
+                                          const int64_t* qs, const int64_t* ks,
+                                          const int64_t* vs, const int64_t* os,
+                                          const int64_t* dos, int causal,
+                                          const int* rows, const int* keys, int nthreads);
+
+/* The float64 gradient of fgqa_oracle_attention_backward_f64 with separate
+ * Q/K (dqk) and V/O (dvd) row lengths. */
+int fgqa_oracle_attention_mla_backward_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                           const uint16_t* o, const uint16_t* grad_o, double scale,
+                                           double* dq, double* dk, double* dv,
+                                           int batch, int sq, int skv, int hq, int hkv, int dqk, int dvd,
+                                           const int64_t* qs, const int64_t* ks,
+                                           const int64_t* vs, const int64_t* os,
+                                           const int64_t* dos, int causal, int nthreads);
 
 /*
  * Sliding-window backward, restating the reference's Triton SWA backward

@@ -88,6 +88,16 @@ def lib() -> ctypes.CDLL:
             _u16p, _u16p, _u16p, _u16p, _u16p, ctypes.c_double, _f64p, _f64p, _f64p,
             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
             _i64p, _i64p, _i64p, _i64p, _i64p, ctypes.c_int, ctypes.c_int]
+        L.fgqa_oracle_prefill_mla_backward_bf16.restype = ctypes.c_int
+        L.fgqa_oracle_prefill_mla_backward_bf16.argtypes = [
+            _u16p, _u16p, _u16p, _u16p, _f32p, _u16p, ctypes.c_float, _f32p, _f32p, _f32p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            _i64p, _i64p, _i64p, _i64p, _i64p, ctypes.c_int, _i32p, _i32p, ctypes.c_int]
+        L.fgqa_oracle_attention_mla_backward_f64.restype = ctypes.c_int
+        L.fgqa_oracle_attention_mla_backward_f64.argtypes = [
+            _u16p, _u16p, _u16p, _u16p, _u16p, ctypes.c_double, _f64p, _f64p, _f64p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+            _i64p, _i64p, _i64p, _i64p, _i64p, ctypes.c_int, ctypes.c_int]
         L.fgqa_oracle_fp8e4m3_to_f32.restype = ctypes.c_float
         L.fgqa_oracle_fp8e4m3_to_f32.argtypes = [ctypes.c_uint8]
         L.fgqa_oracle_decode_paged.restype = ctypes.c_int
@@ -282,14 +292,17 @@ def prefill_backward(q, k, v, o, lse, grad_o, scale, causal=True, layout="bshd",
     limit which dq rows / dk,dv rows are computed (the others are NaN); an
     output not named in `want` is returned as None.  window > 0 (causal):
     the sliding-window backward (SWA/flash_swa_backward_kernel.py), with the
-    forward's sink-adjusted lse."""
+    forward's sink-adjusted lse.  v/o/grad_o rows narrower than q/k rows (MLA:
+    192 and 128) give the MLA backward (flash_mla_backward_kernel.py); dv then
+    has v's row length."""
     q, k, v, o, grad_o = (np.ascontiguousarray(x, dtype=np.uint16) for x in (q, k, v, o, grad_o))
     lse = np.ascontiguousarray(lse, dtype=np.float32)
     B, Sq, Hq, D = _dims(q, layout)
     _, Skv, Hkv, _ = _dims(k, layout)
+    Dv = v.shape[-1]
     dq = np.full((B, Sq, Hq, D), np.nan, dtype=np.float32) if "dq" in want else None
     dk = np.full((B, Skv, Hkv, D), np.nan, dtype=np.float32) if "dk" in want else None
-    dv = np.full((B, Skv, Hkv, D), np.nan, dtype=np.float32) if "dv" in want else None
+    dv = np.full((B, Skv, Hkv, Dv), np.nan, dtype=np.float32) if "dv" in want else None
     qs, ks, vs, os_, dos = (_strides(x, layout) for x in (q, k, v, o, grad_o))
     rr = None if rows is None else np.array(rows, dtype=np.int32)
     kk = None if keys is None else np.array(keys, dtype=np.int32)
@@ -300,6 +313,14 @@ def prefill_backward(q, k, v, o, lse, grad_o, scale, causal=True, layout="bshd",
             _ptr(qs, ctypes.c_int64), _ptr(ks, ctypes.c_int64), _ptr(vs, ctypes.c_int64),
             _ptr(os_, ctypes.c_int64), _ptr(dos, ctypes.c_int64))
     tail = (_ptr(rr, ctypes.c_int32), _ptr(kk, ctypes.c_int32), int(nthreads))
+    if Dv != D:
+        if window > 0:
+            raise ValueError("prefill_backward: the MLA backward has no window form")
+        args = args[:16] + (Dv,) + args[16:]
+        rc = lib().fgqa_oracle_prefill_mla_backward_bf16(*args, int(bool(causal)), *tail)
+        if rc != 0:
+            raise ValueError("fgqa_oracle_prefill_mla_backward_bf16: invalid arguments")
+        return dq, dk, dv
     if window > 0:
         if not causal:
             raise ValueError("prefill_backward: a window needs causal=True")
@@ -316,14 +337,16 @@ def attention_backward_f64(q, k, v, grad_o, scale, causal=True, o=None, layout="
     """Exact gradient of softmax attention in float64.  o=None: delta from P
     (the true gradient); o given (bf16 bits): delta = sum O*dO as the torch
     reference does.  window > 0 and/or sink (float32 [Hq]): causal
-    sliding-window attention with the sink in the denominator.  Returns
-    (dq [B,Sq,Hq,D], dk, dv [B,Skv,Hkv,D]) float64."""
+    sliding-window attention with the sink in the denominator.  v/grad_o rows
+    narrower than q/k rows: the MLA gradient.  Returns (dq [B,Sq,Hq,D], dk
+    [B,Skv,Hkv,D], dv [B,Skv,Hkv,Dv]) float64."""
     q, k, v, grad_o = (np.ascontiguousarray(x, dtype=np.uint16) for x in (q, k, v, grad_o))
     B, Sq, Hq, D = _dims(q, layout)
     _, Skv, Hkv, _ = _dims(k, layout)
+    Dv = v.shape[-1]
     dq = np.empty((B, Sq, Hq, D), dtype=np.float64)
     dk = np.empty((B, Skv, Hkv, D), dtype=np.float64)
-    dv = np.empty((B, Skv, Hkv, D), dtype=np.float64)
+    dv = np.empty((B, Skv, Hkv, Dv), dtype=np.float64)
     qs, ks, vs, dos = (_strides(x, layout) for x in (q, k, v, grad_o))
     os_ = None
     if o is not None:
@@ -335,6 +358,14 @@ def attention_backward_f64(q, k, v, grad_o, scale, causal=True, o=None, layout="
             B, Sq, Skv, Hq, Hkv, D,
             _ptr(qs, ctypes.c_int64), _ptr(ks, ctypes.c_int64), _ptr(vs, ctypes.c_int64),
             _ptr(os_, ctypes.c_int64), _ptr(dos, ctypes.c_int64))
+    if Dv != D:
+        if window > 0 or sink is not None:
+            raise ValueError("attention_backward_f64: the MLA gradient has no window / sink form")
+        args = args[:15] + (Dv,) + args[15:]
+        rc = lib().fgqa_oracle_attention_mla_backward_f64(*args, int(bool(causal)), int(nthreads))
+        if rc != 0:
+            raise ValueError("fgqa_oracle_attention_mla_backward_f64: invalid arguments")
+        return dq, dk, dv
     if window > 0 or sink is not None:
         if not causal:
             raise ValueError("attention_backward_f64: a window or sink needs causal=True")

@@ -879,3 +879,96 @@ def test_swa_backward_oracle_vs_f64(window, with_sink):
         _, lse_nosink = oracle.prefill_swa(q, k, v, SCALE, window, None)
         bq, bk, bv = oracle.prefill_backward(q, k, v, o, lse_nosink, do, SCALE, causal=True, window=window)
         assert not grad_within_tol(oracle.bf16_to_f32(oracle.f32_to_bf16(bv)), ev, ORACLE_GRAD_REL, ORACLE_GRAD_MEAN)
+
+
+# ----------------------------------------------------------------- MLA backward oracle
+MLA_SCALE = 1.0 / math.sqrt(192)
+
+
+def _mla_bwd_inputs(seed, B, Sq, Skv, Hq, Hkv, dqk=192, dv=128):
+    q = oracle.normal_bf16(seed, (B, Sq, Hq, dqk))
+    k = oracle.normal_bf16(seed, (B, Skv, Hkv, dqk), stream=1)
+    v = oracle.normal_bf16(seed, (B, Skv, Hkv, dv), stream=2)
+    do = oracle.normal_bf16(seed, (B, Sq, Hq, dv), stream=3)
+    return q, k, v, do
+
+
+@pytest.mark.parametrize("causal,sq,skv", [(True, 5, 6), (False, 4, 7)])
+def test_mla_backward_f64_matches_finite_differences(causal, sq, skv):
+    """The float64 MLA gradient (Q/K rows of 12, V/O rows of 8) equals central
+    differences of an independent numpy forward."""
+    B, Hq, Hkv = 1, 4, 2
+    q, k, v, do = _mla_bwd_inputs(61, B, sq, skv, Hq, Hkv, dqk=12, dv=8)
+    dq, dk, dv = oracle.attention_backward_f64(q, k, v, do, 0.3, causal=causal)
+    assert dq.shape[-1] == 12 and dk.shape[-1] == 12 and dv.shape[-1] == 8
+    f = [oracle.bf16_to_f32(x).astype(np.float64) for x in (q, k, v, do)]
+    eps = 1e-5
+    for which, grad in ((0, dq), (1, dk), (2, dv)):
+        base = f[which]
+        num = np.zeros_like(base)
+        for idx in np.ndindex(base.shape):
+            old = base[idx]
+            base[idx] = old + eps
+            lp = _loss_numpy_f64(f[0], f[1], f[2], f[3], 0.3, causal)
+            base[idx] = old - eps
+            lm = _loss_numpy_f64(f[0], f[1], f[2], f[3], 0.3, causal)
+            base[idx] = old
+            num[idx] = (lp - lm) / (2 * eps)
+        assert np.allclose(grad, num, rtol=1e-6, atol=1e-7), (which, np.abs(grad - num).max())
+
+
+def test_mla_backward_oracle_equals_gqa_when_dims_match():
+    """The MLA entry point with dqk = dv runs the GQA backward's steps: bit-identical."""
+    import ctypes
+    B, S, Hq, Hkv = 1, 96, 4, 2
+    q, k, v, do = _bwd_inputs(63, B, S, S, Hq, Hkv)
+    o, lse = oracle.prefill(q, k, v, SCALE, causal=True)
+    ref = oracle.prefill_backward(q, k, v, o, lse, do, SCALE, causal=True)
+    outs = [np.full(x.shape, np.nan, dtype=np.float32) for x in ref]
+    st = [np.array([S * Hq * 128, Hq * 128, 128], dtype=np.int64), np.array([S * Hkv * 128, Hkv * 128, 128],
+                                                                             dtype=np.int64)]
+    p16 = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16))  # noqa: E731
+    pf = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))  # noqa: E731
+    pi = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))  # noqa: E731
+    rc = oracle.lib().fgqa_oracle_prefill_mla_backward_bf16(
+        p16(q), p16(k), p16(v), p16(o), pf(lse), p16(do), SCALE, pf(outs[0]), pf(outs[1]), pf(outs[2]),
+        B, S, S, Hq, Hkv, 128, 128, pi(st[0]), pi(st[1]), pi(st[1]), pi(st[0]), pi(st[0]), 1, None, None, 0)
+    assert rc == 0
+    for a, b in zip(outs, ref):
+        assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("B,Sq,Skv,Hq,Hkv,causal", [(1, 128, 128, 4, 4, True), (1, 100, 70, 4, 2, False),
+                                                    (2, 64, 96, 2, 1, True)])
+def test_mla_backward_oracle_vs_f64(B, Sq, Skv, Hq, Hkv, causal):
+    q, k, v, do = _mla_bwd_inputs(65, B, Sq, Skv, Hq, Hkv)
+    o, lse = oracle.prefill_mla(q, k, v, MLA_SCALE, causal=causal)
+    dq, dk, dv = oracle.prefill_backward(q, k, v, o, lse, do, MLA_SCALE, causal=causal)
+    assert dq.shape[-1] == 192 and dk.shape[-1] == 192 and dv.shape[-1] == 128
+    eq, ek, ev = oracle.attention_backward_f64(q, k, v, do, MLA_SCALE, causal=causal, o=o)
+    for name, got, ref in (("dq", dq, eq), ("dk", dk, ek), ("dv", dv, ev)):
+        rounded = oracle.bf16_to_f32(oracle.f32_to_bf16(got))
+        assert_grad_close(rounded, ref, f"MLA backward oracle {name} vs f64", ORACLE_GRAD_REL, ORACLE_GRAD_MEAN)
+
+
+def test_mla_backward_planted_mistakes_are_caught():
+    """MLA slips fail the bar against the float64 gradient: scores over the
+    first 128 dims only, the 1/sqrt(Dv) scale, dP over half of V's dims."""
+    B, S, Hq, Hkv = 1, 128, 4, 2
+    q, k, v, do = _mla_bwd_inputs(67, B, S, S, Hq, Hkv)
+    o, lse = oracle.prefill_mla(q, k, v, MLA_SCALE, causal=True)
+    ref = oracle.attention_backward_f64(q, k, v, do, MLA_SCALE, causal=True, o=o)
+
+    def ok(grads):
+        return all(grad_within_tol(oracle.bf16_to_f32(oracle.f32_to_bf16(g)), r, ORACLE_GRAD_REL, ORACLE_GRAD_MEAN)
+                   for g, r in zip(grads, ref))
+
+    assert ok(oracle.prefill_backward(q, k, v, o, lse, do, MLA_SCALE, causal=True))
+    q128, k128 = q.copy(), k.copy()
+    q128[..., 128:] = 0
+    k128[..., 128:] = 0
+    assert not ok(oracle.prefill_backward(q128, k128, v, o, lse, do, MLA_SCALE, causal=True))
+    assert not ok(oracle.prefill_backward(q, k, v, o, lse, do, 1.0 / math.sqrt(128), causal=True))
+    vh = v.copy()
+    vh[..., 64:] = 0
+    assert not ok(oracle.prefill_backward(q, k, vh, o, lse, do, MLA_SCALE, causal=True))
