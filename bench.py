@@ -413,6 +413,41 @@ def bench_swa_backward(steps, warmup, dev, window=512):
                           "algorithmic_flops": flops, "executed_mfma_flops": flops * 7 // 5})
 
 
+def bench_mla_backward(steps, warmup, dev):
+    """MLA prefill backward (Q/K head dim 192, V/O 128, causal) at the
+    reference's MLA benchmark shape (README: B=1, S=4096, Hq=Hkv=16), fed the
+    GPU MLA forward's O and LSE; one step = every launch of
+    fgqa_prefill_backward_bf16."""
+    import math
+
+    import torch
+
+    import cuda_llm_ops_amd as fg
+    B, S, Hq, Hkv, Dqk, Dv = 1, 4096, 16, 16, 192, 128
+    scale = 1.0 / math.sqrt(Dqk)
+    q = _normal((B, S, Hq, Dqk), 20, 1.0, dev)
+    k = _normal((B, S, Hkv, Dqk), 21, 1.0, dev)
+    v = _normal((B, S, Hkv, Dv), 22, 1.0, dev)
+    do = _normal((B, S, Hq, Dv), 23, 1.0, dev)
+    out, lse = fg.flash_gqa_forward_bshd(q, k, v, scale, causal=True)
+    n_ws = fg.backward_workspace_bytes(B, S, S, Hq, Hkv, head_dim=Dqk, head_dim_v=Dv)
+    ws = torch.empty(max(n_ws, 256), dtype=torch.uint8, device=dev)
+    step = fg.prepare_backward(q, k, v, out, lse, do, scale, causal=True, workspace=ws)
+    total_ms, per = _time_calls(step, steps, warmup)
+    # the reference's causal-halved count, QK + dP + dQ + dK + dV
+    # (test_flash_mla_kernel.py:344-363); the kernels execute S and dP twice
+    flops = B * Hq * 2 * S * S * (3 * Dqk + 2 * Dv) // 2
+    avg = sum(per) / len(per)
+    tflops = flops / (avg * 1e-3) / 1e12
+    return dict(config=f"MLA causal prefill backward, B={B} S={S} Hq={Hq} Hkv={Hkv} Dqk={Dqk} Dv={Dv}",
+                us_avg=round(avg * 1e3, 2), us_median=round(per[len(per) // 2] * 1e3, 2),
+                us_min=round(per[0] * 1e3, 2),
+                roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
+                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                          "kernel": "bwd_prep + bwd_dkdv<192> + bwd_dq<192> (whole step)",
+                          "algorithmic_flops": flops})
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -425,13 +460,14 @@ def main():
     ap.add_argument("--no-paged", action="store_true")
     ap.add_argument("--no-swa", action="store_true")
     ap.add_argument("--no-swa-backward", action="store_true")
+    ap.add_argument("--no-mla-backward", action="store_true")
     ap.add_argument("--no-mla", action="store_true")
     ap.add_argument("--no-sparse", action="store_true")
     ap.add_argument("--page-size", type=int, default=16, help="with --mode paged")
     ap.add_argument("--kv", choices=["bf16", "fp8"], default="bf16", help="with --mode paged")
     ap.add_argument("--all", action="store_true", help="also report configs 1, 3 and 5 (to stderr)")
     ap.add_argument("--mode", choices=["bench", "decode", "paged", "prefill", "swa", "mla", "sparse", "backward",
-                                       "swa_backward", "copy"],
+                                       "swa_backward", "mla_backward", "copy"],
                     default="bench",
                     help="decode/prefill/copy: run only that workload (for profiling) and print its timing")
     ap.add_argument("--config", type=int, default=0,
@@ -478,6 +514,9 @@ def main():
     if args.mode == "swa_backward":
         print(json.dumps({"mode": "swa_backward", **bench_swa_backward(args.steps, args.warmup, dev)}), flush=True)
         return
+    if args.mode == "mla_backward":
+        print(json.dumps({"mode": "mla_backward", **bench_mla_backward(args.steps, args.warmup, dev)}), flush=True)
+        return
 
     res = bench_decode(2, args.steps, args.warmup, args.split_tokens, dev)
     gbs = res["kv_bytes"] / (res["ms_step"] * 1e-3) / 1e9
@@ -521,6 +560,8 @@ def main():
         line["backward"] = bench_backward(4, max(5, args.steps // 2), max(2, args.warmup // 2), dev)
     if not args.no_swa_backward:
         line["swa_backward"] = bench_swa_backward(max(5, args.steps // 2), max(2, args.warmup // 2), dev)
+    if not args.no_mla_backward:
+        line["mla_backward"] = bench_mla_backward(max(5, args.steps // 5), 2, dev)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_decode(res)
     if args.all:

@@ -1,4 +1,4 @@
-"""MI355X-native flash grouped-query attention (decode incl. paged/fp8 KV caches, causal, sliding-window, MLA and sparse-index prefill, and the causal and sliding-window prefill backward).
+"""MI355X-native flash grouped-query attention (decode incl. paged/fp8 KV caches, causal, sliding-window, MLA and sparse-index prefill, and the causal, sliding-window and MLA prefill backward).
 
 The kernels live in libfgqa.so (HIP, gfx950); ``flash_gqa`` is the Python host
 interface over its C ABI (include/fgqa.h).
@@ -16,6 +16,7 @@ from .flash_gqa import (  # noqa: F401
     launch_flash_gqa_forward_bf16_kernel,
     launch_flash_swa_backward_bf16_kernel,
     launch_flash_swa_forward_bf16_kernel,
+    launch_flash_mla_backward_bf16_kernel,
     launch_flash_mla_forward_bf16_kernel,
     launch_flash_sgqa_forward_bf16_kernel,
     flash_sgqa_forward_bshd,

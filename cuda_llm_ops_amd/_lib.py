@@ -140,6 +140,7 @@ class BackwardArgs(ctypes.Structure):
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
         ("window_size", ctypes.c_int32),
+        ("head_dim_v", ctypes.c_int32),
     ]
 
 

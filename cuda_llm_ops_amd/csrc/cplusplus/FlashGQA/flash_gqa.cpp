@@ -143,7 +143,7 @@ void LaunchFlashGqaForwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf1
 static void backward_bshd(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* o, const float* lse,
                           const bf16_t* gradO, float scale, bf16_t* gradQ, bf16_t* gradK, bf16_t* gradV,
                           int batchSize, int seqLengthQ, int seqLengthKv, int numQueryHeads, int numKvHeads,
-                          int headDim, bool causal, int windowSize) {
+                          int headDim, int headDimV, bool causal, int windowSize) {
     fgqa_prefill_backward_args a;
     std::memset(&a, 0, sizeof(a));
     a.q = q;
@@ -164,12 +164,19 @@ static void backward_bshd(const bf16_t* q, const bf16_t* k, const bf16_t* v, con
     a.causal = causal ? 1 : 0;
     a.scale = scale;
     a.window_size = windowSize;
-    // BSHD: q, o, gradO, gradQ [B, Sq, Hq, D]; k, v, gradK, gradV [B, Skv, Hkv, D]
+    a.head_dim_v = headDimV;
+    // BSHD: q, gradQ [B, Sq, Hq, D]; o, gradO [B, Sq, Hq, Dv]; k, gradK [B, Skv, Hkv, D];
+    // v, gradV [B, Skv, Hkv, Dv]
     const int64_t qs[3] = {(int64_t)seqLengthQ * numQueryHeads * headDim, (int64_t)numQueryHeads * headDim, headDim};
+    const int64_t os[3] = {(int64_t)seqLengthQ * numQueryHeads * headDimV, (int64_t)numQueryHeads * headDimV,
+                           headDimV};
     const int64_t ks[3] = {(int64_t)seqLengthKv * numKvHeads * headDim, (int64_t)numKvHeads * headDim, headDim};
+    const int64_t vs[3] = {(int64_t)seqLengthKv * numKvHeads * headDimV, (int64_t)numKvHeads * headDimV, headDimV};
     for (int i = 0; i < 3; ++i) {
-        a.q_stride[i] = a.o_stride[i] = a.grad_o_stride[i] = a.grad_q_stride[i] = qs[i];
-        a.k_stride[i] = a.v_stride[i] = a.grad_k_stride[i] = a.grad_v_stride[i] = ks[i];
+        a.q_stride[i] = a.grad_q_stride[i] = qs[i];
+        a.o_stride[i] = a.grad_o_stride[i] = os[i];
+        a.k_stride[i] = a.grad_k_stride[i] = ks[i];
+        a.v_stride[i] = a.grad_v_stride[i] = vs[i];
     }
     g_last_status = fgqa_prefill_backward_bf16(&a, nullptr);
 }
@@ -179,7 +186,15 @@ void LaunchFlashGqaBackwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf
                                       bf16_t* gradK, bf16_t* gradV, int batchSize, int seqLengthQ, int seqLengthKv,
                                       int numQueryHeads, int numKvHeads, int headDim, bool causal) {
     backward_bshd(q, k, v, o, lse, gradO, scale, gradQ, gradK, gradV, batchSize, seqLengthQ, seqLengthKv,
-                  numQueryHeads, numKvHeads, headDim, causal, 0);
+                  numQueryHeads, numKvHeads, headDim, headDim, causal, 0);
+}
+
+void LaunchFlashMlaBackwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* o,
+                                      const float* lse, const bf16_t* gradO, float scale, bf16_t* gradQ,
+                                      bf16_t* gradK, bf16_t* gradV, int batchSize, int seqLengthQ, int seqLengthKv,
+                                      int numQueryHeads, int numKvHeads, int headDimQk, int headDimV, bool causal) {
+    backward_bshd(q, k, v, o, lse, gradO, scale, gradQ, gradK, gradV, batchSize, seqLengthQ, seqLengthKv,
+                  numQueryHeads, numKvHeads, headDimQk, headDimV, causal, 0);
 }
 
 void LaunchFlashSwaBackwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* o,
@@ -187,7 +202,7 @@ void LaunchFlashSwaBackwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf
                                       bf16_t* gradK, bf16_t* gradV, int batchSize, int seqLengthQ, int seqLengthKv,
                                       int numQueryHeads, int numKvHeads, int headDim, int windowSize) {
     backward_bshd(q, k, v, o, lse, gradO, scale, gradQ, gradK, gradV, batchSize, seqLengthQ, seqLengthKv,
-                  numQueryHeads, numKvHeads, headDim, true, windowSize);
+                  numQueryHeads, numKvHeads, headDim, headDim, true, windowSize);
 }
 
 void LaunchFlashSwaForwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf16_t* v, float scale, bf16_t* o,

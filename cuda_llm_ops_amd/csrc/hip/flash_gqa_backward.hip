@@ -87,6 +87,7 @@ struct BwdParams {
 constexpr int kBwWaves = 4;
 constexpr int kBwThreads = kBwWaves * kWave;
 constexpr int kBwRowBytes = kHeadDim * 2;             // one Q / dO / K / V row
+constexpr int kBwHiRowBytes = 128;                    // dims 128..191 of a 192-wide Q / K row
 
 // ---- key-major kernel
 constexpr int kKvKeys = 128;                          // keys per workgroup
@@ -98,12 +99,22 @@ constexpr int kKvQOff = 0;
 constexpr int kKvDoOff = 3 * kKvTileBytes;
 constexpr int kKvStatOff = 6 * kKvTileBytes;
 constexpr int kKvSmemBytes = kKvStatOff + 3 * kKvStatBytes;
+// MLA: the 128-byte parts of Q[3] follow
+constexpr int kKvQHiTileBytes = kKvRows * kBwHiRowBytes;   // 4 KB
+constexpr int kKvQHiOff = kKvSmemBytes;
+template <int kDk>
+constexpr int kv_smem_bytes() { return kDk > 128 ? kKvSmemBytes + 3 * kKvQHiTileBytes : kKvSmemBytes; }
 
 // ---- query-major kernel
 constexpr int kDqTile = 64;                           // keys per tile
 constexpr int kDqTileBytes = kDqTile * kBwRowBytes;   // 16 KB
 // LDS: K[2] | V[2]
 constexpr int kDqSmemBytes = 4 * kDqTileBytes;
+// MLA: the 128-byte parts of K[2] follow
+constexpr int kDqKHiTileBytes = kDqTile * kBwHiRowBytes;   // 8 KB
+constexpr int kDqKHiOff = kDqSmemBytes;
+template <int kDk>
+constexpr int dq_smem_bytes() { return kDk > 128 ? kDqSmemBytes + 2 * kDqKHiTileBytes : kDqSmemBytes; }
 
 // Q, dO, K and V rows (256 B) sit in LDS with their 16-byte chunks permuted:
 // chunk c of row r goes to slot c ^ bw_swz(r).  bw_swz is a bijection on
@@ -135,6 +146,32 @@ __device__ __forceinline__ int bw_tr_off(int lane, int cb, int h8) {
     const int c = 4 * cb + 2 * gq + ((l16 >> 1) & 1);
     return r * kBwRowBytes + ((c ^ bw_swz(r)) << 4) + 8 * (l16 & 1);
 }
+
+// MLA (Q/K head dim 192, V/O 128): a 192-wide Q or K row is kept as a
+// 256-byte part (dims 0..127, laid out as above) and a 128-byte part (dims
+// 128..191) in a separate tile, whose chunk c of row r sits in slot
+// c ^ bw_swz_hi(r).  bw_swz_hi is a bijection on (r / 2) % 8: 16 consecutive
+// rows read at one chunk fall in 16 different 16-byte bank groups (rows of
+// either parity share none, 128-byte rows alternate halves of a 256-byte
+// bank line).  Its top bit is (r / 2) % 2: rows r and r + 2 read over 4
+// consecutive chunks land in different 4-chunk halves, so the transposed
+// reads are conflict-free too.
+__device__ __forceinline__ int bw_swz_hi(int r) { return (((r >> 1) & 1) << 2) | ((r >> 2) & 3); }
+// bw_tr_off for the 128-byte part (column block cb = 0, 1: dims 128 + 32cb ..)
+__device__ __forceinline__ int bw_tr_off_hi(int lane, int cb, int h8) {
+    const int l16 = lane & 15, gq = (lane >> 4) & 1, g2 = lane >> 5;
+    const int r = 4 * g2 + (l16 >> 2) + 8 * h8;
+    const int c = 4 * cb + 2 * gq + ((l16 >> 1) & 1);
+    return r * kBwHiRowBytes + ((c ^ bw_swz_hi(r)) << 4) + 8 * (l16 & 1);
+}
+template <int kDk>
+struct BwDims {
+    static_assert(kDk == 128 || kDk == 192, "Q/K head dim");
+    static constexpr bool kHi = kDk > 128;        // a 128-byte part per row
+    static constexpr int kRowBytes = kDk * 2;     // one Q / K row in HBM
+    static constexpr int kSteps = kDk / 16;       // MFMA k-steps of S over the Q/K dim
+    static constexpr int kDb = kDk / 32;          // 32-column blocks of dQ / dK
+};
 
 __device__ __forceinline__ bf16x8_t tr_pair(const unsigned char* base, int off0, int off1) {
     const bf16x4_t lo = lds_read_tr16(reinterpret_cast<const __bf16*>(base + off0));
@@ -177,8 +214,9 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(BwdParams p) {
 // with Q/dO(t+2) streaming into the third LDS buffer meanwhile.
 // kSwa: sliding window (a separate instantiation, so the causal kernels carry
 // none of its work).
-template <bool kSwa>
+template <bool kSwa, int kDk>
 __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
+    using D = BwDims<kDk>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -205,16 +243,17 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
     const uint32_t kss = (uint32_t)(p.k_ss * 2);
     const uint32_t vss = (uint32_t)(p.v_ss * 2);
     const __amdgpu_buffer_rsrc_t krs =
-        make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, (uint32_t)(p.skv - 1) * kss + kBwRowBytes);
+        make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, (uint32_t)(p.skv - 1) * kss + D::kRowBytes);
     const __amdgpu_buffer_rsrc_t vrs =
         make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, (uint32_t)(p.skv - 1) * vss + kBwRowBytes);
     const int key = kv0 + 32 * wave + l32;   // this lane's key (column of S)
-    bf16x8_t kop[8], vop[8];
+    bf16x8_t kop[D::kSteps], vop[8];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
+    for (int ks = 0; ks < D::kSteps; ++ks)
         kop[ks] = as_bf16x8(buf_load16(krs, (uint32_t)key * kss + (16 * ks + 8 * g2) * 2));
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
         vop[ks] = as_bf16x8(buf_load16(vrs, (uint32_t)key * vss + (16 * ks + 8 * g2) * 2));
-    }
 
     // step t: head h0 + t / per_head, query block qb0 + t % per_head
     const int qb0 = p.causal ? min(kv0 / kKvRows, p.n_qblocks32) : 0;
@@ -233,7 +272,7 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
         const int hh = h0 + t / per_head;
         const int q0 = (qb0 + t % per_head) * kKvRows;
         const __amdgpu_buffer_rsrc_t qrs =
-            make_rsrc(p.q + b * p.q_sb + hh * p.q_sh, (uint32_t)(p.sq - 1) * qss + kBwRowBytes);
+            make_rsrc(p.q + b * p.q_sb + hh * p.q_sh, (uint32_t)(p.sq - 1) * qss + D::kRowBytes);
         const __amdgpu_buffer_rsrc_t drs =
             make_rsrc(p.dout + b * p.do_sb + hh * p.do_sh, (uint32_t)(p.sq - 1) * dss + kBwRowBytes);
 #pragma unroll
@@ -244,6 +283,13 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
             bw_dma16(lds_base + kKvQOff + bi * kKvTileBytes + r0 * kBwRowBytes, (uint32_t)(q0 + r) * qss + slot, qrs);
             bw_dma16(lds_base + kKvDoOff + bi * kKvTileBytes + r0 * kBwRowBytes, (uint32_t)(q0 + r) * dss + slot, drs);
         }
+        if constexpr (D::kHi) {
+            // dims 128..191 of rows 8w..8w+7: lane l fills slot l % 8 of row 8w + l / 8
+            const int r = 8 * wave + (lane >> 3);
+            const int c = (lane & 7) ^ bw_swz_hi(r);
+            bw_dma16(lds_base + kKvQHiOff + bi * kKvQHiTileBytes + 8 * wave * kBwHiRowBytes,
+                     (uint32_t)(q0 + r) * qss + kBwRowBytes + 16 * c, qrs);
+        }
         if (wave == 0) {
             const int r = q0 + l32;
             const int64_t idx = ((int64_t)b * p.hq + hh) * p.sq + r + (g2 ? rows_q : 0);
@@ -252,24 +298,40 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
         }
     };
 
-    f32x16_t dk_acc[4], dv_acc[4];
+    f32x16_t dk_acc[D::kDb], dv_acc[4];
+#pragma unroll
+    for (int db = 0; db < D::kDb; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dk_acc[db][i] = 0.f;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) dk_acc[db][i] = dv_acc[db][i] = 0.f;
+        for (int i = 0; i < 16; ++i) dv_acc[db][i] = 0.f;
 
     // transposed-read offsets into the Q / dO tiles
-    int trq[4][2];
+    int trq[4][2], trq_hi[2][2];
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
         trq[db][0] = bw_tr_off(lane, db, 0);
         trq[db][1] = bw_tr_off(lane, db, 1);
     }
+    if constexpr (D::kHi) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            trq_hi[cb][0] = bw_tr_off_hi(lane, cb, 0);
+            trq_hi[cb][1] = bw_tr_off_hi(lane, cb, 1);
+        }
+    }
     // b128 row-read offsets of the A operands of S and dP (row l32, chunk 2ks + g2)
-    int roff[8];
+    int roff[8], roff_hi[4];
     const int fl = bw_swz(l32);
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) roff[ks] = l32 * kBwRowBytes + (((2 * ks + g2) ^ fl) << 4);
+    if constexpr (D::kHi) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+            roff_hi[ks] = l32 * kBwHiRowBytes + (((2 * ks + g2) ^ bw_swz_hi(l32)) << 4);
+    }
     const float c2 = p.scale_log2;
     const float scale = p.scale;
     // S = Q K^T and dP = dO V^T of the step in buffer bi: C[q][key], lane
@@ -284,6 +346,12 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
         for (int ks = 0; ks < 8; ++ks) {
             s = mfma32(*reinterpret_cast<const bf16x8_t*>(ql + roff[ks]), kop[ks], s);
             dp = mfma32(*reinterpret_cast<const bf16x8_t*>(dl + roff[ks]), vop[ks], dp);
+        }
+        if constexpr (D::kHi) {
+            const unsigned char* qh = smem + kKvQHiOff + bi * kKvQHiTileBytes;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                s = mfma32(*reinterpret_cast<const bf16x8_t*>(qh + roff_hi[ks]), kop[8 + ks], s);
         }
     };
     // P = exp2(S*scale*log2e - lse*log2e), dS = P (dP - delta) scale, both as
@@ -322,13 +390,20 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
         const unsigned char* ql = smem + kKvQOff + bi * kKvTileBytes;
         const unsigned char* dl = smem + kKvDoOff + bi * kKvTileBytes;
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+        for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
                 const int rb = ks * 16 * kBwRowBytes;
                 dv_acc[db] = mfma32(pop[ks], tr_pair(dl + rb, trq[db][0], trq[db][1]), dv_acc[db]);
                 dk_acc[db] = mfma32(dsop[ks], tr_pair(ql + rb, trq[db][0], trq[db][1]), dk_acc[db]);
             }
+            if constexpr (D::kHi) {
+                const unsigned char* qh = smem + kKvQHiOff + bi * kKvQHiTileBytes + ks * 16 * kBwHiRowBytes;
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb)
+                    dk_acc[4 + cb] = mfma32(dsop[ks], tr_pair(qh, trq_hi[cb][0], trq_hi[cb][1]), dk_acc[4 + cb]);
+            }
+        }
     };
 
     // Triple-buffered Q/dO: step t reads buffers t%3 (dV/dK) and (t+1)%3
@@ -341,7 +416,7 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
     {
         // zero the buffers first: a padded step may read one never loaded
         const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-        for (int off = tid * 16; off < kKvSmemBytes; off += kBwThreads * 16)
+        for (int off = tid * 16; off < kv_smem_bytes<kDk>(); off += kBwThreads * 16)
             *reinterpret_cast<f32x4_t*>(smem + off) = z;
     }
     __syncthreads();
@@ -387,38 +462,41 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
             if (j >= p.skv) continue;
             if (p.dk_part != nullptr) {
                 const int64_t row = (((int64_t)hsp * p.batch + b) * p.hkv + kvh) * p.skv + j;
-                float* dkr = p.dk_part + row * kHeadDim + l32;
+                float* dkr = p.dk_part + row * kDk + l32;
                 float* dvr = p.dv_part + row * kHeadDim + l32;
 #pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    dkr[32 * db] = dk_acc[db][4 * i + r];
-                    dvr[32 * db] = dv_acc[db][4 * i + r];
-                }
+                for (int db = 0; db < D::kDb; ++db) dkr[32 * db] = dk_acc[db][4 * i + r];
+#pragma unroll
+                for (int db = 0; db < 4; ++db) dvr[32 * db] = dv_acc[db][4 * i + r];
             } else {
                 __bf16* dkr = p.dk + b * p.dk_sb + (int64_t)j * p.dk_ss + kvh * p.dk_sh + l32;
                 __bf16* dvr = p.dv + b * p.dv_sb + (int64_t)j * p.dv_ss + kvh * p.dv_sh + l32;
 #pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    dkr[32 * db] = (__bf16)dk_acc[db][4 * i + r];
-                    dvr[32 * db] = (__bf16)dv_acc[db][4 * i + r];
-                }
+                for (int db = 0; db < D::kDb; ++db) dkr[32 * db] = (__bf16)dk_acc[db][4 * i + r];
+#pragma unroll
+                for (int db = 0; db < 4; ++db) dvr[32 * db] = (__bf16)dv_acc[db][4 * i + r];
             }
         }
 }
 
-// Sum of the n_hsplit fp32 partials -> bf16 dK, dV.  16 lanes per key row.
+// Sum of the n_hsplit fp32 partials -> bf16 dK, dV.  16 lanes per key row:
+// lane `part` sums dK elements kDk/16 * part .. (8 or 12) and dV elements
+// 8 * part .. +7.
+template <int kDk>
 __global__ __launch_bounds__(256) void bwd_dkdv_reduce_kernel(BwdParams p) {
+    constexpr int kKq = kDk / 64;   // f32x4 of dK per lane (2 or 3)
     const int64_t rows_kv = (int64_t)p.batch * p.hkv * p.skv;
     const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
     const int part = threadIdx.x & 15;
     if (row >= rows_kv) return;
-    f32x4_t k0 = {0.f, 0.f, 0.f, 0.f}, k1 = k0, v0 = k0, v1 = k0;
+    f32x4_t kq[kKq], v0 = {0.f, 0.f, 0.f, 0.f}, v1 = v0;
+#pragma unroll
+    for (int e = 0; e < kKq; ++e) kq[e] = v0;
     for (int s = 0; s < p.n_hsplit; ++s) {
-        const int64_t off = (s * rows_kv + row) * kHeadDim + part * 8;
-        const f32x4_t* pk = reinterpret_cast<const f32x4_t*>(p.dk_part + off);
-        const f32x4_t* pv = reinterpret_cast<const f32x4_t*>(p.dv_part + off);
-        k0 += pk[0];
-        k1 += pk[1];
+        const f32x4_t* pk = reinterpret_cast<const f32x4_t*>(p.dk_part + (s * rows_kv + row) * kDk + part * 4 * kKq);
+        const f32x4_t* pv = reinterpret_cast<const f32x4_t*>(p.dv_part + (s * rows_kv + row) * kHeadDim + part * 8);
+#pragma unroll
+        for (int e = 0; e < kKq; ++e) kq[e] += pk[e];
         v0 += pv[0];
         v1 += pv[1];
     }
@@ -426,15 +504,20 @@ __global__ __launch_bounds__(256) void bwd_dkdv_reduce_kernel(BwdParams p) {
     const int64_t bh = row / p.skv;
     const int kvh = (int)(bh % p.hkv);
     const int b = (int)(bh / p.hkv);
-    bf16x8_t wk, wv;
+    __bf16* dkr = p.dk + b * p.dk_sb + j * p.dk_ss + kvh * p.dk_sh + part * 4 * kKq;
+#pragma unroll
+    for (int e = 0; e < kKq; ++e) {
+        bf16x4_t w;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) w[x] = (__bf16)kq[e][x];
+        *reinterpret_cast<bf16x4_t*>(dkr + 4 * e) = w;
+    }
+    bf16x8_t wv;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        wk[e] = (__bf16)k0[e];
-        wk[4 + e] = (__bf16)k1[e];
         wv[e] = (__bf16)v0[e];
         wv[4 + e] = (__bf16)v1[e];
     }
-    *reinterpret_cast<bf16x8_t*>(p.dk + b * p.dk_sb + j * p.dk_ss + kvh * p.dk_sh + part * 8) = wk;
     *reinterpret_cast<bf16x8_t*>(p.dv + b * p.dv_sb + j * p.dv_ss + kvh * p.dv_sh + part * 8) = wv;
 }
 
@@ -444,9 +527,11 @@ __global__ __launch_bounds__(256) void bwd_dkdv_reduce_kernel(BwdParams p) {
 // forward kernel.  With kGroups == 2 two groups of 4 waves take the two halves
 // of the unit's key range and add their dQ through LDS at the end (dQ is a
 // plain sum over keys: P comes from the final LSE).
-template <int kGroups, bool kSwa>
+template <int kGroups, bool kSwa, int kDk>
 __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem_all, int qb, int hg, int kvh,
                                         int b) {
+    using D = BwDims<kDk>;
+    static_assert(kGroups == 1 || kDk == 128, "the split dQ kernel is 128-wide only");
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave_wg = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -469,15 +554,16 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem_
     const uint32_t qss = (uint32_t)(p.q_ss * 2);
     const uint32_t dss = (uint32_t)(p.do_ss * 2);
     const __amdgpu_buffer_rsrc_t qrs =
-        make_rsrc(p.q + b * p.q_sb + h * p.q_sh, (uint32_t)(p.sq - 1) * qss + kBwRowBytes);
+        make_rsrc(p.q + b * p.q_sb + h * p.q_sh, (uint32_t)(p.sq - 1) * qss + D::kRowBytes);
     const __amdgpu_buffer_rsrc_t drs =
         make_rsrc(p.dout + b * p.do_sb + h * p.do_sh, (uint32_t)(p.sq - 1) * dss + kBwRowBytes);
-    bf16x8_t qop[8], doop[8];
+    bf16x8_t qop[D::kSteps], doop[8];
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
+    for (int kk = 0; kk < D::kSteps; ++kk)
         qop[kk] = as_bf16x8(buf_load16(qrs, (uint32_t)qrow * qss + (16 * kk + 8 * g2) * 2));
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
         doop[kk] = as_bf16x8(buf_load16(drs, (uint32_t)qrow * dss + (16 * kk + 8 * g2) * 2));
-    }
     const int64_t rows_q = (int64_t)p.batch * p.hq * p.sq;
     const int64_t ridx = ((int64_t)b * p.hq + h) * p.sq + qrow;
     const float nl = (qrow < p.sq) ? p.rowstat[ridx] : 0.f;
@@ -498,7 +584,7 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem_
     const uint32_t kss = (uint32_t)(p.k_ss * 2);
     const uint32_t vss = (uint32_t)(p.v_ss * 2);
     const __amdgpu_buffer_rsrc_t krs =
-        make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, (uint32_t)(p.skv - 1) * kss + kBwRowBytes);
+        make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, (uint32_t)(p.skv - 1) * kss + D::kRowBytes);
     const __amdgpu_buffer_rsrc_t vrs =
         make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, (uint32_t)(p.skv - 1) * vss + kBwRowBytes);
     // K, V tile j (of the group) into buffer bi: rows r = 4*(wave + 4i) + lane/16;
@@ -513,23 +599,47 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem_
             bw_dma16(lds_base + bi * kDqTileBytes + r0 * kBwRowBytes, (uint32_t)(t0 + r) * kss + slot, krs);
             bw_dma16(lds_base + (2 + bi) * kDqTileBytes + r0 * kBwRowBytes, (uint32_t)(t0 + r) * vss + slot, vrs);
         }
+        if constexpr (D::kHi) {
+            // dims 128..191: instruction i fills rows 8(wave + 4i) .. +7, lane l
+            // slot l % 8 of row 8(wave + 4i) + l / 8
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int r0 = 8 * (wave + 4 * i);
+                const int r = r0 + (lane >> 3);
+                const int c = (lane & 7) ^ bw_swz_hi(r);
+                bw_dma16(lds_base + kDqKHiOff + bi * kDqKHiTileBytes + r0 * kBwHiRowBytes,
+                         (uint32_t)(t0 + r) * kss + kBwRowBytes + 16 * c, krs);
+            }
+        }
     };
 
-    f32x16_t dq_acc[4];
+    f32x16_t dq_acc[D::kDb];
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < D::kDb; ++db)
 #pragma unroll
         for (int i = 0; i < 16; ++i) dq_acc[db][i] = 0.f;
-    int trk[4][2];
+    int trk[4][2], trk_hi[2][2];
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
         trk[db][0] = bw_tr_off(lane, db, 0);
         trk[db][1] = bw_tr_off(lane, db, 1);
     }
-    int roff[8];
+    if constexpr (D::kHi) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            trk_hi[cb][0] = bw_tr_off_hi(lane, cb, 0);
+            trk_hi[cb][1] = bw_tr_off_hi(lane, cb, 1);
+        }
+    }
+    int roff[8], roff_hi[4];
     const int fl = bw_swz(l32);
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) roff[kk] = l32 * kBwRowBytes + (((2 * kk + g2) ^ fl) << 4);
+    if constexpr (D::kHi) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+            roff_hi[kk] = l32 * kBwHiRowBytes + (((2 * kk + g2) ^ bw_swz_hi(l32)) << 4);
+    }
     const float c2 = p.scale_log2;
     const float scale = p.scale;
 
@@ -555,6 +665,15 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem_
                 s[tb] = mfma32(*reinterpret_cast<const bf16x8_t*>(kl + off), qop[kk], s[tb]);
                 dp[tb] = mfma32(*reinterpret_cast<const bf16x8_t*>(vl + off), doop[kk], dp[tb]);
             }
+        if constexpr (D::kHi) {
+            const unsigned char* kh = smem + kDqKHiOff + bi * kDqKHiTileBytes;
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                for (int tb = 0; tb < 2; ++tb)
+                    s[tb] = mfma32(*reinterpret_cast<const bf16x8_t*>(kh + tb * 32 * kBwHiRowBytes + roff_hi[kk]),
+                                   qop[8 + kk], s[tb]);
+        }
         // dS^T = P^T (dP^T - delta) scale as the B operand of dQ^T += K^T dS^T:
         // block kb = 2tb + kh holds registers 8kh .. 8kh+7 of S^T block tb,
         // i.e. keys 16kb + 4g2 + 0..3 and 16kb + 8 + 4g2 + 0..3.
@@ -576,10 +695,17 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem_
                 }
         // dQ^T[d][q] += sum over keys of K^T[d][key] dS^T[key][q], 4 column tiles of D
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+        for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
             for (int db = 0; db < 4; ++db)
                 dq_acc[db] = mfma32(tr_pair(kl + 16 * kb * kBwRowBytes, trk[db][0], trk[db][1]), dsop[kb], dq_acc[db]);
+            if constexpr (D::kHi) {
+                const unsigned char* kh = smem + kDqKHiOff + bi * kDqKHiTileBytes + 16 * kb * kBwHiRowBytes;
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb)
+                    dq_acc[4 + cb] = mfma32(tr_pair(kh, trk_hi[cb][0], trk_hi[cb][1]), dsop[kb], dq_acc[4 + cb]);
+            }
+        }
     };
 
     // Double-buffered K/V, two tiles per trip so that buffer offsets are
@@ -587,7 +713,7 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem_
     // and reads a buffer that holds zeros or the previous tile.
     {
         const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-        for (int off = (tid % kBwThreads) * 16; off < kDqSmemBytes; off += kBwThreads * 16)
+        for (int off = (tid % kBwThreads) * 16; off < dq_smem_bytes<kDk>(); off += kBwThreads * 16)
             *reinterpret_cast<f32x4_t*>(smem + off) = z;
     }
     __syncthreads();
@@ -630,7 +756,7 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem_
     if (qrow < p.sq) {
         __bf16* dst = p.dq + b * p.dq_sb + (int64_t)qrow * p.dq_ss + h * p.dq_sh;
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
+        for (int db = 0; db < D::kDb; ++db)
 #pragma unroll
             for (int i4 = 0; i4 < 4; ++i4) {
                 bf16x4_t w;
@@ -653,12 +779,14 @@ __device__ __forceinline__ void dq_block_unit(const BwdParams& p, int* qb, int* 
     *b = stream / (p.n_hgroups * p.hkv);
 }
 
-template <bool kSwa>
-__global__ __launch_bounds__(kBwThreads, 2) void bwd_dq_kernel(BwdParams p) {
+// 128-wide: two workgroups per CU; 192-wide (MLA): one, with the whole
+// register file (Q^T of 12 k-steps, dQ^T of 6 column blocks).
+template <bool kSwa, int kDk>
+__global__ __launch_bounds__(kBwThreads, kDk == 128 ? 2 : 1) void bwd_dq_kernel(BwdParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     int qb, hg, kvh, b;
     dq_block_unit(p, &qb, &hg, &kvh, &b);
-    dq_unit<1, kSwa>(p, smem, qb, hg, kvh, b);
+    dq_unit<1, kSwa, kDk>(p, smem, qb, hg, kvh, b);
 }
 
 template <bool kSwa>
@@ -666,15 +794,18 @@ __global__ __launch_bounds__(2 * kBwThreads, 1) void bwd_dq_split_kernel(BwdPara
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     int qb, hg, kvh, b;
     dq_block_unit(p, &qb, &hg, &kvh, &b);
-    dq_unit<2, kSwa>(p, smem, qb, hg, kvh, b);
+    dq_unit<2, kSwa, 128>(p, smem, qb, hg, kvh, b);
 }
 
 namespace {
 
 struct BwdPlan {
     int n_hsplit;
-    size_t stat_bytes, part_bytes, ws_bytes;
+    size_t stat_bytes, part_k_bytes, part_v_bytes, ws_bytes;
 };
+
+// Q/K head dim of a call: 128, or 192 for MLA (V/O stay 128).
+int backward_dqk(const fgqa_prefill_backward_args* a) { return a->head_dim; }
 
 size_t round256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
@@ -692,9 +823,14 @@ int validate_backward(const fgqa_prefill_backward_args* a) {
     for (const int64_t* s : strides)
         for (int i = 0; i < 3; ++i)
             if (s[i] < 0) return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->head_dim != kHeadDim) return FGQA_ERR_UNSUPPORTED;
+    // (128, 128) and the MLA shape (192, 128) (flash_mla_backward_kernel.py);
+    // MLA has no sliding-window form
+    if (a->head_dim_v < 0) return FGQA_ERR_INVALID_ARGUMENT;
+    const int dv = a->head_dim_v == 0 ? a->head_dim : a->head_dim_v;
+    if (dv != kHeadDim || (a->head_dim != kHeadDim && a->head_dim != 192)) return FGQA_ERR_UNSUPPORTED;
+    if (a->head_dim == 192 && a->window_size > 0) return FGQA_ERR_UNSUPPORTED;
     // query rows past sq must read as zero (rows may not overlap)
-    if (a->q_stride[1] < kHeadDim || a->grad_o_stride[1] < kHeadDim) return FGQA_ERR_UNSUPPORTED;
+    if (a->q_stride[1] < a->head_dim || a->grad_o_stride[1] < kHeadDim) return FGQA_ERR_UNSUPPORTED;
     const int64_t lim = (int64_t)1 << 31;
     if ((int64_t)(a->seqlen_q + 128) * a->q_stride[1] * 2 >= lim ||
         (int64_t)(a->seqlen_q + 128) * a->grad_o_stride[1] * 2 >= lim ||
@@ -746,8 +882,10 @@ BwdPlan plan_backward(const fgqa_prefill_backward_args* a, int cus) {
     const size_t rows_q = (size_t)a->batch * a->num_q_heads * a->seqlen_q;
     const size_t rows_kv = (size_t)a->batch * a->num_kv_heads * a->seqlen_kv;
     pl.stat_bytes = round256(2 * rows_q * sizeof(float));
-    pl.part_bytes = pl.n_hsplit > 1 ? round256((size_t)pl.n_hsplit * rows_kv * kHeadDim * sizeof(float)) : 0;
-    pl.ws_bytes = pl.stat_bytes + 2 * pl.part_bytes;
+    const size_t parts = pl.n_hsplit > 1 ? (size_t)pl.n_hsplit * rows_kv * sizeof(float) : 0;
+    pl.part_k_bytes = round256(parts * backward_dqk(a));
+    pl.part_v_bytes = round256(parts * kHeadDim);
+    pl.ws_bytes = pl.stat_bytes + pl.part_k_bytes + pl.part_v_bytes;
     return pl;
 }
 
@@ -808,7 +946,7 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     p.dv_sb = a->grad_v_stride[0]; p.dv_ss = a->grad_v_stride[1]; p.dv_sh = a->grad_v_stride[2];
     p.rowstat = reinterpret_cast<float*>(ws);
     p.dk_part = pl.n_hsplit > 1 ? reinterpret_cast<float*>(ws + pl.stat_bytes) : nullptr;
-    p.dv_part = pl.n_hsplit > 1 ? reinterpret_cast<float*>(ws + pl.stat_bytes + pl.part_bytes) : nullptr;
+    p.dv_part = pl.n_hsplit > 1 ? reinterpret_cast<float*>(ws + pl.stat_bytes + pl.part_k_bytes) : nullptr;
     p.batch = a->batch;
     p.sq = a->seqlen_q;
     p.skv = a->seqlen_kv;
@@ -843,26 +981,52 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     // carry about the same number of tiles, so there is nothing to balance and
     // the whole-range kernel is faster.  FGQA_BWD_DQ_SPLIT=0/1 forces the choice.
     const bool swa = p.window > 0;
+    const bool mla = backward_dqk(a) == 192;
     bool dq_split = q_units < 4 * (int64_t)cus && !swa;
     if (const char* e = getenv("FGQA_BWD_DQ_SPLIT")) dq_split = e[0] == '1';
+    dq_split = dq_split && !mla;   // the 192-wide dQ kernel needs one wave per SIMD
     // kernel table: [swa] of dK/dV, dQ, split dQ
-    const void* kv_fn[2] = {reinterpret_cast<const void*>(bwd_dkdv_kernel<false>),
-                            reinterpret_cast<const void*>(bwd_dkdv_kernel<true>)};
-    const void* q_fn[2] = {reinterpret_cast<const void*>(bwd_dq_kernel<false>),
-                           reinterpret_cast<const void*>(bwd_dq_kernel<true>)};
+    const void* kv_fn[2] = {reinterpret_cast<const void*>(bwd_dkdv_kernel<false, 128>),
+                            reinterpret_cast<const void*>(bwd_dkdv_kernel<true, 128>)};
+    const void* q_fn[2] = {reinterpret_cast<const void*>(bwd_dq_kernel<false, 128>),
+                           reinterpret_cast<const void*>(bwd_dq_kernel<true, 128>)};
     const void* q2_fn[2] = {reinterpret_cast<const void*>(bwd_dq_split_kernel<false>),
                             reinterpret_cast<const void*>(bwd_dq_split_kernel<true>)};
-    // attribute slots 10..15: the backward kernels
-    if ((st = set_kernel_smem_once(10 + swa, kv_fn[swa], kKvSmemBytes)) != FGQA_OK) return st;
-    if ((st = set_kernel_smem_once(12 + swa, q_fn[swa], kDqSmemBytes)) != FGQA_OK) return st;
-    if ((st = set_kernel_smem_once(14 + swa, q2_fn[swa], 2 * kDqSmemBytes)) != FGQA_OK) return st;
+    // attribute slots 10..17: the backward kernels
+    if (mla) {
+        if ((st = set_kernel_smem_once(16, reinterpret_cast<const void*>(bwd_dkdv_kernel<false, 192>),
+                                       kv_smem_bytes<192>())) != FGQA_OK)
+            return st;
+        if ((st = set_kernel_smem_once(17, reinterpret_cast<const void*>(bwd_dq_kernel<false, 192>),
+                                       dq_smem_bytes<192>())) != FGQA_OK)
+            return st;
+    } else {
+        if ((st = set_kernel_smem_once(10 + swa, kv_fn[swa], kKvSmemBytes)) != FGQA_OK) return st;
+        if ((st = set_kernel_smem_once(12 + swa, q_fn[swa], kDqSmemBytes)) != FGQA_OK) return st;
+        if ((st = set_kernel_smem_once(14 + swa, q2_fn[swa], 2 * kDqSmemBytes)) != FGQA_OK) return st;
+    }
 
     if (rows_q > 0) hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)ceil_div(rows_q, 16)), dim3(256), 0, s, p);
+    if (mla) {
+        if (kv_units > 0)
+            hipLaunchKernelGGL((bwd_dkdv_kernel<false, 192>), dim3((unsigned)kv_units), dim3(kBwThreads),
+                               kv_smem_bytes<192>(), s, p);
+        if (q_units > 0)
+            hipLaunchKernelGGL((bwd_dq_kernel<false, 192>), dim3((unsigned)q_units), dim3(kBwThreads),
+                               dq_smem_bytes<192>(), s, p);
+        if (pl.n_hsplit > 1 && rows_kv > 0)
+            hipLaunchKernelGGL(bwd_dkdv_reduce_kernel<192>, dim3((unsigned)ceil_div(rows_kv, 16)), dim3(256), 0, s,
+                               p);
+        if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
+        return FGQA_OK;
+    }
     if (kv_units > 0) {
         if (swa)
-            hipLaunchKernelGGL(bwd_dkdv_kernel<true>, dim3((unsigned)kv_units), dim3(kBwThreads), kKvSmemBytes, s, p);
+            hipLaunchKernelGGL((bwd_dkdv_kernel<true, 128>), dim3((unsigned)kv_units), dim3(kBwThreads), kKvSmemBytes,
+                               s, p);
         else
-            hipLaunchKernelGGL(bwd_dkdv_kernel<false>, dim3((unsigned)kv_units), dim3(kBwThreads), kKvSmemBytes, s, p);
+            hipLaunchKernelGGL((bwd_dkdv_kernel<false, 128>), dim3((unsigned)kv_units), dim3(kBwThreads), kKvSmemBytes,
+                               s, p);
     }
     if (q_units > 0 && dq_split) {
         if (swa)
@@ -873,12 +1037,14 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
                                2 * kDqSmemBytes, s, p);
     } else if (q_units > 0) {
         if (swa)
-            hipLaunchKernelGGL(bwd_dq_kernel<true>, dim3((unsigned)q_units), dim3(kBwThreads), kDqSmemBytes, s, p);
+            hipLaunchKernelGGL((bwd_dq_kernel<true, 128>), dim3((unsigned)q_units), dim3(kBwThreads), kDqSmemBytes, s,
+                               p);
         else
-            hipLaunchKernelGGL(bwd_dq_kernel<false>, dim3((unsigned)q_units), dim3(kBwThreads), kDqSmemBytes, s, p);
+            hipLaunchKernelGGL((bwd_dq_kernel<false, 128>), dim3((unsigned)q_units), dim3(kBwThreads), kDqSmemBytes, s,
+                               p);
     }
     if (pl.n_hsplit > 1 && rows_kv > 0)
-        hipLaunchKernelGGL(bwd_dkdv_reduce_kernel, dim3((unsigned)ceil_div(rows_kv, 16)), dim3(256), 0, s, p);
+        hipLaunchKernelGGL(bwd_dkdv_reduce_kernel<128>, dim3((unsigned)ceil_div(rows_kv, 16)), dim3(256), 0, s, p);
     if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
     return FGQA_OK;
 }

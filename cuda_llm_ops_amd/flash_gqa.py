@@ -565,6 +565,7 @@ def _backward_args(q, k, v, o, lse, grad_o, dq, dk, dv, scale, causal, layout, w
     a.causal = 1 if causal else 0
     a.scale = float(scale)
     a.window_size = int(window_size)
+    a.head_dim_v = int(v.shape[-1])
     a.q_stride[:] = sbh(q)
     a.k_stride[:] = sbh(k)
     a.v_stride[:] = sbh(v)
@@ -580,22 +581,23 @@ def _backward_args(q, k, v, o, lse, grad_o, dq, dk, dv, scale, causal, layout, w
 
 
 def backward_workspace_bytes(batch, seqlen_q, seqlen_kv, num_q_heads, num_kv_heads, head_dim=128,
-                             window_size=0) -> int:
+                             window_size=0, head_dim_v=0) -> int:
     """Bytes of scratch ``flash_gqa_backward_bshd`` needs for a caller workspace
     (256-byte aligned; depends on the current device's CU count and on the
-    window: a sliding-window backward needs at most the causal one's)."""
+    window: a sliding-window backward needs at most the causal one's).
+    head_dim 192 with head_dim_v 128: the MLA backward."""
+    dv = int(head_dim_v) or head_dim
     a = _lib.BackwardArgs()
     a.batch, a.seqlen_q, a.seqlen_kv = batch, seqlen_q, seqlen_kv
     a.num_q_heads, a.num_kv_heads, a.head_dim = num_q_heads, num_kv_heads, head_dim
+    a.head_dim_v = dv
     a.causal = 1
     a.window_size = int(window_size)
     a.scale = 1.0
-    qs = [seqlen_q * num_q_heads * head_dim, num_q_heads * head_dim, head_dim]
-    ks = [seqlen_kv * num_kv_heads * head_dim, num_kv_heads * head_dim, head_dim]
-    for name in ("q_stride", "o_stride", "grad_o_stride", "grad_q_stride"):
-        getattr(a, name)[:] = qs
-    for name in ("k_stride", "v_stride", "grad_k_stride", "grad_v_stride"):
-        getattr(a, name)[:] = ks
+    for name, d in (("q_stride", head_dim), ("grad_q_stride", head_dim), ("o_stride", dv), ("grad_o_stride", dv)):
+        getattr(a, name)[:] = [seqlen_q * num_q_heads * d, num_q_heads * d, d]
+    for name, d in (("k_stride", head_dim), ("grad_k_stride", head_dim), ("v_stride", dv), ("grad_v_stride", dv)):
+        getattr(a, name)[:] = [seqlen_kv * num_kv_heads * d, num_kv_heads * d, d]
     n = ctypes.c_size_t(0)
     _lib.check(_lib.lib().fgqa_prefill_backward_workspace_bytes(ctypes.byref(a), ctypes.byref(n)),
                "fgqa_prefill_backward_workspace_bytes")
@@ -621,10 +623,12 @@ def _backward_bshd_prepare(q, k, v, o, lse, grad_o, scale, causal, grad_q, grad_
         raise ValueError("expected 4-D BSHD tensors")
     _require_cuda(q, k, v, o, lse, grad_o)
     B, Sq, Hq, D = q.shape
-    if k.shape != v.shape or k.shape[0] != B or k.shape[3] != D:
-        raise ValueError("K and V must be [B, Skv, Hkv, D] matching Q")
-    if o.shape != q.shape or grad_o.shape != q.shape:
-        raise ValueError("O and grad_o must have Q's shape [B, Sq, Hq, D]")
+    Dv = v.shape[3]
+    if k.shape[:3] != v.shape[:3] or k.shape[0] != B or k.shape[3] != D:
+        raise ValueError("K must be [B, Skv, Hkv, D] matching Q and V [B, Skv, Hkv, Dv]")
+    if o.shape != (B, Sq, Hq, Dv) or grad_o.shape != o.shape:
+        raise ValueError("O and grad_o must be [B, Sq, Hq, Dv] with V's head dim")
+    _check_head_dims(D, Dv, window_size)
     if Hq % k.shape[2] != 0:
         raise ValueError("Query heads must be divisible by KV heads")
     if lse.shape != (B, Hq, Sq) or not lse.is_contiguous():
@@ -666,8 +670,8 @@ def prepare_backward(q, k, v, o, lse, grad_o, scale=None, causal=True,
 
 
 def _launch_bhsd_backward(kind, q, k, v, o, lse, grad_o, scale, causal, window_size):
-    """Shared body of the GQA and SWA backward mirrors: the reference's checks
-    and messages (``kind`` is "GQA" or "SWA"), then one C ABI call."""
+    """Shared body of the GQA, SWA and MLA backward mirrors: the reference's
+    checks and messages (``kind`` is "GQA", "SWA" or "MLA"), then one C ABI call."""
     if (q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16
             or o.dtype != torch.bfloat16 or grad_o.dtype != torch.bfloat16):
         raise ValueError(f"Flash {kind} backward expects bf16 inputs and grad_o")
@@ -715,7 +719,9 @@ def _launch_bhsd_backward(kind, q, k, v, o, lse, grad_o, scale, causal, window_s
             raise ValueError("window_size must be positive")
     if any(t.shape[0] != batch for t in (kb, vb, ob, gb)):
         raise ValueError("Q, K, V, O, and grad_o must share batch dimension")
-    if head_dim_v != head_dim_qk:
+    if kind == "MLA":
+        _check_head_dims(head_dim_qk, head_dim_v)
+    elif head_dim_v != head_dim_qk:
         raise ValueError("head_dim_v must equal head_dim_qk on this path")
     _require_cuda(qb, kb, vb, ob, lse_b, gb)
     if scale is None:
@@ -748,6 +754,25 @@ def launch_flash_gqa_backward_bf16_kernel(q, k, v, o, lse, grad_o, scale=None, c
     """
     del block_kv, num_warps, num_stages
     return _launch_bhsd_backward("GQA", q, k, v, o, lse, grad_o, scale, causal, 0)
+
+
+def launch_flash_mla_backward_bf16_kernel(q, k, v, o, lse, grad_o, scale=None, causal=True,
+                                          block_kv=64, num_warps=8, num_stages=3):
+    """Mirror of the reference's Triton MLA backward launcher
+    (src/python/Triton/flash_mla_backward_kernel.py:788-969): BHSD q
+    [B,Hq,Sq,192], k [B,Hkv,Skv,192], v [B,Hkv,Skv,128], o/grad_o
+    [B,Hq,Sq,128] (or 3-D), lse [B,Hq,Sq] from the MLA forward; returns bf16
+    (grad_q, grad_k, grad_v) shaped like q, k, v.  The default scale is
+    1/sqrt(head_dim_qk), as in the reference.
+
+    Same checks and ValueError messages as the reference (:836-890).
+    ``block_kv``, ``num_warps`` and ``num_stages`` are Triton tuning knobs,
+    accepted for signature compatibility only.  Beyond the reference, inputs
+    must share the batch dimension and (head_dim_qk, head_dim_v) must be
+    (192, 128) or (128, 128).
+    """
+    del block_kv, num_warps, num_stages
+    return _launch_bhsd_backward("MLA", q, k, v, o, lse, grad_o, scale, causal, 0)
 
 
 def launch_flash_swa_backward_bf16_kernel(q, k, v, o, lse, grad_o, scale=None, window_size=None,

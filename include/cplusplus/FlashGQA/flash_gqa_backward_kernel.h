@@ -79,3 +79,33 @@ void LaunchFlashSwaBackwardBf16Kernel(const bf16_t* q,
                                       int numKvHeads,
                                       int headDim,
                                       int windowSize);
+
+/**
+ * @brief Launches the MLA bf16 prefill backward (BSHD layout): Q/K head dim
+ *        headDimQk, V/O head dim headDimV.
+ *
+ * Counterpart of the reference's Triton MLA backward launcher
+ * (src/python/Triton/flash_mla_backward_kernel.py:788-969, kernel :202-786).
+ * q, gradQ [B, Sq, Hq, headDimQk]; k, gradK [B, Skv, Hkv, headDimQk];
+ * v, gradV [B, Skv, Hkv, headDimV]; o, gradO [B, Sq, Hq, headDimV]; lse from
+ * LaunchFlashMlaForwardBf16Kernel.  (headDimQk, headDimV) is (192, 128) or
+ * (128, 128).  Other parameters as LaunchFlashGqaBackwardBf16Kernel.
+ */
+void LaunchFlashMlaBackwardBf16Kernel(const bf16_t* q,
+                                      const bf16_t* k,
+                                      const bf16_t* v,
+                                      const bf16_t* o,
+                                      const float* lse,
+                                      const bf16_t* gradO,
+                                      float scale,
+                                      bf16_t* gradQ,
+                                      bf16_t* gradK,
+                                      bf16_t* gradV,
+                                      int batchSize,
+                                      int seqLengthQ,
+                                      int seqLengthKv,
+                                      int numQueryHeads,
+                                      int numKvHeads,
+                                      int headDimQk,
+                                      int headDimV,
+                                      bool causal);

@@ -220,6 +220,12 @@ int fgqa_prefill_bf16(const fgqa_prefill_args* args, void* stream);
  *   (kernel :157-321): row i uses keys [i - window_size + 1, i].  A sink
  *   needs nothing here: it is in the lse the forward wrote (the reference
  *   computes no sink gradient).
+ * head_dim_v  0 (= head_dim) or the V / O / grad_o head dim.  head_dim 192
+ *   with head_dim_v 128 is the MLA backward, replacing the Triton-only
+ *   launch_flash_mla_backward_bf16_kernel (src/python/Triton/
+ *   flash_mla_backward_kernel.py:788-969, kernel :202-786): q, k, grad_q,
+ *   grad_k have 192-element rows, v, o, grad_o, grad_v 128-element rows.
+ *   Supported: (128, 128) and (192, 128) without a window.
  */
 typedef struct fgqa_prefill_backward_args {
     const void* q;
@@ -250,6 +256,7 @@ typedef struct fgqa_prefill_backward_args {
     void* workspace;
     size_t workspace_bytes;
     int32_t window_size;
+    int32_t head_dim_v;
 } fgqa_prefill_backward_args;
 
 /* Bytes of workspace fgqa_prefill_backward_bf16 needs (pointers unused; the

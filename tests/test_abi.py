@@ -44,7 +44,7 @@ def test_cplusplus_entry_points_exported():
                           "LaunchFlashGqaBf16KernelPaged",
                           "LaunchFlashGqaForwardBf16Kernel", "LaunchFlashGqaForwardBf16KernelStrided",
                           "LaunchFlashGqaBackwardBf16Kernel", "LaunchFlashSwaForwardBf16Kernel",
-                          "LaunchFlashSwaBackwardBf16Kernel",
+                          "LaunchFlashSwaBackwardBf16Kernel", "LaunchFlashMlaBackwardBf16Kernel",
                           "LaunchFlashMlaForwardBf16Kernel", "LaunchFlashSgqaForwardBf16Kernel"}
     for d in decls:
         assert re.search(rf"\bT {d}\(", syms), d
@@ -317,11 +317,13 @@ def _backward_args(**kw):
     a.batch, a.seqlen_q, a.seqlen_kv, a.num_q_heads, a.num_kv_heads, a.head_dim = B, Sq, Skv, Hq, Hkv, D
     a.causal = kw.get("causal", 1)
     a.window_size = kw.get("window", 0)
+    a.head_dim_v = kw.get("Dv", 0)
+    Dv = a.head_dim_v or D
     a.scale = kw.get("scale", D ** -0.5)
-    for name in ("q_stride", "o_stride", "grad_o_stride", "grad_q_stride"):
-        getattr(a, name)[:] = [Sq * Hq * D, Hq * D, D]
-    for name in ("k_stride", "v_stride", "grad_k_stride", "grad_v_stride"):
-        getattr(a, name)[:] = [Skv * Hkv * D, Hkv * D, D]
+    for name, d in (("q_stride", D), ("grad_q_stride", D), ("o_stride", Dv), ("grad_o_stride", Dv)):
+        getattr(a, name)[:] = [Sq * Hq * d, Hq * d, d]
+    for name, d in (("k_stride", D), ("grad_k_stride", D), ("v_stride", Dv), ("grad_v_stride", Dv)):
+        getattr(a, name)[:] = [Skv * Hkv * d, Hkv * d, d]
     for name in ("q", "k", "v", "o", "lse", "grad_o", "grad_q", "grad_k", "grad_v"):
         setattr(a, name, kw.get(name, 4096))
     return a
@@ -337,6 +339,10 @@ def _backward_args(**kw):
     (dict(grad_v=4096 + 4), _lib.FGQA_ERR_UNSUPPORTED),
     (dict(window=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(window=64, causal=0), _lib.FGQA_ERR_INVALID_ARGUMENT),   # the window is causal only
+    (dict(D=192, Dv=64), _lib.FGQA_ERR_UNSUPPORTED),               # MLA is (192, 128) only
+    (dict(D=192, Dv=128, window=64), _lib.FGQA_ERR_UNSUPPORTED),   # no MLA window form
+    (dict(D=128, Dv=192), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(Dv=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
 ])
 def test_backward_rejects_before_launch(kw, code):
     assert _lib.lib().fgqa_prefill_backward_bf16(ctypes.byref(_backward_args(**kw)), None) == code
@@ -475,3 +481,28 @@ def test_cmake_build_matches_make(tmp_path):
                 if " T " in line and ("fgqa_" in line or "Launch" in line or "FlashGqa" in line)}
 
     assert exports(str(b / "libfgqa.so")) == exports(_lib.LIB_PATH)
+
+
+def test_mla_backward_mirror_validation_without_gpu():
+    """The MLA backward mirror raises the reference's ValueErrors
+    (flash_mla_backward_kernel.py:837-890) before touching a GPU."""
+    import torch
+    bf = torch.bfloat16
+    q = torch.zeros(2, 4, 64, 192, dtype=bf)
+    k = torch.zeros(2, 2, 64, 192, dtype=bf)
+    v = torch.zeros(2, 2, 64, 128, dtype=bf)
+    o = torch.zeros(2, 4, 64, 128, dtype=bf)
+    lse = torch.zeros(2, 4, 64, dtype=torch.float32)
+    f = fg.launch_flash_mla_backward_bf16_kernel
+    with pytest.raises(ValueError, match="Flash MLA backward expects bf16 inputs and grad_o"):
+        f(q, k, v, o, lse, o.half())
+    with pytest.raises(ValueError, match="Flash MLA backward expects lse to be float32"):
+        f(q, k, v, o, lse.double(), o)
+    with pytest.raises(ValueError, match="Q and K must share head_dim_qk"):
+        f(q, k[..., :128], v, o, lse, o)
+    with pytest.raises(ValueError, match="O and grad_o must share head_dim_v with V"):
+        f(q, k, v, q, lse, o)
+    with pytest.raises(ValueError, match="not supported"):
+        f(q[..., :160], k[..., :160], v, o, lse, o)
+    with pytest.raises(ValueError, match="GPU"):
+        f(q, k, v, o, lse, o)
