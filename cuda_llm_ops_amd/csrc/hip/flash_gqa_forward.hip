@@ -15,7 +15,9 @@
 //                         unit's KV range side by side (2 waves per SIMD) and
 //                         merge their partial (max, sum, O) through LDS.  Used
 //                         when there are too few units to keep every CU busy
-//                         with two workgroups until the end.
+//                         with two workgroups until the end.  The groups run
+//                         ping-pong: while one wave of a SIMD issues the MFMAs
+//                         of a tile, the other runs the softmax of its own.
 //
 // Per wave (32 rows) and 64-token K/V tile j, software pipelined one tile ahead:
 //   phase A: S^T(j+1) = K(j+1) . Q^T          v_mfma_f32_32x32x16_bf16, K from LDS,
@@ -411,16 +413,82 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         wait_vmem();
         __syncthreads();
     };
-    f32x16_t sa[2], sb[2];
-    if (n_tiles > 0) {
-        qk(sa, 0);
-        mask(sa, 0);
-        update_max(rowmax(sa));
-    }
-    __syncthreads();   // every wave has read K(0) before step 0 refills its buffer
-    for (int j = 0; j < n_tiles; j += 2) {
-        step(sa, sb, j);
-        if (j + 1 < n_tiles) step(sb, sa, j + 1);
+    if constexpr (kGroups == 2) {
+        // Ping-pong: the two waves of a SIMD (one per group) alternate an
+        // MFMA phase (S(j+1) = K(j+1).Q^T and O += V(j).P(j), with their LDS
+        // reads) and a VALU phase (mask, row max, exp2, sums and bf16 P of
+        // S(j+1), then the tile loads for the MFMA phase after next), group 1
+        // one phase behind group 0, with a workgroup barrier between phases.
+        // Both groups pass the same number of barriers: group 1 computes S(0)
+        // in an extra leading phase, group 0 ends with an empty one.
+        f32x16_t s[2];
+        if (grp == 0 && n_tiles > 0) qk(s, 0);
+        __syncthreads();
+        if (grp == 1) {
+            if (n_tiles > 0) qk(s, 0);
+            __syncthreads();              // both groups' S(0) phases are past: K(0) is free
+        }
+        // S(j+1) -> P(j+1); then K(j+3) and V(j+2) go into the buffers that
+        // the MFMA phase j has just finished reading.
+        auto vphase = [&](int j) {
+            mask(s, j + 1);
+            update_max(rowmax(s));
+            softmax_p(s);
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) asm volatile("" : "+v"(pop[kb]));
+            asm volatile("" : "+v"(l_run));
+            wait_vmem();                  // K(j+2), V(j+1), issued one VALU phase ago
+            if (j + 3 < n_tiles) issue_tile(j + 3, (j + 1) & 1, -1);
+            if (j + 2 < n_tiles) issue_tile(j + 2, -1, j & 1);
+            __syncthreads();
+        };
+        // S(j+1) (unless this is the last tile) and O += V(j).P(j): K reads
+        // run 4 MFMAs ahead, V reads 4 ahead at 2 per MFMA.
+        auto mphase = [&](auto with_qk, int j) {
+            constexpr int kA = decltype(with_qk)::value ? 2 * D::kSteps : 0;
+            if constexpr (kA > 0) qk(s, (j + 1) & 1);
+            pv(j & 1);
+            if constexpr (kA > 0) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // DS read
+#pragma unroll
+                for (int i = 0; i < kA - 4; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                }
+            } else {
+                __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (i < 12) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            }
+            __syncthreads();
+        };
+        vphase(-1);
+        for (int j = 0; j + 1 < n_tiles; ++j) {
+            mphase(std::true_type{}, j);
+            vphase(j);
+        }
+        if (n_tiles > 0) mphase(std::false_type{}, n_tiles - 1);
+        if (grp == 0) __syncthreads();
+    } else {
+        f32x16_t sa[2], sb[2];
+        if (n_tiles > 0) {
+            qk(sa, 0);
+            mask(sa, 0);
+            update_max(rowmax(sa));
+        }
+        __syncthreads();   // every wave has read K(0) before step 0 refills its buffer
+        for (int j = 0; j < n_tiles; j += 2) {
+            step(sa, sb, j);
+            if (j + 1 < n_tiles) step(sb, sa, j + 1);
+        }
     }
 
     if constexpr (kGroups == 2) {
