@@ -62,26 +62,39 @@ def _normal(shape, seed, sigma, dev):
     return x.to(torch.bfloat16)
 
 
-def _time_calls(fn, steps, warmup):
-    """Per-call durations (ms) from HIP events on torch's current stream, which
-    is the stream every launch of the library goes to."""
+# The auxiliary measurements each follow an idle gap (the CPU baseline, the
+# previous mode's setup): they warm up for at least this long.
+AUX_WARM_MS = 25.0
+
+
+def _time_calls(fn, steps, warmup, min_warm_ms=0.0):
+    """Times `steps` back-to-back calls with HIP events on torch's current
+    stream (the stream every launch of the library goes to): one event before
+    the first call, one after each, so call i lasts from event i to event i+1
+    and no gap is left between calls.  Returns the total (ms) and the sorted
+    per-call durations.  Before that: `warmup` untimed calls, then more untimed
+    calls until `min_warm_ms` of them have run (an idle GPU takes milliseconds
+    to bring its clock back up)."""
+    import time
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
+    if min_warm_ms > 0:
+        t0 = time.perf_counter()
+        while (time.perf_counter() - t0) * 1e3 < min_warm_ms:
+            for _ in range(4):
+                fn()
+            torch.cuda.synchronize()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     torch.cuda.synchronize()
-    t_start.record()
-    for a, b in evs:
-        a.record()
+    evs[0].record()
+    for i in range(steps):
         fn()
-        b.record()
-    t_end.record()
+        evs[i + 1].record()
     torch.cuda.synchronize()
-    per = sorted(a.elapsed_time(b) for a, b in evs)
-    return t_start.elapsed_time(t_end), per
+    per = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(steps))
+    return evs[0].elapsed_time(evs[steps]), per
 
 
 def _decode_setup(cfg, dev, seed=2):
@@ -137,7 +150,7 @@ def bench_prefill(cfg_id, steps, warmup, dev):
 
     step = fg.prepare_prefill(q, k, v, SCALE, out=out, lse=lse, causal=True)
 
-    total_ms, per = _time_calls(step, steps, warmup)
+    total_ms, per = _time_calls(step, steps, warmup, min_warm_ms=AUX_WARM_MS)
     # the reference's causal-halved count (test_flash_gqa_kernel.py:282-301)
     flops = B * Hq * 2 * S * S * (128 + 128) // 2
     avg = sum(per) / len(per)
@@ -192,7 +205,7 @@ def hbm_copy(steps, warmup, dev, nbytes=1 << 30):
     import torch
     src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).normal_()
     dst = torch.empty_like(src)
-    total_ms, per = _time_calls(lambda: dst.copy_(src), steps, warmup)
+    total_ms, per = _time_calls(lambda: dst.copy_(src), steps, warmup, min_warm_ms=AUX_WARM_MS)
     avg = sum(per) / len(per)
     return dict(bytes_read=nbytes, bytes_written=nbytes, us_avg=avg * 1e3,
                 read_plus_write_GBs=2 * nbytes / (avg * 1e-3) / 1e9)
@@ -231,7 +244,7 @@ def bench_paged(cfg_id, steps, warmup, dev, page_size=16, kv="bf16"):
     ws = torch.empty(max(n_ws, 256), dtype=torch.uint8, device=dev)
     step = fg.prepare_decode_paged(q, kc, vc, table, sl, SCALE, k_scale=k_scale, v_scale=v_scale, out=out,
                                    workspace=ws)
-    total_ms, per = _time_calls(step, steps, warmup)
+    total_ms, per = _time_calls(step, steps, warmup, min_warm_ms=AUX_WARM_MS)
     elem = 1 if kv == "fp8" else 2
     kv_bytes = 2 * int(lens.sum()) * Hkv * 128 * elem
     avg = sum(per) / len(per)
@@ -256,7 +269,7 @@ def bench_swa(steps, warmup, dev, window=512):
     out = torch.empty_like(q)
     lse = torch.empty((B, Hq, S), dtype=torch.float32, device=dev)
     step = fg.prepare_prefill(q, k, v, SCALE, out=out, lse=lse, causal=True, window_size=window, sink=sink)
-    total_ms, per = _time_calls(step, steps, warmup)
+    total_ms, per = _time_calls(step, steps, warmup, min_warm_ms=AUX_WARM_MS)
     # the reference's count (test_flash_swa_kernel.py:318-337)
     flops = B * Hq * 2 * S * window * (128 + 128)
     avg = sum(per) / len(per)
@@ -283,7 +296,7 @@ def bench_mla(steps, warmup, dev):
     out = torch.empty((B, S, Hq, Dv), dtype=torch.bfloat16, device=dev)
     lse = torch.empty((B, Hq, S), dtype=torch.float32, device=dev)
     step = fg.prepare_prefill(q, k, v, 1.0 / math.sqrt(Dqk), out=out, lse=lse, causal=True)
-    total_ms, per = _time_calls(step, steps, warmup)
+    total_ms, per = _time_calls(step, steps, warmup, min_warm_ms=AUX_WARM_MS)
     # the reference's causal-halved count (test_flash_mla_kernel.py:282-301)
     flops = B * Hq * 2 * S * S * (Dqk + Dv) // 2
     avg = sum(per) / len(per)
@@ -330,7 +343,7 @@ def bench_sparse(steps, warmup, dev):
     out = torch.empty_like(q)
     lse = torch.empty((B, Hq, S), dtype=torch.float32, device=dev)
     step = fg.prepare_sparse_prefill(q, k, v, idx, SCALE, out=out, lse=lse, causal=True)
-    total_ms, per = _time_calls(step, steps, warmup)
+    total_ms, per = _time_calls(step, steps, warmup, min_warm_ms=AUX_WARM_MS)
     # the reference's count (test_flash_sgqa_kernel.py:488-506)
     flops = 2 * B * Hq * S * n * (128 + 128)
     # K and V rows gathered per launch (one 256-byte K row and V row per list entry,
@@ -364,7 +377,7 @@ def bench_backward(cfg_id, steps, warmup, dev):
     ws = torch.empty(max(n_ws, 256), dtype=torch.uint8, device=dev)
     step = fg.prepare_backward(q, k, v, out, lse, do, SCALE, causal=True, workspace=ws)
 
-    total_ms, per = _time_calls(step, steps, warmup)
+    total_ms, per = _time_calls(step, steps, warmup, min_warm_ms=AUX_WARM_MS)
     # the reference's count, QK + dP + dQ + dK + dV causal-halved
     # (test_flash_gqa_kernel.py:344-363); the kernels execute 7 such GEMMs
     # (S and dP are recomputed by the dQ pass), 7/5 of it
@@ -398,7 +411,7 @@ def bench_swa_backward(steps, warmup, dev, window=512):
     n_ws = fg.backward_workspace_bytes(B, S, S, Hq, Hkv, window_size=window)
     ws = torch.empty(max(n_ws, 256), dtype=torch.uint8, device=dev)
     step = fg.prepare_backward(q, k, v, out, lse, do, SCALE, causal=True, workspace=ws, window_size=window)
-    total_ms, per = _time_calls(step, steps, warmup)
+    total_ms, per = _time_calls(step, steps, warmup, min_warm_ms=AUX_WARM_MS)
     # the reference's count, QK + dP + dQ + dK + dV over the window
     # (test_flash_swa_kernel.py:400-420); the kernels execute 7 such GEMMs
     flops = B * Hq * 2 * S * window * (3 * 128 + 2 * 128)
@@ -433,7 +446,7 @@ def bench_mla_backward(steps, warmup, dev):
     n_ws = fg.backward_workspace_bytes(B, S, S, Hq, Hkv, head_dim=Dqk, head_dim_v=Dv)
     ws = torch.empty(max(n_ws, 256), dtype=torch.uint8, device=dev)
     step = fg.prepare_backward(q, k, v, out, lse, do, scale, causal=True, workspace=ws)
-    total_ms, per = _time_calls(step, steps, warmup)
+    total_ms, per = _time_calls(step, steps, warmup, min_warm_ms=AUX_WARM_MS)
     # the reference's causal-halved count, QK + dP + dQ + dK + dV
     # (test_flash_mla_kernel.py:344-363); the kernels execute S and dP twice
     flops = B * Hq * 2 * S * S * (3 * Dqk + 2 * Dv) // 2
@@ -452,7 +465,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=150)
     ap.add_argument("--split-tokens", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")

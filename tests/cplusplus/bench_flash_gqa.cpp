@@ -28,6 +28,7 @@
 #include <omp.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -113,8 +114,22 @@ Stats time_launches(F&& launch, int warmup, int iters) {
     hipEvent_t e0, e1;
     HIP_CHECK(hipEventCreate(&e0));
     HIP_CHECK(hipEventCreate(&e1));
+    // at least `warmup` launches, and at least 20 ms of them: the CPU check of
+    // the previous configuration leaves the GPU idle for seconds, and its
+    // clock takes milliseconds to come back up
     for (int i = 0; i < warmup; ++i) launch();
     HIP_CHECK(hipDeviceSynchronize());
+    {
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int i = 0; i < 4000; ++i) {
+            launch();
+            if ((i & 7) == 7) {
+                HIP_CHECK(hipDeviceSynchronize());
+                if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(20)) break;
+            }
+        }
+        HIP_CHECK(hipDeviceSynchronize());
+    }
     std::vector<double> us;
     for (int i = 0; i < iters; ++i) {
         HIP_CHECK(hipEventRecord(e0, nullptr));
