@@ -68,13 +68,15 @@ AUX_WARM_MS = 25.0
 
 
 def _time_calls(fn, steps, warmup, min_warm_ms=0.0):
-    """Times `steps` back-to-back calls with HIP events on torch's current
-    stream (the stream every launch of the library goes to): one event before
-    the first call, one after each, so call i lasts from event i to event i+1
-    and no gap is left between calls.  Returns the total (ms) and the sorted
-    per-call durations.  Before that: `warmup` untimed calls, then more untimed
-    calls until `min_warm_ms` of them have run (an idle GPU takes milliseconds
-    to bring its clock back up)."""
+    """Times `steps` calls issued back to back between two HIP events on
+    torch's current stream (the stream every launch of the library goes to),
+    with a synchronize on both sides: the total (ms) over the timed region, so
+    total / steps is the average launch duration.  Then the same number of
+    calls again, each between events of its own, for the sorted per-call
+    durations (median and minimum; those events add a gap per call, so they
+    are not used for the average).  Before the timed region: `warmup`
+    untimed calls, then more until `min_warm_ms` of them have run (an idle GPU
+    takes milliseconds to bring its clock back up)."""
     import time
     import torch
     for _ in range(warmup):
@@ -86,15 +88,23 @@ def _time_calls(fn, steps, warmup, min_warm_ms=0.0):
             for _ in range(4):
                 fn()
             torch.cuda.synchronize()
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    evs[0].record()
-    for i in range(steps):
+    t_start.record()
+    for _ in range(steps):
         fn()
-        evs[i + 1].record()
+    t_end.record()
     torch.cuda.synchronize()
-    per = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(steps))
-    return evs[0].elapsed_time(evs[steps]), per
+    total = t_start.elapsed_time(t_end)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in evs:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    per = sorted(a.elapsed_time(b) for a, b in evs)
+    return total, per
 
 
 def _decode_setup(cfg, dev, seed=2):
@@ -130,7 +140,7 @@ def bench_decode(cfg_id, steps, warmup, split_tokens, dev):
 
     total_ms, per = _time_calls(step, steps, warmup)
     ms_step = total_ms / steps
-    avg_launch_ms = sum(per) / len(per)
+    avg_launch_ms = total_ms / steps
     qo_bytes = 2 * cfg["B"] * cfg["Hq"] * 128 * 2
     return dict(cfg=cfg, q=q, k=k, v=v, lens=lens, out=out, kv_bytes=kv_bytes, qo_bytes=qo_bytes,
                 ms_step=ms_step, avg_launch_ms=avg_launch_ms, median_ms=per[len(per) // 2], min_ms=per[0])
@@ -153,7 +163,7 @@ def bench_prefill(cfg_id, steps, warmup, dev):
     total_ms, per = _time_calls(step, steps, warmup, min_warm_ms=AUX_WARM_MS)
     # the reference's causal-halved count (test_flash_gqa_kernel.py:282-301)
     flops = B * Hq * 2 * S * S * (128 + 128) // 2
-    avg = sum(per) / len(per)
+    avg = total_ms / steps
     tflops = flops / (avg * 1e-3) / 1e12
     return dict(config=f"causal prefill B={B} S={S} Hq={Hq} Hkv={Hkv} D=128 (BASELINE config {cfg_id})",
                 us_avg=round(avg * 1e3, 2), us_median=round(per[len(per) // 2] * 1e3, 2),
@@ -206,7 +216,7 @@ def hbm_copy(steps, warmup, dev, nbytes=1 << 30):
     src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).normal_()
     dst = torch.empty_like(src)
     total_ms, per = _time_calls(lambda: dst.copy_(src), steps, warmup, min_warm_ms=AUX_WARM_MS)
-    avg = sum(per) / len(per)
+    avg = total_ms / steps
     return dict(bytes_read=nbytes, bytes_written=nbytes, us_avg=avg * 1e3,
                 read_plus_write_GBs=2 * nbytes / (avg * 1e-3) / 1e9)
 
@@ -247,7 +257,7 @@ def bench_paged(cfg_id, steps, warmup, dev, page_size=16, kv="bf16"):
     total_ms, per = _time_calls(step, steps, warmup, min_warm_ms=AUX_WARM_MS)
     elem = 1 if kv == "fp8" else 2
     kv_bytes = 2 * int(lens.sum()) * Hkv * 128 * elem
-    avg = sum(per) / len(per)
+    avg = total_ms / steps
     gbs = kv_bytes / (avg * 1e-3) / 1e9
     return dict(config=f"paged decode, BASELINE config {cfg_id} lengths, page {page_size}, {kv} KV",
                 us_avg=round(avg * 1e3, 2), kv_bytes=kv_bytes, GBs=round(gbs, 1),
@@ -272,7 +282,7 @@ def bench_swa(steps, warmup, dev, window=512):
     total_ms, per = _time_calls(step, steps, warmup, min_warm_ms=AUX_WARM_MS)
     # the reference's count (test_flash_swa_kernel.py:318-337)
     flops = B * Hq * 2 * S * window * (128 + 128)
-    avg = sum(per) / len(per)
+    avg = total_ms / steps
     tflops = flops / (avg * 1e-3) / 1e12
     return dict(config=f"sliding-window prefill with sink, B={B} S={S} Hq={Hq} Hkv={Hkv} D=128 window={window}",
                 us_avg=round(avg * 1e3, 2), us_min=round(per[0] * 1e3, 2),
@@ -299,7 +309,7 @@ def bench_mla(steps, warmup, dev):
     total_ms, per = _time_calls(step, steps, warmup, min_warm_ms=AUX_WARM_MS)
     # the reference's causal-halved count (test_flash_mla_kernel.py:282-301)
     flops = B * Hq * 2 * S * S * (Dqk + Dv) // 2
-    avg = sum(per) / len(per)
+    avg = total_ms / steps
     tflops = flops / (avg * 1e-3) / 1e12
     return dict(config=f"MLA causal prefill B={B} S={S} Hq={Hq} Hkv={Hkv} Dqk={Dqk} Dv={Dv}",
                 us_avg=round(avg * 1e3, 2), us_median=round(per[len(per) // 2] * 1e3, 2),
@@ -349,7 +359,7 @@ def bench_sparse(steps, warmup, dev):
     # K and V rows gathered per launch (one 256-byte K row and V row per list entry,
     # shared by the 16 query heads); served mostly from L2 / MALL
     gathered = B * Hkv * S * n * 2 * 256
-    avg = sum(per) / len(per)
+    avg = total_ms / steps
     tflops = flops / (avg * 1e-3) / 1e12
     return dict(config=f"sparse-index prefill B={B} S={S} Hq={Hq} Hkv={Hkv} D=128 entries={n} causal",
                 us_avg=round(avg * 1e3, 2), us_median=round(per[len(per) // 2] * 1e3, 2),
@@ -382,7 +392,7 @@ def bench_backward(cfg_id, steps, warmup, dev):
     # (test_flash_gqa_kernel.py:344-363); the kernels execute 7 such GEMMs
     # (S and dP are recomputed by the dQ pass), 7/5 of it
     flops = B * Hq * 2 * S * S * (3 * 128 + 2 * 128) // 2
-    avg = sum(per) / len(per)
+    avg = total_ms / steps
     tflops = flops / (avg * 1e-3) / 1e12
     return dict(config=f"causal prefill backward B={B} S={S} Hq={Hq} Hkv={Hkv} D=128 (BASELINE config {cfg_id} shape)",
                 us_avg=round(avg * 1e3, 2), us_median=round(per[len(per) // 2] * 1e3, 2),
@@ -415,7 +425,7 @@ def bench_swa_backward(steps, warmup, dev, window=512):
     # the reference's count, QK + dP + dQ + dK + dV over the window
     # (test_flash_swa_kernel.py:400-420); the kernels execute 7 such GEMMs
     flops = B * Hq * 2 * S * window * (3 * 128 + 2 * 128)
-    avg = sum(per) / len(per)
+    avg = total_ms / steps
     tflops = flops / (avg * 1e-3) / 1e12
     return dict(config=f"sliding-window prefill backward, B={B} S={S} Hq={Hq} Hkv={Hkv} D=128 window={window}",
                 us_avg=round(avg * 1e3, 2), us_median=round(per[len(per) // 2] * 1e3, 2),
@@ -450,7 +460,7 @@ def bench_mla_backward(steps, warmup, dev):
     # the reference's causal-halved count, QK + dP + dQ + dK + dV
     # (test_flash_mla_kernel.py:344-363); the kernels execute S and dP twice
     flops = B * Hq * 2 * S * S * (3 * Dqk + 2 * Dv) // 2
-    avg = sum(per) / len(per)
+    avg = total_ms / steps
     tflops = flops / (avg * 1e-3) / 1e12
     return dict(config=f"MLA causal prefill backward, B={B} S={S} Hq={Hq} Hkv={Hkv} Dqk={Dqk} Dv={Dv}",
                 us_avg=round(avg * 1e3, 2), us_median=round(per[len(per) // 2] * 1e3, 2),
