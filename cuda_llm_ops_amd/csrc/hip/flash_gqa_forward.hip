@@ -215,7 +215,8 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
             static_for<D::kDmaK>([&](auto ic) {
                 constexpr int i = decltype(ic)::value;
                 if (kb >= 0) dma16(ic, kdst, koff_dma[i], (uint32_t)t0 * kss, krs);
-                if (i < 4 && vb >= 0) dma16(ic, vdst, voff_dma[i], (uint32_t)t0 * vss, vrs);
+                if constexpr (i < 4)
+                    if (vb >= 0) dma16(ic, vdst, voff_dma[i], (uint32_t)t0 * vss, vrs);
             });
         } else {   // last tile: rows past the last key are clamped to it
             static_for<D::kDmaK>([&](auto ic) {
@@ -224,7 +225,7 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
                     const uint32_t tok = (uint32_t)min(t0 + krow_dma[i], kv_last);
                     dma16(ic, kdst, tok * kss + kcol_dma[i], 0u, krs);
                 }
-                if (i < 4 && vb >= 0) {
+                if (vb >= 0 && i < 4) {
                     const int r = 4 * (wave + 4 * i) + (lane >> 4);
                     const uint32_t tok = (uint32_t)min(t0 + r, kv_last);
                     dma16(ic, vdst, tok * vss + ((l16 ^ (4 * (r & 3))) << 4), 0u, vrs);
