@@ -18,6 +18,9 @@
 //                         with two workgroups until the end.  The groups run
 //                         ping-pong: while one wave of a SIMD issues the MFMAs
 //                         of a tile, the other runs the softmax of its own.
+//                         With head dim 128 it stages the unit's Q tile (once
+//                         for both groups) and its O tile through 32 KB of LDS,
+//                         so those global loads and stores move whole rows.
 //
 // Per wave (32 rows) and 64-token K/V tile j, software pipelined one tile ahead:
 //   phase A: S^T(j+1) = K(j+1) . Q^T          v_mfma_f32_32x32x16_bf16, K from LDS,
@@ -45,6 +48,7 @@
 
 #include "fgqa_device.h"
 #include "fgqa_internal.h"
+
 
 namespace fgqa {
 
@@ -87,6 +91,10 @@ constexpr int kPfVTileBytes = kPfTile * kPfVRowBytes;  // 16 KB
 constexpr float kPfRescaleSlack = 8.f;                 // log2 units: P <= 2^8 between rescales
 // merge area of the split kernel: per wave, 64 O values + max + sum per lane
 constexpr int kPfMergeFloats = 66;
+// Q tile of a unit staged in LDS by the split kernel (head dim 128): 4 waves x
+// 32 rows x 256 bytes, after the two groups' tile buffers (2 x 64 KB + 32 KB =
+// the CU's 160 KB).
+constexpr int kPfQStageBytes = kPfWaves * 32 * kHeadDim * 2;
 
 // Sizes that depend on the Q/K head dim kDk (128, or 192 for MLA).
 template <int kDk>
@@ -151,15 +159,21 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     const int kv_hi = min(kv_end, (t_first + n_tiles) * kPfTile);
 
     // Q^T as the B operand: lane holds Q[q0w + l32][16*kk + 8*g2 .. +7]; rows >= sq read as 0.
+    // The split kernel (head dim 128) stages the unit's Q tile in LDS first
+    // (kStageQ below): a direct load puts 32 rows 4 KB apart (BSHD) into
+    // one instruction, 32 bytes each, and both groups would load the same rows.
+    constexpr bool kStageQ = kGroups == 2 && kDk == kHeadDim;
     const uint32_t qss = (uint32_t)(p.q_ss * 2);
     const __amdgpu_buffer_rsrc_t qrs =
         make_rsrc(p.q + b * p.q_sb + h * p.q_sh, (uint32_t)(p.sq - 1) * qss + D::kRowBytes);
     bf16x8_t qop[D::kSteps];
+    if constexpr (!kStageQ) {
 #pragma unroll
-    for (int kk = 0; kk < D::kSteps; ++kk) {
-        u32x4_t t = buf_load16(qrs, (uint32_t)qrow * qss + (kk * 16 + g2 * 8) * 2);
-        t ^= p.q_sign;
-        qop[kk] = as_bf16x8(t);
+        for (int kk = 0; kk < D::kSteps; ++kk) {
+            u32x4_t t = buf_load16(qrs, (uint32_t)qrow * qss + (kk * 16 + g2 * 8) * 2);
+            t ^= p.q_sign;
+            qop[kk] = as_bf16x8(t);
+        }
     }
 
     // Direct K/V tile loads.  Rows past the last key are clamped to it (their
@@ -291,13 +305,29 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         }
     };
     // Row max of S(j) (log2 units) across both wave halves.
+    // The split kernel's softmax phase runs on a SIMD whose other wave issues
+    // MFMAs, so its reductions use four independent chains (the serial chain
+    // costs the latency of each step); the whole-range kernel keeps one chain,
+    // which needs fewer registers.
     auto rowmax = [&](f32x16_t (&s)[2]) {
-        float tmax = s[0][0];
+        float tmax;
+        if constexpr (kGroups == 2) {
+            float pm[4];
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
+            for (int t = 0; t < 4; ++t) {
+                pm[t] = s[t >> 1][(t & 1) * 8];
 #pragma unroll
-            for (int i = 0; i < 16; ++i)
-                if (tb != 0 || i != 0) tmax = fmaxf(tmax, s[tb][i]);
+                for (int i = 1; i < 8; ++i) pm[t] = fmaxf(pm[t], s[t >> 1][(t & 1) * 8 + i]);
+            }
+            tmax = fmaxf(fmaxf(pm[0], pm[1]), fmaxf(pm[2], pm[3]));
+        } else {
+            tmax = s[0][0];
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (tb != 0 || i != 0) tmax = fmaxf(tmax, s[tb][i]);
+        }
         return half_max(tmax) * c;
     };
     // Move the running max when some row's tile max exceeds it by more than
@@ -318,18 +348,32 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     // exp2(S*scale - max), row sums and the bf16 P^T operands of S(j).
     bf16x8_t pop[4];
     auto softmax_p = [&](f32x16_t (&s)[2]) {
-        float psum = 0.f;
+        if constexpr (kGroups == 2) {
+            float ps[4];
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-            for (int kh = 0; kh < 2; ++kh)
+            for (int t = 0; t < 4; ++t) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float pv = fast_exp2(__builtin_fmaf(s[tb][kh * 8 + e], c, -m_use));
-                    psum += pv;
-                    pop[tb * 2 + kh][e] = (__bf16)pv;
+                    const float pv = fast_exp2(__builtin_fmaf(s[t >> 1][(t & 1) * 8 + e], c, -m_use));
+                    ps[t] = e == 0 ? pv : ps[t] + pv;
+                    pop[t][e] = (__bf16)pv;
                 }
-        l_run += psum;
+            }
+            l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+        } else {
+            float psum = 0.f;
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float pv = fast_exp2(__builtin_fmaf(s[tb][kh * 8 + e], c, -m_use));
+                        psum += pv;
+                        pop[tb * 2 + kh][e] = (__bf16)pv;
+                    }
+            l_run += psum;
+        }
     };
 
     // O^T += V^T(j) . P^T(j) over four 16-token k-blocks.  Slots 0..3 of lane
@@ -368,10 +412,40 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     // branch touches the accumulators (a branch costs register copies), and
     // S(j+1) is computed even on the last step (its tile is fully masked).
     __syncthreads();  // the previous unit may still read the buffers
+    // Staged Q: wave slot w's 32 rows fill 8 KB at kPfQStageBytes/4 * w past
+    // the tile buffers, row r at 256*r with chunk c in slot c ^ (r % 16) (the
+    // K layout).  One load instruction fills 1 KB = 4 whole rows; the wave of
+    // slot w in group g issues instructions 4g .. 4g+3 of its slot's 8, so
+    // each row is fetched once for both groups.
+    [[maybe_unused]] const uint32_t q_lds =
+        lds_base + (2 - grp) * D::kGroupBytes + wave * (kPfQStageBytes / kPfWaves);
+    if constexpr (kStageQ) {
+        auto dmaq = [](auto ic, uint32_t base, uint32_t voffset, __amdgpu_buffer_rsrc_t rsrc) {
+            constexpr int kOff = decltype(ic)::value * 1024;
+            asm volatile("s_add_u32 m0, %0, %3\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                         :: "s"(base), "v"(voffset), "s"(rsrc), "i"(kOff) : "memory", "scc");
+        };
+        static_for<4>([&](auto ic) {
+            const int slot = 64 * (4 * grp + decltype(ic)::value) + lane;
+            const int r = slot >> 4;
+            const uint32_t voff = (uint32_t)(q0w + r) * qss + ((uint32_t)((slot & 15) ^ (r & 15)) << 4);
+            dmaq(ic, q_lds + grp * 4096, voff, qrs);
+        });
+    }
     if (n_tiles > 0) issue_tile(0, 0, 0);
     if (n_tiles > 1) issue_tile(1, 1, -1);
     wait_vmem();
     __syncthreads();
+    if constexpr (kStageQ) {
+        const unsigned char* ql = reinterpret_cast<const unsigned char*>(smem_all) + 2 * D::kGroupBytes +
+                                  wave * (kPfQStageBytes / kPfWaves) + l32 * D::kRowBytes;
+#pragma unroll
+        for (int kk = 0; kk < D::kSteps; ++kk) {
+            u32x4_t t = *reinterpret_cast<const u32x4_t*>(ql + (((2 * kk + g2) ^ (l32 & 15)) << 4));
+            t ^= p.q_sign;
+            qop[kk] = as_bf16x8(t);
+        }
+    }
 
     // One pipelined step.  On entry sc holds the masked S(j) and the running
     // max covers it; on exit sn holds the masked S(j+1), likewise.
@@ -469,6 +543,9 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 if (i < 12) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
             }
+            // all of the phase's MFMAs before its barrier (the scheduler would
+            // otherwise sink the last ones into the softmax phase)
+            __builtin_amdgcn_sched_barrier(0);
             __syncthreads();
         };
         vphase(-1);
@@ -528,9 +605,13 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     const bool has_sink = kSwa && p.sink != nullptr;
     const float sink = has_sink ? p.sink[h] : 0.f;
     const float denom = (l_run > 0.f && has_sink) ? l_run + sink * fast_exp2(-m_use) : l_run;
-    if (qrow < p.sq) {
-        const float inv = (l_run > 0.f) ? 1.f / denom : 0.f;
-        __bf16* orow = p.o + b * p.o_sb + (int64_t)qrow * p.o_ss + h * p.o_sh;
+    const float inv = (l_run > 0.f) ? 1.f / denom : 0.f;
+    if constexpr (kStageQ) {
+        // O goes out through this wave's (now idle) Q area: 8-byte pieces in
+        // (row l32, chunk 4*db + i4, half g2), then whole 256-byte rows, 4 per
+        // store instruction (the accumulator layout would give each store 32
+        // rows 16 bytes each).
+        unsigned char* ol = smem_all + 2 * D::kGroupBytes + wave * (kPfQStageBytes / kPfWaves);
 #pragma unroll
         for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -538,8 +619,33 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
                 bf16x4_t w;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) w[e] = (__bf16)(oacc[db][i4 * 4 + e] * inv);
-                *reinterpret_cast<bf16x4_t*>(orow + db * 32 + i4 * 8 + g2 * 4) = w;
+                *reinterpret_cast<bf16x4_t*>(ol + l32 * kPfVRowBytes + (((4 * db + i4) ^ (l32 & 15)) << 4) + g2 * 8) = w;
             }
+        // this wave's LDS writes complete before its reads (no other wave uses the area)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = 4 * i + (lane >> 4);
+            const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ol + r * kPfVRowBytes + (l16 << 4));
+            if (q0w + r < p.sq) {
+                __bf16* orow = p.o + b * p.o_sb + (int64_t)(q0w + r) * p.o_ss + h * p.o_sh;
+                *reinterpret_cast<u32x4_t*>(orow + ((l16 ^ (r & 15)) << 3)) = v;
+            }
+        }
+    }
+    if (qrow < p.sq) {
+        if constexpr (!kStageQ) {
+            __bf16* orow = p.o + b * p.o_sb + (int64_t)qrow * p.o_ss + h * p.o_sh;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    bf16x4_t w;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) w[e] = (__bf16)(oacc[db][i4 * 4 + e] * inv);
+                    *reinterpret_cast<bf16x4_t*>(orow + db * 32 + i4 * 8 + g2 * 4) = w;
+                }
+        }
         if (p.lse != nullptr && g2 == 0)
             p.lse[((int64_t)b * p.hq + h) * p.sq + qrow] =
                 (l_run > 0.f) ? m_run * kLn2 + logf(denom)
@@ -674,7 +780,8 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
 
     const bool mla = a->head_dim == 192;
     const int group_bytes = mla ? PfDims<192>::kGroupBytes : PfDims<128>::kGroupBytes;
-    const int smem_bytes = (split ? 2 : 1) * group_bytes;
+    // the split kernel with head dim 128 also stages the Q tile in LDS
+    const int smem_bytes = (split ? 2 : 1) * group_bytes + (split && !mla ? kPfQStageBytes : 0);
     // kernel table: plain, window / sink, split, MLA, MLA split
     const int which = mla ? (split ? 4 : 3) : (split ? 2 : (swa ? 1 : 0));
     const void* fns[5] = {reinterpret_cast<const void*>(prefill_kernel<false, 128>),
