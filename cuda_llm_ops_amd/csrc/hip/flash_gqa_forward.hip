@@ -49,7 +49,6 @@
 #include "fgqa_device.h"
 #include "fgqa_internal.h"
 
-
 namespace fgqa {
 
 struct PrefillParams {
@@ -571,21 +570,25 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
 
     if constexpr (kGroups == 2) {
         // Group 1 hands its partial state to group 0 (same wave slot, same lane)
-        // through the tile buffers, idle since the loop's last barrier:
-        // [wave][value][lane] floats.
-        float* mg = reinterpret_cast<float*>(smem_all) + wave * kPfMergeFloats * kWave + lane;
+        // through the tile buffers, idle since the loop's last barrier: per
+        // wave, 16 blocks of [lane][4] O values (one 16-byte access per lane
+        // and block), then [lane] max and [lane] sum.
+        float* mg = reinterpret_cast<float*>(smem_all) + wave * kPfMergeFloats * kWave;
+        f32x4_t* mo = reinterpret_cast<f32x4_t*>(mg) + lane;
         if (grp == 1) {
 #pragma unroll
             for (int db = 0; db < 4; ++db)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) mg[(db * 16 + i) * kWave] = oacc[db][i];
-            mg[64 * kWave] = m_run;
-            mg[65 * kWave] = l_run;
+                for (int i4 = 0; i4 < 4; ++i4)
+                    mo[(db * 4 + i4) * kWave] = f32x4_t{oacc[db][4 * i4], oacc[db][4 * i4 + 1],
+                                                        oacc[db][4 * i4 + 2], oacc[db][4 * i4 + 3]};
+            mg[64 * kWave + lane] = m_run;
+            mg[65 * kWave + lane] = l_run;
         }
         __syncthreads();
         if (grp == 1) return;
-        const float m1 = mg[64 * kWave];
-        const float l1 = mg[65 * kWave];
+        const float m1 = mg[64 * kWave + lane];
+        const float l1 = mg[65 * kWave + lane];
         const float m = fmaxf(m_run, m1);
         const float mu = (m == -INFINITY) ? 0.f : m;
         const float a0 = fast_exp2(m_run - mu);   // 0 when a group saw no key
@@ -593,7 +596,11 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
 #pragma unroll
         for (int db = 0; db < 4; ++db)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) oacc[db][i] = oacc[db][i] * a0 + mg[(db * 16 + i) * kWave] * a1;
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const f32x4_t o1 = mo[(db * 4 + i4) * kWave];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) oacc[db][4 * i4 + e] = oacc[db][4 * i4 + e] * a0 + o1[e] * a1;
+            }
         l_run = l_run * a0 + l1 * a1;
         m_run = m;
         m_use = mu;   // O and the sum are now relative to mu (the sink term uses it)
