@@ -38,7 +38,7 @@ SCALE = 1.0 / math.sqrt(128)
 # changes.
 TRAFFIC_BYTES = {
     "decode_cfg2": 1010662256,   # = Q+K+V+O (1,010,565,120 B) + 0.01 %
-    "prefill_cfg4": 51649536,    # Q+O+LSE 32.25 MiB + K/V 2 MiB fetched once per XCD
+    "prefill_cfg4": 51483996,    # Q+O+LSE 32.25 MiB + K/V 2 MiB fetched once per XCD
 }
 
 DECODE_CONFIGS = {
