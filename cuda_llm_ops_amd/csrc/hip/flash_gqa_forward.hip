@@ -49,6 +49,7 @@
 #include "fgqa_device.h"
 #include "fgqa_internal.h"
 
+
 namespace fgqa {
 
 struct PrefillParams {
@@ -505,6 +506,9 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         // S(j+1) -> P(j+1); then K(j+3) and V(j+2) go into the buffers that
         // the MFMA phase j has just finished reading.
         auto vphase = [&](int j) {
+            // the softmax phase sets the pace: its wave wins issue ties
+            // against the MFMA wave of the same SIMD
+            __builtin_amdgcn_s_setprio(1);
             mask(s, j + 1);
             update_max(rowmax(s));
             softmax_p(s);
@@ -514,6 +518,7 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
             wait_vmem();                  // K(j+2), V(j+1), issued one VALU phase ago
             if (j + 3 < n_tiles) issue_tile(j + 3, (j + 1) & 1, -1);
             if (j + 2 < n_tiles) issue_tile(j + 2, -1, j & 1);
+            __builtin_amdgcn_s_setprio(0);
             __syncthreads();
         };
         // S(j+1) (unless this is the last tile) and O += V(j).P(j): K reads
