@@ -618,15 +618,18 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     const float sink = has_sink ? p.sink[h] : 0.f;
     const float denom = (l_run > 0.f && has_sink) ? l_run + sink * fast_exp2(-m_use) : l_run;
     const float inv = (l_run > 0.f) ? 1.f / denom : 0.f;
-    if constexpr (kGroups == 2) {
-        // O goes out through 8 KB of idle LDS per wave (the wave's Q area, or
-        // with head dim 192 group 1's tile buffers, past the merge area):
+    {
+        // O goes out through 8 KB of idle LDS per wave (the split kernel: the
+        // wave's Q area, or with head dim 192 group 1's tile buffers, past the
+        // merge area; the whole-range kernel: its tile buffers, which every
+        // wave has finished reading at the loop's last barrier):
         // 8-byte pieces in (row l32, chunk 4*db + i4, half g2), then whole
         // 256-byte rows, 4 per store instruction (the accumulator layout would
         // give each store 32 rows 16 bytes each).
-        static_assert(kStageQ || kPfWaves * kPfMergeFloats * kWave * 4 <= D::kGroupBytes,
+        static_assert(kGroups == 1 || kStageQ || kPfWaves * kPfMergeFloats * kWave * 4 <= D::kGroupBytes,
                       "O staging in group 1's buffers must not overlap the merge area");
-        unsigned char* ol = smem_all + (kStageQ ? 2 : 1) * D::kGroupBytes + wave * (kPfQStageBytes / kPfWaves);
+        unsigned char* ol = smem_all + (kGroups == 1 ? 0 : kStageQ ? 2 : 1) * D::kGroupBytes +
+                            wave * (kPfQStageBytes / kPfWaves);
 #pragma unroll
         for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -649,18 +652,6 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         }
     }
     if (qrow < p.sq) {
-        if constexpr (kGroups != 2) {
-            __bf16* orow = p.o + b * p.o_sb + (int64_t)qrow * p.o_ss + h * p.o_sh;
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-#pragma unroll
-                for (int i4 = 0; i4 < 4; ++i4) {
-                    bf16x4_t w;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) w[e] = (__bf16)(oacc[db][i4 * 4 + e] * inv);
-                    *reinterpret_cast<bf16x4_t*>(orow + db * 32 + i4 * 8 + g2 * 4) = w;
-                }
-        }
         if (p.lse != nullptr && g2 == 0)
             p.lse[((int64_t)b * p.hq + h) * p.sq + qrow] =
                 (l_run > 0.f) ? m_run * kLn2 + logf(denom)
