@@ -18,6 +18,11 @@ FGQA_ERR_UNSUPPORTED = -2
 FGQA_ERR_WORKSPACE = -3
 FGQA_ERR_HIP = -4
 
+# fgqa_kernel_choice: the `kernel` / `dq_kernel` fields (0 = automatic)
+FGQA_KERNEL_AUTO = 0
+FGQA_KERNEL_WHOLE = 1
+FGQA_KERNEL_SPLIT = 2
+
 _I64x2 = ctypes.c_int64 * 2
 _I64x3 = ctypes.c_int64 * 3
 
@@ -70,6 +75,7 @@ class PrefillArgs(ctypes.Structure):
         ("window_size", ctypes.c_int32),
         ("sink", ctypes.c_void_p),
         ("head_dim_v", ctypes.c_int32),
+        ("kernel", ctypes.c_int32),
     ]
 
 
@@ -141,6 +147,8 @@ class BackwardArgs(ctypes.Structure):
         ("workspace_bytes", ctypes.c_size_t),
         ("window_size", ctypes.c_int32),
         ("head_dim_v", ctypes.c_int32),
+        ("kv_head_split", ctypes.c_int32),
+        ("dq_kernel", ctypes.c_int32),
     ]
 
 

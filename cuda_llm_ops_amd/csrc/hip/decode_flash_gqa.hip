@@ -754,6 +754,16 @@ DecodeShape shape_of_paged(const fgqa_decode_paged_args* a) {
     return DecodeShape{a->batch, a->max_seqlen, a->num_q_heads, a->num_kv_heads, a->split_tokens, true};
 }
 
+// The paged decode always runs the work-list kernel; a shape the list cannot
+// index (batch >= 2^15 or >= 2^16 splits) is rejected here, so the workspace
+// query and the launch agree and nothing is allocated before the error.
+int plan_paged(const fgqa_decode_paged_args* a, DecodePlan* plan) {
+    const DecodeShape shape = shape_of_paged(a);
+    const int st = plan_decode(&shape, plan);
+    if (st != FGQA_OK) return st;
+    return plan->list ? FGQA_OK : FGQA_ERR_UNSUPPORTED;
+}
+
 }  // namespace
 }  // namespace fgqa
 
@@ -762,8 +772,7 @@ extern "C" int fgqa_decode_paged_workspace_bytes(const fgqa_decode_paged_args* a
     int st = validate_paged(a);
     if (st != FGQA_OK) return st;
     DecodePlan plan;
-    const DecodeShape shape = shape_of_paged(a);
-    st = plan_decode(&shape, &plan);
+    st = plan_paged(a, &plan);
     if (st != FGQA_OK) return st;
     *bytes = plan.ws_bytes;
     return FGQA_OK;
@@ -776,8 +785,7 @@ extern "C" int fgqa_decode_paged(const fgqa_decode_paged_args* a, void* stream) 
     if (st != FGQA_OK) return st;
     if (a->batch == 0) return FGQA_OK;
     DecodePlan plan;
-    const DecodeShape shape = shape_of_paged(a);
-    st = plan_decode(&shape, &plan);
+    st = plan_paged(a, &plan);
     if (st != FGQA_OK) return st;
 
     DecodeParams p;
@@ -836,7 +844,6 @@ extern "C" int fgqa_decode_paged(const fgqa_decode_paged_args* a, void* stream) 
         if (plan.list) work = reinterpret_cast<int32_t*>(w + plan.part_o_bytes + plan.part_ml_bytes);
     }
     p.work = work;
-    if (!plan.list) return FGQA_ERR_UNSUPPORTED;   // batch >= 2^15 or >= 2^16 splits
 
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (a->max_seqlen == 0) {

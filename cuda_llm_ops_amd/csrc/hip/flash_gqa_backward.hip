@@ -36,7 +36,6 @@
 //                      several workgroups: sums their fp32 partial dK/dV.
 #include <math.h>
 #include <stdint.h>
-#include <stdlib.h>
 
 #include <type_traits>
 
@@ -829,6 +828,12 @@ int validate_backward(const fgqa_prefill_backward_args* a) {
     const int dv = a->head_dim_v == 0 ? a->head_dim : a->head_dim_v;
     if (dv != kHeadDim || (a->head_dim != kHeadDim && a->head_dim != 192)) return FGQA_ERR_UNSUPPORTED;
     if (a->head_dim == 192 && a->window_size > 0) return FGQA_ERR_UNSUPPORTED;
+    const int group = a->num_q_heads / a->num_kv_heads;
+    if (a->kv_head_split < 0 || a->kv_head_split > group || (a->kv_head_split > 0 && group % a->kv_head_split != 0))
+        return FGQA_ERR_INVALID_ARGUMENT;
+    if (a->dq_kernel < FGQA_KERNEL_AUTO || a->dq_kernel > FGQA_KERNEL_SPLIT) return FGQA_ERR_INVALID_ARGUMENT;
+    // the 192-wide dQ kernel needs one wave per SIMD: it has no split form
+    if (a->dq_kernel == FGQA_KERNEL_SPLIT && a->head_dim == 192) return FGQA_ERR_UNSUPPORTED;
     // query rows past sq must read as zero (rows may not overlap)
     if (a->q_stride[1] < a->head_dim || a->grad_o_stride[1] < kHeadDim) return FGQA_ERR_UNSUPPORTED;
     const int64_t lim = (int64_t)1 << 31;
@@ -842,9 +847,14 @@ int validate_backward(const fgqa_prefill_backward_args* a) {
     return FGQA_OK;
 }
 
+// The query-side tensors (q, o, lse, grad_o, grad_q) may be NULL when there
+// are no query rows, and the key-side ones (k, v, grad_k, grad_v) when there
+// are no keys: nothing reads or writes them then.
 int validate_backward_pointers(const fgqa_prefill_backward_args* a) {
-    if (a->q == nullptr || a->k == nullptr || a->v == nullptr || a->o == nullptr || a->lse == nullptr ||
-        a->grad_o == nullptr || a->grad_q == nullptr || a->grad_k == nullptr || a->grad_v == nullptr)
+    if (a->seqlen_q > 0 && (a->q == nullptr || a->o == nullptr || a->lse == nullptr || a->grad_o == nullptr ||
+                            a->grad_q == nullptr))
+        return FGQA_ERR_INVALID_ARGUMENT;
+    if (a->seqlen_kv > 0 && (a->k == nullptr || a->v == nullptr || a->grad_k == nullptr || a->grad_v == nullptr))
         return FGQA_ERR_INVALID_ARGUMENT;
     const void* ptrs[8] = {a->q, a->k, a->v, a->o, a->grad_o, a->grad_q, a->grad_k, a->grad_v};
     for (const void* ptr : ptrs)
@@ -862,8 +872,8 @@ int validate_backward_pointers(const fgqa_prefill_backward_args* a) {
 // workgroups per CU; then the heads are split over workgroups, each writing
 // an fp32 partial that bwd_dkdv_reduce_kernel sums.  Under a sliding window
 // every key block carries the same work, so one workgroup per CU (the
-// kernel's occupancy) is enough and halves the partials.  FGQA_BWD_HSPLIT=<n>
-// forces n (a divisor of G) for tests.
+// kernel's occupancy) is enough and halves the partials.  The caller's
+// kv_head_split field, when nonzero, sets n (a divisor of G, validated).
 BwdPlan plan_backward(const fgqa_prefill_backward_args* a, int cus) {
     BwdPlan pl;
     const int group = a->num_q_heads / a->num_kv_heads;
@@ -875,10 +885,7 @@ BwdPlan plan_backward(const fgqa_prefill_backward_args* a, int cus) {
             pl.n_hsplit = d;
             break;
         }
-    if (const char* e = getenv("FGQA_BWD_HSPLIT")) {
-        const int d = atoi(e);
-        if (d >= 1 && d <= group && group % d == 0) pl.n_hsplit = d;
-    }
+    if (a->kv_head_split > 0) pl.n_hsplit = a->kv_head_split;
     const size_t rows_q = (size_t)a->batch * a->num_q_heads * a->seqlen_q;
     const size_t rows_kv = (size_t)a->batch * a->num_kv_heads * a->seqlen_kv;
     pl.stat_bytes = round256(2 * rows_q * sizeof(float));
@@ -914,16 +921,21 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     if (cus <= 0) return FGQA_ERR_HIP;
     const BwdPlan pl = plan_backward(a, cus);
 
-    unsigned char* ws = static_cast<unsigned char*>(a->workspace);
+    // NULL with 0 bytes: the library's buffer; a call that needs no
+    // workspace (no query rows and no head split) takes none.
+    unsigned char* ws = nullptr;
     std::unique_lock<std::mutex> ws_lock;   // held through the launches when the library's buffer is used
-    if (ws == nullptr) {
-        ws_lock = workspace_lock();
-        ws = static_cast<unsigned char*>(internal_workspace(pl.ws_bytes, &st));
-        if (ws == nullptr) return st;
-    } else if (a->workspace_bytes < pl.ws_bytes) {
-        return FGQA_ERR_WORKSPACE;
-    } else if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0) {
-        return FGQA_ERR_UNSUPPORTED;
+    if (pl.ws_bytes > 0) {
+        ws = static_cast<unsigned char*>(a->workspace);
+        if (ws == nullptr && a->workspace_bytes == 0) {
+            ws_lock = workspace_lock();
+            ws = static_cast<unsigned char*>(internal_workspace(pl.ws_bytes, &st));
+            if (st != FGQA_OK) return st;
+        } else if (ws == nullptr || a->workspace_bytes < pl.ws_bytes) {
+            return FGQA_ERR_WORKSPACE;
+        } else if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0) {
+            return FGQA_ERR_UNSUPPORTED;
+        }
     }
 
     BwdParams p;
@@ -944,9 +956,10 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     p.dq_sb = a->grad_q_stride[0]; p.dq_ss = a->grad_q_stride[1]; p.dq_sh = a->grad_q_stride[2];
     p.dk_sb = a->grad_k_stride[0]; p.dk_ss = a->grad_k_stride[1]; p.dk_sh = a->grad_k_stride[2];
     p.dv_sb = a->grad_v_stride[0]; p.dv_ss = a->grad_v_stride[1]; p.dv_sh = a->grad_v_stride[2];
-    p.rowstat = reinterpret_cast<float*>(ws);
-    p.dk_part = pl.n_hsplit > 1 ? reinterpret_cast<float*>(ws + pl.stat_bytes) : nullptr;
-    p.dv_part = pl.n_hsplit > 1 ? reinterpret_cast<float*>(ws + pl.stat_bytes + pl.part_k_bytes) : nullptr;
+    p.rowstat = reinterpret_cast<float*>(ws);   // NULL only without query rows: never read then
+    p.dk_part = pl.n_hsplit > 1 && ws != nullptr ? reinterpret_cast<float*>(ws + pl.stat_bytes) : nullptr;
+    p.dv_part = pl.n_hsplit > 1 && ws != nullptr ? reinterpret_cast<float*>(ws + pl.stat_bytes + pl.part_k_bytes)
+                                                  : nullptr;
     p.batch = a->batch;
     p.sq = a->seqlen_q;
     p.skv = a->seqlen_kv;
@@ -979,12 +992,12 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     // Few dQ units (fewer than 4 per CU): split each unit's key range over two
     // wave groups, as the forward does.  Under a sliding window the units
     // carry about the same number of tiles, so there is nothing to balance and
-    // the whole-range kernel is faster.  FGQA_BWD_DQ_SPLIT=0/1 forces the choice.
+    // the whole-range kernel is faster.  The caller's dq_kernel field can
+    // force either (the 192-wide dQ kernel has no split form: validated).
     const bool swa = p.window > 0;
     const bool mla = backward_dqk(a) == 192;
-    bool dq_split = q_units < 4 * (int64_t)cus && !swa;
-    if (const char* e = getenv("FGQA_BWD_DQ_SPLIT")) dq_split = e[0] == '1';
-    dq_split = dq_split && !mla;   // the 192-wide dQ kernel needs one wave per SIMD
+    const bool dq_split = a->dq_kernel == FGQA_KERNEL_AUTO ? (q_units < 4 * (int64_t)cus && !swa && !mla)
+                                                           : a->dq_kernel == FGQA_KERNEL_SPLIT;
     // kernel table: [swa] of dK/dV, dQ, split dQ
     const void* kv_fn[2] = {reinterpret_cast<const void*>(bwd_dkdv_kernel<false, 128>),
                             reinterpret_cast<const void*>(bwd_dkdv_kernel<true, 128>)};

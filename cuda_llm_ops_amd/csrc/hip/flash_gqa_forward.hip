@@ -31,7 +31,10 @@
 //                                              P^T is the S^T accumulator converted in place
 //            || masks / row max / scale of S(j+1)
 // The running max only moves (and O is rescaled) when a row's new max exceeds
-// it by more than 2^8, so P <= 256 and O stays far inside fp32 range.
+// it by more than 2^8, so P <= 256 and O stays far inside fp32 range.  The
+// split kernel does not even compute the row max per tile: it checks the
+// tile's row sums against 2^16 after the exps, and takes the max (and
+// recomputes P) only when that check fails or a row has no max yet.
 // K(j+2) and V(j+1) stream straight into LDS (buffer_load ... lds) while tile
 // j is computed.
 //
@@ -42,7 +45,6 @@
 // to 80 KB (two workgroups still share a CU's 160 KB).
 #include <math.h>
 #include <stdint.h>
-#include <stdlib.h>
 
 #include <type_traits>
 
@@ -345,7 +347,8 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         }
     };
 
-    // exp2(S*scale - max), row sums and the bf16 P^T operands of S(j).
+    // exp2(S*scale - max) and the bf16 P^T operands of S(j); returns this
+    // lane's share of the tile's row sum.
     bf16x8_t pop[4];
     auto softmax_p = [&](f32x16_t (&s)[2]) {
         if constexpr (kGroups == 2) {
@@ -359,7 +362,7 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
                     pop[t][e] = (__bf16)pv;
                 }
             }
-            l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+            return (ps[0] + ps[1]) + (ps[2] + ps[3]);
         } else {
             float psum = 0.f;
 #pragma unroll
@@ -372,7 +375,7 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
                         psum += pv;
                         pop[tb * 2 + kh][e] = (__bf16)pv;
                     }
-            l_run += psum;
+            return psum;
         }
     };
 
@@ -456,7 +459,7 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         // run on the VALU: each MFMA is followed by its K read for a later
         // MFMA and a slice of the softmax.
         qk(sn, (j + 1) & 1);
-        softmax_p(sc);
+        l_run += softmax_p(sc);
         // keep P here: otherwise the compiler sinks the softmax to its use in phase B
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) asm volatile("" : "+v"(pop[kb]));
@@ -505,13 +508,27 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         }
         // S(j+1) -> P(j+1); then K(j+3) and V(j+2) go into the buffers that
         // the MFMA phase j has just finished reading.
+        // The running max only keeps P and O inside fp32 range (O / sum does
+        // not depend on it), so this phase computes P against the current
+        // max first and takes the row max only when it must: when a row has
+        // no max yet (its first visible keys), or when a lane's share of the
+        // tile's row sum passes 2^16 (some P above 2^11: the tile's max beat
+        // the running max by more than the rescale slack).  Then it moves the
+        // max, rescales O and the sum, and recomputes P, which ends at most
+        // 2^8 per element.  Otherwise every P stays below 2^16 and the row
+        // max is never computed (it is the softmax phase's costliest
+        // reduction, and this phase sets the pace).
         auto vphase = [&](int j) {
             // the softmax phase sets the pace: its wave wins issue ties
             // against the MFMA wave of the same SIMD
             __builtin_amdgcn_s_setprio(1);
             mask(s, j + 1);
-            update_max(rowmax(s));
-            softmax_p(s);
+            float lt = softmax_p(s);
+            if (__builtin_amdgcn_ballot_w64(m_run == -INFINITY || !(lt <= 65536.f)) != 0) {
+                update_max(rowmax(s));
+                lt = softmax_p(s);
+            }
+            l_run += lt;
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) asm volatile("" : "+v"(pop[kb]));
             asm volatile("" : "+v"(l_run));
@@ -709,6 +726,9 @@ int validate_prefill(const fgqa_prefill_args* a) {
     // (128, 128) and the MLA shape (192, 128); MLA has no window / sink form
     if (dv != kHeadDim || (a->head_dim != kHeadDim && a->head_dim != 192)) return FGQA_ERR_UNSUPPORTED;
     if (a->head_dim == 192 && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
+    if (a->kernel < FGQA_KERNEL_AUTO || a->kernel > FGQA_KERNEL_SPLIT) return FGQA_ERR_INVALID_ARGUMENT;
+    // the window / sink variant has no split form
+    if (a->kernel == FGQA_KERNEL_SPLIT && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
     const int64_t lim = (int64_t)1 << 31;
     if ((int64_t)(a->seqlen_q + 128) * a->q_stride[1] * 2 >= lim ||
         (int64_t)(a->seqlen_kv + 128) * a->k_stride[1] * 2 >= lim ||
@@ -719,8 +739,9 @@ int validate_prefill(const fgqa_prefill_args* a) {
         return FGQA_ERR_INVALID_ARGUMENT;
     if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o))
         return FGQA_ERR_UNSUPPORTED;
+    // (O rows go out as 16-byte stores, so O's strides need 8 elements too)
     for (int i = 0; i < 3; ++i)
-        if ((a->q_stride[i] & 7) || (a->k_stride[i] & 7) || (a->v_stride[i] & 7) || (a->o_stride[i] & 3))
+        if ((a->q_stride[i] & 7) || (a->k_stride[i] & 7) || (a->v_stride[i] & 7) || (a->o_stride[i] & 7))
             return FGQA_ERR_UNSUPPORTED;
     return FGQA_OK;
 }
@@ -778,11 +799,11 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
     // let the dispatcher hand heaviest-first units to free CUs.
     // (A sliding window gives every unit about the same number of tiles:
     // nothing to balance, so the whole-range kernel is used.)
+    // The caller's `kernel` field can force either shape (validated above:
+    // the window / sink variant has no split form).
     const bool swa = p.window > 0 || p.sink != nullptr;
-    bool split = units < 4 * (int64_t)cus && !swa;
-    // FGQA_PREFILL_SPLIT=0/1 forces the choice (tuning and tests; the window /
-    // sink variant has no split form).
-    if (const char* e = getenv("FGQA_PREFILL_SPLIT")) split = e[0] == '1' && !swa;
+    const bool split = a->kernel == FGQA_KERNEL_AUTO ? (units < 4 * (int64_t)cus && !swa)
+                                                     : a->kernel == FGQA_KERNEL_SPLIT;
 
     const bool mla = a->head_dim == 192;
     const int group_bytes = mla ? PfDims<192>::kGroupBytes : PfDims<128>::kGroupBytes;

@@ -337,7 +337,18 @@ def launch_decode_flash_gqa_bf16_kernel(q, k, v, out=None):
 
 
 # --------------------------------------------------------------------------- prefill
-def _prefill_args(q, k, v, o, lse, scale, causal, layout, window_size=0, sink=None) -> _lib.PrefillArgs:
+def _kernel_choice(kernel) -> int:
+    """'auto' / 'whole' / 'split' (or the FGQA_KERNEL_* value) -> the C ABI value."""
+    names = {"auto": _lib.FGQA_KERNEL_AUTO, "whole": _lib.FGQA_KERNEL_WHOLE, "split": _lib.FGQA_KERNEL_SPLIT}
+    if isinstance(kernel, str):
+        if kernel not in names:
+            raise ValueError(f"kernel must be one of {sorted(names)}")
+        return names[kernel]
+    return int(kernel)
+
+
+def _prefill_args(q, k, v, o, lse, scale, causal, layout, window_size=0, sink=None,
+                  kernel="auto") -> _lib.PrefillArgs:
     """C ABI argument block for q/k/v/o 4-D in `layout` ('bshd' or 'bhsd')."""
     def sbh(t):
         if layout == "bshd":
@@ -363,6 +374,7 @@ def _prefill_args(q, k, v, o, lse, scale, causal, layout, window_size=0, sink=No
     a.o_stride[:] = sbh(o)
     a.window_size = int(window_size)
     a.sink = _ptr(sink)
+    a.kernel = _kernel_choice(kernel)
     return a
 
 
@@ -394,7 +406,7 @@ def _check_sink(sink, hq, dev):
     return sink.to(torch.float32).contiguous()
 
 
-def _prefill_bshd_prepare(q, k, v, scale, out, lse, causal, window_size=0, sink=None):
+def _prefill_bshd_prepare(q, k, v, scale, out, lse, causal, window_size=0, sink=None, kernel="auto"):
     if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
         raise ValueError("Flash GQA forward expects bf16 inputs")
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
@@ -419,25 +431,29 @@ def _prefill_bshd_prepare(q, k, v, scale, out, lse, causal, window_size=0, sink=
     elif lse.shape != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
         raise ValueError("LSE must be a contiguous fp32 [batch, q_heads, seqlen_q] tensor")
     sink = _check_sink(sink, Hq, q.device)
-    a = _prefill_args(q, k, v, out, lse, scale, causal, "bshd", window_size, sink)
+    a = _prefill_args(q, k, v, out, lse, scale, causal, "bshd", window_size, sink, kernel)
     return a, out, lse, (q, k, v, out, lse, sink)
 
 
-def flash_gqa_forward_bshd(q, k, v, scale=None, out=None, lse=None, causal=True, window_size=0, sink=None):
+def flash_gqa_forward_bshd(q, k, v, scale=None, out=None, lse=None, causal=True, window_size=0, sink=None,
+                           kernel="auto"):
     """Prefill forward in BSHD: q [B,Sq,Hq,D], k [B,Skv,Hkv,D], v [B,Skv,Hkv,Dv]
     -> (out [B,Sq,Hq,Dv], lse [B,Hq,Sq]).  (D, Dv) is (128, 128), or (192, 128)
     for MLA.  window_size > 0 (causal only): row i sees keys [i - window_size + 1, i];
     sink: optional fp32 [Hq] added to the softmax denominator as sink * exp(-max)
-    (the reference's SWA kernel); both need D == Dv == 128."""
-    a, out, lse, _keep = _prefill_bshd_prepare(q, k, v, scale, out, lse, causal, window_size, sink)
+    (the reference's SWA kernel); both need D == Dv == 128.
+    kernel: 'auto', or 'whole' / 'split' to force one kernel shape (the window /
+    sink variant has no split form)."""
+    a, out, lse, _keep = _prefill_bshd_prepare(q, k, v, scale, out, lse, causal, window_size, sink, kernel)
     _lib.check(_lib.lib().fgqa_prefill_bf16(ctypes.byref(a), ctypes.c_void_p(_stream())), "fgqa_prefill_bf16")
     return out, lse
 
 
-def prepare_prefill(q, k, v, scale=None, out=None, lse=None, causal=True, window_size=0, sink=None):
+def prepare_prefill(q, k, v, scale=None, out=None, lse=None, causal=True, window_size=0, sink=None,
+                    kernel="auto"):
     """``flash_gqa_forward_bshd`` validated once; returns a ``PreparedLaunch``
     whose ``out`` is the output tensor (the LSE tensor is ``.lse``)."""
-    a, out, lse, keep = _prefill_bshd_prepare(q, k, v, scale, out, lse, causal, window_size, sink)
+    a, out, lse, keep = _prefill_bshd_prepare(q, k, v, scale, out, lse, causal, window_size, sink, kernel)
     pl = PreparedLaunch(_lib.lib().fgqa_prefill_bf16, a, keep, out, "fgqa_prefill_bf16")
     pl.lse = lse
     return pl
@@ -544,7 +560,7 @@ def _launch_bhsd_prefill(kind, q, k, v, scale, out, lse, causal):
 
 # --------------------------------------------------------------------------- backward
 def _backward_args(q, k, v, o, lse, grad_o, dq, dk, dv, scale, causal, layout, workspace,
-                   window_size=0) -> _lib.BackwardArgs:
+                   window_size=0, kv_head_split=0, dq_kernel="auto") -> _lib.BackwardArgs:
     """C ABI argument block; 4-D tensors in `layout` ('bshd' or 'bhsd')."""
     def sbh(t):
         if layout == "bshd":
@@ -566,6 +582,8 @@ def _backward_args(q, k, v, o, lse, grad_o, dq, dk, dv, scale, causal, layout, w
     a.scale = float(scale)
     a.window_size = int(window_size)
     a.head_dim_v = int(v.shape[-1])
+    a.kv_head_split = int(kv_head_split)
+    a.dq_kernel = _kernel_choice(dq_kernel)
     a.q_stride[:] = sbh(q)
     a.k_stride[:] = sbh(k)
     a.v_stride[:] = sbh(v)
@@ -581,11 +599,12 @@ def _backward_args(q, k, v, o, lse, grad_o, dq, dk, dv, scale, causal, layout, w
 
 
 def backward_workspace_bytes(batch, seqlen_q, seqlen_kv, num_q_heads, num_kv_heads, head_dim=128,
-                             window_size=0, head_dim_v=0) -> int:
+                             window_size=0, head_dim_v=0, kv_head_split=0) -> int:
     """Bytes of scratch ``flash_gqa_backward_bshd`` needs for a caller workspace
     (256-byte aligned; depends on the current device's CU count and on the
     window: a sliding-window backward needs at most the causal one's).
-    head_dim 192 with head_dim_v 128: the MLA backward."""
+    head_dim 192 with head_dim_v 128: the MLA backward.  kv_head_split as in
+    ``flash_gqa_backward_bshd``."""
     dv = int(head_dim_v) or head_dim
     a = _lib.BackwardArgs()
     a.batch, a.seqlen_q, a.seqlen_kv = batch, seqlen_q, seqlen_kv
@@ -593,6 +612,7 @@ def backward_workspace_bytes(batch, seqlen_q, seqlen_kv, num_q_heads, num_kv_hea
     a.head_dim_v = dv
     a.causal = 1
     a.window_size = int(window_size)
+    a.kv_head_split = int(kv_head_split)
     a.scale = 1.0
     for name, d in (("q_stride", head_dim), ("grad_q_stride", head_dim), ("o_stride", dv), ("grad_o_stride", dv)):
         getattr(a, name)[:] = [seqlen_q * num_q_heads * d, num_q_heads * d, d]
@@ -613,7 +633,7 @@ def _grad_out(t, shape, ref, name):
 
 
 def _backward_bshd_prepare(q, k, v, o, lse, grad_o, scale, causal, grad_q, grad_k, grad_v, workspace,
-                           window_size=0):
+                           window_size=0, kv_head_split=0, dq_kernel="auto"):
     for t in (q, k, v, o, grad_o):
         if t.dtype != torch.bfloat16:
             raise ValueError("Flash GQA backward expects bf16 inputs and grad_o")
@@ -640,32 +660,39 @@ def _backward_bshd_prepare(q, k, v, o, lse, grad_o, scale, causal, grad_q, grad_
     grad_k = _grad_out(grad_k, k.shape, q, "grad_k")
     grad_v = _grad_out(grad_v, v.shape, q, "grad_v")
     a = _backward_args(q, k, v, o, lse, grad_o, grad_q, grad_k, grad_v, scale, causal, "bshd", workspace,
-                       window_size)
+                       window_size, kv_head_split, dq_kernel)
     return a, (grad_q, grad_k, grad_v), (q, k, v, o, lse, grad_o, grad_q, grad_k, grad_v, workspace)
 
 
 def flash_gqa_backward_bshd(q, k, v, o, lse, grad_o, scale=None, causal=True,
-                            grad_q=None, grad_k=None, grad_v=None, workspace=None, window_size=0):
+                            grad_q=None, grad_k=None, grad_v=None, workspace=None, window_size=0,
+                            kv_head_split=0, dq_kernel="auto"):
     """Prefill backward in BSHD: q/o/grad_o [B,Sq,Hq,D], k/v [B,Skv,Hkv,D], lse
     [B,Hq,Sq] from the forward -> (grad_q, grad_k, grad_v) bf16 in q/k/v's shapes.
 
     ``window_size`` > 0 (causal only) restricts row i to keys
     [i - window_size + 1, i], the sliding-window backward; pass the forward's
     LSE (with the sink term when the forward had one) and the gradients follow
-    the sink-adjusted softmax."""
+    the sink-adjusted softmax.
+
+    kv_head_split (0 = automatic, else a divisor of Hq / Hkv) and dq_kernel
+    ('auto' / 'whole' / 'split') force the work split of the dK/dV and dQ passes."""
     a, grads, _keep = _backward_bshd_prepare(q, k, v, o, lse, grad_o, scale, causal,
-                                             grad_q, grad_k, grad_v, workspace, window_size)
+                                             grad_q, grad_k, grad_v, workspace, window_size,
+                                             kv_head_split, dq_kernel)
     _lib.check(_lib.lib().fgqa_prefill_backward_bf16(ctypes.byref(a), ctypes.c_void_p(_stream())),
                "fgqa_prefill_backward_bf16")
     return grads
 
 
 def prepare_backward(q, k, v, o, lse, grad_o, scale=None, causal=True,
-                     grad_q=None, grad_k=None, grad_v=None, workspace=None, window_size=0):
+                     grad_q=None, grad_k=None, grad_v=None, workspace=None, window_size=0,
+                     kv_head_split=0, dq_kernel="auto"):
     """``flash_gqa_backward_bshd`` validated once; returns a ``PreparedLaunch``
     whose ``out`` is the (grad_q, grad_k, grad_v) tuple."""
     a, grads, keep = _backward_bshd_prepare(q, k, v, o, lse, grad_o, scale, causal,
-                                            grad_q, grad_k, grad_v, workspace, window_size)
+                                            grad_q, grad_k, grad_v, workspace, window_size,
+                                            kv_head_split, dq_kernel)
     return PreparedLaunch(_lib.lib().fgqa_prefill_backward_bf16, a, keep, grads, "fgqa_prefill_backward_bf16")
 
 

@@ -36,6 +36,16 @@ enum fgqa_status {
 };
 
 /*
+ * Kernel choice of the prefill and backward calls (fields `kernel` and
+ * `dq_kernel`).  AUTO picks by grid size; the others force one kernel shape,
+ * for tuning and tests.  Callers that zero the argument struct get AUTO.
+ *   FGQA_KERNEL_WHOLE  one workgroup runs a 128-row unit over its whole KV range
+ *   FGQA_KERNEL_SPLIT  two wave groups run the two halves of a unit's KV range
+ *                      and merge (the choice for grids under 4 units per CU)
+ */
+enum fgqa_kernel_choice { FGQA_KERNEL_AUTO = 0, FGQA_KERNEL_WHOLE = 1, FGQA_KERNEL_SPLIT = 2 };
+
+/*
  * Single-token decode (flash-decoding: split-KV pass + log-sum-exp combine).
  * Replaces LaunchFlashGqaBf16Kernel, reference
  * include/cplusplus/FlashGQA/decode_flash_gqa_kernel.cuh:28-38
@@ -170,6 +180,9 @@ int fgqa_decode_paged(const fgqa_decode_paged_args* args, void* stream);
  *           src/python/Triton/flash_mla_kernel.py:315-508 (kernel :16-270):
  *           q/k rows hold head_dim elements, v/o rows head_dim_v.  Supported:
  *           (128, 128), and (192, 128) without window or sink.
+ *   kernel  an fgqa_kernel_choice (0 = AUTO).  The window / sink variant has
+ *           no split form: FGQA_KERNEL_SPLIT with either returns
+ *           FGQA_ERR_UNSUPPORTED.
  */
 typedef struct fgqa_prefill_args {
     const void* q;
@@ -192,6 +205,7 @@ typedef struct fgqa_prefill_args {
     int32_t window_size;
     const float* sink;
     int32_t head_dim_v;
+    int32_t kernel;
 } fgqa_prefill_args;
 
 int fgqa_prefill_bf16(const fgqa_prefill_args* args, void* stream);
@@ -226,6 +240,13 @@ int fgqa_prefill_bf16(const fgqa_prefill_args* args, void* stream);
  *   flash_mla_backward_kernel.py:788-969, kernel :202-786): q, k, grad_q,
  *   grad_k have 192-element rows, v, o, grad_o, grad_v 128-element rows.
  *   Supported: (128, 128) and (192, 128) without a window.
+ * kv_head_split  0: automatic.  n >= 1 (a divisor of Hq / Hkv): the dK/dV pass
+ *   splits each KV head's query heads over n workgroups whose fp32 partials a
+ *   reduction sums (n = 1: no partials).  It changes the workspace size.
+ *   Other values return FGQA_ERR_INVALID_ARGUMENT.
+ * dq_kernel  an fgqa_kernel_choice for the dQ pass (0 = AUTO).  The MLA shape
+ *   has no split dQ kernel: FGQA_KERNEL_SPLIT with head_dim 192 returns
+ *   FGQA_ERR_UNSUPPORTED.
  */
 typedef struct fgqa_prefill_backward_args {
     const void* q;
@@ -257,6 +278,8 @@ typedef struct fgqa_prefill_backward_args {
     size_t workspace_bytes;
     int32_t window_size;
     int32_t head_dim_v;
+    int32_t kv_head_split;
+    int32_t dq_kernel;
 } fgqa_prefill_backward_args;
 
 /* Bytes of workspace fgqa_prefill_backward_bf16 needs (pointers unused; the

@@ -146,7 +146,7 @@ def _prefill_args(**kw):
     a.causal = 1
     a.scale = kw.get("scale", D ** -0.5)
     a.q_stride[:] = [Sq * Hq * D, Hq * D, D]
-    a.o_stride[:] = [Sq * Hq * D, Hq * D, D]
+    a.o_stride[:] = kw.get("ostride", [Sq * Hq * D, Hq * D, D])
     a.k_stride[:] = [Skv * Hkv * D, Hkv * D, D]
     a.v_stride[:] = [Skv * Hkv * D, Hkv * D, D]
     for name in ("q", "k", "v", "o"):
@@ -155,6 +155,7 @@ def _prefill_args(**kw):
     a.sink = kw.get("sink", None)
     a.causal = kw.get("causal", 1)
     a.head_dim_v = kw.get("Dv", 0)
+    a.kernel = kw.get("kernel", 0)
     return a
 
 
@@ -162,6 +163,11 @@ def _prefill_args(**kw):
     (dict(Hq=15, Hkv=2), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(Sq=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(scale=float("inf")), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(kernel=3), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(kernel=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(kernel=_lib.FGQA_KERNEL_SPLIT, window=64), _lib.FGQA_ERR_UNSUPPORTED),   # no split SWA kernel
+    (dict(kernel=_lib.FGQA_KERNEL_SPLIT, sink=4096), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(ostride=[256 * 16 * 128, 16 * 128 + 4, 128]), _lib.FGQA_ERR_UNSUPPORTED),  # O rows: 16-byte stores
     (dict(D=256), _lib.FGQA_ERR_UNSUPPORTED),
     (dict(v=None), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(o=4096 + 8), _lib.FGQA_ERR_UNSUPPORTED),
@@ -326,6 +332,8 @@ def _backward_args(**kw):
         getattr(a, name)[:] = [Skv * Hkv * d, Hkv * d, d]
     for name in ("q", "k", "v", "o", "lse", "grad_o", "grad_q", "grad_k", "grad_v"):
         setattr(a, name, kw.get(name, 4096))
+    a.kv_head_split = kw.get("hsplit", 0)
+    a.dq_kernel = kw.get("dq_kernel", 0)
     return a
 
 
@@ -343,6 +351,11 @@ def _backward_args(**kw):
     (dict(D=192, Dv=128, window=64), _lib.FGQA_ERR_UNSUPPORTED),   # no MLA window form
     (dict(D=128, Dv=192), _lib.FGQA_ERR_UNSUPPORTED),
     (dict(Dv=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(hsplit=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(hsplit=3), _lib.FGQA_ERR_INVALID_ARGUMENT),      # not a divisor of G = 16
+    (dict(hsplit=32), _lib.FGQA_ERR_INVALID_ARGUMENT),     # more than G
+    (dict(dq_kernel=3), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(D=192, Dv=128, dq_kernel=_lib.FGQA_KERNEL_SPLIT), _lib.FGQA_ERR_UNSUPPORTED),   # no split MLA dQ
 ])
 def test_backward_rejects_before_launch(kw, code):
     assert _lib.lib().fgqa_prefill_backward_bf16(ctypes.byref(_backward_args(**kw)), None) == code
@@ -453,6 +466,21 @@ def _paged_args(**kw):
 ])
 def test_paged_decode_rejects_before_launch(kw, code):
     assert _lib.lib().fgqa_decode_paged(ctypes.byref(_paged_args(**kw)), None) == code
+
+
+def test_paged_decode_list_limit_rejected_by_query_and_launch():
+    """A batch the work list cannot index (>= 2^15 sequences) is rejected by the
+    workspace query and by the launch alike, before any workspace is taken
+    (an explicit split size keeps the plan off the device)."""
+    L = _lib.lib()
+    a = _paged_args(B=1 << 15)
+    a.split_tokens = 4096
+    n = ctypes.c_size_t(0)
+    assert L.fgqa_decode_paged_workspace_bytes(ctypes.byref(a), ctypes.byref(n)) == _lib.FGQA_ERR_UNSUPPORTED
+    assert L.fgqa_decode_paged(ctypes.byref(a), None) == _lib.FGQA_ERR_UNSUPPORTED
+    b = _paged_args(B=(1 << 15) - 1)
+    b.split_tokens = 4096
+    assert L.fgqa_decode_paged_workspace_bytes(ctypes.byref(b), ctypes.byref(n)) == 0 and n.value > 0
 
 
 def test_paged_decode_empty_batch_is_noop():

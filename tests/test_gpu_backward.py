@@ -47,13 +47,13 @@ def _check(grads, refs, what):
         assert_grad_close(oracle.bf16_to_f32(g), ref, f"{what} {name}")
 
 
-def _gpu_backward(cuda, q, k, v, o, lse, do, scale=SCALE, causal=True, workspace=None):
+def _gpu_backward(cuda, q, k, v, o, lse, do, scale=SCALE, causal=True, workspace=None, **plan):
     import torch
     t = [to_torch_bf16(x, cuda) for x in (q, k, v, o)]
     dod = to_torch_bf16(do, cuda)
     lsed = torch.from_numpy(np.ascontiguousarray(lse)).to(cuda)
     dq, dk, dv = _fg().flash_gqa_backward_bshd(t[0], t[1], t[2], t[3], lsed, dod, scale, causal=causal,
-                                               workspace=workspace)
+                                               workspace=workspace, **plan)
     _sync()
     return from_torch_bf16(dq), from_torch_bf16(dk), from_torch_bf16(dv)
 
@@ -81,29 +81,27 @@ def test_backward_shapes(cuda, B, Sq, Skv, Hq, Hkv, causal):
         assert np.all(oracle.bf16_to_f32(grads[2])[:, Sq:] == 0)
 
 
-@pytest.mark.parametrize("hsplit", ["1", "2", "8"])
-def test_backward_head_split_modes(cuda, monkeypatch, hsplit):
+@pytest.mark.parametrize("hsplit", [1, 2, 8])
+def test_backward_head_split_modes(cuda, hsplit):
     """Heads of a KV group in one workgroup (dK/dV written from registers) or
     split over workgroups (fp32 dK/dV accumulators) give the same gradients."""
-    monkeypatch.setenv("FGQA_BWD_HSPLIT", hsplit)
     print(f"backward hsplit={hsplit}", flush=True)
     q, k, v, o, lse, do = _inputs(810, 1, 384, 384, 16, 2)
     refs = oracle.prefill_backward(q, k, v, o, lse, do, SCALE, causal=True)
-    _check(_gpu_backward(cuda, q, k, v, o, lse, do), refs, f"hsplit={hsplit}")
+    _check(_gpu_backward(cuda, q, k, v, o, lse, do, kv_head_split=hsplit), refs, f"hsplit={hsplit}")
 
 
-@pytest.mark.parametrize("split", ["0", "1"])
+@pytest.mark.parametrize("split", ["whole", "split"])
 @pytest.mark.parametrize("B,Sq,Skv,Hq,Hkv,causal", [
     (1, 320, 320, 16, 1, True), (2, 200, 200, 4, 2, True), (1, 130, 250, 2, 1, False), (1, 64, 64, 3, 1, True)])
-def test_backward_dq_whole_and_split_kernels(cuda, monkeypatch, split, B, Sq, Skv, Hq, Hkv, causal):
+def test_backward_dq_whole_and_split_kernels(cuda, split, B, Sq, Skv, Hq, Hkv, causal):
     """The dQ kernel over a unit's whole key range, or split over two wave
     groups whose dQ is summed through LDS."""
-    monkeypatch.setenv("FGQA_BWD_DQ_SPLIT", split)
-    what = f"dq split={split} B{B} Sq{Sq} Skv{Skv} Hq{Hq} Hkv{Hkv} causal{causal}"
+    what = f"dq kernel={split} B{B} Sq{Sq} Skv{Skv} Hq{Hq} Hkv{Hkv} causal{causal}"
     print(what, flush=True)
     q, k, v, o, lse, do = _inputs(860 + Sq, B, Sq, Skv, Hq, Hkv, causal=causal)
     refs = oracle.prefill_backward(q, k, v, o, lse, do, SCALE, causal=causal)
-    _check(_gpu_backward(cuda, q, k, v, o, lse, do, causal=causal), refs, what)
+    _check(_gpu_backward(cuda, q, k, v, o, lse, do, causal=causal, dq_kernel=split), refs, what)
 
 
 @pytest.mark.parametrize("scale", [0.2, -0.05])
@@ -230,3 +228,48 @@ def test_backward_cplusplus_dropin(cuda):
     assert st() == 0
     torch.cuda.synchronize()
     _check((from_torch_bf16(gq), from_torch_bf16(gk), from_torch_bf16(gv)), refs, "C++ backward")
+
+
+_NO_QUERY_ROWS_SCRIPT = r"""
+import ctypes, sys
+sys.path.insert(0, sys.argv[1])
+import torch
+import cuda_llm_ops_amd._lib as L
+dev = torch.device("cuda:0")
+B, Skv, H, D = 2, 200, 3, 128
+k = torch.randn(B, Skv, H, D, device=dev).to(torch.bfloat16)
+v = torch.randn(B, Skv, H, D, device=dev).to(torch.bfloat16)
+dk = torch.full((B, Skv, H, D), float("nan"), device=dev, dtype=torch.bfloat16)
+dv = torch.full((B, Skv, H, D), float("nan"), device=dev, dtype=torch.bfloat16)
+a = L.BackwardArgs()
+a.k, a.v, a.grad_k, a.grad_v = k.data_ptr(), v.data_ptr(), dk.data_ptr(), dv.data_ptr()
+a.batch, a.seqlen_q, a.seqlen_kv, a.num_q_heads, a.num_kv_heads, a.head_dim = B, 0, Skv, H, H, D
+a.causal, a.scale = 1, D ** -0.5
+for name in ("q_stride", "o_stride", "grad_o_stride", "grad_q_stride"):
+    getattr(a, name)[:] = [H * D, H * D, D]
+for name in ("k_stride", "v_stride", "grad_k_stride", "grad_v_stride"):
+    getattr(a, name)[:] = [Skv * H * D, H * D, D]
+n = ctypes.c_size_t(1)
+assert L.lib().fgqa_prefill_backward_workspace_bytes(ctypes.byref(a), ctypes.byref(n)) == 0 and n.value == 0
+st = L.lib().fgqa_prefill_backward_bf16(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+torch.cuda.synchronize()
+assert st == 0, st
+assert bool((dk == 0).all()) and bool((dv == 0).all()), "dK / dV not zeroed"
+print("no-query-rows backward ok", flush=True)
+"""
+
+
+def test_backward_without_query_rows_zeroes_key_gradients(cuda):
+    """Sq = 0 with Skv > 0 and G = 1: the call needs no workspace, and no query
+    row sees any key, so dK = dV = 0 must still be written -- in a fresh process,
+    where the library's own buffer has never been allocated (q, o, lse, grad_o
+    and grad_q are NULL: nothing reads them)."""
+    import os
+    import subprocess
+    import sys
+    print("backward Sq=0 Skv=200 G=1 (fresh process)", flush=True)
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _NO_QUERY_ROWS_SCRIPT, root], capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "no-query-rows backward ok" in r.stdout

@@ -42,7 +42,7 @@ def _inputs(seed, B, Sq, Skv, Hq, Hkv, uniform=False):
     return q, k, v
 
 
-@pytest.mark.parametrize("split", ["0", "1"])
+@pytest.mark.parametrize("split", ["whole", "split"])
 @pytest.mark.parametrize("B,Sq,Skv,Hq,Hkv,causal", [
     (1, 256, 256, 2, 2, True),     # G = 1, the reference's MLA head layout
     (2, 300, 300, 4, 1, True),     # ragged tail, G = 4
@@ -51,14 +51,13 @@ def _inputs(seed, B, Sq, Skv, Hq, Hkv, uniform=False):
     (1, 330, 200, 6, 3, True),     # Sq > Skv (rows past the keys see all of them)
     (1, 100, 160, 4, 2, True),     # Sq < Skv, causal: top-left aligned
 ])
-def test_mla_shapes(cuda, monkeypatch, split, B, Sq, Skv, Hq, Hkv, causal):
-    monkeypatch.setenv("FGQA_PREFILL_SPLIT", split)
-    what = f"mla split={split} B{B} Sq{Sq} Skv{Skv} Hq{Hq} Hkv{Hkv} causal={causal}"
+def test_mla_shapes(cuda, split, B, Sq, Skv, Hq, Hkv, causal):
+    what = f"mla kernel={split} B{B} Sq{Sq} Skv{Skv} Hq{Hq} Hkv{Hkv} causal={causal}"
     print(what, flush=True)
     q, k, v = _inputs(2000 + Sq + Skv, B, Sq, Skv, Hq, Hkv)
     o_ref, l_ref = oracle.prefill_mla(q, k, v, SCALE, causal=causal)
     qd, kd, vd = (to_torch_bf16(x, cuda) for x in (q, k, v))
-    out, lse = _fg().flash_gqa_forward_bshd(qd, kd, vd, SCALE, causal=causal)
+    out, lse = _fg().flash_gqa_forward_bshd(qd, kd, vd, SCALE, causal=causal, kernel=split)
     assert out.shape == (B, Sq, Hq, DV)
     _check(from_torch_bf16(out), lse.cpu().numpy(), o_ref, l_ref, what)
 
@@ -84,15 +83,10 @@ def test_mla_reference_shape_full_size(cuda):
     q = gpu_normal_bf16((B, S, Hq, DQK), 71, 1.0, cuda)
     k = gpu_normal_bf16((B, S, Hkv, DQK), 72, 1.0, cuda)
     v = gpu_normal_bf16((B, S, Hkv, DV), 73, 1.0, cuda)
-    for split in ("0", "1"):
-        import os
-        os.environ["FGQA_PREFILL_SPLIT"] = split
-        try:
-            print(f"mla full size split={split}", flush=True)
-            out, lse = fg.flash_gqa_forward_bshd(q, k, v, SCALE, causal=True)
-            torch.cuda.synchronize()
-        finally:
-            del os.environ["FGQA_PREFILL_SPLIT"]
+    for split in ("whole", "split"):
+        print(f"mla full size kernel={split}", flush=True)
+        out, lse = fg.flash_gqa_forward_bshd(q, k, v, SCALE, causal=True, kernel=split)
+        torch.cuda.synchronize()
         assert bool(out.isfinite().all())
         for r0, r1 in ((0, 64), (2000, 2064), (S - 64, S)):
             o_ref, l_ref = oracle.prefill_mla(from_torch_bf16(q[:, r0:r1]), from_torch_bf16(k[:, :r1]),

@@ -49,12 +49,12 @@ def _check(grads, refs, what):
         assert_grad_close(oracle.bf16_to_f32(g), ref, f"{what} {name}")
 
 
-def _gpu_backward(cuda, q, k, v, o, lse, do, causal=True, scale=SCALE, workspace=None):
+def _gpu_backward(cuda, q, k, v, o, lse, do, causal=True, scale=SCALE, workspace=None, **plan):
     import torch
     t = [to_torch_bf16(x, cuda) for x in (q, k, v, o, do)]
     lsed = torch.from_numpy(np.ascontiguousarray(lse)).to(cuda)
     dq, dk, dv = _fg().flash_gqa_backward_bshd(t[0], t[1], t[2], t[3], lsed, t[4], scale, causal=causal,
-                                               workspace=workspace)
+                                               workspace=workspace, **plan)
     _sync()
     return from_torch_bf16(dq), from_torch_bf16(dk), from_torch_bf16(dv)
 
@@ -80,15 +80,14 @@ def test_mla_backward_shapes(cuda, B, Sq, Skv, Hq, Hkv, causal):
         assert np.all(oracle.bf16_to_f32(grads[2])[:, Sq:] == 0)
 
 
-@pytest.mark.parametrize("hsplit", ["1", "2", "4"])
-def test_mla_backward_head_split_modes(cuda, monkeypatch, hsplit):
+@pytest.mark.parametrize("hsplit", [1, 2, 4])
+def test_mla_backward_head_split_modes(cuda, hsplit):
     """Heads of a KV group in one workgroup (dK/dV straight from registers) or
     split over workgroups (fp32 partials of 192- and 128-wide rows summed)."""
-    monkeypatch.setenv("FGQA_BWD_HSPLIT", hsplit)
     print(f"mla backward hsplit={hsplit}", flush=True)
     q, k, v, o, lse, do = _inputs(2210, 1, 384, 384, 8, 2)
     refs = oracle.prefill_backward(q, k, v, o, lse, do, SCALE, causal=True)
-    _check(_gpu_backward(cuda, q, k, v, o, lse, do), refs, f"mla hsplit={hsplit}")
+    _check(_gpu_backward(cuda, q, k, v, o, lse, do, kv_head_split=hsplit), refs, f"mla hsplit={hsplit}")
 
 
 @pytest.mark.parametrize("scale", [0.2, -0.05])

@@ -206,13 +206,13 @@ def test_decode_cplusplus_dropin(cuda):
 
 
 # ------------------------------------------------------------------ prefill
-def _prefill_case(cuda, seed, B, Sq, Skv, Hq, Hkv, causal=True, sigma=1.0):
+def _prefill_case(cuda, seed, B, Sq, Skv, Hq, Hkv, causal=True, sigma=1.0, kernel="auto"):
     q = oracle.normal_bf16(seed, (B, Sq, Hq, 128), sigma)
     k = oracle.normal_bf16(seed, (B, Skv, Hkv, 128), sigma, stream=1)
     v = oracle.normal_bf16(seed, (B, Skv, Hkv, 128), sigma, stream=2)
     o_ref, lse_ref = oracle.prefill(q, k, v, SCALE, causal=causal)
     qd, kd, vd = (to_torch_bf16(x, cuda) for x in (q, k, v))
-    out, lse = _fg().flash_gqa_forward_bshd(qd, kd, vd, SCALE, causal=causal)
+    out, lse = _fg().flash_gqa_forward_bshd(qd, kd, vd, SCALE, causal=causal, kernel=kernel)
     _sync()
     return from_torch_bf16(out), lse.cpu().numpy(), o_ref, lse_ref
 
@@ -239,7 +239,7 @@ def test_prefill_shapes(cuda, B, Sq, Skv, Hq, Hkv, causal):
     _check_prefill(o, lse, o_ref, lse_ref, f"prefill B{B} Sq{Sq} Skv{Skv} Hq{Hq} Hkv{Hkv} causal{causal}")
 
 
-@pytest.mark.parametrize("split", ["0", "1"])
+@pytest.mark.parametrize("kernel", ["whole", "split"])
 @pytest.mark.parametrize("B,Sq,Skv,Hq,Hkv,causal", [
     (1, 256, 256, 16, 1, True),
     (2, 300, 300, 8, 2, True),      # odd tile counts per unit
@@ -250,13 +250,36 @@ def test_prefill_shapes(cuda, B, Sq, Skv, Hq, Hkv, causal):
     (1, 1111, 1111, 16, 2, True),   # up to 18 tiles per unit
     (1, 700, 900, 4, 4, False),
 ])
-def test_prefill_whole_and_split_kernels(cuda, monkeypatch, split, B, Sq, Skv, Hq, Hkv, causal):
+def test_prefill_whole_and_split_kernels(cuda, kernel, B, Sq, Skv, Hq, Hkv, causal):
     """Both prefill kernels: one workgroup per unit over its whole KV range,
     and the split kernel (two wave groups on the halves of the range, merged)."""
-    monkeypatch.setenv("FGQA_PREFILL_SPLIT", split)
-    o, lse, o_ref, lse_ref = _prefill_case(cuda, 650 + Sq, B, Sq, Skv, Hq, Hkv, causal)
+    o, lse, o_ref, lse_ref = _prefill_case(cuda, 650 + Sq, B, Sq, Skv, Hq, Hkv, causal, kernel=kernel)
     _check_prefill(o, lse, o_ref, lse_ref,
-                   f"split={split} B{B} Sq{Sq} Skv{Skv} Hq{Hq} Hkv{Hkv} causal{causal}")
+                   f"kernel={kernel} B{B} Sq{Sq} Skv{Skv} Hq{Hq} Hkv{Hkv} causal{causal}")
+
+
+@pytest.mark.parametrize("kernel", ["whole", "split"])
+@pytest.mark.parametrize("case,scale", [("climb", 0.5), ("fall", 0.5), ("sharp", 2.0)])
+def test_prefill_running_max_moves(cuda, kernel, case, scale):
+    """Score distributions that move the running max: keys scaled up along the
+    sequence (each row's max climbs from tile to tile by far more than the
+    rescale slack, so both kernels rescale, and the split kernel's row-sum
+    check fires), scaled down (the first tile holds the max), and logits in
+    the hundreds (exp2 against a stale max would overflow fp32)."""
+    B, S, Hq, Hkv = 1, 640, 8, 1
+    what = f"running max {case} scale={scale} kernel={kernel}"
+    print(what, flush=True)
+    q = oracle.normal_bf16(900, (B, S, Hq, 128))
+    k = oracle.bf16_to_f32(oracle.normal_bf16(900, (B, S, Hkv, 128), stream=1))
+    v = oracle.normal_bf16(900, (B, S, Hkv, 128), stream=2)
+    ramp = np.arange(S, dtype=np.float32) / S
+    f = {"climb": 0.25 + 3.0 * ramp, "fall": 3.25 - 3.0 * ramp, "sharp": np.ones(S, np.float32)}[case]
+    k = oracle.f32_to_bf16(k * f[None, :, None, None])
+    o_ref, lse_ref = oracle.prefill(q, k, v, scale, causal=True)
+    qd, kd, vd = (to_torch_bf16(x, cuda) for x in (q, k, v))
+    out, lse = _fg().flash_gqa_forward_bshd(qd, kd, vd, scale, causal=True, kernel=kernel)
+    _sync()
+    _check_prefill(from_torch_bf16(out), lse.cpu().numpy(), o_ref, lse_ref, what)
 
 
 @pytest.mark.parametrize("scale", [0.2, -0.05])

@@ -30,7 +30,7 @@ def _check(o, lse, o_ref, l_ref, what):
     assert np.max(np.abs(lse[fin] - l_ref[fin]), initial=0.0) <= LSE_TOL, f"{what}: lse"
 
 
-def _case(cuda, seed, B, Sq, Skv, Hq, Hkv, window, with_sink):
+def _case(cuda, seed, B, Sq, Skv, Hq, Hkv, window, with_sink, kernel="auto"):
     import torch
     q = oracle.normal_bf16(seed, (B, Sq, Hq, 128))
     k = oracle.normal_bf16(seed, (B, Skv, Hkv, 128), stream=1)
@@ -39,12 +39,13 @@ def _case(cuda, seed, B, Sq, Skv, Hq, Hkv, window, with_sink):
     o_ref, l_ref = oracle.prefill_swa(q, k, v, SCALE, window, sink)
     qd, kd, vd = (to_torch_bf16(x, cuda) for x in (q, k, v))
     sd = None if sink is None else torch.from_numpy(sink).to(cuda)
-    out, lse = _fg().flash_gqa_forward_bshd(qd, kd, vd, SCALE, causal=True, window_size=window, sink=sd)
+    out, lse = _fg().flash_gqa_forward_bshd(qd, kd, vd, SCALE, causal=True, window_size=window, sink=sd,
+                                            kernel=kernel)
     torch.cuda.synchronize()
     return from_torch_bf16(out), lse.cpu().numpy(), o_ref, l_ref
 
 
-@pytest.mark.parametrize("split", ["0", "1"])
+@pytest.mark.parametrize("kernel", ["auto", "whole"])
 @pytest.mark.parametrize("B,S,Hq,Hkv,window,with_sink", [
     (1, 300, 16, 1, 64, True),
     (2, 500, 8, 2, 17, True),     # window not a multiple of the tile
@@ -52,12 +53,22 @@ def _case(cuda, seed, B, Sq, Skv, Hq, Hkv, window, with_sink):
     (1, 257, 4, 4, 100, False),   # no sink: plain windowed softmax
     (1, 700, 4, 1, 4096, True),   # window past the sequence: causal + sink
 ])
-def test_swa_shapes(cuda, monkeypatch, split, B, S, Hq, Hkv, window, with_sink):
-    """(The window / sink variant has no split form: FGQA_PREFILL_SPLIT=1 must not select one.)"""
-    monkeypatch.setenv("FGQA_PREFILL_SPLIT", split)
-    what = f"swa split={split} B{B} S{S} Hq{Hq} Hkv{Hkv} W{window} sink={with_sink}"
+def test_swa_shapes(cuda, kernel, B, S, Hq, Hkv, window, with_sink):
+    what = f"swa kernel={kernel} B{B} S{S} Hq{Hq} Hkv{Hkv} W{window} sink={with_sink}"
     print(what, flush=True)
-    _check(*_case(cuda, 1000 + S + window, B, S, S, Hq, Hkv, window, with_sink), what)
+    _check(*_case(cuda, 1000 + S + window, B, S, S, Hq, Hkv, window, with_sink, kernel), what)
+
+
+def test_swa_split_kernel_request_is_unsupported(cuda):
+    """The window / sink variant has no split form: asking for it is an error
+    (FGQA_ERR_UNSUPPORTED), not a silent fallback."""
+    import torch
+    fg = _fg()
+    q = torch.zeros((1, 64, 4, 128), device=cuda, dtype=torch.bfloat16)
+    k = torch.zeros((1, 64, 1, 128), device=cuda, dtype=torch.bfloat16)
+    with pytest.raises(fg.FgqaError) as e:
+        fg.flash_gqa_forward_bshd(q, k, k, SCALE, causal=True, window_size=16, kernel="split")
+    assert e.value.status == -2
 
 
 def test_swa_rows_past_the_keys(cuda):

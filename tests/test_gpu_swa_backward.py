@@ -54,12 +54,12 @@ def _check(grads, refs, what):
         assert_grad_close(oracle.bf16_to_f32(g), ref, f"{what} {name}")
 
 
-def _gpu_backward(cuda, q, k, v, o, lse, do, window, scale=SCALE):
+def _gpu_backward(cuda, q, k, v, o, lse, do, window, scale=SCALE, **plan):
     import torch
     t = [to_torch_bf16(x, cuda) for x in (q, k, v, o, do)]
     lsed = torch.from_numpy(np.ascontiguousarray(lse)).to(cuda)
     dq, dk, dv = _fg().flash_gqa_backward_bshd(t[0], t[1], t[2], t[3], lsed, t[4], scale, causal=True,
-                                               window_size=window)
+                                               window_size=window, **plan)
     _sync()
     return from_torch_bf16(dq), from_torch_bf16(dk), from_torch_bf16(dv)
 
@@ -98,39 +98,36 @@ def test_swa_backward_unequal_lengths(cuda, B, Sq, Skv, Hq, Hkv, window):
         assert np.all(oracle.bf16_to_f32(grads[2])[:, Sq:] == 0)
 
 
-@pytest.mark.parametrize("hsplit", ["1", "2", "8"])
-def test_swa_backward_head_split_modes(cuda, monkeypatch, hsplit):
+@pytest.mark.parametrize("hsplit", [1, 2, 8])
+def test_swa_backward_head_split_modes(cuda, hsplit):
     """Heads of a KV group in one workgroup or split over workgroups."""
-    monkeypatch.setenv("FGQA_BWD_HSPLIT", hsplit)
     print(f"swa backward hsplit={hsplit}", flush=True)
     q, k, v, o, lse, do = _inputs(1510, 1, 384, 384, 16, 2, 96)
     refs = oracle.prefill_backward(q, k, v, o, lse, do, SCALE, causal=True, window=96)
-    _check(_gpu_backward(cuda, q, k, v, o, lse, do, 96), refs, f"swa hsplit={hsplit}")
+    _check(_gpu_backward(cuda, q, k, v, o, lse, do, 96, kv_head_split=hsplit), refs, f"swa hsplit={hsplit}")
 
 
-@pytest.mark.parametrize("split", ["0", "1"])
+@pytest.mark.parametrize("split", ["whole", "split"])
 @pytest.mark.parametrize("B,S,Hq,Hkv,window", [
     (1, 320, 16, 1, 70), (2, 200, 4, 2, 33), (1, 64, 3, 1, 5), (1, 600, 2, 1, 300)])
-def test_swa_backward_dq_whole_and_split_kernels(cuda, monkeypatch, split, B, S, Hq, Hkv, window):
+def test_swa_backward_dq_whole_and_split_kernels(cuda, split, B, S, Hq, Hkv, window):
     """The dQ kernel over a unit's windowed key range, whole or split over two
     wave groups."""
-    monkeypatch.setenv("FGQA_BWD_DQ_SPLIT", split)
-    what = f"swa dq split={split} B{B} S{S} Hq{Hq} Hkv{Hkv} W{window}"
+    what = f"swa dq kernel={split} B{B} S{S} Hq{Hq} Hkv{Hkv} W{window}"
     print(what, flush=True)
     q, k, v, o, lse, do = _inputs(1560 + S + window, B, S, S, Hq, Hkv, window)
     refs = oracle.prefill_backward(q, k, v, o, lse, do, SCALE, causal=True, window=window)
-    _check(_gpu_backward(cuda, q, k, v, o, lse, do, window), refs, what)
+    _check(_gpu_backward(cuda, q, k, v, o, lse, do, window, dq_kernel=split), refs, what)
 
 
-def test_swa_backward_window_past_sequence_equals_causal_without_sink(cuda, monkeypatch):
+def test_swa_backward_window_past_sequence_equals_causal_without_sink(cuda):
     """A window at least the sequence length and no sink is the causal backward
     (bit for bit, with the same work split: the plans differ by default)."""
-    monkeypatch.setenv("FGQA_BWD_HSPLIT", "2")
-    monkeypatch.setenv("FGQA_BWD_DQ_SPLIT", "1")
     print("swa backward == causal backward", flush=True)
     q, k, v, o, lse, do = _inputs(1600, 1, 256, 256, 8, 2, 256, with_sink=False)
-    g_w = _gpu_backward(cuda, q, k, v, o, lse, do, 256)
-    g_c = _gpu_backward(cuda, q, k, v, o, lse, do, 0)
+    plan = dict(kv_head_split=2, dq_kernel="split")
+    g_w = _gpu_backward(cuda, q, k, v, o, lse, do, 256, **plan)
+    g_c = _gpu_backward(cuda, q, k, v, o, lse, do, 0, **plan)
     for a, b in zip(g_w, g_c):
         assert np.array_equal(a, b)
 
