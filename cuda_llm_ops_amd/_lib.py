@@ -200,6 +200,8 @@ def lib() -> ctypes.CDLL:
         L.fgqa_decode_workspace_bytes.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ctypes.c_size_t)]
         L.fgqa_decode_bf16.restype = ctypes.c_int
         L.fgqa_decode_bf16.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.c_void_p]
+        L.fgqa_decode_bf16_noalloc.restype = ctypes.c_int
+        L.fgqa_decode_bf16_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.c_void_p]
         L.fgqa_prefill_bf16.restype = ctypes.c_int
         L.fgqa_prefill_bf16.argtypes = [ctypes.POINTER(PrefillArgs), ctypes.c_void_p]
         L.fgqa_decode_paged_workspace_bytes.restype = ctypes.c_int

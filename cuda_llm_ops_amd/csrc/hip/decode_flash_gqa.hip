@@ -619,7 +619,44 @@ extern "C" int fgqa_decode_workspace_bytes(const fgqa_decode_args* a, size_t* by
     return FGQA_OK;
 }
 
-extern "C" int fgqa_decode_bf16(const fgqa_decode_args* a, void* stream) {
+// Device scratch of fgqa_decode_bf16_noalloc: the split partials and the
+// ragged work list of one call (FGQA_DECODE_NOALLOC_SCRATCH_BYTES, held by
+// every device the library runs on until the process ends).  In host code the
+// name `scratch` is a host-side stand-in, not a device address: the address is
+// looked up once per device (hipGetSymbolAddress, with that device current)
+// and only that pointer is passed to kernels.
+namespace fgqa {
+namespace {
+constexpr size_t kNoAllocScratchBytes = FGQA_DECODE_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kScratchDevices] = {nullptr};
+
+// The current device's copy of `scratch` (its address is looked up on the
+// first call on that device).  Returns nullptr and sets *status on failure.
+void* noalloc_scratch(int* status) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices) {
+        *status = FGQA_ERR_HIP;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) {
+            *status = FGQA_ERR_HIP;
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = ptr;
+    }
+    *status = FGQA_OK;
+    return g_scratch_ptr[dev];
+}
+
+// The decode call; `noalloc`: the workspace is the device scratch above
+// (the caller passes none), never the caller's or the library's buffer.
+int decode_run(const fgqa_decode_args* a, void* stream, bool noalloc) {
     int st = validate_decode(a);
     if (st != FGQA_OK) return st;
     st = validate_decode_pointers(a);
@@ -667,7 +704,13 @@ extern "C" int fgqa_decode_bf16(const fgqa_decode_args* a, void* stream) {
     std::unique_lock<std::mutex> ws_lock;   // held through the launches when the library's buffer is used
     if (plan.ws_bytes > 0) {
         void* ws = a->workspace;
-        if (ws == nullptr && a->workspace_bytes == 0) {
+        if (noalloc) {
+            // the partials and the list are written before they are read, so
+            // the previous call's contents need no clearing
+            if (plan.ws_bytes > kNoAllocScratchBytes) return FGQA_ERR_WORKSPACE;
+            ws = noalloc_scratch(&st);
+            if (ws == nullptr) return st;
+        } else if (ws == nullptr && a->workspace_bytes == 0) {
             ws_lock = workspace_lock();
             ws = internal_workspace(plan.ws_bytes, &st);
             if (st != FGQA_OK) return st;
@@ -706,6 +749,16 @@ extern "C" int fgqa_decode_bf16(const fgqa_decode_args* a, void* stream) {
     }
     if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
     return FGQA_OK;
+}
+
+}  // namespace
+}  // namespace fgqa
+
+extern "C" int fgqa_decode_bf16(const fgqa_decode_args* a, void* stream) { return decode_run(a, stream, false); }
+
+extern "C" int fgqa_decode_bf16_noalloc(const fgqa_decode_args* a, void* stream) {
+    if (a != nullptr && (a->workspace != nullptr || a->workspace_bytes != 0)) return FGQA_ERR_INVALID_ARGUMENT;
+    return decode_run(a, stream, true);
 }
 
 // ---------------------------------------------------------------- paged KV cache

@@ -98,6 +98,24 @@ int fgqa_decode_workspace_bytes(const fgqa_decode_args* args, size_t* bytes);
 int fgqa_decode_bf16(const fgqa_decode_args* args, void* stream);
 
 /*
+ * fgqa_decode_bf16 that allocates nothing.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results as fgqa_decode_bf16, except that `workspace` must be
+ * NULL and `workspace_bytes` 0 (else FGQA_ERR_INVALID_ARGUMENT): the split
+ * partials and the ragged work list go to a device array built into the
+ * library, FGQA_DECODE_NOALLOC_SCRATCH_BYTES on every device it runs on,
+ * held until the process ends.  A call whose plan needs more
+ * (fgqa_decode_workspace_bytes() above that size) returns FGQA_ERR_WORKSPACE
+ * and launches nothing; BASELINE-size ragged batches (64 x 64 heads, 32 K
+ * tokens) need about half of it.  All calls on one device share that array:
+ * calls that overlap on the GPU (different streams, or host threads racing)
+ * corrupt each other's results; calls on one stream are safe.
+ */
+#define FGQA_DECODE_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int fgqa_decode_bf16_noalloc(const fgqa_decode_args* args, void* stream);
+
+/*
  * Decode over a paged KV cache (block table), in bf16 or fp8.  No counterpart
  * in the reference: it extends the decode above (and its per-sequence
  * lengths) to the paged layout serving engines keep their KV cache in.

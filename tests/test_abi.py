@@ -22,7 +22,7 @@ def _exported():
 def test_c_abi_symbols_exported():
     hdr = open(os.path.join(ROOT, "include", "fgqa.h")).read()
     names = set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(fgqa_\w+)\s*\(", hdr, flags=re.M))
-    assert names == {"fgqa_decode_workspace_bytes", "fgqa_decode_bf16", "fgqa_prefill_bf16",
+    assert names == {"fgqa_decode_workspace_bytes", "fgqa_decode_bf16", "fgqa_decode_bf16_noalloc", "fgqa_prefill_bf16",
                      "fgqa_prefill_backward_workspace_bytes", "fgqa_prefill_backward_bf16",
                      "fgqa_decode_paged_workspace_bytes", "fgqa_decode_paged", "fgqa_sparse_prefill_bf16",
                      "fgqa_status_string", "fgqa_version"}
