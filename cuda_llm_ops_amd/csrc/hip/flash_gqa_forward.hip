@@ -20,7 +20,8 @@
 //                         of a tile, the other runs the softmax of its own.
 //                         With head dim 128 it stages the unit's Q tile (once
 //                         for both groups) and its O tile through 32 KB of LDS,
-//                         so those global loads and stores move whole rows.
+//                         so those global loads and stores move whole rows;
+//                         the two groups then merge and store half of O each.
 //
 // Per wave (32 rows) and 64-token K/V tile j, software pipelined one tile ahead:
 //   phase A: S^T(j+1) = K(j+1) . Q^T          v_mfma_f32_32x32x16_bf16, K from LDS,
@@ -222,7 +223,9 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         const int r = 4 * (wave + 4 * i) + (lane >> 4);
         voff_dma[i] = (uint32_t)r * vss + ((l16 ^ (4 * (r & 3))) << 4);
     }
-    auto issue_tile = [&](int j, int kb, int vb) {
+    // kb / vb: an int, or (split kernel loop) a std::integral_constant, so that
+    // every LDS address folds into the instructions' offset fields
+    auto issue_tile = [&](int j, auto kb, auto vb) {
         const int t0 = (t_first + j) * kPfTile;
         const uint32_t kdst = lds_base + kb * D::kKTileBytes + 1024 * wave;
         const uint32_t vdst = lds_base + 2 * D::kKTileBytes + vb * kPfVTileBytes + 1024 * wave;
@@ -259,7 +262,7 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
 #pragma unroll
     for (int kk = 0; kk < D::kKoffRegs; ++kk)
         koff[kk] = l32 * D::kRowBytes + (((2 * kk + g2) ^ D::kswz(l32)) << 4);
-    auto qk = [&](f32x16_t (&s)[2], int buf) {
+    auto qk = [&](f32x16_t (&s)[2], auto buf) {
         const unsigned char* kl = smem + buf * D::kKTileBytes;
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
@@ -393,7 +396,7 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         for (int db = 0; db < 4; ++db)
             voff[db] = (4 * g2 + q4) * kPfVRowBytes + ((4 * (db ^ q4) + 2 * dh + ((l16 >> 1) & 1)) << 4) + 8 * (l16 & 1);
     }
-    auto pv = [&](int buf) {
+    auto pv = [&](auto buf) {
         const unsigned char* vl = smem + 2 * D::kKTileBytes + buf * kPfVTileBytes;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
@@ -409,6 +412,14 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
 
     // this wave's direct LDS loads have landed (then a barrier publishes them)
     auto wait_vmem = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
+    // every load of this wave but the newest n has landed (loads complete in
+    // order); n is a multiple of 4 up to 8 (the split kernel's K and V tiles
+    // at head dim 128 take 4 instructions per wave each)
+    [[maybe_unused]] auto wait_vmem_but = [](int n) {
+        if (n >= 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else if (n >= 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    };
 
     // K runs one tile ahead of V: iteration j reads K(j+1) and V(j) while
     // K(j+2) and V(j+1) land in the buffers freed by iteration j-1.  No
@@ -435,9 +446,19 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
             dmaq(ic, q_lds + grp * 4096, voff, qrs);
         });
     }
-    if (n_tiles > 0) issue_tile(0, 0, 0);
-    if (n_tiles > 1) issue_tile(1, 1, -1);
-    wait_vmem();
+    if constexpr (kStageQ) {
+        // the first barrier needs Q and K(0) only: V(0) and K(1) are waited
+        // for by the first softmax phase
+        static_assert(D::kDmaK == 4, "wait_vmem_but counts 4 loads per tile");
+        if (n_tiles > 0) issue_tile(0, 0, -1);
+        if (n_tiles > 0) issue_tile(0, -1, 0);
+        if (n_tiles > 1) issue_tile(1, 1, -1);
+        wait_vmem_but((n_tiles > 0 ? 4 : 0) + (n_tiles > 1 ? 4 : 0));
+    } else {
+        if (n_tiles > 0) issue_tile(0, 0, 0);
+        if (n_tiles > 1) issue_tile(1, 1, -1);
+        wait_vmem();
+    }
     __syncthreads();
     if constexpr (kStageQ) {
         const unsigned char* ql = reinterpret_cast<const unsigned char*>(smem_all) + 2 * D::kGroupBytes +
@@ -518,10 +539,33 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         // 2^8 per element.  Otherwise every P stays below 2^16 and the row
         // max is never computed (it is the softmax phase's costliest
         // reduction, and this phase sets the pace).
-        auto vphase = [&](int j) {
+        // j: the MFMA phase this softmax phase follows (-1 for the first one);
+        // par = j & 1 as a constant.
+        auto vphase = [&](int j, auto par) {
+            constexpr int P = decltype(par)::value;
+            using CK = std::integral_constant<int, 1 - P>;   // K buffer of tile j + 3
+            using CV = std::integral_constant<int, P>;       // V buffer of tile j + 2
+            using CN = std::integral_constant<int, -1>;
             // the softmax phase sets the pace: its wave wins issue ties
             // against the MFMA wave of the same SIMD
             __builtin_amdgcn_s_setprio(1);
+            // Head dim 128: the next tiles go in first, under the softmax (the
+            // MFMA phase j before this one's barrier has finished with K
+            // buffer (j+1)&1 and V buffer j&1); the loads of the previous
+            // softmax phase are awaited at the end.  Issuing a tile's loads
+            // stalls the issuing wave for a few hundred cycles, which the
+            // softmax then no longer waits behind.
+            [[maybe_unused]] int n_new = 0;
+            if constexpr (kStageQ) {
+                if (j + 3 < n_tiles) {
+                    issue_tile(j + 3, CK{}, CN{});
+                    n_new += D::kDmaK;
+                }
+                if (j + 2 < n_tiles) {
+                    issue_tile(j + 2, CN{}, CV{});
+                    n_new += 4;
+                }
+            }
             mask(s, j + 1);
             float lt = softmax_p(s);
             if (__builtin_amdgcn_ballot_w64(m_run == -INFINITY || !(lt <= 65536.f)) != 0) {
@@ -532,18 +576,26 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) asm volatile("" : "+v"(pop[kb]));
             asm volatile("" : "+v"(l_run));
-            wait_vmem();                  // K(j+2), V(j+1), issued one VALU phase ago
-            if (j + 3 < n_tiles) issue_tile(j + 3, (j + 1) & 1, -1);
-            if (j + 2 < n_tiles) issue_tile(j + 2, -1, j & 1);
+            if constexpr (kStageQ) {
+                wait_vmem_but(n_new);         // K(j+2), V(j+1), issued one softmax phase ago
+            } else {
+                wait_vmem();                  // K(j+2), V(j+1), issued one softmax phase ago
+                if (j + 3 < n_tiles) issue_tile(j + 3, CK{}, CN{});
+                if (j + 2 < n_tiles) issue_tile(j + 2, CN{}, CV{});
+            }
             __builtin_amdgcn_s_setprio(0);
             __syncthreads();
         };
         // S(j+1) (unless this is the last tile) and O += V(j).P(j): K reads
         // run 4 MFMAs ahead, V reads 4 ahead at 2 per MFMA.
-        auto mphase = [&](auto with_qk, int j) {
+        // par = j & 1 as a constant: the buffer offsets are then instruction
+        // immediates, and the phase issues nothing but LDS reads and MFMAs.
+        auto mphase = [&](auto with_qk, int j, auto par) {
             constexpr int kA = decltype(with_qk)::value ? 2 * D::kSteps : 0;
-            if constexpr (kA > 0) qk(s, (j + 1) & 1);
-            pv(j & 1);
+            constexpr int P = decltype(par)::value;
+            (void)j;
+            if constexpr (kA > 0) qk(s, std::integral_constant<int, 1 - P>{});
+            pv(std::integral_constant<int, P>{});
             if constexpr (kA > 0) {
                 __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // DS read
 #pragma unroll
@@ -569,12 +621,26 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
             __builtin_amdgcn_sched_barrier(0);
             __syncthreads();
         };
-        vphase(-1);
-        for (int j = 0; j + 1 < n_tiles; ++j) {
-            mphase(std::true_type{}, j);
-            vphase(j);
+        // the loop runs two tiles per trip, so that every buffer index is a constant
+        using C0 = std::integral_constant<int, 0>;
+        using C1 = std::integral_constant<int, 1>;
+        vphase(-1, C1{});
+        int j = 0;
+        for (; j + 2 < n_tiles; j += 2) {
+            mphase(std::true_type{}, j, C0{});
+            vphase(j, C0{});
+            mphase(std::true_type{}, j + 1, C1{});
+            vphase(j + 1, C1{});
         }
-        if (n_tiles > 0) mphase(std::false_type{}, n_tiles - 1);
+        if (j + 1 < n_tiles) {
+            mphase(std::true_type{}, j, C0{});
+            vphase(j, C0{});
+            ++j;
+        }
+        if (n_tiles > 0) {
+            if (j & 1) mphase(std::false_type{}, j, C1{});
+            else mphase(std::false_type{}, j, C0{});
+        }
         if (grp == 0) __syncthreads();
     } else {
         f32x16_t sa[2], sb[2];
@@ -590,7 +656,62 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         }
     }
 
-    if constexpr (kGroups == 2) {
+    if constexpr (kGroups == 2 && kStageQ) {
+        // Head dim 128: each group keeps O columns 64*grp .. +63 (blocks
+        // 2*grp, 2*grp + 1) and hands the other half, with its max and sum, to
+        // the same wave slot of the other group through its own tile
+        // buffers (idle since the loop's last barrier): 8 blocks of [lane][4]
+        // floats, then [lane] max and [lane] sum.  Both groups then merge and
+        // store their half, so neither waits for the other to store all of O.
+        // Both merge in one form, group 0's terms first, so the two halves of
+        // a row share bit-identical max, sum and weights.
+        float* mine = reinterpret_cast<float*>(smem_all + grp * D::kGroupBytes) + wave * 34 * kWave;
+        const float* theirs = reinterpret_cast<const float*>(smem_all + (1 - grp) * D::kGroupBytes) + wave * 34 * kWave;
+        f32x4_t* mw = reinterpret_cast<f32x4_t*>(mine) + lane;
+        const f32x4_t* mr = reinterpret_cast<const f32x4_t*>(theirs) + lane;
+        auto handoff = [&](auto od) {
+            constexpr int o = decltype(od)::value;
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4)
+                    mw[(k * 4 + i4) * kWave] = f32x4_t{oacc[o + k][4 * i4], oacc[o + k][4 * i4 + 1],
+                                                       oacc[o + k][4 * i4 + 2], oacc[o + k][4 * i4 + 3]};
+        };
+        if (grp == 0) handoff(std::integral_constant<int, 2>{});
+        else handoff(std::integral_constant<int, 0>{});
+        mine[32 * kWave + lane] = m_run;
+        mine[33 * kWave + lane] = l_run;
+        __syncthreads();
+        const float m_o = theirs[32 * kWave + lane];
+        const float l_o = theirs[33 * kWave + lane];
+        const float mA = grp == 0 ? m_run : m_o, lA = grp == 0 ? l_run : l_o;   // group 0's
+        const float mB = grp == 0 ? m_o : m_run, lB = grp == 0 ? l_o : l_run;   // group 1's
+        const float m = fmaxf(mA, mB);
+        const float mu = (m == -INFINITY) ? 0.f : m;
+        const float aA = fast_exp2(mA - mu);   // 0 when a group saw no key
+        const float aB = fast_exp2(mB - mu);
+        auto merge_half = [&](auto kd) {
+            constexpr int o = decltype(kd)::value;
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    const f32x4_t other = mr[(k * 4 + i4) * kWave];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float own = oacc[o + k][4 * i4 + e];
+                        const float oa = grp == 0 ? own : other[e], ob = grp == 0 ? other[e] : own;
+                        oacc[o + k][4 * i4 + e] = __builtin_fmaf(oa, aA, ob * aB);
+                    }
+                }
+        };
+        if (grp == 0) merge_half(std::integral_constant<int, 0>{});
+        else merge_half(std::integral_constant<int, 2>{});
+        l_run = __builtin_fmaf(lA, aA, lB * aB);
+        m_run = m;
+        m_use = mu;
+    } else if constexpr (kGroups == 2) {
         // Group 1 hands its partial state to group 0 (same wave slot, same lane)
         // through the tile buffers, idle since the loop's last barrier: per
         // wave, 16 blocks of [lane][4] O values (one 16-byte access per lane
@@ -635,7 +756,39 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     const float sink = has_sink ? p.sink[h] : 0.f;
     const float denom = (l_run > 0.f && has_sink) ? l_run + sink * fast_exp2(-m_use) : l_run;
     const float inv = (l_run > 0.f) ? 1.f / denom : 0.f;
-    {
+    if constexpr (kGroups == 2 && kStageQ) {
+        // this group's 64 columns of the wave's 32 rows go out through 4 KB of
+        // the (idle) Q area: 8-byte pieces into 128-byte half rows, chunk c of
+        // row r in slot c ^ (r % 8), then 8 half rows per store instruction
+        unsigned char* ol = smem_all + 2 * D::kGroupBytes + (grp * kPfWaves + wave) * 4096;
+        auto stage = [&](auto kd) {
+            constexpr int o = decltype(kd)::value;
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    bf16x4_t w;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) w[e] = (__bf16)(oacc[o + k][i4 * 4 + e] * inv);
+                    *reinterpret_cast<bf16x4_t*>(ol + l32 * 128 + (((4 * k + i4) ^ (l32 & 7)) << 4) + g2 * 8) = w;
+                }
+        };
+        if (grp == 0) stage(std::integral_constant<int, 0>{});
+        else stage(std::integral_constant<int, 2>{});
+        // this wave's LDS writes complete before its reads (no other wave uses the area)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 8 * i + (lane >> 3);
+            const int cc = lane & 7;
+            const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ol + r * 128 + ((cc ^ (r & 7)) << 4));
+            if (q0w + r < p.sq) {
+                __bf16* orow = p.o + b * p.o_sb + (int64_t)(q0w + r) * p.o_ss + h * p.o_sh;
+                *reinterpret_cast<u32x4_t*>(orow + 64 * grp + 8 * cc) = v;
+            }
+        }
+        if (grp == 1) return;   // group 0 writes the LSE
+    } else {
         // O goes out through 8 KB of idle LDS per wave (the split kernel: the
         // wave's Q area, or with head dim 192 group 1's tile buffers, past the
         // merge area; the whole-range kernel: its tile buffers, which every
