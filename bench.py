@@ -4,12 +4,16 @@ Default (the driver's contract): BASELINE config 2, GQA decode at B=60,
 S=4096, Hq=128, Hkv=8, D=128, bf16 in/out, fp32 accumulation, inputs resident
 in HBM.  One "step" = one decode over the whole batch.  Prints ONE JSON line:
 value = decode KV-read throughput in GB/s (decimal), with the roofline of the
-decode kernel against 8 TB/s HBM, the paged-KV decode (bf16 and fp8 caches)
-at config 3's lengths, the causal prefill of BASELINE config 4 and its
-backward (TFLOPS against 2.5 PFLOP/s bf16 dense MFMA) beside it, and the CPU
-oracle timed on a bounded sample of the same decode workload.
+decode kernel against 8 TB/s HBM.  Beside it: the other BASELINE configs (1
+and 3 decode, 4 and 5 causal prefill, each with its roofline: TFLOPS against
+2.5 PFLOP/s bf16 dense MFMA for prefill), the paged-KV decode (bf16 and fp8
+caches) at config 3's lengths, the sliding-window, MLA and sparse-index
+prefill and the backward passes; max-abs / mean-abs of each BASELINE
+config's output against the CPU oracle (sampled batches or rows, outside the
+timed regions); and the CPU oracle timed on a bounded sample of the decode
+workload (`cpu_baseline`) and on all of config 4 (`cpu_baseline_prefill`).
 
-    python bench.py [--steps K] [--warmup W] [--split-tokens N] [--no-cpu] [--all]
+    python bench.py [--steps K] [--warmup W] [--split-tokens N] [--no-cpu] [--no-configs] [--no-check]
 
 Only one GPU is used: --gpus N with N > 1 exits with a message.
 """
@@ -146,7 +150,98 @@ def bench_decode(cfg_id, steps, warmup, split_tokens, dev):
                 ms_step=ms_step, avg_launch_ms=avg_launch_ms, median_ms=per[len(per) // 2], min_ms=per[0])
 
 
-def bench_prefill(cfg_id, steps, warmup, dev):
+def _host_u16(t):
+    import numpy as np
+    import torch
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _err(out_u16, ref_u16):
+    """max-abs and mean-abs of a bf16 output against the oracle's (the parity
+    figures of the reference harness, test_decode_flash_gqa.cu:311-319)."""
+    import numpy as np
+
+    import oracle
+    d = np.abs(oracle.bf16_to_f32(out_u16).astype(np.float64) - oracle.bf16_to_f32(ref_u16))
+    return float(d.max()), float(d.sum()), int(d.size)
+
+
+def decode_check(res, batches, threads):
+    """GPU decode output (the last timed step's) against the C oracle on the
+    listed batches, all heads; outside the timed region."""
+    import numpy as np
+
+    import oracle
+    mx, sm, n = 0.0, 0.0, 0
+    for b in batches:
+        L = res["cfg"]["S"] if res["lens"] is None else int(res["lens"][b])
+        ref, _ = oracle.decode(_host_u16(res["q"][b:b + 1]), _host_u16(res["k"][b:b + 1, :L]),
+                               _host_u16(res["v"][b:b + 1, :L]), SCALE, nthreads=threads, with_lse=False)
+        m, s, c = _err(_host_u16(res["out"][b:b + 1]), ref)
+        mx, sm, n = max(mx, m), sm + s, n + c
+    return dict(max_abs=mx, mean_abs=sm / n, tol={"max_abs": 2e-2, "mean_abs": 2e-3},
+                sample=f"batches {list(batches)}, all heads, against the C oracle")
+
+
+def decode_block(cfg_id, steps, warmup, dev, check_batches, threads):
+    """A decode config beside the default line: timing, HBM roofline and the
+    oracle check (check_batches None: the shortest and longest sequences and
+    two fixed ones)."""
+    import numpy as np
+    res = bench_decode(cfg_id, steps, warmup, 0, dev)
+    if check_batches is None:
+        check_batches = sorted({int(np.argmin(res["lens"])), int(np.argmax(res["lens"])), 7, 40})
+    cfg = res["cfg"]
+    achieved = res["kv_bytes"] / (res["avg_launch_ms"] * 1e-3) / 1e9
+    block = dict(
+        config=f"GQA decode B={cfg['B']} S={'<=' if cfg['ragged'] else ''}{cfg['S']} Hq={cfg['Hq']} "
+               f"Hkv={cfg['Hkv']} D=128{' ragged lengths' if cfg['ragged'] else ''} (BASELINE config {cfg_id})",
+        us_avg=round(res["avg_launch_ms"] * 1e3, 2), us_median=round(res["median_ms"] * 1e3, 2),
+        us_min=round(res["min_ms"] * 1e3, 2), GBs=round(achieved, 2),
+        roofline={"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                  "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_BYTES.get(f"decode_cfg{cfg_id}"),
+                  "algorithmic_bytes": res["kv_bytes"]},
+        error=decode_check(res, check_batches, threads))
+    if cfg_id == 1:
+        block["note"] = "1 MiB of KV stays in the caches: a latency figure, not an HBM-bound one"
+    return block
+
+
+def prefill_check(t, row_blocks, threads):
+    """GPU prefill output against the C oracle on row blocks (b, r0, r1) of
+    every query head; outside the timed region."""
+    mx, sm, n = 0.0, 0.0, 0
+    import oracle
+    for b, r0, r1 in row_blocks:
+        ref, _ = oracle.prefill(_host_u16(t["q"][b:b + 1, r0:r1]), _host_u16(t["k"][b:b + 1, :r1]),
+                                _host_u16(t["v"][b:b + 1, :r1]), SCALE, causal=True, q_offset=r0,
+                                nthreads=threads)
+        m, s, c = _err(_host_u16(t["out"][b:b + 1, r0:r1]), ref)
+        mx, sm, n = max(mx, m), sm + s, n + c
+    return dict(max_abs=mx, mean_abs=sm / n, tol={"max_abs": 2e-2, "mean_abs": 2e-3})
+
+
+def cpu_baseline_prefill(t, threads):
+    """The C oracle (OpenMP over batch x head x query block) on all of BASELINE
+    config 4, timed on the host cores; its output also gives config 4's
+    max-abs / mean-abs over every row and head."""
+    import oracle
+    qh, kh, vh = _host_u16(t["q"]), _host_u16(t["k"]), _host_u16(t["v"])
+    B, S, Hq = qh.shape[0], qh.shape[1], qh.shape[2]
+    t0 = time.perf_counter()
+    ref, _ = oracle.prefill(qh, kh, vh, SCALE, causal=True, nthreads=threads)
+    elapsed = time.perf_counter() - t0
+    flops = B * Hq * 2 * S * S * (128 + 128) // 2
+    m, s, c = _err(_host_u16(t["out"]), ref)
+    cpu = dict(value=round(flops / elapsed / 1e12, 5), unit="TFLOP/s", cores=threads, kind="port",
+               sample=f"the whole config 4 prefill (all {S} rows, {Hq} heads), {elapsed:.2f} s on {threads} "
+                      f"OpenMP threads; FLOPs counted as on the GPU (causal-halved)")
+    err = dict(max_abs=m, mean_abs=s / c, tol={"max_abs": 2e-2, "mean_abs": 2e-3},
+               sample="every row and head, against the C oracle")
+    return cpu, err
+
+
+def bench_prefill(cfg_id, steps, warmup, dev, keep=None):
     import torch
 
     import cuda_llm_ops_amd as fg
@@ -165,13 +260,15 @@ def bench_prefill(cfg_id, steps, warmup, dev):
     flops = B * Hq * 2 * S * S * (128 + 128) // 2
     avg = total_ms / steps
     tflops = flops / (avg * 1e-3) / 1e12
+    if keep is not None:
+        keep.update(q=q, k=k, v=v, out=out, lse=lse)
     return dict(config=f"causal prefill B={B} S={S} Hq={Hq} Hkv={Hkv} D=128 (BASELINE config {cfg_id})",
                 us_avg=round(avg * 1e3, 2), us_median=round(per[len(per) // 2] * 1e3, 2),
                 us_min=round(per[0] * 1e3, 2),
                 roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
                           "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
                           "traffic": TRAFFIC_BYTES.get(f"prefill_cfg{cfg_id}"),
-                          "kernel": "prefill_split_kernel" if cfg_id == 4 else "prefill_kernel",
+                          "kernel": "prefill_split_kernel" if B * Hq * S // 128 < 4 * 256 else "prefill_kernel",
                           "algorithmic_flops": flops})
 
 
@@ -488,7 +585,9 @@ def main():
     ap.add_argument("--no-sparse", action="store_true")
     ap.add_argument("--page-size", type=int, default=16, help="with --mode paged")
     ap.add_argument("--kv", choices=["bf16", "fp8"], default="bf16", help="with --mode paged")
-    ap.add_argument("--all", action="store_true", help="also report configs 1, 3 and 5 (to stderr)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="leave out BASELINE configs 1, 3 and 5 (reported by default)")
+    ap.add_argument("--no-check", action="store_true", help="leave out the oracle checks (max-abs / mean-abs)")
     ap.add_argument("--mode", choices=["bench", "decode", "paged", "prefill", "swa", "mla", "sparse", "backward",
                                        "swa_backward", "mla_backward", "copy"],
                     default="bench",
@@ -568,8 +667,30 @@ def main():
                      "min_launch_us": round(res["min_ms"] * 1e3, 2)},
         "decode_all_tensor_GBs": round((res["kv_bytes"] + res["qo_bytes"]) / (res["ms_step"] * 1e-3) / 1e9, 2),
     }
+    threads = min(os.cpu_count() or 1, 16)
+    if not args.no_check:
+        line["error"] = decode_check(res, (0, 29, 59), threads)
+    keep4 = {}
     if not args.no_prefill:
-        line["prefill"] = bench_prefill(4, args.steps, args.warmup, dev)
+        line["prefill"] = bench_prefill(4, args.steps, args.warmup, dev, keep=keep4)
+    if not args.no_configs:
+        line["decode_cfg1"] = decode_block(1, args.steps, args.warmup, dev, (0, 1), threads)
+        line["decode_cfg3"] = decode_block(3, max(5, args.steps // 5), 2, dev, None, threads)
+        keep5 = {}
+        line["prefill_cfg5"] = bench_prefill(5, max(3, args.steps // 10), 2, dev, keep=keep5)
+        if not args.no_check:
+            S5, B5 = PREFILL_CONFIGS[5]["S"], PREFILL_CONFIGS[5]["B"]
+            import numpy as np
+            rng = np.random.default_rng(5)
+            blocks = [(0, 0, 128), (0, S5 - 128, S5)]
+            for b in range(B5):
+                for r0 in sorted(rng.integers(0, S5 // 32, size=2) * 32):
+                    blocks.append((b, int(r0), int(r0) + 32))
+            line["prefill_cfg5"]["error"] = prefill_check(keep5, blocks, threads)
+            line["prefill_cfg5"]["error"]["sample"] = (
+                f"rows [0,128) and [{S5 - 128},{S5}) of batch 0 and two random 32-row blocks of every batch "
+                f"({sum(r1 - r0 for _, r0, r1 in blocks)} rows x 32 heads), against the C oracle")
+        del keep5
     if not args.no_paged:
         line["decode_paged"] = [bench_paged(3, max(5, args.steps // 5), 2, dev, 16, kv)
                                 for kv in ("bf16", "fp8")]
@@ -587,14 +708,10 @@ def main():
         line["mla_backward"] = bench_mla_backward(max(5, args.steps // 5), 2, dev)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_decode(res)
-    if args.all:
-        for cid in (1, 3):
-            r = bench_decode(cid, args.steps, args.warmup, 0, dev)
-            print(json.dumps({"config": cid, "us_avg": r["avg_launch_ms"] * 1e3,
-                              "GBs": r["kv_bytes"] / (r["avg_launch_ms"] * 1e-3) / 1e9}), file=sys.stderr)
-            del r
-        r = bench_prefill(5, max(3, args.steps // 10), 2, dev)
-        print(json.dumps({"config": 5, **r}), file=sys.stderr)
+        if keep4:
+            line["cpu_baseline_prefill"], err4 = cpu_baseline_prefill(keep4, threads)
+            if not args.no_check:
+                line["prefill"]["error"] = err4
     print(json.dumps(line), flush=True)
 
 

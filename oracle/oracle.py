@@ -13,7 +13,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+# FGQA_ORACLE_LIB selects another build of the same oracle (the sanitizer
+# build, `make -C oracle liboracle_san.so`); by default the optimised one.
+_LIB_PATH = os.path.abspath(os.environ.get("FGQA_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so"))
 _lib = None
 
 _u16p = ctypes.POINTER(ctypes.c_uint16)

@@ -40,6 +40,7 @@
 
 #include "FlashGQA/decode_flash_gqa_kernel.h"
 #include "FlashGQA/flash_gqa_forward_kernel.h"
+#include "Utils/utils.h"
 #include "fgqa_oracle.h"
 
 namespace {
@@ -206,7 +207,8 @@ bool run_decode(const Config& c, const Options& opt, int threads) {
         // padding past each length is NaN: it must never be read
 #pragma omp parallel for schedule(dynamic)
         for (int b = 0; b < B; ++b)
-            for (size_t i = (size_t)b * S * Hkv * D + (size_t)lens[b] * Hkv * D; i < (size_t)(b + 1) * S * Hkv * D; ++i)
+            for (int64_t i = GET_1D_INDEX_FROM_4D(b, lens[b], 0, 0, S, Hkv, D);
+                 i < GET_1D_INDEX_FROM_4D(b + 1, 0, 0, 0, S, Hkv, D); ++i)
                 k[i] = v[i] = 0x7FC0;
     }
     int64_t valid = 0;
@@ -336,8 +338,8 @@ bool run_prefill(const Config& c, const Options& opt, int threads) {
         for (int r = 0; r < bl.n; ++r)
             for (int h = 0; h < Hq; ++h)
                 for (int d = 0; d < D; ++d)
-                    err.add(out[(size_t)bl.b * qs[0] + (size_t)(bl.r0 + r) * qs[1] + (size_t)h * D + d],
-                            ref[((size_t)r * Hq + h) * D + d]);
+                    err.add(out[GET_1D_INDEX_FROM_4D(bl.b, bl.r0 + r, h, d, S, Hq, D)],
+                            ref[GET_1D_INDEX_FROM_3D(r, h, d, Hq, D)]);
         for (int h = 0; h < Hq; ++h)
             for (int r = 0; r < bl.n; ++r) {
                 const double g = lse[((size_t)bl.b * Hq + h) * S + bl.r0 + r];
