@@ -40,7 +40,6 @@ fgqa_decode_args contiguous_decode(const bf16_t* q, const bf16_t* k, const bf16_
 void LaunchFlashGqaBf16Kernel(const bf16_t* q, const bf16_t* k, const bf16_t* v, float scale, bf16_t* o,
                               float* oIntermediate, int batchSize, int seqLength, int numQueryHeads,
                               int numKvHeads, int headDim) {
-    (void)oIntermediate;
     // The reference returns before launching when batchSize or seqLength is
     // not positive (decode_flash_gqa_kernel.cu:416-418); so does the drop-in.
     if (batchSize <= 0 || seqLength <= 0) {
@@ -49,7 +48,18 @@ void LaunchFlashGqaBf16Kernel(const bf16_t* q, const bf16_t* k, const bf16_t* v,
     }
     fgqa_decode_args a =
         contiguous_decode(q, k, v, scale, o, batchSize, seqLength, numQueryHeads, numKvHeads, headDim);
-    g_last_status = fgqa_decode_bf16(&a, nullptr);
+    // The split partials (two or more fp32 rows per query head, with their
+    // max and sum) never fit in oIntermediate's batchSize * numQueryHeads *
+    // headDim floats, so they go to the library's fixed device scratch: the
+    // call allocates nothing and does not synchronize.  Only a plan beyond
+    // that scratch falls back to the library's cached buffer.
+    (void)oIntermediate;
+    size_t need = 0;
+    int st = fgqa_decode_workspace_bytes(&a, &need);
+    if (st == FGQA_OK)
+        st = need <= FGQA_DECODE_NOALLOC_SCRATCH_BYTES ? fgqa_decode_bf16_noalloc(&a, nullptr)
+                                                        : fgqa_decode_bf16(&a, nullptr);
+    g_last_status = st;
 }
 
 void LaunchFlashGqaBf16KernelVarlen(const bf16_t* q, const bf16_t* k, const bf16_t* v, float scale, bf16_t* o,
@@ -58,7 +68,13 @@ void LaunchFlashGqaBf16KernelVarlen(const bf16_t* q, const bf16_t* k, const bf16
     fgqa_decode_args a =
         contiguous_decode(q, k, v, scale, o, batchSize, maxSeqLength, numQueryHeads, numKvHeads, headDim);
     a.seqlens = seqLengths;
-    g_last_status = fgqa_decode_bf16(&a, nullptr);
+    // split partials and the ragged work list in the fixed device scratch, as above
+    size_t need = 0;
+    int st = fgqa_decode_workspace_bytes(&a, &need);
+    if (st == FGQA_OK)
+        st = need <= FGQA_DECODE_NOALLOC_SCRATCH_BYTES ? fgqa_decode_bf16_noalloc(&a, nullptr)
+                                                        : fgqa_decode_bf16(&a, nullptr);
+    g_last_status = st;
 }
 
 void LaunchFlashGqaBf16KernelPaged(const bf16_t* q, const void* kCache, const void* vCache, bool kvFp8, float scale,

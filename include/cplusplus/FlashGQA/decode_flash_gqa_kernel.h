@@ -21,7 +21,11 @@ constexpr int WARP_SIZE = 64;
  * @param o Device output tensor [batchSize, numQueryHeads, headDim].
  * @param oIntermediate Device fp32 buffer of batchSize*numQueryHeads*headDim floats.
  *        Accepted for signature compatibility and left untouched: the split
- *        partials live in a library-owned per-device workspace.
+ *        partials (two or more fp32 rows per query head, with their max and
+ *        sum) do not fit in it and go to the library's fixed device scratch
+ *        (fgqa_decode_bf16_noalloc), so the call allocates nothing; calls
+ *        that share that scratch must not overlap on the GPU.  Only a plan
+ *        beyond it (over 32 MiB of partials) uses the library's cached buffer.
  * @param batchSize Batch size.
  * @param seqLength Sequence length (any value >= 1; the reference required a multiple of 128).
  * @param numQueryHeads Number of query heads.
@@ -46,7 +50,9 @@ void LaunchFlashGqaBf16Kernel(const bf16_t* q,
 /**
  * @brief Ragged variant: per-sequence valid lengths (device int32 [batchSize],
  *        each <= maxSeqLength) over K/V padded to maxSeqLength; positions at or
- *        past a sequence's length are never read.  No reference counterpart.
+ *        past a sequence's length are never read.  Split partials go to the
+ *        library's fixed device scratch, as for LaunchFlashGqaBf16Kernel.  No
+ *        reference counterpart.
  */
 void LaunchFlashGqaBf16KernelVarlen(const bf16_t* q,
                                     const bf16_t* k,

@@ -176,29 +176,35 @@ def test_decode_config3_ragged_full_size(cuda):
 
 
 def test_decode_cplusplus_dropin(cuda):
-    """The reference-signature C++ entry point LaunchFlashGqaBf16Kernel (default stream)."""
+    """The reference-signature C++ entry point LaunchFlashGqaBf16Kernel (default
+    stream), twice in a row at two shapes whose split plans differ: both match
+    the oracle, and oIntermediate is left untouched (the partials live in the
+    library's fixed device scratch, so the call allocates nothing)."""
     import torch
     fg = _fg()
     L = fg.lib()
-    B, S, Hq, Hkv = 2, 512, 32, 2
-    q = oracle.normal_bf16(500, (B, Hq, 128))
-    k = oracle.normal_bf16(500, (B, S, Hkv, 128), stream=1)
-    v = oracle.normal_bf16(500, (B, S, Hkv, 128), stream=2)
-    o_ref, _ = oracle.decode(q, k, v, SCALE)
-    qd, kd, vd = (to_torch_bf16(x, cuda) for x in (q, k, v))
-    od = torch.zeros((B, Hq, 128), dtype=torch.bfloat16, device=cuda)
-    oi = torch.zeros((B, Hq, 128), dtype=torch.float32, device=cuda)
     fn = getattr(L, "_Z24LaunchFlashGqaBf16KernelPK6bf16_tS1_S1_fPS_Pfiiiii")
     fn.restype = None
-    torch.cuda.synchronize()
-    fn(ctypes.c_void_p(qd.data_ptr()), ctypes.c_void_p(kd.data_ptr()), ctypes.c_void_p(vd.data_ptr()),
-       ctypes.c_float(SCALE), ctypes.c_void_p(od.data_ptr()), ctypes.c_void_p(oi.data_ptr()),
-       B, S, Hq, Hkv, 128)
     st = getattr(L, "_Z21FlashGqaGetLastStatusv")
     st.restype = ctypes.c_int
-    assert st() == 0
-    torch.cuda.synchronize()
-    assert_close(od.float().cpu().numpy(), oracle.bf16_to_f32(o_ref), "C++ drop-in decode")
+    for seed, (B, S, Hq, Hkv) in ((500, (2, 512, 32, 2)), (501, (1, 8192, 16, 1))):
+        need = fg.decode_workspace_bytes(B, S, Hq, Hkv)
+        assert 0 < need <= 32 << 20, need
+        q = oracle.normal_bf16(seed, (B, Hq, 128))
+        k = oracle.normal_bf16(seed, (B, S, Hkv, 128), stream=1)
+        v = oracle.normal_bf16(seed, (B, S, Hkv, 128), stream=2)
+        o_ref, _ = oracle.decode(q, k, v, SCALE)
+        qd, kd, vd = (to_torch_bf16(x, cuda) for x in (q, k, v))
+        od = torch.zeros((B, Hq, 128), dtype=torch.bfloat16, device=cuda)
+        oi = torch.full((B, Hq, 128), 7.0, dtype=torch.float32, device=cuda)
+        torch.cuda.synchronize()
+        fn(ctypes.c_void_p(qd.data_ptr()), ctypes.c_void_p(kd.data_ptr()), ctypes.c_void_p(vd.data_ptr()),
+           ctypes.c_float(SCALE), ctypes.c_void_p(od.data_ptr()), ctypes.c_void_p(oi.data_ptr()),
+           B, S, Hq, Hkv, 128)
+        assert st() == 0
+        torch.cuda.synchronize()
+        assert_close(od.float().cpu().numpy(), oracle.bf16_to_f32(o_ref), f"C++ drop-in decode B={B} S={S}")
+        assert bool((oi == 7.0).all().item()), "oIntermediate was written"
     # unsupported head_dim: silent no-op, status says why
     fn(ctypes.c_void_p(qd.data_ptr()), ctypes.c_void_p(kd.data_ptr()), ctypes.c_void_p(vd.data_ptr()),
        ctypes.c_float(SCALE), ctypes.c_void_p(od.data_ptr()), ctypes.c_void_p(oi.data_ptr()), B, S, Hq, Hkv, 64)
