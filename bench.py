@@ -41,8 +41,8 @@ SCALE = 1.0 / math.sqrt(128)
 # with the commands are profiles/*_hbm_traffic.md.  Re-measure when a kernel
 # changes.
 TRAFFIC_BYTES = {
-    "decode_cfg2": 1010662256,   # = Q+K+V+O (1,010,565,120 B) + 0.01 %
-    "prefill_cfg4": 51483996,    # Q+O+LSE 32.25 MiB + K/V 2 MiB fetched once per XCD
+    "decode_cfg2": 1010681051,   # = Q+K+V+O (1,010,565,120 B) + 0.01 %
+    "prefill_cfg4": 50974758,    # Q+O+LSE 32.25 MiB + K/V 2 MiB fetched about once per XCD
 }
 
 DECODE_CONFIGS = {
