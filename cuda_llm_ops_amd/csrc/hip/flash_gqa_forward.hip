@@ -15,7 +15,9 @@
 //                         unit's KV range side by side (2 waves per SIMD) and
 //                         merge their partial (max, sum, O) through LDS.  Used
 //                         when there are too few units to keep every CU busy
-//                         with two workgroups until the end.  The groups run
+//                         with two workgroups until the end.  Persistent: one
+//                         workgroup per CU runs its share of the units in a
+//                         fixed order that balances their tile counts.  The groups run
 //                         ping-pong: while one wave of a SIMD issues the MFMAs
 //                         of a tile, the other runs the softmax of its own.
 //                         With head dim 128 it stages the unit's Q tile (once
@@ -136,7 +138,11 @@ template <int kGroups, bool kSwa, int kDk>
 __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* smem_all, int qb, int hg, int kvh,
                                         int b) {
     using D = PfDims<kDk>;
-    const int tid = threadIdx.x;
+    // opaque in the split kernel: its loop over units recomputes what depends
+    // on the thread index inside each unit instead of holding it in
+    // registers across the loop
+    int tid = threadIdx.x;
+    if constexpr (kGroups == 2) asm volatile("" : "+v"(tid));
     const int lane = tid & (kWave - 1);
     const int wave_wg = __builtin_amdgcn_readfirstlane(tid / kWave);   // wave-uniform
     const int grp = wave_wg / kPfWaves;
@@ -590,12 +596,54 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         // run 4 MFMAs ahead, V reads 4 ahead at 2 per MFMA.
         // par = j & 1 as a constant: the buffer offsets are then instruction
         // immediates, and the phase issues nothing but LDS reads and MFMAs.
+        // The operand reads are written in the order they should issue: the
+        // phase's 16 (or 24) K operands and then its 16 V operands form one
+        // stream, each read 4 MFMAs ahead of its use into a ring of 4
+        // registers.  So even a schedule that keeps source order (which the
+        // compiler falls back to when it judges a region's register pressure
+        // too high) keeps the reads ahead of the MFMAs.
         auto mphase = [&](auto with_qk, int j, auto par) {
             constexpr int kA = decltype(with_qk)::value ? 2 * D::kSteps : 0;
             constexpr int P = decltype(par)::value;
+            constexpr int kOps = kA + 16;
             (void)j;
-            if constexpr (kA > 0) qk(s, std::integral_constant<int, 1 - P>{});
-            pv(std::integral_constant<int, P>{});
+            const unsigned char* kl = smem + (1 - P) * D::kKTileBytes;
+            const unsigned char* vl = smem + 2 * D::kKTileBytes + P * kPfVTileBytes;
+            // operand i: K operand (kk, tb) = (i / 2, i % 2) for i < kA, else V
+            // operand (kb, db) = ((i - kA) / 4, (i - kA) % 4)
+            auto fetch = [&](auto ic) -> bf16x8_t {
+                constexpr int i = decltype(ic)::value;
+                if constexpr (i < kA) {
+                    constexpr int kk = i / 2, tb = i % 2;
+                    const int off = tb * 32 * D::kRowBytes + koff[kk % D::kKoffRegs] + (kk / D::kKoffRegs) * 128;
+                    return *reinterpret_cast<const bf16x8_t*>(kl + off);
+                } else {
+                    constexpr int kb = (i - kA) / 4, db = (i - kA) % 4;
+                    const unsigned char* base = vl + 16 * kb * kPfVRowBytes + voff[db];
+                    const bf16x4_t lo = lds_read_tr16(reinterpret_cast<const __bf16*>(base));
+                    const bf16x4_t hi = lds_read_tr16(reinterpret_cast<const __bf16*>(base + 8 * kPfVRowBytes));
+                    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                }
+            };
+            bf16x8_t ring[4];
+            static_for<4>([&](auto ic) { ring[decltype(ic)::value] = fetch(ic); });
+            if constexpr (kA > 0) {
+#pragma unroll
+                for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) s[tb][i] = 0.f;
+            }
+            static_for<kOps>([&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                const bf16x8_t a = ring[i % 4];
+                if constexpr (i < kA) {
+                    s[i % 2] = mfma32(a, qop[i / 2], s[i % 2]);
+                } else {
+                    constexpr int kb = (i - kA) / 4, db = (i - kA) % 4;
+                    oacc[db] = mfma32(a, pop[kb], oacc[db]);
+                }
+                if constexpr (i + 4 < kOps) ring[i % 4] = fetch(std::integral_constant<int, i + 4>{});
+            });
             if constexpr (kA > 0) {
                 __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // DS read
 #pragma unroll
@@ -829,13 +877,12 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     }
 }
 
-// Block -> unit.  Units are ranked heaviest first (the causal KV range grows
+// Rank -> unit.  Units are ranked heaviest first (the causal KV range grows
 // with the query block), so the dispatcher hands long units out before short
-// ones.  The stream (head group, kv head, batch) is the fastest index: with a
+// ones (and the persistent split kernel can pair long ranks with short).  The stream (head group, kv head, batch) is the fastest index: with a
 // multiple of 8 streams each stream's blocks share one XCD and its L2 (blocks
 // go round-robin over the 8 XCDs).
-__device__ __forceinline__ void pf_block_unit(const PrefillParams& p, int* qb, int* hg, int* kvh, int* b) {
-    const int r = blockIdx.x;
+__device__ __forceinline__ void pf_rank_unit(const PrefillParams& p, int r, int* qb, int* hg, int* kvh, int* b) {
     const int stream = r % p.n_streams;
     const int rank_q = r / p.n_streams;
     *qb = p.causal ? p.n_qblocks - 1 - rank_q : rank_q;
@@ -848,16 +895,47 @@ template <bool kSwa, int kDk>
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     int qb, hg, kvh, b;
-    pf_block_unit(p, &qb, &hg, &kvh, &b);
+    pf_rank_unit(p, blockIdx.x, &qb, &hg, &kvh, &b);
     pf_unit<1, kSwa, kDk>(p, smem, qb, hg, kvh, b);
 }
 
+// The kernel's parameters read again from the kernarg segment through a
+// pointer the compiler cannot see through, so that a loop over units keeps
+// none of them in scalar registers across a unit (they would be spilled and
+// reloaded one lane read at a time).
+__device__ __forceinline__ PrefillParams pf_params_reread(const PrefillParams& p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    (void)p;
+    typedef const __attribute__((address_space(4))) PrefillParams* KernargParams;
+    KernargParams pp = (KernargParams)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(pp));
+    return *pp;
+#else
+    return p;   // the host pass never runs device code
+#endif
+}
+
+// Persistent: gridDim.x = min(units, CUs) workgroups, one per CU.  Workgroup
+// w runs ranks w, 2G-1-w, 2G+w, 4G-1-w, ... (G = gridDim.x): each lap over
+// the heaviest-first ranks goes the other way, so every CU's units add up to
+// about the same number of tiles (under a causal mask a rank-r unit plus a
+// rank 2G-1-r unit hold as many tiles as any other such pair), and a CU moves
+// to its next unit without a round trip through the dispatcher.
 template <int kDk>
-__global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_split_kernel(PrefillParams p) {
+__global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_split_kernel(PrefillParams p0) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    int qb, hg, kvh, b;
-    pf_block_unit(p, &qb, &hg, &kvh, &b);
-    pf_unit<2, false, kDk>(p, smem, qb, hg, kvh, b);
+    const int units = p0.n_qblocks * p0.n_streams;
+    const int g = gridDim.x;
+    const int w = blockIdx.x;
+#pragma nounroll
+    for (int lap = 0;; ++lap) {
+        const int r = (lap & 1) ? (lap + 1) * g - 1 - w : lap * g + w;
+        if (r >= units) break;   // later laps hold only higher ranks
+        const PrefillParams p = pf_params_reread(p0);
+        int qb, hg, kvh, b;
+        pf_rank_unit(p, r, &qb, &hg, &kvh, &b);
+        pf_unit<2, false, kDk>(p, smem, qb, hg, kvh, b);
+    }
 }
 
 namespace {
@@ -949,7 +1027,7 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
     if (cus <= 0) return FGQA_ERR_HIP;
     // Few units (fewer than 4 per CU): split each unit's KV range over two
     // wave groups so a CU never runs a long unit with one wave per SIMD, and
-    // let the dispatcher hand heaviest-first units to free CUs.
+    // give each CU a share of the units whose tile counts add up evenly.
     // (A sliding window gives every unit about the same number of tiles:
     // nothing to balance, so the whole-range kernel is used.)
     // The caller's `kernel` field can force either shape (validated above:
@@ -972,7 +1050,8 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
     // attribute slots 0..4: the prefill kernels
     if (const int e = set_kernel_smem_once(which, fns[which], smem_bytes); e != FGQA_OK) return e;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 grid((unsigned)units);
+    // the split kernel is persistent: at most one workgroup per CU
+    const dim3 grid((unsigned)(split && units > cus ? cus : units));
     switch (which) {
         case 0: hipLaunchKernelGGL((prefill_kernel<false, 128>), grid, dim3(kPfThreads), smem_bytes, s, p); break;
         case 1: hipLaunchKernelGGL((prefill_kernel<true, 128>), grid, dim3(kPfThreads), smem_bytes, s, p); break;
