@@ -22,6 +22,34 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 
+// Division by a runtime divisor d >= 1 of numerators 0 <= x < 2^31 with a
+// multiplier the host computes once (Granlund & Montgomery, "Division by
+// invariant integers using multiplication", PLDI 1994, Theorem 4.2 with
+// N = 31): l = ceil(log2 d), m = ceil(2^(31 + l) / d) < 2^32, and
+// x / d = (x * m) >> (31 + l), i.e. mulhi(x, m) >> (l - 1) for d >= 2.
+// Two scalar instructions instead of the ~25 of a general division, which
+// kernels pay per work unit when they map a rank to its unit.
+struct FastDiv {
+    int d;          // the divisor
+    uint32_t mul;   // m (unused when d == 1)
+    int shift;      // l - 1 (unused when d == 1)
+};
+
+inline FastDiv make_fast_div(int d) {
+    FastDiv f{d, 0u, 0};
+    if (d <= 1) return f;
+    int l = 0;
+    while ((1ll << l) < d) ++l;
+    f.mul = (uint32_t)(((1ull << (31 + l)) + (uint64_t)d - 1) / (uint64_t)d);
+    f.shift = l - 1;
+    return f;
+}
+
+__host__ __device__ __forceinline__ int fast_div(int x, FastDiv f) {
+    const uint32_t hi = (uint32_t)(((uint64_t)(uint32_t)x * f.mul) >> 32);   // a scalar mul_hi on the device
+    return f.d == 1 ? x : (int)(hi >> f.shift);
+}
+
 constexpr int kWave = 64;
 constexpr int kHeadDim = 128;
 constexpr float kLog2e = 1.4426950408889634f;

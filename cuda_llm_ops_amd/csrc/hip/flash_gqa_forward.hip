@@ -68,10 +68,12 @@ struct PrefillParams {
     int64_t v_sb, v_ss, v_sh;
     int64_t o_sb, o_ss, o_sh;
     int batch, sq, skv, hq, hkv, group, causal;
-    int hb;          // heads per unit
+    int hb;          // heads per unit (1, 2 or 4)
+    int hb_log2;     // log2(hb)
     int n_hgroups;   // group / hb
     int n_qblocks;   // ceil(sq / (128 / hb))
     int n_streams;   // n_hgroups * hkv * batch
+    FastDiv div_streams, div_hgroups, div_hkv;   // by n_streams, n_hgroups, hkv
     float scale_log2;   // |scale| * log2(e)
     uint32_t q_sign;    // 0x80008000 when scale < 0 (Q is negated on load), else 0
     int window;         // > 0: sliding window, row i sees keys [i - window + 1, i] (causal)
@@ -151,10 +153,10 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     const int l32 = lane & 31;
     const int l16 = lane & 15;
     const int g2 = lane >> 5;
-    const int qrows = 128 / p.hb;
+    const int qrows = 128 >> p.hb_log2;
     const int q_wg0 = qb * qrows;
-    const int h = kvh * p.group + hg * p.hb + (wave % p.hb);
-    const int q0w = q_wg0 + (wave / p.hb) * 32;
+    const int h = kvh * p.group + hg * p.hb + (wave & (p.hb - 1));
+    const int q0w = q_wg0 + (wave >> p.hb_log2) * 32;
     const int qrow = q0w + l32;
 
     int kv_end = p.skv;
@@ -883,12 +885,13 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
 // multiple of 8 streams each stream's blocks share one XCD and its L2 (blocks
 // go round-robin over the 8 XCDs).
 __device__ __forceinline__ void pf_rank_unit(const PrefillParams& p, int r, int* qb, int* hg, int* kvh, int* b) {
-    const int stream = r % p.n_streams;
-    const int rank_q = r / p.n_streams;
+    const int rank_q = fast_div(r, p.div_streams);
+    const int stream = r - rank_q * p.n_streams;
     *qb = p.causal ? p.n_qblocks - 1 - rank_q : rank_q;
-    *hg = stream % p.n_hgroups;
-    *kvh = (stream / p.n_hgroups) % p.hkv;
-    *b = stream / (p.n_hgroups * p.hkv);
+    const int t = fast_div(stream, p.div_hgroups);   // kv head + hkv * batch
+    *hg = stream - t * p.n_hgroups;
+    *b = fast_div(t, p.div_hkv);
+    *kvh = t - *b * p.hkv;
 }
 
 template <bool kSwa, int kDk>
@@ -1013,9 +1016,13 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
     p.group = a->num_q_heads / a->num_kv_heads;
     p.causal = a->causal ? 1 : 0;
     p.hb = (p.group % 4 == 0) ? 4 : (p.group % 2 == 0) ? 2 : 1;
+    p.hb_log2 = p.hb == 4 ? 2 : p.hb == 2 ? 1 : 0;
     p.n_hgroups = p.group / p.hb;
     p.n_qblocks = (int)ceil_div(p.sq, 128 / p.hb);
     p.n_streams = p.n_hgroups * p.hkv * p.batch;
+    p.div_streams = make_fast_div(p.n_streams);
+    p.div_hgroups = make_fast_div(p.n_hgroups);
+    p.div_hkv = make_fast_div(p.hkv);
     p.scale_log2 = fabsf(a->scale) * kLog2e;
     p.q_sign = (a->scale < 0.f) ? 0x80008000u : 0u;
     p.window = a->window_size;
