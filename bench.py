@@ -254,6 +254,8 @@ def bench_prefill(cfg_id, steps, warmup, dev, keep=None):
     lse = torch.empty((B, Hq, S), dtype=torch.float32, device=dev)
 
     step = fg.prepare_prefill(q, k, v, SCALE, out=out, lse=lse, causal=True)
+    kernel = {"whole": "prefill_kernel", "split": "prefill_split_kernel",
+              "wide": "prefill_wide_kernel"}[fg.prefill_kernel_choice(q, k, v, causal=True)]
 
     total_ms, per = _time_calls(step, steps, warmup, min_warm_ms=AUX_WARM_MS)
     # the reference's causal-halved count (test_flash_gqa_kernel.py:282-301)
@@ -268,7 +270,7 @@ def bench_prefill(cfg_id, steps, warmup, dev, keep=None):
                 roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
                           "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
                           "traffic": TRAFFIC_BYTES.get(f"prefill_cfg{cfg_id}"),
-                          "kernel": "prefill_split_kernel" if B * Hq * S // 128 < 4 * 256 else "prefill_kernel",
+                          "kernel": kernel,
                           "algorithmic_flops": flops})
 
 

@@ -26,6 +26,7 @@ from .flash_gqa import (  # noqa: F401
     prepare_backward,
     prepare_decode,
     prepare_decode_paged,
+    prefill_kernel_choice,
     prepare_prefill,
     PreparedLaunch,
 )

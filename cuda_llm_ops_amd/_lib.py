@@ -22,6 +22,7 @@ FGQA_ERR_HIP = -4
 FGQA_KERNEL_AUTO = 0
 FGQA_KERNEL_WHOLE = 1
 FGQA_KERNEL_SPLIT = 2
+FGQA_KERNEL_WIDE = 3
 
 _I64x2 = ctypes.c_int64 * 2
 _I64x3 = ctypes.c_int64 * 3
@@ -204,6 +205,8 @@ def lib() -> ctypes.CDLL:
         L.fgqa_decode_bf16_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.c_void_p]
         L.fgqa_prefill_bf16.restype = ctypes.c_int
         L.fgqa_prefill_bf16.argtypes = [ctypes.POINTER(PrefillArgs), ctypes.c_void_p]
+        L.fgqa_prefill_kernel_choice.restype = ctypes.c_int
+        L.fgqa_prefill_kernel_choice.argtypes = [ctypes.POINTER(PrefillArgs), ctypes.POINTER(ctypes.c_int32)]
         L.fgqa_decode_paged_workspace_bytes.restype = ctypes.c_int
         L.fgqa_decode_paged_workspace_bytes.argtypes = [ctypes.POINTER(PagedDecodeArgs),
                                                         ctypes.POINTER(ctypes.c_size_t)]

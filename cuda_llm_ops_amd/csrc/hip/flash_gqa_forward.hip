@@ -24,6 +24,15 @@
 //                         for both groups) and its O tile through 32 KB of LDS,
 //                         so those global loads and stores move whole rows;
 //                         the two groups then merge and store half of O each.
+//   prefill_wide_kernel   8 waves on a 256-row unit: the two groups take 128
+//                         rows each and share every K/V tile (half the tile
+//                         loads per row).  Units pair heaviest with lightest;
+//                         a pair runs on two workgroups of one XCD, the first
+//                         taking the heavy unit's first tiles, the second the
+//                         rest of it and then the light unit; the heavy unit's
+//                         two partial results merge through device memory.
+//                         Used when the pairs fill the CUs (BASELINE-size
+//                         causal grids such as S=4096, Hq=16, Hkv=1).
 //
 // Per wave (32 rows) and 64-token K/V tile j, software pipelined one tile ahead:
 //   phase A: S^T(j+1) = K(j+1) . Q^T          v_mfma_f32_32x32x16_bf16, K from LDS,
@@ -49,6 +58,7 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "fgqa_device.h"
@@ -68,7 +78,7 @@ struct PrefillParams {
     int64_t v_sb, v_ss, v_sh;
     int64_t o_sb, o_ss, o_sh;
     int batch, sq, skv, hq, hkv, group, causal;
-    int hb;          // heads per unit (1, 2 or 4)
+    int hb;          // heads per unit (1, 2 or 4; the wide kernel 1, 2, 4 or 8)
     int hb_log2;     // log2(hb)
     int n_hgroups;   // group / hb
     int n_qblocks;   // ceil(sq / (128 / hb))
@@ -78,6 +88,23 @@ struct PrefillParams {
     uint32_t q_sign;    // 0x80008000 when scale < 0 (Q is negated on load), else 0
     int window;         // > 0: sliding window, row i sees keys [i - window + 1, i] (causal)
     const float* sink;  // nullable [Hq]: added to the softmax denominator as sink * exp(-max)
+    // wide kernel: tiles a pair's heavy unit keeps beyond half the pair's
+    // tiles on its first workgroup, and the partial-result slots and arrival
+    // counters of split units (device scratch)
+    int wide_bias;
+    float* wide_part;
+    unsigned* wide_ctr;
+};
+
+// A segment of a wide unit: tiles [lo, hi) of its KV range.  part_own != null:
+// the unit's other tiles run on another workgroup; whichever of the two
+// finishes second merges both partial results (slot 0: the segment holding
+// the unit's first tiles, slot 1: the other).
+struct PfSeg {
+    int lo, hi;
+    int slot;          // this segment's slot (0 or 1)
+    float* part;       // the unit's two slots, kPfPartFloats each
+    unsigned* ctr;     // the unit's arrival counter (0 between launches)
 };
 
 // f(integral_constant<int, 0>), ..., f(integral_constant<int, N-1>): an
@@ -102,6 +129,17 @@ constexpr int kPfMergeFloats = 66;
 // 32 rows x 256 bytes, after the two groups' tile buffers (2 x 64 KB + 32 KB =
 // the CU's 160 KB).
 constexpr int kPfQStageBytes = kPfWaves * 32 * kHeadDim * 2;
+// Wide kernel (head dim 128): both wave groups work on one set of tile
+// buffers (K0, K1, V0, V1: 64 KB), followed by the 256-row unit's Q tile
+// (64 KB, later its O tile) and one word that broadcasts the arrival count.
+// A split unit's partial result: 66 floats per lane (64 of O, max, sum) of
+// each of the 8 waves.
+constexpr int kPwTileBytes = 4 * kPfVTileBytes;
+constexpr int kPwQBytes = 2 * kPfQStageBytes;
+constexpr int kPwSmemBytes = kPwTileBytes + kPwQBytes + 16;
+constexpr int kPfPartFloats = 2 * kPfWaves * kPfMergeFloats * kWave;
+// most split units one launch may hold (two partial slots and a counter each)
+constexpr int kPwMaxSplit = 128;
 
 // Sizes that depend on the Q/K head dim kDk (128, or 192 for MLA).
 template <int kDk>
@@ -136,10 +174,14 @@ struct PfDims {
 // unit's KV range; tiles past the range are fully masked and add nothing.
 // kSwa: sliding window and/or sink (a separate instantiation, so the plain
 // causal kernels carry none of its work).
-template <int kGroups, bool kSwa, int kDk>
+// kWide (with kGroups == 2, head dim 128): a 256-row unit whose two groups
+// take 128 rows each and share every K/V tile; the call runs segment `seg` of
+// the unit's KV range.
+template <int kGroups, bool kSwa, int kDk, bool kWide = false>
 __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* smem_all, int qb, int hg, int kvh,
-                                        int b) {
+                                        int b, PfSeg seg = PfSeg{0, 0, 0, nullptr, nullptr}) {
     using D = PfDims<kDk>;
+    static_assert(!kWide || (kGroups == 2 && kDk == kHeadDim && !kSwa), "wide units: two groups, head dim 128");
     // opaque in the split kernel: its loop over units recomputes what depends
     // on the thread index inside each unit instead of holding it in
     // registers across the loop
@@ -149,14 +191,16 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     const int wave_wg = __builtin_amdgcn_readfirstlane(tid / kWave);   // wave-uniform
     const int grp = wave_wg / kPfWaves;
     const int wave = wave_wg % kPfWaves;
-    unsigned char* smem = smem_all + grp * D::kGroupBytes;
+    unsigned char* smem = kWide ? smem_all : smem_all + grp * D::kGroupBytes;
     const int l32 = lane & 31;
     const int l16 = lane & 15;
     const int g2 = lane >> 5;
-    const int qrows = 128 >> p.hb_log2;
+    // the wave's 32 rows: slot `wslot` of the unit (a wide unit has 8 slots)
+    const int wslot = kWide ? wave_wg : wave;
+    const int qrows = (kWide ? 256 : 128) >> p.hb_log2;
     const int q_wg0 = qb * qrows;
-    const int h = kvh * p.group + hg * p.hb + (wave & (p.hb - 1));
-    const int q0w = q_wg0 + (wave >> p.hb_log2) * 32;
+    const int h = kvh * p.group + hg * p.hb + (wslot & (p.hb - 1));
+    const int q0w = q_wg0 + (wslot >> p.hb_log2) * 32;
     const int qrow = q0w + l32;
 
     int kv_end = p.skv;
@@ -164,8 +208,10 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     // a sliding window starts the unit at the tile holding its first row's first key
     const int t_lo = (kSwa && p.window > 0) ? max(0, q_wg0 - p.window + 1) / kPfTile : 0;
     const int unit_tiles = max(0, (kv_end + kPfTile - 1) / kPfTile - t_lo);
-    const int n_tiles = kGroups == 1 ? unit_tiles : (unit_tiles + 1) / 2;   // loop trips, same for both groups
-    const int t_first = t_lo + grp * n_tiles;                                 // first tile of this group
+    // loop trips, same for both groups, and this group's first tile
+    const int n_tiles = kWide ? seg.hi - seg.lo : kGroups == 1 ? unit_tiles : (unit_tiles + 1) / 2;
+    const int t_first = kWide ? seg.lo : t_lo + grp * n_tiles;
+    (void)unit_tiles;
     // keys this group may use: the unit's range, cut at the group's last tile
     const int kv_hi = min(kv_end, (t_first + n_tiles) * kPfTile);
 
@@ -440,8 +486,32 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     // slot w in group g issues instructions 4g .. 4g+3 of its slot's 8, so
     // each row is fetched once for both groups.
     [[maybe_unused]] const uint32_t q_lds =
-        lds_base + (2 - grp) * D::kGroupBytes + wave * (kPfQStageBytes / kPfWaves);
-    if constexpr (kStageQ) {
+        kWide ? lds_base + kPwTileBytes + wave_wg * (kPfQStageBytes / kPfWaves)
+              : lds_base + (2 - grp) * D::kGroupBytes + wave * (kPfQStageBytes / kPfWaves);
+    if constexpr (kWide) {
+        // a wide unit's waves have rows of their own: each loads its 8 KB
+        auto dmaq = [](auto ic, uint32_t base, uint32_t voffset, __amdgpu_buffer_rsrc_t rsrc) {
+            constexpr int kOff = decltype(ic)::value * 1024;
+            asm volatile("s_add_u32 m0, %0, %3\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                         :: "s"(base), "v"(voffset), "s"(rsrc), "i"(kOff) : "memory", "scc");
+        };
+        static_for<8>([&](auto ic) {
+            const int slot = 64 * decltype(ic)::value + lane;
+            const int r = slot >> 4;
+            const uint32_t voff = (uint32_t)(q0w + r) * qss + ((uint32_t)((slot & 15) ^ (r & 15)) << 4);
+            dmaq(ic, q_lds, voff, qrs);
+        });
+        // group 0 loads K(0); group 1 loads V(0) and K(1), awaited by the end
+        // of its S(0) phase (group 0's first MFMA phase comes after that)
+        if (grp == 0) {
+            if (n_tiles > 0) issue_tile(0, 0, -1);
+            wait_vmem();
+        } else {
+            if (n_tiles > 0) issue_tile(0, -1, 0);
+            if (n_tiles > 1) issue_tile(1, 1, -1);
+            wait_vmem_but((n_tiles > 0 ? 4 : 0) + (n_tiles > 1 ? 4 : 0));
+        }
+    } else if constexpr (kStageQ) {
         auto dmaq = [](auto ic, uint32_t base, uint32_t voffset, __amdgpu_buffer_rsrc_t rsrc) {
             constexpr int kOff = decltype(ic)::value * 1024;
             asm volatile("s_add_u32 m0, %0, %3\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
@@ -454,7 +524,8 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
             dmaq(ic, q_lds + grp * 4096, voff, qrs);
         });
     }
-    if constexpr (kStageQ) {
+    if constexpr (kWide) {
+    } else if constexpr (kStageQ) {
         // the first barrier needs Q and K(0) only: V(0) and K(1) are waited
         // for by the first softmax phase
         static_assert(D::kDmaK == 4, "wait_vmem_but counts 4 loads per tile");
@@ -469,8 +540,10 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     }
     __syncthreads();
     if constexpr (kStageQ) {
-        const unsigned char* ql = reinterpret_cast<const unsigned char*>(smem_all) + 2 * D::kGroupBytes +
-                                  wave * (kPfQStageBytes / kPfWaves) + l32 * D::kRowBytes;
+        const unsigned char* ql = reinterpret_cast<const unsigned char*>(smem_all) +
+                                  (kWide ? kPwTileBytes + wave_wg * (kPfQStageBytes / kPfWaves)
+                                         : 2 * D::kGroupBytes + wave * (kPfQStageBytes / kPfWaves)) +
+                                  l32 * D::kRowBytes;
 #pragma unroll
         for (int kk = 0; kk < D::kSteps; ++kk) {
             u32x4_t t = *reinterpret_cast<const u32x4_t*>(ql + (((2 * kk + g2) ^ (l32 & 15)) << 4));
@@ -533,6 +606,7 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         __syncthreads();
         if (grp == 1) {
             if (n_tiles > 0) qk(s, 0);
+            if constexpr (kWide) wait_vmem();   // V(0), K(1)
             __syncthreads();              // both groups' S(0) phases are past: K(0) is free
         }
         // S(j+1) -> P(j+1); then K(j+3) and V(j+2) go into the buffers that
@@ -564,7 +638,15 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
             // stalls the issuing wave for a few hundred cycles, which the
             // softmax then no longer waits behind.
             [[maybe_unused]] int n_new = 0;
-            if constexpr (kStageQ) {
+            if constexpr (kWide) {
+                // wide units share the tiles: group 1 alone loads them, into
+                // the buffers both groups' MFMA phases j have finished with,
+                // and awaits them at the end of its next MFMA phase
+                if (grp == 1) {
+                    if (j + 3 < n_tiles) issue_tile(j + 3, CK{}, CN{});
+                    if (j + 2 < n_tiles) issue_tile(j + 2, CN{}, CV{});
+                }
+            } else if constexpr (kStageQ) {
                 if (j + 3 < n_tiles) {
                     issue_tile(j + 3, CK{}, CN{});
                     n_new += D::kDmaK;
@@ -584,7 +666,8 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) asm volatile("" : "+v"(pop[kb]));
             asm volatile("" : "+v"(l_run));
-            if constexpr (kStageQ) {
+            if constexpr (kWide) {
+            } else if constexpr (kStageQ) {
                 wait_vmem_but(n_new);         // K(j+2), V(j+1), issued one softmax phase ago
             } else {
                 wait_vmem();                  // K(j+2), V(j+1), issued one softmax phase ago
@@ -669,6 +752,9 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
             // all of the phase's MFMAs before its barrier (the scheduler would
             // otherwise sink the last ones into the softmax phase)
             __builtin_amdgcn_sched_barrier(0);
+            if constexpr (kWide) {
+                if (grp == 1) wait_vmem();   // the tiles its last softmax phase loaded
+            }
             __syncthreads();
         };
         // the loop runs two tiles per trip, so that every buffer index is a constant
@@ -706,7 +792,74 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         }
     }
 
-    if constexpr (kGroups == 2 && kStageQ) {
+    if constexpr (kWide) {
+        if (seg.part != nullptr) {
+            // Split unit: the first of its two segments to finish publishes
+            // its partial (O, max, sum of every lane) in its slot and counts
+            // its arrival; the second merges that with its own and writes the
+            // output.  A segment that finds no arrival publishes, and merges
+            // anyway if the other one arrived in the meantime.  The merger
+            // sets the counter back to 0 for the next launch.
+            // Ordering: every wave's stores complete (workgroup release) before
+            // the barrier; thread 0's device-scope release on the counter then
+            // makes them visible device-wide (one L2 write-back for the
+            // workgroup), and the reader's thread 0 acquires before the
+            // barrier that lets its waves read (one L2 invalidate).
+            unsigned* word = reinterpret_cast<unsigned*>(smem_all + kPwTileBytes + kPwQBytes);
+            const int woff = wave_wg * kPfMergeFloats * kWave;
+            float* own = seg.part + seg.slot * kPfPartFloats + woff;
+            const float* other = seg.part + (1 - seg.slot) * kPfPartFloats + woff;
+            if (tid == 0) *word = __hip_atomic_load(seg.ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            bool merge = *word != 0u;
+            if (!merge) {
+                f32x4_t* o4 = reinterpret_cast<f32x4_t*>(own) + lane;
+#pragma unroll
+                for (int db = 0; db < 4; ++db)
+#pragma unroll
+                    for (int i4 = 0; i4 < 4; ++i4)
+                        o4[(db * 4 + i4) * kWave] = f32x4_t{oacc[db][4 * i4], oacc[db][4 * i4 + 1],
+                                                            oacc[db][4 * i4 + 2], oacc[db][4 * i4 + 3]};
+                own[64 * kWave + lane] = m_run;
+                own[65 * kWave + lane] = l_run;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                __syncthreads();
+                if (tid == 0) *word = __hip_atomic_fetch_add(seg.ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+                __syncthreads();
+                merge = *word != 0u;
+                if (!merge) return;   // the other segment merges
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");   // after thread 0's device-scope acquire
+            if (tid == 0) __hip_atomic_store(seg.ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // slot 0's terms first whichever merges, so the output does not
+            // depend on the order of arrival
+            const bool first = seg.slot == 0;
+            const float m_o = other[64 * kWave + lane];
+            const float l_o = other[65 * kWave + lane];
+            const float mA = first ? m_run : m_o, lA = first ? l_run : l_o;
+            const float mB = first ? m_o : m_run, lB = first ? l_o : l_run;
+            const float m = fmaxf(mA, mB);
+            const float mu = (m == -INFINITY) ? 0.f : m;
+            const float aA = fast_exp2(mA - mu);   // 0 when a segment saw no key
+            const float aB = fast_exp2(mB - mu);
+            const f32x4_t* r4 = reinterpret_cast<const f32x4_t*>(other) + lane;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    const f32x4_t ot = r4[(db * 4 + i4) * kWave];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float mine = oacc[db][4 * i4 + e];
+                        const float oa = first ? mine : ot[e], ob = first ? ot[e] : mine;
+                        oacc[db][4 * i4 + e] = __builtin_fmaf(oa, aA, ob * aB);
+                    }
+                }
+            l_run = __builtin_fmaf(lA, aA, lB * aB);
+            m_run = m;
+            m_use = mu;
+        }
+    } else if constexpr (kGroups == 2 && kStageQ) {
         // Head dim 128: each group keeps O columns 64*grp .. +63 (blocks
         // 2*grp, 2*grp + 1) and hands the other half, with its max and sum, to
         // the same wave slot of the other group through its own tile
@@ -806,7 +959,7 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     const float sink = has_sink ? p.sink[h] : 0.f;
     const float denom = (l_run > 0.f && has_sink) ? l_run + sink * fast_exp2(-m_use) : l_run;
     const float inv = (l_run > 0.f) ? 1.f / denom : 0.f;
-    if constexpr (kGroups == 2 && kStageQ) {
+    if constexpr (kGroups == 2 && kStageQ && !kWide) {
         // this group's 64 columns of the wave's 32 rows go out through 4 KB of
         // the (idle) Q area: 8-byte pieces into 128-byte half rows, chunk c of
         // row r in slot c ^ (r % 8), then 8 half rows per store instruction
@@ -848,8 +1001,9 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         // give each store 32 rows 16 bytes each).
         static_assert(kGroups == 1 || kStageQ || kPfWaves * kPfMergeFloats * kWave * 4 <= D::kGroupBytes,
                       "O staging in group 1's buffers must not overlap the merge area");
-        unsigned char* ol = smem_all + (kGroups == 1 ? 0 : kStageQ ? 2 : 1) * D::kGroupBytes +
-                            wave * (kPfQStageBytes / kPfWaves);
+        unsigned char* ol = kWide ? smem_all + kPwTileBytes + wave_wg * (kPfQStageBytes / kPfWaves)
+                                  : smem_all + (kGroups == 1 ? 0 : kStageQ ? 2 : 1) * D::kGroupBytes +
+                                        wave * (kPfQStageBytes / kPfWaves);
 #pragma unroll
         for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -941,7 +1095,134 @@ __global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_split_kernel(Prefil
     }
 }
 
+// Wide kernel (head dim 128, no window or sink): 256-row units whose two wave
+// groups take 128 rows each and share every K/V tile, so a CU loads half the
+// tile bytes per row of the split kernel.  There are half as many units as
+// the split kernel's, too few to balance whole units over the CUs: units pair
+// heaviest with lightest (rank r with rank units - 1 - r), and a pair runs on
+// two workgroups of one XCD (blocks w and w + 8; blocks go round-robin over
+// the 8 XCDs).  The first runs the heavy unit's first tiles; the second the
+// rest of the heavy unit and then the light unit.  The first keeps wide_bias
+// tiles beyond half the pair's tiles, which pays for the second's extra unit
+// start.  The heavy unit's two partial results merge through device memory
+// (pf_unit: whichever segment finishes second merges).
+__device__ __forceinline__ int pf_unit_tiles(const PrefillParams& p, int qb, int qrows) {
+    int kv_end = p.skv;
+    if (p.causal) kv_end = min(kv_end, min((qb + 1) * qrows, p.sq));
+    return (kv_end + kPfTile - 1) / kPfTile;
+}
+
+__global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_wide_kernel(PrefillParams p0) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    const int w = blockIdx.x;
+    const int role = (w >> 3) & 1;
+    const int pair = ((w >> 4) << 3) | (w & 7);
+    const int units = p0.n_qblocks * p0.n_streams;
+    if (pair >= (units + 1) / 2) return;
+#pragma nounroll
+    for (int sgi = 0; sgi < 2; ++sgi) {
+        const PrefillParams p = pf_params_reread(p0);
+        const int qrows = 256 >> p.hb_log2;
+        const int rh = pair, rl = units - 1 - pair;   // rl == rh: the middle unit of an odd count
+        int qb, hg, kvh, b;
+        pf_rank_unit(p, rh, &qb, &hg, &kvh, &b);
+        const int nh = pf_unit_tiles(p, qb, qrows);
+        int nl = 0;
+        if (rl != rh) {
+            int qb2, hg2, kvh2, b2;
+            pf_rank_unit(p, rl, &qb2, &hg2, &kvh2, &b2);
+            nl = pf_unit_tiles(p, qb2, qrows);
+        }
+        // the first workgroup's share of the heavy unit
+        const int a = min(nh, (nh + nl + p.wide_bias + 1) >> 1);
+        const bool split = a < nh;
+        PfSeg seg{0, a, role, nullptr, p.wide_ctr + pair};
+        if (role == 0) {
+            if (sgi > 0) break;
+            if (split) seg.part = p.wide_part + (size_t)pair * 2 * kPfPartFloats;
+        } else if (sgi == 0) {
+            if (!split) continue;
+            seg.lo = a;
+            seg.hi = nh;
+            seg.part = p.wide_part + (size_t)pair * 2 * kPfPartFloats;
+        } else {
+            if (rl == rh) break;
+            pf_rank_unit(p, rl, &qb, &hg, &kvh, &b);
+            seg.lo = 0;
+            seg.hi = nl;
+        }
+        pf_unit<2, false, kHeadDim, true>(p, smem, qb, hg, kvh, b, seg);
+    }
+}
+
+// Partial-result slots and arrival counters of the wide kernel's split units
+// (kPwMaxSplit units; held by every device the library runs on until the
+// process ends; the counters start at 0 and each launch leaves them at 0).
+// In host code the names are host-side stand-ins, not device addresses: the
+// addresses are looked up once per device (hipGetSymbolAddress, with that
+// device current) and only those pointers are passed to kernels.  Launches
+// that overlap on one device share them and would race.
+static __device__ __align__(256) float pw_part[(size_t)kPwMaxSplit * 2 * kPfPartFloats];
+static __device__ __align__(256) unsigned pw_ctr[kPwMaxSplit];
+
 namespace {
+
+constexpr int kPwDevices = 64;
+std::mutex g_pw_mutex;
+float* g_pw_part[kPwDevices] = {nullptr};
+unsigned* g_pw_ctr[kPwDevices] = {nullptr};
+
+// The current device's copies of pw_part and pw_ctr.
+int pw_scratch(float** part, unsigned** ctr) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kPwDevices) return FGQA_ERR_HIP;
+    std::lock_guard<std::mutex> lock(g_pw_mutex);
+    if (g_pw_part[dev] == nullptr) {
+        void* pp = nullptr;
+        void* cp = nullptr;
+        if (hipGetSymbolAddress(&pp, HIP_SYMBOL(pw_part)) != hipSuccess || pp == nullptr ||
+            hipGetSymbolAddress(&cp, HIP_SYMBOL(pw_ctr)) != hipSuccess || cp == nullptr)
+            return FGQA_ERR_HIP;
+        g_pw_part[dev] = static_cast<float*>(pp);
+        g_pw_ctr[dev] = static_cast<unsigned*>(cp);
+    }
+    *part = g_pw_part[dev];
+    *ctr = g_pw_ctr[dev];
+    return FGQA_OK;
+}
+
+// Unit pairs of the wide kernel: 256-row units of up to 8 heads of a KV group.
+int64_t wide_pairs(const fgqa_prefill_args* a) {
+    const int group = a->num_q_heads / a->num_kv_heads;
+    const int hbw = group % 8 == 0 ? 8 : group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
+    const int64_t units = ceil_div(a->seqlen_q, 256 / hbw) * (int64_t)(group / hbw) * a->num_kv_heads * a->batch;
+    return (units + 1) / 2;
+}
+
+// The kernel shape a validated call runs on a device with `cus` CUs: the
+// caller's `kernel`, or for AUTO the choice by grid size:
+//  - wide: causal, head dim 128, no window or sink, and the wide kernel's
+//    unit pairs fill the CUs (two workgroups per pair, within 1/8 of one per CU);
+//  - split: fewer than 4 of the 128-row units per CU, no window or sink: each
+//    unit's KV range runs on two wave groups, so a CU never runs a long unit
+//    with one wave per SIMD, and each CU gets a share of the units whose tile
+//    counts add up evenly;
+//  - whole: the rest (a sliding window gives every unit about the same number
+//    of tiles: nothing to balance).
+int prefill_choice(const fgqa_prefill_args* a, int cus) {
+    if (a->kernel != FGQA_KERNEL_AUTO) return a->kernel;
+    const int group = a->num_q_heads / a->num_kv_heads;
+    const int hb = group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
+    const bool swa = a->window_size > 0 || a->sink != nullptr;
+    const bool mla = a->head_dim == 192;
+    const int64_t units = ceil_div(a->seqlen_q, 128 / hb) * (int64_t)(group / hb) * a->num_kv_heads * a->batch;
+    const int64_t pairs = wide_pairs(a);
+    const int64_t wide_grid = 16 * ceil_div(pairs, 8);
+    if (!mla && !swa && a->causal && pairs <= kPwMaxSplit && wide_grid <= cus && 8 * wide_grid >= 7 * (int64_t)cus)
+        return FGQA_KERNEL_WIDE;
+    if (units < 4 * (int64_t)cus && !swa) return FGQA_KERNEL_SPLIT;
+    return FGQA_KERNEL_WHOLE;
+}
 
 int validate_prefill(const fgqa_prefill_args* a) {
     if (a == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
@@ -960,9 +1241,11 @@ int validate_prefill(const fgqa_prefill_args* a) {
     // (128, 128) and the MLA shape (192, 128); MLA has no window / sink form
     if (dv != kHeadDim || (a->head_dim != kHeadDim && a->head_dim != 192)) return FGQA_ERR_UNSUPPORTED;
     if (a->head_dim == 192 && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
-    if (a->kernel < FGQA_KERNEL_AUTO || a->kernel > FGQA_KERNEL_SPLIT) return FGQA_ERR_INVALID_ARGUMENT;
-    // the window / sink variant has no split form
-    if (a->kernel == FGQA_KERNEL_SPLIT && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
+    if (a->kernel < FGQA_KERNEL_AUTO || a->kernel > FGQA_KERNEL_WIDE) return FGQA_ERR_INVALID_ARGUMENT;
+    // the window / sink variant has no split or wide form; the wide kernel has head dim 128 only
+    if ((a->kernel == FGQA_KERNEL_SPLIT || a->kernel == FGQA_KERNEL_WIDE) && (a->window_size > 0 || a->sink != nullptr))
+        return FGQA_ERR_UNSUPPORTED;
+    if (a->kernel == FGQA_KERNEL_WIDE && a->head_dim != kHeadDim) return FGQA_ERR_UNSUPPORTED;
     const int64_t lim = (int64_t)1 << 31;
     if ((int64_t)(a->seqlen_q + 128) * a->q_stride[1] * 2 >= lim ||
         (int64_t)(a->seqlen_kv + 128) * a->k_stride[1] * 2 >= lim ||
@@ -984,6 +1267,17 @@ int validate_prefill(const fgqa_prefill_args* a) {
 }  // namespace fgqa
 
 using namespace fgqa;
+
+extern "C" int fgqa_prefill_kernel_choice(const fgqa_prefill_args* a, int32_t* kernel) {
+    int st = validate_prefill(a);
+    if (st != FGQA_OK) return st;
+    if (kernel == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
+    if (a->kernel == FGQA_KERNEL_WIDE && wide_pairs(a) > kPwMaxSplit) return FGQA_ERR_UNSUPPORTED;
+    const int cus = device_cu_count();
+    if (cus <= 0) return FGQA_ERR_HIP;
+    *kernel = prefill_choice(a, cus);
+    return FGQA_OK;
+}
 
 extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
     int st = validate_prefill(a);
@@ -1027,23 +1321,43 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
     p.q_sign = (a->scale < 0.f) ? 0x80008000u : 0u;
     p.window = a->window_size;
     p.sink = a->sink;
+    p.wide_bias = 0;
+    p.wide_part = nullptr;
+    p.wide_ctr = nullptr;
 
     const int64_t units = (int64_t)p.n_qblocks * p.n_streams;
     if (units >= ((int64_t)1 << 31)) return FGQA_ERR_UNSUPPORTED;
+    if (a->kernel == FGQA_KERNEL_WIDE && wide_pairs(a) > kPwMaxSplit) return FGQA_ERR_UNSUPPORTED;
     const int cus = device_cu_count();
     if (cus <= 0) return FGQA_ERR_HIP;
-    // Few units (fewer than 4 per CU): split each unit's KV range over two
-    // wave groups so a CU never runs a long unit with one wave per SIMD, and
-    // give each CU a share of the units whose tile counts add up evenly.
-    // (A sliding window gives every unit about the same number of tiles:
-    // nothing to balance, so the whole-range kernel is used.)
-    // The caller's `kernel` field can force either shape (validated above:
-    // the window / sink variant has no split form).
+    const int choice = prefill_choice(a, cus);
     const bool swa = p.window > 0 || p.sink != nullptr;
-    const bool split = a->kernel == FGQA_KERNEL_AUTO ? (units < 4 * (int64_t)cus && !swa)
-                                                     : a->kernel == FGQA_KERNEL_SPLIT;
-
     const bool mla = a->head_dim == 192;
+    const bool split = choice == FGQA_KERNEL_SPLIT;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (choice == FGQA_KERNEL_WIDE) {
+        // 256-row units: up to 8 heads of a KV group
+        const int hbw = (p.group % 8 == 0) ? 8 : p.hb;
+        p.hb = hbw;
+        p.hb_log2 = hbw == 8 ? 3 : hbw == 4 ? 2 : hbw == 2 ? 1 : 0;
+        p.n_hgroups = p.group / hbw;
+        p.n_qblocks = (int)ceil_div(p.sq, 256 / hbw);
+        p.n_streams = p.n_hgroups * p.hkv * p.batch;
+        p.div_streams = make_fast_div(p.n_streams);
+        p.div_hgroups = make_fast_div(p.n_hgroups);
+        p.wide_bias = 3;
+        if (const int e = pw_scratch(&p.wide_part, &p.wide_ctr); e != FGQA_OK) return e;
+        // attribute slot 5: the wide kernel
+        if (const int e = set_kernel_smem_once(5, reinterpret_cast<const void*>(prefill_wide_kernel), kPwSmemBytes);
+            e != FGQA_OK)
+            return e;
+        // blocks w and w + 8 of each 16 run one pair
+        const dim3 grid((unsigned)(16 * ceil_div(wide_pairs(a), 8)));
+        hipLaunchKernelGGL(prefill_wide_kernel, grid, dim3(2 * kPfThreads), kPwSmemBytes, s, p);
+        if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
+        return FGQA_OK;
+    }
+
     const int group_bytes = mla ? PfDims<192>::kGroupBytes : PfDims<128>::kGroupBytes;
     // the split kernel with head dim 128 also stages the Q tile in LDS
     const int smem_bytes = (split ? 2 : 1) * group_bytes + (split && !mla ? kPfQStageBytes : 0);
@@ -1056,7 +1370,6 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
                           reinterpret_cast<const void*>(prefill_split_kernel<192>)};
     // attribute slots 0..4: the prefill kernels
     if (const int e = set_kernel_smem_once(which, fns[which], smem_bytes); e != FGQA_OK) return e;
-    const hipStream_t s = static_cast<hipStream_t>(stream);
     // the split kernel is persistent: at most one workgroup per CU
     const dim3 grid((unsigned)(split && units > cus ? cus : units));
     switch (which) {

@@ -339,7 +339,8 @@ def launch_decode_flash_gqa_bf16_kernel(q, k, v, out=None):
 # --------------------------------------------------------------------------- prefill
 def _kernel_choice(kernel) -> int:
     """'auto' / 'whole' / 'split' (or the FGQA_KERNEL_* value) -> the C ABI value."""
-    names = {"auto": _lib.FGQA_KERNEL_AUTO, "whole": _lib.FGQA_KERNEL_WHOLE, "split": _lib.FGQA_KERNEL_SPLIT}
+    names = {"auto": _lib.FGQA_KERNEL_AUTO, "whole": _lib.FGQA_KERNEL_WHOLE, "split": _lib.FGQA_KERNEL_SPLIT,
+             "wide": _lib.FGQA_KERNEL_WIDE}
     if isinstance(kernel, str):
         if kernel not in names:
             raise ValueError(f"kernel must be one of {sorted(names)}")
@@ -457,6 +458,18 @@ def prepare_prefill(q, k, v, scale=None, out=None, lse=None, causal=True, window
     pl = PreparedLaunch(_lib.lib().fgqa_prefill_bf16, a, keep, out, "fgqa_prefill_bf16")
     pl.lse = lse
     return pl
+
+
+def prefill_kernel_choice(q, k, v, causal=True, window_size=0, sink=None, kernel="auto") -> str:
+    """The kernel shape ('whole', 'split' or 'wide') ``flash_gqa_forward_bshd``
+    runs for these tensors on the current device (what ``kernel='auto'``
+    resolves to); launches nothing."""
+    a, _out, _lse, _keep = _prefill_bshd_prepare(q, k, v, None, None, None, causal, window_size, sink, kernel)
+    c = ctypes.c_int32(0)
+    st = _lib.lib().fgqa_prefill_kernel_choice(ctypes.byref(a), ctypes.byref(c))
+    if st != _lib.FGQA_OK:
+        raise _lib.FgqaError(st, "fgqa_prefill_kernel_choice")
+    return {_lib.FGQA_KERNEL_WHOLE: "whole", _lib.FGQA_KERNEL_SPLIT: "split", _lib.FGQA_KERNEL_WIDE: "wide"}[c.value]
 
 
 def launch_flash_gqa_forward_bf16_kernel(q, k, v, scale=None, out=None, lse=None, causal=True,

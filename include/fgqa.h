@@ -42,8 +42,14 @@ enum fgqa_status {
  *   FGQA_KERNEL_WHOLE  one workgroup runs a 128-row unit over its whole KV range
  *   FGQA_KERNEL_SPLIT  two wave groups run the two halves of a unit's KV range
  *                      and merge (the choice for grids under 4 units per CU)
+ *   FGQA_KERNEL_WIDE   (prefill forward, head dim 128, no window or sink) two
+ *                      wave groups share each K/V tile of a 256-row unit; a
+ *                      unit's KV range may be split over two workgroups that
+ *                      merge through device memory the library holds (at most
+ *                      256 units per call, else FGQA_ERR_UNSUPPORTED; calls
+ *                      that overlap on one device must not both use it)
  */
-enum fgqa_kernel_choice { FGQA_KERNEL_AUTO = 0, FGQA_KERNEL_WHOLE = 1, FGQA_KERNEL_SPLIT = 2 };
+enum fgqa_kernel_choice { FGQA_KERNEL_AUTO = 0, FGQA_KERNEL_WHOLE = 1, FGQA_KERNEL_SPLIT = 2, FGQA_KERNEL_WIDE = 3 };
 
 /*
  * Single-token decode (flash-decoding: split-KV pass + log-sum-exp combine).
@@ -227,6 +233,12 @@ typedef struct fgqa_prefill_args {
 } fgqa_prefill_args;
 
 int fgqa_prefill_bf16(const fgqa_prefill_args* args, void* stream);
+
+/* The kernel shape (FGQA_KERNEL_WHOLE, _SPLIT or _WIDE) fgqa_prefill_bf16
+ * runs for these arguments on the current device: `kernel`, or what AUTO
+ * picks.  Same validation and status codes as the call; launches nothing.
+ * (No counterpart in the reference, whose prefill has one kernel shape.) */
+int fgqa_prefill_kernel_choice(const fgqa_prefill_args* args, int32_t* kernel);
 
 /*
  * Prefill backward: dQ, dK, dV of the causal (or full) forward above.

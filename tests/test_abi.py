@@ -23,6 +23,7 @@ def test_c_abi_symbols_exported():
     hdr = open(os.path.join(ROOT, "include", "fgqa.h")).read()
     names = set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(fgqa_\w+)\s*\(", hdr, flags=re.M))
     assert names == {"fgqa_decode_workspace_bytes", "fgqa_decode_bf16", "fgqa_decode_bf16_noalloc", "fgqa_prefill_bf16",
+                     "fgqa_prefill_kernel_choice",
                      "fgqa_prefill_backward_workspace_bytes", "fgqa_prefill_backward_bf16",
                      "fgqa_decode_paged_workspace_bytes", "fgqa_decode_paged", "fgqa_sparse_prefill_bf16",
                      "fgqa_status_string", "fgqa_version"}
@@ -163,10 +164,14 @@ def _prefill_args(**kw):
     (dict(Hq=15, Hkv=2), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(Sq=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(scale=float("inf")), _lib.FGQA_ERR_INVALID_ARGUMENT),
-    (dict(kernel=3), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(kernel=4), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(kernel=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(kernel=_lib.FGQA_KERNEL_SPLIT, window=64), _lib.FGQA_ERR_UNSUPPORTED),   # no split SWA kernel
     (dict(kernel=_lib.FGQA_KERNEL_SPLIT, sink=4096), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(kernel=_lib.FGQA_KERNEL_WIDE, window=64), _lib.FGQA_ERR_UNSUPPORTED),    # no wide SWA kernel
+    (dict(kernel=_lib.FGQA_KERNEL_WIDE, sink=4096), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(kernel=_lib.FGQA_KERNEL_WIDE, D=192, Dv=128), _lib.FGQA_ERR_UNSUPPORTED),   # no wide MLA kernel
+    (dict(kernel=_lib.FGQA_KERNEL_WIDE, Sq=4128, Skv=4128), _lib.FGQA_ERR_UNSUPPORTED),   # 129 unit pairs
     (dict(ostride=[256 * 16 * 128, 16 * 128 + 4, 128]), _lib.FGQA_ERR_UNSUPPORTED),  # O rows: 16-byte stores
     (dict(D=256), _lib.FGQA_ERR_UNSUPPORTED),
     (dict(v=None), _lib.FGQA_ERR_INVALID_ARGUMENT),
@@ -182,6 +187,10 @@ def _prefill_args(**kw):
 ])
 def test_prefill_rejects_before_launch(kw, code):
     assert _lib.lib().fgqa_prefill_bf16(ctypes.byref(_prefill_args(**kw)), None) == code
+    if code != _lib.FGQA_OK:   # the kernel-choice query validates the same way
+        c = ctypes.c_int32(-7)
+        assert _lib.lib().fgqa_prefill_kernel_choice(ctypes.byref(_prefill_args(**kw)), ctypes.byref(c)) == code
+        assert c.value == -7
 
 
 def test_ctypes_structs_match_the_header(tmp_path):

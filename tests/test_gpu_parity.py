@@ -245,7 +245,7 @@ def test_prefill_shapes(cuda, B, Sq, Skv, Hq, Hkv, causal):
     _check_prefill(o, lse, o_ref, lse_ref, f"prefill B{B} Sq{Sq} Skv{Skv} Hq{Hq} Hkv{Hkv} causal{causal}")
 
 
-@pytest.mark.parametrize("kernel", ["whole", "split"])
+@pytest.mark.parametrize("kernel", ["whole", "split", "wide"])
 @pytest.mark.parametrize("B,Sq,Skv,Hq,Hkv,causal", [
     (1, 256, 256, 16, 1, True),
     (2, 300, 300, 8, 2, True),      # odd tile counts per unit
@@ -255,16 +255,23 @@ def test_prefill_shapes(cuda, B, Sq, Skv, Hq, Hkv, causal):
     (2, 64, 640, 16, 4, True),
     (1, 1111, 1111, 16, 2, True),   # up to 18 tiles per unit
     (1, 700, 900, 4, 4, False),
+    (1, 2048, 2048, 16, 1, True),   # 128 wide units of 8 heads: every pair but the lightest split
+    (3, 1000, 1000, 8, 1, True),    # odd number of wide units (the middle one alone)
+    (1, 1500, 1500, 4, 2, True),    # wide units of 4 heads x 64 positions
+    (1, 900, 900, 2, 1, True),      # 2 heads x 128 positions
+    (1, 1300, 1300, 1, 1, True),    # 1 head x 256 positions
 ])
 def test_prefill_whole_and_split_kernels(cuda, kernel, B, Sq, Skv, Hq, Hkv, causal):
-    """Both prefill kernels: one workgroup per unit over its whole KV range,
-    and the split kernel (two wave groups on the halves of the range, merged)."""
+    """The prefill kernels: one workgroup per unit over its whole KV range, the
+    split kernel (two wave groups on the halves of the range, merged), and the
+    wide kernel (two wave groups on one tile, a unit's range split over two
+    workgroups that merge through device memory)."""
     o, lse, o_ref, lse_ref = _prefill_case(cuda, 650 + Sq, B, Sq, Skv, Hq, Hkv, causal, kernel=kernel)
     _check_prefill(o, lse, o_ref, lse_ref,
                    f"kernel={kernel} B{B} Sq{Sq} Skv{Skv} Hq{Hq} Hkv{Hkv} causal{causal}")
 
 
-@pytest.mark.parametrize("kernel", ["whole", "split"])
+@pytest.mark.parametrize("kernel", ["whole", "split", "wide"])
 @pytest.mark.parametrize("case,scale", [("climb", 0.5), ("fall", 0.5), ("sharp", 2.0)])
 def test_prefill_running_max_moves(cuda, kernel, case, scale):
     """Score distributions that move the running max: keys scaled up along the
@@ -285,7 +292,22 @@ def test_prefill_running_max_moves(cuda, kernel, case, scale):
     qd, kd, vd = (to_torch_bf16(x, cuda) for x in (q, k, v))
     out, lse = _fg().flash_gqa_forward_bshd(qd, kd, vd, scale, causal=True, kernel=kernel)
     _sync()
-    _check_prefill(from_torch_bf16(out), lse.cpu().numpy(), o_ref, lse_ref, what)
+    o = from_torch_bf16(out)
+    if case == "sharp":
+        # Logits in the hundreds make each output one V value scaled by its
+        # bf16 P; how the kernels round P against a running max that trails
+        # the row max by up to 2^8 moves some outputs by one bf16 step, which
+        # is 0.031 at |O| >= 4, above the 2e-2 bar: here the bar is
+        # max(2e-2, one bf16 step of the expected value) per element.
+        got, ref = oracle.bf16_to_f32(o), oracle.bf16_to_f32(o_ref)
+        step = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))) - 7)
+        assert np.all(np.abs(got - ref) <= np.maximum(2e-2, step)), what
+        assert_close(got, ref, what, max_abs=np.inf)   # mean-abs bar unchanged
+        fin = np.isfinite(lse_ref)
+        assert np.array_equal(np.isfinite(lse.cpu().numpy()), fin)
+        assert np.max(np.abs(lse.cpu().numpy()[fin] - lse_ref[fin]), initial=0.0) <= LSE_TOL
+        return
+    _check_prefill(o, lse.cpu().numpy(), o_ref, lse_ref, what)
 
 
 @pytest.mark.parametrize("scale", [0.2, -0.05])
@@ -374,6 +396,52 @@ def test_prefill_config4_full_size(cuda):
     assert bool(out.isfinite().all())
     for rows in ((0, 128), (1000, 1064), (4096 - 128, 4096)):
         _sampled_prefill_check(q, k, v, out, lse, rows, 0, "config4")
+
+
+def test_prefill_auto_kernel_choice(cuda):
+    """What AUTO resolves to on this device: the wide kernel at BASELINE
+    config 4 (its 128 unit pairs fill the 256 CUs), the split kernel for a
+    small grid, the whole-range kernel at config 5 and with a sliding window."""
+    import torch
+    fg = _fg()
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+
+    def choice(B, S, Hq, Hkv, **kw):
+        q = torch.empty((B, S, Hq, 128), dtype=torch.bfloat16, device=cuda)
+        k = torch.empty((B, S, Hkv, 128), dtype=torch.bfloat16, device=cuda)
+        return fg.prefill_kernel_choice(q, k, k, **kw)
+
+    if cus == 256:
+        assert choice(1, 4096, 16, 1) == "wide"
+    assert choice(1, 1024, 16, 1) == "split"
+    assert choice(4, 16384, 32, 8) == "whole"
+    assert choice(1, 4096, 16, 1, window_size=128) == "whole"
+    assert choice(1, 4096, 16, 1, kernel="split") == "split"
+
+
+def test_prefill_wide_config4_repeatable(cuda):
+    """The wide kernel at BASELINE config 4, where every pair of its 256-row
+    units but one splits its heavy unit over two workgroups: three launches in
+    a row give bit-identical output (the arrival counters return to 0, and the
+    merge does not depend on which workgroup finishes first), and sampled rows
+    of split units match the oracle."""
+    import torch
+    fg = _fg()
+    B, S, Hq, Hkv = 1, 4096, 16, 1
+    q = gpu_normal_bf16((B, S, Hq, 128), 44, 1.0, cuda)
+    k = gpu_normal_bf16((B, S, Hkv, 128), 45, 1.0, cuda)
+    v = gpu_normal_bf16((B, S, Hkv, 128), 46, 1.0, cuda)
+    runs = []
+    for _ in range(3):
+        out, lse = fg.flash_gqa_forward_bshd(q, k, v, SCALE, kernel="wide")
+        _sync()
+        runs.append((out.clone(), lse.clone()))
+    for out, lse in runs[1:]:
+        assert torch.equal(out, runs[0][0]) and torch.equal(lse, runs[0][1]), "wide kernel: launches differ"
+    out, lse = runs[0]
+    assert bool(out.isfinite().all())
+    for rows in ((0, 64), (2016, 2080), (4096 - 96, 4096)):
+        _sampled_prefill_check(q, k, v, out, lse, rows, 0, "config4 wide")
 
 
 def test_prefill_config5_full_size(cuda):
