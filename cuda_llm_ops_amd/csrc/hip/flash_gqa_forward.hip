@@ -104,7 +104,7 @@ struct PfSeg {
     int lo, hi;
     int slot;          // this segment's slot (0 or 1)
     float* part;       // the unit's two slots, kPfPartFloats each
-    unsigned* ctr;     // the unit's arrival counter (0 between launches)
+    unsigned* ctr;     // the unit's 4 words: arrival counter, XCD of each slot (0 between launches)
 };
 
 // f(integral_constant<int, 0>), ..., f(integral_constant<int, N-1>): an
@@ -136,7 +136,7 @@ constexpr int kPfQStageBytes = kPfWaves * 32 * kHeadDim * 2;
 // each of the 8 waves.
 constexpr int kPwTileBytes = 4 * kPfVTileBytes;
 constexpr int kPwQBytes = 2 * kPfQStageBytes;
-constexpr int kPwSmemBytes = kPwTileBytes + kPwQBytes + 16;
+constexpr int kPwSmemBytes = kPwTileBytes + kPwQBytes + 16;   // + 3 words that broadcast counter reads
 constexpr int kPfPartFloats = 2 * kPfWaves * kPfMergeFloats * kWave;
 // most split units one launch may hold (two partial slots and a counter each)
 constexpr int kPwMaxSplit = 128;
@@ -480,6 +480,16 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     // branch touches the accumulators (a branch costs register copies), and
     // S(j+1) is computed even on the last step (its tile is fully masked).
     __syncthreads();  // the previous unit may still read the buffers
+    // wide split segment: this workgroup's XCD, for the other segment of the unit
+    [[maybe_unused]] uint32_t my_xcc1 = 0;
+    if constexpr (kWide) {
+        if (seg.part != nullptr) {
+            uint32_t hw;
+            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(hw));
+            my_xcc1 = (hw & 15u) + 1u;
+            if (tid == 0) __hip_atomic_store(seg.ctr + 1 + seg.slot, my_xcc1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
     // Staged Q: wave slot w's 32 rows fill 8 KB at kPfQStageBytes/4 * w past
     // the tile buffers, row r at 256*r with chunk c in slot c ^ (r % 16) (the
     // K layout).  One load instruction fills 1 KB = 4 whole rows; the wave of
@@ -799,20 +809,32 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
             // its arrival; the second merges that with its own and writes the
             // output.  A segment that finds no arrival publishes, and merges
             // anyway if the other one arrived in the meantime.  The merger
-            // sets the counter back to 0 for the next launch.
-            // Ordering: every wave's stores complete (workgroup release) before
-            // the barrier; thread 0's device-scope release on the counter then
-            // makes them visible device-wide (one L2 write-back for the
-            // workgroup), and the reader's thread 0 acquires before the
-            // barrier that lets its waves read (one L2 invalidate).
+            // sets the unit's words back to 0 for the next launch.
+            // Words of the unit: ctr[0] counts arrivals as 1 + the publisher's
+            // XCD, ctr[1 + slot] holds 1 + the XCD of the segment in that slot
+            // (written at its start).  Ordering: every wave waits for its own
+            // partial stores (they are then in its XCD's L2: the L1 writes
+            // through) before the barrier after which thread 0 counts the
+            // arrival.  When the other segment runs on the same XCD (blocks w
+            // and w + 8 do: blocks go round-robin over the XCDs) the two share
+            // that L2, and the reader only invalidates its L1 (the compiler's
+            // own acquire for workgroups spread over CUs of one L2); otherwise
+            // thread 0 counts with a device-scope release (one L2 write-back
+            // for the workgroup) and the reader's waves acquire at device
+            // scope.
             unsigned* word = reinterpret_cast<unsigned*>(smem_all + kPwTileBytes + kPwQBytes);
             const int woff = wave_wg * kPfMergeFloats * kWave;
             float* own = seg.part + seg.slot * kPfPartFloats + woff;
             const float* other = seg.part + (1 - seg.slot) * kPfPartFloats + woff;
-            if (tid == 0) *word = __hip_atomic_load(seg.ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+            if (tid == 0) {
+                word[0] = __hip_atomic_load(seg.ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                word[1] = __hip_atomic_load(seg.ctr + 2 - seg.slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
             __syncthreads();
-            bool merge = *word != 0u;
+            unsigned arrived = word[0];
+            bool merge = arrived != 0u;
             if (!merge) {
+                const bool near = word[1] == my_xcc1;   // the reader shares this XCD's L2
                 f32x4_t* o4 = reinterpret_cast<f32x4_t*>(own) + lane;
 #pragma unroll
                 for (int db = 0; db < 4; ++db)
@@ -822,15 +844,24 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
                                                             oacc[db][4 * i4 + 2], oacc[db][4 * i4 + 3]};
                 own[64 * kWave + lane] = m_run;
                 own[65 * kWave + lane] = l_run;
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's partial is in L2
                 __syncthreads();
-                if (tid == 0) *word = __hip_atomic_fetch_add(seg.ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+                if (tid == 0)
+                    word[2] = near ? __hip_atomic_fetch_add(seg.ctr, my_xcc1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                   : __hip_atomic_fetch_add(seg.ctr, my_xcc1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
                 __syncthreads();
-                merge = *word != 0u;
+                arrived = word[2];
+                merge = arrived != 0u;
                 if (!merge) return;   // the other segment merges
             }
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");   // after thread 0's device-scope acquire
-            if (tid == 0) __hip_atomic_store(seg.ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // every wave acquires the other partial
+            if (arrived == my_xcc1) asm volatile("buffer_inv sc0" ::: "memory");
+            else __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            if (tid == 0) {
+                __hip_atomic_store(seg.ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(seg.ctr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(seg.ctr + 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
             // slot 0's terms first whichever merges, so the output does not
             // depend on the order of arrival
             const bool first = seg.slot == 0;
@@ -1136,7 +1167,7 @@ __global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_wide_kernel(Prefill
         // the first workgroup's share of the heavy unit
         const int a = min(nh, (nh + nl + p.wide_bias + 1) >> 1);
         const bool split = a < nh;
-        PfSeg seg{0, a, role, nullptr, p.wide_ctr + pair};
+        PfSeg seg{0, a, role, nullptr, p.wide_ctr + 4 * pair};
         if (role == 0) {
             if (sgi > 0) break;
             if (split) seg.part = p.wide_part + (size_t)pair * 2 * kPfPartFloats;
@@ -1163,7 +1194,7 @@ __global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_wide_kernel(Prefill
 // device current) and only those pointers are passed to kernels.  Launches
 // that overlap on one device share them and would race.
 static __device__ __align__(256) float pw_part[(size_t)kPwMaxSplit * 2 * kPfPartFloats];
-static __device__ __align__(256) unsigned pw_ctr[kPwMaxSplit];
+static __device__ __align__(256) unsigned pw_ctr[4 * kPwMaxSplit];
 
 namespace {
 
