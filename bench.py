@@ -42,7 +42,7 @@ SCALE = 1.0 / math.sqrt(128)
 # changes.
 TRAFFIC_BYTES = {
     "decode_cfg2": 1010681051,   # = Q+K+V+O (1,010,565,120 B) + 0.01 %
-    "prefill_cfg4": 83422515,    # Q+O+LSE 32.25 MiB, K/V per XCD, split units' partials written and read back
+    "prefill_cfg4": 83448320,    # Q+O+LSE 32.25 MiB, K/V per XCD, split units' partials written and read back
 }
 
 DECODE_CONFIGS = {
