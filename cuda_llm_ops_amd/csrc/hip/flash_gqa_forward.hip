@@ -181,7 +181,7 @@ template <int kGroups, bool kSwa, int kDk, bool kWide = false>
 __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* smem_all, int qb, int hg, int kvh,
                                         int b, PfSeg seg = PfSeg{0, 0, 0, nullptr, nullptr}) {
     using D = PfDims<kDk>;
-    static_assert(!kWide || (kGroups == 2 && kDk == kHeadDim && !kSwa), "wide units: two groups, head dim 128");
+    static_assert(!kWide || (kGroups == 2 && kDk == kHeadDim), "wide units: two groups, head dim 128");
     // opaque in the split kernel: its loop over units recomputes what depends
     // on the thread index inside each unit instead of holding it in
     // registers across the loop
@@ -210,7 +210,7 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     const int unit_tiles = max(0, (kv_end + kPfTile - 1) / kPfTile - t_lo);
     // loop trips, same for both groups, and this group's first tile
     const int n_tiles = kWide ? seg.hi - seg.lo : kGroups == 1 ? unit_tiles : (unit_tiles + 1) / 2;
-    const int t_first = kWide ? seg.lo : t_lo + grp * n_tiles;
+    const int t_first = kWide ? t_lo + seg.lo : t_lo + grp * n_tiles;
     (void)unit_tiles;
     // keys this group may use: the unit's range, cut at the group's last tile
     const int kv_hi = min(kv_end, (t_first + n_tiles) * kPfTile);
@@ -1137,12 +1137,16 @@ __global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_split_kernel(Prefil
 // tiles beyond half the pair's tiles, which pays for the second's extra unit
 // start.  The heavy unit's two partial results merge through device memory
 // (pf_unit: whichever segment finishes second merges).
+// Tiles of a unit's KV range (a sliding window starts it at the tile that
+// holds its first row's first key).
 __device__ __forceinline__ int pf_unit_tiles(const PrefillParams& p, int qb, int qrows) {
     int kv_end = p.skv;
     if (p.causal) kv_end = min(kv_end, min((qb + 1) * qrows, p.sq));
-    return (kv_end + kPfTile - 1) / kPfTile;
+    const int t_lo = p.window > 0 ? max(0, qb * qrows - p.window + 1) / kPfTile : 0;
+    return max(0, (kv_end + kPfTile - 1) / kPfTile - t_lo);
 }
 
+template <bool kSwa>
 __global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_wide_kernel(PrefillParams p0) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int w = blockIdx.x;
@@ -1182,7 +1186,7 @@ __global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_wide_kernel(Prefill
             seg.lo = 0;
             seg.hi = nl;
         }
-        pf_unit<2, false, kHeadDim, true>(p, smem, qb, hg, kvh, b, seg);
+        pf_unit<2, kSwa, kHeadDim, true>(p, smem, qb, hg, kvh, b, seg);
     }
 }
 
@@ -1233,7 +1237,9 @@ int64_t wide_pairs(const fgqa_prefill_args* a) {
 // The kernel shape a validated call runs on a device with `cus` CUs: the
 // caller's `kernel`, or for AUTO the choice by grid size:
 //  - wide: causal, head dim 128, no window or sink, and the wide kernel's
-//    unit pairs fill the CUs (two workgroups per pair, within 1/8 of one per CU);
+//    unit pairs fill the CUs (two workgroups per pair, within 1/8 of one per
+//    CU).  Forced, it also runs the window / sink form (at the reference's
+//    window of 512 in 27.5 us, against 26.1 us for the whole-range kernel);
 //  - split: fewer than 4 of the 128-row units per CU, no window or sink: each
 //    unit's KV range runs on two wave groups, so a CU never runs a long unit
 //    with one wave per SIMD, and each CU gets a share of the units whose tile
@@ -1273,9 +1279,8 @@ int validate_prefill(const fgqa_prefill_args* a) {
     if (dv != kHeadDim || (a->head_dim != kHeadDim && a->head_dim != 192)) return FGQA_ERR_UNSUPPORTED;
     if (a->head_dim == 192 && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
     if (a->kernel < FGQA_KERNEL_AUTO || a->kernel > FGQA_KERNEL_WIDE) return FGQA_ERR_INVALID_ARGUMENT;
-    // the window / sink variant has no split or wide form; the wide kernel has head dim 128 only
-    if ((a->kernel == FGQA_KERNEL_SPLIT || a->kernel == FGQA_KERNEL_WIDE) && (a->window_size > 0 || a->sink != nullptr))
-        return FGQA_ERR_UNSUPPORTED;
+    // the window / sink variant has no split form; the wide kernel has head dim 128 only
+    if (a->kernel == FGQA_KERNEL_SPLIT && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
     if (a->kernel == FGQA_KERNEL_WIDE && a->head_dim != kHeadDim) return FGQA_ERR_UNSUPPORTED;
     const int64_t lim = (int64_t)1 << 31;
     if ((int64_t)(a->seqlen_q + 128) * a->q_stride[1] * 2 >= lim ||
@@ -1378,13 +1383,14 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
         p.div_hgroups = make_fast_div(p.n_hgroups);
         p.wide_bias = 3;
         if (const int e = pw_scratch(&p.wide_part, &p.wide_ctr); e != FGQA_OK) return e;
-        // attribute slot 5: the wide kernel
-        if (const int e = set_kernel_smem_once(5, reinterpret_cast<const void*>(prefill_wide_kernel), kPwSmemBytes);
-            e != FGQA_OK)
-            return e;
+        // attribute slots 5, 6: the wide kernels
+        const void* wfn = swa ? reinterpret_cast<const void*>(prefill_wide_kernel<true>)
+                              : reinterpret_cast<const void*>(prefill_wide_kernel<false>);
+        if (const int e = set_kernel_smem_once(swa ? 6 : 5, wfn, kPwSmemBytes); e != FGQA_OK) return e;
         // blocks w and w + 8 of each 16 run one pair
         const dim3 grid((unsigned)(16 * ceil_div(wide_pairs(a), 8)));
-        hipLaunchKernelGGL(prefill_wide_kernel, grid, dim3(2 * kPfThreads), kPwSmemBytes, s, p);
+        if (swa) hipLaunchKernelGGL(prefill_wide_kernel<true>, grid, dim3(2 * kPfThreads), kPwSmemBytes, s, p);
+        else hipLaunchKernelGGL(prefill_wide_kernel<false>, grid, dim3(2 * kPfThreads), kPwSmemBytes, s, p);
         if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
         return FGQA_OK;
     }

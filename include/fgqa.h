@@ -42,7 +42,7 @@ enum fgqa_status {
  *   FGQA_KERNEL_WHOLE  one workgroup runs a 128-row unit over its whole KV range
  *   FGQA_KERNEL_SPLIT  two wave groups run the two halves of a unit's KV range
  *                      and merge (the choice for grids under 4 units per CU)
- *   FGQA_KERNEL_WIDE   (prefill forward, head dim 128, no window or sink) two
+ *   FGQA_KERNEL_WIDE   (prefill forward, head dim 128) two
  *                      wave groups share each K/V tile of a 256-row unit; a
  *                      unit's KV range may be split over two workgroups that
  *                      merge through device memory the library holds (at most
@@ -206,7 +206,7 @@ int fgqa_decode_paged(const fgqa_decode_paged_args* args, void* stream);
  *           (128, 128), and (192, 128) without window or sink.
  *   kernel  an fgqa_kernel_choice (0 = AUTO).  The window / sink variant has
  *           no split form: FGQA_KERNEL_SPLIT with either returns
- *           FGQA_ERR_UNSUPPORTED.
+ *           FGQA_ERR_UNSUPPORTED (FGQA_KERNEL_WIDE runs it).
  */
 typedef struct fgqa_prefill_args {
     const void* q;

@@ -45,13 +45,15 @@ def _case(cuda, seed, B, Sq, Skv, Hq, Hkv, window, with_sink, kernel="auto"):
     return from_torch_bf16(out), lse.cpu().numpy(), o_ref, l_ref
 
 
-@pytest.mark.parametrize("kernel", ["auto", "whole"])
+@pytest.mark.parametrize("kernel", ["auto", "whole", "wide"])
 @pytest.mark.parametrize("B,S,Hq,Hkv,window,with_sink", [
     (1, 300, 16, 1, 64, True),
     (2, 500, 8, 2, 17, True),     # window not a multiple of the tile
     (1, 400, 6, 3, 1, True),      # each row sees itself only
     (1, 257, 4, 4, 100, False),   # no sink: plain windowed softmax
     (1, 700, 4, 1, 4096, True),   # window past the sequence: causal + sink
+    (1, 2048, 16, 1, 300, True),  # wide kernel: early units shorter, their pairs split
+    (1, 1500, 8, 1, 1000, True),
 ])
 def test_swa_shapes(cuda, kernel, B, S, Hq, Hkv, window, with_sink):
     what = f"swa kernel={kernel} B{B} S{S} Hq{Hq} Hkv{Hkv} W{window} sink={with_sink}"
