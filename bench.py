@@ -256,6 +256,15 @@ def bench_prefill(cfg_id, steps, warmup, dev, keep=None):
     step = fg.prepare_prefill(q, k, v, SCALE, out=out, lse=lse, causal=True)
     kernel = {"whole": "prefill_kernel", "split": "prefill_split_kernel",
               "wide": "prefill_wide_kernel"}[fg.prefill_kernel_choice(q, k, v, causal=True)]
+    if kernel == "prefill_wide_kernel":
+        # unit pairs that fill the CUs split units over two workgroups; more
+        # run whole units on a persistent grid
+        G = Hq // Hkv
+        hb = 8 if G % 8 == 0 else 4 if G % 4 == 0 else 2 if G % 2 == 0 else 1
+        pairs = (B * Hkv * (G // hb) * -(-S // (256 // hb)) + 1) // 2
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        if pairs > 128 or 2 * pairs > cus:
+            kernel = "prefill_wide_persistent_kernel"
 
     total_ms, per = _time_calls(step, steps, warmup, min_warm_ms=AUX_WARM_MS)
     # the reference's causal-halved count (test_flash_gqa_kernel.py:282-301)

@@ -1190,6 +1190,29 @@ __global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_wide_kernel(Prefill
     }
 }
 
+// Wide kernel for grids with more unit pairs than the split form holds:
+// persistent, one workgroup per CU; workgroup w runs ranks w, 2G-1-w, 2G+w,
+// ... (G = gridDim.x) of the heaviest-first order as whole units, so each
+// lap goes the other way and every CU's units add up to about the same
+// number of tiles.
+template <bool kSwa>
+__global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_wide_persistent_kernel(PrefillParams p0) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    const int units = p0.n_qblocks * p0.n_streams;
+    const int g = gridDim.x;
+    const int w = blockIdx.x;
+#pragma nounroll
+    for (int lap = 0;; ++lap) {
+        const int r = (lap & 1) ? (lap + 1) * g - 1 - w : lap * g + w;
+        if (r >= units) break;   // later laps hold only higher ranks
+        const PrefillParams p = pf_params_reread(p0);
+        int qb, hg, kvh, b;
+        pf_rank_unit(p, r, &qb, &hg, &kvh, &b);
+        const PfSeg seg{0, pf_unit_tiles(p, qb, 256 >> p.hb_log2), 0, nullptr, nullptr};
+        pf_unit<2, kSwa, kHeadDim, true>(p, smem, qb, hg, kvh, b, seg);
+    }
+}
+
 // Partial-result slots and arrival counters of the wide kernel's split units
 // (kPwMaxSplit units; held by every device the library runs on until the
 // process ends; the counters start at 0 and each launch leaves them at 0).
@@ -1244,6 +1267,9 @@ int64_t wide_pairs(const fgqa_prefill_args* a) {
 //    unit's KV range runs on two wave groups, so a CU never runs a long unit
 //    with one wave per SIMD, and each CU gets a share of the units whose tile
 //    counts add up evenly;
+//  - wide again for the causal head-dim-128 grids left (at least 4 of the
+//    128-row units per CU), as whole 256-row units on a persistent grid
+//    (config 5: 7.84 -> 7.00 ms against the whole-range kernel);
 //  - whole: the rest (a sliding window gives every unit about the same number
 //    of tiles: nothing to balance).
 int prefill_choice(const fgqa_prefill_args* a, int cus) {
@@ -1258,6 +1284,7 @@ int prefill_choice(const fgqa_prefill_args* a, int cus) {
     if (!mla && !swa && a->causal && pairs <= kPwMaxSplit && wide_grid <= cus && 8 * wide_grid >= 7 * (int64_t)cus)
         return FGQA_KERNEL_WIDE;
     if (units < 4 * (int64_t)cus && !swa) return FGQA_KERNEL_SPLIT;
+    if (!mla && !swa && a->causal) return FGQA_KERNEL_WIDE;   // whole wide units, persistent
     return FGQA_KERNEL_WHOLE;
 }
 
@@ -1308,7 +1335,6 @@ extern "C" int fgqa_prefill_kernel_choice(const fgqa_prefill_args* a, int32_t* k
     int st = validate_prefill(a);
     if (st != FGQA_OK) return st;
     if (kernel == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->kernel == FGQA_KERNEL_WIDE && wide_pairs(a) > kPwMaxSplit) return FGQA_ERR_UNSUPPORTED;
     const int cus = device_cu_count();
     if (cus <= 0) return FGQA_ERR_HIP;
     *kernel = prefill_choice(a, cus);
@@ -1363,7 +1389,6 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
 
     const int64_t units = (int64_t)p.n_qblocks * p.n_streams;
     if (units >= ((int64_t)1 << 31)) return FGQA_ERR_UNSUPPORTED;
-    if (a->kernel == FGQA_KERNEL_WIDE && wide_pairs(a) > kPwMaxSplit) return FGQA_ERR_UNSUPPORTED;
     const int cus = device_cu_count();
     if (cus <= 0) return FGQA_ERR_HIP;
     const int choice = prefill_choice(a, cus);
@@ -1382,6 +1407,19 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
         p.div_streams = make_fast_div(p.n_streams);
         p.div_hgroups = make_fast_div(p.n_hgroups);
         p.wide_bias = 3;
+        const int64_t pairs = wide_pairs(a);
+        if (pairs > kPwMaxSplit || 2 * pairs > cus) {
+            // more pairs than one per two CUs: whole units on a persistent grid
+            const void* pfn = swa ? reinterpret_cast<const void*>(prefill_wide_persistent_kernel<true>)
+                                  : reinterpret_cast<const void*>(prefill_wide_persistent_kernel<false>);
+            if (const int e = set_kernel_smem_once(swa ? 8 : 7, pfn, kPwSmemBytes); e != FGQA_OK) return e;
+            const int64_t units_w = (int64_t)p.n_qblocks * p.n_streams;
+            const dim3 grid((unsigned)(units_w < cus ? units_w : cus));
+            if (swa) hipLaunchKernelGGL(prefill_wide_persistent_kernel<true>, grid, dim3(2 * kPfThreads), kPwSmemBytes, s, p);
+            else hipLaunchKernelGGL(prefill_wide_persistent_kernel<false>, grid, dim3(2 * kPfThreads), kPwSmemBytes, s, p);
+            if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
+            return FGQA_OK;
+        }
         if (const int e = pw_scratch(&p.wide_part, &p.wide_ctr); e != FGQA_OK) return e;
         // attribute slots 5, 6: the wide kernels
         const void* wfn = swa ? reinterpret_cast<const void*>(prefill_wide_kernel<true>)

@@ -42,12 +42,13 @@ enum fgqa_status {
  *   FGQA_KERNEL_WHOLE  one workgroup runs a 128-row unit over its whole KV range
  *   FGQA_KERNEL_SPLIT  two wave groups run the two halves of a unit's KV range
  *                      and merge (the choice for grids under 4 units per CU)
- *   FGQA_KERNEL_WIDE   (prefill forward, head dim 128) two
- *                      wave groups share each K/V tile of a 256-row unit; a
+ *   FGQA_KERNEL_WIDE   (prefill forward, head dim 128) two wave groups
+ *                      share each K/V tile of a 256-row unit.  With at most
+ *                      one unit pair per two CUs (and at most 128 pairs) a
  *                      unit's KV range may be split over two workgroups that
- *                      merge through device memory the library holds (at most
- *                      256 units per call, else FGQA_ERR_UNSUPPORTED; calls
- *                      that overlap on one device must not both use it)
+ *                      merge through device memory the library holds (calls
+ *                      that overlap on one device must not both use it);
+ *                      larger grids run whole units on a persistent grid
  */
 enum fgqa_kernel_choice { FGQA_KERNEL_AUTO = 0, FGQA_KERNEL_WHOLE = 1, FGQA_KERNEL_SPLIT = 2, FGQA_KERNEL_WIDE = 3 };
 

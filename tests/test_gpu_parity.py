@@ -260,6 +260,8 @@ def test_prefill_shapes(cuda, B, Sq, Skv, Hq, Hkv, causal):
     (1, 1500, 1500, 4, 2, True),    # wide units of 4 heads x 64 positions
     (1, 900, 900, 2, 1, True),      # 2 heads x 128 positions
     (1, 1300, 1300, 1, 1, True),    # 1 head x 256 positions
+    (16, 512, 512, 16, 1, True),    # 256 unit pairs: the wide kernel runs whole units, persistent
+    (4, 600, 600, 8, 2, False),     # the same, non-causal
 ])
 def test_prefill_whole_and_split_kernels(cuda, kernel, B, Sq, Skv, Hq, Hkv, causal):
     """The prefill kernels: one workgroup per unit over its whole KV range, the
@@ -400,8 +402,9 @@ def test_prefill_config4_full_size(cuda):
 
 def test_prefill_auto_kernel_choice(cuda):
     """What AUTO resolves to on this device: the wide kernel at BASELINE
-    config 4 (its 128 unit pairs fill the 256 CUs), the split kernel for a
-    small grid, the whole-range kernel at config 5 and with a sliding window."""
+    config 4 (its 128 unit pairs fill the 256 CUs) and at config 5 (whole
+    units, persistent), the split kernel for a small grid, the whole-range
+    kernel with a sliding window and for the MLA head dims."""
     import torch
     fg = _fg()
     cus = torch.cuda.get_device_properties(cuda).multi_processor_count
@@ -414,7 +417,7 @@ def test_prefill_auto_kernel_choice(cuda):
     if cus == 256:
         assert choice(1, 4096, 16, 1) == "wide"
     assert choice(1, 1024, 16, 1) == "split"
-    assert choice(4, 16384, 32, 8) == "whole"
+    assert choice(4, 16384, 32, 8) == "wide"
     assert choice(1, 4096, 16, 1, window_size=128) == "whole"
     assert choice(1, 4096, 16, 1, kernel="split") == "split"
 
