@@ -69,6 +69,9 @@ def _run(cuda, q, k, v, idx, scale=SCALE, causal=True):
     (1, 100, 100, 6, 2, 20, True),      # G = 3: a partial head group
     (1, 150, 300, 4, 1, 64, False),     # Sq < Skv
     (1, 300, 120, 4, 1, 64, True),      # Sq > Skv
+    (1, 700, 700, 16, 1, 512, True),    # the longest list the kernel sorts by key
+    (1, 700, 700, 16, 1, 513, True),    # one longer: taken in list order
+    (1, 400, 900, 4, 2, 1000, False),   # list order, non-causal
 ])
 def test_sparse_shapes(cuda, B, Sq, Skv, Hq, Hkv, nsparse, causal):
     what = f"sparse B{B} Sq{Sq} Skv{Skv} Hq{Hq} Hkv{Hkv} n{nsparse} causal={causal}"
