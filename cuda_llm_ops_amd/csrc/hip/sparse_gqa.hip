@@ -431,7 +431,7 @@ int validate_sparse(const fgqa_sparse_prefill_args* a) {
         (reinterpret_cast<uintptr_t>(a->kv_indices) & 3u))
         return FGQA_ERR_UNSUPPORTED;
     for (int i = 0; i < 3; ++i)
-        if ((a->q_stride[i] & 7) || (a->k_stride[i] & 7) || (a->v_stride[i] & 7) || (a->o_stride[i] & 3))
+        if ((a->q_stride[i] & 7) || (a->k_stride[i] & 7) || (a->v_stride[i] & 7) || (a->o_stride[i] & 7))
             return FGQA_ERR_UNSUPPORTED;
     return FGQA_OK;
 }

@@ -223,7 +223,7 @@ def _sparse_args(**kw):
     a.causal = 1
     a.scale = kw.get("scale", D ** -0.5)
     a.q_stride[:] = [Sq * Hq * D, Hq * D, D]
-    a.o_stride[:] = [Sq * Hq * D, Hq * D, D]
+    a.o_stride[:] = kw.get("ostride", [Sq * Hq * D, Hq * D, D])
     a.k_stride[:] = [Skv * Hkv * D, Hkv * D, D]
     a.v_stride[:] = [Skv * Hkv * D, Hkv * D, D]
     a.idx_stride[:] = [Hkv * Sq * n, Sq * n, n]
@@ -241,6 +241,7 @@ def _sparse_args(**kw):
     (dict(kv_indices=None), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(kv_indices=4098), _lib.FGQA_ERR_UNSUPPORTED),   # int32 entries need 4-byte alignment
     (dict(q=4096 + 8), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(ostride=[256 * 16 * 128, 16 * 128 + 4, 128]), _lib.FGQA_ERR_UNSUPPORTED),   # strides: multiples of 8
 ])
 def test_sparse_prefill_rejects_before_launch(kw, code):
     assert _lib.lib().fgqa_sparse_prefill_bf16(ctypes.byref(_sparse_args(**kw)), None) == code
