@@ -447,6 +447,42 @@ def test_prefill_wide_config4_repeatable(cuda):
         _sampled_prefill_check(q, k, v, out, lse, rows, 0, "config4 wide")
 
 
+def test_prefill_wide_graph_replays(cuda):
+    """The wide kernel (split units merging through the library's device
+    memory) captured in a HIP graph: every launch leaves the arrival counters
+    at 0 and no memset is recorded, so each replay, with eager launches and
+    synchronizations between replays, must match the eager result exactly."""
+    import torch
+    fg = _fg()
+    B, S, Hq, Hkv = 1, 2048, 16, 1   # 64 unit pairs, all but the lightest split
+    q = gpu_normal_bf16((B, S, Hq, 128), 47, 1.0, cuda)
+    k = gpu_normal_bf16((B, S, Hkv, 128), 48, 1.0, cuda)
+    v = gpu_normal_bf16((B, S, Hkv, 128), 49, 1.0, cuda)
+    out = torch.empty_like(q)
+    lse = torch.empty((B, Hq, S), dtype=torch.float32, device=cuda)
+    step = fg.prepare_prefill(q, k, v, SCALE, out=out, lse=lse, causal=True, kernel="wide")
+    step()   # one-time set-up (kernel attributes, device memory lookup) outside the capture
+    _sync()
+    ref_o, ref_l = out.clone(), lse.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    for i in range(4):
+        out.zero_()
+        lse.zero_()
+        g.replay()
+        _sync()
+        assert torch.equal(out, ref_o) and torch.equal(lse, ref_l), f"replay {i}"
+        step()   # an eager launch between replays
+        _sync()
+        assert torch.equal(out, ref_o), f"eager launch after replay {i}"
+    _sampled_prefill_check(q, k, v, out, lse, (S - 64, S), 0, "wide kernel after graph replays")
+
+
 def test_prefill_config5_full_size(cuda):
     """B=4, S=16384, Hq=32, Hkv=8, causal, N(0, 0.5^2): sampled rows."""
     fg = _fg()
