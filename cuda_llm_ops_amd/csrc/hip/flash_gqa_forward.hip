@@ -137,6 +137,10 @@ constexpr int kPfQStageBytes = kPfWaves * 32 * kHeadDim * 2;
 constexpr int kPwTileBytes = 4 * kPfVTileBytes;
 constexpr int kPwQBytes = 2 * kPfQStageBytes;
 constexpr int kPwSmemBytes = kPwTileBytes + kPwQBytes + 16;   // + 3 words that broadcast counter reads
+// With the MLA head dim (192) the wide kernel loads Q straight into registers
+// (a 256-row Q tile does not fit beside the 80 KB of tiles) and stages O in
+// the tile buffers, idle after the loop.
+constexpr int pw_smem_bytes(int dk) { return dk == kHeadDim ? kPwSmemBytes : 2 * (64 * 384) + 2 * kPfVTileBytes + 16; }
 constexpr int kPfPartFloats = 2 * kPfWaves * kPfMergeFloats * kWave;
 // most split units one launch may hold (two partial slots and a counter each)
 constexpr int kPwMaxSplit = 128;
@@ -181,7 +185,9 @@ template <int kGroups, bool kSwa, int kDk, bool kWide = false>
 __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* smem_all, int qb, int hg, int kvh,
                                         int b, PfSeg seg = PfSeg{0, 0, 0, nullptr, nullptr}) {
     using D = PfDims<kDk>;
-    static_assert(!kWide || (kGroups == 2 && kDk == kHeadDim), "wide units: two groups, head dim 128");
+    static_assert(!kWide || kGroups == 2, "wide units: two groups");
+    // wide: the tile buffers, then (head dim 128) the Q/O area, then 3 broadcast words
+    [[maybe_unused]] constexpr int kWWords = D::kGroupBytes + (kDk == kHeadDim ? kPwQBytes : 0);
     // opaque in the split kernel: its loop over units recomputes what depends
     // on the thread index inside each unit instead of holding it in
     // registers across the loop
@@ -500,17 +506,20 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
               : lds_base + (2 - grp) * D::kGroupBytes + wave * (kPfQStageBytes / kPfWaves);
     if constexpr (kWide) {
         // a wide unit's waves have rows of their own: each loads its 8 KB
-        auto dmaq = [](auto ic, uint32_t base, uint32_t voffset, __amdgpu_buffer_rsrc_t rsrc) {
-            constexpr int kOff = decltype(ic)::value * 1024;
-            asm volatile("s_add_u32 m0, %0, %3\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                         :: "s"(base), "v"(voffset), "s"(rsrc), "i"(kOff) : "memory", "scc");
-        };
-        static_for<8>([&](auto ic) {
-            const int slot = 64 * decltype(ic)::value + lane;
-            const int r = slot >> 4;
-            const uint32_t voff = (uint32_t)(q0w + r) * qss + ((uint32_t)((slot & 15) ^ (r & 15)) << 4);
-            dmaq(ic, q_lds, voff, qrs);
-        });
+        // (head dim 192: Q came straight into registers above)
+        if constexpr (kStageQ) {
+            auto dmaq = [](auto ic, uint32_t base, uint32_t voffset, __amdgpu_buffer_rsrc_t rsrc) {
+                constexpr int kOff = decltype(ic)::value * 1024;
+                asm volatile("s_add_u32 m0, %0, %3\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                             :: "s"(base), "v"(voffset), "s"(rsrc), "i"(kOff) : "memory", "scc");
+            };
+            static_for<8>([&](auto ic) {
+                const int slot = 64 * decltype(ic)::value + lane;
+                const int r = slot >> 4;
+                const uint32_t voff = (uint32_t)(q0w + r) * qss + ((uint32_t)((slot & 15) ^ (r & 15)) << 4);
+                dmaq(ic, q_lds, voff, qrs);
+            });
+        }
         // group 0 loads K(0); group 1 loads V(0) and K(1), awaited by the end
         // of its S(0) phase (group 0's first MFMA phase comes after that)
         if (grp == 0) {
@@ -519,7 +528,7 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         } else {
             if (n_tiles > 0) issue_tile(0, -1, 0);
             if (n_tiles > 1) issue_tile(1, 1, -1);
-            wait_vmem_but((n_tiles > 0 ? 4 : 0) + (n_tiles > 1 ? 4 : 0));
+            wait_vmem_but((n_tiles > 0 ? 4 : 0) + (n_tiles > 1 ? D::kDmaK : 0));
         }
     } else if constexpr (kStageQ) {
         auto dmaq = [](auto ic, uint32_t base, uint32_t voffset, __amdgpu_buffer_rsrc_t rsrc) {
@@ -822,7 +831,7 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
             // thread 0 counts with a device-scope release (one L2 write-back
             // for the workgroup) and the reader's waves acquire at device
             // scope.
-            unsigned* word = reinterpret_cast<unsigned*>(smem_all + kPwTileBytes + kPwQBytes);
+            unsigned* word = reinterpret_cast<unsigned*>(smem_all + kWWords);
             const int woff = wave_wg * kPfMergeFloats * kWave;
             float* own = seg.part + seg.slot * kPfPartFloats + woff;
             const float* other = seg.part + (1 - seg.slot) * kPfPartFloats + woff;
@@ -1032,7 +1041,7 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         // give each store 32 rows 16 bytes each).
         static_assert(kGroups == 1 || kStageQ || kPfWaves * kPfMergeFloats * kWave * 4 <= D::kGroupBytes,
                       "O staging in group 1's buffers must not overlap the merge area");
-        unsigned char* ol = kWide ? smem_all + kPwTileBytes + wave_wg * (kPfQStageBytes / kPfWaves)
+        unsigned char* ol = kWide ? smem_all + (kStageQ ? kPwTileBytes : 0) + wave_wg * (kPfQStageBytes / kPfWaves)
                                   : smem_all + (kGroups == 1 ? 0 : kStageQ ? 2 : 1) * D::kGroupBytes +
                                         wave * (kPfQStageBytes / kPfWaves);
 #pragma unroll
@@ -1146,7 +1155,7 @@ __device__ __forceinline__ int pf_unit_tiles(const PrefillParams& p, int qb, int
     return max(0, (kv_end + kPfTile - 1) / kPfTile - t_lo);
 }
 
-template <bool kSwa>
+template <bool kSwa, int kDk>
 __global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_wide_kernel(PrefillParams p0) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int w = blockIdx.x;
@@ -1186,7 +1195,7 @@ __global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_wide_kernel(Prefill
             seg.lo = 0;
             seg.hi = nl;
         }
-        pf_unit<2, kSwa, kHeadDim, true>(p, smem, qb, hg, kvh, b, seg);
+        pf_unit<2, kSwa, kDk, true>(p, smem, qb, hg, kvh, b, seg);
     }
 }
 
@@ -1195,7 +1204,7 @@ __global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_wide_kernel(Prefill
 // ... (G = gridDim.x) of the heaviest-first order as whole units, so each
 // lap goes the other way and every CU's units add up to about the same
 // number of tiles.
-template <bool kSwa>
+template <bool kSwa, int kDk>
 __global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_wide_persistent_kernel(PrefillParams p0) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int units = p0.n_qblocks * p0.n_streams;
@@ -1209,7 +1218,7 @@ __global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_wide_persistent_ker
         int qb, hg, kvh, b;
         pf_rank_unit(p, r, &qb, &hg, &kvh, &b);
         const PfSeg seg{0, pf_unit_tiles(p, qb, 256 >> p.hb_log2), 0, nullptr, nullptr};
-        pf_unit<2, kSwa, kHeadDim, true>(p, smem, qb, hg, kvh, b, seg);
+        pf_unit<2, kSwa, kDk, true>(p, smem, qb, hg, kvh, b, seg);
     }
 }
 
@@ -1259,9 +1268,9 @@ int64_t wide_pairs(const fgqa_prefill_args* a) {
 
 // The kernel shape a validated call runs on a device with `cus` CUs: the
 // caller's `kernel`, or for AUTO the choice by grid size:
-//  - wide: causal, head dim 128, no window or sink, and the wide kernel's
-//    unit pairs fill the CUs (two workgroups per pair, within 1/8 of one per
-//    CU).  Forced, it also runs the window / sink form (at the reference's
+//  - wide: causal, no window or sink, and the wide kernel's unit pairs fill
+//    the CUs (two workgroups per pair, within 1/8 of one per CU; the MLA
+//    shape 83.9 -> 82.4 us).  Forced, it also runs the window / sink form (at the reference's
 //    window of 512 in 27.5 us, against 26.1 us for the whole-range kernel);
 //  - split: fewer than 4 of the 128-row units per CU, no window or sink: each
 //    unit's KV range runs on two wave groups, so a CU never runs a long unit
@@ -1281,7 +1290,7 @@ int prefill_choice(const fgqa_prefill_args* a, int cus) {
     const int64_t units = ceil_div(a->seqlen_q, 128 / hb) * (int64_t)(group / hb) * a->num_kv_heads * a->batch;
     const int64_t pairs = wide_pairs(a);
     const int64_t wide_grid = 16 * ceil_div(pairs, 8);
-    if (!mla && !swa && a->causal && pairs <= kPwMaxSplit && wide_grid <= cus && 8 * wide_grid >= 7 * (int64_t)cus)
+    if (!swa && a->causal && pairs <= kPwMaxSplit && wide_grid <= cus && 8 * wide_grid >= 7 * (int64_t)cus)
         return FGQA_KERNEL_WIDE;
     if (units < 4 * (int64_t)cus && !swa) return FGQA_KERNEL_SPLIT;
     if (!mla && !swa && a->causal) return FGQA_KERNEL_WIDE;   // whole wide units, persistent
@@ -1308,7 +1317,6 @@ int validate_prefill(const fgqa_prefill_args* a) {
     if (a->kernel < FGQA_KERNEL_AUTO || a->kernel > FGQA_KERNEL_WIDE) return FGQA_ERR_INVALID_ARGUMENT;
     // the window / sink variant has no split form; the wide kernel has head dim 128 only
     if (a->kernel == FGQA_KERNEL_SPLIT && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
-    if (a->kernel == FGQA_KERNEL_WIDE && a->head_dim != kHeadDim) return FGQA_ERR_UNSUPPORTED;
     const int64_t lim = (int64_t)1 << 31;
     if ((int64_t)(a->seqlen_q + 128) * a->q_stride[1] * 2 >= lim ||
         (int64_t)(a->seqlen_kv + 128) * a->k_stride[1] * 2 >= lim ||
@@ -1410,25 +1418,35 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
         const int64_t pairs = wide_pairs(a);
         if (pairs > kPwMaxSplit || 2 * pairs > cus) {
             // more pairs than one per two CUs: whole units on a persistent grid
-            const void* pfn = swa ? reinterpret_cast<const void*>(prefill_wide_persistent_kernel<true>)
-                                  : reinterpret_cast<const void*>(prefill_wide_persistent_kernel<false>);
-            if (const int e = set_kernel_smem_once(swa ? 8 : 7, pfn, kPwSmemBytes); e != FGQA_OK) return e;
+            // attribute slots 7, 8, 9: the persistent wide kernels (plain, window, MLA)
+            const int slot = mla ? 9 : swa ? 8 : 7;
+            const void* pfn = mla   ? reinterpret_cast<const void*>(prefill_wide_persistent_kernel<false, 192>)
+                              : swa ? reinterpret_cast<const void*>(prefill_wide_persistent_kernel<true, kHeadDim>)
+                                    : reinterpret_cast<const void*>(prefill_wide_persistent_kernel<false, kHeadDim>);
+            const int sm = pw_smem_bytes(a->head_dim);
+            if (const int e = set_kernel_smem_once(slot, pfn, sm); e != FGQA_OK) return e;
             const int64_t units_w = (int64_t)p.n_qblocks * p.n_streams;
             const dim3 grid((unsigned)(units_w < cus ? units_w : cus));
-            if (swa) hipLaunchKernelGGL(prefill_wide_persistent_kernel<true>, grid, dim3(2 * kPfThreads), kPwSmemBytes, s, p);
-            else hipLaunchKernelGGL(prefill_wide_persistent_kernel<false>, grid, dim3(2 * kPfThreads), kPwSmemBytes, s, p);
+            if (mla) hipLaunchKernelGGL((prefill_wide_persistent_kernel<false, 192>), grid, dim3(2 * kPfThreads), sm, s, p);
+            else if (swa) hipLaunchKernelGGL((prefill_wide_persistent_kernel<true, kHeadDim>), grid, dim3(2 * kPfThreads), sm, s, p);
+            else hipLaunchKernelGGL((prefill_wide_persistent_kernel<false, kHeadDim>), grid, dim3(2 * kPfThreads), sm, s, p);
             if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
             return FGQA_OK;
         }
         if (const int e = pw_scratch(&p.wide_part, &p.wide_ctr); e != FGQA_OK) return e;
         // attribute slots 5, 6: the wide kernels
-        const void* wfn = swa ? reinterpret_cast<const void*>(prefill_wide_kernel<true>)
-                              : reinterpret_cast<const void*>(prefill_wide_kernel<false>);
-        if (const int e = set_kernel_smem_once(swa ? 6 : 5, wfn, kPwSmemBytes); e != FGQA_OK) return e;
+        // attribute slots 5, 6, 18: the wide kernels (plain, window, MLA)
+        const int wslot = mla ? 18 : swa ? 6 : 5;
+        const void* wfn = mla   ? reinterpret_cast<const void*>(prefill_wide_kernel<false, 192>)
+                          : swa ? reinterpret_cast<const void*>(prefill_wide_kernel<true, kHeadDim>)
+                                : reinterpret_cast<const void*>(prefill_wide_kernel<false, kHeadDim>);
+        const int wsm = pw_smem_bytes(a->head_dim);
+        if (const int e = set_kernel_smem_once(wslot, wfn, wsm); e != FGQA_OK) return e;
         // blocks w and w + 8 of each 16 run one pair
         const dim3 grid((unsigned)(16 * ceil_div(wide_pairs(a), 8)));
-        if (swa) hipLaunchKernelGGL(prefill_wide_kernel<true>, grid, dim3(2 * kPfThreads), kPwSmemBytes, s, p);
-        else hipLaunchKernelGGL(prefill_wide_kernel<false>, grid, dim3(2 * kPfThreads), kPwSmemBytes, s, p);
+        if (mla) hipLaunchKernelGGL((prefill_wide_kernel<false, 192>), grid, dim3(2 * kPfThreads), wsm, s, p);
+        else if (swa) hipLaunchKernelGGL((prefill_wide_kernel<true, kHeadDim>), grid, dim3(2 * kPfThreads), wsm, s, p);
+        else hipLaunchKernelGGL((prefill_wide_kernel<false, kHeadDim>), grid, dim3(2 * kPfThreads), wsm, s, p);
         if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
         return FGQA_OK;
     }

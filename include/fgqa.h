@@ -42,7 +42,7 @@ enum fgqa_status {
  *   FGQA_KERNEL_WHOLE  one workgroup runs a 128-row unit over its whole KV range
  *   FGQA_KERNEL_SPLIT  two wave groups run the two halves of a unit's KV range
  *                      and merge (the choice for grids under 4 units per CU)
- *   FGQA_KERNEL_WIDE   (prefill forward, head dim 128) two wave groups
+ *   FGQA_KERNEL_WIDE   (prefill forward) two wave groups
  *                      share each K/V tile of a 256-row unit.  With at most
  *                      one unit pair per two CUs (and at most 128 pairs) a
  *                      unit's KV range may be split over two workgroups that

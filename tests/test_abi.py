@@ -168,7 +168,6 @@ def _prefill_args(**kw):
     (dict(kernel=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(kernel=_lib.FGQA_KERNEL_SPLIT, window=64), _lib.FGQA_ERR_UNSUPPORTED),   # no split SWA kernel
     (dict(kernel=_lib.FGQA_KERNEL_SPLIT, sink=4096), _lib.FGQA_ERR_UNSUPPORTED),
-    (dict(kernel=_lib.FGQA_KERNEL_WIDE, D=192, Dv=128), _lib.FGQA_ERR_UNSUPPORTED),   # no wide MLA kernel
     (dict(ostride=[256 * 16 * 128, 16 * 128 + 4, 128]), _lib.FGQA_ERR_UNSUPPORTED),  # O rows: 16-byte stores
     (dict(D=256), _lib.FGQA_ERR_UNSUPPORTED),
     (dict(v=None), _lib.FGQA_ERR_INVALID_ARGUMENT),

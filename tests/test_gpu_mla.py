@@ -42,9 +42,11 @@ def _inputs(seed, B, Sq, Skv, Hq, Hkv, uniform=False):
     return q, k, v
 
 
-@pytest.mark.parametrize("split", ["whole", "split"])
+@pytest.mark.parametrize("split", ["whole", "split", "wide"])
 @pytest.mark.parametrize("B,Sq,Skv,Hq,Hkv,causal", [
     (1, 256, 256, 2, 2, True),     # G = 1, the reference's MLA head layout
+    (1, 1500, 1500, 4, 4, True),   # G = 1, wide units of 256 positions, split pairs
+    (8, 600, 600, 16, 16, True),   # more unit pairs than one per two CUs: whole wide units, persistent
     (2, 300, 300, 4, 1, True),     # ragged tail, G = 4
     (1, 257, 257, 16, 1, True),    # G = 16
     (1, 200, 330, 2, 1, False),    # non-causal, Sq != Skv
@@ -76,14 +78,14 @@ def test_mla_reference_inputs_and_negative_scale(cuda):
 
 def test_mla_reference_shape_full_size(cuda):
     """The reference's MLA benchmark shape (B=1, S=4096, Hq=Hkv=16, Dqk=192, Dv=128,
-    causal), N(0,1) inputs: sampled row blocks against the oracle, both kernels."""
+    causal), N(0,1) inputs: sampled row blocks against the oracle, every kernel."""
     import torch
     fg = _fg()
     B, S, Hq, Hkv = 1, 4096, 16, 16
     q = gpu_normal_bf16((B, S, Hq, DQK), 71, 1.0, cuda)
     k = gpu_normal_bf16((B, S, Hkv, DQK), 72, 1.0, cuda)
     v = gpu_normal_bf16((B, S, Hkv, DV), 73, 1.0, cuda)
-    for split in ("whole", "split"):
+    for split in ("whole", "split", "wide"):
         print(f"mla full size kernel={split}", flush=True)
         out, lse = fg.flash_gqa_forward_bshd(q, k, v, SCALE, causal=True, kernel=split)
         torch.cuda.synchronize()
