@@ -1286,14 +1286,16 @@ int prefill_choice(const fgqa_prefill_args* a, int cus) {
     const int group = a->num_q_heads / a->num_kv_heads;
     const int hb = group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
     const bool swa = a->window_size > 0 || a->sink != nullptr;
-    const bool mla = a->head_dim == 192;
     const int64_t units = ceil_div(a->seqlen_q, 128 / hb) * (int64_t)(group / hb) * a->num_kv_heads * a->batch;
     const int64_t pairs = wide_pairs(a);
     const int64_t wide_grid = 16 * ceil_div(pairs, 8);
     if (!swa && a->causal && pairs <= kPwMaxSplit && wide_grid <= cus && 8 * wide_grid >= 7 * (int64_t)cus)
         return FGQA_KERNEL_WIDE;
+    // causal, no window: the persistent wide kernel from 2 units per CU on (measured on
+    // head dims 128 and 192 from 512 to 16384 units: 3-14 % ahead of split and whole);
+    // below that the split kernel's shorter ranges fill the chip better
+    if (!swa && a->causal) return units < 2 * (int64_t)cus ? FGQA_KERNEL_SPLIT : FGQA_KERNEL_WIDE;
     if (units < 4 * (int64_t)cus && !swa) return FGQA_KERNEL_SPLIT;
-    if (!mla && !swa && a->causal) return FGQA_KERNEL_WIDE;   // whole wide units, persistent
     return FGQA_KERNEL_WHOLE;
 }
 
@@ -1315,7 +1317,7 @@ int validate_prefill(const fgqa_prefill_args* a) {
     if (dv != kHeadDim || (a->head_dim != kHeadDim && a->head_dim != 192)) return FGQA_ERR_UNSUPPORTED;
     if (a->head_dim == 192 && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
     if (a->kernel < FGQA_KERNEL_AUTO || a->kernel > FGQA_KERNEL_WIDE) return FGQA_ERR_INVALID_ARGUMENT;
-    // the window / sink variant has no split form; the wide kernel has head dim 128 only
+    // the window / sink variant has no split form
     if (a->kernel == FGQA_KERNEL_SPLIT && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
     const int64_t lim = (int64_t)1 << 31;
     if ((int64_t)(a->seqlen_q + 128) * a->q_stride[1] * 2 >= lim ||

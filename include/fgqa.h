@@ -41,7 +41,8 @@ enum fgqa_status {
  * for tuning and tests.  Callers that zero the argument struct get AUTO.
  *   FGQA_KERNEL_WHOLE  one workgroup runs a 128-row unit over its whole KV range
  *   FGQA_KERNEL_SPLIT  two wave groups run the two halves of a unit's KV range
- *                      and merge (the choice for grids under 4 units per CU)
+ *                      and merge (the choice for causal grids under 2 units
+ *                      per CU and non-causal grids under 4)
  *   FGQA_KERNEL_WIDE   (prefill forward) two wave groups
  *                      share each K/V tile of a 256-row unit.  With at most
  *                      one unit pair per two CUs (and at most 128 pairs) a
@@ -49,6 +50,8 @@ enum fgqa_status {
  *                      merge through device memory the library holds (calls
  *                      that overlap on one device must not both use it);
  *                      larger grids run whole units on a persistent grid
+ *                      (AUTO's choice for causal grids without a window or
+ *                      sink from 2 units per CU)
  */
 enum fgqa_kernel_choice { FGQA_KERNEL_AUTO = 0, FGQA_KERNEL_WHOLE = 1, FGQA_KERNEL_SPLIT = 2, FGQA_KERNEL_WIDE = 3 };
 

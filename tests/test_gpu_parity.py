@@ -402,22 +402,31 @@ def test_prefill_config4_full_size(cuda):
 
 def test_prefill_auto_kernel_choice(cuda):
     """What AUTO resolves to on this device: the wide kernel at BASELINE
-    config 4 (its 128 unit pairs fill the 256 CUs) and at config 5 (whole
-    units, persistent), the split kernel for a small grid, the whole-range
-    kernel with a sliding window and for the MLA head dims."""
+    config 4 (its 128 unit pairs fill the 256 CUs), at config 5 and at other
+    causal grids of 2 or more 128-row units per CU (whole units, persistent),
+    for both head-dim shapes; the split kernel for a small grid and for a
+    non-causal grid below 4 units per CU; the whole-range kernel with a
+    sliding window and for large non-causal grids."""
     import torch
     fg = _fg()
     cus = torch.cuda.get_device_properties(cuda).multi_processor_count
 
-    def choice(B, S, Hq, Hkv, **kw):
-        q = torch.empty((B, S, Hq, 128), dtype=torch.bfloat16, device=cuda)
-        k = torch.empty((B, S, Hkv, 128), dtype=torch.bfloat16, device=cuda)
-        return fg.prefill_kernel_choice(q, k, k, **kw)
+    def choice(B, S, Hq, Hkv, dk=128, **kw):
+        q = torch.empty((B, S, Hq, dk), dtype=torch.bfloat16, device=cuda)
+        k = torch.empty((B, S, Hkv, dk), dtype=torch.bfloat16, device=cuda)
+        v = torch.empty((B, S, Hkv, 128), dtype=torch.bfloat16, device=cuda)
+        return fg.prefill_kernel_choice(q, k, v, **kw)
 
     if cus == 256:
         assert choice(1, 4096, 16, 1) == "wide"
+        assert choice(1, 4096, 16, 16, dk=192) == "wide"
+        assert choice(8, 1024, 32, 8) == "wide"          # 2048 units
+        assert choice(2, 1024, 16, 4) == "split"         # 256 units
     assert choice(1, 1024, 16, 1) == "split"
     assert choice(4, 16384, 32, 8) == "wide"
+    assert choice(4, 8192, 16, 16, dk=192) == "wide"
+    assert choice(1, 1024, 16, 16, dk=192) == "split"
+    assert choice(4, 16384, 32, 8, causal=False) == "whole"
     assert choice(1, 4096, 16, 1, window_size=128) == "whole"
     assert choice(1, 4096, 16, 1, kernel="split") == "split"
 
