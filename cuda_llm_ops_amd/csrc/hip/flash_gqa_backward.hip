@@ -523,20 +523,14 @@ __global__ __launch_bounds__(256) void bwd_dkdv_reduce_kernel(BwdParams p) {
 // ---------------------------------------------------------------- dQ
 // Unit = 128 query rows: hb heads of one KV group x (128 / hb) positions,
 // wave w -> head (w % hb), positions 32 * (w / hb) .. +31 of the unit, as the
-// forward kernel.  With kGroups == 2 two groups of 4 waves take the two halves
-// of the unit's key range and add their dQ through LDS at the end (dQ is a
-// plain sum over keys: P comes from the final LSE).
-template <int kGroups, bool kSwa, int kDk>
-__device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem_all, int qb, int hg, int kvh,
-                                        int b) {
+// forward kernel; the whole key range of the unit (the split form,
+// dq_unit_pp below, gives each half of it to a group of its own).
+template <bool kSwa, int kDk>
+__device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem, int qb, int hg, int kvh, int b) {
     using D = BwDims<kDk>;
-    static_assert(kGroups == 1 || kDk == 128, "the split dQ kernel is 128-wide only");
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
-    const int wave_wg = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const int grp = wave_wg / kBwWaves;
-    const int wave = wave_wg % kBwWaves;
-    unsigned char* smem = smem_all + grp * kDqSmemBytes;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int l32 = lane & 31;
     const int l16 = lane & 15;
     const int g2 = lane >> 5;
@@ -573,9 +567,9 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem_
     // a window starts the unit at the tile holding its first row's first key
     const int t_lo = kSwa ? max(0, q_wg0 - p.window + 1) / kDqTile : 0;
     const int unit_tiles = max(0, (kv_end + kDqTile - 1) / kDqTile - t_lo);
-    const int n_tiles = kGroups == 1 ? unit_tiles : (unit_tiles + 1) / 2;   // same for both groups
-    const int t_first = t_lo + grp * n_tiles;
-    // keys this lane's row may use: below kv_hi (end of the group's range) and,
+    const int n_tiles = unit_tiles;
+    const int t_first = t_lo;
+    // keys this lane's row may use: below kv_hi (end of the unit's range) and,
     // under the causal mask, at most qrow
     const int kv_hi = min(kv_end, (t_first + n_tiles) * kDqTile);
     const int row_lim = (qrow >= p.sq) ? 0 : min(kv_hi, p.causal ? qrow + 1 : p.skv);
@@ -712,7 +706,7 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem_
     // and reads a buffer that holds zeros or the previous tile.
     {
         const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-        for (int off = (tid % kBwThreads) * 16; off < dq_smem_bytes<kDk>(); off += kBwThreads * 16)
+        for (int off = tid * 16; off < dq_smem_bytes<kDk>(); off += kBwThreads * 16)
             *reinterpret_cast<f32x4_t*>(smem + off) = z;
     }
     __syncthreads();
@@ -733,29 +727,272 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem_
         __syncthreads();
     }
 
-    if constexpr (kGroups == 2) {
-        // group 1 hands its dQ^T to group 0 through the (idle) tile buffers:
-        // [wave][value][lane] floats
-        float* mg = reinterpret_cast<float*>(smem_all) + wave * 64 * kWave + lane;
-        if (grp == 1) {
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) mg[(db * 16 + i) * kWave] = dq_acc[db][i];
-        }
-        __syncthreads();
-        if (grp == 1) return;
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) dq_acc[db][i] += mg[(db * 16 + i) * kWave];
-    }
-
     // dQ^T: lane (q = l32, half g2), block db register i <-> d = 32db + 8(i/4) + 4g2 + i%4
     if (qrow < p.sq) {
         __bf16* dst = p.dq + b * p.dq_sb + (int64_t)qrow * p.dq_ss + h * p.dq_sh;
 #pragma unroll
         for (int db = 0; db < D::kDb; ++db)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                bf16x4_t w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w[e] = (__bf16)dq_acc[db][i4 * 4 + e];
+                *reinterpret_cast<bf16x4_t*>(dst + db * 32 + i4 * 8 + g2 * 4) = w;
+            }
+    }
+}
+
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void bw_static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        bw_static_for<N, I + 1>(f);
+    }
+}
+
+// Split dQ unit, ping-pong (head dim 128): dq_unit's unit, with the two halves
+// of its key range on two groups of 4 waves that add their dQ through LDS at
+// the end (dQ is a plain sum over keys: P comes from the final LSE).  The two waves of a SIMD (one per group)
+// alternate an MFMA phase (dQ^T += K(j)^T dS^T(j), then S^T(j+1) = K(j+1) Q^T
+// and dP^T(j+1) = V(j+1) dO^T: 48 MFMAs with their LDS reads) and a VALU phase
+// (dS^T(j+1) from S^T, dP^T; then the tile loads for the MFMA phase after
+// next), group 1 one phase behind group 0, with a workgroup barrier between
+// phases.  Each group has its own tiles: K(j) in buffer j % 3 (an MFMA phase
+// reads K(j) and K(j+1)), V(j) in buffer j % 2.
+constexpr int kDqPpGroupBytes = 5 * kDqTileBytes;       // K[3] | V[2]: 80 KB
+constexpr int kDqPpSmemBytes = 2 * kDqPpGroupBytes;     // 160 KB
+constexpr int kRing = 3;                                 // operands read ahead (4: no faster)
+
+template <bool kSwa>
+__device__ __forceinline__ void dq_unit_pp(const BwdParams& p, unsigned char* smem_all, int qb, int hg, int kvh,
+                                           int b) {
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave_wg = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int grp = wave_wg / kBwWaves;
+    const int wave = wave_wg % kBwWaves;
+    unsigned char* smem = smem_all + grp * kDqPpGroupBytes;
+    const int l32 = lane & 31;
+    const int l16 = lane & 15;
+    const int g2 = lane >> 5;
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)smem;
+
+    const int qrows = 128 / p.hb;
+    const int q_wg0 = qb * qrows;
+    const int h = kvh * p.group + hg * p.hb + (wave % p.hb);
+    const int q0w = q_wg0 + (wave / p.hb) * 32;
+    const int qrow = q0w + l32;
+
+    const uint32_t qss = (uint32_t)(p.q_ss * 2);
+    const uint32_t dss = (uint32_t)(p.do_ss * 2);
+    const __amdgpu_buffer_rsrc_t qrs = make_rsrc(p.q + b * p.q_sb + h * p.q_sh, (uint32_t)(p.sq - 1) * qss + kBwRowBytes);
+    const __amdgpu_buffer_rsrc_t drs =
+        make_rsrc(p.dout + b * p.do_sb + h * p.do_sh, (uint32_t)(p.sq - 1) * dss + kBwRowBytes);
+    bf16x8_t qop[8], doop[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+        qop[kk] = as_bf16x8(buf_load16(qrs, (uint32_t)qrow * qss + (16 * kk + 8 * g2) * 2));
+        doop[kk] = as_bf16x8(buf_load16(drs, (uint32_t)qrow * dss + (16 * kk + 8 * g2) * 2));
+    }
+    const int64_t rows_q = (int64_t)p.batch * p.hq * p.sq;
+    const int64_t ridx = ((int64_t)b * p.hq + h) * p.sq + qrow;
+    const float nl = (qrow < p.sq) ? p.rowstat[ridx] : 0.f;
+    const float nd = (qrow < p.sq) ? p.rowstat[rows_q + ridx] : 0.f;
+
+    int kv_end = p.skv;
+    if (p.causal) kv_end = min(kv_end, min(q_wg0 + qrows, p.sq));
+    const int t_lo = kSwa ? max(0, q_wg0 - p.window + 1) / kDqTile : 0;
+    const int unit_tiles = max(0, (kv_end + kDqTile - 1) / kDqTile - t_lo);
+    const int n_tiles = (unit_tiles + 1) / 2;   // the same for both groups
+    const int t_first = t_lo + grp * n_tiles;
+    const int kv_hi = min(kv_end, (t_first + n_tiles) * kDqTile);
+    const int row_lim = (qrow >= p.sq) ? 0 : min(kv_hi, p.causal ? qrow + 1 : p.skv);
+
+    const uint32_t kss = (uint32_t)(p.k_ss * 2);
+    const uint32_t vss = (uint32_t)(p.v_ss * 2);
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, (uint32_t)(p.skv - 1) * kss + kBwRowBytes);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, (uint32_t)(p.skv - 1) * vss + kBwRowBytes);
+    // K(j) -> buffer j % 3, V(j) -> buffer 3 + j % 2; rows r = 4*(wave + 4i) + lane/16
+    // (8 load instructions per wave); keys >= skv read as zero
+    auto issue = [&](int j) {
+        const int t0 = (t_first + j) * kDqTile;
+        const uint32_t kb = lds_base + (uint32_t)(j % 3) * kDqTileBytes;
+        const uint32_t vb = lds_base + (uint32_t)(3 + (j & 1)) * kDqTileBytes;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r0 = 4 * (wave + 4 * i);
+            const int r = r0 + (lane >> 4);
+            const int slot = (l16 ^ bw_swz(r)) << 4;
+            bw_dma16(kb + r0 * kBwRowBytes, (uint32_t)(t0 + r) * kss + slot, krs);
+            bw_dma16(vb + r0 * kBwRowBytes, (uint32_t)(t0 + r) * vss + slot, vrs);
+        }
+    };
+
+    f32x16_t dq_acc[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dq_acc[db][i] = 0.f;
+    int trk[4][2];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+        trk[db][0] = bw_tr_off(lane, db, 0);
+        trk[db][1] = bw_tr_off(lane, db, 1);
+    }
+    int roff[8];
+    const int fl = bw_swz(l32);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) roff[kk] = l32 * kBwRowBytes + (((2 * kk + g2) ^ fl) << 4);
+    const float c2 = p.scale_log2;
+    const float scale = p.scale;
+
+    if (n_tiles > 0) {
+        f32x16_t s[2], dp[2];
+        bf16x8_t dsop[4];
+        // MFMA phase j: dQ(j) (when kDq) and S^T/dP^T(j+1) (when kSdp; j = -1
+        // computes tile 0's).  Operand i of the phase's stream: dQ operand
+        // (kb, db) = (i / 4, i % 4) for i < kQ, else S/dP operand r = i - kQ:
+        // k-step r / 4, 32-key block (r / 2) % 2, K (r even) or V.  Each is
+        // read kRing MFMAs ahead into a ring of kRing registers.
+        auto mphase = [&](auto with_dq, auto with_sdp, int j) {
+            constexpr bool kDq = decltype(with_dq)::value;
+            constexpr bool kSdp = decltype(with_sdp)::value;
+            constexpr int kQ = kDq ? 16 : 0;
+            constexpr int kOps = kQ + (kSdp ? 32 : 0);
+            // buffer offsets as opaque scalars: each per-lane offset then takes
+            // one add per phase, the rest are instruction immediates
+            uint32_t kco = (uint32_t)(kDq ? j % 3 : 0) * kDqTileBytes;
+            uint32_t kno = (uint32_t)(kSdp ? (j + 1) % 3 : 0) * kDqTileBytes;
+            uint32_t vno = (uint32_t)(3 + (kSdp ? (j + 1) & 1 : 0)) * kDqTileBytes;
+            asm volatile("" : "+s"(kco), "+s"(kno), "+s"(vno));
+            const unsigned char* kc = smem + kco;
+            const unsigned char* kn = smem + kno;
+            const unsigned char* vn = smem + vno;
+            auto fetch = [&](auto ic) -> bf16x8_t {
+                constexpr int i = decltype(ic)::value;
+                if constexpr (i < kQ) {
+                    constexpr int kb = i / 4, db = i % 4;
+                    return tr_pair(kc + 16 * kb * kBwRowBytes, trk[db][0], trk[db][1]);
+                } else {
+                    constexpr int r = i - kQ, kk = r / 4, tb = (r / 2) % 2;
+                    const unsigned char* base = (r % 2 == 0) ? kn : vn;
+                    return *reinterpret_cast<const bf16x8_t*>(base + tb * 32 * kBwRowBytes + roff[kk]);
+                }
+            };
+            bf16x8_t ring[kRing];
+            bw_static_for<kRing>([&](auto ic) {
+                if constexpr (decltype(ic)::value < kOps) ring[decltype(ic)::value] = fetch(ic);
+            });
+            if constexpr (kSdp) {
+#pragma unroll
+                for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) s[tb][i] = dp[tb][i] = 0.f;
+            }
+            bw_static_for<kOps>([&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                const bf16x8_t a = ring[i % kRing];
+                if constexpr (i < kQ) {
+                    dq_acc[i % 4] = mfma32(a, dsop[i / 4], dq_acc[i % 4]);
+                } else {
+                    constexpr int r = i - kQ, kk = r / 4, tb = (r / 2) % 2;
+                    if constexpr (r % 2 == 0) s[tb] = mfma32(a, qop[kk], s[tb]);
+                    else dp[tb] = mfma32(a, doop[kk], dp[tb]);
+                }
+                if constexpr (i + kRing < kOps) ring[i % kRing] = fetch(std::integral_constant<int, i + kRing>{});
+            });
+            // DS reads: 2 per dQ operand, 1 per S/dP operand, kRing operands ahead
+            if constexpr (kQ > 0) __builtin_amdgcn_sched_group_barrier(0x100, 2 * kRing, 0);
+            else __builtin_amdgcn_sched_group_barrier(0x100, kRing, 0);
+#pragma unroll
+            for (int i = 0; i < kOps; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                if (i + kRing < kQ) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                else if (i + kRing < kOps) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+        };
+        // VALU phase after MFMA phase j: dS^T(j+1) as the B operand of
+        // dQ^T += K^T dS^T (block kb = 2tb + kh holds registers 8kh .. 8kh+7
+        // of S^T block tb); K(j+3), V(j+3) go into the buffers MFMA phase j
+        // has finished with, and the loads of the previous VALU phase are
+        // awaited at the end.
+        auto vphase = [&](int j) {
+            __builtin_amdgcn_s_setprio(1);
+            const bool more = j + 3 < n_tiles;
+            if (more) issue(j + 3);
+            const int t0 = (t_first + j + 1) * kDqTile;
+            const int m = row_lim - t0 - 4 * g2;
+            [[maybe_unused]] const int lo = qrow - p.window + 1 - t0 - 4 * g2;
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int i = kh * 8 + e;
+                        float pv = fast_exp2(__builtin_fmaf(s[tb][i], c2, nl));
+                        const int idx = 32 * tb + 8 * (i >> 2) + (i & 3);
+                        if constexpr (kSwa)
+                            pv = (idx < m && idx >= lo) ? pv : 0.f;
+                        else
+                            pv = (idx < m) ? pv : 0.f;
+                        dsop[tb * 2 + kh][e] = (__bf16)(pv * __builtin_fmaf(dp[tb][i], scale, nd));
+                    }
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) asm volatile("" : "+v"(dsop[kb]));
+            if (more) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_setprio(0);
+            __syncthreads();
+        };
+
+        // tiles 0 and 1 first; tile 0 is awaited now, tile 1 by the end of
+        // the first VALU phase (vphase(-1) issues tile 2)
+        issue(0);
+        if (n_tiles > 1) {
+            issue(1);
+            asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        } else {
+            bw_wait_vmem();
+        }
+        __syncthreads();
+        // Both groups pass the same number of barriers: group 1 computes
+        // S/dP(0) in an extra leading phase, group 0 ends with an empty one.
+        if (grp == 0) mphase(std::false_type{}, std::true_type{}, -1);
+        else __syncthreads();
+        if (grp == 1) mphase(std::false_type{}, std::true_type{}, -1);
+        vphase(-1);
+        for (int j = 0; j + 1 < n_tiles; ++j) {
+            mphase(std::true_type{}, std::true_type{}, j);
+            vphase(j);
+        }
+        mphase(std::true_type{}, std::false_type{}, n_tiles - 1);
+        if (grp == 0) __syncthreads();
+    }
+
+    // group 1 hands its dQ^T to group 0 through group 0's (idle) tile
+    // buffers: [wave][value][lane] floats
+    float* mg = reinterpret_cast<float*>(smem_all) + wave * 64 * kWave + lane;
+    if (grp == 1) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mg[(db * 16 + i) * kWave] = dq_acc[db][i];
+    }
+    __syncthreads();
+    if (grp == 1) return;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dq_acc[db][i] += mg[(db * 16 + i) * kWave];
+
+    // dQ^T: lane (q = l32, half g2), block db register i <-> d = 32db + 8(i/4) + 4g2 + i%4
+    if (qrow < p.sq) {
+        __bf16* dst = p.dq + b * p.dq_sb + (int64_t)qrow * p.dq_ss + h * p.dq_sh;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
 #pragma unroll
             for (int i4 = 0; i4 < 4; ++i4) {
                 bf16x4_t w;
@@ -785,7 +1022,7 @@ __global__ __launch_bounds__(kBwThreads, kDk == 128 ? 2 : 1) void bwd_dq_kernel(
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     int qb, hg, kvh, b;
     dq_block_unit(p, &qb, &hg, &kvh, &b);
-    dq_unit<1, kSwa, kDk>(p, smem, qb, hg, kvh, b);
+    dq_unit<kSwa, kDk>(p, smem, qb, hg, kvh, b);
 }
 
 template <bool kSwa>
@@ -793,7 +1030,7 @@ __global__ __launch_bounds__(2 * kBwThreads, 1) void bwd_dq_split_kernel(BwdPara
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     int qb, hg, kvh, b;
     dq_block_unit(p, &qb, &hg, &kvh, &b);
-    dq_unit<2, kSwa, 128>(p, smem, qb, hg, kvh, b);
+    dq_unit_pp<kSwa>(p, smem, qb, hg, kvh, b);
 }
 
 namespace {
@@ -1016,7 +1253,7 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     } else {
         if ((st = set_kernel_smem_once(10 + swa, kv_fn[swa], kKvSmemBytes)) != FGQA_OK) return st;
         if ((st = set_kernel_smem_once(12 + swa, q_fn[swa], kDqSmemBytes)) != FGQA_OK) return st;
-        if ((st = set_kernel_smem_once(14 + swa, q2_fn[swa], 2 * kDqSmemBytes)) != FGQA_OK) return st;
+        if ((st = set_kernel_smem_once(14 + swa, q2_fn[swa], kDqPpSmemBytes)) != FGQA_OK) return st;
     }
 
     if (rows_q > 0) hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)ceil_div(rows_q, 16)), dim3(256), 0, s, p);
@@ -1044,10 +1281,10 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     if (q_units > 0 && dq_split) {
         if (swa)
             hipLaunchKernelGGL(bwd_dq_split_kernel<true>, dim3((unsigned)q_units), dim3(2 * kBwThreads),
-                               2 * kDqSmemBytes, s, p);
+                               kDqPpSmemBytes, s, p);
         else
             hipLaunchKernelGGL(bwd_dq_split_kernel<false>, dim3((unsigned)q_units), dim3(2 * kBwThreads),
-                               2 * kDqSmemBytes, s, p);
+                               kDqPpSmemBytes, s, p);
     } else if (q_units > 0) {
         if (swa)
             hipLaunchKernelGGL((bwd_dq_kernel<true, 128>), dim3((unsigned)q_units), dim3(kBwThreads), kDqSmemBytes, s,
