@@ -89,6 +89,7 @@ constexpr int kBwRowBytes = kHeadDim * 2;             // one Q / dO / K / V row
 constexpr int kBwHiRowBytes = 128;                    // dims 128..191 of a 192-wide Q / K row
 
 // ---- key-major kernel
+constexpr int kKvRing = 4;                            // operands read ahead in a step
 constexpr int kKvKeys = 128;                          // keys per workgroup
 constexpr int kKvRows = 32;                           // query rows per step
 constexpr int kKvTileBytes = kKvRows * kBwRowBytes;   // 8 KB: Q or dO of one step
@@ -176,6 +177,14 @@ __device__ __forceinline__ bf16x8_t tr_pair(const unsigned char* base, int off0,
     const bf16x4_t lo = lds_read_tr16(reinterpret_cast<const __bf16*>(base + off0));
     const bf16x4_t hi = lds_read_tr16(reinterpret_cast<const __bf16*>(base + off1));
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void bw_static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        bw_static_for<N, I + 1>(f);
+    }
 }
 
 // ---------------------------------------------------------------- prep
@@ -381,29 +390,6 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
             }
         }
     };
-    // dV += P^T dO, dK += dS^T Q: C[key][d], 4 column tiles of D; k-step ks
-    // takes query rows 16ks + 4g2 + 0..3 and 16ks + 8 + 4g2 + 0..3, read
-    // transposed from the tiles.
-    auto dkdv = [&](auto bi_c) {
-        constexpr int bi = decltype(bi_c)::value;
-        const unsigned char* ql = smem + kKvQOff + bi * kKvTileBytes;
-        const unsigned char* dl = smem + kKvDoOff + bi * kKvTileBytes;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const int rb = ks * 16 * kBwRowBytes;
-                dv_acc[db] = mfma32(pop[ks], tr_pair(dl + rb, trq[db][0], trq[db][1]), dv_acc[db]);
-                dk_acc[db] = mfma32(dsop[ks], tr_pair(ql + rb, trq[db][0], trq[db][1]), dk_acc[db]);
-            }
-            if constexpr (D::kHi) {
-                const unsigned char* qh = smem + kKvQHiOff + bi * kKvQHiTileBytes + ks * 16 * kBwHiRowBytes;
-#pragma unroll
-                for (int cb = 0; cb < 2; ++cb)
-                    dk_acc[4 + cb] = mfma32(dsop[ks], tr_pair(qh, trq_hi[cb][0], trq_hi[cb][1]), dk_acc[4 + cb]);
-            }
-        }
-    };
 
     // Triple-buffered Q/dO: step t reads buffers t%3 (dV/dK) and (t+1)%3
     // (S/dP of the next step) while step t+2 lands in (t+2)%3, which step t-1
@@ -434,11 +420,65 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
         const int q0 = (qb0 + t % per_head) * kKvRows;
         const int m = (t < n_iter) ? (p.causal ? key - q0 - 4 * g2 : -64) : 64;
         const int mx = key + p.window - 1 - q0 - 4 * g2;
-        // phase A: S/dP(t+1) on the MFMA pipe while P/dS(t) run on the VALU
-        sdp(sn, dpn, bn);
+        // S/dP(t+1), then dV += P^T dO and dK += dS^T Q of step t (C[key][d],
+        // 4 column tiles of D; k-step ks takes query rows 16ks + 4g2 + 0..3
+        // and 16ks + 8 + 4g2 + 0..3, read transposed from the tiles), as one
+        // stream of operands read kKvRing MFMAs ahead into a ring of
+        // registers; P/dS(t) on the VALU between (the scheduler moves them up
+        // under the S/dP MFMAs).  Pinning the order with sched_group_barrier
+        // (reads kKvRing ahead, with or without the VALU spread over the S/dP
+        // MFMAs) was 5-17 % slower.
+        constexpr int BC = decltype(bc)::value, BN = decltype(bn)::value;
+        constexpr int kS = D::kHi ? 20 : 16;
+        constexpr int kOps = kS + (D::kHi ? 20 : 16);
+        constexpr int kR = kKvRing;
+        const unsigned char* qln = smem + kKvQOff + BN * kKvTileBytes;
+        const unsigned char* dln = smem + kKvDoOff + BN * kKvTileBytes;
+        const unsigned char* qlc = smem + kKvQOff + BC * kKvTileBytes;
+        const unsigned char* dlc = smem + kKvDoOff + BC * kKvTileBytes;
+        auto fetch = [&](auto ic) -> bf16x8_t {
+            constexpr int i = decltype(ic)::value;
+            if constexpr (i < 16) {
+                // S (i even) / dP (i odd) A operand, k-step i / 2
+                return *reinterpret_cast<const bf16x8_t*>((i % 2 == 0 ? qln : dln) + roff[i / 2]);
+            } else if constexpr (i < kS) {
+                const unsigned char* qh = smem + kKvQHiOff + BN * kKvQHiTileBytes;
+                return *reinterpret_cast<const bf16x8_t*>(qh + roff_hi[(i - 16) % 4]);
+            } else if constexpr (i < kS + 16) {
+                // dV (r even) / dK (r odd) B operand: k-step r / 8, column block (r / 2) % 4
+                constexpr int r = i - kS, ks = r / 8, db = (r / 2) % 4;
+                return tr_pair((r % 2 == 0 ? dlc : qlc) + ks * 16 * kBwRowBytes, trq[db % 4][0], trq[db % 4][1]);
+            } else {
+                constexpr int r = i - kS - 16, ks = r / 2, cb = r % 2;
+                const unsigned char* qh = smem + kKvQHiOff + BC * kKvQHiTileBytes + ks * 16 * kBwHiRowBytes;
+                return tr_pair(qh, trq_hi[cb % 2][0], trq_hi[cb % 2][1]);
+            }
+        };
+        bf16x8_t ring[kR];
+        bw_static_for<kR>([&](auto ic) { ring[decltype(ic)::value] = fetch(ic); });
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sn[i] = dpn[i] = 0.f;
+        auto op = [&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            const bf16x8_t a = ring[i % kR];
+            if constexpr (i < 16) {
+                if constexpr (i % 2 == 0) sn = mfma32(a, kop[i / 2], sn);
+                else dpn = mfma32(a, vop[i / 2], dpn);
+            } else if constexpr (i < kS) {
+                sn = mfma32(a, kop[8 + (i - 16) % 4], sn);
+            } else if constexpr (i < kS + 16) {
+                constexpr int r = i - kS, ks = r / 8, db = (r / 2) % 4;
+                if constexpr (r % 2 == 0) dv_acc[db] = mfma32(pop[ks], a, dv_acc[db]);
+                else dk_acc[db] = mfma32(dsop[ks], a, dk_acc[db]);
+            } else {
+                constexpr int r = i - kS - 16, ks = r / 2, cb = r % 2;
+                dk_acc[4 + cb % 2] = mfma32(dsop[ks], a, dk_acc[4 + cb % 2]);
+            }
+            if constexpr (i + kR < kOps) ring[i % kR] = fetch(std::integral_constant<int, i + kR>{});
+        };
+        bw_static_for<kS>(op);
         softmax(sc, dpc, bc, m, mx);
-        // phase B: dV/dK(t)
-        dkdv(bc);
+        bw_static_for<kOps - kS>([&](auto ic) { op(std::integral_constant<int, kS + decltype(ic)::value>{}); });
         bw_wait_vmem();
         __syncthreads();
     };
@@ -739,14 +779,6 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem,
                 for (int e = 0; e < 4; ++e) w[e] = (__bf16)dq_acc[db][i4 * 4 + e];
                 *reinterpret_cast<bf16x4_t*>(dst + db * 32 + i4 * 8 + g2 * 4) = w;
             }
-    }
-}
-
-template <int N, int I = 0, typename F>
-__device__ __forceinline__ void bw_static_for(F&& f) {
-    if constexpr (I < N) {
-        f(std::integral_constant<int, I>{});
-        bw_static_for<N, I + 1>(f);
     }
 }
 
