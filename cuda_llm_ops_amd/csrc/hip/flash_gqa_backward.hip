@@ -276,9 +276,17 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
     const __amdgpu_buffer_rsrc_t srs = make_rsrc(p.rowstat, (uint32_t)(2 * rows_q * 4));
     // Q, dO rows of step t (wave w fetches rows 8w..8w+7 of each) and their
     // statistics (wave 0) into buffer bi.  Rows >= sq read as zero.
-    auto issue = [&](int t, int bi) {
-        const int hh = h0 + t / per_head;
-        const int q0 = (qb0 + t % per_head) * kKvRows;
+    // Steps are loaded in order, so the (head, query block) of the next load
+    // advances by one per call (no division per step).
+    int ld_h = h0, ld_qb = qb0;
+    int cur_qb = qb0;   // query block of the step being computed
+    auto issue = [&](int bi) {
+        const int hh = ld_h;
+        const int q0 = ld_qb * kKvRows;
+        if (++ld_qb == qb_end) {
+            ld_qb = qb0;
+            ++ld_h;
+        }
         const __amdgpu_buffer_rsrc_t qrs =
             make_rsrc(p.q + b * p.q_sb + hh * p.q_sh, (uint32_t)(p.sq - 1) * qss + D::kRowBytes);
         const __amdgpu_buffer_rsrc_t drs =
@@ -405,8 +413,8 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
             *reinterpret_cast<f32x4_t*>(smem + off) = z;
     }
     __syncthreads();
-    if (n_iter > 0) issue(0, 0);
-    if (n_iter > 1) issue(1, 1);
+    if (n_iter > 0) issue(0);
+    if (n_iter > 1) issue(1);
     bw_wait_vmem();
     __syncthreads();
 
@@ -416,8 +424,10 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
     // step t: sc/dpc hold S/dP(t), sn/dpn receive S/dP(t+1); buffers BC = t%3,
     // BN = (t+1)%3, BF = (t+2)%3
     auto step = [&](f32x16_t& sc, f32x16_t& dpc, f32x16_t& sn, f32x16_t& dpn, int t, auto bc, auto bn, auto bf) {
-        if (t + 2 < n_iter) issue(t + 2, decltype(bf)::value);
-        const int q0 = (qb0 + t % per_head) * kKvRows;
+        if (t + 2 < n_iter) issue(decltype(bf)::value);
+        // query block of step t (advanced once per step, as the loads are)
+        const int q0 = cur_qb * kKvRows;
+        if (++cur_qb == qb_end) cur_qb = qb0;
         const int m = (t < n_iter) ? (p.causal ? key - q0 - 4 * g2 : -64) : 64;
         const int mx = key + p.window - 1 - q0 - 4 * g2;
         // S/dP(t+1), then dV += P^T dO and dK += dS^T Q of step t (C[key][d],
