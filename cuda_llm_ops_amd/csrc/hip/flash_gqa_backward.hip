@@ -694,33 +694,60 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem,
         constexpr int bi = decltype(bi_c)::value;
         const unsigned char* kl = smem + bi * kDqTileBytes;
         const unsigned char* vl = smem + (2 + bi) * kDqTileBytes;
-        // S^T = K Q^T, dP^T = V dO^T: C[key][q], lane (q = l32, half g2)
+        [[maybe_unused]] const unsigned char* khl = smem + kDqKHiOff + bi * kDqKHiTileBytes;
+        // S^T = K Q^T, dP^T = V dO^T (C[key][q], lane (q = l32, half g2)), then
+        // dQ^T += K^T dS^T, as one stream of operands read kR MFMAs ahead into
+        // a ring of registers, with dS^T on the VALU between the two parts.
+        // Operand i < 32: k-step i / 4, 32-key block (i / 2) % 2, K (i even) or
+        // V; then (192-wide) the K rows' 128-byte parts; then per 16-key block
+        // kb the transposed K operands of dQ^T's column blocks.
+        constexpr int kSd = 32 + (D::kHi ? 8 : 0);
+        constexpr int kPer = D::kHi ? 6 : 4;
+        constexpr int kOps = kSd + 4 * kPer;
+        constexpr int kR = D::kHi ? 4 : 3;
+        auto fetch = [&](auto ic) -> bf16x8_t {
+            constexpr int i = decltype(ic)::value;
+            if constexpr (i < 32) {
+                constexpr int kk = i / 4, tb = (i / 2) % 2;
+                return *reinterpret_cast<const bf16x8_t*>((i % 2 == 0 ? kl : vl) + tb * 32 * kBwRowBytes + roff[kk]);
+            } else if constexpr (i < kSd) {
+                constexpr int r = i - 32, kk = r / 2, tb = r % 2;
+                return *reinterpret_cast<const bf16x8_t*>(khl + tb * 32 * kBwHiRowBytes + roff_hi[kk % 4]);
+            } else {
+                constexpr int r = i - kSd, kb = r / kPer, c = r % kPer;
+                if constexpr (c < 4) return tr_pair(kl + 16 * kb * kBwRowBytes, trk[c][0], trk[c][1]);
+                else return tr_pair(khl + 16 * kb * kBwHiRowBytes, trk_hi[(c - 4) % 2][0], trk_hi[(c - 4) % 2][1]);
+            }
+        };
         f32x16_t s[2], dp[2];
+        bf16x8_t dsop[4];
+        bf16x8_t ring[kR];
+        bw_static_for<kR>([&](auto ic) { ring[decltype(ic)::value] = fetch(ic); });
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
             for (int i = 0; i < 16; ++i) s[tb][i] = dp[tb][i] = 0.f;
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk)
-#pragma unroll
-            for (int tb = 0; tb < 2; ++tb) {
-                const int off = tb * 32 * kBwRowBytes + roff[kk];
-                s[tb] = mfma32(*reinterpret_cast<const bf16x8_t*>(kl + off), qop[kk], s[tb]);
-                dp[tb] = mfma32(*reinterpret_cast<const bf16x8_t*>(vl + off), doop[kk], dp[tb]);
+        auto op = [&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            const bf16x8_t a = ring[i % kR];
+            if constexpr (i < 32) {
+                constexpr int kk = i / 4, tb = (i / 2) % 2;
+                if constexpr (i % 2 == 0) s[tb] = mfma32(a, qop[kk], s[tb]);
+                else dp[tb] = mfma32(a, doop[kk], dp[tb]);
+            } else if constexpr (i < kSd) {
+                constexpr int r = i - 32, kk = r / 2, tb = r % 2;
+                s[tb] = mfma32(a, qop[8 + kk % 4], s[tb]);
+            } else {
+                constexpr int r = i - kSd, kb = r / kPer, c = r % kPer;
+                if constexpr (c < 4) dq_acc[c] = mfma32(a, dsop[kb], dq_acc[c]);
+                else dq_acc[4 + (c - 4) % 2] = mfma32(a, dsop[kb], dq_acc[4 + (c - 4) % 2]);
             }
-        if constexpr (D::kHi) {
-            const unsigned char* kh = smem + kDqKHiOff + bi * kDqKHiTileBytes;
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-                for (int tb = 0; tb < 2; ++tb)
-                    s[tb] = mfma32(*reinterpret_cast<const bf16x8_t*>(kh + tb * 32 * kBwHiRowBytes + roff_hi[kk]),
-                                   qop[8 + kk], s[tb]);
-        }
+            if constexpr (i + kR < kOps) ring[i % kR] = fetch(std::integral_constant<int, i + kR>{});
+        };
+        bw_static_for<kSd>(op);
         // dS^T = P^T (dP^T - delta) scale as the B operand of dQ^T += K^T dS^T:
         // block kb = 2tb + kh holds registers 8kh .. 8kh+7 of S^T block tb,
         // i.e. keys 16kb + 4g2 + 0..3 and 16kb + 8 + 4g2 + 0..3.
-        bf16x8_t dsop[4];
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
@@ -736,19 +763,7 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem,
                         pv = (idx < m) ? pv : 0.f;
                     dsop[tb * 2 + kh][e] = (__bf16)(pv * __builtin_fmaf(dp[tb][i], scale, nd));
                 }
-        // dQ^T[d][q] += sum over keys of K^T[d][key] dS^T[key][q], 4 column tiles of D
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-                dq_acc[db] = mfma32(tr_pair(kl + 16 * kb * kBwRowBytes, trk[db][0], trk[db][1]), dsop[kb], dq_acc[db]);
-            if constexpr (D::kHi) {
-                const unsigned char* kh = smem + kDqKHiOff + bi * kDqKHiTileBytes + 16 * kb * kBwHiRowBytes;
-#pragma unroll
-                for (int cb = 0; cb < 2; ++cb)
-                    dq_acc[4 + cb] = mfma32(tr_pair(kh, trk_hi[cb][0], trk_hi[cb][1]), dsop[kb], dq_acc[4 + cb]);
-            }
-        }
+        bw_static_for<kOps - kSd>([&](auto ic) { op(std::integral_constant<int, kSd + decltype(ic)::value>{}); });
     };
 
     // Double-buffered K/V, two tiles per trip so that buffer offsets are
