@@ -89,7 +89,7 @@ constexpr int kBwRowBytes = kHeadDim * 2;             // one Q / dO / K / V row
 constexpr int kBwHiRowBytes = 128;                    // dims 128..191 of a 192-wide Q / K row
 
 // ---- key-major kernel
-constexpr int kKvRing = 4;                            // operands read ahead in a step
+constexpr int kKvRing = 6;                            // operands read ahead in a step
 constexpr int kKvKeys = 128;                          // keys per workgroup
 constexpr int kKvRows = 32;                           // query rows per step
 constexpr int kKvTileBytes = kKvRows * kBwRowBytes;   // 8 KB: Q or dO of one step
@@ -434,8 +434,10 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
         // 4 column tiles of D; k-step ks takes query rows 16ks + 4g2 + 0..3
         // and 16ks + 8 + 4g2 + 0..3, read transposed from the tiles), as one
         // stream of operands read kKvRing MFMAs ahead into a ring of
-        // registers; P/dS(t) on the VALU between (the scheduler moves them up
-        // under the S/dP MFMAs).  Pinning the order with sched_group_barrier
+        // registers (6 ahead: 0.4 % faster than 4 at the 4096-token, 16-head
+        // shape, 1.5 % with the MLA head dims); P/dS(t) on the VALU between
+        // (the scheduler moves them up under the S/dP MFMAs).  Pinning the
+        // order with sched_group_barrier
         // (reads kKvRing ahead, with or without the VALU spread over the S/dP
         // MFMAs) was 5-17 % slower.
         constexpr int BC = decltype(bc)::value, BN = decltype(bn)::value;
@@ -697,14 +699,15 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem,
         [[maybe_unused]] const unsigned char* khl = smem + kDqKHiOff + bi * kDqKHiTileBytes;
         // S^T = K Q^T, dP^T = V dO^T (C[key][q], lane (q = l32, half g2)), then
         // dQ^T += K^T dS^T, as one stream of operands read kR MFMAs ahead into
-        // a ring of registers, with dS^T on the VALU between the two parts.
+        // a ring of registers, with dS^T on the VALU between the two parts
+        // (6 ahead at head dim 192; 3 at 128, where a deeper ring spills).
         // Operand i < 32: k-step i / 4, 32-key block (i / 2) % 2, K (i even) or
         // V; then (192-wide) the K rows' 128-byte parts; then per 16-key block
         // kb the transposed K operands of dQ^T's column blocks.
         constexpr int kSd = 32 + (D::kHi ? 8 : 0);
         constexpr int kPer = D::kHi ? 6 : 4;
         constexpr int kOps = kSd + 4 * kPer;
-        constexpr int kR = D::kHi ? 4 : 3;
+        constexpr int kR = D::kHi ? 6 : 3;
         auto fetch = [&](auto ic) -> bf16x8_t {
             constexpr int i = decltype(ic)::value;
             if constexpr (i < 32) {
