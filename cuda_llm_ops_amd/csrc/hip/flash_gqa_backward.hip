@@ -81,6 +81,9 @@ struct BwdParams {
     int q_streams;    // n_hgroups * hkv * batch
     float scale;
     float scale_log2;   // scale * log2(e)
+    // prep: row -> (b, h, i) by magic-number division when B * Hq * Sq < 2^31
+    int prep_fast;
+    FastDiv div_sq, div_hq;
 };
 
 constexpr int kBwWaves = 4;
@@ -195,10 +198,19 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(BwdParams p) {
     const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
     const int part = threadIdx.x & 15;
     if (row >= rows_q) return;
-    const int i = (int)(row % p.sq);
-    const int64_t bh = row / p.sq;
-    const int h = (int)(bh % p.hq);
-    const int b = (int)(bh / p.hq);
+    int i, h, b;
+    if (p.prep_fast) {
+        const int r = (int)row;
+        const int bh = fast_div(r, p.div_sq);
+        i = r - bh * p.sq;
+        b = fast_div(bh, p.div_hq);
+        h = bh - b * p.hq;
+    } else {
+        i = (int)(row % p.sq);
+        const int64_t bh = row / p.sq;
+        h = (int)(bh % p.hq);
+        b = (int)(bh / p.hq);
+    }
     const u32x4_t ov = *reinterpret_cast<const u32x4_t*>(p.o + b * p.o_sb + i * p.o_ss + h * p.o_sh + part * 8);
     const u32x4_t dv = *reinterpret_cast<const u32x4_t*>(p.dout + b * p.do_sb + i * p.do_ss + h * p.do_sh + part * 8);
     const bf16x8_t o8 = as_bf16x8(ov), d8 = as_bf16x8(dv);
@@ -1269,6 +1281,9 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     p.hs = p.group / pl.n_hsplit;
     p.n_kvblocks = (int)ceil_div(p.skv, kKvKeys);
     p.kv_streams = pl.n_hsplit * p.hkv * p.batch;
+    p.prep_fast = (int64_t)p.batch * p.hq * p.sq < ((int64_t)1 << 31) ? 1 : 0;
+    p.div_sq = make_fast_div(p.sq > 0 ? p.sq : 1);
+    p.div_hq = make_fast_div(p.hq);
     p.n_qblocks32 = (int)ceil_div(p.sq, kKvRows);
     p.hb = (p.group % 4 == 0) ? 4 : (p.group % 2 == 0) ? 2 : 1;
     p.n_hgroups = p.group / p.hb;
