@@ -104,6 +104,19 @@ def test_backward_dq_whole_and_split_kernels(cuda, split, B, Sq, Skv, Hq, Hkv, c
     _check(_gpu_backward(cuda, q, k, v, o, lse, do, causal=causal, dq_kernel=split), refs, what)
 
 
+@pytest.mark.parametrize("Skv", [64, 128, 192, 320, 448, 704, 832])
+def test_backward_dq_split_tile_counts(cuda, Skv):
+    """The split dQ kernel's two groups cycle three K buffers and two V
+    buffers over their half of the key range: non-causal rows over 1 to 13
+    key tiles give each group 1 to 7 tiles (every position of the cycle,
+    and a second half that is partly or wholly past the keys)."""
+    what = f"dq split tile counts Skv={Skv}"
+    print(what, flush=True)
+    q, k, v, o, lse, do = _inputs(1700 + Skv, 1, 128, Skv, 4, 1, causal=False)
+    refs = oracle.prefill_backward(q, k, v, o, lse, do, SCALE, causal=False)
+    _check(_gpu_backward(cuda, q, k, v, o, lse, do, causal=False, dq_kernel="split"), refs, what)
+
+
 @pytest.mark.parametrize("scale", [0.2, -0.05])
 def test_backward_scale_values(cuda, scale):
     print(f"backward scale={scale}", flush=True)
