@@ -23,6 +23,7 @@ FGQA_KERNEL_AUTO = 0
 FGQA_KERNEL_WHOLE = 1
 FGQA_KERNEL_SPLIT = 2
 FGQA_KERNEL_WIDE = 3
+FGQA_KERNEL_TALL = 4
 
 _I64x2 = ctypes.c_int64 * 2
 _I64x3 = ctypes.c_int64 * 3

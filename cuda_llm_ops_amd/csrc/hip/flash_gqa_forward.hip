@@ -63,63 +63,14 @@
 
 #include "fgqa_device.h"
 #include "fgqa_internal.h"
+#include "prefill_common.h"
+#include "prefill_tall.h"
 
 
 namespace fgqa {
 
-struct PrefillParams {
-    const __bf16* q;
-    const __bf16* k;
-    const __bf16* v;
-    __bf16* o;
-    float* lse;
-    int64_t q_sb, q_ss, q_sh;
-    int64_t k_sb, k_ss, k_sh;
-    int64_t v_sb, v_ss, v_sh;
-    int64_t o_sb, o_ss, o_sh;
-    int batch, sq, skv, hq, hkv, group, causal;
-    int hb;          // heads per unit (1, 2 or 4; the wide kernel 1, 2, 4 or 8)
-    int hb_log2;     // log2(hb)
-    int n_hgroups;   // group / hb
-    int n_qblocks;   // ceil(sq / (128 / hb))
-    int n_streams;   // n_hgroups * hkv * batch
-    FastDiv div_streams, div_hgroups, div_hkv;   // by n_streams, n_hgroups, hkv
-    float scale_log2;   // |scale| * log2(e)
-    uint32_t q_sign;    // 0x80008000 when scale < 0 (Q is negated on load), else 0
-    int window;         // > 0: sliding window, row i sees keys [i - window + 1, i] (causal)
-    const float* sink;  // nullable [Hq]: added to the softmax denominator as sink * exp(-max)
-    // wide kernel: tiles a pair's heavy unit keeps beyond half the pair's
-    // tiles on its first workgroup, and the partial-result slots and arrival
-    // counters of split units (device scratch)
-    int wide_bias;
-    float* wide_part;
-    unsigned* wide_ctr;
-};
-
-// A segment of a wide unit: tiles [lo, hi) of its KV range.  part_own != null:
-// the unit's other tiles run on another workgroup; whichever of the two
-// finishes second merges both partial results (slot 0: the segment holding
-// the unit's first tiles, slot 1: the other).
-struct PfSeg {
-    int lo, hi;
-    int slot;          // this segment's slot (0 or 1)
-    float* part;       // the unit's two slots, kPfPartFloats each
-    unsigned* ctr;     // the unit's 4 words: arrival counter, XCD of each slot (0 between launches)
-};
-
-// f(integral_constant<int, 0>), ..., f(integral_constant<int, N-1>): an
-// unrolled loop whose index is a constant expression in the body.
-template <int N, int I = 0, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    if constexpr (I < N) {
-        f(std::integral_constant<int, I>{});
-        static_for<N, I + 1>(f);
-    }
-}
-
 constexpr int kPfWaves = 4;                            // waves per group (one unit's rows)
 constexpr int kPfThreads = kPfWaves * kWave;
-constexpr int kPfTile = 64;                            // KV tokens per tile
 constexpr int kPfVRowBytes = kHeadDim * 2;             // one V row (V/O head dim 128)
 constexpr int kPfVTileBytes = kPfTile * kPfVRowBytes;  // 16 KB
 constexpr float kPfRescaleSlack = 8.f;                 // log2 units: P <= 2^8 between rescales
@@ -141,9 +92,7 @@ constexpr int kPwSmemBytes = kPwTileBytes + kPwQBytes + 16;   // + 3 words that 
 // (a 256-row Q tile does not fit beside the 80 KB of tiles) and stages O in
 // the tile buffers, idle after the loop.
 constexpr int pw_smem_bytes(int dk) { return dk == kHeadDim ? kPwSmemBytes : 2 * (64 * 384) + 2 * kPfVTileBytes + 16; }
-constexpr int kPfPartFloats = 2 * kPfWaves * kPfMergeFloats * kWave;
-// most split units one launch may hold (two partial slots and a counter each)
-constexpr int kPwMaxSplit = 128;
+static_assert(kPfPartFloats == 2 * kPfWaves * kPfMergeFloats * kWave, "merge slot size");
 
 // Sizes that depend on the Q/K head dim kDk (128, or 192 for MLA).
 template <int kDk>
@@ -1073,43 +1022,12 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     }
 }
 
-// Rank -> unit.  Units are ranked heaviest first (the causal KV range grows
-// with the query block), so the dispatcher hands long units out before short
-// ones (and the persistent split kernel can pair long ranks with short).  The stream (head group, kv head, batch) is the fastest index: with a
-// multiple of 8 streams each stream's blocks share one XCD and its L2 (blocks
-// go round-robin over the 8 XCDs).
-__device__ __forceinline__ void pf_rank_unit(const PrefillParams& p, int r, int* qb, int* hg, int* kvh, int* b) {
-    const int rank_q = fast_div(r, p.div_streams);
-    const int stream = r - rank_q * p.n_streams;
-    *qb = p.causal ? p.n_qblocks - 1 - rank_q : rank_q;
-    const int t = fast_div(stream, p.div_hgroups);   // kv head + hkv * batch
-    *hg = stream - t * p.n_hgroups;
-    *b = fast_div(t, p.div_hkv);
-    *kvh = t - *b * p.hkv;
-}
-
 template <bool kSwa, int kDk>
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     int qb, hg, kvh, b;
     pf_rank_unit(p, blockIdx.x, &qb, &hg, &kvh, &b);
     pf_unit<1, kSwa, kDk>(p, smem, qb, hg, kvh, b);
-}
-
-// The kernel's parameters read again from the kernarg segment through a
-// pointer the compiler cannot see through, so that a loop over units keeps
-// none of them in scalar registers across a unit (they would be spilled and
-// reloaded one lane read at a time).
-__device__ __forceinline__ PrefillParams pf_params_reread(const PrefillParams& p) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    (void)p;
-    typedef const __attribute__((address_space(4))) PrefillParams* KernargParams;
-    KernargParams pp = (KernargParams)__builtin_amdgcn_kernarg_segment_ptr();
-    asm volatile("" : "+s"(pp));
-    return *pp;
-#else
-    return p;   // the host pass never runs device code
-#endif
 }
 
 // Persistent: gridDim.x = min(units, CUs) workgroups, one per CU.  Workgroup
@@ -1146,15 +1064,6 @@ __global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_split_kernel(Prefil
 // tiles beyond half the pair's tiles, which pays for the second's extra unit
 // start.  The heavy unit's two partial results merge through device memory
 // (pf_unit: whichever segment finishes second merges).
-// Tiles of a unit's KV range (a sliding window starts it at the tile that
-// holds its first row's first key).
-__device__ __forceinline__ int pf_unit_tiles(const PrefillParams& p, int qb, int qrows) {
-    int kv_end = p.skv;
-    if (p.causal) kv_end = min(kv_end, min((qb + 1) * qrows, p.sq));
-    const int t_lo = p.window > 0 ? max(0, qb * qrows - p.window + 1) / kPfTile : 0;
-    return max(0, (kv_end + kPfTile - 1) / kPfTile - t_lo);
-}
-
 template <bool kSwa, int kDk>
 __global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_wide_kernel(PrefillParams p0) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -1316,7 +1225,10 @@ int validate_prefill(const fgqa_prefill_args* a) {
     // (128, 128) and the MLA shape (192, 128); MLA has no window / sink form
     if (dv != kHeadDim || (a->head_dim != kHeadDim && a->head_dim != 192)) return FGQA_ERR_UNSUPPORTED;
     if (a->head_dim == 192 && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
-    if (a->kernel < FGQA_KERNEL_AUTO || a->kernel > FGQA_KERNEL_WIDE) return FGQA_ERR_INVALID_ARGUMENT;
+    if (a->kernel < FGQA_KERNEL_AUTO || a->kernel > FGQA_KERNEL_TALL) return FGQA_ERR_INVALID_ARGUMENT;
+    // the tall kernel: head dim 128, no window or sink
+    if (a->kernel == FGQA_KERNEL_TALL && (a->head_dim != kHeadDim || a->window_size > 0 || a->sink != nullptr))
+        return FGQA_ERR_UNSUPPORTED;
     // the window / sink variant has no split form
     if (a->kernel == FGQA_KERNEL_SPLIT && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
     const int64_t lim = (int64_t)1 << 31;
@@ -1406,7 +1318,7 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
     const bool mla = a->head_dim == 192;
     const bool split = choice == FGQA_KERNEL_SPLIT;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (choice == FGQA_KERNEL_WIDE) {
+    if (choice == FGQA_KERNEL_WIDE || choice == FGQA_KERNEL_TALL) {
         // 256-row units: up to 8 heads of a KV group
         const int hbw = (p.group % 8 == 0) ? 8 : p.hb;
         p.hb = hbw;
@@ -1418,6 +1330,15 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
         p.div_hgroups = make_fast_div(p.n_hgroups);
         p.wide_bias = 3;
         const int64_t pairs = wide_pairs(a);
+        if (choice == FGQA_KERNEL_TALL) {
+            // unit pairs on two workgroups each when they fit the merge slots
+            // and the CUs (causal grids: whole units differ in length),
+            // else whole units on a persistent grid
+            const bool use_pairs = a->causal && pairs <= kPwMaxSplit && 2 * pairs <= cus;
+            if (use_pairs)
+                if (const int e = pw_scratch(&p.wide_part, &p.wide_ctr); e != FGQA_OK) return e;
+            return launch_prefill_tall(p, use_pairs, cus, s);
+        }
         if (pairs > kPwMaxSplit || 2 * pairs > cus) {
             // more pairs than one per two CUs: whole units on a persistent grid
             // attribute slots 7, 8, 9: the persistent wide kernels (plain, window, MLA)

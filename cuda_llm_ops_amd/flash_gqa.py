@@ -340,7 +340,7 @@ def launch_decode_flash_gqa_bf16_kernel(q, k, v, out=None):
 def _kernel_choice(kernel) -> int:
     """'auto' / 'whole' / 'split' (or the FGQA_KERNEL_* value) -> the C ABI value."""
     names = {"auto": _lib.FGQA_KERNEL_AUTO, "whole": _lib.FGQA_KERNEL_WHOLE, "split": _lib.FGQA_KERNEL_SPLIT,
-             "wide": _lib.FGQA_KERNEL_WIDE}
+             "wide": _lib.FGQA_KERNEL_WIDE, "tall": _lib.FGQA_KERNEL_TALL}
     if isinstance(kernel, str):
         if kernel not in names:
             raise ValueError(f"kernel must be one of {sorted(names)}")
@@ -469,7 +469,8 @@ def prefill_kernel_choice(q, k, v, causal=True, window_size=0, sink=None, kernel
     st = _lib.lib().fgqa_prefill_kernel_choice(ctypes.byref(a), ctypes.byref(c))
     if st != _lib.FGQA_OK:
         raise _lib.FgqaError(st, "fgqa_prefill_kernel_choice")
-    return {_lib.FGQA_KERNEL_WHOLE: "whole", _lib.FGQA_KERNEL_SPLIT: "split", _lib.FGQA_KERNEL_WIDE: "wide"}[c.value]
+    return {_lib.FGQA_KERNEL_WHOLE: "whole", _lib.FGQA_KERNEL_SPLIT: "split", _lib.FGQA_KERNEL_WIDE: "wide",
+            _lib.FGQA_KERNEL_TALL: "tall"}[c.value]
 
 
 def launch_flash_gqa_forward_bf16_kernel(q, k, v, scale=None, out=None, lse=None, causal=True,

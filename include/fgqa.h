@@ -52,8 +52,19 @@ enum fgqa_status {
  *                      larger grids run whole units on a persistent grid
  *                      (AUTO's choice for causal grids without a window or
  *                      sink from 2 units per CU)
+ *   FGQA_KERNEL_TALL   (prefill forward, head_dim 128, no window or sink) the
+ *                      256-row units of FGQA_KERNEL_WIDE on four waves of 64
+ *                      rows each, one wave per SIMD, each K/V operand read
+ *                      from LDS feeding two MFMAs; the same unit pairs and
+ *                      merge scratch, or whole units on a persistent grid
  */
-enum fgqa_kernel_choice { FGQA_KERNEL_AUTO = 0, FGQA_KERNEL_WHOLE = 1, FGQA_KERNEL_SPLIT = 2, FGQA_KERNEL_WIDE = 3 };
+enum fgqa_kernel_choice {
+    FGQA_KERNEL_AUTO = 0,
+    FGQA_KERNEL_WHOLE = 1,
+    FGQA_KERNEL_SPLIT = 2,
+    FGQA_KERNEL_WIDE = 3,
+    FGQA_KERNEL_TALL = 4
+};
 
 /*
  * Single-token decode (flash-decoding: split-KV pass + log-sum-exp combine).

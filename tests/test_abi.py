@@ -164,8 +164,11 @@ def _prefill_args(**kw):
     (dict(Hq=15, Hkv=2), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(Sq=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(scale=float("inf")), _lib.FGQA_ERR_INVALID_ARGUMENT),
-    (dict(kernel=4), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(kernel=5), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(kernel=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
+    (dict(kernel=_lib.FGQA_KERNEL_TALL, window=64), _lib.FGQA_ERR_UNSUPPORTED),    # tall: no window / sink
+    (dict(kernel=_lib.FGQA_KERNEL_TALL, sink=4096), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(kernel=_lib.FGQA_KERNEL_TALL, D=192, Dv=128), _lib.FGQA_ERR_UNSUPPORTED),   # tall: head dim 128
     (dict(kernel=_lib.FGQA_KERNEL_SPLIT, window=64), _lib.FGQA_ERR_UNSUPPORTED),   # no split SWA kernel
     (dict(kernel=_lib.FGQA_KERNEL_SPLIT, sink=4096), _lib.FGQA_ERR_UNSUPPORTED),
     (dict(ostride=[256 * 16 * 128, 16 * 128 + 4, 128]), _lib.FGQA_ERR_UNSUPPORTED),  # O rows: 16-byte stores

@@ -245,7 +245,7 @@ def test_prefill_shapes(cuda, B, Sq, Skv, Hq, Hkv, causal):
     _check_prefill(o, lse, o_ref, lse_ref, f"prefill B{B} Sq{Sq} Skv{Skv} Hq{Hq} Hkv{Hkv} causal{causal}")
 
 
-@pytest.mark.parametrize("kernel", ["whole", "split", "wide"])
+@pytest.mark.parametrize("kernel", ["whole", "split", "wide", "tall"])
 @pytest.mark.parametrize("B,Sq,Skv,Hq,Hkv,causal", [
     (1, 256, 256, 16, 1, True),
     (2, 300, 300, 8, 2, True),      # odd tile counts per unit
@@ -265,15 +265,16 @@ def test_prefill_shapes(cuda, B, Sq, Skv, Hq, Hkv, causal):
 ])
 def test_prefill_whole_and_split_kernels(cuda, kernel, B, Sq, Skv, Hq, Hkv, causal):
     """The prefill kernels: one workgroup per unit over its whole KV range, the
-    split kernel (two wave groups on the halves of the range, merged), and the
+    split kernel (two wave groups on the halves of the range, merged), the
     wide kernel (two wave groups on one tile, a unit's range split over two
-    workgroups that merge through device memory)."""
+    workgroups that merge through device memory), and the tall kernel (the
+    wide kernel's units on four waves of 64 rows each)."""
     o, lse, o_ref, lse_ref = _prefill_case(cuda, 650 + Sq, B, Sq, Skv, Hq, Hkv, causal, kernel=kernel)
     _check_prefill(o, lse, o_ref, lse_ref,
                    f"kernel={kernel} B{B} Sq{Sq} Skv{Skv} Hq{Hq} Hkv{Hkv} causal{causal}")
 
 
-@pytest.mark.parametrize("kernel", ["whole", "split", "wide"])
+@pytest.mark.parametrize("kernel", ["whole", "split", "wide", "tall"])
 @pytest.mark.parametrize("case,scale", [("climb", 0.5), ("fall", 0.5), ("sharp", 2.0)])
 def test_prefill_running_max_moves(cuda, kernel, case, scale):
     """Score distributions that move the running max: keys scaled up along the
