@@ -146,8 +146,13 @@ def bench_decode(cfg_id, steps, warmup, split_tokens, dev):
     ms_step = total_ms / steps
     avg_launch_ms = total_ms / steps
     qo_bytes = 2 * cfg["B"] * cfg["Hq"] * 128 * 2
+    # no workspace: one split per (batch, KV head) stream, no combine pass
+    kernel = ("decode_split_kernel, one split per (batch, KV head), no combine" if n_ws == 0 else
+              "decode_list_kernel + decode_combine_kernel (device-built ragged work list, split-KV)"
+              if cfg["ragged"] else "decode_split_kernel + decode_combine_kernel (split-KV)")
     return dict(cfg=cfg, q=q, k=k, v=v, lens=lens, out=out, kv_bytes=kv_bytes, qo_bytes=qo_bytes,
-                ms_step=ms_step, avg_launch_ms=avg_launch_ms, median_ms=per[len(per) // 2], min_ms=per[0])
+                ms_step=ms_step, avg_launch_ms=avg_launch_ms, median_ms=per[len(per) // 2], min_ms=per[0],
+                kernel=kernel)
 
 
 def _host_u16(t):
@@ -234,6 +239,7 @@ def cpu_baseline_prefill(t, threads):
     flops = B * Hq * 2 * S * S * (128 + 128) // 2
     m, s, c = _err(_host_u16(t["out"]), ref)
     cpu = dict(value=round(flops / elapsed / 1e12, 5), unit="TFLOP/s", cores=threads, kind="port",
+               host_cores=_host_cores(),
                sample=f"the whole config 4 prefill (all {S} rows, {Hq} heads), {elapsed:.2f} s on {threads} "
                       f"OpenMP threads; FLOPs counted as on the GPU (causal-halved)")
     err = dict(max_abs=m, mean_abs=s / c, tol={"max_abs": 2e-2, "mean_abs": 2e-3},
@@ -254,17 +260,7 @@ def bench_prefill(cfg_id, steps, warmup, dev, keep=None):
     lse = torch.empty((B, Hq, S), dtype=torch.float32, device=dev)
 
     step = fg.prepare_prefill(q, k, v, SCALE, out=out, lse=lse, causal=True)
-    kernel = {"whole": "prefill_kernel", "split": "prefill_split_kernel",
-              "wide": "prefill_wide_kernel"}[fg.prefill_kernel_choice(q, k, v, causal=True)]
-    if kernel == "prefill_wide_kernel":
-        # unit pairs that fill the CUs split units over two workgroups; more
-        # run whole units on a persistent grid
-        G = Hq // Hkv
-        hb = 8 if G % 8 == 0 else 4 if G % 4 == 0 else 2 if G % 2 == 0 else 1
-        pairs = (B * Hkv * (G // hb) * -(-S // (256 // hb)) + 1) // 2
-        cus = torch.cuda.get_device_properties(dev).multi_processor_count
-        if pairs > 128 or 2 * pairs > cus:
-            kernel = "prefill_wide_persistent_kernel"
+    kernel = fg.prefill_kernel_name(q, k, v, causal=True)   # what AUTO launches, as the library reports it
 
     total_ms, per = _time_calls(step, steps, warmup, min_warm_ms=AUX_WARM_MS)
     # the reference's causal-halved count (test_flash_gqa_kernel.py:282-301)
@@ -281,6 +277,16 @@ def bench_prefill(cfg_id, steps, warmup, dev, keep=None):
                           "traffic": TRAFFIC_BYTES.get(f"prefill_cfg{cfg_id}"),
                           "kernel": kernel,
                           "algorithmic_flops": flops})
+
+
+def _host_cores():
+    """The host's logical CPUs and those this process may run on (the CPU
+    baselines use min(these, 16) OpenMP threads: `cores`)."""
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    return {"logical": os.cpu_count(), "usable": usable}
 
 
 def cpu_baseline_decode(res, budget_s=12.0):
@@ -312,6 +318,7 @@ def cpu_baseline_decode(res, budget_s=12.0):
         done_bytes += 2 * n_tok * cfg["Hkv"] * 128 * 2
         nb += 1
     return dict(value=round(done_bytes / elapsed / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                host_cores=_host_cores(),
                 sample=f"{nb} sequence decodes ({nb / B:.2f} passes over the {B}-sequence workload, all heads, "
                        f"all tokens), {elapsed:.1f} s on {threads} OpenMP threads")
 
@@ -672,7 +679,7 @@ def main():
                    "split_tokens": args.split_tokens or "auto"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_BYTES.get("decode_cfg2"),
-                     "kernel": "decode (split-KV pass + LSE combine)", "algorithmic_bytes": res["kv_bytes"],
+                     "kernel": res["kernel"], "algorithmic_bytes": res["kv_bytes"],
                      "avg_launch_us": round(res["avg_launch_ms"] * 1e3, 2),
                      "median_launch_us": round(res["median_ms"] * 1e3, 2),
                      "min_launch_us": round(res["min_ms"] * 1e3, 2)},

@@ -27,6 +27,7 @@ from .flash_gqa import (  # noqa: F401
     prepare_decode,
     prepare_decode_paged,
     prefill_kernel_choice,
+    prefill_kernel_name,
     prepare_prefill,
     PreparedLaunch,
 )

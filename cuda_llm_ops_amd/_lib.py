@@ -78,8 +78,13 @@ class PrefillArgs(ctypes.Structure):
         ("sink", ctypes.c_void_p),
         ("head_dim_v", ctypes.c_int32),
         ("kernel", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
     ]
 
+
+# leading bytes of a prefill workspace that must be zero before its first use
+FGQA_PREFILL_WORKSPACE_ZERO_BYTES = 4096
 
 FGQA_KV_BF16 = 0
 FGQA_KV_FP8_E4M3 = 1
@@ -208,6 +213,10 @@ def lib() -> ctypes.CDLL:
         L.fgqa_prefill_bf16.argtypes = [ctypes.POINTER(PrefillArgs), ctypes.c_void_p]
         L.fgqa_prefill_kernel_choice.restype = ctypes.c_int
         L.fgqa_prefill_kernel_choice.argtypes = [ctypes.POINTER(PrefillArgs), ctypes.POINTER(ctypes.c_int32)]
+        L.fgqa_prefill_kernel_name.restype = ctypes.c_int
+        L.fgqa_prefill_kernel_name.argtypes = [ctypes.POINTER(PrefillArgs), ctypes.POINTER(ctypes.c_char_p)]
+        L.fgqa_prefill_workspace_bytes.restype = ctypes.c_int
+        L.fgqa_prefill_workspace_bytes.argtypes = [ctypes.POINTER(PrefillArgs), ctypes.POINTER(ctypes.c_size_t)]
         L.fgqa_decode_paged_workspace_bytes.restype = ctypes.c_int
         L.fgqa_decode_paged_workspace_bytes.argtypes = [ctypes.POINTER(PagedDecodeArgs),
                                                         ctypes.POINTER(ctypes.c_size_t)]

@@ -1131,39 +1131,42 @@ __global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_wide_persistent_ker
     }
 }
 
-// Partial-result slots and arrival counters of the wide kernel's split units
-// (kPwMaxSplit units; held by every device the library runs on until the
-// process ends; the counters start at 0 and each launch leaves them at 0).
-// In host code the names are host-side stand-ins, not device addresses: the
-// addresses are looked up once per device (hipGetSymbolAddress, with that
-// device current) and only those pointers are passed to kernels.  Launches
-// that overlap on one device share them and would race.
-static __device__ __align__(256) float pw_part[(size_t)kPwMaxSplit * 2 * kPfPartFloats];
-static __device__ __align__(256) unsigned pw_ctr[4 * kPwMaxSplit];
+// Merge scratch of the kernels that split a unit's KV range over two
+// workgroups, in the layout of a caller workspace: the arrival counters (4
+// words per unit pair) in the first FGQA_PREFILL_WORKSPACE_ZERO_BYTES, then
+// two partial-result slots per pair.
+static_assert(4 * sizeof(unsigned) * kPwMaxSplit <= FGQA_PREFILL_WORKSPACE_ZERO_BYTES, "counters");
+constexpr size_t merge_scratch_bytes_for(int64_t pairs) {
+    return (size_t)FGQA_PREFILL_WORKSPACE_ZERO_BYTES + (size_t)pairs * 2 * kPfPartFloats * sizeof(float);
+}
+
+// The library's merge scratch for calls that pass no workspace (kPwMaxSplit
+// pairs; held by every device the library runs on until the process ends; the
+// counters start at 0 and each launch leaves them at 0).  In host code the
+// name is a host-side stand-in, not a device address: the address is looked
+// up once per device (hipGetSymbolAddress, with that device current) and only
+// that pointer is passed to kernels.  Launches that overlap on one device
+// share it and would race: such callers pass workspaces of their own.
+static __device__ __align__(256) unsigned char pw_scratch_mem[merge_scratch_bytes_for(kPwMaxSplit)];
 
 namespace {
 
 constexpr int kPwDevices = 64;
 std::mutex g_pw_mutex;
-float* g_pw_part[kPwDevices] = {nullptr};
-unsigned* g_pw_ctr[kPwDevices] = {nullptr};
+unsigned char* g_pw_scratch[kPwDevices] = {nullptr};
 
-// The current device's copies of pw_part and pw_ctr.
-int pw_scratch(float** part, unsigned** ctr) {
+// The current device's copy of pw_scratch_mem.
+int pw_scratch(unsigned char** mem) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kPwDevices) return FGQA_ERR_HIP;
     std::lock_guard<std::mutex> lock(g_pw_mutex);
-    if (g_pw_part[dev] == nullptr) {
+    if (g_pw_scratch[dev] == nullptr) {
         void* pp = nullptr;
-        void* cp = nullptr;
-        if (hipGetSymbolAddress(&pp, HIP_SYMBOL(pw_part)) != hipSuccess || pp == nullptr ||
-            hipGetSymbolAddress(&cp, HIP_SYMBOL(pw_ctr)) != hipSuccess || cp == nullptr)
+        if (hipGetSymbolAddress(&pp, HIP_SYMBOL(pw_scratch_mem)) != hipSuccess || pp == nullptr)
             return FGQA_ERR_HIP;
-        g_pw_part[dev] = static_cast<float*>(pp);
-        g_pw_ctr[dev] = static_cast<unsigned*>(cp);
+        g_pw_scratch[dev] = static_cast<unsigned char*>(pp);
     }
-    *part = g_pw_part[dev];
-    *ctr = g_pw_ctr[dev];
+    *mem = g_pw_scratch[dev];
     return FGQA_OK;
 }
 
@@ -1174,6 +1177,16 @@ int64_t wide_pairs(const fgqa_prefill_args* a) {
     const int64_t units = ceil_div(a->seqlen_q, 256 / hbw) * (int64_t)(group / hbw) * a->num_kv_heads * a->batch;
     return (units + 1) / 2;
 }
+
+// Whether the 256-row kernels run unit pairs on two workgroups each (at most
+// kPwMaxSplit pairs and one pair per two CUs; the tall kernel only under a
+// causal mask, where units differ in length) rather than whole units on a
+// persistent grid.
+bool wide_on_pairs(const fgqa_prefill_args* a, int cus) {
+    const int64_t pairs = wide_pairs(a);
+    return pairs <= kPwMaxSplit && 2 * pairs <= cus;
+}
+bool tall_on_pairs(const fgqa_prefill_args* a, int cus) { return a->causal && wide_on_pairs(a, cus); }
 
 // The kernel shape a validated call runs on a device with `cus` CUs: the
 // caller's `kernel`, or for AUTO the choice by grid size:
@@ -1206,6 +1219,16 @@ int prefill_choice(const fgqa_prefill_args* a, int cus) {
     if (!swa && a->causal) return units < 2 * (int64_t)cus ? FGQA_KERNEL_SPLIT : FGQA_KERNEL_WIDE;
     if (units < 4 * (int64_t)cus && !swa) return FGQA_KERNEL_SPLIT;
     return FGQA_KERNEL_WHOLE;
+}
+
+// Merge scratch bytes a validated call with kernel `choice` needs on a device
+// with `cus` CUs: the 256-row kernels on their pair grid (at most kPwMaxSplit
+// pairs, one per two CUs) split units only under a causal mask, where units
+// differ in length; everything else needs none.
+size_t merge_scratch_bytes(const fgqa_prefill_args* a, int choice, int cus) {
+    if ((choice != FGQA_KERNEL_WIDE && choice != FGQA_KERNEL_TALL) || !a->causal) return 0;
+    if (a->batch == 0 || a->seqlen_q == 0 || !wide_on_pairs(a, cus)) return 0;
+    return merge_scratch_bytes_for(wide_pairs(a));
 }
 
 int validate_prefill(const fgqa_prefill_args* a) {
@@ -1263,6 +1286,33 @@ extern "C" int fgqa_prefill_kernel_choice(const fgqa_prefill_args* a, int32_t* k
     return FGQA_OK;
 }
 
+extern "C" int fgqa_prefill_kernel_name(const fgqa_prefill_args* a, const char** name) {
+    int st = validate_prefill(a);
+    if (st != FGQA_OK) return st;
+    if (name == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
+    const int cus = device_cu_count();
+    if (cus <= 0) return FGQA_ERR_HIP;
+    switch (prefill_choice(a, cus)) {
+        case FGQA_KERNEL_WHOLE: *name = "prefill_kernel"; break;
+        case FGQA_KERNEL_SPLIT: *name = "prefill_split_kernel"; break;
+        case FGQA_KERNEL_WIDE:
+            *name = wide_on_pairs(a, cus) ? "prefill_wide_kernel" : "prefill_wide_persistent_kernel";
+            break;
+        default: *name = tall_on_pairs(a, cus) ? "prefill_tall_pairs_kernel" : "prefill_tall_persistent_kernel"; break;
+    }
+    return FGQA_OK;
+}
+
+extern "C" int fgqa_prefill_workspace_bytes(const fgqa_prefill_args* a, size_t* bytes) {
+    int st = validate_prefill(a);
+    if (st != FGQA_OK) return st;
+    if (bytes == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
+    const int cus = device_cu_count();
+    if (cus <= 0) return FGQA_ERR_HIP;
+    *bytes = merge_scratch_bytes(a, prefill_choice(a, cus), cus);
+    return FGQA_OK;
+}
+
 extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
     int st = validate_prefill(a);
     if (st != FGQA_OK) return st;
@@ -1314,6 +1364,19 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
     const int cus = device_cu_count();
     if (cus <= 0) return FGQA_ERR_HIP;
     const int choice = prefill_choice(a, cus);
+    // merge scratch: the caller's workspace, or with none the library's
+    if (const size_t need = merge_scratch_bytes(a, choice, cus); need > 0) {
+        unsigned char* ws = static_cast<unsigned char*>(a->workspace);
+        if (ws == nullptr && a->workspace_bytes == 0) {
+            if (const int e = pw_scratch(&ws); e != FGQA_OK) return e;
+        } else if (ws == nullptr || a->workspace_bytes < need) {
+            return FGQA_ERR_WORKSPACE;
+        } else if ((reinterpret_cast<uintptr_t>(ws) & 255u) != 0) {
+            return FGQA_ERR_UNSUPPORTED;
+        }
+        p.wide_ctr = reinterpret_cast<unsigned*>(ws);
+        p.wide_part = reinterpret_cast<float*>(ws + FGQA_PREFILL_WORKSPACE_ZERO_BYTES);
+    }
     const bool swa = p.window > 0 || p.sink != nullptr;
     const bool mla = a->head_dim == 192;
     const bool split = choice == FGQA_KERNEL_SPLIT;
@@ -1329,17 +1392,8 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
         p.div_streams = make_fast_div(p.n_streams);
         p.div_hgroups = make_fast_div(p.n_hgroups);
         p.wide_bias = 3;
-        const int64_t pairs = wide_pairs(a);
-        if (choice == FGQA_KERNEL_TALL) {
-            // unit pairs on two workgroups each when they fit the merge slots
-            // and the CUs (causal grids: whole units differ in length),
-            // else whole units on a persistent grid
-            const bool use_pairs = a->causal && pairs <= kPwMaxSplit && 2 * pairs <= cus;
-            if (use_pairs)
-                if (const int e = pw_scratch(&p.wide_part, &p.wide_ctr); e != FGQA_OK) return e;
-            return launch_prefill_tall(p, use_pairs, cus, s);
-        }
-        if (pairs > kPwMaxSplit || 2 * pairs > cus) {
+        if (choice == FGQA_KERNEL_TALL) return launch_prefill_tall(p, tall_on_pairs(a, cus), cus, s);
+        if (!wide_on_pairs(a, cus)) {
             // more pairs than one per two CUs: whole units on a persistent grid
             // attribute slots 7, 8, 9: the persistent wide kernels (plain, window, MLA)
             const int slot = mla ? 9 : swa ? 8 : 7;
@@ -1356,7 +1410,6 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
             if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
             return FGQA_OK;
         }
-        if (const int e = pw_scratch(&p.wide_part, &p.wide_ctr); e != FGQA_OK) return e;
         // attribute slots 5, 6: the wide kernels
         // attribute slots 5, 6, 18: the wide kernels (plain, window, MLA)
         const int wslot = mla ? 18 : swa ? 6 : 5;

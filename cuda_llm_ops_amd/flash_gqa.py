@@ -50,6 +50,8 @@ __all__ = [
     "backward_workspace_bytes",
     "prepare_decode",
     "prepare_prefill",
+    "prefill_kernel_choice",
+    "prefill_kernel_name",
     "prepare_backward",
     "PreparedLaunch",
 ]
@@ -392,8 +394,47 @@ def _check_head_dims(dqk, dv, window_size=0, sink=None):
         raise ValueError("a sliding window or sink needs head_dim_qk == head_dim_v == 128")
 
 
+# Merge scratch of the prefill kernels that split a unit over two workgroups
+# (include/fgqa.h, fgqa_prefill_args.workspace): one per (device, stream), so
+# calls on different streams never share one, and calls on one stream run in
+# order.
+_PREFILL_WORKSPACES = {}
+
+
+def _new_prefill_workspace(nbytes, device):
+    """Uninitialised device bytes (torch's blocks are 512-byte aligned) whose
+    arrival-counter prefix is zeroed on the current stream, before any launch
+    that uses it."""
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    ws[:_lib.FGQA_PREFILL_WORKSPACE_ZERO_BYTES].zero_()
+    return ws
+
+
+def _attach_prefill_workspace(a, device, own=False):
+    """Sets `a`'s workspace for the kernel its call runs on this device: the
+    current stream's cached one, or (own) a new one; None when the kernel
+    needs none.  Returns the tensor, which the caller keeps alive."""
+    n = ctypes.c_size_t(0)
+    _lib.check(_lib.lib().fgqa_prefill_workspace_bytes(ctypes.byref(a), ctypes.byref(n)),
+               "fgqa_prefill_workspace_bytes")
+    if n.value == 0:
+        return None
+    if own:
+        ws = _new_prefill_workspace(n.value, device)
+    else:
+        key = (device.index, _stream())
+        ws = _PREFILL_WORKSPACES.get(key)
+        if ws is None or ws.numel() < n.value:
+            ws = _new_prefill_workspace(n.value, device)
+            _PREFILL_WORKSPACES[key] = ws
+    a.workspace = ws.data_ptr()
+    a.workspace_bytes = ws.numel()
+    return ws
+
+
 def _prefill(q, k, v, o, lse, scale, causal, layout, window_size=0, sink=None):
     a = _prefill_args(q, k, v, o, lse, scale, causal, layout, window_size, sink)
+    _attach_prefill_workspace(a, q.device)
     _lib.check(_lib.lib().fgqa_prefill_bf16(ctypes.byref(a), ctypes.c_void_p(_stream())), "fgqa_prefill_bf16")
 
 
@@ -443,9 +484,12 @@ def flash_gqa_forward_bshd(q, k, v, scale=None, out=None, lse=None, causal=True,
     for MLA.  window_size > 0 (causal only): row i sees keys [i - window_size + 1, i];
     sink: optional fp32 [Hq] added to the softmax denominator as sink * exp(-max)
     (the reference's SWA kernel); both need D == Dv == 128.
-    kernel: 'auto', or 'whole' / 'split' to force one kernel shape (the window /
-    sink variant has no split form)."""
+    kernel: 'auto', or 'whole' / 'split' / 'wide' / 'tall' to force one kernel
+    shape (the window / sink variant has no split or tall form).  The kernels
+    that merge a unit's two halves through device memory get a workspace held
+    per (device, stream), so calls on different streams may overlap."""
     a, out, lse, _keep = _prefill_bshd_prepare(q, k, v, scale, out, lse, causal, window_size, sink, kernel)
+    _attach_prefill_workspace(a, q.device)
     _lib.check(_lib.lib().fgqa_prefill_bf16(ctypes.byref(a), ctypes.c_void_p(_stream())), "fgqa_prefill_bf16")
     return out, lse
 
@@ -453,24 +497,51 @@ def flash_gqa_forward_bshd(q, k, v, scale=None, out=None, lse=None, causal=True,
 def prepare_prefill(q, k, v, scale=None, out=None, lse=None, causal=True, window_size=0, sink=None,
                     kernel="auto"):
     """``flash_gqa_forward_bshd`` validated once; returns a ``PreparedLaunch``
-    whose ``out`` is the output tensor (the LSE tensor is ``.lse``)."""
+    whose ``out`` is the output tensor (the LSE tensor is ``.lse``).  It owns
+    its merge workspace (when its kernel needs one), so its calls must not
+    overlap on the GPU, as they would share ``out`` anyway."""
     a, out, lse, keep = _prefill_bshd_prepare(q, k, v, scale, out, lse, causal, window_size, sink, kernel)
+    keep = keep + (_attach_prefill_workspace(a, q.device, own=True),)
     pl = PreparedLaunch(_lib.lib().fgqa_prefill_bf16, a, keep, out, "fgqa_prefill_bf16")
     pl.lse = lse
     return pl
 
 
+def _prefill_query_args(q, k, v, causal, window_size, sink, kernel):
+    """The argument block of a BSHD prefill call for queries that launch
+    nothing: no output tensors are allocated (O's pointer is Q's, its
+    strides the contiguous ones, LSE none)."""
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("expected 4-D BSHD tensors")
+    B, Sq, Hq, _ = q.shape
+    Dv = v.shape[3]
+    a = _prefill_args(q, k, v, q, None, 1.0, causal, "bshd", window_size, sink, kernel)
+    a.o_stride[:] = [Sq * Hq * Dv, Hq * Dv, Dv]
+    return a
+
+
 def prefill_kernel_choice(q, k, v, causal=True, window_size=0, sink=None, kernel="auto") -> str:
-    """The kernel shape ('whole', 'split' or 'wide') ``flash_gqa_forward_bshd``
-    runs for these tensors on the current device (what ``kernel='auto'``
-    resolves to); launches nothing."""
-    a, _out, _lse, _keep = _prefill_bshd_prepare(q, k, v, None, None, None, causal, window_size, sink, kernel)
+    """The kernel shape ('whole', 'split', 'wide' or 'tall')
+    ``flash_gqa_forward_bshd`` runs for these tensors on the current device
+    (what ``kernel='auto'`` resolves to); launches and allocates nothing."""
+    a = _prefill_query_args(q, k, v, causal, window_size, sink, kernel)
     c = ctypes.c_int32(0)
     st = _lib.lib().fgqa_prefill_kernel_choice(ctypes.byref(a), ctypes.byref(c))
     if st != _lib.FGQA_OK:
         raise _lib.FgqaError(st, "fgqa_prefill_kernel_choice")
     return {_lib.FGQA_KERNEL_WHOLE: "whole", _lib.FGQA_KERNEL_SPLIT: "split", _lib.FGQA_KERNEL_WIDE: "wide",
             _lib.FGQA_KERNEL_TALL: "tall"}[c.value]
+
+
+def prefill_kernel_name(q, k, v, causal=True, window_size=0, sink=None, kernel="auto") -> str:
+    """The name of the kernel function ``flash_gqa_forward_bshd`` launches for
+    these tensors on the current device (it tells apart the grid forms of one
+    kernel shape, e.g. ``prefill_wide_kernel`` on unit pairs and
+    ``prefill_wide_persistent_kernel``); launches and allocates nothing."""
+    a = _prefill_query_args(q, k, v, causal, window_size, sink, kernel)
+    name = ctypes.c_char_p()
+    _lib.check(_lib.lib().fgqa_prefill_kernel_name(ctypes.byref(a), ctypes.byref(name)), "fgqa_prefill_kernel_name")
+    return name.value.decode()
 
 
 def launch_flash_gqa_forward_bf16_kernel(q, k, v, scale=None, out=None, lse=None, causal=True,

@@ -222,7 +222,22 @@ int fgqa_decode_paged(const fgqa_decode_paged_args* args, void* stream);
  *   kernel  an fgqa_kernel_choice (0 = AUTO).  The window / sink variant has
  *           no split form: FGQA_KERNEL_SPLIT with either returns
  *           FGQA_ERR_UNSUPPORTED (FGQA_KERNEL_WIDE runs it).
+ *   workspace / workspace_bytes  device scratch of at least
+ *           fgqa_prefill_workspace_bytes() bytes, 256-byte aligned, for the
+ *           kernels that split a unit's KV range over two workgroups (the
+ *           wide and tall kernels on causal grids whose unit pairs fill the
+ *           CUs, such as S=4096, Hq=16, Hkv=1); the other shapes need none.
+ *           Its first FGQA_PREFILL_WORKSPACE_ZERO_BYTES bytes (the arrival
+ *           counters) must be zero before its first use; every call leaves
+ *           them zero when it completes, so the workspace can be reused
+ *           (graph replays included) without clearing.  Calls that overlap
+ *           on the GPU must not share a workspace: concurrent calls on
+ *           different streams each pass their own.  NULL / 0 uses the
+ *           library's per-device scratch, which every such NULL call on
+ *           that device shares.  Callers that zero the struct get NULL / 0.
  */
+#define FGQA_PREFILL_WORKSPACE_ZERO_BYTES 4096
+
 typedef struct fgqa_prefill_args {
     const void* q;
     const void* k;
@@ -245,15 +260,32 @@ typedef struct fgqa_prefill_args {
     const float* sink;
     int32_t head_dim_v;
     int32_t kernel;
+    void* workspace;
+    size_t workspace_bytes;
 } fgqa_prefill_args;
 
 int fgqa_prefill_bf16(const fgqa_prefill_args* args, void* stream);
+
+/* Bytes of workspace fgqa_prefill_bf16 needs for these arguments on the
+ * current device (0: the chosen kernel needs none).  Same validation as the
+ * call; launches nothing.  (No counterpart in the reference, whose Triton
+ * launcher keeps no state between its kernel's workgroups.) */
+int fgqa_prefill_workspace_bytes(const fgqa_prefill_args* args, size_t* bytes);
 
 /* The kernel shape (FGQA_KERNEL_WHOLE, _SPLIT or _WIDE) fgqa_prefill_bf16
  * runs for these arguments on the current device: `kernel`, or what AUTO
  * picks.  Same validation and status codes as the call; launches nothing.
  * (No counterpart in the reference, whose prefill has one kernel shape.) */
 int fgqa_prefill_kernel_choice(const fgqa_prefill_args* args, int32_t* kernel);
+
+/* The name of the kernel function fgqa_prefill_bf16 launches for these
+ * arguments on the current device (static storage), which also tells apart
+ * the grid forms of one kernel shape: "prefill_kernel",
+ * "prefill_split_kernel", "prefill_wide_kernel" (unit pairs),
+ * "prefill_wide_persistent_kernel", "prefill_tall_pairs_kernel" or
+ * "prefill_tall_persistent_kernel".  Same validation as the call; launches
+ * nothing.  (No counterpart in the reference.) */
+int fgqa_prefill_kernel_name(const fgqa_prefill_args* args, const char** name);
 
 /*
  * Prefill backward: dQ, dK, dV of the causal (or full) forward above.

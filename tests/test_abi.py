@@ -23,7 +23,7 @@ def test_c_abi_symbols_exported():
     hdr = open(os.path.join(ROOT, "include", "fgqa.h")).read()
     names = set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(fgqa_\w+)\s*\(", hdr, flags=re.M))
     assert names == {"fgqa_decode_workspace_bytes", "fgqa_decode_bf16", "fgqa_decode_bf16_noalloc", "fgqa_prefill_bf16",
-                     "fgqa_prefill_kernel_choice",
+                     "fgqa_prefill_kernel_choice", "fgqa_prefill_kernel_name", "fgqa_prefill_workspace_bytes",
                      "fgqa_prefill_backward_workspace_bytes", "fgqa_prefill_backward_bf16",
                      "fgqa_decode_paged_workspace_bytes", "fgqa_decode_paged", "fgqa_sparse_prefill_bf16",
                      "fgqa_status_string", "fgqa_version"}

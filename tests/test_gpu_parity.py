@@ -432,29 +432,140 @@ def test_prefill_auto_kernel_choice(cuda):
     assert choice(1, 4096, 16, 1, kernel="split") == "split"
 
 
-def test_prefill_wide_config4_repeatable(cuda):
-    """The wide kernel at BASELINE config 4, where every pair of its 256-row
-    units but one splits its heavy unit over two workgroups: three launches in
-    a row give bit-identical output (the arrival counters return to 0, and the
-    merge does not depend on which workgroup finishes first), and sampled rows
-    of split units match the oracle."""
+@pytest.mark.parametrize("kernel", ["wide", "tall"])
+def test_prefill_wide_config4_repeatable(cuda, kernel):
+    """The wide (and tall) kernel at BASELINE config 4, where every pair of its
+    256-row units but one splits its heavy unit over two workgroups: 200
+    launches in a row, each compared bit for bit with the first (the arrival
+    counters return to 0, and the merge does not depend on which workgroup
+    finishes first), and sampled rows of split units match the oracle."""
     import torch
     fg = _fg()
     B, S, Hq, Hkv = 1, 4096, 16, 1
     q = gpu_normal_bf16((B, S, Hq, 128), 44, 1.0, cuda)
     k = gpu_normal_bf16((B, S, Hkv, 128), 45, 1.0, cuda)
     v = gpu_normal_bf16((B, S, Hkv, 128), 46, 1.0, cuda)
-    runs = []
-    for _ in range(3):
-        out, lse = fg.flash_gqa_forward_bshd(q, k, v, SCALE, kernel="wide")
-        _sync()
-        runs.append((out.clone(), lse.clone()))
-    for out, lse in runs[1:]:
-        assert torch.equal(out, runs[0][0]) and torch.equal(lse, runs[0][1]), "wide kernel: launches differ"
-    out, lse = runs[0]
-    assert bool(out.isfinite().all())
+    out0, lse0 = fg.flash_gqa_forward_bshd(q, k, v, SCALE, kernel=kernel)
+    out, lse = torch.empty_like(out0), torch.empty_like(lse0)
+    step = fg.prepare_prefill(q, k, v, SCALE, out=out, lse=lse, causal=True, kernel=kernel)
+    diff = torch.zeros((), dtype=torch.int32, device=cuda)
+    for i in range(200):
+        step()
+        # count launches that differ, on the device (no synchronisation per launch)
+        same = (out.view(torch.int16) == out0.view(torch.int16)).all() & (lse.view(torch.int32) ==
+                                                                          lse0.view(torch.int32)).all()
+        diff += (~same).to(torch.int32)
+        if i % 50 == 49:
+            assert int(diff.item()) == 0, f"{kernel} kernel: a launch before {i + 1} differs from the first"
+    assert bool(out0.isfinite().all())
     for rows in ((0, 64), (2016, 2080), (4096 - 96, 4096)):
-        _sampled_prefill_check(q, k, v, out, lse, rows, 0, "config4 wide")
+        _sampled_prefill_check(q, k, v, out0, lse0, rows, 0, f"config4 {kernel}")
+
+
+def test_prefill_concurrent_streams_config4(cuda):
+    """Config-4 prefills on two streams of the same priority at once: the
+    kernels that merge a unit's two halves through device memory get a
+    workspace per stream from the Python mirror, so each stream's output is
+    bit-identical to its serial run (a shared merge slot would mix them)."""
+    import torch
+    fg = _fg()
+    B, S, Hq, Hkv = 1, 4096, 16, 1
+    ins = [tuple(gpu_normal_bf16(shape, seed, 1.0, cuda) for shape, seed in
+                 (((B, S, Hq, 128), 60 + 3 * i), ((B, S, Hkv, 128), 61 + 3 * i), ((B, S, Hkv, 128), 62 + 3 * i)))
+           for i in range(2)]
+    assert fg.prefill_kernel_choice(*ins[0]) in ("wide", "split")
+    serial = [fg.flash_gqa_forward_bshd(*x, SCALE) for x in ins]
+    _sync()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [[None] * 2 for _ in range(20)]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    for r in range(20):
+        for i, s in enumerate(streams):
+            with torch.cuda.stream(s):
+                outs[r][i] = fg.flash_gqa_forward_bshd(*ins[i], SCALE)
+    for s in streams:
+        torch.cuda.current_stream().wait_stream(s)
+    _sync()
+    for r in range(20):
+        for i in range(2):
+            o, l = outs[r][i]
+            assert torch.equal(o, serial[i][0]) and torch.equal(l, serial[i][1]), f"round {r} stream {i}"
+
+
+def test_prefill_caller_workspace(cuda):
+    """The merge workspace through the C ABI: the size query at config 4, a
+    caller workspace (zeroed counter prefix) giving the library scratch's
+    output bit for bit, twice in a row without clearing, and the refusals (too
+    small, NULL with a size, misaligned) before any launch."""
+    import torch
+    from cuda_llm_ops_amd import _lib
+    from cuda_llm_ops_amd import flash_gqa as fgm
+    fg = _fg()
+    L = fg.lib()
+    B, S, Hq, Hkv = 1, 4096, 16, 1
+    q = gpu_normal_bf16((B, S, Hq, 128), 70, 1.0, cuda)
+    k = gpu_normal_bf16((B, S, Hkv, 128), 71, 1.0, cuda)
+    v = gpu_normal_bf16((B, S, Hkv, 128), 72, 1.0, cuda)
+    out = torch.empty_like(q)
+    lse = torch.empty((B, Hq, S), dtype=torch.float32, device=cuda)
+    a = fgm._prefill_args(q, k, v, out, lse, SCALE, True, "bshd", kernel="wide")
+    n = ctypes.c_size_t(0)
+    assert L.fgqa_prefill_workspace_bytes(ctypes.byref(a), ctypes.byref(n)) == 0
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    pairs = (2 * (S // 32) + 1) // 2   # 256-row units: 8 heads x 32 positions, 2 head groups
+    if 2 * pairs <= cus:
+        assert n.value == 4096 + pairs * 2 * (2 * 4 * 66 * 64) * 4
+    else:
+        assert n.value == 0
+    st = torch.cuda.current_stream().cuda_stream
+    assert L.fgqa_prefill_bf16(ctypes.byref(a), ctypes.c_void_p(st)) == 0   # library scratch
+    _sync()
+    ref_o, ref_l = out.clone(), lse.clone()
+    if n.value == 0:
+        return
+    ws = torch.empty(n.value + 512, dtype=torch.uint8, device=cuda)
+    ws[:4096].zero_()
+    a.workspace, a.workspace_bytes = ws.data_ptr(), n.value
+    for _ in range(2):
+        out.zero_()
+        assert L.fgqa_prefill_bf16(ctypes.byref(a), ctypes.c_void_p(st)) == 0
+        _sync()
+        assert torch.equal(out, ref_o) and torch.equal(lse, ref_l)
+    assert int(ws[:4096].to(torch.int32).abs().sum()) == 0, "counters left nonzero"
+    a.workspace_bytes = n.value - 1
+    assert L.fgqa_prefill_bf16(ctypes.byref(a), ctypes.c_void_p(st)) == _lib.FGQA_ERR_WORKSPACE
+    a.workspace, a.workspace_bytes = None, n.value
+    assert L.fgqa_prefill_bf16(ctypes.byref(a), ctypes.c_void_p(st)) == _lib.FGQA_ERR_WORKSPACE
+    a.workspace, a.workspace_bytes = ws.data_ptr() + 16, n.value
+    assert L.fgqa_prefill_bf16(ctypes.byref(a), ctypes.c_void_p(st)) == _lib.FGQA_ERR_UNSUPPORTED
+    # shapes whose kernels merge nothing need no workspace
+    a2 = fgm._prefill_args(q, k, v, out, lse, SCALE, False, "bshd", kernel="wide")
+    assert L.fgqa_prefill_workspace_bytes(ctypes.byref(a2), ctypes.byref(n)) == 0 and n.value == 0
+    a3 = fgm._prefill_args(q, k, v, out, lse, SCALE, True, "bshd", kernel="split")
+    assert L.fgqa_prefill_workspace_bytes(ctypes.byref(a3), ctypes.byref(n)) == 0 and n.value == 0
+
+
+def test_prefill_kernel_names(cuda):
+    """The kernel function the library reports for a call: the grid form of
+    the 256-row kernels follows the pair count."""
+    import torch
+    fg = _fg()
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+
+    def name(B, S, Hq, Hkv, **kw):
+        q = torch.empty((B, S, Hq, 128), dtype=torch.bfloat16, device=cuda)
+        k = torch.empty((B, S, Hkv, 128), dtype=torch.bfloat16, device=cuda)
+        return fg.prefill_kernel_name(q, k, k, **kw)
+
+    assert name(4, 16384, 32, 8) == "prefill_wide_persistent_kernel"
+    assert name(4, 16384, 32, 8, kernel="tall") == "prefill_tall_persistent_kernel"
+    assert name(1, 1024, 16, 1, kernel="split") == "prefill_split_kernel"
+    assert name(1, 1024, 16, 1, kernel="whole") == "prefill_kernel"
+    if cus == 256:
+        assert name(1, 4096, 16, 1) == "prefill_wide_kernel"
+        assert name(1, 4096, 16, 1, kernel="tall") == "prefill_tall_pairs_kernel"
+        assert name(1, 4096, 16, 1, causal=False, kernel="tall") == "prefill_tall_persistent_kernel"
 
 
 def test_prefill_wide_graph_replays(cuda):
