@@ -496,124 +496,29 @@ __global__ __launch_bounds__(kDecThreads) void decode_combine_kernel(DecodeParam
     if (p.lse != nullptr && (tid & 15) == 0) p.lse[(int64_t)b * p.hq + qh] = M * kLn2 + logf(L);
 }
 
+// One pass of the 4 decode waves covers the planner's split rounding.
+static_assert(kDecWaves * kDecStep == plan::kDecodeStepRound, "decode split rounding");
+
 namespace {
+using plan::DecodePlan;
+using plan::DecodeShape;
 
-constexpr int kStepRound = kDecWaves * kDecStep;  // 128 tokens: one pass of the 4 waves
-constexpr int kMaxAutoChunk = 4096;               // longest split the planner picks by itself
-
-struct DecodePlan {
-    int chunk;
-    int nsplit;
-    bool list;            // ragged batch: work list of non-empty splits
-    size_t part_o_bytes;
-    size_t part_ml_bytes;
-    size_t ws_bytes;
-};
-
-constexpr int kRaggedChunk = 4096;   // split length for ragged batches (work-list mode)
-
-int validate_decode(const fgqa_decode_args* a) {
-    if (a == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->batch < 0 || a->max_seqlen < 0 || a->num_q_heads <= 0 || a->num_kv_heads <= 0 ||
-        a->head_dim <= 0)
-        return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->num_q_heads % a->num_kv_heads != 0) return FGQA_ERR_INVALID_ARGUMENT;
-    if (!isfinite(a->scale)) return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->split_tokens < 0) return FGQA_ERR_INVALID_ARGUMENT;
-    for (int i = 0; i < 2; ++i)
-        if (a->q_stride[i] < 0 || a->o_stride[i] < 0) return FGQA_ERR_INVALID_ARGUMENT;
-    for (int i = 0; i < 3; ++i)
-        if (a->k_stride[i] < 0 || a->v_stride[i] < 0) return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->head_dim != kHeadDim) return FGQA_ERR_UNSUPPORTED;
-    if (a->num_q_heads / a->num_kv_heads > 16) return FGQA_ERR_UNSUPPORTED;
-    // 32-bit buffer offsets: the furthest byte addressed inside one sequence.
-    const int64_t lim = (int64_t)1 << 31;
-    if ((int64_t)(a->max_seqlen + 64) * a->k_stride[1] * 2 >= lim ||
-        (int64_t)(a->max_seqlen + 64) * a->v_stride[1] * 2 >= lim)
-        return FGQA_ERR_UNSUPPORTED;
-    return FGQA_OK;
+// The split plan of a validated call on the current device.
+int plan_on_device(const DecodeShape& shape, DecodePlan* pl) {
+    const int cus = plan::decode_needs_cus(shape) ? device_cu_count() : 0;
+    return plan::plan_decode(shape, cus, pl);
 }
-
-int validate_decode_pointers(const fgqa_decode_args* a) {
-    if (a->batch == 0) return FGQA_OK;
-    if (a->q == nullptr || a->k == nullptr || a->v == nullptr || a->o == nullptr)
-        return FGQA_ERR_INVALID_ARGUMENT;
-    if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o))
-        return FGQA_ERR_UNSUPPORTED;
-    for (int i = 0; i < 2; ++i)
-        if ((a->q_stride[i] & 7) || (a->o_stride[i] & 7)) return FGQA_ERR_UNSUPPORTED;
-    for (int i = 0; i < 3; ++i)
-        if ((a->k_stride[i] & 7) || (a->v_stride[i] & 7)) return FGQA_ERR_UNSUPPORTED;
-    return FGQA_OK;
-}
-
-// Split plan from the sizes alone (shared by the contiguous and paged entries).
-struct DecodeShape {
-    int batch, max_seqlen, num_q_heads, num_kv_heads, split_tokens;
-    bool ragged;   // per-sequence lengths are given
-};
-
-int plan_decode(const DecodeShape* a, DecodePlan* plan) {
-    const int64_t S = a->max_seqlen > 0 ? a->max_seqlen : 1;
-    // Ragged batches get a work list of their non-empty splits (built on the
-    // device from the lengths), so no workgroup is spent on padding.
-    plan->list = a->ragged && a->batch < (1 << 15);
-    int64_t chunk;
-    if (a->split_tokens > 0) {
-        chunk = ceil_div(a->split_tokens, kStepRound) * kStepRound;
-    } else if (plan->list) {
-        chunk = kRaggedChunk;
-    } else {
-        // The KV stream is HBM-bound: a split only pays when there are too
-        // few (batch, kv head) streams to occupy every CU, or when sequences
-        // are long enough that one workgroup per stream would leave a long
-        // tail.  Splits cost a partial write/read and a combine pass.
-        const int cus = device_cu_count();
-        if (cus <= 0) return FGQA_ERR_HIP;
-        const int64_t items = (int64_t)(a->batch > 0 ? a->batch : 1) * a->num_kv_heads;
-        int64_t want = (items >= cus) ? 1 : ceil_div(4LL * cus, items);
-        const int64_t max_splits = ceil_div(S, kStepRound);
-        if (want > max_splits) want = max_splits;
-        if (want < 1) want = 1;
-        chunk = ceil_div(ceil_div(S, want), kStepRound) * kStepRound;
-        if (chunk > kMaxAutoChunk) chunk = kMaxAutoChunk;
-    }
-    if (chunk < kStepRound) chunk = kStepRound;
-    if (chunk > S) chunk = ceil_div(S, kStepRound) * kStepRound;
-    plan->chunk = (int)chunk;
-    plan->nsplit = (int)ceil_div(S, chunk);
-    if (plan->nsplit >= (1 << 16)) plan->list = false;
-    const int64_t slots = (int64_t)a->batch * a->num_q_heads * plan->nsplit;
-    plan->part_o_bytes = 0;
-    plan->part_ml_bytes = 0;
-    if (plan->nsplit > 1) {
-        plan->part_o_bytes = (size_t)(ceil_div(slots * kHeadDim * 4, 256) * 256);
-        plan->part_ml_bytes = (size_t)(ceil_div(slots * 2 * 4, 256) * 256);
-    }
-    plan->ws_bytes = plan->part_o_bytes + plan->part_ml_bytes;
-    if (plan->list) plan->ws_bytes += (size_t)(1 + (int64_t)a->batch * plan->nsplit) * 4;
-    return FGQA_OK;
-}
-
 }  // namespace
 }  // namespace fgqa
 
 using namespace fgqa;
 
-namespace {
-DecodeShape shape_of(const fgqa_decode_args* a) {
-    return DecodeShape{a->batch, a->max_seqlen, a->num_q_heads, a->num_kv_heads, a->split_tokens,
-                       a->seqlens != nullptr};
-}
-}  // namespace
-
 extern "C" int fgqa_decode_workspace_bytes(const fgqa_decode_args* a, size_t* bytes) {
     if (bytes == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
-    int st = validate_decode(a);
+    int st = plan::validate_decode(a);
     if (st != FGQA_OK) return st;
     DecodePlan plan;
-    const DecodeShape shape = shape_of(a);
-    st = plan_decode(&shape, &plan);
+    st = plan_on_device(plan::decode_shape(a), &plan);
     if (st != FGQA_OK) return st;
     *bytes = plan.ws_bytes;
     return FGQA_OK;
@@ -657,14 +562,13 @@ void* noalloc_scratch(int* status) {
 // The decode call; `noalloc`: the workspace is the device scratch above
 // (the caller passes none), never the caller's or the library's buffer.
 int decode_run(const fgqa_decode_args* a, void* stream, bool noalloc) {
-    int st = validate_decode(a);
+    int st = plan::validate_decode(a);
     if (st != FGQA_OK) return st;
-    st = validate_decode_pointers(a);
+    st = plan::validate_decode_pointers(a);
     if (st != FGQA_OK) return st;
     if (a->batch == 0) return FGQA_OK;
     DecodePlan plan;
-    const DecodeShape shape = shape_of(a);
-    st = plan_decode(&shape, &plan);
+    st = plan_on_device(plan::decode_shape(a), &plan);
     if (st != FGQA_OK) return st;
 
     DecodeParams p;
@@ -762,83 +666,25 @@ extern "C" int fgqa_decode_bf16_noalloc(const fgqa_decode_args* a, void* stream)
 }
 
 // ---------------------------------------------------------------- paged KV cache
-namespace fgqa {
-namespace {
-
-int validate_paged(const fgqa_decode_paged_args* a) {
-    if (a == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->batch < 0 || a->max_seqlen < 0 || a->num_q_heads <= 0 || a->num_kv_heads <= 0 || a->head_dim <= 0 ||
-        a->page_size <= 0 || a->num_pages < 0 || a->block_table_stride < 0)
-        return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->num_q_heads % a->num_kv_heads != 0) return FGQA_ERR_INVALID_ARGUMENT;
-    if (!isfinite(a->scale) || !isfinite(a->k_scale) || !isfinite(a->v_scale)) return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->split_tokens < 0) return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->kv_dtype != FGQA_KV_BF16 && a->kv_dtype != FGQA_KV_FP8_E4M3) return FGQA_ERR_INVALID_ARGUMENT;
-    if ((a->page_size & (a->page_size - 1)) != 0 || a->page_size > (1 << 20)) return FGQA_ERR_UNSUPPORTED;
-    // the block table row covers max_seqlen tokens
-    if ((int64_t)a->max_seqlen > a->block_table_stride * (int64_t)a->page_size) return FGQA_ERR_INVALID_ARGUMENT;
-    for (int i = 0; i < 2; ++i)
-        if (a->q_stride[i] < 0 || a->o_stride[i] < 0) return FGQA_ERR_INVALID_ARGUMENT;
-    for (int i = 0; i < 3; ++i)
-        if (a->k_stride[i] < 0 || a->v_stride[i] < 0) return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->head_dim != kHeadDim) return FGQA_ERR_UNSUPPORTED;
-    if (a->num_q_heads / a->num_kv_heads > 16) return FGQA_ERR_UNSUPPORTED;
-    return FGQA_OK;
-}
-
-int validate_paged_pointers(const fgqa_decode_paged_args* a) {
-    if (a->batch == 0) return FGQA_OK;
-    if (a->q == nullptr || a->o == nullptr || a->seqlens == nullptr || a->block_table == nullptr)
-        return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->max_seqlen > 0 && (a->k_cache == nullptr || a->v_cache == nullptr || a->num_pages == 0))
-        return FGQA_ERR_INVALID_ARGUMENT;
-    if (!aligned16(a->q) || !aligned16(a->o) || !aligned16(a->k_cache) || !aligned16(a->v_cache))
-        return FGQA_ERR_UNSUPPORTED;
-    for (int i = 0; i < 2; ++i)
-        if ((a->q_stride[i] & 7) || (a->o_stride[i] & 7)) return FGQA_ERR_UNSUPPORTED;
-    // 16-byte aligned rows: strides in elements of the cache type
-    const int64_t m = (a->kv_dtype == FGQA_KV_FP8_E4M3) ? 15 : 7;
-    for (int i = 0; i < 3; ++i)
-        if ((a->k_stride[i] & m) || (a->v_stride[i] & m)) return FGQA_ERR_UNSUPPORTED;
-    return FGQA_OK;
-}
-
-DecodeShape shape_of_paged(const fgqa_decode_paged_args* a) {
-    return DecodeShape{a->batch, a->max_seqlen, a->num_q_heads, a->num_kv_heads, a->split_tokens, true};
-}
-
-// The paged decode always runs the work-list kernel; a shape the list cannot
-// index (batch >= 2^15 or >= 2^16 splits) is rejected here, so the workspace
-// query and the launch agree and nothing is allocated before the error.
-int plan_paged(const fgqa_decode_paged_args* a, DecodePlan* plan) {
-    const DecodeShape shape = shape_of_paged(a);
-    const int st = plan_decode(&shape, plan);
-    if (st != FGQA_OK) return st;
-    return plan->list ? FGQA_OK : FGQA_ERR_UNSUPPORTED;
-}
-
-}  // namespace
-}  // namespace fgqa
-
 extern "C" int fgqa_decode_paged_workspace_bytes(const fgqa_decode_paged_args* a, size_t* bytes) {
     if (bytes == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
-    int st = validate_paged(a);
+    int st = plan::validate_paged(a);
     if (st != FGQA_OK) return st;
     DecodePlan plan;
-    st = plan_paged(a, &plan);
+    st = plan::plan_paged(a, &plan);
     if (st != FGQA_OK) return st;
     *bytes = plan.ws_bytes;
     return FGQA_OK;
 }
 
 extern "C" int fgqa_decode_paged(const fgqa_decode_paged_args* a, void* stream) {
-    int st = validate_paged(a);
+    int st = plan::validate_paged(a);
     if (st != FGQA_OK) return st;
-    st = validate_paged_pointers(a);
+    st = plan::validate_paged_pointers(a);
     if (st != FGQA_OK) return st;
     if (a->batch == 0) return FGQA_OK;
     DecodePlan plan;
-    st = plan_paged(a, &plan);
+    st = plan::plan_paged(a, &plan);
     if (st != FGQA_OK) return st;
 
     DecodeParams p;

@@ -8,6 +8,7 @@
 #include <stdint.h>
 
 #include "fgqa.h"
+#include "../host/fgqa_plan.h"   // aligned16, ceil_div and the host-only validation / planning
 
 namespace fgqa {
 
@@ -26,9 +27,5 @@ void* internal_workspace(size_t bytes, int* status);
 // Sets a kernel's dynamic-LDS limit once per device (the attribute is per
 // kernel and per device).  slot: a distinct small index per kernel.
 int set_kernel_smem_once(int slot, const void* fn, int bytes);
-
-inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
-inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace fgqa

@@ -1105,130 +1105,34 @@ __global__ __launch_bounds__(2 * kBwThreads, 1) void bwd_dq_split_kernel(BwdPara
     dq_unit_pp<kSwa>(p, smem, qb, hg, kvh, b);
 }
 
-namespace {
+static_assert(kKvKeys == plan::kBackwardKvKeys, "keys per dK/dV workgroup");
 
-struct BwdPlan {
-    int n_hsplit;
-    size_t stat_bytes, part_k_bytes, part_v_bytes, ws_bytes;
-};
-
-// Q/K head dim of a call: 128, or 192 for MLA (V/O stay 128).
-int backward_dqk(const fgqa_prefill_backward_args* a) { return a->head_dim; }
-
-size_t round256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
-
-int validate_backward(const fgqa_prefill_backward_args* a) {
-    if (a == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->batch < 0 || a->seqlen_q < 0 || a->seqlen_kv < 0 || a->num_q_heads <= 0 ||
-        a->num_kv_heads <= 0 || a->head_dim <= 0)
-        return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->num_q_heads % a->num_kv_heads != 0) return FGQA_ERR_INVALID_ARGUMENT;
-    if (!isfinite(a->scale)) return FGQA_ERR_INVALID_ARGUMENT;
-    // a sliding window is a causal window (flash_swa_backward_kernel.py:278-282)
-    if (a->window_size < 0 || (a->window_size > 0 && !a->causal)) return FGQA_ERR_INVALID_ARGUMENT;
-    const int64_t* strides[8] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride,
-                                 a->grad_o_stride, a->grad_q_stride, a->grad_k_stride, a->grad_v_stride};
-    for (const int64_t* s : strides)
-        for (int i = 0; i < 3; ++i)
-            if (s[i] < 0) return FGQA_ERR_INVALID_ARGUMENT;
-    // (128, 128) and the MLA shape (192, 128) (flash_mla_backward_kernel.py);
-    // MLA has no sliding-window form
-    if (a->head_dim_v < 0) return FGQA_ERR_INVALID_ARGUMENT;
-    const int dv = a->head_dim_v == 0 ? a->head_dim : a->head_dim_v;
-    if (dv != kHeadDim || (a->head_dim != kHeadDim && a->head_dim != 192)) return FGQA_ERR_UNSUPPORTED;
-    if (a->head_dim == 192 && a->window_size > 0) return FGQA_ERR_UNSUPPORTED;
-    const int group = a->num_q_heads / a->num_kv_heads;
-    if (a->kv_head_split < 0 || a->kv_head_split > group || (a->kv_head_split > 0 && group % a->kv_head_split != 0))
-        return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->dq_kernel < FGQA_KERNEL_AUTO || a->dq_kernel > FGQA_KERNEL_SPLIT) return FGQA_ERR_INVALID_ARGUMENT;
-    // the 192-wide dQ kernel needs one wave per SIMD: it has no split form
-    if (a->dq_kernel == FGQA_KERNEL_SPLIT && a->head_dim == 192) return FGQA_ERR_UNSUPPORTED;
-    // query rows past sq must read as zero (rows may not overlap)
-    if (a->q_stride[1] < a->head_dim || a->grad_o_stride[1] < kHeadDim) return FGQA_ERR_UNSUPPORTED;
-    const int64_t lim = (int64_t)1 << 31;
-    if ((int64_t)(a->seqlen_q + 128) * a->q_stride[1] * 2 >= lim ||
-        (int64_t)(a->seqlen_q + 128) * a->grad_o_stride[1] * 2 >= lim ||
-        (int64_t)(a->seqlen_kv + 128) * a->k_stride[1] * 2 >= lim ||
-        (int64_t)(a->seqlen_kv + 128) * a->v_stride[1] * 2 >= lim)
-        return FGQA_ERR_UNSUPPORTED;
-    // the row statistics are addressed through one buffer resource
-    if ((int64_t)a->batch * a->num_q_heads * a->seqlen_q * 8 >= lim) return FGQA_ERR_UNSUPPORTED;
-    return FGQA_OK;
-}
-
-// The query-side tensors (q, o, lse, grad_o, grad_q) may be NULL when there
-// are no query rows, and the key-side ones (k, v, grad_k, grad_v) when there
-// are no keys: nothing reads or writes them then.
-int validate_backward_pointers(const fgqa_prefill_backward_args* a) {
-    if (a->seqlen_q > 0 && (a->q == nullptr || a->o == nullptr || a->lse == nullptr || a->grad_o == nullptr ||
-                            a->grad_q == nullptr))
-        return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->seqlen_kv > 0 && (a->k == nullptr || a->v == nullptr || a->grad_k == nullptr || a->grad_v == nullptr))
-        return FGQA_ERR_INVALID_ARGUMENT;
-    const void* ptrs[8] = {a->q, a->k, a->v, a->o, a->grad_o, a->grad_q, a->grad_k, a->grad_v};
-    for (const void* ptr : ptrs)
-        if (!aligned16(ptr)) return FGQA_ERR_UNSUPPORTED;
-    const int64_t* strides[8] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride,
-                                 a->grad_o_stride, a->grad_q_stride, a->grad_k_stride, a->grad_v_stride};
-    for (const int64_t* s : strides)
-        for (int i = 0; i < 3; ++i)
-            if (s[i] & 7) return FGQA_ERR_UNSUPPORTED;
-    return FGQA_OK;
-}
-
-// Query heads per dK/dV workgroup: all G query heads of a KV head (dK/dV
-// written once, straight from registers) unless that leaves fewer than 2
-// workgroups per CU; then the heads are split over workgroups, each writing
-// an fp32 partial that bwd_dkdv_reduce_kernel sums.  Under a sliding window
-// every key block carries the same work, so one workgroup per CU (the
-// kernel's occupancy) is enough and halves the partials.  The caller's
-// kv_head_split field, when nonzero, sets n (a divisor of G, validated).
-BwdPlan plan_backward(const fgqa_prefill_backward_args* a, int cus) {
-    BwdPlan pl;
-    const int group = a->num_q_heads / a->num_kv_heads;
-    const int64_t base = ceil_div(a->seqlen_kv, kKvKeys) * (int64_t)a->num_kv_heads * a->batch;
-    const int64_t want = (a->window_size > 0 ? 1 : 2) * (int64_t)cus;
-    pl.n_hsplit = group;
-    for (int d = 1; d <= group; ++d)
-        if (group % d == 0 && base * d >= want) {
-            pl.n_hsplit = d;
-            break;
-        }
-    if (a->kv_head_split > 0) pl.n_hsplit = a->kv_head_split;
-    const size_t rows_q = (size_t)a->batch * a->num_q_heads * a->seqlen_q;
-    const size_t rows_kv = (size_t)a->batch * a->num_kv_heads * a->seqlen_kv;
-    pl.stat_bytes = round256(2 * rows_q * sizeof(float));
-    const size_t parts = pl.n_hsplit > 1 ? (size_t)pl.n_hsplit * rows_kv * sizeof(float) : 0;
-    pl.part_k_bytes = round256(parts * backward_dqk(a));
-    pl.part_v_bytes = round256(parts * kHeadDim);
-    pl.ws_bytes = pl.stat_bytes + pl.part_k_bytes + pl.part_v_bytes;
-    return pl;
-}
-
-}  // namespace
 }  // namespace fgqa
 
 using namespace fgqa;
 
 extern "C" int fgqa_prefill_backward_workspace_bytes(const fgqa_prefill_backward_args* a, size_t* bytes) {
     if (bytes == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
-    const int st = validate_backward(a);
+    const int st = plan::validate_backward(a);
     if (st != FGQA_OK) return st;
     const int cus = device_cu_count();
     if (cus <= 0) return FGQA_ERR_HIP;
-    *bytes = plan_backward(a, cus).ws_bytes;
+    *bytes = plan::plan_backward(a, cus).ws_bytes;
     return FGQA_OK;
 }
 
 extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, void* stream) {
-    int st = validate_backward(a);
+    int st = plan::validate_backward(a);
     if (st != FGQA_OK) return st;
     if (a->batch == 0 || (a->seqlen_q == 0 && a->seqlen_kv == 0)) return FGQA_OK;
-    st = validate_backward_pointers(a);
+    st = plan::validate_backward_pointers(a);
     if (st != FGQA_OK) return st;
     const int cus = device_cu_count();
     if (cus <= 0) return FGQA_ERR_HIP;
-    const BwdPlan pl = plan_backward(a, cus);
+    const plan::BwdPlan pl = plan::plan_backward(a, cus);
+    // (every count below fits the 32-bit fields of BwdParams)
+    st = plan::check_backward_grid(a, pl);
+    if (st != FGQA_OK) return st;
 
     // NULL with 0 bytes: the library's buffer; a call that needs no
     // workspace (no query rows and no head split) takes none.
@@ -1297,9 +1201,6 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     const int64_t rows_kv = (int64_t)p.batch * p.hkv * p.skv;
     const int64_t kv_units = (int64_t)p.n_kvblocks * p.kv_streams;
     const int64_t q_units = (int64_t)p.n_qunits * p.q_streams;
-    if (ceil_div(rows_q, 16) >= ((int64_t)1 << 31) || ceil_div(rows_kv, 16) >= ((int64_t)1 << 31) ||
-        kv_units >= ((int64_t)1 << 31) || q_units >= ((int64_t)1 << 31))
-        return FGQA_ERR_UNSUPPORTED;
 
     // Few dQ units (fewer than 4 per CU): split each unit's key range over two
     // wave groups, as the forward does.  Under a sliding window the units
@@ -1307,7 +1208,7 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     // the whole-range kernel is faster.  The caller's dq_kernel field can
     // force either (the 192-wide dQ kernel has no split form: validated).
     const bool swa = p.window > 0;
-    const bool mla = backward_dqk(a) == 192;
+    const bool mla = a->head_dim == 192;
     const bool dq_split = a->dq_kernel == FGQA_KERNEL_AUTO ? (q_units < 4 * (int64_t)cus && !swa && !mla)
                                                            : a->dq_kernel == FGQA_KERNEL_SPLIT;
     // kernel table: [swa] of dK/dV, dQ, split dQ

@@ -1134,11 +1134,7 @@ __global__ __launch_bounds__(2 * kPfThreads, 1) void prefill_wide_persistent_ker
 // Merge scratch of the kernels that split a unit's KV range over two
 // workgroups, in the layout of a caller workspace: the arrival counters (4
 // words per unit pair) in the first FGQA_PREFILL_WORKSPACE_ZERO_BYTES, then
-// two partial-result slots per pair.
-static_assert(4 * sizeof(unsigned) * kPwMaxSplit <= FGQA_PREFILL_WORKSPACE_ZERO_BYTES, "counters");
-constexpr size_t merge_scratch_bytes_for(int64_t pairs) {
-    return (size_t)FGQA_PREFILL_WORKSPACE_ZERO_BYTES + (size_t)pairs * 2 * kPfPartFloats * sizeof(float);
-}
+// two partial-result slots per pair (plan::merge_scratch_bytes_for).
 
 // The library's merge scratch for calls that pass no workspace (kPwMaxSplit
 // pairs; held by every device the library runs on until the process ends; the
@@ -1147,7 +1143,7 @@ constexpr size_t merge_scratch_bytes_for(int64_t pairs) {
 // up once per device (hipGetSymbolAddress, with that device current) and only
 // that pointer is passed to kernels.  Launches that overlap on one device
 // share it and would race: such callers pass workspaces of their own.
-static __device__ __align__(256) unsigned char pw_scratch_mem[merge_scratch_bytes_for(kPwMaxSplit)];
+static __device__ __align__(256) unsigned char pw_scratch_mem[plan::merge_scratch_bytes_for(kPwMaxSplit)];
 
 namespace {
 
@@ -1170,106 +1166,9 @@ int pw_scratch(unsigned char** mem) {
     return FGQA_OK;
 }
 
-// Unit pairs of the wide kernel: 256-row units of up to 8 heads of a KV group.
-int64_t wide_pairs(const fgqa_prefill_args* a) {
-    const int group = a->num_q_heads / a->num_kv_heads;
-    const int hbw = group % 8 == 0 ? 8 : group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
-    const int64_t units = ceil_div(a->seqlen_q, 256 / hbw) * (int64_t)(group / hbw) * a->num_kv_heads * a->batch;
-    return (units + 1) / 2;
-}
-
-// Whether the 256-row kernels run unit pairs on two workgroups each (at most
-// kPwMaxSplit pairs and one pair per two CUs; the tall kernel only under a
-// causal mask, where units differ in length) rather than whole units on a
-// persistent grid.
-bool wide_on_pairs(const fgqa_prefill_args* a, int cus) {
-    const int64_t pairs = wide_pairs(a);
-    return pairs <= kPwMaxSplit && 2 * pairs <= cus;
-}
-bool tall_on_pairs(const fgqa_prefill_args* a, int cus) { return a->causal && wide_on_pairs(a, cus); }
-
-// The kernel shape a validated call runs on a device with `cus` CUs: the
-// caller's `kernel`, or for AUTO the choice by grid size:
-//  - wide: causal, no window or sink, and the wide kernel's unit pairs fill
-//    the CUs (two workgroups per pair, within 1/8 of one per CU; the MLA
-//    shape 83.9 -> 82.4 us).  Forced, it also runs the window / sink form (at the reference's
-//    window of 512 in 27.5 us, against 26.1 us for the whole-range kernel);
-//  - split: fewer than 4 of the 128-row units per CU, no window or sink: each
-//    unit's KV range runs on two wave groups, so a CU never runs a long unit
-//    with one wave per SIMD, and each CU gets a share of the units whose tile
-//    counts add up evenly;
-//  - wide again for the causal head-dim-128 grids left (at least 4 of the
-//    128-row units per CU), as whole 256-row units on a persistent grid
-//    (config 5: 7.84 -> 7.00 ms against the whole-range kernel);
-//  - whole: the rest (a sliding window gives every unit about the same number
-//    of tiles: nothing to balance).
-int prefill_choice(const fgqa_prefill_args* a, int cus) {
-    if (a->kernel != FGQA_KERNEL_AUTO) return a->kernel;
-    const int group = a->num_q_heads / a->num_kv_heads;
-    const int hb = group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
-    const bool swa = a->window_size > 0 || a->sink != nullptr;
-    const int64_t units = ceil_div(a->seqlen_q, 128 / hb) * (int64_t)(group / hb) * a->num_kv_heads * a->batch;
-    const int64_t pairs = wide_pairs(a);
-    const int64_t wide_grid = 16 * ceil_div(pairs, 8);
-    if (!swa && a->causal && pairs <= kPwMaxSplit && wide_grid <= cus && 8 * wide_grid >= 7 * (int64_t)cus)
-        return FGQA_KERNEL_WIDE;
-    // causal, no window: the persistent wide kernel from 2 units per CU on (measured on
-    // head dims 128 and 192 from 512 to 16384 units: 3-14 % ahead of split and whole);
-    // below that the split kernel's shorter ranges fill the chip better
-    if (!swa && a->causal) return units < 2 * (int64_t)cus ? FGQA_KERNEL_SPLIT : FGQA_KERNEL_WIDE;
-    if (units < 4 * (int64_t)cus && !swa) return FGQA_KERNEL_SPLIT;
-    return FGQA_KERNEL_WHOLE;
-}
-
-// Merge scratch bytes a validated call with kernel `choice` needs on a device
-// with `cus` CUs: the 256-row kernels on their pair grid (at most kPwMaxSplit
-// pairs, one per two CUs) split units only under a causal mask, where units
-// differ in length; everything else needs none.
-size_t merge_scratch_bytes(const fgqa_prefill_args* a, int choice, int cus) {
-    if ((choice != FGQA_KERNEL_WIDE && choice != FGQA_KERNEL_TALL) || !a->causal) return 0;
-    if (a->batch == 0 || a->seqlen_q == 0 || !wide_on_pairs(a, cus)) return 0;
-    return merge_scratch_bytes_for(wide_pairs(a));
-}
-
-int validate_prefill(const fgqa_prefill_args* a) {
-    if (a == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->batch < 0 || a->seqlen_q < 0 || a->seqlen_kv < 0 || a->num_q_heads <= 0 ||
-        a->num_kv_heads <= 0 || a->head_dim <= 0)
-        return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->num_q_heads % a->num_kv_heads != 0) return FGQA_ERR_INVALID_ARGUMENT;
-    if (!isfinite(a->scale)) return FGQA_ERR_INVALID_ARGUMENT;
-    // a sliding window is a causal window (flash_swa_kernel.py: kv <= q)
-    if (a->window_size < 0 || (a->window_size > 0 && !a->causal)) return FGQA_ERR_INVALID_ARGUMENT;
-    for (int i = 0; i < 3; ++i)
-        if (a->q_stride[i] < 0 || a->k_stride[i] < 0 || a->v_stride[i] < 0 || a->o_stride[i] < 0)
-            return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->head_dim_v < 0) return FGQA_ERR_INVALID_ARGUMENT;
-    const int dv = a->head_dim_v == 0 ? a->head_dim : a->head_dim_v;
-    // (128, 128) and the MLA shape (192, 128); MLA has no window / sink form
-    if (dv != kHeadDim || (a->head_dim != kHeadDim && a->head_dim != 192)) return FGQA_ERR_UNSUPPORTED;
-    if (a->head_dim == 192 && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
-    if (a->kernel < FGQA_KERNEL_AUTO || a->kernel > FGQA_KERNEL_TALL) return FGQA_ERR_INVALID_ARGUMENT;
-    // the tall kernel: head dim 128, no window or sink
-    if (a->kernel == FGQA_KERNEL_TALL && (a->head_dim != kHeadDim || a->window_size > 0 || a->sink != nullptr))
-        return FGQA_ERR_UNSUPPORTED;
-    // the window / sink variant has no split form
-    if (a->kernel == FGQA_KERNEL_SPLIT && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
-    const int64_t lim = (int64_t)1 << 31;
-    if ((int64_t)(a->seqlen_q + 128) * a->q_stride[1] * 2 >= lim ||
-        (int64_t)(a->seqlen_kv + 128) * a->k_stride[1] * 2 >= lim ||
-        (int64_t)(a->seqlen_kv + 128) * a->v_stride[1] * 2 >= lim)
-        return FGQA_ERR_UNSUPPORTED;
-    if (a->batch == 0 || a->seqlen_q == 0) return FGQA_OK;
-    if (a->q == nullptr || a->k == nullptr || a->v == nullptr || a->o == nullptr)
-        return FGQA_ERR_INVALID_ARGUMENT;
-    if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o))
-        return FGQA_ERR_UNSUPPORTED;
-    // (O rows go out as 16-byte stores, so O's strides need 8 elements too)
-    for (int i = 0; i < 3; ++i)
-        if ((a->q_stride[i] & 7) || (a->k_stride[i] & 7) || (a->v_stride[i] & 7) || (a->o_stride[i] & 7))
-            return FGQA_ERR_UNSUPPORTED;
-    return FGQA_OK;
-}
+using plan::tall_on_pairs;
+using plan::wide_on_pairs;
+using plan::wide_pairs;
 
 }  // namespace
 }  // namespace fgqa
@@ -1277,44 +1176,37 @@ int validate_prefill(const fgqa_prefill_args* a) {
 using namespace fgqa;
 
 extern "C" int fgqa_prefill_kernel_choice(const fgqa_prefill_args* a, int32_t* kernel) {
-    int st = validate_prefill(a);
+    int st = plan::validate_prefill(a);
     if (st != FGQA_OK) return st;
     if (kernel == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
     const int cus = device_cu_count();
     if (cus <= 0) return FGQA_ERR_HIP;
-    *kernel = prefill_choice(a, cus);
+    *kernel = plan::prefill_choice(a, cus);
     return FGQA_OK;
 }
 
 extern "C" int fgqa_prefill_kernel_name(const fgqa_prefill_args* a, const char** name) {
-    int st = validate_prefill(a);
+    int st = plan::validate_prefill(a);
     if (st != FGQA_OK) return st;
     if (name == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
     const int cus = device_cu_count();
     if (cus <= 0) return FGQA_ERR_HIP;
-    switch (prefill_choice(a, cus)) {
-        case FGQA_KERNEL_WHOLE: *name = "prefill_kernel"; break;
-        case FGQA_KERNEL_SPLIT: *name = "prefill_split_kernel"; break;
-        case FGQA_KERNEL_WIDE:
-            *name = wide_on_pairs(a, cus) ? "prefill_wide_kernel" : "prefill_wide_persistent_kernel";
-            break;
-        default: *name = tall_on_pairs(a, cus) ? "prefill_tall_pairs_kernel" : "prefill_tall_persistent_kernel"; break;
-    }
+    *name = plan::prefill_kernel_name(a, cus);
     return FGQA_OK;
 }
 
 extern "C" int fgqa_prefill_workspace_bytes(const fgqa_prefill_args* a, size_t* bytes) {
-    int st = validate_prefill(a);
+    int st = plan::validate_prefill(a);
     if (st != FGQA_OK) return st;
     if (bytes == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
     const int cus = device_cu_count();
     if (cus <= 0) return FGQA_ERR_HIP;
-    *bytes = merge_scratch_bytes(a, prefill_choice(a, cus), cus);
+    *bytes = plan::merge_scratch_bytes(a, plan::prefill_choice(a, cus), cus);
     return FGQA_OK;
 }
 
 extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
-    int st = validate_prefill(a);
+    int st = plan::validate_prefill(a);
     if (st != FGQA_OK) return st;
     if (a->batch == 0 || a->seqlen_q == 0) return FGQA_OK;
 
@@ -1363,9 +1255,9 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
     if (units >= ((int64_t)1 << 31)) return FGQA_ERR_UNSUPPORTED;
     const int cus = device_cu_count();
     if (cus <= 0) return FGQA_ERR_HIP;
-    const int choice = prefill_choice(a, cus);
+    const int choice = plan::prefill_choice(a, cus);
     // merge scratch: the caller's workspace, or with none the library's
-    if (const size_t need = merge_scratch_bytes(a, choice, cus); need > 0) {
+    if (const size_t need = plan::merge_scratch_bytes(a, choice, cus); need > 0) {
         unsigned char* ws = static_cast<unsigned char*>(a->workspace);
         if (ws == nullptr && a->workspace_bytes == 0) {
             if (const int e = pw_scratch(&ws); e != FGQA_OK) return e;

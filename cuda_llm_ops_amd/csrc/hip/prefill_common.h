@@ -9,6 +9,7 @@
 #include <type_traits>
 
 #include "fgqa_device.h"
+#include "../host/fgqa_plan.h"
 
 namespace fgqa {
 
@@ -69,11 +70,10 @@ constexpr int kPwMaxSplit = 128;
 // floats of one partial-result slot (O, running max and sum of every lane of
 // the 256-row unit's waves): 8 waves x 66 or 4 waves x 132 floats per lane
 constexpr int kPfPartFloats = 2 * 4 * 66 * kWave;
-// bytes of merge scratch a launch with `pairs` split-capable unit pairs needs:
-// the partial slots, then the counter words
-constexpr int64_t pw_scratch_bytes(int64_t pairs) {
-    return pairs * (2 * (int64_t)kPfPartFloats * 4 + 16);
-}
+// (the host planner sizes the merge scratch from the same figures)
+static_assert(kPwMaxSplit == plan::kPrefillMaxSplit && kPfPartFloats == plan::kPrefillPartFloats,
+              "merge scratch layout");
+static_assert(4 * sizeof(unsigned) * kPwMaxSplit <= FGQA_PREFILL_WORKSPACE_ZERO_BYTES, "counters");
 
 // Rank -> unit.  Units are ranked heaviest first (the causal KV range grows
 // with the query block), so the dispatcher hands long units out before short

@@ -403,46 +403,14 @@ __global__ __launch_bounds__(kSpWaves * kWave, 2) void sparse_prefill_kernel(Spa
     }
 }
 
-namespace {
+static_assert(kSpWaves == plan::kSparseWaves, "waves per sparse workgroup");
 
-int validate_sparse(const fgqa_sparse_prefill_args* a) {
-    if (a == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->batch < 0 || a->seqlen_q < 0 || a->seqlen_kv < 0 || a->num_q_heads <= 0 || a->num_kv_heads <= 0 ||
-        a->head_dim <= 0 || a->num_sparse_kv < 1)
-        return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->num_q_heads % a->num_kv_heads != 0) return FGQA_ERR_INVALID_ARGUMENT;
-    if (!isfinite(a->scale)) return FGQA_ERR_INVALID_ARGUMENT;
-    for (int i = 0; i < 3; ++i)
-        if (a->q_stride[i] < 0 || a->k_stride[i] < 0 || a->v_stride[i] < 0 || a->o_stride[i] < 0 ||
-            a->idx_stride[i] < 0)
-            return FGQA_ERR_INVALID_ARGUMENT;
-    if (a->head_dim != kHeadDim) return FGQA_ERR_UNSUPPORTED;
-    const int64_t lim = (int64_t)1 << 31;
-    if ((int64_t)a->seqlen_kv * a->k_stride[1] * 2 + 256 >= lim ||
-        (int64_t)a->seqlen_kv * a->v_stride[1] * 2 + 256 >= lim ||
-        (int64_t)a->num_q_heads * a->q_stride[2] * 2 >= lim || (int64_t)a->num_sparse_kv * 4 >= lim)
-        return FGQA_ERR_UNSUPPORTED;
-    if (a->batch == 0 || a->seqlen_q == 0) return FGQA_OK;
-    // (with Skv = 0 no K/V row is read: k and v may be null)
-    if (a->q == nullptr || a->o == nullptr || a->kv_indices == nullptr ||
-        (a->seqlen_kv > 0 && (a->k == nullptr || a->v == nullptr)))
-        return FGQA_ERR_INVALID_ARGUMENT;
-    if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o) ||
-        (reinterpret_cast<uintptr_t>(a->kv_indices) & 3u))
-        return FGQA_ERR_UNSUPPORTED;
-    for (int i = 0; i < 3; ++i)
-        if ((a->q_stride[i] & 7) || (a->k_stride[i] & 7) || (a->v_stride[i] & 7) || (a->o_stride[i] & 7))
-            return FGQA_ERR_UNSUPPORTED;
-    return FGQA_OK;
-}
-
-}  // namespace
 }  // namespace fgqa
 
 using namespace fgqa;
 
 extern "C" int fgqa_sparse_prefill_bf16(const fgqa_sparse_prefill_args* a, void* stream) {
-    int st = validate_sparse(a);
+    int st = plan::validate_sparse(a);
     if (st != FGQA_OK) return st;
     if (a->batch == 0 || a->seqlen_q == 0) return FGQA_OK;
 

@@ -30,7 +30,9 @@ extern "C" {
 enum fgqa_status {
     FGQA_OK = 0,
     FGQA_ERR_INVALID_ARGUMENT = -1, /* null pointer, negative size, Hq % Hkv != 0 ... */
-    FGQA_ERR_UNSUPPORTED = -2,      /* valid but not implemented: head_dim, group size, alignment */
+    FGQA_ERR_UNSUPPORTED = -2,      /* valid but not implemented: head_dim, group size, alignment,
+                                       sequence lengths above 2^30, grids of 2^31 workgroups or more,
+                                       one sequence's K/V/Q span reaching 2 GiB */
     FGQA_ERR_WORKSPACE = -3,        /* caller workspace smaller than fgqa_decode_workspace_bytes */
     FGQA_ERR_HIP = -4               /* a HIP runtime call or kernel launch failed */
 };

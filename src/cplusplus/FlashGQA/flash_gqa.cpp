@@ -1,5 +1,7 @@
 // C++ operator entry points of the FlashGQA path, implemented over the C ABI
 // (include/fgqa.h).  Host-only C++: no HIP types or calls in this file.
+#include <climits>
+#include <cstdint>
 #include <cstring>
 
 #include "FlashGQA/decode_flash_gqa_kernel.h"
@@ -9,6 +11,14 @@
 
 namespace {
 thread_local int g_last_status = FGQA_OK;
+
+// a * b * c, or INT64_MAX when the product overflows: the C ABI refuses such
+// a stride (FGQA_ERR_UNSUPPORTED) instead of the product wrapping around.
+int64_t mul3(int64_t a, int64_t b, int64_t c) {
+    int64_t ab = 0, abc = 0;
+    if (__builtin_mul_overflow(a, b, &ab) || __builtin_mul_overflow(ab, c, &abc)) return INT64_MAX;
+    return abc;
+}
 
 fgqa_decode_args contiguous_decode(const bf16_t* q, const bf16_t* k, const bf16_t* v, float scale, bf16_t* o,
                                    int batchSize, int seqLength, int numQueryHeads, int numKvHeads, int headDim) {
@@ -29,7 +39,7 @@ fgqa_decode_args contiguous_decode(const bf16_t* q, const bf16_t* k, const bf16_
     a.q_stride[1] = headDim;
     a.o_stride[0] = a.q_stride[0];
     a.o_stride[1] = a.q_stride[1];
-    a.k_stride[0] = (int64_t)seqLength * numKvHeads * headDim;
+    a.k_stride[0] = mul3(seqLength, numKvHeads, headDim);
     a.k_stride[1] = (int64_t)numKvHeads * headDim;
     a.k_stride[2] = headDim;
     for (int i = 0; i < 3; ++i) a.v_stride[i] = a.k_stride[i];
@@ -90,7 +100,12 @@ void LaunchFlashGqaBf16KernelPaged(const bf16_t* q, const void* kCache, const vo
     a.block_table = blockTable;
     a.seqlens = seqLengths;
     a.batch = batchSize;
-    a.max_seqlen = (maxPagesPerSeq > 0 && pageSize > 0) ? maxPagesPerSeq * pageSize : 0;
+    const int64_t max_tokens = (maxPagesPerSeq > 0 && pageSize > 0) ? (int64_t)maxPagesPerSeq * pageSize : 0;
+    if (max_tokens > INT_MAX) {   // the C ABI's max_seqlen is an int
+        g_last_status = FGQA_ERR_UNSUPPORTED;
+        return;
+    }
+    a.max_seqlen = (int)max_tokens;
     a.num_q_heads = numQueryHeads;
     a.num_kv_heads = numKvHeads;
     a.head_dim = headDim;
@@ -105,7 +120,7 @@ void LaunchFlashGqaBf16KernelPaged(const bf16_t* q, const void* kCache, const vo
     a.q_stride[1] = headDim;
     a.o_stride[0] = a.q_stride[0];
     a.o_stride[1] = a.q_stride[1];
-    a.k_stride[0] = (int64_t)pageSize * numKvHeads * headDim;
+    a.k_stride[0] = mul3(pageSize, numKvHeads, headDim);
     a.k_stride[1] = (int64_t)numKvHeads * headDim;
     a.k_stride[2] = headDim;
     for (int i = 0; i < 3; ++i) a.v_stride[i] = a.k_stride[i];
@@ -150,8 +165,8 @@ void LaunchFlashGqaForwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf1
                                      float* lse, int batchSize, int seqLengthQ, int seqLengthKv, int numQueryHeads,
                                      int numKvHeads, int headDim, bool causal) {
     // BSHD: q, o [B, Sq, Hq, D]; k, v [B, Skv, Hkv, D]
-    const int64_t qs[3] = {(int64_t)seqLengthQ * numQueryHeads * headDim, (int64_t)numQueryHeads * headDim, headDim};
-    const int64_t ks[3] = {(int64_t)seqLengthKv * numKvHeads * headDim, (int64_t)numKvHeads * headDim, headDim};
+    const int64_t qs[3] = {mul3(seqLengthQ, numQueryHeads, headDim), (int64_t)numQueryHeads * headDim, headDim};
+    const int64_t ks[3] = {mul3(seqLengthKv, numKvHeads, headDim), (int64_t)numKvHeads * headDim, headDim};
     LaunchFlashGqaForwardBf16KernelStrided(q, k, v, scale, o, lse, batchSize, seqLengthQ, seqLengthKv,
                                            numQueryHeads, numKvHeads, headDim, causal, qs, ks, ks, qs);
 }
@@ -183,11 +198,10 @@ static void backward_bshd(const bf16_t* q, const bf16_t* k, const bf16_t* v, con
     a.head_dim_v = headDimV;
     // BSHD: q, gradQ [B, Sq, Hq, D]; o, gradO [B, Sq, Hq, Dv]; k, gradK [B, Skv, Hkv, D];
     // v, gradV [B, Skv, Hkv, Dv]
-    const int64_t qs[3] = {(int64_t)seqLengthQ * numQueryHeads * headDim, (int64_t)numQueryHeads * headDim, headDim};
-    const int64_t os[3] = {(int64_t)seqLengthQ * numQueryHeads * headDimV, (int64_t)numQueryHeads * headDimV,
-                           headDimV};
-    const int64_t ks[3] = {(int64_t)seqLengthKv * numKvHeads * headDim, (int64_t)numKvHeads * headDim, headDim};
-    const int64_t vs[3] = {(int64_t)seqLengthKv * numKvHeads * headDimV, (int64_t)numKvHeads * headDimV, headDimV};
+    const int64_t qs[3] = {mul3(seqLengthQ, numQueryHeads, headDim), (int64_t)numQueryHeads * headDim, headDim};
+    const int64_t os[3] = {mul3(seqLengthQ, numQueryHeads, headDimV), (int64_t)numQueryHeads * headDimV, headDimV};
+    const int64_t ks[3] = {mul3(seqLengthKv, numKvHeads, headDim), (int64_t)numKvHeads * headDim, headDim};
+    const int64_t vs[3] = {mul3(seqLengthKv, numKvHeads, headDimV), (int64_t)numKvHeads * headDimV, headDimV};
     for (int i = 0; i < 3; ++i) {
         a.q_stride[i] = a.grad_q_stride[i] = qs[i];
         a.o_stride[i] = a.grad_o_stride[i] = os[i];
@@ -239,8 +253,8 @@ void LaunchFlashSwaForwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf1
     a.head_dim = headDim;
     a.causal = 1;
     a.scale = scale;
-    const int64_t qs[3] = {(int64_t)seqLengthQ * numQueryHeads * headDim, (int64_t)numQueryHeads * headDim, headDim};
-    const int64_t ks[3] = {(int64_t)seqLengthKv * numKvHeads * headDim, (int64_t)numKvHeads * headDim, headDim};
+    const int64_t qs[3] = {mul3(seqLengthQ, numQueryHeads, headDim), (int64_t)numQueryHeads * headDim, headDim};
+    const int64_t ks[3] = {mul3(seqLengthKv, numKvHeads, headDim), (int64_t)numKvHeads * headDim, headDim};
     for (int i = 0; i < 3; ++i) {
         a.q_stride[i] = a.o_stride[i] = qs[i];
         a.k_stride[i] = a.v_stride[i] = ks[i];
@@ -278,16 +292,16 @@ void LaunchFlashMlaForwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf1
         g_last_status = FGQA_ERR_INVALID_ARGUMENT;
         return;
     }
-    a.q_stride[0] = (int64_t)seqLengthQ * numQueryHeads * headDimQk;
+    a.q_stride[0] = mul3(seqLengthQ, numQueryHeads, headDimQk);
     a.q_stride[1] = (int64_t)numQueryHeads * headDimQk;
     a.q_stride[2] = headDimQk;
-    a.k_stride[0] = (int64_t)seqLengthKv * numKvHeads * headDimQk;
+    a.k_stride[0] = mul3(seqLengthKv, numKvHeads, headDimQk);
     a.k_stride[1] = (int64_t)numKvHeads * headDimQk;
     a.k_stride[2] = headDimQk;
-    a.v_stride[0] = (int64_t)seqLengthKv * numKvHeads * headDimV;
+    a.v_stride[0] = mul3(seqLengthKv, numKvHeads, headDimV);
     a.v_stride[1] = (int64_t)numKvHeads * headDimV;
     a.v_stride[2] = headDimV;
-    a.o_stride[0] = (int64_t)seqLengthQ * numQueryHeads * headDimV;
+    a.o_stride[0] = mul3(seqLengthQ, numQueryHeads, headDimV);
     a.o_stride[1] = (int64_t)numQueryHeads * headDimV;
     a.o_stride[2] = headDimV;
     g_last_status = fgqa_prefill_bf16(&a, nullptr);
@@ -314,13 +328,13 @@ void LaunchFlashSgqaForwardBf16Kernel(const bf16_t* q, const bf16_t* k, const bf
     a.num_sparse_kv = numSparseKv;
     a.causal = causal ? 1 : 0;
     a.scale = scale;
-    const int64_t qs[3] = {(int64_t)seqLengthQ * numQueryHeads * headDim, (int64_t)numQueryHeads * headDim, headDim};
-    const int64_t ks[3] = {(int64_t)seqLengthKv * numKvHeads * headDim, (int64_t)numKvHeads * headDim, headDim};
+    const int64_t qs[3] = {mul3(seqLengthQ, numQueryHeads, headDim), (int64_t)numQueryHeads * headDim, headDim};
+    const int64_t ks[3] = {mul3(seqLengthKv, numKvHeads, headDim), (int64_t)numKvHeads * headDim, headDim};
     for (int i = 0; i < 3; ++i) {
         a.q_stride[i] = a.o_stride[i] = qs[i];
         a.k_stride[i] = a.v_stride[i] = ks[i];
     }
-    a.idx_stride[0] = (int64_t)numKvHeads * seqLengthQ * numSparseKv;
+    a.idx_stride[0] = mul3(numKvHeads, seqLengthQ, numSparseKv);
     a.idx_stride[1] = (int64_t)seqLengthQ * numSparseKv;
     a.idx_stride[2] = numSparseKv;
     g_last_status = fgqa_sparse_prefill_bf16(&a, nullptr);

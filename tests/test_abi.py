@@ -120,6 +120,39 @@ def test_decode_rejects_before_launch(kw, code):
     assert _lib.lib().fgqa_decode_bf16(ctypes.byref(a), None) == code
 
 
+@pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="fake device pointers: run only where no GPU could launch")
+def test_noalloc_decode_refuses_oversize_plan_before_launch():
+    """fgqa_decode_bf16_noalloc with a ragged B=1024, Hq=64, 32 K-token plan
+    (256 MiB of partials, past the 32 MiB built-in scratch): FGQA_ERR_WORKSPACE
+    from the host planner, before any HIP call.  A caller workspace is refused
+    outright.  (The GPU suite repeats the refusal over real tensors.)"""
+    L = _lib.lib()
+    a = _decode_args(B=1024, S=32768, Hq=64, Hkv=8, split_tokens=0)
+    a.seqlens = 4096
+    st, need = _ws(a)
+    assert st == 0 and need > 32 << 20
+    assert L.fgqa_decode_bf16_noalloc(ctypes.byref(a), None) == _lib.FGQA_ERR_WORKSPACE
+    b = _decode_args()
+    b.workspace, b.workspace_bytes = 4096, 1 << 20
+    assert L.fgqa_decode_bf16_noalloc(ctypes.byref(b), None) == _lib.FGQA_ERR_INVALID_ARGUMENT
+
+
+def test_extreme_sizes_are_refused_before_launch():
+    """Sizes the kernels' integer widths cannot hold come back as
+    FGQA_ERR_UNSUPPORTED from every entry, with no device call."""
+    L = _lib.lib()
+    a = _decode_args(S=(1 << 30) + 1)
+    a.k_stride[1] = a.v_stride[1] = 0
+    assert _ws(a)[0] == _lib.FGQA_ERR_UNSUPPORTED
+    assert L.fgqa_decode_bf16(ctypes.byref(a), None) == _lib.FGQA_ERR_UNSUPPORTED
+    a = _decode_args(B=3)
+    a.k_stride[0] = (1 << 62)   # batch 2's rows at 2^63 elements
+    assert L.fgqa_decode_bf16(ctypes.byref(a), None) == _lib.FGQA_ERR_UNSUPPORTED
+    p = _prefill_args()
+    p.batch, p.seqlen_q, p.seqlen_kv = 2**31 - 1, 32, 32
+    assert L.fgqa_prefill_bf16(ctypes.byref(p), None) == _lib.FGQA_ERR_UNSUPPORTED
+
+
 def test_decode_rejects_pointers_and_alignment():
     L = _lib.lib()
     a = _decode_args(q=None)

@@ -21,7 +21,9 @@ def test_oracle_tests_pass_under_asan_and_ubsan():
     subprocess.run(["make", "-C", os.path.join(ROOT, "oracle"), "-B", "liboracle_san.so"], check=True,
                    stdout=subprocess.DEVNULL)
     env = dict(os.environ)
-    env["LD_PRELOAD"] = f"{_runtime('libasan.so')} {_runtime('libubsan.so')}"
+    # the sanitizer runtimes first, then whatever the environment preloads already
+    env["LD_PRELOAD"] = " ".join(x for x in (_runtime("libasan.so"), _runtime("libubsan.so"),
+                                             os.environ.get("LD_PRELOAD", "")) if x)
     env["ASAN_OPTIONS"] = "detect_leaks=0:abort_on_error=1"
     env["UBSAN_OPTIONS"] = "print_stacktrace=1:halt_on_error=1"
     env["FGQA_ORACLE_LIB"] = os.path.join(ROOT, "oracle", "liboracle_san.so")

@@ -91,22 +91,25 @@ def test_noalloc_decode_refuses_oversize_plan_and_caller_workspace(cuda):
     import torch
     import cuda_llm_ops_amd._lib as L
     print("noalloc refusals", flush=True)
-    q = torch.zeros((2, 16, 128), dtype=torch.bfloat16, device=cuda)
-    k = torch.zeros((2, 64, 2, 128), dtype=torch.bfloat16, device=cuda)
+    # B=256, Hq=64, Hkv=8, 512 tokens in splits of 128: 4 splits per sequence,
+    # 32.5 MiB of partials.  Every tensor has the shape the struct describes
+    # (K and V 256 MiB each), so even a launch would stay inside them.
+    B, Hq, Hkv, S = 256, 64, 8, 512
+    q = torch.zeros((B, Hq, 128), dtype=torch.bfloat16, device=cuda)
+    k = torch.zeros((B, S, Hkv, 128), dtype=torch.bfloat16, device=cuda)
     o = torch.zeros_like(q)
-    lse = torch.zeros((2, 16), dtype=torch.float32, device=cuda)
-    sl = torch.full((2,), 64, dtype=torch.int32, device=cuda)
-    a = _args(q, k, k, o, lse, sl, 64)
-    # ragged plan of B=1024, 64 heads, 32 K tokens: 256 MiB of partials, recorded
-    # in the struct only (the kernels would read past these small tensors, but
-    # the call is refused before any launch)
-    a.batch, a.num_q_heads, a.num_kv_heads, a.max_seqlen = 1024, 64, 8, 32768
+    lse = torch.zeros((B, Hq), dtype=torch.float32, device=cuda)
+    sl = torch.full((B,), S, dtype=torch.int32, device=cuda)
+    a = _args(q, k, k, o, lse, sl, S)
+    a.split_tokens = 128
     ws = ctypes.c_size_t(0)
     assert L.lib().fgqa_decode_workspace_bytes(ctypes.byref(a), ctypes.byref(ws)) == 0
     assert ws.value > SCRATCH_BYTES
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     assert L.lib().fgqa_decode_bf16_noalloc(ctypes.byref(a), s) == L.FGQA_ERR_WORKSPACE
-    b = _args(q, k, k, o, lse, sl, 64)
+    torch.cuda.synchronize()
+    assert torch.isfinite(lse).all() and bool((lse == 0).all()), "a refused call wrote its outputs"
+    b = _args(q, k, k, o, lse, sl, S)
     b.workspace, b.workspace_bytes = o.data_ptr(), 1 << 20
     assert L.lib().fgqa_decode_bf16_noalloc(ctypes.byref(b), s) == L.FGQA_ERR_INVALID_ARGUMENT
     torch.cuda.synchronize()
