@@ -25,7 +25,11 @@
 // slot t % page), in bf16 or in OCP fp8 e4m3 with per-tensor scales.  fp8 rows
 // are widened to bf16 exactly (v_cvt_scalef32_pk_bf16_fp8, scale 1) as they are
 // staged in LDS; the K scale is folded into the softmax scale and the V scale
-// into the output, so the arithmetic after staging is the bf16 path's.
+// into the output, so the arithmetic after staging is the bf16 path's.  bf16
+// pages of 4 rows or more are read by page segment (min(page, 32) rows of a
+// step): one buffer resource per segment, the wave's pages taken from one
+// vector load of the block table per 64 segments; other pages (and fp8) look
+// up each row's page and form its 64-bit address.
 #include <math.h>
 
 #include "fgqa_device.h"
@@ -89,8 +93,12 @@ __device__ __forceinline__ int clamp_len(const DecodeParams& p, int b) {
     return min(max(len, 0), p.max_seqlen);
 }
 
-// One (split, kv head, batch) item of pass 1.
-template <int kKv>
+// One (split, kv head, batch) item of pass 1.  kSeg (paged caches, 0 or a
+// power of two from one load instruction's rows up to 32): the rows of a
+// 32-token step fall into page segments of kSeg rows (kSeg = min(page, 32)),
+// each read through one buffer resource; 0 is the general form, with a page
+// lookup and a 64-bit address per row.
+template <int kKv, int kSeg = 0>
 __device__ __forceinline__ void dec_item(const DecodeParams& p, unsigned char* smem, int split, int kvh, int b) {
     const int len = clamp_len(p, b);
     const int t_begin = split * p.chunk;
@@ -111,7 +119,8 @@ __device__ __forceinline__ void dec_item(const DecodeParams& p, unsigned char* s
     const int t_end = min(t_begin + p.chunk, len);
 
     const int lane = tid & (kWave - 1);
-    const int wave = tid / kWave;
+    constexpr bool kUni = kSeg > 0;
+    const int wave = kUni ? __builtin_amdgcn_readfirstlane(tid / kWave) : tid / kWave;
     const int l16 = lane & 15;
     const int g4 = lane >> 4;
 
@@ -167,8 +176,50 @@ __device__ __forceinline__ void dec_item(const DecodeParams& p, unsigned char* s
     const int32_t* bt = p.block_table + (int64_t)b * p.bt_stride;
     const int pmask = (1 << p.page_shift) - 1;
     int pg[kRows];
+    // kSeg > 0: segment g of a step (rows kSeg*g .. +kSeg-1, one page) is
+    // read through one buffer resource per cache, starting at the segment's
+    // first row and ending at the split's last token (rows past it read as
+    // zeros).  The wave's segment pages come 64 at a time from one vector
+    // load of the block table (lane l: the wave's segment pt_first + l, its
+    // segments numbered n * kSegs + g for its n-th step) and are taken out
+    // with v_readlane (a scalar load would share its wait counter with the
+    // LDS traffic).  Load instruction i
+    // of a segment reads its rows kR*i .. kR*i + kR - 1 at a per-lane offset
+    // that is the same in every segment and step.  The host picks kSeg only
+    // when a page's bytes stay below 2^31.
+    constexpr int kR = (kKv == kKvPagedFp8) ? 8 : 4;           // rows per load instruction
+    constexpr int kSegs = kUni ? kDecStep / kSeg : 1;          // segments per step
+    constexpr int kPerSeg = kRows / kSegs;                     // load instructions per segment
+    static_assert(!kUni || (kSeg >= kR && kSeg <= kDecStep && kPerSeg * kSegs == kRows), "page segment");
+    constexpr uint32_t kRowBytes = kHeadDim * kElemBytes;
+    const uint32_t kss_e = (uint32_t)(p.k_ss * kElemBytes);
+    const uint32_t vss_e = (uint32_t)(p.v_ss * kElemBytes);
+    const int64_t ksb_e = p.k_sb * kElemBytes;
+    const int64_t vsb_e = p.v_sb * kElemBytes;
+    const int t_end_u = kUni ? __builtin_amdgcn_readfirstlane(t_end) : t_end;
+    [[maybe_unused]] uint32_t kvoff[kPerSeg], vvoff[kPerSeg];
+    if constexpr (kUni) {
+        const int lr = (kKv == kKvPagedFp8) ? fp8_row : g4;             // the lane's row in an instruction
+        const int cb = (kKv == kKvPagedFp8) ? fp8_chunk * 16 : l16 * 16;
+#pragma unroll
+        for (int i = 0; i < kPerSeg; ++i) {
+            kvoff[i] = (uint32_t)(kR * i + lr) * kss_e + cb;
+            vvoff[i] = (uint32_t)(kR * i + lr) * vss_e + cb;
+        }
+    }
+    [[maybe_unused]] int pt_lane = 0;       // block table entry of segment pt_first + lane
+    [[maybe_unused]] int pt_first = -kWave;
+    [[maybe_unused]] auto pt_load = [&](int first) {
+        const int n = first + lane;
+        const int tok = min(t_begin + (wave + kDecWaves * (n / kSegs)) * kDecStep + kSeg * (n % kSegs), t_end_u - 1);
+        pt_lane = bt[tok >> p.page_shift];
+        pt_first = first;
+    };
+    if constexpr (kUni) pt_load(0);
     auto fetch_pages = [&](int s) {
-        if constexpr (kKv != kKvContig) {
+        if constexpr (kUni) {
+            (void)s;   // the pages are taken out in load_step
+        } else if constexpr (kKv != kKvContig) {
 #pragma unroll
             for (int r = 0; r < kRows; ++r) {
                 const int tok = min(t_begin + s * kDecStep + row_of(r), t_end - 1);
@@ -178,7 +229,29 @@ __device__ __forceinline__ void dec_item(const DecodeParams& p, unsigned char* s
     };
     auto load_step = [&](int s) {
         const int t0 = t_begin + s * kDecStep;
-        if constexpr (kKv == kKvContig) {
+        if constexpr (kUni) {
+            const int n0 = ((s - wave) / kDecWaves) * kSegs;   // the wave's first segment of step s
+            if (n0 + kSegs > pt_first + kWave) pt_load(n0);
+#pragma unroll
+            for (int g = 0; g < kSegs; ++g) {
+                pg[g] = min(max(__builtin_amdgcn_readlane(pt_lane, n0 - pt_first + g), 0), p.num_pages - 1);
+            }
+#pragma unroll
+            for (int g = 0; g < kSegs; ++g) {
+                const int tok = t0 + kSeg * g;
+                const int nv = min(kSeg, t_end_u - tok);   // rows before the split's end
+                const uint32_t slot = (uint32_t)(tok & pmask);
+                const __amdgpu_buffer_rsrc_t kr = make_rsrc(kbase + pg[g] * ksb_e + slot * kss_e,
+                                                            nv > 0 ? (uint32_t)(nv - 1) * kss_e + kRowBytes : 0u);
+                const __amdgpu_buffer_rsrc_t vr = make_rsrc(vbase + pg[g] * vsb_e + slot * vss_e,
+                                                            nv > 0 ? (uint32_t)(nv - 1) * vss_e + kRowBytes : 0u);
+#pragma unroll
+                for (int i = 0; i < kPerSeg; ++i) {
+                    kreg[g * kPerSeg + i] = buf_load16_nt(kr, kvoff[i]);
+                    vreg[g * kPerSeg + i] = buf_load16_nt(vr, vvoff[i]);
+                }
+            }
+        } else if constexpr (kKv == kKvContig) {
 #pragma unroll
             for (int r = 0; r < 8; ++r) kreg[r] = buf_load16_nt(krs, (uint32_t)(t0 + r * 4 + g4) * kss + l16 * 16);
 #pragma unroll
@@ -439,14 +512,14 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(DecodeParams 
 
 // Pass 1 over the ragged work list: a fixed grid walks the entries, each
 // entry once per kv head (kv head fastest, so heads of one split run together).
-template <int kKv>
+template <int kKv, int kSeg = 0>
 __global__ __launch_bounds__(kDecThreads) void decode_list_kernel(DecodeParams p) {
     __shared__ __attribute__((aligned(16))) unsigned char smem[kDecSmemBytes];
     const int total = p.work[0] * p.hkv;
     for (int item = blockIdx.x; item < total; item += gridDim.x) {
         const int e = p.work[1 + item / p.hkv];
         __syncthreads();   // the previous item's merge buffers alias the staging area
-        dec_item<kKv>(p, smem, e & 0xffff, item % p.hkv, e >> 16);
+        dec_item<kKv, kSeg>(p, smem, e & 0xffff, item % p.hkv, e >> 16);
     }
 }
 
@@ -754,10 +827,27 @@ extern "C" int fgqa_decode_paged(const fgqa_decode_paged_args* a, void* stream) 
         const int64_t max_items = (int64_t)p.batch * plan.nsplit * p.hkv;
         const int grid = (int)(max_items < 2LL * cus ? max_items : 2LL * cus);
         hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p, work);
-        if (a->kv_dtype == FGQA_KV_FP8_E4M3)
-            hipLaunchKernelGGL(decode_list_kernel<kKvPagedFp8>, dim3(grid), dim3(kDecThreads), 0, s, p);
-        else
-            hipLaunchKernelGGL(decode_list_kernel<kKvPagedBf16>, dim3(grid), dim3(kDecThreads), 0, s, p);
+        // bf16 pages of at least 4 rows (one load instruction's) whose bytes
+        // stay below 2^31: page segments of min(page, 32) rows, each read
+        // through one buffer resource (−4 % at BASELINE config 3's lengths
+        // with pages of 16 and 64).  fp8 pages keep the per-row form, which
+        // measured 2 % faster for them.
+        const bool fp8 = a->kv_dtype == FGQA_KV_FP8_E4M3;
+        const bool small_pages = (int64_t)a->page_size * a->k_stride[1] * 2 < ((int64_t)1 << 31) &&
+                                 (int64_t)a->page_size * a->v_stride[1] * 2 < ((int64_t)1 << 31);
+        const int seg = !small_pages ? 0 : a->page_size >= 32 ? 32 : a->page_size >= 4 ? a->page_size : 0;
+        const dim3 g(grid), t(kDecThreads);
+        if (fp8) {
+            hipLaunchKernelGGL((decode_list_kernel<kKvPagedFp8, 0>), g, t, 0, s, p);
+        } else {
+            switch (seg) {
+                case 32: hipLaunchKernelGGL((decode_list_kernel<kKvPagedBf16, 32>), g, t, 0, s, p); break;
+                case 16: hipLaunchKernelGGL((decode_list_kernel<kKvPagedBf16, 16>), g, t, 0, s, p); break;
+                case 8: hipLaunchKernelGGL((decode_list_kernel<kKvPagedBf16, 8>), g, t, 0, s, p); break;
+                case 4: hipLaunchKernelGGL((decode_list_kernel<kKvPagedBf16, 4>), g, t, 0, s, p); break;
+                default: hipLaunchKernelGGL((decode_list_kernel<kKvPagedBf16, 0>), g, t, 0, s, p); break;
+            }
+        }
         if (plan.nsplit > 1)
             hipLaunchKernelGGL(decode_combine_kernel, dim3(p.hkv, p.batch), dim3(kDecThreads), 0, s, p);
     }

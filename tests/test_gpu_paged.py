@@ -65,11 +65,23 @@ def _check(o, lse, o_ref, l_ref, what):
 
 
 @pytest.mark.parametrize("fp8", [False, True])
-@pytest.mark.parametrize("page_size", [1, 16, 64, 256])
+@pytest.mark.parametrize("page_size", [1, 2, 4, 8, 16, 32, 64, 256])
 def test_paged_page_sizes(cuda, page_size, fp8):
     what = f"paged page={page_size} fp8={fp8}"
     print(what, flush=True)
     o, lse, o_ref, l_ref = _case(cuda, 900 + page_size, 3, 16, 2, 700, [700, 1, 333], page_size, fp8)
+    _check(o, lse, o_ref, l_ref, what)
+
+
+@pytest.mark.parametrize("page_size", [4, 8, 16, 32, 128])
+def test_paged_segments_split_inside_pages(cuda, page_size):
+    """bf16 pages read by page segment, with 128-token splits (a split ends
+    inside a page for pages of 256) and lengths that end inside a segment, a
+    load instruction and a page."""
+    what = f"paged segments page={page_size}"
+    print(what, flush=True)
+    lens = [1023, 131, 5, 1024, 769]
+    o, lse, o_ref, l_ref = _case(cuda, 950 + page_size, 5, 16, 2, 1024, lens, page_size, False, split_tokens=128)
     _check(o, lse, o_ref, l_ref, what)
 
 
