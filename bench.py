@@ -517,7 +517,7 @@ def bench_backward(cfg_id, steps, warmup, dev):
                 us_min=round(per[0] * 1e3, 2),
                 roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
                           "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-                          "kernel": "bwd_prep + bwd_dkdv + bwd_dq(_split) + bwd_dkdv_reduce (whole step)",
+                          "kernel": "bwd_dq(_split) + bwd_dkdv + bwd_dkdv_reduce (whole step)",
                           "algorithmic_flops": flops, "executed_mfma_flops": flops * 7 // 5})
 
 
@@ -550,7 +550,7 @@ def bench_swa_backward(steps, warmup, dev, window=512):
                 us_min=round(per[0] * 1e3, 2),
                 roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
                           "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-                          "kernel": "bwd_prep + bwd_dkdv + bwd_dq(_split) + bwd_dkdv_reduce (whole step)",
+                          "kernel": "bwd_dq(_split) + bwd_dkdv + bwd_dkdv_reduce (whole step)",
                           "algorithmic_flops": flops, "executed_mfma_flops": flops * 7 // 5})
 
 
@@ -585,7 +585,7 @@ def bench_mla_backward(steps, warmup, dev):
                 us_min=round(per[0] * 1e3, 2),
                 roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
                           "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-                          "kernel": "bwd_prep + bwd_dkdv<192> + bwd_dq<192> (whole step)",
+                          "kernel": "bwd_dq<192> + bwd_dkdv<192> (whole step)",
                           "algorithmic_flops": flops})
 
 

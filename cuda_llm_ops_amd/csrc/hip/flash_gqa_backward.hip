@@ -18,8 +18,15 @@
 // gradient goes through an atomic: each is owned by exactly one workgroup and
 // P, dP are recomputed where needed.  Results are deterministic.
 //
-// Launches on the caller's stream:
-//   bwd_prep_kernel    per query row: -lse*log2(e) and -delta*scale.
+// Launches on the caller's stream, in this order:
+//   bwd_dq_kernel      query-major, the forward kernel's work unit (128 query
+//                      rows: heads x positions of one KV group, one wave per
+//                      32 rows): first each row's -lse*log2(e) and
+//                      -delta*scale (stored for dK/dV), then per 64-key tile
+//                      S^T = K Q^T, dP^T = V dO^T (Q^T, dO^T in registers,
+//                      K/V tiles in LDS), dS^T on the VALU, dQ^T += K^T dS^T
+//                      (K read transposed).  bwd_dq_split_kernel: the same
+//                      unit with its key range split over two wave groups.
 //   bwd_dkdv_kernel    key-major: a workgroup owns a 128-key block of one KV
 //                      head (wave w: keys 32w..32w+31, K/V rows in registers)
 //                      and loops over (query head of its subset, 32-row query
@@ -27,11 +34,6 @@
 //                      P and dS on the VALU (in place as bf16 A operands),
 //                      dV += P^T dO, dK += dS^T Q (dO/Q read transposed,
 //                      ds_read_b64_tr_b16).  dK/dV stay in registers (fp32).
-//   bwd_dq_kernel      query-major, the forward kernel's work unit (128 query
-//                      rows: heads x positions of one KV group, one wave per
-//                      32 rows): per 64-key tile S^T = K Q^T, dP^T = V dO^T
-//                      (Q^T, dO^T in registers, K/V tiles in LDS), dS^T on the
-//                      VALU, dQ^T += K^T dS^T (K read transposed).
 //   bwd_dkdv_reduce_kernel  only when a KV head's query heads are split over
 //                      several workgroups: sums their fp32 partial dK/dV.
 #include <math.h>
@@ -81,9 +83,6 @@ struct BwdParams {
     int q_streams;    // n_hgroups * hkv * batch
     float scale;
     float scale_log2;   // scale * log2(e)
-    // prep: row -> (b, h, i) by magic-number division when B * Hq * Sq < 2^31
-    int prep_fast;
-    FastDiv div_sq, div_hq;
 };
 
 constexpr int kBwWaves = 4;
@@ -190,41 +189,24 @@ __device__ __forceinline__ void bw_static_for(F&& f) {
     }
 }
 
-// ---------------------------------------------------------------- prep
-// 16 lanes per query row (8 elements each).  Rows are numbered (b, h, i) in
-// the LSE layout [B, Hq, Sq].
-__global__ __launch_bounds__(256) void bwd_prep_kernel(BwdParams p) {
-    const int64_t rows_q = (int64_t)p.batch * p.hq * p.sq;
-    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-    const int part = threadIdx.x & 15;
-    if (row >= rows_q) return;
-    int i, h, b;
-    if (p.prep_fast) {
-        const int r = (int)row;
-        const int bh = fast_div(r, p.div_sq);
-        i = r - bh * p.sq;
-        b = fast_div(bh, p.div_hq);
-        h = bh - b * p.hq;
-    } else {
-        i = (int)(row % p.sq);
-        const int64_t bh = row / p.sq;
-        h = (int)(bh % p.hq);
-        b = (int)(bh / p.hq);
-    }
-    const u32x4_t ov = *reinterpret_cast<const u32x4_t*>(p.o + b * p.o_sb + i * p.o_ss + h * p.o_sh + part * 8);
-    const u32x4_t dv = *reinterpret_cast<const u32x4_t*>(p.dout + b * p.do_sb + i * p.do_ss + h * p.do_sh + part * 8);
-    const bf16x8_t o8 = as_bf16x8(ov), d8 = as_bf16x8(dv);
-    float acc = 0.f;
+// ---------------------------------------------------------------- row statistics
+// -lse*log2(e) and -delta*scale of one query row, delta = sum_d O[d] dO[d],
+// computed by the dQ kernels (which hold the row's dO) and stored for the
+// dK/dV kernel that runs after them.  A lane holds elements 16kk + 8g2 .. +7
+// of the row (kk = 0..7): part 2kk + g2 of 16 eight-element parts.  delta is
+// the parts' sums added as a balanced tree over the part index (partner
+// p ^ 1, then p ^ 2, p ^ 4, p ^ 8), so it does not depend on how the row is
+// spread over lanes.
+__device__ __forceinline__ float row_delta(const bf16x8_t (&oop)[8], const bf16x8_t (&doop)[8]) {
+    float pair[8];   // parts 2kk and 2kk + 1 (the other half-wave holds the second)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc += (float)o8[e] * (float)d8[e];
-    acc = xor_sum(acc, 1);
-    acc = xor_sum(acc, 2);
-    acc = xor_sum(acc, 4);
-    acc = xor_sum(acc, 8);
-    if (part == 0) {
-        p.rowstat[row] = -p.lse[row] * kLog2e;
-        p.rowstat[rows_q + row] = -acc * p.scale;
+    for (int kk = 0; kk < 8; ++kk) {
+        float acc = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += (float)oop[kk][e] * (float)doop[kk][e];
+        pair[kk] = xor_sum(acc, 32);
     }
+    return ((pair[0] + pair[1]) + (pair[2] + pair[3])) + ((pair[4] + pair[5]) + (pair[6] + pair[7]));
 }
 
 // ---------------------------------------------------------------- dK / dV
@@ -614,17 +596,22 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem,
         make_rsrc(p.q + b * p.q_sb + h * p.q_sh, (uint32_t)(p.sq - 1) * qss + D::kRowBytes);
     const __amdgpu_buffer_rsrc_t drs =
         make_rsrc(p.dout + b * p.do_sb + h * p.do_sh, (uint32_t)(p.sq - 1) * dss + kBwRowBytes);
-    bf16x8_t qop[D::kSteps], doop[8];
+    const uint32_t oss = (uint32_t)(p.o_ss * 2);
+    const __amdgpu_buffer_rsrc_t ors =
+        make_rsrc(p.o + b * p.o_sb + h * p.o_sh, (uint32_t)(p.sq - 1) * oss + kBwRowBytes);
+    bf16x8_t qop[D::kSteps], doop[8], oop[8];
 #pragma unroll
     for (int kk = 0; kk < D::kSteps; ++kk)
         qop[kk] = as_bf16x8(buf_load16(qrs, (uint32_t)qrow * qss + (16 * kk + 8 * g2) * 2));
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
+    for (int kk = 0; kk < 8; ++kk) {
         doop[kk] = as_bf16x8(buf_load16(drs, (uint32_t)qrow * dss + (16 * kk + 8 * g2) * 2));
+        oop[kk] = as_bf16x8(buf_load16(ors, (uint32_t)qrow * oss + (16 * kk + 8 * g2) * 2));
+    }
     const int64_t rows_q = (int64_t)p.batch * p.hq * p.sq;
     const int64_t ridx = ((int64_t)b * p.hq + h) * p.sq + qrow;
-    const float nl = (qrow < p.sq) ? p.rowstat[ridx] : 0.f;
-    const float nd = (qrow < p.sq) ? p.rowstat[rows_q + ridx] : 0.f;
+    const float nl = (qrow < p.sq) ? -p.lse[ridx] * kLog2e : 0.f;
+    float nd = 0.f;   // set once O has arrived (after the first tile's loads are issued)
 
     int kv_end = p.skv;
     if (p.causal) kv_end = min(kv_end, min(q_wg0 + qrows, p.sq));
@@ -792,6 +779,12 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem,
     __syncthreads();
     if (n_tiles > 0) issue(0, 0);
     bw_wait_vmem();
+    // the row's statistics, for this kernel's tiles and stored for dK/dV
+    nd = (qrow < p.sq) ? -row_delta(oop, doop) * p.scale : 0.f;
+    if (qrow < p.sq && g2 == 0) {
+        p.rowstat[ridx] = nl;
+        p.rowstat[rows_q + ridx] = nd;
+    }
     __syncthreads();
     using C0 = std::integral_constant<int, 0>;
     using C1 = std::integral_constant<int, 1>;
@@ -860,16 +853,28 @@ __device__ __forceinline__ void dq_unit_pp(const BwdParams& p, unsigned char* sm
     const __amdgpu_buffer_rsrc_t qrs = make_rsrc(p.q + b * p.q_sb + h * p.q_sh, (uint32_t)(p.sq - 1) * qss + kBwRowBytes);
     const __amdgpu_buffer_rsrc_t drs =
         make_rsrc(p.dout + b * p.do_sb + h * p.do_sh, (uint32_t)(p.sq - 1) * dss + kBwRowBytes);
-    bf16x8_t qop[8], doop[8];
+    const uint32_t oss = (uint32_t)(p.o_ss * 2);
+    const __amdgpu_buffer_rsrc_t ors = make_rsrc(p.o + b * p.o_sb + h * p.o_sh, (uint32_t)(p.sq - 1) * oss + kBwRowBytes);
+    bf16x8_t qop[8], doop[8], oop[8];
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
         qop[kk] = as_bf16x8(buf_load16(qrs, (uint32_t)qrow * qss + (16 * kk + 8 * g2) * 2));
         doop[kk] = as_bf16x8(buf_load16(drs, (uint32_t)qrow * dss + (16 * kk + 8 * g2) * 2));
+        oop[kk] = as_bf16x8(buf_load16(ors, (uint32_t)qrow * oss + (16 * kk + 8 * g2) * 2));
     }
     const int64_t rows_q = (int64_t)p.batch * p.hq * p.sq;
     const int64_t ridx = ((int64_t)b * p.hq + h) * p.sq + qrow;
-    const float nl = (qrow < p.sq) ? p.rowstat[ridx] : 0.f;
-    const float nd = (qrow < p.sq) ? p.rowstat[rows_q + ridx] : 0.f;
+    const float nl = (qrow < p.sq) ? -p.lse[ridx] * kLog2e : 0.f;
+    float nd = 0.f;   // set once O has arrived (after the first tiles' loads are issued)
+    // the row's statistics, for this unit's tiles and stored for dK/dV (both
+    // groups hold the same rows: group 0 stores them)
+    auto stats = [&]() {
+        nd = (qrow < p.sq) ? -row_delta(oop, doop) * p.scale : 0.f;
+        if (qrow < p.sq && g2 == 0 && grp == 0) {
+            p.rowstat[ridx] = nl;
+            p.rowstat[rows_q + ridx] = nd;
+        }
+    };
 
     int kv_end = p.skv;
     if (p.causal) kv_end = min(kv_end, min(q_wg0 + qrows, p.sq));
@@ -1029,6 +1034,7 @@ __device__ __forceinline__ void dq_unit_pp(const BwdParams& p, unsigned char* sm
         } else {
             bw_wait_vmem();
         }
+        stats();
         __syncthreads();
         // Both groups pass the same number of barriers: group 1 computes
         // S/dP(0) in an extra leading phase, group 0 ends with an empty one.
@@ -1042,6 +1048,9 @@ __device__ __forceinline__ void dq_unit_pp(const BwdParams& p, unsigned char* sm
         }
         mphase(std::true_type{}, std::false_type{}, n_tiles - 1);
         if (grp == 0) __syncthreads();
+    } else {
+        bw_wait_vmem();
+        stats();
     }
 
     // group 1 hands its dQ^T to group 0 through group 0's (idle) tile
@@ -1185,9 +1194,6 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     p.hs = p.group / pl.n_hsplit;
     p.n_kvblocks = (int)ceil_div(p.skv, kKvKeys);
     p.kv_streams = pl.n_hsplit * p.hkv * p.batch;
-    p.prep_fast = (int64_t)p.batch * p.hq * p.sq < ((int64_t)1 << 31) ? 1 : 0;
-    p.div_sq = make_fast_div(p.sq > 0 ? p.sq : 1);
-    p.div_hq = make_fast_div(p.hq);
     p.n_qblocks32 = (int)ceil_div(p.sq, kKvRows);
     p.hb = (p.group % 4 == 0) ? 4 : (p.group % 2 == 0) ? 2 : 1;
     p.n_hgroups = p.group / p.hb;
@@ -1197,7 +1203,6 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     p.scale_log2 = a->scale * kLog2e;
 
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    const int64_t rows_q = (int64_t)p.batch * p.hq * p.sq;
     const int64_t rows_kv = (int64_t)p.batch * p.hkv * p.skv;
     const int64_t kv_units = (int64_t)p.n_kvblocks * p.kv_streams;
     const int64_t q_units = (int64_t)p.n_qunits * p.q_streams;
@@ -1232,27 +1237,20 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
         if ((st = set_kernel_smem_once(14 + swa, q2_fn[swa], kDqPpSmemBytes)) != FGQA_OK) return st;
     }
 
-    if (rows_q > 0) hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)ceil_div(rows_q, 16)), dim3(256), 0, s, p);
+    // dQ first: its kernels store each row's statistics, which dK/dV reads.
+    // (Without query rows there are no dQ units, and dK/dV reads no row.)
     if (mla) {
-        if (kv_units > 0)
-            hipLaunchKernelGGL((bwd_dkdv_kernel<false, 192>), dim3((unsigned)kv_units), dim3(kBwThreads),
-                               kv_smem_bytes<192>(), s, p);
         if (q_units > 0)
             hipLaunchKernelGGL((bwd_dq_kernel<false, 192>), dim3((unsigned)q_units), dim3(kBwThreads),
                                dq_smem_bytes<192>(), s, p);
+        if (kv_units > 0)
+            hipLaunchKernelGGL((bwd_dkdv_kernel<false, 192>), dim3((unsigned)kv_units), dim3(kBwThreads),
+                               kv_smem_bytes<192>(), s, p);
         if (pl.n_hsplit > 1 && rows_kv > 0)
             hipLaunchKernelGGL(bwd_dkdv_reduce_kernel<192>, dim3((unsigned)ceil_div(rows_kv, 16)), dim3(256), 0, s,
                                p);
         if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
         return FGQA_OK;
-    }
-    if (kv_units > 0) {
-        if (swa)
-            hipLaunchKernelGGL((bwd_dkdv_kernel<true, 128>), dim3((unsigned)kv_units), dim3(kBwThreads), kKvSmemBytes,
-                               s, p);
-        else
-            hipLaunchKernelGGL((bwd_dkdv_kernel<false, 128>), dim3((unsigned)kv_units), dim3(kBwThreads), kKvSmemBytes,
-                               s, p);
     }
     if (q_units > 0 && dq_split) {
         if (swa)
@@ -1268,6 +1266,14 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
         else
             hipLaunchKernelGGL((bwd_dq_kernel<false, 128>), dim3((unsigned)q_units), dim3(kBwThreads), kDqSmemBytes, s,
                                p);
+    }
+    if (kv_units > 0) {
+        if (swa)
+            hipLaunchKernelGGL((bwd_dkdv_kernel<true, 128>), dim3((unsigned)kv_units), dim3(kBwThreads), kKvSmemBytes,
+                               s, p);
+        else
+            hipLaunchKernelGGL((bwd_dkdv_kernel<false, 128>), dim3((unsigned)kv_units), dim3(kBwThreads), kKvSmemBytes,
+                               s, p);
     }
     if (pl.n_hsplit > 1 && rows_kv > 0)
         hipLaunchKernelGGL(bwd_dkdv_reduce_kernel<128>, dim3((unsigned)ceil_div(rows_kv, 16)), dim3(256), 0, s, p);
