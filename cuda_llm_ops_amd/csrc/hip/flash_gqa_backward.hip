@@ -482,6 +482,12 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
             }
             if constexpr (i + kR < kOps) ring[i % kR] = fetch(std::integral_constant<int, i + kR>{});
         };
+        // The scheduler's small-GEMM interleave (LLVM's IGLP strategy 0)
+        // issues the operand reads progressively further ahead of their
+        // MFMAs (up to 14 in flight) instead of just before each; without
+        // it most MFMAs waited on an LDS read (lgkmcnt 0 or 1).  Strategies
+        // 1-3 were slower.
+        __builtin_amdgcn_iglp_opt(0);
         bw_static_for<kS>(op);
         softmax(sc, dpc, bc, m, mx);
         bw_static_for<kOps - kS>([&](auto ic) { op(std::integral_constant<int, kS + decltype(ic)::value>{}); });
@@ -746,6 +752,7 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem,
             }
             if constexpr (i + kR < kOps) ring[i % kR] = fetch(std::integral_constant<int, i + kR>{});
         };
+        __builtin_amdgcn_iglp_opt(0);   // operand reads run ahead, as in the dK/dV step
         bw_static_for<kSd>(op);
         // dS^T = P^T (dP^T - delta) scale as the B operand of dQ^T += K^T dS^T:
         // block kb = 2tb + kh holds registers 8kh .. 8kh+7 of S^T block tb,
