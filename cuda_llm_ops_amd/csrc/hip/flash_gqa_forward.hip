@@ -534,16 +534,13 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) asm volatile("" : "+v"(pop[kb]));
         asm volatile("" : "+v"(l_run));
-        // K reads run 4 MFMAs ahead of their use; the softmax's ~96 VALU ops
-        // spread over the phase's 16 (or 24) MFMAs
-        constexpr int kA = 2 * D::kSteps;
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);       // DS read
-#pragma unroll
-        for (int i = 0; i < kA; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 96 / kA, 0);   // VALU
-            if (i < kA - 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
-        }
+        // The scheduler's small-GEMM interleave (LLVM's IGLP strategy 0)
+        // places the K reads and the softmax's ~96 VALU ops among the
+        // phase's 16 (or 24) MFMAs: 4.9 % faster at the reference's
+        // sliding-window shape than pinning one K read 4 MFMAs ahead and
+        // 96 / 16 VALU ops after each MFMA (strategies 2 and 3, the MFMA /
+        // exp interleaves, were no faster than the pinning).
+        __builtin_amdgcn_iglp_opt(0);
         mask(sn, j + 1);
         // phase B: P(j).V(j) on the MFMA pipe while the row max of S(j+1)
         // runs on the VALU.
