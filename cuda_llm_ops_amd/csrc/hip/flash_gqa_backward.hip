@@ -867,20 +867,36 @@ __device__ __forceinline__ void dq_unit_pp(const BwdParams& p, unsigned char* sm
     for (int kk = 0; kk < 8; ++kk) {
         qop[kk] = as_bf16x8(buf_load16(qrs, (uint32_t)qrow * qss + (16 * kk + 8 * g2) * 2));
         doop[kk] = as_bf16x8(buf_load16(drs, (uint32_t)qrow * dss + (16 * kk + 8 * g2) * 2));
-        oop[kk] = as_bf16x8(buf_load16(ors, (uint32_t)qrow * oss + (16 * kk + 8 * g2) * 2));
+    }
+    if (grp == 0) {
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) oop[kk] = as_bf16x8(buf_load16(ors, (uint32_t)qrow * oss + (16 * kk + 8 * g2) * 2));
     }
     const int64_t rows_q = (int64_t)p.batch * p.hq * p.sq;
     const int64_t ridx = ((int64_t)b * p.hq + h) * p.sq + qrow;
     const float nl = (qrow < p.sq) ? -p.lse[ridx] * kLog2e : 0.f;
     float nd = 0.f;   // set once O has arrived (after the first tiles' loads are issued)
-    // the row's statistics, for this unit's tiles and stored for dK/dV (both
-    // groups hold the same rows: group 0 stores them)
+    // The rows' statistics, for this unit's tiles and stored for dK/dV.  Both
+    // groups hold the same rows (wave w of each, lane for lane), so group 0
+    // alone loads O and computes them, and hands -delta*scale to group 1
+    // through group 1's third K buffer, which group 1 first fills in its first
+    // VALU phase.
+    float* const nd_x = reinterpret_cast<float*>(smem_all + kDqPpGroupBytes + 2 * kDqTileBytes) + wave * kWave + lane;
     auto stats = [&]() {
+        if (grp != 0) return;
         nd = (qrow < p.sq) ? -row_delta(oop, doop) * p.scale : 0.f;
-        if (qrow < p.sq && g2 == 0 && grp == 0) {
+        *nd_x = nd;
+        if (qrow < p.sq && g2 == 0) {
             p.rowstat[ridx] = nl;
             p.rowstat[rows_q + ridx] = nd;
         }
+    };
+    // group 1, after the barrier that follows stats(): the value is read and
+    // awaited before the buffer's first tile load is issued
+    auto stats_in = [&]() {
+        if (grp != 1) return;
+        nd = *nd_x;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     };
 
     int kv_end = p.skv;
@@ -1043,6 +1059,7 @@ __device__ __forceinline__ void dq_unit_pp(const BwdParams& p, unsigned char* sm
         }
         stats();
         __syncthreads();
+        stats_in();
         // Both groups pass the same number of barriers: group 1 computes
         // S/dP(0) in an extra leading phase, group 0 ends with an empty one.
         if (grp == 0) mphase(std::false_type{}, std::true_type{}, -1);
