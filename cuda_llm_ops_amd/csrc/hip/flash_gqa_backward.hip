@@ -215,8 +215,10 @@ __device__ __forceinline__ float row_delta(const bf16x8_t (&oop)[8], const bf16x
 //   phase B: dV += P(t)^T dO(t), dK += dS(t)^T Q(t) on the MFMA pipe
 // with Q/dO(t+2) streaming into the third LDS buffer meanwhile.
 // kSwa: sliding window (a separate instantiation, so the causal kernels carry
-// none of its work).
-template <bool kSwa, int kDk>
+// none of its work).  kAddMask: the mask enters as an additive -inf on S (any
+// nonzero scale); without it (scale 0, where -inf * 0 is not -inf) as a select
+// on P.
+template <bool kSwa, int kDk, bool kAddMask>
 __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
     using D = BwDims<kDk>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -346,14 +348,60 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
     const float scale = p.scale;
     // S = Q K^T and dP = dO V^T of the step in buffer bi: C[q][key], lane
     // (key l32, half g2), register 4i + r <-> query row 8i + 4g2 + r
+    // Element (i, r) of a step's S block is query row q0 + 8i + 4g2 + r; it is
+    // masked (P = 0) when 8i + r < m, with m = key - q0 - 4g2 under the causal
+    // mask, and (window) when 8i + r > mx, mx = key + window - 1 - q0 - 4g2;
+    // steps past n_iter are fully masked.  Rows >= sq need no mask: their dO
+    // rows and -delta*scale read as zero, so P.dO and dS vanish; keys >= skv
+    // only reach their own dK/dV rows, which are never stored.
+    //
+    // kAddMask: the accumulator of a step's S starts at 0 or, on a step whose
+    // block the mask cuts (wave-uniform: the diagonal, the window's edge,
+    // padding), at ninf for each masked element, ninf = -inf times the sign of
+    // scale, so that S * scale * log2(e) is -inf and P = exp2(-inf) = +0 and
+    // dS = 0 * x, the values the select gives (for finite Q and K).  Only the
+    // first MFMA of S's chain differs between the two (its C operand: the
+    // literal 0, or the start values), and the softmax carries no
+    // per-element select: two VALU ops per element fewer.
+    const int wk0 = kv0 + 32 * wave;   // the wave's first key
+    const float ninf = c2 > 0.f ? -INFINITY : INFINITY;
+    auto is_cut = [&](int ts, int q0s) {
+        bool cut = ts >= n_iter || (p.causal && q0s < wk0 + 31);
+        if constexpr (kSwa) cut = cut || q0s + 31 > wk0 + p.window - 1;
+        return cut;
+    };
+    // the start values of a cut step's S block
+    auto bias = [&](int ts, int q0s) {
+        const int m = (ts < n_iter) ? (p.causal ? key - q0s - 4 * g2 : -64) : 64;
+        const int mx = key + p.window - 1 - q0s - 4 * g2;
+        f32x16_t b;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const bool vis = kSwa ? (8 * i + r >= m && 8 * i + r <= mx) : (8 * i + r >= m);
+                b[4 * i + r] = vis ? 0.f : ninf;
+            }
+        return b;
+    };
+    // S's first MFMA (k-step 0), with the mask's start values on cut steps
+    auto s_first = [&](const bf16x8_t& a, int ts, int q0s) -> f32x16_t {
+        f32x16_t z;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) z[i] = 0.f;
+        if (kAddMask && is_cut(ts, q0s)) return mfma32(a, kop[0], bias(ts, q0s));
+        return mfma32(a, kop[0], z);
+    };
     auto sdp = [&](f32x16_t& s, f32x16_t& dp, auto bi_c) {
         constexpr int bi = decltype(bi_c)::value;
         const unsigned char* ql = smem + kKvQOff + bi * kKvTileBytes;
         const unsigned char* dl = smem + kKvDoOff + bi * kKvTileBytes;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) s[i] = dp[i] = 0.f;
+        for (int i = 0; i < 16; ++i) dp[i] = 0.f;
+        s = s_first(*reinterpret_cast<const bf16x8_t*>(ql + roff[0]), 0, qb0 * kKvRows);
+        dp = mfma32(*reinterpret_cast<const bf16x8_t*>(dl + roff[0]), vop[0], dp);
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
+        for (int ks = 1; ks < 8; ++ks) {
             s = mfma32(*reinterpret_cast<const bf16x8_t*>(ql + roff[ks]), kop[ks], s);
             dp = mfma32(*reinterpret_cast<const bf16x8_t*>(dl + roff[ks]), vop[ks], dp);
         }
@@ -365,12 +413,8 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
         }
     };
     // P = exp2(S*scale*log2e - lse*log2e), dS = P (dP - delta) scale, both as
-    // bf16 A operands (k-step ks = registers 8ks .. 8ks+7).  Element (i, r) is
-    // query row q0 + 8i + 4g2 + r; it is masked (P = 0) when 8i + r < m, with
-    // m = key - q0 - 4g2 under the causal mask, and (window) when 8i + r > mx,
-    // mx = key + window - 1 - q0 - 4g2.  Rows >= sq need no mask: their
-    // dO rows and -delta*scale read as zero, so P.dO and dS vanish; keys >= skv
-    // only reach their own dK/dV rows, which are never stored.
+    // bf16 A operands (k-step ks = registers 8ks .. 8ks+7); without kAddMask
+    // the mask above is a select here.
     bf16x8_t pop[2], dsop[2];
     auto softmax = [&](const f32x16_t& s, const f32x16_t& dp, auto bi_c, int m, int mx) {
         constexpr int bi = decltype(bi_c)::value;
@@ -382,9 +426,9 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 float pv = fast_exp2(__builtin_fmaf(s[4 * i + r], c2, nl[r]));
-                if constexpr (kSwa)
+                if constexpr (!kAddMask && kSwa)
                     pv = (8 * i + r >= m && 8 * i + r <= mx) ? pv : 0.f;
-                else
+                else if constexpr (!kAddMask)
                     pv = (8 * i + r >= m) ? pv : 0.f;
                 const float ds = pv * __builtin_fmaf(dp[4 * i + r], scale, nd[r]);
                 pop[i >> 1][(i & 1) * 4 + r] = (__bf16)pv;
@@ -422,8 +466,9 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
         // query block of step t (advanced once per step, as the loads are)
         const int q0 = cur_qb * kKvRows;
         if (++cur_qb == qb_end) cur_qb = qb0;
-        const int m = (t < n_iter) ? (p.causal ? key - q0 - 4 * g2 : -64) : 64;
-        const int mx = key + p.window - 1 - q0 - 4 * g2;
+        [[maybe_unused]] const int m = (t < n_iter) ? (p.causal ? key - q0 - 4 * g2 : -64) : 64;
+        [[maybe_unused]] const int mx = key + p.window - 1 - q0 - 4 * g2;
+
         // S/dP(t+1), then dV += P^T dO and dK += dS^T Q of step t (C[key][d],
         // 4 column tiles of D; k-step ks takes query rows 16ks + 4g2 + 0..3
         // and 16ks + 8 + 4g2 + 0..3, read transposed from the tiles), as one
@@ -463,11 +508,17 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
         bf16x8_t ring[kR];
         bw_static_for<kR>([&](auto ic) { ring[decltype(ic)::value] = fetch(ic); });
 #pragma unroll
-        for (int i = 0; i < 16; ++i) sn[i] = dpn[i] = 0.f;
+        for (int i = 0; i < 16; ++i) dpn[i] = 0.f;
+        // S(t+1)'s first MFMA ahead of the scheduled stream (cur_qb is now
+        // step t+1's block); its operand slot is refilled as op 0 would
+        sn = s_first(ring[0], t + 1, cur_qb * kKvRows);
+        ring[0] = fetch(std::integral_constant<int, kR>{});
         auto op = [&](auto ic) {
             constexpr int i = decltype(ic)::value;
             const bf16x8_t a = ring[i % kR];
-            if constexpr (i < 16) {
+            if constexpr (i == 0) {
+                (void)a;   // issued above
+            } else if constexpr (i < 16) {
                 if constexpr (i % 2 == 0) sn = mfma32(a, kop[i / 2], sn);
                 else dpn = mfma32(a, vop[i / 2], dpn);
             } else if constexpr (i < kS) {
@@ -480,7 +531,7 @@ __global__ __launch_bounds__(kBwThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
                 constexpr int r = i - kS - 16, ks = r / 2, cb = r % 2;
                 dk_acc[4 + cb % 2] = mfma32(dsop[ks], a, dk_acc[4 + cb % 2]);
             }
-            if constexpr (i + kR < kOps) ring[i % kR] = fetch(std::integral_constant<int, i + kR>{});
+            if constexpr (i > 0 && i + kR < kOps) ring[i % kR] = fetch(std::integral_constant<int, i + kR>{});
         };
         // The scheduler's small-GEMM interleave (LLVM's IGLP strategy 0)
         // issues the operand reads progressively further ahead of their
@@ -1240,23 +1291,27 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     const bool mla = a->head_dim == 192;
     const bool dq_split = a->dq_kernel == FGQA_KERNEL_AUTO ? (q_units < 4 * (int64_t)cus && !swa && !mla)
                                                            : a->dq_kernel == FGQA_KERNEL_SPLIT;
-    // kernel table: [swa] of dK/dV, dQ, split dQ
-    const void* kv_fn[2] = {reinterpret_cast<const void*>(bwd_dkdv_kernel<false, 128>),
-                            reinterpret_cast<const void*>(bwd_dkdv_kernel<true, 128>)};
+    // the dK/dV kernel's mask: additive (-inf on S) unless the scale is 0
+    const int am = p.scale_log2 != 0.f ? 1 : 0;
+    // kernel table: [swa] of dK/dV ([additive mask] too), dQ, split dQ
+    const void* kv_fn[2][2] = {{reinterpret_cast<const void*>(bwd_dkdv_kernel<false, 128, false>),
+                                reinterpret_cast<const void*>(bwd_dkdv_kernel<false, 128, true>)},
+                               {reinterpret_cast<const void*>(bwd_dkdv_kernel<true, 128, false>),
+                                reinterpret_cast<const void*>(bwd_dkdv_kernel<true, 128, true>)}};
+    const void* kv192_fn[2] = {reinterpret_cast<const void*>(bwd_dkdv_kernel<false, 192, false>),
+                               reinterpret_cast<const void*>(bwd_dkdv_kernel<false, 192, true>)};
     const void* q_fn[2] = {reinterpret_cast<const void*>(bwd_dq_kernel<false, 128>),
                            reinterpret_cast<const void*>(bwd_dq_kernel<true, 128>)};
     const void* q2_fn[2] = {reinterpret_cast<const void*>(bwd_dq_split_kernel<false>),
                             reinterpret_cast<const void*>(bwd_dq_split_kernel<true>)};
-    // attribute slots 10..17: the backward kernels
+    // attribute slots 10..17 and 24..26: the backward kernels
     if (mla) {
-        if ((st = set_kernel_smem_once(16, reinterpret_cast<const void*>(bwd_dkdv_kernel<false, 192>),
-                                       kv_smem_bytes<192>())) != FGQA_OK)
-            return st;
+        if ((st = set_kernel_smem_once(am ? 16 : 26, kv192_fn[am], kv_smem_bytes<192>())) != FGQA_OK) return st;
         if ((st = set_kernel_smem_once(17, reinterpret_cast<const void*>(bwd_dq_kernel<false, 192>),
                                        dq_smem_bytes<192>())) != FGQA_OK)
             return st;
     } else {
-        if ((st = set_kernel_smem_once(10 + swa, kv_fn[swa], kKvSmemBytes)) != FGQA_OK) return st;
+        if ((st = set_kernel_smem_once((am ? 10 : 24) + swa, kv_fn[swa][am], kKvSmemBytes)) != FGQA_OK) return st;
         if ((st = set_kernel_smem_once(12 + swa, q_fn[swa], kDqSmemBytes)) != FGQA_OK) return st;
         if ((st = set_kernel_smem_once(14 + swa, q2_fn[swa], kDqPpSmemBytes)) != FGQA_OK) return st;
     }
@@ -1267,8 +1322,11 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
         if (q_units > 0)
             hipLaunchKernelGGL((bwd_dq_kernel<false, 192>), dim3((unsigned)q_units), dim3(kBwThreads),
                                dq_smem_bytes<192>(), s, p);
-        if (kv_units > 0)
-            hipLaunchKernelGGL((bwd_dkdv_kernel<false, 192>), dim3((unsigned)kv_units), dim3(kBwThreads),
+        if (kv_units > 0 && am)
+            hipLaunchKernelGGL((bwd_dkdv_kernel<false, 192, true>), dim3((unsigned)kv_units), dim3(kBwThreads),
+                               kv_smem_bytes<192>(), s, p);
+        else if (kv_units > 0)
+            hipLaunchKernelGGL((bwd_dkdv_kernel<false, 192, false>), dim3((unsigned)kv_units), dim3(kBwThreads),
                                kv_smem_bytes<192>(), s, p);
         if (pl.n_hsplit > 1 && rows_kv > 0)
             hipLaunchKernelGGL(bwd_dkdv_reduce_kernel<192>, dim3((unsigned)ceil_div(rows_kv, 16)), dim3(256), 0, s,
@@ -1292,12 +1350,11 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
                                p);
     }
     if (kv_units > 0) {
-        if (swa)
-            hipLaunchKernelGGL((bwd_dkdv_kernel<true, 128>), dim3((unsigned)kv_units), dim3(kBwThreads), kKvSmemBytes,
-                               s, p);
-        else
-            hipLaunchKernelGGL((bwd_dkdv_kernel<false, 128>), dim3((unsigned)kv_units), dim3(kBwThreads), kKvSmemBytes,
-                               s, p);
+        const dim3 g((unsigned)kv_units), t(kBwThreads);
+        if (swa && am) hipLaunchKernelGGL((bwd_dkdv_kernel<true, 128, true>), g, t, kKvSmemBytes, s, p);
+        else if (swa) hipLaunchKernelGGL((bwd_dkdv_kernel<true, 128, false>), g, t, kKvSmemBytes, s, p);
+        else if (am) hipLaunchKernelGGL((bwd_dkdv_kernel<false, 128, true>), g, t, kKvSmemBytes, s, p);
+        else hipLaunchKernelGGL((bwd_dkdv_kernel<false, 128, false>), g, t, kKvSmemBytes, s, p);
     }
     if (pl.n_hsplit > 1 && rows_kv > 0)
         hipLaunchKernelGGL(bwd_dkdv_reduce_kernel<128>, dim3((unsigned)ceil_div(rows_kv, 16)), dim3(256), 0, s, p);

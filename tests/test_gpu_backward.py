@@ -117,7 +117,9 @@ def test_backward_dq_split_tile_counts(cuda, Skv):
     _check(_gpu_backward(cuda, q, k, v, o, lse, do, causal=False, dq_kernel="split"), refs, what)
 
 
-@pytest.mark.parametrize("scale", [0.2, -0.05])
+# a negative scale masks S with +inf (S * scale is then -inf); a zero scale
+# runs the dK/dV kernel's select form of the mask
+@pytest.mark.parametrize("scale", [0.2, -0.05, 0.0])
 def test_backward_scale_values(cuda, scale):
     print(f"backward scale={scale}", flush=True)
     q, k, v, o, lse, do = _inputs(820, 1, 200, 200, 4, 1, scale=scale)

@@ -90,7 +90,8 @@ def test_mla_backward_head_split_modes(cuda, hsplit):
     _check(_gpu_backward(cuda, q, k, v, o, lse, do, kv_head_split=hsplit), refs, f"mla hsplit={hsplit}")
 
 
-@pytest.mark.parametrize("scale", [0.2, -0.05])
+# a zero scale runs the dK/dV kernel's select form of the mask
+@pytest.mark.parametrize("scale", [0.2, -0.05, 0.0])
 def test_mla_backward_scale_values(cuda, scale):
     print(f"mla backward scale={scale}", flush=True)
     q, k, v, o, lse, do = _inputs(2220, 1, 200, 200, 4, 2, scale=scale)

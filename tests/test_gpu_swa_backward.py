@@ -80,6 +80,17 @@ def test_swa_backward_shapes(cuda, B, S, Hq, Hkv, window, with_sink):
     _check(_gpu_backward(cuda, q, k, v, o, lse, do, window), refs, what)
 
 
+@pytest.mark.parametrize("scale", [-0.07, 0.0])
+def test_swa_backward_scale_values(cuda, scale):
+    """The window's two mask edges with a negative scale (S masked by +inf) and
+    with scale 0 (the dK/dV kernel's select form)."""
+    what = f"swa backward scale={scale}"
+    print(what, flush=True)
+    q, k, v, o, lse, do = _inputs(1500, 1, 300, 300, 8, 2, 40, True, scale=scale)
+    refs = oracle.prefill_backward(q, k, v, o, lse, do, scale, causal=True, window=40)
+    _check(_gpu_backward(cuda, q, k, v, o, lse, do, 40, scale=scale), refs, what)
+
+
 @pytest.mark.parametrize("B,Sq,Skv,Hq,Hkv,window", [
     (1, 161, 97, 4, 1, 40),        # Sq > Skv: rows past the last key's window get zero dQ
     (2, 64, 640, 16, 4, 48),       # Sq < Skv: keys >= Sq get zero dK / dV
