@@ -628,7 +628,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_reduce_kernel(BwdParams p) {
 // wave w -> head (w % hb), positions 32 * (w / hb) .. +31 of the unit, as the
 // forward kernel; the whole key range of the unit (the split form,
 // dq_unit_pp below, gives each half of it to a group of its own).
-template <bool kSwa, int kDk>
+template <bool kSwa, int kDk, bool kAddMask>
 __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem, int qb, int hg, int kvh, int b) {
     using D = BwDims<kDk>;
     const int tid = threadIdx.x;
@@ -748,7 +748,11 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem,
     // 32tb + 8(i/4) + 4g2 + i%4 of the tile; it is used when 32tb + 8(i/4) + i%4 < m,
     // m = row_lim - (tile start) - 4g2 (m <= 0 masks the whole tile), and
     // (window) when it is >= lo, lo = qrow - window + 1 - (tile start) - 4g2.
-    auto tile = [&](auto bi_c, int m, int lo) {
+    // kAddMask: as in the dK/dV kernel, S^T's accumulators start at 0, or on
+    // a tile the mask cuts for this wave's rows (`cut`, wave-uniform) at
+    // ninf for each unused element, and dS^T carries no select.
+    const float ninf = c2 > 0.f ? -INFINITY : INFINITY;
+    auto tile = [&](auto bi_c, int m, int lo, bool cut) {
         constexpr int bi = decltype(bi_c)::value;
         const unsigned char* kl = smem + bi * kDqTileBytes;
         const unsigned char* vl = smem + (2 + bi) * kDqTileBytes;
@@ -785,11 +789,46 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem,
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) s[tb][i] = dp[tb][i] = 0.f;
+            for (int i = 0; i < 16; ++i) dp[tb][i] = 0.f;
+        if constexpr (kAddMask) {
+            // the two S^T chains' first MFMAs (operands 0 and 2) ahead of the
+            // scheduled stream, with the mask's start values on a cut tile;
+            // their operand slots are refilled as ops 0 and 2 would
+            f32x16_t z;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) z[i] = 0.f;
+            if (cut) {
+                f32x16_t bias[2];
+#pragma unroll
+                for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int idx = 32 * tb + 8 * (i >> 2) + (i & 3);
+                        const bool vis = kSwa ? (idx < m && idx >= lo) : (idx < m);
+                        bias[tb][i] = vis ? 0.f : ninf;
+                    }
+                s[0] = mfma32(ring[0], qop[0], bias[0]);
+                s[1] = mfma32(ring[2], qop[0], bias[1]);
+            } else {
+                s[0] = mfma32(ring[0], qop[0], z);
+                s[1] = mfma32(ring[2], qop[0], z);
+            }
+            ring[0] = fetch(std::integral_constant<int, kR>{});
+            ring[2 % kR] = fetch(std::integral_constant<int, 2 + kR>{});
+        } else {
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) s[tb][i] = 0.f;
+        }
+        // ops 0 and 2 with kAddMask: issued above
+        auto issued = [](int i) { return kAddMask && (i == 0 || i == 2); };
         auto op = [&](auto ic) {
             constexpr int i = decltype(ic)::value;
             const bf16x8_t a = ring[i % kR];
-            if constexpr (i < 32) {
+            if constexpr (issued(i)) {
+                (void)a;
+            } else if constexpr (i < 32) {
                 constexpr int kk = i / 4, tb = (i / 2) % 2;
                 if constexpr (i % 2 == 0) s[tb] = mfma32(a, qop[kk], s[tb]);
                 else dp[tb] = mfma32(a, doop[kk], dp[tb]);
@@ -801,7 +840,7 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem,
                 if constexpr (c < 4) dq_acc[c] = mfma32(a, dsop[kb], dq_acc[c]);
                 else dq_acc[4 + (c - 4) % 2] = mfma32(a, dsop[kb], dq_acc[4 + (c - 4) % 2]);
             }
-            if constexpr (i + kR < kOps) ring[i % kR] = fetch(std::integral_constant<int, i + kR>{});
+            if constexpr (!issued(i) && i + kR < kOps) ring[i % kR] = fetch(std::integral_constant<int, i + kR>{});
         };
         __builtin_amdgcn_iglp_opt(0);   // operand reads run ahead, as in the dK/dV step
         bw_static_for<kSd>(op);
@@ -817,9 +856,9 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem,
                     const int i = kh * 8 + e;
                     float pv = fast_exp2(__builtin_fmaf(s[tb][i], c2, nl));
                     const int idx = 32 * tb + 8 * (i >> 2) + (i & 3);
-                    if constexpr (kSwa)
+                    if constexpr (!kAddMask && kSwa)
                         pv = (idx < m && idx >= lo) ? pv : 0.f;
-                    else
+                    else if constexpr (!kAddMask)
                         pv = (idx < m) ? pv : 0.f;
                     dsop[tb * 2 + kh][e] = (__bf16)(pv * __builtin_fmaf(dp[tb][i], scale, nd));
                 }
@@ -846,14 +885,25 @@ __device__ __forceinline__ void dq_unit(const BwdParams& p, unsigned char* smem,
     __syncthreads();
     using C0 = std::integral_constant<int, 0>;
     using C1 = std::integral_constant<int, 1>;
+    // Does the mask cut an element of tile jj for this wave's rows q0w ..
+    // q0w+31 (wave-uniform)?  A tile past n_tiles, keys at or past kv_hi,
+    // rows past sq, a key after the first row (causal), or a key before the
+    // last row's window.  Every other tile is wholly visible.
+    auto tile_cut = [&](int jj) {
+        const int t0 = (t_first + jj) * kDqTile;
+        bool cut = jj >= n_tiles || t0 + kDqTile > kv_hi || q0w + 31 >= p.sq || (p.causal && t0 + kDqTile - 1 > q0w);
+        if constexpr (kSwa) cut = cut || t0 < q0w + 31 - p.window + 1;
+        return cut;
+    };
     for (int j = 0; j < n_tiles; j += 2) {
         if (j + 1 < n_tiles) issue(j + 1, 1);
-        tile(C0{}, row_lim - (t_first + j) * kDqTile - 4 * g2, qrow - p.window + 1 - (t_first + j) * kDqTile - 4 * g2);
+        tile(C0{}, row_lim - (t_first + j) * kDqTile - 4 * g2, qrow - p.window + 1 - (t_first + j) * kDqTile - 4 * g2,
+             tile_cut(j));
         bw_wait_vmem();
         __syncthreads();
         if (j + 2 < n_tiles) issue(j + 2, 0);
         tile(C1{}, (j + 1 < n_tiles) ? row_lim - (t_first + j + 1) * kDqTile - 4 * g2 : 0,
-             qrow - p.window + 1 - (t_first + j + 1) * kDqTile - 4 * g2);
+             qrow - p.window + 1 - (t_first + j + 1) * kDqTile - 4 * g2, tile_cut(j + 1));
         bw_wait_vmem();
         __syncthreads();
     }
@@ -1173,12 +1223,12 @@ __device__ __forceinline__ void dq_block_unit(const BwdParams& p, int* qb, int* 
 
 // 128-wide: two workgroups per CU; 192-wide (MLA): one, with the whole
 // register file (Q^T of 12 k-steps, dQ^T of 6 column blocks).
-template <bool kSwa, int kDk>
+template <bool kSwa, int kDk, bool kAddMask>
 __global__ __launch_bounds__(kBwThreads, kDk == 128 ? 2 : 1) void bwd_dq_kernel(BwdParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     int qb, hg, kvh, b;
     dq_block_unit(p, &qb, &hg, &kvh, &b);
-    dq_unit<kSwa, kDk>(p, smem, qb, hg, kvh, b);
+    dq_unit<kSwa, kDk, kAddMask>(p, smem, qb, hg, kvh, b);
 }
 
 template <bool kSwa>
@@ -1300,27 +1350,32 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
                                 reinterpret_cast<const void*>(bwd_dkdv_kernel<true, 128, true>)}};
     const void* kv192_fn[2] = {reinterpret_cast<const void*>(bwd_dkdv_kernel<false, 192, false>),
                                reinterpret_cast<const void*>(bwd_dkdv_kernel<false, 192, true>)};
-    const void* q_fn[2] = {reinterpret_cast<const void*>(bwd_dq_kernel<false, 128>),
-                           reinterpret_cast<const void*>(bwd_dq_kernel<true, 128>)};
+    const void* q_fn[2][2] = {{reinterpret_cast<const void*>(bwd_dq_kernel<false, 128, false>),
+                               reinterpret_cast<const void*>(bwd_dq_kernel<false, 128, true>)},
+                              {reinterpret_cast<const void*>(bwd_dq_kernel<true, 128, false>),
+                               reinterpret_cast<const void*>(bwd_dq_kernel<true, 128, true>)}};
+    const void* q192_fn[2] = {reinterpret_cast<const void*>(bwd_dq_kernel<false, 192, false>),
+                              reinterpret_cast<const void*>(bwd_dq_kernel<false, 192, true>)};
     const void* q2_fn[2] = {reinterpret_cast<const void*>(bwd_dq_split_kernel<false>),
                             reinterpret_cast<const void*>(bwd_dq_split_kernel<true>)};
-    // attribute slots 10..17 and 24..26: the backward kernels
+    // attribute slots 10..17 and 24..29: the backward kernels
     if (mla) {
         if ((st = set_kernel_smem_once(am ? 16 : 26, kv192_fn[am], kv_smem_bytes<192>())) != FGQA_OK) return st;
-        if ((st = set_kernel_smem_once(17, reinterpret_cast<const void*>(bwd_dq_kernel<false, 192>),
-                                       dq_smem_bytes<192>())) != FGQA_OK)
-            return st;
+        if ((st = set_kernel_smem_once(am ? 17 : 29, q192_fn[am], dq_smem_bytes<192>())) != FGQA_OK) return st;
     } else {
         if ((st = set_kernel_smem_once((am ? 10 : 24) + swa, kv_fn[swa][am], kKvSmemBytes)) != FGQA_OK) return st;
-        if ((st = set_kernel_smem_once(12 + swa, q_fn[swa], kDqSmemBytes)) != FGQA_OK) return st;
+        if ((st = set_kernel_smem_once((am ? 12 : 27) + swa, q_fn[swa][am], kDqSmemBytes)) != FGQA_OK) return st;
         if ((st = set_kernel_smem_once(14 + swa, q2_fn[swa], kDqPpSmemBytes)) != FGQA_OK) return st;
     }
 
     // dQ first: its kernels store each row's statistics, which dK/dV reads.
     // (Without query rows there are no dQ units, and dK/dV reads no row.)
     if (mla) {
-        if (q_units > 0)
-            hipLaunchKernelGGL((bwd_dq_kernel<false, 192>), dim3((unsigned)q_units), dim3(kBwThreads),
+        if (q_units > 0 && am)
+            hipLaunchKernelGGL((bwd_dq_kernel<false, 192, true>), dim3((unsigned)q_units), dim3(kBwThreads),
+                               dq_smem_bytes<192>(), s, p);
+        else if (q_units > 0)
+            hipLaunchKernelGGL((bwd_dq_kernel<false, 192, false>), dim3((unsigned)q_units), dim3(kBwThreads),
                                dq_smem_bytes<192>(), s, p);
         if (kv_units > 0 && am)
             hipLaunchKernelGGL((bwd_dkdv_kernel<false, 192, true>), dim3((unsigned)kv_units), dim3(kBwThreads),
@@ -1342,12 +1397,11 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
             hipLaunchKernelGGL(bwd_dq_split_kernel<false>, dim3((unsigned)q_units), dim3(2 * kBwThreads),
                                kDqPpSmemBytes, s, p);
     } else if (q_units > 0) {
-        if (swa)
-            hipLaunchKernelGGL((bwd_dq_kernel<true, 128>), dim3((unsigned)q_units), dim3(kBwThreads), kDqSmemBytes, s,
-                               p);
-        else
-            hipLaunchKernelGGL((bwd_dq_kernel<false, 128>), dim3((unsigned)q_units), dim3(kBwThreads), kDqSmemBytes, s,
-                               p);
+        const dim3 g((unsigned)q_units), t(kBwThreads);
+        if (swa && am) hipLaunchKernelGGL((bwd_dq_kernel<true, 128, true>), g, t, kDqSmemBytes, s, p);
+        else if (swa) hipLaunchKernelGGL((bwd_dq_kernel<true, 128, false>), g, t, kDqSmemBytes, s, p);
+        else if (am) hipLaunchKernelGGL((bwd_dq_kernel<false, 128, true>), g, t, kDqSmemBytes, s, p);
+        else hipLaunchKernelGGL((bwd_dq_kernel<false, 128, false>), g, t, kDqSmemBytes, s, p);
     }
     if (kv_units > 0) {
         const dim3 g((unsigned)kv_units), t(kBwThreads);
