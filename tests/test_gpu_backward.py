@@ -274,6 +274,26 @@ print("no-query-rows backward ok", flush=True)
 """
 
 
+@pytest.mark.parametrize("split", ["whole", "split"])
+def test_backward_without_keys_zeroes_dq(cuda, split):
+    """Sq > 0 with Skv = 0: no dQ unit has a key tile, so each writes dQ = 0
+    (and still stores its rows' statistics; no dK/dV kernel runs to read
+    them), for both dQ kernels."""
+    import torch
+    print(f"backward Sq=100 Skv=0 dq={split}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(77)
+    q = torch.randn(1, 100, 4, 128, generator=g).to(torch.bfloat16).to(cuda)
+    o = torch.randn(1, 100, 4, 128, generator=g).to(torch.bfloat16).to(cuda)
+    do = torch.randn(1, 100, 4, 128, generator=g).to(torch.bfloat16).to(cuda)
+    k = torch.empty(1, 0, 1, 128, dtype=torch.bfloat16, device=cuda)
+    v = torch.empty_like(k)
+    lse = torch.zeros(1, 4, 100, device=cuda)
+    dq, dk, dv = _fg().flash_gqa_backward_bshd(q, k, v, o, lse, do, SCALE, causal=False, dq_kernel=split)
+    _sync()
+    assert dk.shape == (1, 0, 1, 128) and dv.shape == (1, 0, 1, 128)
+    assert torch.count_nonzero(dq.float()).item() == 0
+
+
 def test_backward_without_query_rows_zeroes_key_gradients(cuda):
     """Sq = 0 with Skv > 0 and G = 1: the call needs no workspace, and no query
     row sees any key, so dK = dV = 0 must still be written -- in a fresh process,
