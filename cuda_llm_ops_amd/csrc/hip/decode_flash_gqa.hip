@@ -93,16 +93,19 @@ __device__ __forceinline__ int clamp_len(const DecodeParams& p, int b) {
     return min(max(len, 0), p.max_seqlen);
 }
 
-// One (split, kv head, batch) item of pass 1.  kSeg (paged caches, 0 or a
-// power of two from one load instruction's rows up to 32): the rows of a
-// 32-token step fall into page segments of kSeg rows (kSeg = min(page, 32)),
-// each read through one buffer resource; 0 is the general form, with a page
-// lookup and a 64-bit address per row.
+// One (split, kv head, batch) item of pass 1, run by 4 waves (tid: the
+// thread's index among them, smem: their kDecSmemBytes of LDS).  kSeg (paged
+// caches, 0 or a power of two from one load instruction's rows up to 32): the
+// rows of a 32-token step fall into page segments of kSeg rows
+// (kSeg = min(page, 32)), each read through one buffer resource; 0 is the
+// general form, with a page lookup and a 64-bit address per row.
+// The only workgroup barriers are the two of the wave merge (none when the
+// split is empty), so two items of one split can share a workgroup.
 template <int kKv, int kSeg = 0>
-__device__ __forceinline__ void dec_item(const DecodeParams& p, unsigned char* smem, int split, int kvh, int b) {
+__device__ __forceinline__ void dec_item(const DecodeParams& p, unsigned char* smem, int split, int kvh, int b,
+                                         int tid) {
     const int len = clamp_len(p, b);
     const int t_begin = split * p.chunk;
-    const int tid = threadIdx.x;
     if (t_begin >= len) {
         // Empty split: the combine never reads it.  Without a combine pass an
         // empty sequence still needs its O = 0, lse = -inf written here.
@@ -220,10 +223,15 @@ __device__ __forceinline__ void dec_item(const DecodeParams& p, unsigned char* s
         if constexpr (kUni) {
             (void)s;   // the pages are taken out in load_step
         } else if constexpr (kKv != kKvContig) {
+            // Raw entries: they are clamped where load_step uses them.  A
+            // clamp here would make the wave wait for the table loads at once,
+            // and vector loads complete in order, so that wait would also take
+            // the K/V loads issued just before, leaving none in flight while
+            // the step computes.
 #pragma unroll
             for (int r = 0; r < kRows; ++r) {
                 const int tok = min(t_begin + s * kDecStep + row_of(r), t_end - 1);
-                pg[r] = min(max(bt[tok >> p.page_shift], 0), p.num_pages - 1);
+                pg[r] = bt[tok >> p.page_shift];
             }
         }
     };
@@ -261,8 +269,9 @@ __device__ __forceinline__ void dec_item(const DecodeParams& p, unsigned char* s
 #pragma unroll
             for (int r = 0; r < kRows; ++r) {
                 const int slot = min(t0 + row_of(r), t_end - 1) & pmask;
-                const int64_t ko = ((int64_t)pg[r] * p.k_sb + (int64_t)slot * p.k_ss) * kElemBytes + cb;
-                const int64_t vo = ((int64_t)pg[r] * p.v_sb + (int64_t)slot * p.v_ss) * kElemBytes + cb;
+                const int page = min(max(pg[r], 0), p.num_pages - 1);
+                const int64_t ko = ((int64_t)page * p.k_sb + (int64_t)slot * p.k_ss) * kElemBytes + cb;
+                const int64_t vo = ((int64_t)page * p.v_sb + (int64_t)slot * p.v_ss) * kElemBytes + cb;
                 kreg[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(kbase + ko));
                 vreg[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(vbase + vo));
             }
@@ -424,7 +433,7 @@ __device__ __forceinline__ void dec_item(const DecodeParams& p, unsigned char* s
 // Pass 1 over the full (split, kv head, batch) grid.
 __global__ __launch_bounds__(kDecThreads) void decode_split_kernel(DecodeParams p) {
     __shared__ __attribute__((aligned(16))) unsigned char smem[kDecSmemBytes];
-    dec_item<kKvContig>(p, smem, blockIdx.x, blockIdx.y, blockIdx.z);
+    dec_item<kKvContig>(p, smem, blockIdx.x, blockIdx.y, blockIdx.z, threadIdx.x);
 }
 
 // Ragged batches: build the work list of non-empty splits, full-length splits
@@ -512,15 +521,44 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(DecodeParams 
 
 // Pass 1 over the ragged work list: a fixed grid walks the entries, each
 // entry once per kv head (kv head fastest, so heads of one split run together).
-template <int kKv, int kSeg = 0>
-__global__ __launch_bounds__(kDecThreads) void decode_list_kernel(DecodeParams p) {
-    __shared__ __attribute__((aligned(16))) unsigned char smem[kDecSmemBytes];
-    const int total = p.work[0] * p.hkv;
+// kPair (an even number of kv heads): 8-wave workgroups, waves 0-3 on kv head
+// 2j and waves 4-7 on kv head 2j + 1 of the same split.  Each half reads its
+// own head's rows, but the two halves' loads of one token arrive together, so
+// the 2 x 128-byte (fp8) or 2 x 256-byte (bf16) pieces of a cache row that lie
+// side by side in memory are read at the same time: a streaming read of
+// config 3's fp8 page pattern ran at 5.84 TB/s with one head per workgroup and
+// 6.45 TB/s with head pairs.  Both halves of a workgroup hold the same split
+// of the same sequence, so they pass the same workgroup barriers.
+template <int kKv, int kSeg = 0, bool kPair = false>
+__global__ __launch_bounds__(kPair ? 2 * kDecThreads : kDecThreads) void decode_list_kernel(DecodeParams p) {
+    __shared__ __attribute__((aligned(16))) unsigned char smem[(kPair ? 2 : 1) * kDecSmemBytes];
+    // wave-uniform (readfirstlane), so the buffer resources built from the
+    // head stay scalar
+    const int half = kPair ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kDecThreads)) : 0;
+    const int per_entry = kPair ? p.hkv / 2 : p.hkv;
+    const int total = p.work[0] * per_entry;
     for (int item = blockIdx.x; item < total; item += gridDim.x) {
-        const int e = p.work[1 + item / p.hkv];
+        const int e = p.work[1 + item / per_entry];
+        const int kvh = kPair ? 2 * (item % per_entry) + half : item % per_entry;
         __syncthreads();   // the previous item's merge buffers alias the staging area
-        dec_item<kKv, kSeg>(p, smem, e & 0xffff, item % p.hkv, e >> 16);
+        dec_item<kKv, kSeg>(p, smem + half * kDecSmemBytes, e & 0xffff, kvh, e >> 16,
+                            (int)threadIdx.x - half * kDecThreads);
     }
+}
+
+// Launches pass 1 over the work list: the head-pair form (one 8-wave
+// workgroup per CU) when the kv heads pair up, else two 4-wave workgroups per
+// CU.  Persistent: the grid never exceeds what the CUs hold at once.
+template <int kKv, int kSeg>
+static void launch_list(const DecodeParams& p, int nsplit, int cus, hipStream_t s) {
+    const bool pair = (p.hkv % 2) == 0;
+    const int64_t items = (int64_t)p.batch * nsplit * (pair ? p.hkv / 2 : p.hkv);   // most the list can hold
+    const int64_t slots = (int64_t)(pair ? 1 : 2) * cus;
+    const int grid = (int)(items < slots ? items : slots);
+    if (pair)
+        hipLaunchKernelGGL((decode_list_kernel<kKv, kSeg, true>), dim3(grid), dim3(2 * kDecThreads), 0, s, p);
+    else
+        hipLaunchKernelGGL((decode_list_kernel<kKv, kSeg, false>), dim3(grid), dim3(kDecThreads), 0, s, p);
 }
 
 // Log-sum-exp merge of the per-split partials of one (kv head, batch).
@@ -713,10 +751,8 @@ int decode_run(const fgqa_decode_args* a, void* stream, bool noalloc) {
     } else if (plan.list) {
         const int cus = device_cu_count();
         if (cus <= 0) return FGQA_ERR_HIP;
-        const int64_t max_items = (int64_t)p.batch * plan.nsplit * p.hkv;
-        const int grid = (int)(max_items < 2LL * cus ? max_items : 2LL * cus);   // two per CU, persistent
         hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p, work);
-        hipLaunchKernelGGL(decode_list_kernel<kKvContig>, dim3(grid), dim3(kDecThreads), 0, s, p);
+        launch_list<kKvContig, 0>(p, plan.nsplit, cus, s);
         if (plan.nsplit > 1)
             hipLaunchKernelGGL(decode_combine_kernel, dim3(p.hkv, p.batch), dim3(kDecThreads), 0, s, p);
     } else {
@@ -824,28 +860,30 @@ extern "C" int fgqa_decode_paged(const fgqa_decode_paged_args* a, void* stream) 
     } else {
         const int cus = device_cu_count();
         if (cus <= 0) return FGQA_ERR_HIP;
-        const int64_t max_items = (int64_t)p.batch * plan.nsplit * p.hkv;
-        const int grid = (int)(max_items < 2LL * cus ? max_items : 2LL * cus);
         hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p, work);
-        // bf16 pages of at least 4 rows (one load instruction's) whose bytes
-        // stay below 2^31: page segments of min(page, 32) rows, each read
-        // through one buffer resource (−4 % at BASELINE config 3's lengths
-        // with pages of 16 and 64).  fp8 pages keep the per-row form, which
-        // measured 2 % faster for them.
+        // Pages of at least one load instruction's rows (4 bf16, 8 fp8) whose
+        // bytes stay below 2^31: page segments of min(page, 32) rows, each
+        // read through one buffer resource (at BASELINE config 3's lengths
+        // with 16- and 64-token pages: bf16 -4 %, fp8 with head pairs -1 to
+        // -2 % against the per-row form).
         const bool fp8 = a->kv_dtype == FGQA_KV_FP8_E4M3;
         const bool small_pages = (int64_t)a->page_size * a->k_stride[1] * 2 < ((int64_t)1 << 31) &&
                                  (int64_t)a->page_size * a->v_stride[1] * 2 < ((int64_t)1 << 31);
         const int seg = !small_pages ? 0 : a->page_size >= 32 ? 32 : a->page_size >= 4 ? a->page_size : 0;
-        const dim3 g(grid), t(kDecThreads);
         if (fp8) {
-            hipLaunchKernelGGL((decode_list_kernel<kKvPagedFp8, 0>), g, t, 0, s, p);
+            switch (seg >= 8 ? seg : 0) {
+                case 32: launch_list<kKvPagedFp8, 32>(p, plan.nsplit, cus, s); break;
+                case 16: launch_list<kKvPagedFp8, 16>(p, plan.nsplit, cus, s); break;
+                case 8: launch_list<kKvPagedFp8, 8>(p, plan.nsplit, cus, s); break;
+                default: launch_list<kKvPagedFp8, 0>(p, plan.nsplit, cus, s); break;
+            }
         } else {
             switch (seg) {
-                case 32: hipLaunchKernelGGL((decode_list_kernel<kKvPagedBf16, 32>), g, t, 0, s, p); break;
-                case 16: hipLaunchKernelGGL((decode_list_kernel<kKvPagedBf16, 16>), g, t, 0, s, p); break;
-                case 8: hipLaunchKernelGGL((decode_list_kernel<kKvPagedBf16, 8>), g, t, 0, s, p); break;
-                case 4: hipLaunchKernelGGL((decode_list_kernel<kKvPagedBf16, 4>), g, t, 0, s, p); break;
-                default: hipLaunchKernelGGL((decode_list_kernel<kKvPagedBf16, 0>), g, t, 0, s, p); break;
+                case 32: launch_list<kKvPagedBf16, 32>(p, plan.nsplit, cus, s); break;
+                case 16: launch_list<kKvPagedBf16, 16>(p, plan.nsplit, cus, s); break;
+                case 8: launch_list<kKvPagedBf16, 8>(p, plan.nsplit, cus, s); break;
+                case 4: launch_list<kKvPagedBf16, 4>(p, plan.nsplit, cus, s); break;
+                default: launch_list<kKvPagedBf16, 0>(p, plan.nsplit, cus, s); break;
             }
         }
         if (plan.nsplit > 1)

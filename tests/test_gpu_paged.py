@@ -73,16 +73,30 @@ def test_paged_page_sizes(cuda, page_size, fp8):
     _check(o, lse, o_ref, l_ref, what)
 
 
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("Hkv", [1, 3])
+def test_paged_odd_kv_heads(cuda, Hkv, fp8):
+    """Odd kv head counts run the one-head-per-workgroup list kernel (even
+    counts pair two heads in an 8-wave workgroup)."""
+    what = f"paged Hkv={Hkv} fp8={fp8}"
+    print(what, flush=True)
+    for page_size in (2, 16):
+        o, lse, o_ref, l_ref = _case(cuda, 970 + Hkv + page_size, 3, 4 * Hkv, Hkv, 700, [700, 1, 333], page_size,
+                                     fp8)
+        _check(o, lse, o_ref, l_ref, f"{what} page={page_size}")
+
+
 @pytest.mark.parametrize("page_size", [4, 8, 16, 32, 128])
 def test_paged_segments_split_inside_pages(cuda, page_size):
-    """bf16 pages read by page segment, with 128-token splits (a split ends
+    """Pages read by page segment, with 128-token splits (a split ends
     inside a page for pages of 256) and lengths that end inside a segment, a
-    load instruction and a page."""
-    what = f"paged segments page={page_size}"
-    print(what, flush=True)
+    load instruction and a page; bf16 and fp8 (fp8 segments start at 8 rows)."""
     lens = [1023, 131, 5, 1024, 769]
-    o, lse, o_ref, l_ref = _case(cuda, 950 + page_size, 5, 16, 2, 1024, lens, page_size, False, split_tokens=128)
-    _check(o, lse, o_ref, l_ref, what)
+    for fp8 in (False, True):
+        what = f"paged segments page={page_size} fp8={fp8}"
+        print(what, flush=True)
+        o, lse, o_ref, l_ref = _case(cuda, 950 + page_size, 5, 16, 2, 1024, lens, page_size, fp8, split_tokens=128)
+        _check(o, lse, o_ref, l_ref, what)
 
 
 @pytest.mark.parametrize("G", [1, 4, 16])

@@ -102,6 +102,20 @@ def test_decode_ragged_nan_padding(cuda):
         assert np.all(oracle.bf16_to_f32(o[0]) == 0) and np.all(np.isneginf(lse[0]))
 
 
+@pytest.mark.parametrize("Hkv", [1, 3, 4])
+def test_decode_ragged_kv_head_counts(cuda, Hkv):
+    """The ragged work list with odd kv head counts (one head per workgroup)
+    and an even one (two heads per 8-wave workgroup), one split and several."""
+    sl = [0, 1, 129, 500, 2047, 2048, 700]
+    for split in (4096, 256):
+        what = f"ragged Hkv={Hkv} split={split}"
+        print(what, flush=True)
+        o, lse, o_ref, lse_ref = _decode_case(cuda, 420 + Hkv, len(sl), 4 * Hkv, Hkv, 2048, seqlens=sl,
+                                              nan_pad=True, split_tokens=split)
+        _check_decode(o, lse, o_ref, lse_ref, what)
+        assert np.all(oracle.bf16_to_f32(o[0]) == 0) and np.all(np.isneginf(lse[0]))
+
+
 def test_decode_known_answers(cuda):
     import torch
     B, Hq, Hkv, S = 2, 16, 1, 3000
