@@ -150,7 +150,8 @@ def bench_decode(cfg_id, steps, warmup, split_tokens, dev):
     avg_launch_ms = total_ms / steps
     qo_bytes = 2 * cfg["B"] * cfg["Hq"] * 128 * 2
     # no workspace: one split per (batch, KV head) stream, no combine pass
-    kernel = ("decode_split_kernel, one split per (batch, KV head), no combine" if n_ws == 0 else
+    kernel = ("decode_split_kernel, one split per (batch, KV head), KV head pairs per workgroup, no combine"
+              if n_ws == 0 else
               "decode_list_kernel + decode_combine_kernel (device-built ragged work list, split-KV)"
               if cfg["ragged"] else "decode_split_kernel + decode_combine_kernel (split-KV)")
     return dict(cfg=cfg, q=q, k=k, v=v, lens=lens, out=out, kv_bytes=kv_bytes, qo_bytes=qo_bytes,

@@ -3,9 +3,11 @@
 // Replaces the reference's decode_flash_gqa_bf16_kernel
 // (src/cplusplus/FlashGQA/decode_flash_gqa_kernel.cu:119-389), which walks the
 // whole sequence serially per (kv head, batch) workgroup.  Here:
-//   pass 1 (decode_split_kernel): one workgroup per (split of the KV sequence,
-//     kv head, batch).  Each of its 4 waves streams 32-token steps; every K/V
-//     byte is read once from HBM and serves all G query heads of the group.
+//   pass 1 (decode_split_kernel): 4 waves per (split of the KV sequence,
+//     kv head, batch), two such items (adjacent kv heads) per 8-wave
+//     workgroup when the kv heads pair up.  Each wave streams 32-token steps;
+//     every K/V byte is read once from HBM and serves all G query heads of
+//     the group.
 //       K and V rows stream in with coalesced 16-byte non-temporal loads
 //       (a quarter-wave reads one 256-byte row) and are staged in LDS
 //       S^T[t][h] = K[t][:] . Q[h][:]        v_mfma_f32_16x16x32_bf16
@@ -430,10 +432,18 @@ __device__ __forceinline__ void dec_item(const DecodeParams& p, unsigned char* s
     }
 }
 
-// Pass 1 over the full (split, kv head, batch) grid.
-__global__ __launch_bounds__(kDecThreads) void decode_split_kernel(DecodeParams p) {
-    __shared__ __attribute__((aligned(16))) unsigned char smem[kDecSmemBytes];
-    dec_item<kKvContig>(p, smem, blockIdx.x, blockIdx.y, blockIdx.z, threadIdx.x);
+// Pass 1 over the full (split, kv head, batch) grid.  kPair (an even number
+// of kv heads): 8-wave workgroups over (split, kv head pair, batch), waves 0-3
+// on kv head 2j and waves 4-7 on kv head 2j + 1, so that the two 256-byte
+// pieces of a token's cache row that lie side by side are read together (at
+// 480 four-wave workgroups 159.5 us, 240 eight-wave ones
+// 145.4 us, outputs bit-identical).
+template <bool kPair>
+__global__ __launch_bounds__(kPair ? 2 * kDecThreads : kDecThreads) void decode_split_kernel(DecodeParams p) {
+    __shared__ __attribute__((aligned(16))) unsigned char smem[(kPair ? 2 : 1) * kDecSmemBytes];
+    const int half = kPair ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kDecThreads)) : 0;
+    dec_item<kKvContig>(p, smem + half * kDecSmemBytes, blockIdx.x, kPair ? 2 * (int)blockIdx.y + half : blockIdx.y,
+                        blockIdx.z, (int)threadIdx.x - half * kDecThreads);
 }
 
 // Ragged batches: build the work list of non-empty splits, full-length splits
@@ -756,7 +766,17 @@ int decode_run(const fgqa_decode_args* a, void* stream, bool noalloc) {
         if (plan.nsplit > 1)
             hipLaunchKernelGGL(decode_combine_kernel, dim3(p.hkv, p.batch), dim3(kDecThreads), 0, s, p);
     } else {
-        hipLaunchKernelGGL(decode_split_kernel, dim3(p.nsplit, p.hkv, p.batch), dim3(kDecThreads), 0, s, p);
+        // Head pairs once the grid holds at least one item per CU; smaller
+        // grids are latency-bound and keep one item per workgroup (BASELINE
+        // config 1's 16 items: 9.9 us paired, 9.4 us not).
+        const int cus = device_cu_count();
+        if (cus <= 0) return FGQA_ERR_HIP;
+        const bool pair = p.hkv % 2 == 0 && (int64_t)p.nsplit * p.hkv * p.batch >= cus;
+        if (pair)
+            hipLaunchKernelGGL(decode_split_kernel<true>, dim3(p.nsplit, p.hkv / 2, p.batch), dim3(2 * kDecThreads), 0,
+                               s, p);
+        else
+            hipLaunchKernelGGL(decode_split_kernel<false>, dim3(p.nsplit, p.hkv, p.batch), dim3(kDecThreads), 0, s, p);
         if (plan.nsplit > 1)
             hipLaunchKernelGGL(decode_combine_kernel, dim3(p.hkv, p.batch), dim3(kDecThreads), 0, s, p);
     }

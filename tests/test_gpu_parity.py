@@ -159,6 +159,16 @@ def test_decode_config2_full_size(cuda):
                                                   v.permute(0, 2, 1, 3).contiguous())
     _sync()
     assert torch.equal(out2[:, :, 0, :], out)
+    # split-KV over kv head pairs (960 items, combine pass) on the same inputs
+    for split in (1024, 2048):
+        lse2 = torch.empty_like(lse)
+        out3 = fg.decode_flash_gqa_bshd(q, k, v, SCALE, lse=lse2, split_tokens=split)
+        _sync()
+        o3 = from_torch_bf16(out3)
+        for b in (0, 59):
+            o_ref, lse_ref = oracle.decode(from_torch_bf16(q[b:b + 1]), from_torch_bf16(k[b:b + 1]),
+                                           from_torch_bf16(v[b:b + 1]), SCALE)
+            _check_decode(o3[b:b + 1], lse2[b:b + 1].cpu().numpy(), o_ref, lse_ref, f"config2 split {split} batch {b}")
 
 
 def test_decode_config3_ragged_full_size(cuda):
