@@ -88,4 +88,4 @@ extern "C" const char* fgqa_status_string(int status) {
     }
 }
 
-extern "C" int fgqa_version(void) { return 200; }
+extern "C" int fgqa_version(void) { return 201; }

@@ -1168,6 +1168,111 @@ using plan::wide_on_pairs;
 using plan::wide_pairs;
 
 }  // namespace
+
+// Head dims below 128: rows of D elements (at b/s/h strides) -> contiguous
+// zero-padded rows of 128.  A thread per 16-byte piece of a padded row
+// (grid-stride); 2-byte reads, so the source needs no alignment.
+__global__ __launch_bounds__(256) void pad_rows_kernel(const __bf16* src, int64_t sb, int64_t ss, int64_t sh, int S,
+                                                       int H, int D, __bf16* dst, int64_t pieces) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < pieces; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = i >> 4;
+        const int c = (int)(i & 15) * 8;
+        const int h = (int)(row % H);
+        const int64_t t = row / H;
+        const __bf16* r = src + (t / S) * sb + (t % S) * ss + h * sh;
+        bf16x8_t v;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = (c + j < D) ? r[c + j] : (__bf16)0.f;
+        *reinterpret_cast<bf16x8_t*>(dst + row * kHeadDim + c) = v;
+    }
+}
+
+// The first D columns of contiguous rows of 128 -> rows at b/s/h strides.
+__global__ __launch_bounds__(256) void unpad_rows_kernel(const __bf16* src, __bf16* dst, int64_t db, int64_t ds,
+                                                         int64_t dh, int S, int H, int D, int64_t pieces) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < pieces; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = i >> 4;
+        const int c = (int)(i & 15) * 8;
+        if (c >= D) continue;
+        const int h = (int)(row % H);
+        const int64_t t = row / H;
+        __bf16* r = dst + (t / S) * db + (t % S) * ds + h * dh;
+        const bf16x8_t v = *reinterpret_cast<const bf16x8_t*>(src + row * kHeadDim + c);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (c + j < D) r[c + j] = v[j];
+    }
+}
+
+// Grid of the copy kernels: a thread per piece, at most 2^16 workgroups.
+inline unsigned copy_grid(int64_t pieces) { return (unsigned)(ceil_div(pieces, 256) < 65536 ? ceil_div(pieces, 256) : 65536); }
+
+namespace {
+
+// The launches of a validated (128, 128) or MLA call.
+int prefill_launch(const fgqa_prefill_args* a, hipStream_t s);
+
+int launch_pad(const void* src, const int64_t* st, int S, int H, int D, int B, __bf16* dst, hipStream_t s) {
+    const int64_t pieces = (int64_t)B * S * H * 16;
+    if (pieces == 0) return FGQA_OK;
+    hipLaunchKernelGGL(pad_rows_kernel, dim3(copy_grid(pieces)), dim3(256), 0, s,
+                       static_cast<const __bf16*>(src), st[0], st[1], st[2], S, H, D, dst, pieces);
+    return FGQA_OK;
+}
+
+// Head dims below 128 (plan::prefill_padded): pad, run the (128, 128)
+// kernels on the copies, unpad O.  The copies live in the caller's workspace
+// after the merge scratch, or with none in the library's cached buffer (the
+// merge scratch then being the library's per-device one).
+int prefill_padded_launch(const fgqa_prefill_args* a, hipStream_t s) {
+    const int cus = device_cu_count();
+    if (cus <= 0) return FGQA_ERR_HIP;
+    fgqa_prefill_args pa = plan::padded_args(a);
+    const size_t merge = plan::merge_scratch_bytes(&pa, plan::prefill_choice(&pa, cus), cus);
+    const plan::PadLayout L = plan::pad_layout(a, merge);
+    std::unique_lock<std::mutex> lock;
+    unsigned char* base = nullptr;   // the copies: base + L.q .. base + L.total
+    unsigned char* ws = static_cast<unsigned char*>(a->workspace);
+    if (ws == nullptr && a->workspace_bytes == 0) {
+        lock = workspace_lock();
+        int st = FGQA_OK;
+        unsigned char* buf = static_cast<unsigned char*>(internal_workspace(L.total - L.q, &st));
+        if (st != FGQA_OK) return st;
+        base = buf - L.q;
+    } else if (ws == nullptr || a->workspace_bytes < L.total) {
+        return FGQA_ERR_WORKSPACE;
+    } else if ((reinterpret_cast<uintptr_t>(ws) & 255u) != 0) {
+        return FGQA_ERR_UNSUPPORTED;
+    } else {
+        base = ws;
+        if (merge > 0) {
+            pa.workspace = ws;
+            pa.workspace_bytes = merge;
+        }
+    }
+    __bf16* qp = reinterpret_cast<__bf16*>(base + L.q);
+    __bf16* kp = reinterpret_cast<__bf16*>(base + L.k);
+    __bf16* vp = reinterpret_cast<__bf16*>(base + L.v);
+    __bf16* op = reinterpret_cast<__bf16*>(base + L.o);
+    const int dv = a->head_dim_v == 0 ? a->head_dim : a->head_dim_v;
+    launch_pad(a->q, a->q_stride, a->seqlen_q, a->num_q_heads, a->head_dim, a->batch, qp, s);
+    launch_pad(a->k, a->k_stride, a->seqlen_kv, a->num_kv_heads, a->head_dim, a->batch, kp, s);
+    launch_pad(a->v, a->v_stride, a->seqlen_kv, a->num_kv_heads, dv, a->batch, vp, s);
+    if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
+    pa.q = qp;
+    pa.k = kp;
+    pa.v = vp;
+    pa.o = op;
+    if (const int st = prefill_launch(&pa, s); st != FGQA_OK) return st;
+    const int64_t pieces = (int64_t)a->batch * a->seqlen_q * a->num_q_heads * 16;
+    hipLaunchKernelGGL(unpad_rows_kernel, dim3(copy_grid(pieces)), dim3(256), 0, s, op,
+                       static_cast<__bf16*>(a->o), a->o_stride[0], a->o_stride[1], a->o_stride[2], a->seqlen_q,
+                       a->num_q_heads, dv, pieces);
+    if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
+    return FGQA_OK;
+}
+
+}  // namespace
 }  // namespace fgqa
 
 using namespace fgqa;
@@ -1178,7 +1283,8 @@ extern "C" int fgqa_prefill_kernel_choice(const fgqa_prefill_args* a, int32_t* k
     if (kernel == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
     const int cus = device_cu_count();
     if (cus <= 0) return FGQA_ERR_HIP;
-    *kernel = plan::prefill_choice(a, cus);
+    const fgqa_prefill_args pa = plan::prefill_padded(a) ? plan::padded_args(a) : *a;
+    *kernel = plan::prefill_choice(&pa, cus);
     return FGQA_OK;
 }
 
@@ -1188,7 +1294,8 @@ extern "C" int fgqa_prefill_kernel_name(const fgqa_prefill_args* a, const char**
     if (name == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
     const int cus = device_cu_count();
     if (cus <= 0) return FGQA_ERR_HIP;
-    *name = plan::prefill_kernel_name(a, cus);
+    const fgqa_prefill_args pa = plan::prefill_padded(a) ? plan::padded_args(a) : *a;
+    *name = plan::prefill_kernel_name(&pa, cus);
     return FGQA_OK;
 }
 
@@ -1198,7 +1305,7 @@ extern "C" int fgqa_prefill_workspace_bytes(const fgqa_prefill_args* a, size_t* 
     if (bytes == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
     const int cus = device_cu_count();
     if (cus <= 0) return FGQA_ERR_HIP;
-    *bytes = plan::merge_scratch_bytes(a, plan::prefill_choice(a, cus), cus);
+    *bytes = plan::prefill_workspace_bytes(a, cus);
     return FGQA_OK;
 }
 
@@ -1206,7 +1313,14 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
     int st = plan::validate_prefill(a);
     if (st != FGQA_OK) return st;
     if (a->batch == 0 || a->seqlen_q == 0) return FGQA_OK;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    return plan::prefill_padded(a) ? prefill_padded_launch(a, s) : prefill_launch(a, s);
+}
 
+namespace fgqa {
+namespace {
+
+int prefill_launch(const fgqa_prefill_args* a, hipStream_t s) {
     PrefillParams p;
     p.q = static_cast<const __bf16*>(a->q);
     p.k = static_cast<const __bf16*>(a->k);
@@ -1269,7 +1383,6 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
     const bool swa = p.window > 0 || p.sink != nullptr;
     const bool mla = a->head_dim == 192;
     const bool split = choice == FGQA_KERNEL_SPLIT;
-    const hipStream_t s = static_cast<hipStream_t>(stream);
     if (choice == FGQA_KERNEL_WIDE || choice == FGQA_KERNEL_TALL) {
         // 256-row units: up to 8 heads of a KV group
         const int hbw = (p.group % 8 == 0) ? 8 : p.hb;
@@ -1340,3 +1453,6 @@ extern "C" int fgqa_prefill_bf16(const fgqa_prefill_args* a, void* stream) {
     if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
     return FGQA_OK;
 }
+
+}  // namespace
+}  // namespace fgqa

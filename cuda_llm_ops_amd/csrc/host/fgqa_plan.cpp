@@ -181,6 +181,44 @@ int plan_paged(const fgqa_decode_paged_args* a, DecodePlan* plan) {
 
 // ---------------------------------------------------------------- prefill
 
+bool prefill_padded(const fgqa_prefill_args* a) {
+    const int dv = a->head_dim_v == 0 ? a->head_dim : a->head_dim_v;
+    return a->head_dim > 0 && dv > 0 && a->head_dim <= kHeadDim && dv <= kHeadDim &&
+           !(a->head_dim == kHeadDim && dv == kHeadDim);
+}
+
+fgqa_prefill_args padded_args(const fgqa_prefill_args* a) {
+    fgqa_prefill_args p = *a;
+    p.head_dim = kHeadDim;
+    p.head_dim_v = 0;
+    const int64_t qs[3] = {(int64_t)a->seqlen_q * a->num_q_heads * kHeadDim, (int64_t)a->num_q_heads * kHeadDim,
+                           kHeadDim};
+    const int64_t ks[3] = {(int64_t)a->seqlen_kv * a->num_kv_heads * kHeadDim, (int64_t)a->num_kv_heads * kHeadDim,
+                           kHeadDim};
+    for (int i = 0; i < 3; ++i) {
+        p.q_stride[i] = p.o_stride[i] = qs[i];
+        p.k_stride[i] = p.v_stride[i] = ks[i];
+    }
+    p.q = p.k = p.v = p.o = nullptr;
+    p.workspace = nullptr;
+    p.workspace_bytes = 0;
+    return p;
+}
+
+PadLayout pad_layout(const fgqa_prefill_args* a, size_t merge_bytes) {
+    const i128 qb = (i128)a->batch * a->seqlen_q * a->num_q_heads * kHeadDim * 2;
+    const i128 kb = (i128)a->batch * a->seqlen_kv * a->num_kv_heads * kHeadDim * 2;
+    PadLayout L;
+    // the copies never touch the zeroed counter prefix, which later calls
+    // on the same workspace count on even when this one merges nothing
+    L.q = round256(merge_bytes > kPrefillZeroBytes ? merge_bytes : kPrefillZeroBytes);
+    L.k = L.q + round256(qb);
+    L.v = L.k + round256(kb);
+    L.o = L.v + round256(kb);
+    L.total = L.o + round256(qb);
+    return L;
+}
+
 int validate_prefill(const fgqa_prefill_args* a) {
     if (a == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
     if (a->batch < 0 || a->seqlen_q < 0 || a->seqlen_kv < 0 || a->num_q_heads <= 0 || a->num_kv_heads <= 0 ||
@@ -195,14 +233,16 @@ int validate_prefill(const fgqa_prefill_args* a) {
             return FGQA_ERR_INVALID_ARGUMENT;
     if (a->head_dim_v < 0) return FGQA_ERR_INVALID_ARGUMENT;
     const int dv = a->head_dim_v == 0 ? a->head_dim : a->head_dim_v;
-    // (128, 128) and the MLA shape (192, 128); MLA has no window / sink form
-    if (dv != kHeadDim || (a->head_dim != kHeadDim && a->head_dim != 192)) return FGQA_ERR_UNSUPPORTED;
+    // (128, 128), the MLA shape (192, 128), and head dims up to 128 run on
+    // zero-padded copies; MLA has no window / sink form
+    const bool padded = prefill_padded(a);
+    if (!padded && (dv != kHeadDim || (a->head_dim != kHeadDim && a->head_dim != 192))) return FGQA_ERR_UNSUPPORTED;
     if (a->head_dim == 192 && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
     if (a->kernel < FGQA_KERNEL_AUTO || a->kernel > FGQA_KERNEL_TALL) return FGQA_ERR_INVALID_ARGUMENT;
     // the window / sink variant has no split form
     if (a->kernel == FGQA_KERNEL_SPLIT && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
-    // the tall kernel: head dim 128, no window or sink
-    if (a->kernel == FGQA_KERNEL_TALL && (a->head_dim != kHeadDim || a->window_size > 0 || a->sink != nullptr))
+    // the tall kernel: head dim 128 (or padded to it), no window or sink
+    if (a->kernel == FGQA_KERNEL_TALL && (a->head_dim == 192 || a->window_size > 0 || a->sink != nullptr))
         return FGQA_ERR_UNSUPPORTED;
     if (a->seqlen_q > kMaxTokens || a->seqlen_kv > kMaxTokens) return FGQA_ERR_UNSUPPORTED;
     if (span_reaches_2g((int64_t)a->seqlen_q + 128, a->q_stride[1]) ||
@@ -218,8 +258,21 @@ int validate_prefill(const fgqa_prefill_args* a) {
     }
     // unit indices are 32-bit: (query blocks of 32 rows) x heads x batch
     if ((i128)ceil_div(a->seqlen_q, 32) * a->num_q_heads * a->batch >= kLim31) return FGQA_ERR_UNSUPPORTED;
+    if (padded) {
+        // the copies must pass as a (128, 128) call themselves, and the
+        // workspace that holds them stays within the planners' limit
+        fgqa_prefill_args p = padded_args(a);
+        const uintptr_t dummy = 256;   // validation only: aligned, non-null
+        p.q = p.k = p.v = reinterpret_cast<const void*>(dummy);
+        p.o = reinterpret_cast<void*>(dummy);
+        if (const int st = validate_prefill(&p); st != FGQA_OK) return st;
+        if ((i128)pad_layout(a, merge_scratch_bytes_for(kPrefillMaxSplit)).total >= kMaxWorkspace)
+            return FGQA_ERR_UNSUPPORTED;
+    }
     if (a->batch == 0 || a->seqlen_q == 0) return FGQA_OK;
     if (a->q == nullptr || a->k == nullptr || a->v == nullptr || a->o == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
+    // the copies are made with 2-byte accesses: any alignment and strides
+    if (padded) return FGQA_OK;
     if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o)) return FGQA_ERR_UNSUPPORTED;
     // (O rows go out as 16-byte stores, so O's strides need 8 elements too)
     for (int i = 0; i < 3; ++i)
@@ -268,6 +321,12 @@ int prefill_choice(const fgqa_prefill_args* a, int cus) {
     if (!swa && a->causal) return units < 2 * (int64_t)cus ? FGQA_KERNEL_SPLIT : FGQA_KERNEL_WIDE;
     if (units < 4 * (int64_t)cus && !swa) return FGQA_KERNEL_SPLIT;
     return FGQA_KERNEL_WHOLE;
+}
+
+size_t prefill_workspace_bytes(const fgqa_prefill_args* a, int cus) {
+    if (!prefill_padded(a)) return merge_scratch_bytes(a, prefill_choice(a, cus), cus);
+    const fgqa_prefill_args p = padded_args(a);
+    return pad_layout(a, merge_scratch_bytes(&p, prefill_choice(&p, cus), cus)).total;
 }
 
 size_t merge_scratch_bytes(const fgqa_prefill_args* a, int choice, int cus) {

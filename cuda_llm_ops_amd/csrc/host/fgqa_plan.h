@@ -70,6 +70,26 @@ constexpr int kPrefillPartFloats = 2 * 4 * 66 * 64;   // floats of one partial-r
 constexpr size_t kPrefillZeroBytes = FGQA_PREFILL_WORKSPACE_ZERO_BYTES;
 
 int validate_prefill(const fgqa_prefill_args* a);
+// Head dims up to 128 other than (128, 128): the call copies Q, K and V into
+// zero-padded [B, S, H, 128] rows, runs the (128, 128) kernels on them and
+// copies the first head_dim_v columns of O back.  (Zero columns add nothing
+// to Q.K^T, and the padded columns of O are dropped; the reference's Triton
+// kernels pad their head-dim blocks to a power of two the same way,
+// src/python/Triton/flash_gqa_kernel.py:266-269, 80-94.)
+bool prefill_padded(const fgqa_prefill_args* a);
+// The (128, 128) call on the copies: same shape and options, contiguous
+// strides, null tensor pointers and no workspace (the caller fills them in).
+fgqa_prefill_args padded_args(const fgqa_prefill_args* a);
+// Byte offsets in the padded call's workspace: the merge scratch of the
+// (128, 128) call at 0 (its zeroed prefix first; at least the prefix when
+// that call merges nothing), then the copies of Q, K, V and O, each 256-byte
+// aligned.
+struct PadLayout {
+    size_t q, k, v, o, total;
+};
+PadLayout pad_layout(const fgqa_prefill_args* a, size_t merge_bytes);
+// fgqa_prefill_workspace_bytes of a validated call.
+size_t prefill_workspace_bytes(const fgqa_prefill_args* a, int cus);
 // Unit pairs of the 256-row kernels (units of up to 8 heads of a KV group).
 int64_t wide_pairs(const fgqa_prefill_args* a);
 // Whether the 256-row kernels run unit pairs on two workgroups each (at most

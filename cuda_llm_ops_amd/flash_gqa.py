@@ -382,16 +382,32 @@ def _prefill_args(q, k, v, o, lse, scale, causal, layout, window_size=0, sink=No
 
 
 # (Q/K head dim, V/O head dim) pairs the prefill kernels are built for:
-# GQA, and MLA (src/python/Triton/flash_mla_kernel.py's 192 / 128).
+# GQA, and MLA (src/python/Triton/flash_mla_kernel.py's 192 / 128).  The
+# forward also takes any other pair with both dims at most 128: the library
+# runs it on copies zero-padded to 128, as the reference's Triton launcher
+# pads its head-dim blocks to a power of two
+# (src/python/Triton/flash_gqa_kernel.py:266-269).
 PREFILL_HEAD_DIMS = ((128, 128), (192, 128))
 
 
-def _check_head_dims(dqk, dv, window_size=0, sink=None):
-    if (dqk, dv) not in PREFILL_HEAD_DIMS:
+def _padded_head_dims(dqk, dv):
+    return 0 < dqk <= 128 and 0 < dv <= 128 and (dqk, dv) != (128, 128)
+
+
+def _check_head_dims(dqk, dv, window_size=0, sink=None, padded_ok=False):
+    if (dqk, dv) not in PREFILL_HEAD_DIMS and not (padded_ok and _padded_head_dims(dqk, dv)):
+        more = ", or both at most 128" if padded_ok else ""
         raise ValueError(f"(head_dim_qk, head_dim_v) = ({dqk}, {dv}) is not supported; "
-                         f"supported: {PREFILL_HEAD_DIMS}")
-    if dqk != dv and (int(window_size) != 0 or sink is not None):
-        raise ValueError("a sliding window or sink needs head_dim_qk == head_dim_v == 128")
+                         f"supported: {PREFILL_HEAD_DIMS}{more}")
+    if (dqk, dv) == (192, 128) and (int(window_size) != 0 or sink is not None):
+        raise ValueError("a sliding window or sink needs head_dim_qk == head_dim_v")
+
+
+def _out_ready(t, dqk, dv) -> bool:
+    """A prefill output the library can write: kernel-ready rows, or (head
+    dims run on padded copies, whose O is copied out element by element) rows
+    whose head dim is contiguous."""
+    return _kernel_ready(t) or (_padded_head_dims(dqk, dv) and t.stride(-1) == 1)
 
 
 # Merge scratch of the prefill kernels that split a unit over two workgroups
@@ -460,13 +476,13 @@ def _prefill_bshd_prepare(q, k, v, scale, out, lse, causal, window_size=0, sink=
         raise ValueError("K must be [B, Skv, Hkv, D] matching Q and V [B, Skv, Hkv, Dv]")
     if Hq % k.shape[2] != 0:
         raise ValueError("Query heads must be divisible by KV heads")
-    _check_head_dims(D, Dv, window_size, sink)
+    _check_head_dims(D, Dv, window_size, sink, padded_ok=True)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     q, k, v = _prep(q), _prep(k), _prep(v)
     if out is None:
         out = torch.empty((B, Sq, Hq, Dv), device=q.device, dtype=torch.bfloat16)
-    elif out.shape != (B, Sq, Hq, Dv) or out.dtype != torch.bfloat16 or not _kernel_ready(out):
+    elif out.shape != (B, Sq, Hq, Dv) or out.dtype != torch.bfloat16 or not _out_ready(out, D, Dv):
         raise ValueError("Output must be a bf16 [batch, seqlen_q, q_heads, head_dim_v] tensor with contiguous rows")
     if lse is None:
         lse = torch.empty((B, Hq, Sq), device=q.device, dtype=torch.float32)
@@ -603,7 +619,7 @@ def _launch_bhsd_prefill(kind, q, k, v, scale, out, lse, causal):
         raise ValueError("Query heads must be divisible by KV heads")
     if kind == "GQA" and head_dim_v != head_dim_qk:
         raise ValueError("head_dim_v must equal head_dim_qk on this path")
-    _check_head_dims(head_dim_qk, head_dim_v)
+    _check_head_dims(head_dim_qk, head_dim_v, padded_ok=True)
     if scale is None:
         scale = 1.0 / math.sqrt(head_dim_qk)
     qb, kb, vb = _prep(qb), _prep(kb), _prep(vb)
@@ -618,7 +634,7 @@ def _launch_bhsd_prefill(kind, q, k, v, scale, out, lse, causal):
             if out.dim() != 4:
                 raise ValueError("Output must be 4D when Q is 4D")
             out_b = out
-        if out_b.dtype != torch.bfloat16 or not _kernel_ready(out_b):
+        if out_b.dtype != torch.bfloat16 or not _out_ready(out_b, head_dim_qk, head_dim_v):
             raise ValueError("Output must be bf16 with contiguous, 16-byte aligned rows")
     if out_b.shape != (batch, q_heads, seqlen_q, head_dim_v):
         raise ValueError("Output must have shape [batch, q_heads, seqlen_q, head_dim_v]")
@@ -965,7 +981,7 @@ def launch_flash_swa_forward_bf16_kernel(q, k, v, scale=None, out=None, lse=None
             if out.dim() != 4:
                 raise ValueError("Output must be 4D when Q is 4D")
             out_b = out
-        if out_b.dtype != torch.bfloat16 or not _kernel_ready(out_b):
+        if out_b.dtype != torch.bfloat16 or not _out_ready(out_b, head_dim_qk, head_dim_v):
             raise ValueError("Output must be bf16 with contiguous, 16-byte aligned rows")
     if out_b.shape != (batch, q_heads, seqlen_q, head_dim_v):
         raise ValueError("Output must have shape [batch, q_heads, seqlen_q, head_dim_v]")

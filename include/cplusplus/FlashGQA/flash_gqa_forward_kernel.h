@@ -23,7 +23,9 @@
  * @param seqLengthKv Key/value sequence length.
  * @param numQueryHeads Number of query heads.
  * @param numKvHeads Number of KV heads (must divide numQueryHeads).
- * @param headDim Per-head embedding dimension (128).
+ * @param headDim Per-head embedding dimension: 128, or any value in [1, 128)
+ *        (run on copies zero-padded to 128, as the reference's Triton launcher
+ *        pads its head-dim blocks, src/python/Triton/flash_gqa_kernel.py:266-269).
  * @param causal Apply the top-left aligned causal mask (query i sees keys j <= i).
  */
 void LaunchFlashGqaForwardBf16Kernel(const bf16_t* q,
@@ -89,7 +91,8 @@ void LaunchFlashSwaForwardBf16Kernel(const bf16_t* q,
  * @brief MLA prefill forward (BSHD): Q/K head dim headDimQk, V/O head dim
  *        headDimV, the C++ counterpart of the reference's Triton-only MLA
  *        launcher (src/python/Triton/flash_mla_kernel.py:315-508, kernel
- *        :16-270).  Supported: (headDimQk, headDimV) = (192, 128) or (128, 128).
+ *        :16-270).  Supported: (headDimQk, headDimV) = (192, 128), or any pair
+ *        with both dims in [1, 128] (below 128 on zero-padded copies).
  * @param q Device query tensor [batchSize, seqLengthQ, numQueryHeads, headDimQk].
  * @param k Device key tensor [batchSize, seqLengthKv, numKvHeads, headDimQk].
  * @param v Device value tensor [batchSize, seqLengthKv, numKvHeads, headDimV].

@@ -220,7 +220,15 @@ int fgqa_decode_paged(const fgqa_decode_paged_args* args, void* stream);
  *           launch_flash_mla_forward_bf16_kernel, reference
  *           src/python/Triton/flash_mla_kernel.py:315-508 (kernel :16-270):
  *           q/k rows hold head_dim elements, v/o rows head_dim_v.  Supported:
- *           (128, 128), and (192, 128) without window or sink.
+ *           (128, 128); (192, 128) without window or sink; and any other pair
+ *           with both dims in [1, 128], which the call runs on copies of
+ *           q, k, v zero-padded to 128 (zero columns add nothing to q.k^T)
+ *           before copying the first head_dim_v columns of O out, as the
+ *           reference's Triton launcher pads its head-dim blocks to a power
+ *           of two (src/python/Triton/flash_gqa_kernel.py:266-269).  Those
+ *           copies are made element by element, so such calls need neither
+ *           16-byte alignment nor strides in multiples of 8.  Head dims
+ *           above 128 (other than MLA's) return FGQA_ERR_UNSUPPORTED.
  *   kernel  an fgqa_kernel_choice (0 = AUTO).  The window / sink variant has
  *           no split form: FGQA_KERNEL_SPLIT with either returns
  *           FGQA_ERR_UNSUPPORTED (FGQA_KERNEL_WIDE runs it).
@@ -228,7 +236,11 @@ int fgqa_decode_paged(const fgqa_decode_paged_args* args, void* stream);
  *           fgqa_prefill_workspace_bytes() bytes, 256-byte aligned, for the
  *           kernels that split a unit's KV range over two workgroups (the
  *           wide and tall kernels on causal grids whose unit pairs fill the
- *           CUs, such as S=4096, Hq=16, Hkv=1); the other shapes need none.
+ *           CUs, such as S=4096, Hq=16, Hkv=1), and for the padded copies
+ *           of head dims below 128 (after the counters and merge slots); the
+ *           other shapes need none.  With NULL / 0, head dims below 128 keep
+ *           their copies in the library's per-device cached buffer (the
+ *           decode's, grown with hipMalloc when too small).
  *           Its first FGQA_PREFILL_WORKSPACE_ZERO_BYTES bytes (the arrival
  *           counters) must be zero before its first use; every call leaves
  *           them zero when it completes, so the workspace can be reused

@@ -408,6 +408,89 @@ static void test_prefill_rejections() {
     CHECK(plan::validate_prefill(&b) == FGQA_ERR_INVALID_ARGUMENT);
 }
 
+// Head dims up to 128 other than (128, 128) run on zero-padded copies.
+static fgqa_prefill_args with_head_dims(fgqa_prefill_args a, int dqk, int dv) {
+    a.head_dim = dqk;
+    a.head_dim_v = dv;
+    a.q_stride[0] = (int64_t)a.seqlen_q * a.num_q_heads * dqk;
+    a.q_stride[1] = (int64_t)a.num_q_heads * dqk;
+    a.q_stride[2] = dqk;
+    a.k_stride[0] = (int64_t)a.seqlen_kv * a.num_kv_heads * dqk;
+    a.k_stride[1] = (int64_t)a.num_kv_heads * dqk;
+    a.k_stride[2] = dqk;
+    a.v_stride[0] = (int64_t)a.seqlen_kv * a.num_kv_heads * dv;
+    a.v_stride[1] = (int64_t)a.num_kv_heads * dv;
+    a.v_stride[2] = dv;
+    a.o_stride[0] = (int64_t)a.seqlen_q * a.num_q_heads * dv;
+    a.o_stride[1] = (int64_t)a.num_q_heads * dv;
+    a.o_stride[2] = dv;
+    return a;
+}
+
+static void test_prefill_padded_head_dims() {
+    const fgqa_prefill_args c4 = prefill_args(1, 4096, 16, 1, true);
+    CHECK(!plan::prefill_padded(&c4));
+    fgqa_prefill_args m = c4;
+    m.head_dim = 192;
+    m.head_dim_v = 128;
+    CHECK(!plan::prefill_padded(&m));
+    // config 4's shape at D = 64: the (128, 128) call on copies, whose
+    // workspace is the wide kernel's merge scratch, then Q, K, V and O
+    // padded to 128 (16 MiB, 1 MiB, 1 MiB, 16 MiB)
+    fgqa_prefill_args a = with_head_dims(c4, 64, 64);
+    CHECK(plan::prefill_padded(&a));
+    CHECK(plan::validate_prefill(&a) == FGQA_OK);
+    const fgqa_prefill_args p = plan::padded_args(&a);
+    CHECK(p.head_dim == 128 && p.head_dim_v == 0 && p.q == nullptr && p.workspace == nullptr);
+    CHECK(p.q_stride[0] == 4096 * 16 * 128 && p.q_stride[1] == 16 * 128 && p.q_stride[2] == 128);
+    CHECK(p.k_stride[1] == 128 && p.v_stride[1] == 128 && p.o_stride[1] == 16 * 128);
+    CHECK(p.causal == 1 && p.scale == a.scale && p.kernel == a.kernel);
+    CHECK(plan::prefill_choice(&p, kCus) == FGQA_KERNEL_WIDE);
+    const size_t merge = 4096u + 128u * 2 * 33792 * 4;
+    const plan::PadLayout L = plan::pad_layout(&a, merge);
+    CHECK(L.q == merge && L.k == L.q + (16u << 20) && L.v == L.k + (1u << 20) && L.o == L.v + (1u << 20));
+    CHECK(L.total == L.o + (16u << 20));
+    CHECK(plan::prefill_workspace_bytes(&a, kCus) == L.total);
+    CHECK(plan::prefill_workspace_bytes(&c4, kCus) == merge);
+    // no merge scratch: the copies still start after the zeroed counter
+    // prefix, which a later call on the same workspace may merge through
+    CHECK(plan::pad_layout(&a, 0).q == FGQA_PREFILL_WORKSPACE_ZERO_BYTES);
+    CHECK(plan::pad_layout(&a, 100).q == FGQA_PREFILL_WORKSPACE_ZERO_BYTES);
+    CHECK(plan::prefill_workspace_bytes(&a, 255) == plan::pad_layout(&a, 0).total);
+    // every pair with both dims in [1, 128]; odd dims, rows at any alignment
+    // (the copies are made with 2-byte accesses)
+    const int dims[][2] = {{64, 128}, {128, 64}, {1, 1}, {100, 36}, {8, 128}, {127, 127}};
+    for (const auto& d : dims) {
+        fgqa_prefill_args b = with_head_dims(c4, d[0], d[1]);
+        b.q = static_cast<const char*>(fake(1)) + 2;   // 2-byte aligned only
+        CHECK(plan::prefill_padded(&b));
+        CHECK(plan::validate_prefill(&b) == FGQA_OK);
+    }
+    // above 128 (other than MLA's Q/K 192 with V 128): not built
+    const int bad[][2] = {{129, 129}, {64, 129}, {256, 256}, {192, 64}, {128, 192}};
+    for (const auto& d : bad) {
+        fgqa_prefill_args b = with_head_dims(c4, d[0], d[1]);
+        CHECK(!plan::prefill_padded(&b));
+        CHECK(plan::validate_prefill(&b) == FGQA_ERR_UNSUPPORTED);
+    }
+    // the window and sink forms, and a forced tall kernel, take padded dims
+    fgqa_prefill_args w = a;
+    w.window_size = 512;
+    w.sink = reinterpret_cast<const float*>(fake(9));
+    CHECK(plan::validate_prefill(&w) == FGQA_OK);
+    w = a;
+    w.kernel = FGQA_KERNEL_TALL;
+    CHECK(plan::validate_prefill(&w) == FGQA_OK);
+    // a shape whose rows fit 32-bit offsets at D = 64 but whose copies at
+    // 128 do not: (2^20 - 72) rows of 16 x 128 elements reach 2^31 bytes
+    fgqa_prefill_args big = with_head_dims(prefill_args(1, (1 << 20) - 200, 16, 1, true), 64, 64);
+    fgqa_prefill_args big128 = prefill_args(1, (1 << 20) - 200, 16, 1, true);
+    CHECK(plan::validate_prefill(&big128) == FGQA_ERR_UNSUPPORTED);
+    CHECK(plan::validate_prefill(&big) == FGQA_ERR_UNSUPPORTED);
+    big = with_head_dims(prefill_args(1, (1 << 19) - 200, 16, 1, true), 64, 64);
+    CHECK(plan::validate_prefill(&big) == FGQA_OK);
+}
+
 // ---------------------------------------------------------------- backward
 
 static fgqa_prefill_backward_args backward_args(int B, int S, int hq, int hkv) {
@@ -719,6 +802,7 @@ int main() {
     test_paged();
     test_prefill_known_shapes();
     test_prefill_rejections();
+    test_prefill_padded_head_dims();
     test_backward();
     test_sparse();
     fuzz(20261202u, 200000);
