@@ -22,6 +22,7 @@ from .flash_gqa import (  # noqa: F401
     flash_sgqa_forward_bshd,
     prepare_sparse_prefill,
     PREFILL_HEAD_DIMS,
+    BACKWARD_HEAD_DIMS,
     paged_decode_workspace_bytes,
     prepare_backward,
     prepare_decode,

@@ -94,23 +94,27 @@ constexpr int kPwSmemBytes = kPwTileBytes + kPwQBytes + 16;   // + 3 words that 
 constexpr int pw_smem_bytes(int dk) { return dk == kHeadDim ? kPwSmemBytes : 2 * (64 * 384) + 2 * kPfVTileBytes + 16; }
 static_assert(kPfPartFloats == 2 * kPfWaves * kPfMergeFloats * kWave, "merge slot size");
 
-// Sizes that depend on the Q/K head dim kDk (128, or 192 for MLA).
+// Sizes that depend on the Q/K head dim kDk (128; 192 for MLA; 256, which
+// only the whole-range kernel is built for).
 template <int kDk>
 struct PfDims {
-    static_assert(kDk == 128 || kDk == 192, "Q/K head dim");
+    static_assert(kDk == 128 || kDk == 192 || kDk == 256, "Q/K head dim");
     static constexpr int kRowBytes = kDk * 2;                         // one K row
     static constexpr int kChunks = kDk / 8;                           // 16-byte chunks per K row
-    static constexpr int kKTileBytes = kPfTile * kRowBytes;           // 16 or 24 KB
+    static constexpr int kKTileBytes = kPfTile * kRowBytes;           // 16, 24 or 32 KB
     static constexpr int kGroupBytes = 2 * kKTileBytes + 2 * kPfVTileBytes;   // K0, K1, V0, V1
     static constexpr int kSteps = kDk / 16;                           // MFMA k-steps over the head dim
     static constexpr int kDmaK = kDk / 32;                            // K-tile DMA instructions per wave
-    static constexpr int kKoffRegs = kDk == 128 ? 8 : 4;              // per-lane K read offsets
+    // Per-lane K read offsets: k-steps kk and kk + kKoffRegs read chunks
+    // 2 * kKoffRegs apart, which the swizzle keeps 32 * kKoffRegs bytes apart.
+    static constexpr int kKoffRegs = kDk == 192 ? 4 : 8;
     // K swizzle: chunk c of row r sits in slot c ^ kswz(r).  16 consecutive
-    // rows read at one chunk hit 16 distinct 16-byte bank groups: 256-byte
-    // rows all start at bank 0 (XOR with r % 16); 384-byte rows start at bank
-    // 0 or 32 by row parity, so an XOR with (r / 2) % 8 (which keeps c inside
-    // its aligned block of 8) spreads each parity class over 8 groups.
-    static __device__ __forceinline__ int kswz(int r) { return kDk == 128 ? (r & 15) : ((r >> 1) & 7); }
+    // rows read at one chunk hit 16 distinct 16-byte bank groups: 256- and
+    // 512-byte rows all start at bank 0 (XOR with r % 16, which keeps c inside
+    // its aligned block of 16); 384-byte rows start at bank 0 or 32 by row
+    // parity, so an XOR with (r / 2) % 8 (which keeps c inside its aligned
+    // block of 8) spreads each parity class over 8 groups.
+    static __device__ __forceinline__ int kswz(int r) { return kDk == 192 ? ((r >> 1) & 7) : (r & 15); }
     static_assert(kPfWaves * kPfMergeFloats * kWave * 4 <= 2 * kGroupBytes, "merge area must fit in the tile buffers");
 };
 
@@ -281,7 +285,7 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
         for (int kk = 0; kk < D::kSteps; ++kk)
 #pragma unroll
             for (int tb = 0; tb < 2; ++tb) {
-                const int off = tb * 32 * D::kRowBytes + koff[kk % D::kKoffRegs] + (kk / D::kKoffRegs) * 128;
+                const int off = tb * 32 * D::kRowBytes + koff[kk % D::kKoffRegs] + (kk / D::kKoffRegs) * (D::kKoffRegs * 32);
                 const bf16x8_t ka = *reinterpret_cast<const bf16x8_t*>(kl + off);
                 s[tb] = mfma32(ka, qop[kk], s[tb]);
             }
@@ -665,7 +669,7 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
                 constexpr int i = decltype(ic)::value;
                 if constexpr (i < kA) {
                     constexpr int kk = i / 2, tb = i % 2;
-                    const int off = tb * 32 * D::kRowBytes + koff[kk % D::kKoffRegs] + (kk / D::kKoffRegs) * 128;
+                    const int off = tb * 32 * D::kRowBytes + koff[kk % D::kKoffRegs] + (kk / D::kKoffRegs) * (D::kKoffRegs * 32);
                     return *reinterpret_cast<const bf16x8_t*>(kl + off);
                 } else {
                     constexpr int kb = (i - kA) / 4, db = (i - kA) % 4;
@@ -1019,8 +1023,10 @@ __device__ __forceinline__ void pf_unit(const PrefillParams& p, unsigned char* s
     }
 }
 
+// (Q/K head dim 256: 96 KB of tile buffers, one workgroup per CU, so each
+// wave may hold up to 512 registers.)
 template <bool kSwa, int kDk>
-__global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(kPfThreads, kDk == 256 ? 1 : 2) void prefill_kernel(PrefillParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     int qb, hg, kvh, b;
     pf_rank_unit(p, blockIdx.x, &qb, &hg, &kvh, &b);
@@ -1169,35 +1175,38 @@ using plan::wide_pairs;
 
 }  // namespace
 
-// Head dims below 128: rows of D elements (at b/s/h strides) -> contiguous
-// zero-padded rows of 128.  A thread per 16-byte piece of a padded row
-// (grid-stride); 2-byte reads, so the source needs no alignment.
+// Head dims the kernels are not built for: rows of D elements (at b/s/h
+// strides) -> contiguous zero-padded rows of 8 << wlog2 elements (128, 192
+// or 256: pieces per row 16, 24 or 32, `ppr`).  A thread per 16-byte piece
+// of a padded row (grid-stride); 2-byte reads, so the source needs no
+// alignment.
 __global__ __launch_bounds__(256) void pad_rows_kernel(const __bf16* src, int64_t sb, int64_t ss, int64_t sh, int S,
-                                                       int H, int D, __bf16* dst, int64_t pieces) {
+                                                       int H, int D, int ppr, __bf16* dst, int64_t pieces) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < pieces; i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t row = i >> 4;
-        const int c = (int)(i & 15) * 8;
+        const int64_t row = i / ppr;
+        const int c = (int)(i - row * ppr) * 8;
         const int h = (int)(row % H);
         const int64_t t = row / H;
         const __bf16* r = src + (t / S) * sb + (t % S) * ss + h * sh;
         bf16x8_t v;
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = (c + j < D) ? r[c + j] : (__bf16)0.f;
-        *reinterpret_cast<bf16x8_t*>(dst + row * kHeadDim + c) = v;
+        *reinterpret_cast<bf16x8_t*>(dst + row * (8 * ppr) + c) = v;
     }
 }
 
-// The first D columns of contiguous rows of 128 -> rows at b/s/h strides.
-__global__ __launch_bounds__(256) void unpad_rows_kernel(const __bf16* src, __bf16* dst, int64_t db, int64_t ds,
-                                                         int64_t dh, int S, int H, int D, int64_t pieces) {
+// The first D columns of contiguous rows of 8 * ppr elements -> rows at
+// b/s/h strides.
+__global__ __launch_bounds__(256) void unpad_rows_kernel(const __bf16* src, int ppr, __bf16* dst, int64_t db,
+                                                         int64_t ds, int64_t dh, int S, int H, int D, int64_t pieces) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < pieces; i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t row = i >> 4;
-        const int c = (int)(i & 15) * 8;
+        const int64_t row = i / ppr;
+        const int c = (int)(i - row * ppr) * 8;
         if (c >= D) continue;
         const int h = (int)(row % H);
         const int64_t t = row / H;
         __bf16* r = dst + (t / S) * db + (t % S) * ds + h * dh;
-        const bf16x8_t v = *reinterpret_cast<const bf16x8_t*>(src + row * kHeadDim + c);
+        const bf16x8_t v = *reinterpret_cast<const bf16x8_t*>(src + row * (8 * ppr) + c);
 #pragma unroll
         for (int j = 0; j < 8; ++j)
             if (c + j < D) r[c + j] = v[j];
@@ -1212,18 +1221,21 @@ namespace {
 // The launches of a validated (128, 128) or MLA call.
 int prefill_launch(const fgqa_prefill_args* a, hipStream_t s);
 
-int launch_pad(const void* src, const int64_t* st, int S, int H, int D, int B, __bf16* dst, hipStream_t s) {
-    const int64_t pieces = (int64_t)B * S * H * 16;
+// rows of D elements -> rows of `width` (128, 192 or 256)
+int launch_pad(const void* src, const int64_t* st, int S, int H, int D, int B, int width, __bf16* dst,
+               hipStream_t s) {
+    const int64_t pieces = (int64_t)B * S * H * (width / 8);
     if (pieces == 0) return FGQA_OK;
     hipLaunchKernelGGL(pad_rows_kernel, dim3(copy_grid(pieces)), dim3(256), 0, s,
-                       static_cast<const __bf16*>(src), st[0], st[1], st[2], S, H, D, dst, pieces);
+                       static_cast<const __bf16*>(src), st[0], st[1], st[2], S, H, D, width / 8, dst, pieces);
     return FGQA_OK;
 }
 
-// Head dims below 128 (plan::prefill_padded): pad, run the (128, 128)
-// kernels on the copies, unpad O.  The copies live in the caller's workspace
-// after the merge scratch, or with none in the library's cached buffer (the
-// merge scratch then being the library's per-device one).
+// Head dims the kernels are not built for (plan::prefill_padded): pad, run
+// the built kernels on the copies (once per 128 columns of V), unpad O.  The
+// copies live in the caller's workspace after the merge scratch, or with
+// none in the library's cached buffer (the merge scratch then being the
+// library's per-device one).
 int prefill_padded_launch(const fgqa_prefill_args* a, hipStream_t s) {
     const int cus = device_cu_count();
     if (cus <= 0) return FGQA_ERR_HIP;
@@ -1255,17 +1267,22 @@ int prefill_padded_launch(const fgqa_prefill_args* a, hipStream_t s) {
     __bf16* vp = reinterpret_cast<__bf16*>(base + L.v);
     __bf16* op = reinterpret_cast<__bf16*>(base + L.o);
     const int dv = a->head_dim_v == 0 ? a->head_dim : a->head_dim_v;
-    launch_pad(a->q, a->q_stride, a->seqlen_q, a->num_q_heads, a->head_dim, a->batch, qp, s);
-    launch_pad(a->k, a->k_stride, a->seqlen_kv, a->num_kv_heads, a->head_dim, a->batch, kp, s);
-    launch_pad(a->v, a->v_stride, a->seqlen_kv, a->num_kv_heads, dv, a->batch, vp, s);
+    const int dkp = plan::padded_dk(a), dvp = plan::padded_dv(a);
+    launch_pad(a->q, a->q_stride, a->seqlen_q, a->num_q_heads, a->head_dim, a->batch, dkp, qp, s);
+    launch_pad(a->k, a->k_stride, a->seqlen_kv, a->num_kv_heads, a->head_dim, a->batch, dkp, kp, s);
+    launch_pad(a->v, a->v_stride, a->seqlen_kv, a->num_kv_heads, dv, a->batch, dvp, vp, s);
     if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
     pa.q = qp;
     pa.k = kp;
-    pa.v = vp;
-    pa.o = op;
-    if (const int st = prefill_launch(&pa, s); st != FGQA_OK) return st;
-    const int64_t pieces = (int64_t)a->batch * a->seqlen_q * a->num_q_heads * 16;
-    hipLaunchKernelGGL(unpad_rows_kernel, dim3(copy_grid(pieces)), dim3(256), 0, s, op,
+    // V / O rows of 256: a launch per 128 columns (each recomputes the
+    // scores and writes the same LSE)
+    for (int c0 = 0; c0 < dvp; c0 += kHeadDim) {
+        pa.v = vp + c0;
+        pa.o = op + c0;
+        if (const int st = prefill_launch(&pa, s); st != FGQA_OK) return st;
+    }
+    const int64_t pieces = (int64_t)a->batch * a->seqlen_q * a->num_q_heads * (dvp / 8);
+    hipLaunchKernelGGL(unpad_rows_kernel, dim3(copy_grid(pieces)), dim3(256), 0, s, op, dvp / 8,
                        static_cast<__bf16*>(a->o), a->o_stride[0], a->o_stride[1], a->o_stride[2], a->seqlen_q,
                        a->num_q_heads, dv, pieces);
     if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
@@ -1383,6 +1400,18 @@ int prefill_launch(const fgqa_prefill_args* a, hipStream_t s) {
     const bool swa = p.window > 0 || p.sink != nullptr;
     const bool mla = a->head_dim == 192;
     const bool split = choice == FGQA_KERNEL_SPLIT;
+    if (a->head_dim == 256) {
+        // Q/K head dim 256: the whole-range kernel (the plan refuses the
+        // other shapes); attribute slots 22, 23
+        const int sm = PfDims<256>::kGroupBytes;
+        const void* fn = swa ? reinterpret_cast<const void*>(prefill_kernel<true, 256>)
+                             : reinterpret_cast<const void*>(prefill_kernel<false, 256>);
+        if (const int e = set_kernel_smem_once(swa ? 23 : 22, fn, sm); e != FGQA_OK) return e;
+        if (swa) hipLaunchKernelGGL((prefill_kernel<true, 256>), dim3((unsigned)units), dim3(kPfThreads), sm, s, p);
+        else hipLaunchKernelGGL((prefill_kernel<false, 256>), dim3((unsigned)units), dim3(kPfThreads), sm, s, p);
+        if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
+        return FGQA_OK;
+    }
     if (choice == FGQA_KERNEL_WIDE || choice == FGQA_KERNEL_TALL) {
         // 256-row units: up to 8 heads of a KV group
         const int hbw = (p.group % 8 == 0) ? 8 : p.hb;

@@ -181,23 +181,37 @@ int plan_paged(const fgqa_decode_paged_args* a, DecodePlan* plan) {
 
 // ---------------------------------------------------------------- prefill
 
+namespace {
+int head_dim_v_of(const fgqa_prefill_args* a) { return a->head_dim_v == 0 ? a->head_dim : a->head_dim_v; }
+// the pairs the kernels are built for: Q/K 128, 192 or 256, V/O 128
+bool native_head_dims(int dqk, int dv) { return dv == kHeadDim && (dqk == kHeadDim || dqk == 192 || dqk == 256); }
+}  // namespace
+
 bool prefill_padded(const fgqa_prefill_args* a) {
-    const int dv = a->head_dim_v == 0 ? a->head_dim : a->head_dim_v;
-    return a->head_dim > 0 && dv > 0 && a->head_dim <= kHeadDim && dv <= kHeadDim &&
-           !(a->head_dim == kHeadDim && dv == kHeadDim);
+    const int dv = head_dim_v_of(a);
+    return a->head_dim > 0 && dv > 0 && a->head_dim <= 256 && dv <= 256 && !native_head_dims(a->head_dim, dv);
 }
+
+int padded_dk(const fgqa_prefill_args* a) {
+    return a->head_dim <= kHeadDim ? kHeadDim : a->head_dim == 192 ? 192 : 256;
+}
+
+int padded_dv(const fgqa_prefill_args* a) { return head_dim_v_of(a) <= kHeadDim ? kHeadDim : 2 * kHeadDim; }
 
 fgqa_prefill_args padded_args(const fgqa_prefill_args* a) {
     fgqa_prefill_args p = *a;
-    p.head_dim = kHeadDim;
-    p.head_dim_v = 0;
-    const int64_t qs[3] = {(int64_t)a->seqlen_q * a->num_q_heads * kHeadDim, (int64_t)a->num_q_heads * kHeadDim,
-                           kHeadDim};
-    const int64_t ks[3] = {(int64_t)a->seqlen_kv * a->num_kv_heads * kHeadDim, (int64_t)a->num_kv_heads * kHeadDim,
-                           kHeadDim};
+    const int dk = padded_dk(a), dv = padded_dv(a);
+    p.head_dim = dk;
+    p.head_dim_v = kHeadDim;
+    const int64_t qs[3] = {(int64_t)a->seqlen_q * a->num_q_heads * dk, (int64_t)a->num_q_heads * dk, dk};
+    const int64_t os[3] = {(int64_t)a->seqlen_q * a->num_q_heads * dv, (int64_t)a->num_q_heads * dv, dv};
+    const int64_t ks[3] = {(int64_t)a->seqlen_kv * a->num_kv_heads * dk, (int64_t)a->num_kv_heads * dk, dk};
+    const int64_t vs[3] = {(int64_t)a->seqlen_kv * a->num_kv_heads * dv, (int64_t)a->num_kv_heads * dv, dv};
     for (int i = 0; i < 3; ++i) {
-        p.q_stride[i] = p.o_stride[i] = qs[i];
-        p.k_stride[i] = p.v_stride[i] = ks[i];
+        p.q_stride[i] = qs[i];
+        p.o_stride[i] = os[i];
+        p.k_stride[i] = ks[i];
+        p.v_stride[i] = vs[i];
     }
     p.q = p.k = p.v = p.o = nullptr;
     p.workspace = nullptr;
@@ -206,16 +220,17 @@ fgqa_prefill_args padded_args(const fgqa_prefill_args* a) {
 }
 
 PadLayout pad_layout(const fgqa_prefill_args* a, size_t merge_bytes) {
-    const i128 qb = (i128)a->batch * a->seqlen_q * a->num_q_heads * kHeadDim * 2;
-    const i128 kb = (i128)a->batch * a->seqlen_kv * a->num_kv_heads * kHeadDim * 2;
+    const int dk = padded_dk(a), dv = padded_dv(a);
+    const i128 rq = (i128)a->batch * a->seqlen_q * a->num_q_heads * 2;
+    const i128 rk = (i128)a->batch * a->seqlen_kv * a->num_kv_heads * 2;
     PadLayout L;
     // the copies never touch the zeroed counter prefix, which later calls
     // on the same workspace count on even when this one merges nothing
     L.q = round256(merge_bytes > kPrefillZeroBytes ? merge_bytes : kPrefillZeroBytes);
-    L.k = L.q + round256(qb);
-    L.v = L.k + round256(kb);
-    L.o = L.v + round256(kb);
-    L.total = L.o + round256(qb);
+    L.k = L.q + round256(rq * dk);
+    L.v = L.k + round256(rk * dk);
+    L.o = L.v + round256(rk * dv);
+    L.total = L.o + round256(rq * dv);
     return L;
 }
 
@@ -232,18 +247,22 @@ int validate_prefill(const fgqa_prefill_args* a) {
         if (a->q_stride[i] < 0 || a->k_stride[i] < 0 || a->v_stride[i] < 0 || a->o_stride[i] < 0)
             return FGQA_ERR_INVALID_ARGUMENT;
     if (a->head_dim_v < 0) return FGQA_ERR_INVALID_ARGUMENT;
-    const int dv = a->head_dim_v == 0 ? a->head_dim : a->head_dim_v;
-    // (128, 128), the MLA shape (192, 128), and head dims up to 128 run on
-    // zero-padded copies; MLA has no window / sink form
+    const int dv = head_dim_v_of(a);
+    // (128, 128), the MLA shape (192, 128) and (256, 128); any other pair up
+    // to 256 runs on zero-padded copies; the 192 kernels have no window /
+    // sink form
     const bool padded = prefill_padded(a);
-    if (!padded && (dv != kHeadDim || (a->head_dim != kHeadDim && a->head_dim != 192))) return FGQA_ERR_UNSUPPORTED;
-    if (a->head_dim == 192 && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
+    if (!padded && !native_head_dims(a->head_dim, dv)) return FGQA_ERR_UNSUPPORTED;
+    const int dk_run = padded ? padded_dk(a) : a->head_dim;
+    if (dk_run == 192 && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
     if (a->kernel < FGQA_KERNEL_AUTO || a->kernel > FGQA_KERNEL_TALL) return FGQA_ERR_INVALID_ARGUMENT;
     // the window / sink variant has no split form
     if (a->kernel == FGQA_KERNEL_SPLIT && (a->window_size > 0 || a->sink != nullptr)) return FGQA_ERR_UNSUPPORTED;
     // the tall kernel: head dim 128 (or padded to it), no window or sink
-    if (a->kernel == FGQA_KERNEL_TALL && (a->head_dim == 192 || a->window_size > 0 || a->sink != nullptr))
+    if (a->kernel == FGQA_KERNEL_TALL && (dk_run != kHeadDim || a->window_size > 0 || a->sink != nullptr))
         return FGQA_ERR_UNSUPPORTED;
+    // Q/K head dim 256: the whole-range kernel only
+    if (dk_run == 256 && a->kernel != FGQA_KERNEL_AUTO && a->kernel != FGQA_KERNEL_WHOLE) return FGQA_ERR_UNSUPPORTED;
     if (a->seqlen_q > kMaxTokens || a->seqlen_kv > kMaxTokens) return FGQA_ERR_UNSUPPORTED;
     if (span_reaches_2g((int64_t)a->seqlen_q + 128, a->q_stride[1]) ||
         span_reaches_2g((int64_t)a->seqlen_kv + 128, a->k_stride[1]) ||
@@ -310,6 +329,7 @@ bool tall_on_pairs(const fgqa_prefill_args* a, int cus) { return a->causal && wi
 // The tall kernel runs only when forced.
 int prefill_choice(const fgqa_prefill_args* a, int cus) {
     if (a->kernel != FGQA_KERNEL_AUTO) return a->kernel;
+    if (a->head_dim == 256) return FGQA_KERNEL_WHOLE;
     const int group = a->num_q_heads / a->num_kv_heads;
     const int hb = group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
     const bool swa = a->window_size > 0 || a->sink != nullptr;

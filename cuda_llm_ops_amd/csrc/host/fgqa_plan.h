@@ -70,15 +70,21 @@ constexpr int kPrefillPartFloats = 2 * 4 * 66 * 64;   // floats of one partial-r
 constexpr size_t kPrefillZeroBytes = FGQA_PREFILL_WORKSPACE_ZERO_BYTES;
 
 int validate_prefill(const fgqa_prefill_args* a);
-// Head dims up to 128 other than (128, 128): the call copies Q, K and V into
-// zero-padded [B, S, H, 128] rows, runs the (128, 128) kernels on them and
-// copies the first head_dim_v columns of O back.  (Zero columns add nothing
-// to Q.K^T, and the padded columns of O are dropped; the reference's Triton
-// kernels pad their head-dim blocks to a power of two the same way,
+// Head-dim pairs up to 256 other than the built ones (Q/K 128, 192 or 256
+// with V/O 128): the call copies Q and K into zero-padded rows of
+// padded_dk() = 128, 192 or 256 elements and V into rows of padded_dv() =
+// 128 or 256, runs the built kernels on the copies (once per 128 columns of
+// V) and copies the first head_dim_v columns of O back.  (Zero columns add
+// nothing to Q.K^T, and the padded columns of O are dropped; the reference's
+// Triton kernels pad their head-dim blocks to a power of two the same way,
 // src/python/Triton/flash_gqa_kernel.py:266-269, 80-94.)
 bool prefill_padded(const fgqa_prefill_args* a);
-// The (128, 128) call on the copies: same shape and options, contiguous
-// strides, null tensor pointers and no workspace (the caller fills them in).
+int padded_dk(const fgqa_prefill_args* a);
+int padded_dv(const fgqa_prefill_args* a);
+// The call on the copies (head dims padded_dk() and 128, V and O rows of
+// padded_dv() elements): same shape and options, contiguous strides, null
+// tensor pointers and no workspace (the caller fills them in, and offsets V
+// and O by 128 columns for the second launch when padded_dv() is 256).
 fgqa_prefill_args padded_args(const fgqa_prefill_args* a);
 // Byte offsets in the padded call's workspace: the merge scratch of the
 // (128, 128) call at 0 (its zeroed prefix first; at least the prefix when

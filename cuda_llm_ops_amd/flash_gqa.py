@@ -40,6 +40,7 @@ __all__ = [
     "flash_sgqa_forward_bshd",
     "prepare_sparse_prefill",
     "PREFILL_HEAD_DIMS",
+    "BACKWARD_HEAD_DIMS",
     "decode_flash_gqa_bshd",
     "decode_flash_gqa_paged",
     "paged_decode_workspace_bytes",
@@ -382,25 +383,29 @@ def _prefill_args(q, k, v, o, lse, scale, causal, layout, window_size=0, sink=No
 
 
 # (Q/K head dim, V/O head dim) pairs the prefill kernels are built for:
-# GQA, and MLA (src/python/Triton/flash_mla_kernel.py's 192 / 128).  The
-# forward also takes any other pair with both dims at most 128: the library
-# runs it on copies zero-padded to 128, as the reference's Triton launcher
-# pads its head-dim blocks to a power of two
-# (src/python/Triton/flash_gqa_kernel.py:266-269).
-PREFILL_HEAD_DIMS = ((128, 128), (192, 128))
+# GQA, MLA (src/python/Triton/flash_mla_kernel.py's 192 / 128) and Q/K 256.
+# The forward also takes any other pair with both dims at most 256: the
+# library runs it on copies zero-padded to a built pair (V in 128-column
+# halves), as the reference's Triton launcher pads its head-dim blocks to a
+# power of two (src/python/Triton/flash_gqa_kernel.py:266-269).  The
+# backward takes (128, 128) and (192, 128).
+PREFILL_HEAD_DIMS = ((128, 128), (192, 128), (256, 128))
+BACKWARD_HEAD_DIMS = ((128, 128), (192, 128))
 
 
 def _padded_head_dims(dqk, dv):
-    return 0 < dqk <= 128 and 0 < dv <= 128 and (dqk, dv) != (128, 128)
+    return 0 < dqk <= 256 and 0 < dv <= 256 and (dqk, dv) not in PREFILL_HEAD_DIMS
 
 
 def _check_head_dims(dqk, dv, window_size=0, sink=None, padded_ok=False):
-    if (dqk, dv) not in PREFILL_HEAD_DIMS and not (padded_ok and _padded_head_dims(dqk, dv)):
-        more = ", or both at most 128" if padded_ok else ""
+    built = PREFILL_HEAD_DIMS if padded_ok else BACKWARD_HEAD_DIMS
+    if (dqk, dv) not in built and not (padded_ok and _padded_head_dims(dqk, dv)):
+        more = ", or both at most 256" if padded_ok else ""
         raise ValueError(f"(head_dim_qk, head_dim_v) = ({dqk}, {dv}) is not supported; "
-                         f"supported: {PREFILL_HEAD_DIMS}{more}")
-    if (dqk, dv) == (192, 128) and (int(window_size) != 0 or sink is not None):
-        raise ValueError("a sliding window or sink needs head_dim_qk == head_dim_v")
+                         f"supported: {built}{more}")
+    # the 192 kernels (MLA, and Q/K 192 with any V dim) have no window / sink form
+    if dqk == 192 and (int(window_size) != 0 or sink is not None):
+        raise ValueError("a sliding window or sink is not supported with head_dim_qk 192")
 
 
 def _out_ready(t, dqk, dv) -> bool:

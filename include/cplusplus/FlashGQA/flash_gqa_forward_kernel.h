@@ -23,9 +23,10 @@
  * @param seqLengthKv Key/value sequence length.
  * @param numQueryHeads Number of query heads.
  * @param numKvHeads Number of KV heads (must divide numQueryHeads).
- * @param headDim Per-head embedding dimension: 128, or any value in [1, 128)
- *        (run on copies zero-padded to 128, as the reference's Triton launcher
- *        pads its head-dim blocks, src/python/Triton/flash_gqa_kernel.py:266-269).
+ * @param headDim Per-head embedding dimension in [1, 256]: 128 runs the kernels
+ *        directly, other values run on copies zero-padded to 128 or 256, as the
+ *        reference's Triton launcher pads its head-dim blocks
+ *        (src/python/Triton/flash_gqa_kernel.py:266-269).
  * @param causal Apply the top-left aligned causal mask (query i sees keys j <= i).
  */
 void LaunchFlashGqaForwardBf16Kernel(const bf16_t* q,
@@ -92,7 +93,7 @@ void LaunchFlashSwaForwardBf16Kernel(const bf16_t* q,
  *        headDimV, the C++ counterpart of the reference's Triton-only MLA
  *        launcher (src/python/Triton/flash_mla_kernel.py:315-508, kernel
  *        :16-270).  Supported: (headDimQk, headDimV) = (192, 128), or any pair
- *        with both dims in [1, 128] (below 128 on zero-padded copies).
+ *        with both dims in [1, 256] (on zero-padded copies unless built).
  * @param q Device query tensor [batchSize, seqLengthQ, numQueryHeads, headDimQk].
  * @param k Device key tensor [batchSize, seqLengthKv, numKvHeads, headDimQk].
  * @param v Device value tensor [batchSize, seqLengthKv, numKvHeads, headDimV].

@@ -219,16 +219,21 @@ int fgqa_decode_paged(const fgqa_decode_paged_args* args, void* stream);
  *           head_dim_v = 128 is the MLA prefill, replacing the Triton-only
  *           launch_flash_mla_forward_bf16_kernel, reference
  *           src/python/Triton/flash_mla_kernel.py:315-508 (kernel :16-270):
- *           q/k rows hold head_dim elements, v/o rows head_dim_v.  Supported:
- *           (128, 128); (192, 128) without window or sink; and any other pair
- *           with both dims in [1, 128], which the call runs on copies of
- *           q, k, v zero-padded to 128 (zero columns add nothing to q.k^T)
- *           before copying the first head_dim_v columns of O out, as the
- *           reference's Triton launcher pads its head-dim blocks to a power
- *           of two (src/python/Triton/flash_gqa_kernel.py:266-269).  Those
- *           copies are made element by element, so such calls need neither
- *           16-byte alignment nor strides in multiples of 8.  Head dims
- *           above 128 (other than MLA's) return FGQA_ERR_UNSUPPORTED.
+ *           q/k rows hold head_dim elements, v/o rows head_dim_v.  Built:
+ *           (128, 128); (192, 128) without window or sink; (256, 128) (the
+ *           whole-range kernel only: FGQA_KERNEL_AUTO or _WHOLE).  Any other
+ *           pair with both dims in [1, 256] runs on copies of q and k
+ *           zero-padded to 128, 192 (for head_dim 192) or 256, and of v to
+ *           128 or 256 (then one launch per 128 columns, each recomputing the
+ *           scores), before the first head_dim_v columns of O are copied
+ *           out, as the reference's Triton launcher pads its head-dim blocks
+ *           to a power of two (src/python/Triton/flash_gqa_kernel.py:
+ *           266-269); zero columns add nothing to q.k^T.  Those copies are
+ *           made element by element, so such calls need neither 16-byte
+ *           alignment nor strides in multiples of 8.  Head dims above 256
+ *           return FGQA_ERR_UNSUPPORTED, and so do a window or sink with
+ *           head_dim 192 and FGQA_KERNEL_SPLIT / _WIDE / _TALL with q/k
+ *           padded to 256.
  *   kernel  an fgqa_kernel_choice (0 = AUTO).  The window / sink variant has
  *           no split form: FGQA_KERNEL_SPLIT with either returns
  *           FGQA_ERR_UNSUPPORTED (FGQA_KERNEL_WIDE runs it).

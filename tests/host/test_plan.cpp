@@ -380,7 +380,7 @@ static void test_prefill_rejections() {
     b.head_dim = 192;   // MLA shape (V stays 128)
     b.head_dim_v = 128;
     CHECK(plan::validate_prefill(&b) == FGQA_OK);
-    b.head_dim_v = 192;
+    b.head_dim_v = 320;
     CHECK(plan::validate_prefill(&b) == FGQA_ERR_UNSUPPORTED);
     b = a;
     b.o_stride[1] = 2052;
@@ -441,7 +441,7 @@ static void test_prefill_padded_head_dims() {
     CHECK(plan::prefill_padded(&a));
     CHECK(plan::validate_prefill(&a) == FGQA_OK);
     const fgqa_prefill_args p = plan::padded_args(&a);
-    CHECK(p.head_dim == 128 && p.head_dim_v == 0 && p.q == nullptr && p.workspace == nullptr);
+    CHECK(p.head_dim == 128 && p.head_dim_v == 128 && p.q == nullptr && p.workspace == nullptr);
     CHECK(p.q_stride[0] == 4096 * 16 * 128 && p.q_stride[1] == 16 * 128 && p.q_stride[2] == 128);
     CHECK(p.k_stride[1] == 128 && p.v_stride[1] == 128 && p.o_stride[1] == 16 * 128);
     CHECK(p.causal == 1 && p.scale == a.scale && p.kernel == a.kernel);
@@ -466,13 +466,55 @@ static void test_prefill_padded_head_dims() {
         CHECK(plan::prefill_padded(&b));
         CHECK(plan::validate_prefill(&b) == FGQA_OK);
     }
-    // above 128 (other than MLA's Q/K 192 with V 128): not built
-    const int bad[][2] = {{129, 129}, {64, 129}, {256, 256}, {192, 64}, {128, 192}};
+    // up to 256: Q/K padded to 128, 192 (MLA's kernels) or 256 (the
+    // whole-range kernel), V/O to 128 or 256 (two launches of 128 columns)
+    struct Pad { int dqk, dv, dk_run, dv_run; };
+    const Pad pads[] = {{129, 129, 256, 256}, {64, 129, 128, 256}, {256, 256, 256, 256}, {192, 64, 192, 128},
+                        {128, 192, 128, 256}, {200, 72, 256, 128}, {192, 192, 192, 256}, {1, 256, 128, 256}};
+    for (const Pad& d : pads) {
+        fgqa_prefill_args b = with_head_dims(c4, d.dqk, d.dv);
+        CHECK(plan::prefill_padded(&b));
+        CHECK(plan::validate_prefill(&b) == FGQA_OK);
+        CHECK(plan::padded_dk(&b) == d.dk_run && plan::padded_dv(&b) == d.dv_run);
+        const fgqa_prefill_args p2 = plan::padded_args(&b);
+        CHECK(p2.head_dim == d.dk_run && p2.head_dim_v == 128);
+        CHECK(p2.q_stride[2] == d.dk_run && p2.k_stride[2] == d.dk_run);
+        CHECK(p2.v_stride[2] == d.dv_run && p2.o_stride[2] == d.dv_run && p2.o_stride[1] == 16 * d.dv_run);
+        // Q/K 256 runs the whole-range kernel, which merges nothing
+        if (d.dk_run == 256) CHECK(plan::prefill_choice(&p2, kCus) == FGQA_KERNEL_WHOLE);
+        const plan::PadLayout Lb = plan::pad_layout(&b, 0);
+        CHECK(Lb.k - Lb.q == (size_t)4096 * 16 * d.dk_run * 2 && Lb.v - Lb.k == (size_t)4096 * d.dk_run * 2);
+        CHECK(Lb.o - Lb.v == (size_t)4096 * d.dv_run * 2 && Lb.total - Lb.o == (size_t)4096 * 16 * d.dv_run * 2);
+    }
+    // (256, 128) is built: no copies
+    fgqa_prefill_args n256 = with_head_dims(c4, 256, 128);
+    CHECK(!plan::prefill_padded(&n256));
+    CHECK(plan::validate_prefill(&n256) == FGQA_OK);
+    CHECK(plan::prefill_choice(&n256, kCus) == FGQA_KERNEL_WHOLE);
+    CHECK(plan::prefill_workspace_bytes(&n256, kCus) == 0);
+    n256.kernel = FGQA_KERNEL_SPLIT;
+    CHECK(plan::validate_prefill(&n256) == FGQA_ERR_UNSUPPORTED);
+    n256.kernel = FGQA_KERNEL_WHOLE;
+    CHECK(plan::validate_prefill(&n256) == FGQA_OK);
+    n256.window_size = 64;   // the whole-range kernel has the window form
+    CHECK(plan::validate_prefill(&n256) == FGQA_OK);
+    // above 256: not built
+    const int bad[][2] = {{257, 257}, {64, 257}, {300, 128}, {1000, 8}};
     for (const auto& d : bad) {
         fgqa_prefill_args b = with_head_dims(c4, d[0], d[1]);
         CHECK(!plan::prefill_padded(&b));
         CHECK(plan::validate_prefill(&b) == FGQA_ERR_UNSUPPORTED);
     }
+    // the 192 kernels have no window form, padded or not
+    fgqa_prefill_args w192 = with_head_dims(c4, 192, 64);
+    w192.window_size = 64;
+    CHECK(plan::validate_prefill(&w192) == FGQA_ERR_UNSUPPORTED);
+    // forced shapes the 256 kernel lacks
+    fgqa_prefill_args f256 = with_head_dims(c4, 160, 96);
+    f256.kernel = FGQA_KERNEL_WIDE;
+    CHECK(plan::validate_prefill(&f256) == FGQA_ERR_UNSUPPORTED);
+    f256.kernel = FGQA_KERNEL_TALL;
+    CHECK(plan::validate_prefill(&f256) == FGQA_ERR_UNSUPPORTED);
     // the window and sink forms, and a forced tall kernel, take padded dims
     fgqa_prefill_args w = a;
     w.window_size = 512;

@@ -202,18 +202,22 @@ def _prefill_args(**kw):
     (dict(kernel=_lib.FGQA_KERNEL_TALL, window=64), _lib.FGQA_ERR_UNSUPPORTED),    # tall: no window / sink
     (dict(kernel=_lib.FGQA_KERNEL_TALL, sink=4096), _lib.FGQA_ERR_UNSUPPORTED),
     (dict(kernel=_lib.FGQA_KERNEL_TALL, D=192, Dv=128), _lib.FGQA_ERR_UNSUPPORTED),   # tall: head dim 128
+    (dict(kernel=_lib.FGQA_KERNEL_TALL, D=200), _lib.FGQA_ERR_UNSUPPORTED),           # (padded to 256)
+    (dict(kernel=_lib.FGQA_KERNEL_SPLIT, D=256, Dv=128), _lib.FGQA_ERR_UNSUPPORTED),  # 256: whole-range only
+    (dict(kernel=_lib.FGQA_KERNEL_WIDE, D=160, Dv=96), _lib.FGQA_ERR_UNSUPPORTED),
     (dict(kernel=_lib.FGQA_KERNEL_SPLIT, window=64), _lib.FGQA_ERR_UNSUPPORTED),   # no split SWA kernel
     (dict(kernel=_lib.FGQA_KERNEL_SPLIT, sink=4096), _lib.FGQA_ERR_UNSUPPORTED),
     (dict(ostride=[256 * 16 * 128, 16 * 128 + 4, 128]), _lib.FGQA_ERR_UNSUPPORTED),  # O rows: 16-byte stores
-    (dict(D=256), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(D=257), _lib.FGQA_ERR_UNSUPPORTED),             # head dims above 256 are not built
+    (dict(D=512), _lib.FGQA_ERR_UNSUPPORTED),
     (dict(v=None), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(o=4096 + 8), _lib.FGQA_ERR_UNSUPPORTED),
     (dict(window=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(window=64, causal=0), _lib.FGQA_ERR_INVALID_ARGUMENT),   # a window is causal
     (dict(Dv=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
-    (dict(D=192), _lib.FGQA_ERR_UNSUPPORTED),             # head_dim_v 0 means 192: not built
-    (dict(D=192, Dv=64), _lib.FGQA_ERR_UNSUPPORTED),
-    (dict(D=128, Dv=192), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(D=192, window=64), _lib.FGQA_ERR_UNSUPPORTED),  # (192, 192) runs the 192 kernels: no window
+    (dict(D=192, Dv=64, sink=4096), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(D=128, Dv=300), _lib.FGQA_ERR_UNSUPPORTED),
     (dict(D=192, Dv=128, window=64), _lib.FGQA_ERR_UNSUPPORTED),   # MLA has no window form
     (dict(D=192, Dv=128, sink=4096), _lib.FGQA_ERR_UNSUPPORTED),
 ])

@@ -1,9 +1,11 @@
-"""GPU tests of the prefill with head dims below 128 against the CPU oracle.
+"""GPU tests of the prefill at head dims other than the built (128, 128),
+(192, 128) and (256, 128) against the CPU oracle.
 
 The reference's Triton launcher takes any head dim and pads its head-dim
 blocks to a power of two (src/python/Triton/flash_gqa_kernel.py:266-269);
-this library runs such calls on copies of Q, K and V zero-padded to 128 and
-copies the first head_dim_v columns of O back.  The oracle
+this library runs such calls on copies of Q and K zero-padded to 128, 192 or
+256 and of V to 128 or 256 (two launches of 128 columns), and copies the
+first head_dim_v columns of O back.  The oracle
 (oracle/fgqa_oracle.c: fgqa_oracle_prefill_bf16, _mla_bf16, _swa_bf16) takes
 the head dims as they are, so these tests check the padding against the
 unpadded maths.  Bar: max-abs 2e-2 and mean-abs 2e-3 on bf16 outputs, LSE
@@ -42,9 +44,17 @@ def _inputs(seed, B, Sq, Skv, Hq, Hkv, dqk, dv):
     return q, k, v
 
 
-@pytest.mark.parametrize("kernel", ["auto", "whole", "split", "wide"])
-@pytest.mark.parametrize("dqk,dv", [(64, 64), (32, 32), (96, 96), (100, 100), (64, 128), (128, 64), (72, 40),
-                                    (1, 8)])
+DIMS = [(64, 64), (32, 32), (96, 96), (100, 100), (64, 128), (128, 64), (72, 40), (1, 8),
+        (256, 256), (256, 128), (192, 64), (128, 192), (200, 72), (160, 160), (192, 192), (8, 256)]
+
+
+def _kernels(dqk):
+    """The kernel shapes a pair runs on: Q/K above 128 (other than 192) pads
+    to 256, which only the whole-range kernel is built for."""
+    return ["auto", "whole"] if dqk > 128 and dqk != 192 else ["auto", "whole", "split", "wide"]
+
+
+@pytest.mark.parametrize("dqk,dv,kernel", [(a, b, k) for a, b in DIMS for k in _kernels(a)])
 @pytest.mark.parametrize("B,Sq,Skv,Hq,Hkv,causal", [
     (1, 300, 300, 8, 2, True),
     (2, 200, 330, 4, 1, False),
@@ -83,20 +93,22 @@ def test_padded_equal_dims_match_the_gqa_oracle(cuda):
     assert not bool(o128[..., 64:].any())
 
 
-def test_padded_window_and_sink(cuda):
-    """The sliding-window form with a sink at D = 64."""
+@pytest.mark.parametrize("D", [64, 256, 200])
+def test_padded_window_and_sink(cuda, D):
+    """The sliding-window form with a sink at D = 64 (on the 128 kernels),
+    256 (the 256 whole-range kernel, V in two launches) and 200."""
     import torch
     fg = _fg()
-    print("D=64 window+sink", flush=True)
+    print(f"D={D} window+sink", flush=True)
     B, S, Hq, Hkv, W = 1, 700, 8, 2, 96
-    scale = 1.0 / 8
-    q, k, v = _inputs(3200, B, S, S, Hq, Hkv, 64, 64)
+    scale = 1.0 / math.sqrt(D)
+    q, k, v = _inputs(3200 + D, B, S, S, Hq, Hkv, D, D)
     sink = np.random.default_rng(5).random(Hq, dtype=np.float32) + 1e-6
     o_ref, l_ref = oracle.prefill_swa(q, k, v, scale, W, sink)
     qd, kd, vd = (to_torch_bf16(x, cuda) for x in (q, k, v))
     out, lse = fg.flash_gqa_forward_bshd(qd, kd, vd, scale, causal=True, window_size=W,
                                          sink=torch.from_numpy(sink).to(cuda))
-    _check(from_torch_bf16(out), lse.cpu().numpy(), o_ref, l_ref, "D=64 window+sink")
+    _check(from_torch_bf16(out), lse.cpu().numpy(), o_ref, l_ref, f"D={D} window+sink")
 
 
 def test_padded_strided_unaligned_tensors(cuda):

@@ -127,7 +127,8 @@ def test_mla_reference_mirror_bhsd(cuda):
     with pytest.raises(ValueError, match="Output must have shape"):
         fg.launch_flash_mla_forward_bf16_kernel(t(q), t(k), t(v), out=torch.empty_like(t(q)))
     with pytest.raises(ValueError, match="not supported"):
-        fg.launch_flash_mla_forward_bf16_kernel(t(q), t(k), t(v)[..., :64])
+        v320 = torch.zeros((*t(v).shape[:-1], 320), dtype=torch.bfloat16, device=cuda)
+        fg.launch_flash_mla_forward_bf16_kernel(t(q), t(k), v320)
 
 
 def test_mla_mirror_equal_dims_is_the_gqa_prefill(cuda):
@@ -170,5 +171,14 @@ def test_mla_cplusplus_entry(cuda):
     assert st() == 0
     torch.cuda.synchronize()
     _check(from_torch_bf16(od), ld.cpu().numpy(), o_ref, l_ref, "C++ MLA")
-    fn(p(qd), p(kd), p(vd), ctypes.c_float(SCALE), p(od), p(ld), B, S, S, Hq, Hkv, DQK, 64, True)
-    assert st() == -2   # (192, 64) is not built
+    # (192, 64): the 192 kernels on V zero-padded to 128
+    v64 = vd[..., :64].contiguous()
+    o64 = torch.zeros((B, S, Hq, 64), dtype=torch.bfloat16, device=cuda)
+    fn(p(qd), p(kd), p(v64), ctypes.c_float(SCALE), p(o64), p(ld), B, S, S, Hq, Hkv, DQK, 64, True)
+    assert st() == 0
+    torch.cuda.synchronize()
+    o_ref64, l_ref64 = oracle.prefill_mla(q, k, np.ascontiguousarray(v[..., :64]), SCALE, causal=True)
+    _check(from_torch_bf16(o64), ld.cpu().numpy(), o_ref64, l_ref64, "C++ (192, 64)")
+    # V rows above 256 are not built: refused before any launch
+    fn(p(qd), p(kd), p(vd), ctypes.c_float(SCALE), p(od), p(ld), B, S, S, Hq, Hkv, DQK, 320, True)
+    assert st() == -2
