@@ -70,8 +70,12 @@ def _normal(shape, seed, sigma, dev):
 
 
 # The auxiliary measurements each follow an idle gap (the CPU baseline, the
-# previous mode's setup): they warm up for at least this long.
-AUX_WARM_MS = 25.0
+# previous mode's setup): they warm up for at least this long.  After an idle
+# second, config 4's prefill ran 73-85 us per launch in its first 10 ms, 70-71
+# us at 25 ms and settled at 68.0 us from about 60 ms on (the same in three
+# trials on one MI355X), so a shorter warm-up times the clock's ramp, not the
+# kernel.
+AUX_WARM_MS = 150.0
 
 
 def _time_calls(fn, steps, warmup, min_warm_ms=0.0):

@@ -115,18 +115,20 @@ Stats time_launches(F&& launch, int warmup, int iters) {
     hipEvent_t e0, e1;
     HIP_CHECK(hipEventCreate(&e0));
     HIP_CHECK(hipEventCreate(&e1));
-    // at least `warmup` launches, and at least 20 ms of them: the CPU check of
-    // the previous configuration leaves the GPU idle for seconds, and its
-    // clock takes milliseconds to come back up
+    // at least `warmup` launches, and at least 150 ms of them: the CPU check
+    // of the previous configuration leaves the GPU idle for seconds, and the
+    // clock under a compute-bound kernel settles only after about 60 ms
+    // (config 4's prefill: 73-85 us per launch in the first 10 ms, 68 us from
+    // 60 ms on)
     for (int i = 0; i < warmup; ++i) launch();
     HIP_CHECK(hipDeviceSynchronize());
     {
         const auto t0 = std::chrono::steady_clock::now();
-        for (int i = 0; i < 4000; ++i) {
+        for (int i = 0; i < 40000; ++i) {
             launch();
             if ((i & 7) == 7) {
                 HIP_CHECK(hipDeviceSynchronize());
-                if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(20)) break;
+                if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(150)) break;
             }
         }
         HIP_CHECK(hipDeviceSynchronize());
