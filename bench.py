@@ -41,10 +41,11 @@ SCALE = 1.0 / math.sqrt(128)
 # with the commands are profiles/*_hbm_traffic.md.  Re-measure when a kernel
 # changes.
 # HBM bytes per dispatch of the dominant kernel, from rocprofv3 FETCH_SIZE (x 2.0,
-# the factor a 1 GiB copy calibrates) + WRITE_SIZE; re-measured on the current
-# kernels (decode 1,010,672,640 B; prefill 83,495,424 B: within 0.06 % of these).
+# the factor a 1 GiB copy calibrates) + WRITE_SIZE, on the current kernels
+# (decode_split_kernel with KV head pairs; the prefill's re-measurement read
+# 83,495,424 B, within 0.06 % of the figure below).
 TRAFFIC_BYTES = {
-    "decode_cfg2": 1010681051,   # = Q+K+V+O (1,010,565,120 B) + 0.01 %
+    "decode_cfg2": 1010671543,   # = Q+K+V+O (1,010,565,120 B) + 0.01 %
     "prefill_cfg4": 83448320,    # Q+O+LSE 32.25 MiB, K/V per XCD, split units' partials written and read back
 }
 
