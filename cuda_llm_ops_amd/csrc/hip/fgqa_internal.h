@@ -28,4 +28,14 @@ void* internal_workspace(size_t bytes, int* status);
 // kernel and per device).  slot: a distinct small index per kernel.
 int set_kernel_smem_once(int slot, const void* fn, int bytes);
 
+// Copies for head dims the kernels are not built for (flash_gqa_forward.hip):
+// B x S x H rows of D bf16 elements at element strides st = {b, s, h} ->
+// contiguous rows of `width` (a multiple of 8) zero-padded elements, and
+// back (the first D columns of each row).  2-byte accesses: no alignment
+// needed.  Launch errors are left for hipGetLastError.
+void launch_pad_rows(const void* src, const int64_t* st, int B, int S, int H, int D, int width, void* dst,
+                     hipStream_t s);
+void launch_unpad_rows(const void* src, int width, void* dst, const int64_t* st, int B, int S, int H, int D,
+                       hipStream_t s);
+
 }  // namespace fgqa

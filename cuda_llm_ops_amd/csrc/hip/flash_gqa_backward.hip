@@ -1251,9 +1251,16 @@ extern "C" int fgqa_prefill_backward_workspace_bytes(const fgqa_prefill_backward
     if (st != FGQA_OK) return st;
     const int cus = device_cu_count();
     if (cus <= 0) return FGQA_ERR_HIP;
-    *bytes = plan::plan_backward(a, cus).ws_bytes;
+    *bytes = plan::backward_workspace_bytes(a, cus);
     return FGQA_OK;
 }
+
+namespace fgqa {
+namespace {
+int backward_launch(const fgqa_prefill_backward_args* a, hipStream_t s);
+int backward_padded_launch(const fgqa_prefill_backward_args* a, hipStream_t s);
+}  // namespace
+}  // namespace fgqa
 
 extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, void* stream) {
     int st = plan::validate_backward(a);
@@ -1261,6 +1268,66 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     if (a->batch == 0 || (a->seqlen_q == 0 && a->seqlen_kv == 0)) return FGQA_OK;
     st = plan::validate_backward_pointers(a);
     if (st != FGQA_OK) return st;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    return plan::backward_padded(a) ? backward_padded_launch(a, s) : backward_launch(a, s);
+}
+
+namespace fgqa {
+namespace {
+
+// Head dims the kernels are not built for (plan::backward_padded): pad Q, K,
+// V, O and dO, run the built kernels on the copies, unpad dQ, dK and dV.
+// The copies live after the built call's own workspace, in the caller's
+// workspace or with none in the library's cached buffer.
+int backward_padded_launch(const fgqa_prefill_backward_args* a, hipStream_t s) {
+    const int cus = device_cu_count();
+    if (cus <= 0) return FGQA_ERR_HIP;
+    fgqa_prefill_backward_args pa = plan::backward_padded_args(a);
+    const size_t inner = plan::plan_backward(&pa, cus).ws_bytes;
+    const plan::BwdPadLayout L = plan::backward_pad_layout(a, inner);
+    std::unique_lock<std::mutex> lock;   // held through the launches when the library's buffer is used
+    unsigned char* ws = static_cast<unsigned char*>(a->workspace);
+    if (ws == nullptr && a->workspace_bytes == 0) {
+        lock = workspace_lock();
+        int st = FGQA_OK;
+        ws = static_cast<unsigned char*>(internal_workspace(L.total, &st));
+        if (st != FGQA_OK) return st;
+    } else if (ws == nullptr || a->workspace_bytes < L.total) {
+        return FGQA_ERR_WORKSPACE;
+    } else if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0) {
+        return FGQA_ERR_UNSUPPORTED;
+    }
+    if (inner > 0) {
+        pa.workspace = ws;   // the built call's workspace: the first `inner` bytes
+        pa.workspace_bytes = inner;
+    }
+    const int B = a->batch, sq = a->seqlen_q, skv = a->seqlen_kv, hq = a->num_q_heads, hkv = a->num_kv_heads;
+    const int dqk = a->head_dim, dv = a->head_dim_v == 0 ? a->head_dim : a->head_dim_v, dk = pa.head_dim;
+    pa.q = ws + L.q;
+    pa.k = ws + L.k;
+    pa.v = ws + L.v;
+    pa.o = ws + L.o;
+    pa.grad_o = ws + L.dout;
+    pa.grad_q = ws + L.dq;
+    pa.grad_k = ws + L.dk;
+    pa.grad_v = ws + L.dv;
+    launch_pad_rows(a->q, a->q_stride, B, sq, hq, dqk, dk, ws + L.q, s);
+    launch_pad_rows(a->k, a->k_stride, B, skv, hkv, dqk, dk, ws + L.k, s);
+    launch_pad_rows(a->v, a->v_stride, B, skv, hkv, dv, kHeadDim, ws + L.v, s);
+    launch_pad_rows(a->o, a->o_stride, B, sq, hq, dv, kHeadDim, ws + L.o, s);
+    launch_pad_rows(a->grad_o, a->grad_o_stride, B, sq, hq, dv, kHeadDim, ws + L.dout, s);
+    if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
+    if (const int st = backward_launch(&pa, s); st != FGQA_OK) return st;
+    launch_unpad_rows(ws + L.dq, dk, a->grad_q, a->grad_q_stride, B, sq, hq, dqk, s);
+    launch_unpad_rows(ws + L.dk, dk, a->grad_k, a->grad_k_stride, B, skv, hkv, dqk, s);
+    launch_unpad_rows(ws + L.dv, kHeadDim, a->grad_v, a->grad_v_stride, B, skv, hkv, dv, s);
+    if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
+    return FGQA_OK;
+}
+
+// The launches of a validated call with built head dims.
+int backward_launch(const fgqa_prefill_backward_args* a, hipStream_t s) {
+    int st = FGQA_OK;
     const int cus = device_cu_count();
     if (cus <= 0) return FGQA_ERR_HIP;
     const plan::BwdPlan pl = plan::plan_backward(a, cus);
@@ -1327,7 +1394,6 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     p.scale = a->scale;
     p.scale_log2 = a->scale * kLog2e;
 
-    const hipStream_t s = static_cast<hipStream_t>(stream);
     const int64_t rows_kv = (int64_t)p.batch * p.hkv * p.skv;
     const int64_t kv_units = (int64_t)p.n_kvblocks * p.kv_streams;
     const int64_t q_units = (int64_t)p.n_qunits * p.q_streams;
@@ -1415,3 +1481,6 @@ extern "C" int fgqa_prefill_backward_bf16(const fgqa_prefill_backward_args* a, v
     if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
     return FGQA_OK;
 }
+
+}  // namespace
+}  // namespace fgqa

@@ -1216,20 +1216,26 @@ __global__ __launch_bounds__(256) void unpad_rows_kernel(const __bf16* src, int 
 // Grid of the copy kernels: a thread per piece, at most 2^16 workgroups.
 inline unsigned copy_grid(int64_t pieces) { return (unsigned)(ceil_div(pieces, 256) < 65536 ? ceil_div(pieces, 256) : 65536); }
 
+void launch_pad_rows(const void* src, const int64_t* st, int B, int S, int H, int D, int width, void* dst,
+                     hipStream_t s) {
+    const int64_t pieces = (int64_t)B * S * H * (width / 8);
+    if (pieces == 0) return;
+    hipLaunchKernelGGL(pad_rows_kernel, dim3(copy_grid(pieces)), dim3(256), 0, s, static_cast<const __bf16*>(src),
+                       st[0], st[1], st[2], S, H, D, width / 8, static_cast<__bf16*>(dst), pieces);
+}
+
+void launch_unpad_rows(const void* src, int width, void* dst, const int64_t* st, int B, int S, int H, int D,
+                       hipStream_t s) {
+    const int64_t pieces = (int64_t)B * S * H * (width / 8);
+    if (pieces == 0) return;
+    hipLaunchKernelGGL(unpad_rows_kernel, dim3(copy_grid(pieces)), dim3(256), 0, s, static_cast<const __bf16*>(src),
+                       width / 8, static_cast<__bf16*>(dst), st[0], st[1], st[2], S, H, D, pieces);
+}
+
 namespace {
 
 // The launches of a validated (128, 128) or MLA call.
 int prefill_launch(const fgqa_prefill_args* a, hipStream_t s);
-
-// rows of D elements -> rows of `width` (128, 192 or 256)
-int launch_pad(const void* src, const int64_t* st, int S, int H, int D, int B, int width, __bf16* dst,
-               hipStream_t s) {
-    const int64_t pieces = (int64_t)B * S * H * (width / 8);
-    if (pieces == 0) return FGQA_OK;
-    hipLaunchKernelGGL(pad_rows_kernel, dim3(copy_grid(pieces)), dim3(256), 0, s,
-                       static_cast<const __bf16*>(src), st[0], st[1], st[2], S, H, D, width / 8, dst, pieces);
-    return FGQA_OK;
-}
 
 // Head dims the kernels are not built for (plan::prefill_padded): pad, run
 // the built kernels on the copies (once per 128 columns of V), unpad O.  The
@@ -1268,9 +1274,9 @@ int prefill_padded_launch(const fgqa_prefill_args* a, hipStream_t s) {
     __bf16* op = reinterpret_cast<__bf16*>(base + L.o);
     const int dv = a->head_dim_v == 0 ? a->head_dim : a->head_dim_v;
     const int dkp = plan::padded_dk(a), dvp = plan::padded_dv(a);
-    launch_pad(a->q, a->q_stride, a->seqlen_q, a->num_q_heads, a->head_dim, a->batch, dkp, qp, s);
-    launch_pad(a->k, a->k_stride, a->seqlen_kv, a->num_kv_heads, a->head_dim, a->batch, dkp, kp, s);
-    launch_pad(a->v, a->v_stride, a->seqlen_kv, a->num_kv_heads, dv, a->batch, dvp, vp, s);
+    launch_pad_rows(a->q, a->q_stride, a->batch, a->seqlen_q, a->num_q_heads, a->head_dim, dkp, qp, s);
+    launch_pad_rows(a->k, a->k_stride, a->batch, a->seqlen_kv, a->num_kv_heads, a->head_dim, dkp, kp, s);
+    launch_pad_rows(a->v, a->v_stride, a->batch, a->seqlen_kv, a->num_kv_heads, dv, dvp, vp, s);
     if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
     pa.q = qp;
     pa.k = kp;
@@ -1281,10 +1287,7 @@ int prefill_padded_launch(const fgqa_prefill_args* a, hipStream_t s) {
         pa.o = op + c0;
         if (const int st = prefill_launch(&pa, s); st != FGQA_OK) return st;
     }
-    const int64_t pieces = (int64_t)a->batch * a->seqlen_q * a->num_q_heads * (dvp / 8);
-    hipLaunchKernelGGL(unpad_rows_kernel, dim3(copy_grid(pieces)), dim3(256), 0, s, op, dvp / 8,
-                       static_cast<__bf16*>(a->o), a->o_stride[0], a->o_stride[1], a->o_stride[2], a->seqlen_q,
-                       a->num_q_heads, dv, pieces);
+    launch_unpad_rows(op, dvp, a->o, a->o_stride, a->batch, a->seqlen_q, a->num_q_heads, dv, s);
     if (hipGetLastError() != hipSuccess) return FGQA_ERR_HIP;
     return FGQA_OK;
 }

@@ -366,6 +366,53 @@ const char* prefill_kernel_name(const fgqa_prefill_args* a, int cus) {
 
 // ---------------------------------------------------------------- backward
 
+bool backward_padded(const fgqa_prefill_backward_args* a) {
+    const int dv = a->head_dim_v == 0 ? a->head_dim : a->head_dim_v;
+    const bool dk_ok = (a->head_dim > 0 && a->head_dim <= kHeadDim) || a->head_dim == 192;
+    const bool built = dv == kHeadDim && (a->head_dim == kHeadDim || a->head_dim == 192);
+    return dk_ok && dv > 0 && dv <= kHeadDim && !built;
+}
+
+int backward_padded_dk(const fgqa_prefill_backward_args* a) { return a->head_dim <= kHeadDim ? kHeadDim : 192; }
+
+fgqa_prefill_backward_args backward_padded_args(const fgqa_prefill_backward_args* a) {
+    fgqa_prefill_backward_args p = *a;
+    const int dk = backward_padded_dk(a);
+    p.head_dim = dk;
+    p.head_dim_v = kHeadDim;
+    const int64_t sq = a->seqlen_q, skv = a->seqlen_kv, hq = a->num_q_heads, hkv = a->num_kv_heads;
+    const int64_t qs[3] = {sq * hq * dk, hq * dk, dk}, os[3] = {sq * hq * kHeadDim, hq * kHeadDim, kHeadDim};
+    const int64_t ks[3] = {skv * hkv * dk, hkv * dk, dk}, vs[3] = {skv * hkv * kHeadDim, hkv * kHeadDim, kHeadDim};
+    for (int i = 0; i < 3; ++i) {
+        p.q_stride[i] = p.grad_q_stride[i] = qs[i];
+        p.o_stride[i] = p.grad_o_stride[i] = os[i];
+        p.k_stride[i] = p.grad_k_stride[i] = ks[i];
+        p.v_stride[i] = p.grad_v_stride[i] = vs[i];
+    }
+    p.q = p.k = p.v = p.o = p.grad_o = nullptr;
+    p.grad_q = p.grad_k = p.grad_v = nullptr;
+    p.workspace = nullptr;
+    p.workspace_bytes = 0;
+    return p;
+}
+
+BwdPadLayout backward_pad_layout(const fgqa_prefill_backward_args* a, size_t ws_bytes) {
+    const int dk = backward_padded_dk(a);
+    const i128 rq = (i128)a->batch * a->seqlen_q * a->num_q_heads * 2;
+    const i128 rk = (i128)a->batch * a->seqlen_kv * a->num_kv_heads * 2;
+    BwdPadLayout L;
+    L.q = round256(ws_bytes);
+    L.k = L.q + round256(rq * dk);
+    L.v = L.k + round256(rk * dk);
+    L.o = L.v + round256(rk * kHeadDim);
+    L.dout = L.o + round256(rq * kHeadDim);
+    L.dq = L.dout + round256(rq * kHeadDim);
+    L.dk = L.dq + round256(rq * dk);
+    L.dv = L.dk + round256(rk * dk);
+    L.total = L.dv + round256(rk * kHeadDim);
+    return L;
+}
+
 int validate_backward(const fgqa_prefill_backward_args* a) {
     if (a == nullptr) return FGQA_ERR_INVALID_ARGUMENT;
     if (a->batch < 0 || a->seqlen_q < 0 || a->seqlen_kv < 0 || a->num_q_heads <= 0 || a->num_kv_heads <= 0 ||
@@ -384,16 +431,21 @@ int validate_backward(const fgqa_prefill_backward_args* a) {
     // MLA has no sliding-window form
     if (a->head_dim_v < 0) return FGQA_ERR_INVALID_ARGUMENT;
     const int dv = a->head_dim_v == 0 ? a->head_dim : a->head_dim_v;
-    if (dv != kHeadDim || (a->head_dim != kHeadDim && a->head_dim != 192)) return FGQA_ERR_UNSUPPORTED;
-    if (a->head_dim == 192 && a->window_size > 0) return FGQA_ERR_UNSUPPORTED;
+    // other head dims up to 128 (Q/K up to 128 or 192, V/O up to 128) run on
+    // zero-padded copies
+    const bool padded = backward_padded(a);
+    if (!padded && (dv != kHeadDim || (a->head_dim != kHeadDim && a->head_dim != 192))) return FGQA_ERR_UNSUPPORTED;
+    const int dk_run = padded ? backward_padded_dk(a) : a->head_dim;
+    if (dk_run == 192 && a->window_size > 0) return FGQA_ERR_UNSUPPORTED;
     const int group = a->num_q_heads / a->num_kv_heads;
     if (a->kv_head_split < 0 || a->kv_head_split > group || (a->kv_head_split > 0 && group % a->kv_head_split != 0))
         return FGQA_ERR_INVALID_ARGUMENT;
     if (a->dq_kernel < FGQA_KERNEL_AUTO || a->dq_kernel > FGQA_KERNEL_SPLIT) return FGQA_ERR_INVALID_ARGUMENT;
     // the 192-wide dQ kernel needs one wave per SIMD: it has no split form
-    if (a->dq_kernel == FGQA_KERNEL_SPLIT && a->head_dim == 192) return FGQA_ERR_UNSUPPORTED;
-    // query rows past sq must read as zero (rows may not overlap)
-    if (a->q_stride[1] < a->head_dim || a->grad_o_stride[1] < kHeadDim) return FGQA_ERR_UNSUPPORTED;
+    if (a->dq_kernel == FGQA_KERNEL_SPLIT && dk_run == 192) return FGQA_ERR_UNSUPPORTED;
+    // query rows past sq must read as zero (rows may not overlap; the
+    // padded copies are contiguous)
+    if (!padded && (a->q_stride[1] < a->head_dim || a->grad_o_stride[1] < kHeadDim)) return FGQA_ERR_UNSUPPORTED;
     if (a->seqlen_q > kMaxTokens || a->seqlen_kv > kMaxTokens) return FGQA_ERR_UNSUPPORTED;
     if (span_reaches_2g((int64_t)a->seqlen_q + 128, a->q_stride[1]) ||
         span_reaches_2g((int64_t)a->seqlen_q + 128, a->grad_o_stride[1]) ||
@@ -411,8 +463,15 @@ int validate_backward(const fgqa_prefill_backward_args* a) {
     // the row statistics are addressed through one buffer resource
     if ((i128)a->batch * a->num_q_heads * a->seqlen_q * 8 >= kLim31) return FGQA_ERR_UNSUPPORTED;
     // the dK/dV partials of a full head split stay describable
-    if ((i128)a->batch * a->num_q_heads * a->seqlen_kv * (a->head_dim + kHeadDim) * 4 > kMaxWorkspace)
+    if ((i128)a->batch * a->num_q_heads * a->seqlen_kv * (dk_run + kHeadDim) * 4 > kMaxWorkspace)
         return FGQA_ERR_UNSUPPORTED;
+    if (padded) {
+        // the copies must pass as a built call themselves, and the workspace
+        // that holds them stays within the planners' limit
+        const fgqa_prefill_backward_args p = backward_padded_args(a);
+        if (const int st = validate_backward(&p); st != FGQA_OK) return st;
+        if ((i128)backward_pad_layout(a, 0).total >= kMaxWorkspace) return FGQA_ERR_UNSUPPORTED;
+    }
     return FGQA_OK;
 }
 
@@ -422,6 +481,8 @@ int validate_backward_pointers(const fgqa_prefill_backward_args* a) {
         return FGQA_ERR_INVALID_ARGUMENT;
     if (a->seqlen_kv > 0 && (a->k == nullptr || a->v == nullptr || a->grad_k == nullptr || a->grad_v == nullptr))
         return FGQA_ERR_INVALID_ARGUMENT;
+    // padded head dims: the copies are made with 2-byte accesses
+    if (backward_padded(a)) return FGQA_OK;
     const void* ptrs[8] = {a->q, a->k, a->v, a->o, a->grad_o, a->grad_q, a->grad_k, a->grad_v};
     for (const void* ptr : ptrs)
         if (!aligned16(ptr)) return FGQA_ERR_UNSUPPORTED;
@@ -460,6 +521,12 @@ BwdPlan plan_backward(const fgqa_prefill_backward_args* a, int cus) {
     pl.part_v_bytes = round256(parts * kHeadDim);
     pl.ws_bytes = pl.stat_bytes + pl.part_k_bytes + pl.part_v_bytes;
     return pl;
+}
+
+size_t backward_workspace_bytes(const fgqa_prefill_backward_args* a, int cus) {
+    if (!backward_padded(a)) return plan_backward(a, cus).ws_bytes;
+    const fgqa_prefill_backward_args p = backward_padded_args(a);
+    return backward_pad_layout(a, plan_backward(&p, cus).ws_bytes).total;
 }
 
 int check_backward_grid(const fgqa_prefill_backward_args* a, const BwdPlan& pl) {

@@ -122,6 +122,27 @@ struct BwdPlan {
 };
 
 int validate_backward(const fgqa_prefill_backward_args* a);
+// Q/K head dims up to 128 (or 192) with V/O head dims up to 128, other than
+// the built (128, 128) and (192, 128): the call copies Q, K, V, O and dO
+// into zero-padded rows (Q/K of backward_padded_dk() = 128 or 192 elements,
+// the others of 128), runs the built kernels on the copies and copies the
+// first head_dim / head_dim_v columns of dQ, dK and dV back.  Zero columns
+// of Q and K add nothing to the scores, zero columns of O and dO nothing to
+// the row statistic sum(O * dO), and the padded gradient columns are dropped.
+bool backward_padded(const fgqa_prefill_backward_args* a);
+int backward_padded_dk(const fgqa_prefill_backward_args* a);
+// The call on the copies: same shape and options, contiguous strides, null
+// tensor pointers and no workspace (the caller fills them in).
+fgqa_prefill_backward_args backward_padded_args(const fgqa_prefill_backward_args* a);
+// Byte offsets in the padded call's workspace: the built call's workspace
+// (ws_bytes) at 0, then the copies of Q, K, V, O, dO, dQ, dK, dV, each
+// 256-byte aligned.
+struct BwdPadLayout {
+    size_t q, k, v, o, dout, dq, dk, dv, total;
+};
+BwdPadLayout backward_pad_layout(const fgqa_prefill_backward_args* a, size_t ws_bytes);
+// fgqa_prefill_backward_workspace_bytes of a validated call.
+size_t backward_workspace_bytes(const fgqa_prefill_backward_args* a, int cus);
 int validate_backward_pointers(const fgqa_prefill_backward_args* a);
 BwdPlan plan_backward(const fgqa_prefill_backward_args* a, int cus);
 // FGQA_ERR_UNSUPPORTED when a grid or a row count of the launches planned by

@@ -388,7 +388,8 @@ def _prefill_args(q, k, v, o, lse, scale, causal, layout, window_size=0, sink=No
 # library runs it on copies zero-padded to a built pair (V in 128-column
 # halves), as the reference's Triton launcher pads its head-dim blocks to a
 # power of two (src/python/Triton/flash_gqa_kernel.py:266-269).  The
-# backward takes (128, 128) and (192, 128).
+# backward is built for (128, 128) and (192, 128), and takes Q/K head dims
+# up to 128 (or 192) with V/O head dims up to 128 on padded copies.
 PREFILL_HEAD_DIMS = ((128, 128), (192, 128), (256, 128))
 BACKWARD_HEAD_DIMS = ((128, 128), (192, 128))
 
@@ -397,10 +398,16 @@ def _padded_head_dims(dqk, dv):
     return 0 < dqk <= 256 and 0 < dv <= 256 and (dqk, dv) not in PREFILL_HEAD_DIMS
 
 
+def _padded_backward_head_dims(dqk, dv):
+    return (0 < dqk <= 128 or dqk == 192) and 0 < dv <= 128 and (dqk, dv) not in BACKWARD_HEAD_DIMS
+
+
 def _check_head_dims(dqk, dv, window_size=0, sink=None, padded_ok=False):
+    """padded_ok: the forward's rule (any pair up to 256); else the backward's."""
     built = PREFILL_HEAD_DIMS if padded_ok else BACKWARD_HEAD_DIMS
-    if (dqk, dv) not in built and not (padded_ok and _padded_head_dims(dqk, dv)):
-        more = ", or both at most 256" if padded_ok else ""
+    padded = _padded_head_dims(dqk, dv) if padded_ok else _padded_backward_head_dims(dqk, dv)
+    if (dqk, dv) not in built and not padded:
+        more = ", or both at most 256" if padded_ok else ", or Q/K up to 128 (or 192) with V/O up to 128"
         raise ValueError(f"(head_dim_qk, head_dim_v) = ({dqk}, {dv}) is not supported; "
                          f"supported: {built}{more}")
     # the 192 kernels (MLA, and Q/K 192 with any V dim) have no window / sink form
@@ -730,10 +737,13 @@ def backward_workspace_bytes(batch, seqlen_q, seqlen_kv, num_q_heads, num_kv_hea
     return int(n.value)
 
 
-def _grad_out(t, shape, ref, name):
+def _grad_out(t, shape, ref, name, padded=False):
+    """A gradient output: kernel-ready rows, or with padded head dims (whose
+    gradients are copied out element by element) rows with a contiguous head dim."""
     if t is None:
         return torch.empty(shape, device=ref.device, dtype=torch.bfloat16)
-    if tuple(t.shape) != tuple(shape) or t.dtype != torch.bfloat16 or not _kernel_ready(t):
+    ready = _kernel_ready(t) or (padded and t.stride(-1) == 1)
+    if tuple(t.shape) != tuple(shape) or t.dtype != torch.bfloat16 or not ready:
         raise ValueError(f"{name} must be a bf16 tensor of shape {list(shape)} with contiguous, aligned rows")
     return t
 
@@ -762,9 +772,10 @@ def _backward_bshd_prepare(q, k, v, o, lse, grad_o, scale, causal, grad_q, grad_
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     q, k, v, o, grad_o = (_prep(t) for t in (q, k, v, o, grad_o))
-    grad_q = _grad_out(grad_q, q.shape, q, "grad_q")
-    grad_k = _grad_out(grad_k, k.shape, q, "grad_k")
-    grad_v = _grad_out(grad_v, v.shape, q, "grad_v")
+    padded = _padded_backward_head_dims(D, Dv)
+    grad_q = _grad_out(grad_q, q.shape, q, "grad_q", padded)
+    grad_k = _grad_out(grad_k, k.shape, q, "grad_k", padded)
+    grad_v = _grad_out(grad_v, v.shape, q, "grad_v", padded)
     a = _backward_args(q, k, v, o, lse, grad_o, grad_q, grad_k, grad_v, scale, causal, "bshd", workspace,
                        window_size, kv_head_split, dq_kernel)
     return a, (grad_q, grad_k, grad_v), (q, k, v, o, lse, grad_o, grad_q, grad_k, grad_v, workspace)

@@ -335,7 +335,13 @@ int fgqa_prefill_kernel_name(const fgqa_prefill_args* args, const char** name);
  *   launch_flash_mla_backward_bf16_kernel (src/python/Triton/
  *   flash_mla_backward_kernel.py:788-969, kernel :202-786): q, k, grad_q,
  *   grad_k have 192-element rows, v, o, grad_o, grad_v 128-element rows.
- *   Supported: (128, 128) and (192, 128) without a window.
+ *   Built: (128, 128), and (192, 128) without a window.  Q/K head dims up to
+ *   128 (or 192, without a window) with V/O head dims up to 128 run on copies
+ *   of q, k, v, o, grad_o zero-padded to a built pair (element by element:
+ *   no alignment needed), the first columns of the padded gradients copied
+ *   out; the copies live in the workspace after the built call's own bytes
+ *   (fgqa_prefill_backward_workspace_bytes includes them).  Other head dims
+ *   return FGQA_ERR_UNSUPPORTED.
  * kv_head_split  0: automatic.  n >= 1 (a divisor of Hq / Hkv): the dK/dV pass
  *   splits each KV head's query heads over n workgroups whose fp32 partials a
  *   reduction sums (n = 1: no partials).  It changes the workspace size.

@@ -608,6 +608,55 @@ static void test_backward() {
     a = backward_args(1, 4096, 16, 1);
     a.q_stride[1] = 64;
     CHECK(plan::validate_backward(&a) == FGQA_ERR_UNSUPPORTED);
+    // padded head dims: Q/K up to 128 (run at 128) or 192 (run at 192), V/O
+    // up to 128 (run at 128); any alignment
+    {
+        struct Pad { int dqk, dv, dk_run; bool ok; };
+        const Pad pads[] = {{64, 64, 128, true},   {1, 1, 128, true},    {100, 36, 128, true}, {192, 64, 192, true},
+                            {128, 64, 128, true},  {64, 128, 128, true}, {200, 128, 0, false}, {64, 129, 0, false},
+                            {256, 128, 0, false}, {128, 192, 0, false}};
+        for (const Pad& d : pads) {
+            fgqa_prefill_backward_args b = backward_args(1, 4096, 16, 1);
+            b.head_dim = d.dqk;
+            b.head_dim_v = d.dv;
+            const int64_t qs[3] = {4096LL * 16 * d.dqk, 16LL * d.dqk, d.dqk}, os[3] = {4096LL * 16 * d.dv, 16LL * d.dv, d.dv};
+            const int64_t ks[3] = {4096LL * d.dqk, d.dqk, d.dqk}, vs[3] = {4096LL * d.dv, d.dv, d.dv};
+            memcpy(b.q_stride, qs, sizeof qs);
+            memcpy(b.grad_q_stride, qs, sizeof qs);
+            memcpy(b.o_stride, os, sizeof os);
+            memcpy(b.grad_o_stride, os, sizeof os);
+            memcpy(b.k_stride, ks, sizeof ks);
+            memcpy(b.grad_k_stride, ks, sizeof ks);
+            memcpy(b.v_stride, vs, sizeof vs);
+            memcpy(b.grad_v_stride, vs, sizeof vs);
+            b.grad_v = static_cast<char*>(b.grad_v) + 2;   // 2-byte aligned only
+            CHECK(plan::backward_padded(&b) == d.ok);
+            CHECK(plan::validate_backward(&b) == (d.ok ? FGQA_OK : FGQA_ERR_UNSUPPORTED));
+            if (!d.ok) continue;
+            CHECK(plan::validate_backward_pointers(&b) == FGQA_OK);
+            CHECK(plan::backward_padded_dk(&b) == d.dk_run);
+            const fgqa_prefill_backward_args p = plan::backward_padded_args(&b);
+            CHECK(p.head_dim == d.dk_run && p.head_dim_v == 128 && p.q == nullptr && p.workspace == nullptr);
+            CHECK(p.q_stride[1] == 16 * d.dk_run && p.grad_k_stride[1] == d.dk_run && p.o_stride[1] == 16 * 128);
+            CHECK(!plan::backward_padded(&p) && plan::validate_backward(&p) == FGQA_OK);
+            const size_t inner = plan::plan_backward(&p, kCus).ws_bytes;
+            const plan::BwdPadLayout L = plan::backward_pad_layout(&b, inner);
+            const size_t rq = 4096u * 16 * 2, rk = 4096u * 2;
+            CHECK(L.q == inner && L.k - L.q == rq * d.dk_run && L.v - L.k == rk * d.dk_run);
+            CHECK(L.o - L.v == rk * 128 && L.dout - L.o == rq * 128 && L.dq - L.dout == rq * 128);
+            CHECK(L.dk - L.dq == rq * d.dk_run && L.dv - L.dk == rk * d.dk_run && L.total - L.dv == rk * 128);
+            CHECK(plan::backward_workspace_bytes(&b, kCus) == L.total);
+            fgqa_prefill_backward_args w = b;
+            w.window_size = 64;
+            CHECK(plan::validate_backward(&w) == (d.dk_run == 192 ? FGQA_ERR_UNSUPPORTED : FGQA_OK));
+            w = b;
+            w.dq_kernel = FGQA_KERNEL_SPLIT;
+            CHECK(plan::validate_backward(&w) == (d.dk_run == 192 ? FGQA_ERR_UNSUPPORTED : FGQA_OK));
+        }
+        const fgqa_prefill_backward_args built = backward_args(1, 4096, 16, 1);
+        CHECK(!plan::backward_padded(&built));
+        CHECK(plan::backward_workspace_bytes(&built, kCus) == plan::plan_backward(&built, kCus).ws_bytes);
+    }
     // a huge batch without query rows: the row statistics are empty, but the
     // dK/dV grid of 2^31 - 1 batches x 2^12 heads cannot be indexed
     a = backward_args(INT_MAX, 0, 4096, 4096);

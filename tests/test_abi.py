@@ -387,13 +387,15 @@ def _backward_args(**kw):
     (dict(Hq=15, Hkv=2), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(Sq=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(scale=float("nan")), _lib.FGQA_ERR_INVALID_ARGUMENT),
-    (dict(D=64), _lib.FGQA_ERR_UNSUPPORTED),
+    (dict(D=200), _lib.FGQA_ERR_UNSUPPORTED),             # Q/K 200: neither built nor padded
+    (dict(D=64, Dv=200), _lib.FGQA_ERR_UNSUPPORTED),      # V/O above 128
     (dict(lse=None), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(grad_k=None), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(grad_v=4096 + 4), _lib.FGQA_ERR_UNSUPPORTED),
     (dict(window=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
     (dict(window=64, causal=0), _lib.FGQA_ERR_INVALID_ARGUMENT),   # the window is causal only
-    (dict(D=192, Dv=64), _lib.FGQA_ERR_UNSUPPORTED),               # MLA is (192, 128) only
+    (dict(D=192, Dv=160), _lib.FGQA_ERR_UNSUPPORTED),              # V/O above 128
+    (dict(D=192, Dv=64, window=64), _lib.FGQA_ERR_UNSUPPORTED),    # padded to 192: no window form
     (dict(D=192, Dv=128, window=64), _lib.FGQA_ERR_UNSUPPORTED),   # no MLA window form
     (dict(D=128, Dv=192), _lib.FGQA_ERR_UNSUPPORTED),
     (dict(Dv=-1), _lib.FGQA_ERR_INVALID_ARGUMENT),
