@@ -27,7 +27,7 @@
  * @param seqLengthKv Key/value sequence length.
  * @param numQueryHeads Number of query heads.
  * @param numKvHeads Number of KV heads (must divide numQueryHeads).
- * @param headDim Per-head embedding dimension (128).
+ * @param headDim Per-head embedding dimension: 128, or any value in [1, 128) on zero-padded copies.
  * @param causal The forward's top-left aligned causal mask (query i sees keys j <= i).
  *
  * Uses the library's per-device cached workspace on the default stream; the
@@ -88,8 +88,9 @@ void LaunchFlashSwaBackwardBf16Kernel(const bf16_t* q,
  * (src/python/Triton/flash_mla_backward_kernel.py:788-969, kernel :202-786).
  * q, gradQ [B, Sq, Hq, headDimQk]; k, gradK [B, Skv, Hkv, headDimQk];
  * v, gradV [B, Skv, Hkv, headDimV]; o, gradO [B, Sq, Hq, headDimV]; lse from
- * LaunchFlashMlaForwardBf16Kernel.  (headDimQk, headDimV) is (192, 128) or
- * (128, 128).  Other parameters as LaunchFlashGqaBackwardBf16Kernel.
+ * LaunchFlashMlaForwardBf16Kernel.  (headDimQk, headDimV): built for (192, 128)
+ * and (128, 128); headDimQk up to 128 (or 192) with headDimV up to 128 runs on
+ * zero-padded copies.  Other parameters as LaunchFlashGqaBackwardBf16Kernel.
  */
 void LaunchFlashMlaBackwardBf16Kernel(const bf16_t* q,
                                       const bf16_t* k,
