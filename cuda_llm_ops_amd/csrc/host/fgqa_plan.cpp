@@ -332,13 +332,22 @@ int prefill_choice(const fgqa_prefill_args* a, int cus) {
     if (a->head_dim == 256) return FGQA_KERNEL_WHOLE;
     const int group = a->num_q_heads / a->num_kv_heads;
     const int hb = group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
-    const bool swa = a->window_size > 0 || a->sink != nullptr;
+    const bool win = a->window_size > 0;
+    const bool swa = win || a->sink != nullptr;
     const int64_t units = ceil_div(a->seqlen_q, 128 / hb) * (int64_t)(group / hb) * a->num_kv_heads * a->batch;
     const int64_t pairs = wide_pairs(a);
     const int64_t wide_grid = 16 * ceil_div(pairs, 8);
     if (!swa && a->causal && pairs <= kPrefillMaxSplit && wide_grid <= cus && 8 * wide_grid >= 7 * (int64_t)cus)
         return FGQA_KERNEL_WIDE;
     if (!swa && a->causal) return units < 2 * (int64_t)cus ? FGQA_KERNEL_SPLIT : FGQA_KERNEL_WIDE;
+    // A window of at least 1536 keys (24 tiles per unit), or a sink without a
+    // window over a grid of a 128-row unit per CU: the 256-row kernels'
+    // shared tiles pay for their fewer, longer units.  Measured on four
+    // shapes (S = 4096 to 16384, Hkv 1 and 8): windows of 1536-3072 keys 3-8 %
+    // faster than the whole-range kernel (at 512-1024 keys its two workgroups
+    // per CU win or tie); a sink alone 4-20 % faster (config 4's shape: 87.5
+    // against 70.1 us).
+    if (swa && a->causal && (win ? a->window_size >= 1536 : units >= (int64_t)cus)) return FGQA_KERNEL_WIDE;
     if (units < 4 * (int64_t)cus && !swa) return FGQA_KERNEL_SPLIT;
     return FGQA_KERNEL_WHOLE;
 }

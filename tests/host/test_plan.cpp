@@ -354,6 +354,21 @@ static void test_prefill_known_shapes() {
     fgqa_prefill_args w = prefill_args(1, 4096, 16, 1, true);
     w.window_size = 512;
     CHECK(plan::prefill_choice(&w, kCus) == FGQA_KERNEL_WHOLE);
+    w.window_size = 1024;
+    CHECK(plan::prefill_choice(&w, kCus) == FGQA_KERNEL_WHOLE);
+    // long windows, and a sink without a window over 2 units per CU: the
+    // 256-row kernels (no split form with a window or sink)
+    w.window_size = 1536;
+    CHECK(plan::prefill_choice(&w, kCus) == FGQA_KERNEL_WIDE);
+    w.window_size = 0;
+    w.sink = reinterpret_cast<const float*>(fake(9));
+    CHECK(plan::prefill_choice(&w, kCus) == FGQA_KERNEL_WIDE);
+    fgqa_prefill_args ws = prefill_args(1, 2048, 16, 1, true);   // 256 units of 128 rows
+    ws.sink = w.sink;
+    CHECK(plan::prefill_choice(&ws, kCus) == FGQA_KERNEL_WIDE);
+    ws = prefill_args(1, 1024, 16, 1, true);
+    ws.sink = w.sink;
+    CHECK(plan::prefill_choice(&ws, kCus) == FGQA_KERNEL_WHOLE);
 }
 
 static void test_prefill_rejections() {

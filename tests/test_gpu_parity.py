@@ -453,6 +453,13 @@ def test_prefill_auto_kernel_choice(cuda):
     assert choice(1, 1024, 16, 16, dk=192) == "split"
     assert choice(4, 16384, 32, 8, causal=False) == "whole"
     assert choice(1, 4096, 16, 1, window_size=128) == "whole"
+    assert choice(1, 4096, 16, 1, window_size=1024) == "whole"
+    assert choice(1, 4096, 16, 1, window_size=2048) == "wide"   # long windows: the 256-row kernels
+    sink = torch.ones(16, dtype=torch.float32, device=cuda)
+    if cus == 256:
+        assert choice(1, 4096, 16, 1, sink=sink) == "wide"     # a sink alone, a unit per CU or more
+        assert choice(1, 2048, 16, 1, sink=sink) == "wide"
+    assert choice(1, 1024, 16, 1, sink=sink) == "whole"
     assert choice(1, 4096, 16, 1, kernel="split") == "split"
 
 

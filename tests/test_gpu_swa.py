@@ -61,6 +61,34 @@ def test_swa_shapes(cuda, kernel, B, S, Hq, Hkv, window, with_sink):
     _check(*_case(cuda, 1000 + S + window, B, S, S, Hq, Hkv, window, with_sink, kernel), what)
 
 
+@pytest.mark.parametrize("window", [0, 2048])
+def test_swa_long_window_and_sink_only_config4_shape(cuda, window):
+    """Config 4's shape (B=1, S=4096, Hq=16, Hkv=1) with a sink and no window,
+    and with a 2048-key window: AUTO runs the 256-row kernel there; its rows
+    (first, middle, last blocks) and the whole-range kernel's match the
+    oracle (a window of S keys stands for none)."""
+    import torch
+    fg = _fg()
+    B, S, Hq, Hkv = 1, 4096, 16, 1
+    q = gpu_normal_bf16((B, S, Hq, 128), 61, 1.0, cuda)
+    k = gpu_normal_bf16((B, S, Hkv, 128), 62, 1.0, cuda)
+    v = gpu_normal_bf16((B, S, Hkv, 128), 63, 1.0, cuda)
+    sink = np.random.default_rng(7).random(Hq).astype(np.float32) * 4 + 1e-6
+    sd = torch.from_numpy(sink).to(cuda)
+    if torch.cuda.get_device_properties(cuda).multi_processor_count == 256:
+        assert fg.prefill_kernel_choice(q, k, v, window_size=window, sink=sd) == "wide"
+    h = [from_torch_bf16(x) for x in (q, k, v)]
+    for kern in ("auto", "whole"):
+        print(f"swa config 4 shape window={window} kernel={kern}", flush=True)
+        out, lse = fg.flash_gqa_forward_bshd(q, k, v, SCALE, causal=True, window_size=window, sink=sd, kernel=kern)
+        torch.cuda.synchronize()
+        for r0, r1 in ((0, 64), (2000, 2064), (S - 64, S)):
+            o_ref, l_ref = oracle.prefill_swa(h[0][:, r0:r1], h[1][:, :r1], h[2][:, :r1], SCALE, window or S, sink,
+                                              q_offset=r0)
+            _check(from_torch_bf16(out[:, r0:r1]), lse[:, :, r0:r1].cpu().numpy(), o_ref, l_ref,
+                   f"swa window={window} kernel={kern} rows {r0}:{r1}")
+
+
 def test_swa_split_kernel_request_is_unsupported(cuda):
     """The window / sink variant has no split form: asking for it is an error
     (FGQA_ERR_UNSUPPORTED), not a silent fallback."""
