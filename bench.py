@@ -32,6 +32,7 @@ if ROOT not in sys.path:
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
 BF16_PEAK_TFLOPS = 2516.6      # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/clk/CU
+PEAK_SCLK_MHZ = 2400.0         # the shader clock that figure assumes
 SCALE = 1.0 / math.sqrt(128)
 
 # HBM bytes per launch of the dominant kernel, from rocprofv3 --pmc FETCH_SIZE and
@@ -116,7 +117,60 @@ def _time_calls(fn, steps, warmup, min_warm_ms=0.0):
         b.record()
     torch.cuda.synchronize()
     per = sorted(a.elapsed_time(b) for a, b in evs)
+    # then `steps` calls more between two clock samples, for _clock_fields
+    global _LAST_SCLK_MHZ
+    _LAST_SCLK_MHZ = _sclk_mhz(fn, steps)
     return total, per
+
+
+# Shader clock (MHz) averaged over the last `_time_calls` call's extra pass
+# (None when the two samples ran on different XCDs or the entry is missing).
+_LAST_SCLK_MHZ = None
+
+
+def _sclk_mhz(fn, n, samples=1024):
+    """Average shader clock over n back-to-back calls: fgqa_clock_sample
+    before and after them on torch's current stream (the launch stream)
+    reads, from `samples` workgroups spread over the CUs, each CU's
+    shader-clock counter and the 100 MHz real-time counter; the median over
+    the CUs sampled both times."""
+    import ctypes
+
+    import torch
+
+    from cuda_llm_ops_amd import _lib
+    buf = torch.zeros((2, samples, 3), dtype=torch.int64, device="cuda")
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    L = _lib.lib()
+    if L.fgqa_clock_sample(ctypes.c_void_p(buf[0].data_ptr()), samples, s) != 0:
+        return None
+    for _ in range(n):
+        fn()
+    if L.fgqa_clock_sample(ctypes.c_void_p(buf[1].data_ptr()), samples, s) != 0:
+        return None
+    torch.cuda.synchronize()
+    first = {}
+    for t, r, cu in buf[0].tolist():
+        first.setdefault(cu, (t, r))
+    mhz = []
+    for t, r, cu in buf[1].tolist():
+        if cu in first and r > first[cu][1] and t > first[cu][0]:
+            mhz.append((t - first[cu][0]) / (r - first[cu][1]) * 100.0)
+            del first[cu]
+    if not mhz:
+        return None
+    mhz.sort()
+    return round(mhz[len(mhz) // 2], 1)
+
+
+def _clock_fields(tflops):
+    """The MFMA roofline's clock fields: the shader clock the kernel sustained
+    over its measurement, and the fraction of the dense peak scaled to that
+    clock (the 2,516.6 TFLOP/s figure assumes 2.4 GHz)."""
+    if not _LAST_SCLK_MHZ:
+        return {"sclk_mhz": None, "frac_at_sclk": None}
+    return {"sclk_mhz": _LAST_SCLK_MHZ,
+            "frac_at_sclk": round(tflops / (BF16_PEAK_TFLOPS * _LAST_SCLK_MHZ / PEAK_SCLK_MHZ), 4)}
 
 
 def _decode_setup(cfg, dev, seed=2):
@@ -161,7 +215,7 @@ def bench_decode(cfg_id, steps, warmup, split_tokens, dev):
               if cfg["ragged"] else "decode_split_kernel + decode_combine_kernel (split-KV)")
     return dict(cfg=cfg, q=q, k=k, v=v, lens=lens, out=out, kv_bytes=kv_bytes, qo_bytes=qo_bytes,
                 ms_step=ms_step, avg_launch_ms=avg_launch_ms, median_ms=per[len(per) // 2], min_ms=per[0],
-                kernel=kernel)
+                kernel=kernel, sclk_mhz=_LAST_SCLK_MHZ)
 
 
 def _host_u16(t):
@@ -282,7 +336,7 @@ def bench_prefill(cfg_id, steps, warmup, dev, keep=None):
                 us_avg=round(avg * 1e3, 2), us_median=round(per[len(per) // 2] * 1e3, 2),
                 us_min=round(per[0] * 1e3, 2),
                 roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
-                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4), **_clock_fields(tflops),
                           "traffic": TRAFFIC_BYTES.get(f"prefill_cfg{cfg_id}"),
                           "kernel": kernel,
                           "algorithmic_flops": flops})
@@ -411,7 +465,7 @@ def bench_swa(steps, warmup, dev, window=512):
     return dict(config=f"sliding-window prefill with sink, B={B} S={S} Hq={Hq} Hkv={Hkv} D=128 window={window}",
                 us_avg=round(avg * 1e3, 2), us_min=round(per[0] * 1e3, 2),
                 roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
-                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4), **_clock_fields(tflops),
                           "algorithmic_flops": flops})
 
 
@@ -439,7 +493,7 @@ def bench_mla(steps, warmup, dev):
                 us_avg=round(avg * 1e3, 2), us_median=round(per[len(per) // 2] * 1e3, 2),
                 us_min=round(per[0] * 1e3, 2),
                 roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
-                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4), **_clock_fields(tflops),
                           "algorithmic_flops": flops})
 
 
@@ -490,7 +544,7 @@ def bench_sparse(steps, warmup, dev):
                 us_min=round(per[0] * 1e3, 2),
                 gathered_bytes=gathered, gather_GBs=round(gathered / (avg * 1e-3) / 1e9, 1),
                 roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
-                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4), **_clock_fields(tflops),
                           "algorithmic_flops": flops})
 
 
@@ -522,7 +576,7 @@ def bench_backward(cfg_id, steps, warmup, dev):
                 us_avg=round(avg * 1e3, 2), us_median=round(per[len(per) // 2] * 1e3, 2),
                 us_min=round(per[0] * 1e3, 2),
                 roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
-                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4), **_clock_fields(tflops),
                           "kernel": "bwd_dq(_split) + bwd_dkdv + bwd_dkdv_reduce (whole step)",
                           "algorithmic_flops": flops, "executed_mfma_flops": flops * 7 // 5})
 
@@ -555,7 +609,7 @@ def bench_swa_backward(steps, warmup, dev, window=512):
                 us_avg=round(avg * 1e3, 2), us_median=round(per[len(per) // 2] * 1e3, 2),
                 us_min=round(per[0] * 1e3, 2),
                 roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
-                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4), **_clock_fields(tflops),
                           "kernel": "bwd_dq(_split) + bwd_dkdv + bwd_dkdv_reduce (whole step)",
                           "algorithmic_flops": flops, "executed_mfma_flops": flops * 7 // 5})
 
@@ -590,7 +644,7 @@ def bench_mla_backward(steps, warmup, dev):
                 us_avg=round(avg * 1e3, 2), us_median=round(per[len(per) // 2] * 1e3, 2),
                 us_min=round(per[0] * 1e3, 2),
                 roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
-                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                          "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4), **_clock_fields(tflops),
                           "kernel": "bwd_dq<192> + bwd_dkdv<192> (whole step)",
                           "algorithmic_flops": flops})
 
@@ -691,7 +745,7 @@ def main():
                      "kernel": res["kernel"], "algorithmic_bytes": res["kv_bytes"],
                      "avg_launch_us": round(res["avg_launch_ms"] * 1e3, 2),
                      "median_launch_us": round(res["median_ms"] * 1e3, 2),
-                     "min_launch_us": round(res["min_ms"] * 1e3, 2)},
+                     "min_launch_us": round(res["min_ms"] * 1e3, 2), "sclk_mhz": res["sclk_mhz"]},
         "decode_all_tensor_GBs": round((res["kv_bytes"] + res["qo_bytes"]) / (res["ms_step"] * 1e-3) / 1e9, 2),
     }
     threads = min(os.cpu_count() or 1, 16)

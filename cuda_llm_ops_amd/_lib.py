@@ -233,6 +233,8 @@ def lib() -> ctypes.CDLL:
         L.fgqa_status_string.argtypes = [ctypes.c_int]
         L.fgqa_version.restype = ctypes.c_int
         L.fgqa_version.argtypes = []
+        L.fgqa_clock_sample.restype = ctypes.c_int
+        L.fgqa_clock_sample.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
         _lib = L
     return _lib
 

@@ -75,7 +75,32 @@ void* internal_workspace(size_t bytes, int* status) {
     return g_ws_ptr[dev];
 }
 
+// Workgroup w's first thread reads its CU's shader-clock counter
+// (s_memtime), the 100 MHz real-time counter (s_memrealtime) and where it
+// runs (XCD number, and the SE / SH / CU fields of HW_ID), and stores them
+// at out[3w .. 3w+2].
+__global__ __launch_bounds__(64) void clock_sample_kernel(unsigned long long* out) {
+    if (threadIdx.x != 0) return;
+    const unsigned long long t = __builtin_amdgcn_s_memtime();
+    const unsigned long long r = __builtin_amdgcn_s_memrealtime();
+    unsigned xcc, hw;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+    unsigned long long* o = out + 3 * (size_t)blockIdx.x;
+    o[0] = t;
+    o[1] = r;
+    o[2] = ((unsigned long long)(xcc & 15u) << 8) | ((hw >> 8) & 0xffu);
+}
+
 }  // namespace fgqa
+
+extern "C" int fgqa_clock_sample(unsigned long long* out, int samples, void* stream) {
+    if (out == nullptr || (reinterpret_cast<uintptr_t>(out) & 7u) != 0 || samples < 1 || samples > 65536)
+        return FGQA_ERR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(fgqa::clock_sample_kernel, dim3((unsigned)samples), dim3(64), 0,
+                       static_cast<hipStream_t>(stream), out);
+    return hipGetLastError() == hipSuccess ? FGQA_OK : FGQA_ERR_HIP;
+}
 
 extern "C" const char* fgqa_status_string(int status) {
     switch (status) {

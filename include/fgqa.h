@@ -437,6 +437,18 @@ const char* fgqa_status_string(int status);
 /* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
 int fgqa_version(void);
 
+/* Measurement helper (no counterpart in the reference): enqueues on `stream`
+ * `samples` (1 .. 65536) one-wave workgroups; workgroup w stores to the
+ * device array out[3w .. 3w+2] (8-byte aligned) its CU's shader-clock
+ * counter (s_memtime), the 100 MHz real-time counter (s_memrealtime) and
+ * (xcd << 8) | the SE, SH and CU fields of HW_ID, which names the CU.  Two
+ * such launches on one stream around a run of launches give, for each CU
+ * sampled by both, the average shader clock over the run:
+ * (t1 - t0) / (r1 - r0) * 100 MHz (the counters of different CUs are not
+ * aligned, so only samples of one CU are differenced).  Used by bench.py to
+ * record the clock the MFMA-bound kernels sustain. */
+int fgqa_clock_sample(unsigned long long* out, int samples, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

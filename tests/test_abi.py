@@ -26,7 +26,7 @@ def test_c_abi_symbols_exported():
                      "fgqa_prefill_kernel_choice", "fgqa_prefill_kernel_name", "fgqa_prefill_workspace_bytes",
                      "fgqa_prefill_backward_workspace_bytes", "fgqa_prefill_backward_bf16",
                      "fgqa_decode_paged_workspace_bytes", "fgqa_decode_paged", "fgqa_sparse_prefill_bf16",
-                     "fgqa_status_string", "fgqa_version"}
+                     "fgqa_status_string", "fgqa_version", "fgqa_clock_sample"}
     L = _lib.lib()
     syms = _exported()
     for n in names:
