@@ -27,11 +27,12 @@
 // slot t % page), in bf16 or in OCP fp8 e4m3 with per-tensor scales.  fp8 rows
 // are widened to bf16 exactly (v_cvt_scalef32_pk_bf16_fp8, scale 1) as they are
 // staged in LDS; the K scale is folded into the softmax scale and the V scale
-// into the output, so the arithmetic after staging is the bf16 path's.  bf16
-// pages of 4 rows or more are read by page segment (min(page, 32) rows of a
-// step): one buffer resource per segment, the wave's pages taken from one
-// vector load of the block table per 64 segments; other pages (and fp8) look
-// up each row's page and form its 64-bit address.
+// into the output, so the arithmetic after staging is the bf16 path's.  Pages
+// of at least one load instruction's rows (4 bf16 rows, 8 fp8 rows) are read
+// by page segment (min(page, 32) rows of a step): one buffer resource per
+// segment, the wave's pages taken from one vector load of the block table per
+// 64 segments; smaller pages, and caches whose page bytes reach 2^31, look up
+// each row's page and form its 64-bit address.
 #include <math.h>
 
 #include "fgqa_device.h"
