@@ -593,21 +593,43 @@ __global__ __launch_bounds__(kDecThreads) void decode_combine_kernel(DecodeParam
         return;
     }
     const int64_t base = ((int64_t)b * p.hkv + kvh) * p.nsplit;
+    // Splits in batches of kCombineBatch whose loads are all issued before any
+    // is used (slots past the last valid split re-read it and are masked), so
+    // a batch costs one memory round trip; the sums run in split order.
+    constexpr int kCombineBatch = 8;
     float M = -INFINITY;
-    for (int s = 0; s < nvalid; ++s) M = fmaxf(M, p.part_ml[((base + s) * p.group + h) * 2]);
+    for (int s0 = 0; s0 < nvalid; s0 += kCombineBatch) {
+        float mv[kCombineBatch];
+#pragma unroll
+        for (int i = 0; i < kCombineBatch; ++i)
+            mv[i] = p.part_ml[((base + min(s0 + i, nvalid - 1)) * p.group + h) * 2];
+#pragma unroll
+        for (int i = 0; i < kCombineBatch; ++i) M = fmaxf(M, mv[i]);
+    }
     float L = 0.f;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < nvalid; ++s) {
-        const int64_t slot = (base + s) * p.group + h;
-        const float ms = p.part_ml[slot * 2];
-        const float c = (ms == -INFINITY) ? 0.f : fast_exp2(ms - M);
-        L += c * p.part_ml[slot * 2 + 1];
-        const f32x4_t a = *reinterpret_cast<const f32x4_t*>(p.part_o + slot * kHeadDim + d0);
-        const f32x4_t bb = *reinterpret_cast<const f32x4_t*>(p.part_o + slot * kHeadDim + d0 + 4);
+    for (int s0 = 0; s0 < nvalid; s0 += kCombineBatch) {
+        float ms[kCombineBatch], ls[kCombineBatch];
+        f32x4_t a[kCombineBatch], bb[kCombineBatch];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            acc[j] += c * a[j];
-            acc[4 + j] += c * bb[j];
+        for (int i = 0; i < kCombineBatch; ++i) {
+            const int64_t slot = (base + min(s0 + i, nvalid - 1)) * p.group + h;
+            ms[i] = p.part_ml[slot * 2];
+            ls[i] = p.part_ml[slot * 2 + 1];
+            a[i] = *reinterpret_cast<const f32x4_t*>(p.part_o + slot * kHeadDim + d0);
+            bb[i] = *reinterpret_cast<const f32x4_t*>(p.part_o + slot * kHeadDim + d0 + 4);
+        }
+        // selects, not a branch, so the loads above stay ahead of every use
+#pragma unroll
+        for (int i = 0; i < kCombineBatch; ++i) {
+            const bool valid = s0 + i < nvalid;
+            const float c = (ms[i] == -INFINITY) ? 0.f : fast_exp2(ms[i] - M);
+            L = valid ? L + c * ls[i] : L;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[j] = valid ? acc[j] + c * a[i][j] : acc[j];
+                acc[4 + j] = valid ? acc[4 + j] + c * bb[i][j] : acc[4 + j];
+            }
         }
     }
     const float inv = 1.f / L;
